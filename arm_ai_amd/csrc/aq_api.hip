@@ -1,0 +1,524 @@
+// aq_api.hip -- the extern "C" boundary (include/aq.h) of libarm_ai_amd.so.
+//
+// Host-side replacement for candle-core 0.8.4's QMatMul / QTensor on the
+// CPU (reached from native/arm_ai_nif/src/llama_candle.rs:42 at load and
+// :93 / :119 at prefill / decode).  Weights are uploaded once, repacked into
+// HBM planes, and every matmul runs as: activation quantizer kernel (Q8_K, or
+// Q8_0 for Q8_0 weights) -> matvec (m <= 8) or MFMA GEMM (m > 8) on the
+// context's stream.  Errors are status codes plus a thread-local message;
+// nothing here aborts (the reference crate builds with panic = "abort",
+// Cargo.toml:33, which this library must not inherit).
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <new>
+#include <string>
+
+#include "../../include/aq.h"
+#include "aq_internal.h"
+
+using namespace aq;
+
+struct aq_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    void *scratch = nullptr;  // device, grow-only
+    size_t scratch_bytes = 0;
+    void *pinned = nullptr;  // host staging, grow-only
+    size_t pinned_bytes = 0;
+};
+
+struct aq_qweight {
+    int type = 0;
+    int device = 0;
+    int64_t n = 0, k = 0;
+    void *base = nullptr;
+    size_t bytes = 0;
+    WPlanes planes{};
+};
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+#define HIP_TRY(call)                                                                      \
+    do {                                                                                   \
+        hipError_t e_ = (call);                                                            \
+        if (e_ != hipSuccess) return fail(AQ_ERR_HIP, "%s: %s", #call, hipGetErrorString(e_)); \
+    } while (0)
+
+int block_elems(int type) {
+    switch (type) {
+    case AQ_TYPE_Q4_K:
+    case AQ_TYPE_Q6_K: return QK_K;
+    case AQ_TYPE_Q8_0: return QK8_0;
+    default: return 0;
+    }
+}
+int block_bytes(int type) {
+    switch (type) {
+    case AQ_TYPE_Q4_K: return 144;
+    case AQ_TYPE_Q6_K: return 210;
+    case AQ_TYPE_Q8_0: return 34;
+    default: return 0;
+    }
+}
+
+// Per-block bytes of each plane (qs, qh, meta, d), see aq_internal.h.
+void plane_bytes(int type, size_t pb[4]) {
+    pb[0] = pb[1] = pb[2] = pb[3] = 0;
+    if (type == AQ_TYPE_Q4_K) { pb[0] = 128; pb[2] = 16; }
+    if (type == AQ_TYPE_Q6_K) { pb[0] = 128; pb[1] = 64; pb[2] = 16; pb[3] = 2; }
+    if (type == AQ_TYPE_Q8_0) { pb[0] = 32; pb[3] = 2; }
+}
+
+int use_device(int device) {
+    int cur = -1;
+    if (hipGetDevice(&cur) == hipSuccess && cur == device) return AQ_OK;
+    HIP_TRY(hipSetDevice(device));
+    return AQ_OK;
+}
+
+int ensure_scratch(aq_ctx *c, size_t bytes) {
+    if (bytes <= c->scratch_bytes) return AQ_OK;
+    size_t want = align_up(bytes + bytes / 4, 1 << 20);
+    if (c->scratch) {
+        HIP_TRY(hipStreamSynchronize(c->stream));
+        HIP_TRY(hipFree(c->scratch));
+        c->scratch = nullptr;
+        c->scratch_bytes = 0;
+    }
+    void *p = nullptr;
+    if (hipMalloc(&p, want) != hipSuccess) {
+        (void)hipGetLastError();
+        return fail(AQ_ERR_OOM, "hipMalloc of %zu bytes of scratch failed", want);
+    }
+    c->scratch = p;
+    c->scratch_bytes = want;
+    return AQ_OK;
+}
+
+int ensure_pinned(aq_ctx *c, size_t bytes) {
+    if (bytes <= c->pinned_bytes) return AQ_OK;
+    size_t want = align_up(bytes + bytes / 4, 1 << 20);
+    if (c->pinned) {
+        HIP_TRY(hipStreamSynchronize(c->stream));
+        HIP_TRY(hipHostFree(c->pinned));
+        c->pinned = nullptr;
+        c->pinned_bytes = 0;
+    }
+    void *p = nullptr;
+    if (hipHostMalloc(&p, want, hipHostMallocDefault) != hipSuccess) {
+        (void)hipGetLastError();
+        return fail(AQ_ERR_OOM, "hipHostMalloc of %zu bytes failed", want);
+    }
+    c->pinned = p;
+    c->pinned_bytes = want;
+    return AQ_OK;
+}
+
+// Scratch layout for one matmul call: [activation planes | x f32 | y f32 | S | Smin | gemm workspace]
+struct CallLayout {
+    size_t act, x, y, s, smin, ws, total;
+};
+CallLayout call_layout(const aq_qweight *w, int64_t m, bool host_io, bool dump, bool gemm) {
+    CallLayout L;
+    size_t off = 0;
+    L.act = off;
+    off += align_up(act_sizes(m, w->k).total, 256);
+    L.x = off;
+    if (host_io) off += align_up((size_t)m * w->k * 4, 256);
+    L.y = off;
+    if (host_io) off += align_up((size_t)m * w->n * 4, 256);
+    const size_t nblk = (size_t)(w->k / block_elems(w->type));
+    L.s = off;
+    if (dump) off += align_up((size_t)m * w->n * nblk * 4, 256);
+    L.smin = off;
+    if (dump) off += align_up((size_t)m * w->n * nblk * 4, 256);
+    L.ws = off;
+    if (gemm) off += align_up(gemm_workspace_bytes(w->type, m, w->n, w->k), 256);
+    L.total = off;
+    return L;
+}
+
+bool use_gemm(const aq_qweight *w, int64_t m) { return m > 8 && gemm_workspace_bytes(w->type, m, w->n, w->k) != (size_t)-1; }
+
+int check_mm(aq_ctx *ctx, const aq_qweight *w, int64_t m, int64_t k) {
+    if (!ctx) return fail(AQ_ERR_INVALID_ARG, "null context");
+    if (!w) return fail(AQ_ERR_INVALID_ARG, "null weight");
+    if (m < 0) return fail(AQ_ERR_INVALID_ARG, "negative m (%lld)", (long long)m);
+    if (k != w->k) return fail(AQ_ERR_SHAPE, "lhs last dim %lld != weight k %lld", (long long)k, (long long)w->k);
+    if (w->device != ctx->device) return fail(AQ_ERR_INVALID_ARG, "weight is on device %d, context on %d", w->device, ctx->device);
+    return AQ_OK;
+}
+
+// Quantise d_x [m][k] into the activation planes at `act`, then run the
+// matmul into d_y.  All on ctx->stream.
+int run_matmul(aq_ctx *ctx, const aq_qweight *w, const float *d_x, int64_t m, float *d_y, void *act, int32_t *dS,
+               int32_t *dSmin, void *ws, size_t ws_bytes) {
+    ActPlanes a = act_planes(act, m, w->k);
+    hipError_t e = w->type == AQ_TYPE_Q8_0 ? launch_quantize_q8_0(d_x, m, w->k, a, ctx->stream)
+                                           : launch_quantize_q8k(d_x, m, w->k, a, ctx->stream);
+    if (e != hipSuccess) return fail(AQ_ERR_HIP, "activation quantizer: %s", hipGetErrorString(e));
+    if (use_gemm(w, m)) {
+        e = launch_gemm(w->type, w->planes, w->n, w->k, a, m, d_y, dS, dSmin, ws, ws_bytes, ctx->stream);
+        if (e == hipSuccess) return AQ_OK;
+        if (e != hipErrorNotSupported) return fail(AQ_ERR_HIP, "gemm: %s", hipGetErrorString(e));
+    }
+    e = launch_matvec(w->type, w->planes, w->n, w->k, a, m, d_y, dS, dSmin, ctx->stream);
+    if (e == hipErrorNotSupported) return fail(AQ_ERR_SHAPE, "k=%lld is larger than the matvec supports", (long long)w->k);
+    if (e != hipSuccess) return fail(AQ_ERR_HIP, "matvec: %s", hipGetErrorString(e));
+    return AQ_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int aq_abi_version(void) { return 1; }
+
+const char *aq_last_error(void) { return g_err.c_str(); }
+
+int aq_device_count(int *count) {
+    if (!count) return fail(AQ_ERR_INVALID_ARG, "null count");
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        n = 0;
+    }
+    *count = n;
+    return AQ_OK;
+}
+
+int aq_ctx_create(int device, aq_ctx **out) {
+    if (!out) return fail(AQ_ERR_INVALID_ARG, "null out");
+    *out = nullptr;
+    int n = 0;
+    aq_device_count(&n);
+    if (n == 0) return fail(AQ_ERR_NO_DEVICE, "no HIP device visible");
+    if (device < 0 || device >= n) return fail(AQ_ERR_NO_DEVICE, "device %d out of range (%d visible)", device, n);
+    int rc = use_device(device);
+    if (rc) return rc;
+    aq_ctx *c = new (std::nothrow) aq_ctx();
+    if (!c) return fail(AQ_ERR_OOM, "out of host memory");
+    c->device = device;
+    if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {
+        delete c;
+        return fail(AQ_ERR_HIP, "hipStreamCreateWithFlags failed");
+    }
+    *out = c;
+    return AQ_OK;
+}
+
+int aq_ctx_destroy(aq_ctx *c) {
+    if (!c) return AQ_OK;
+    use_device(c->device);
+    if (c->stream) (void)hipStreamSynchronize(c->stream);
+    if (c->scratch) (void)hipFree(c->scratch);
+    if (c->pinned) (void)hipHostFree(c->pinned);
+    if (c->stream) (void)hipStreamDestroy(c->stream);
+    delete c;
+    return AQ_OK;
+}
+
+int aq_ctx_synchronize(aq_ctx *c) {
+    if (!c) return fail(AQ_ERR_INVALID_ARG, "null context");
+    int rc = use_device(c->device);
+    if (rc) return rc;
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    return AQ_OK;
+}
+
+int aq_ctx_stream(aq_ctx *c, void **stream) {
+    if (!c || !stream) return fail(AQ_ERR_INVALID_ARG, "null argument");
+    *stream = (void *)c->stream;
+    return AQ_OK;
+}
+
+static int upload_impl(aq_ctx *ctx, int type, const void *blocks, size_t nbytes, int64_t n, int64_t k,
+                       bool src_on_device, aq_qweight **out) {
+    if (!out) return fail(AQ_ERR_INVALID_ARG, "null out");
+    *out = nullptr;
+    if (!ctx || !blocks) return fail(AQ_ERR_INVALID_ARG, "null argument");
+    const int be = block_elems(type);
+    if (!be) return fail(AQ_ERR_UNSUPPORTED_TYPE, "unsupported weight type %d", type);
+    if (n <= 0 || k <= 0) return fail(AQ_ERR_SHAPE, "bad weight shape (%lld, %lld)", (long long)n, (long long)k);
+    if (k % be) return fail(AQ_ERR_SHAPE, "k=%lld is not a multiple of the block size %d", (long long)k, be);
+    if (n > 0x7fffffff || k > 0x7fffffff) return fail(AQ_ERR_SHAPE, "weight dimension too large");
+    const size_t nb = (size_t)(k / be);
+    const size_t row_bytes = nb * block_bytes(type);
+    if (nbytes != row_bytes * (size_t)n)
+        return fail(AQ_ERR_SHAPE, "nbytes=%zu != n*k/%d*%d = %zu", nbytes, be, block_bytes(type), row_bytes * (size_t)n);
+    int rc = use_device(ctx->device);
+    if (rc) return rc;
+    size_t pb[4];
+    plane_bytes(type, pb);
+    size_t off[4], total = 0;
+    for (int i = 0; i < 4; i++) {
+        off[i] = total;
+        total += align_up(pb[i] * nb * (size_t)n, 256);
+    }
+    aq_qweight *w = new (std::nothrow) aq_qweight();
+    if (!w) return fail(AQ_ERR_OOM, "out of host memory");
+    if (hipMalloc(&w->base, total) != hipSuccess) {
+        (void)hipGetLastError();
+        delete w;
+        return fail(AQ_ERR_OOM, "hipMalloc of %zu weight bytes failed", total);
+    }
+    w->type = type;
+    w->device = ctx->device;
+    w->n = n;
+    w->k = k;
+    w->bytes = total;
+    uint8_t *base = (uint8_t *)w->base;
+    w->planes.qs = base + off[0];
+    w->planes.qh = pb[1] ? base + off[1] : nullptr;
+    w->planes.meta = pb[2] ? base + off[2] : nullptr;
+    w->planes.d = pb[3] ? (const uint16_t *)(base + off[3]) : nullptr;
+
+    // Stage whole rows through a bounded device buffer (256 MiB) unless the
+    // blocks are already on the device.
+    const size_t stage_cap = (size_t)256 << 20;
+    int64_t rows_per = (int64_t)(stage_cap / row_bytes);
+    if (rows_per < 1) rows_per = 1;
+    if (rows_per > n) rows_per = n;
+    void *stage = nullptr;
+    if (!src_on_device) {
+        if (hipMalloc(&stage, (size_t)rows_per * row_bytes) != hipSuccess) {
+            (void)hipGetLastError();
+            (void)hipFree(w->base);
+            delete w;
+            return fail(AQ_ERR_OOM, "hipMalloc of the upload staging buffer failed");
+        }
+    }
+    int status = AQ_OK;
+    for (int64_t r0 = 0; r0 < n && status == AQ_OK; r0 += rows_per) {
+        const int64_t rows = (n - r0) < rows_per ? (n - r0) : rows_per;
+        const uint8_t *src = (const uint8_t *)blocks + (size_t)r0 * row_bytes;
+        if (!src_on_device) {
+            if (hipMemcpyAsync(stage, src, (size_t)rows * row_bytes, hipMemcpyHostToDevice, ctx->stream) != hipSuccess) {
+                status = fail(AQ_ERR_HIP, "weight upload copy failed");
+                break;
+            }
+            src = (const uint8_t *)stage;
+        }
+        const size_t rb = (size_t)r0 * nb;
+        hipError_t e = launch_repack(type, src, rows, k, base + off[0] + rb * pb[0], pb[1] ? base + off[1] + rb * pb[1] : nullptr,
+                                     pb[2] ? base + off[2] + rb * pb[2] : nullptr, pb[3] ? base + off[3] + rb * pb[3] : nullptr,
+                                     ctx->stream);
+        if (e != hipSuccess) status = fail(AQ_ERR_HIP, "repack: %s", hipGetErrorString(e));
+        // the staging buffer is reused by the next chunk
+        if (status == AQ_OK && hipStreamSynchronize(ctx->stream) != hipSuccess) status = fail(AQ_ERR_HIP, "upload sync failed");
+    }
+    if (stage) (void)hipFree(stage);
+    if (status != AQ_OK) {
+        (void)hipFree(w->base);
+        delete w;
+        return status;
+    }
+    *out = w;
+    return AQ_OK;
+}
+
+int aq_qweight_upload(aq_ctx *ctx, int type, const void *blocks, size_t nbytes, int64_t n, int64_t k, aq_qweight **out) {
+    return upload_impl(ctx, type, blocks, nbytes, n, k, false, out);
+}
+
+int aq_qweight_upload_device(aq_ctx *ctx, int type, const void *d_blocks, size_t nbytes, int64_t n, int64_t k,
+                             aq_qweight **out) {
+    return upload_impl(ctx, type, d_blocks, nbytes, n, k, true, out);
+}
+
+int aq_qweight_free(aq_qweight *w) {
+    if (!w) return AQ_OK;
+    use_device(w->device);
+    if (w->base) (void)hipFree(w->base);
+    delete w;
+    return AQ_OK;
+}
+
+int aq_qweight_info(const aq_qweight *w, int *type, int64_t *n, int64_t *k, size_t *device_bytes) {
+    if (!w) return fail(AQ_ERR_INVALID_ARG, "null weight");
+    if (type) *type = w->type;
+    if (n) *n = w->n;
+    if (k) *k = w->k;
+    if (device_bytes) *device_bytes = w->bytes;
+    return AQ_OK;
+}
+
+int aq_qmatmul_f32(aq_ctx *ctx, const aq_qweight *w, const float *lhs, int64_t m, int64_t k, float *dst) {
+    int rc = check_mm(ctx, w, m, k);
+    if (rc) return rc;
+    if (m == 0) return AQ_OK;
+    if (!lhs || !dst) return fail(AQ_ERR_INVALID_ARG, "null lhs or dst");
+    if ((rc = use_device(ctx->device))) return rc;
+    const bool gemm = use_gemm(w, m);
+    CallLayout L = call_layout(w, m, true, false, gemm);
+    if ((rc = ensure_scratch(ctx, L.total))) return rc;
+    const size_t xin = (size_t)m * k * 4, yout = (size_t)m * w->n * 4;
+    if ((rc = ensure_pinned(ctx, xin > yout ? xin : yout))) return rc;
+    uint8_t *S = (uint8_t *)ctx->scratch;
+    float *d_x = (float *)(S + L.x), *d_y = (float *)(S + L.y);
+    memcpy(ctx->pinned, lhs, xin);
+    HIP_TRY(hipMemcpyAsync(d_x, ctx->pinned, xin, hipMemcpyHostToDevice, ctx->stream));
+    if ((rc = run_matmul(ctx, w, d_x, m, d_y, S + L.act, nullptr, nullptr, S + L.ws, L.total - L.ws))) return rc;
+    HIP_TRY(hipMemcpyAsync(ctx->pinned, d_y, yout, hipMemcpyDeviceToHost, ctx->stream));
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    memcpy(dst, ctx->pinned, yout);
+    return AQ_OK;
+}
+
+int aq_qmatmul_f32_device(aq_ctx *ctx, const aq_qweight *w, const float *d_lhs, int64_t m, int64_t k, float *d_dst) {
+    int rc = check_mm(ctx, w, m, k);
+    if (rc) return rc;
+    if (m == 0) return AQ_OK;
+    if (!d_lhs || !d_dst) return fail(AQ_ERR_INVALID_ARG, "null lhs or dst");
+    if ((rc = use_device(ctx->device))) return rc;
+    const bool gemm = use_gemm(w, m);
+    CallLayout L = call_layout(w, m, false, false, gemm);
+    if ((rc = ensure_scratch(ctx, L.total))) return rc;
+    uint8_t *S = (uint8_t *)ctx->scratch;
+    return run_matmul(ctx, w, d_lhs, m, d_dst, S + L.act, nullptr, nullptr, S + L.ws, L.total - L.ws);
+}
+
+size_t aq_act_bytes(int act_type, int64_t m, int64_t k) {
+    if ((act_type != AQ_TYPE_Q8_K && act_type != AQ_TYPE_Q8_0) || m < 0 || k <= 0) return 0;
+    return align_up(act_sizes(m, k).total, 256);
+}
+
+int aq_quantize_act_device(aq_ctx *ctx, int act_type, const float *d_x, int64_t m, int64_t k, void *d_act) {
+    if (!ctx) return fail(AQ_ERR_INVALID_ARG, "null context");
+    if (act_type != AQ_TYPE_Q8_K && act_type != AQ_TYPE_Q8_0)
+        return fail(AQ_ERR_UNSUPPORTED_TYPE, "activation type %d is not Q8_K or Q8_0", act_type);
+    const int blk = act_type == AQ_TYPE_Q8_K ? QK_K : QK8_0;
+    if (m < 0 || k <= 0 || k % blk) return fail(AQ_ERR_SHAPE, "bad activation shape (%lld, %lld)", (long long)m, (long long)k);
+    if (m == 0) return AQ_OK;
+    if (!d_x || !d_act) return fail(AQ_ERR_INVALID_ARG, "null argument");
+    if ((uintptr_t)d_act & 255) return fail(AQ_ERR_INVALID_ARG, "activation buffer must be 256-byte aligned");
+    int rc = use_device(ctx->device);
+    if (rc) return rc;
+    ActPlanes a = act_planes(d_act, m, k);
+    hipError_t e = act_type == AQ_TYPE_Q8_K ? launch_quantize_q8k(d_x, m, k, a, ctx->stream)
+                                            : launch_quantize_q8_0(d_x, m, k, a, ctx->stream);
+    if (e != hipSuccess) return fail(AQ_ERR_HIP, "quantizer: %s", hipGetErrorString(e));
+    return AQ_OK;
+}
+
+int aq_qmatmul_preq_device(aq_ctx *ctx, const aq_qweight *w, const void *d_act, int64_t m, int64_t k, float *d_dst) {
+    int rc = check_mm(ctx, w, m, k);
+    if (rc) return rc;
+    if (m == 0) return AQ_OK;
+    if (!d_act || !d_dst) return fail(AQ_ERR_INVALID_ARG, "null activation or dst");
+    if ((uintptr_t)d_act & 255) return fail(AQ_ERR_INVALID_ARG, "activation buffer must be 256-byte aligned");
+    if ((rc = use_device(ctx->device))) return rc;
+    ActPlanes a = act_planes((void *)d_act, m, k);
+    if (use_gemm(w, m)) {
+        CallLayout L = call_layout(w, m, false, false, true);
+        if ((rc = ensure_scratch(ctx, L.total))) return rc;
+        hipError_t e = launch_gemm(w->type, w->planes, w->n, w->k, a, m, d_dst, nullptr, nullptr,
+                                   (uint8_t *)ctx->scratch + L.ws, L.total - L.ws, ctx->stream);
+        if (e == hipSuccess) return AQ_OK;
+        if (e != hipErrorNotSupported) return fail(AQ_ERR_HIP, "gemm: %s", hipGetErrorString(e));
+    }
+    hipError_t e = launch_matvec(w->type, w->planes, w->n, w->k, a, m, d_dst, nullptr, nullptr, ctx->stream);
+    if (e == hipErrorNotSupported) return fail(AQ_ERR_SHAPE, "k=%lld is larger than the matvec supports", (long long)w->k);
+    if (e != hipSuccess) return fail(AQ_ERR_HIP, "matvec: %s", hipGetErrorString(e));
+    return AQ_OK;
+}
+
+static int quantize_host(aq_ctx *ctx, int atype, const float *x, int64_t m, int64_t k, void *out_blocks) {
+    if (!ctx) return fail(AQ_ERR_INVALID_ARG, "null context");
+    const int blk = atype == AQ_TYPE_Q8_K ? QK_K : QK8_0;
+    if (m < 0 || k <= 0) return fail(AQ_ERR_SHAPE, "bad shape (%lld, %lld)", (long long)m, (long long)k);
+    if (k % blk) return fail(AQ_ERR_SHAPE, "k=%lld is not a multiple of %d", (long long)k, blk);
+    if (m == 0) return AQ_OK;
+    if (!x || !out_blocks) return fail(AQ_ERR_INVALID_ARG, "null argument");
+    int rc = use_device(ctx->device);
+    if (rc) return rc;
+    const size_t act = align_up(act_sizes(m, k).total, 256), xin = (size_t)m * k * 4;
+    if ((rc = ensure_scratch(ctx, act + xin))) return rc;
+    if ((rc = ensure_pinned(ctx, act > xin ? act : xin))) return rc;
+    uint8_t *S = (uint8_t *)ctx->scratch;
+    float *d_x = (float *)(S + act);
+    memcpy(ctx->pinned, x, xin);
+    HIP_TRY(hipMemcpyAsync(d_x, ctx->pinned, xin, hipMemcpyHostToDevice, ctx->stream));
+    ActPlanes a = act_planes(S, m, k);
+    hipError_t e = atype == AQ_TYPE_Q8_K ? launch_quantize_q8k(d_x, m, k, a, ctx->stream)
+                                         : launch_quantize_q8_0(d_x, m, k, a, ctx->stream);
+    if (e != hipSuccess) return fail(AQ_ERR_HIP, "quantizer: %s", hipGetErrorString(e));
+    HIP_TRY(hipMemcpyAsync(ctx->pinned, S, act, hipMemcpyDeviceToHost, ctx->stream));
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    // planes -> GGUF blocks
+    ActPlanes h = act_planes(ctx->pinned, m, k);
+    uint8_t *o = (uint8_t *)out_blocks;
+    if (atype == AQ_TYPE_Q8_K) {
+        const int64_t nb = k / QK_K;
+        for (int64_t r = 0; r < m; r++)
+            for (int64_t b = 0; b < nb; b++) {
+                uint8_t *blkp = o + (size_t)(r * nb + b) * 292;
+                memcpy(blkp, &h.d[r * nb + b], 4);
+                memcpy(blkp + 4, h.qs + r * k + b * QK_K, 256);
+                memcpy(blkp + 260, h.bsums + r * (k / 16) + b * 16, 32);
+            }
+    } else {
+        const int64_t nb = k / QK8_0;
+        for (int64_t r = 0; r < m; r++)
+            for (int64_t b = 0; b < nb; b++) {
+                uint8_t *blkp = o + (size_t)(r * nb + b) * 34;
+                memcpy(blkp, &h.d16[r * nb + b], 2);
+                memcpy(blkp + 2, h.qs + r * k + b * QK8_0, 32);
+            }
+    }
+    return AQ_OK;
+}
+
+int aq_quantize_q8k(aq_ctx *ctx, const float *x, int64_t m, int64_t k, void *out_blocks) {
+    return quantize_host(ctx, AQ_TYPE_Q8_K, x, m, k, out_blocks);
+}
+
+int aq_quantize_q8_0(aq_ctx *ctx, const float *x, int64_t m, int64_t k, void *out_blocks) {
+    return quantize_host(ctx, AQ_TYPE_Q8_0, x, m, k, out_blocks);
+}
+
+int aq_qmatmul_block_sums(aq_ctx *ctx, const aq_qweight *w, const float *lhs, int64_t m, int64_t k, int32_t *S,
+                          int32_t *Smin) {
+    int rc = check_mm(ctx, w, m, k);
+    if (rc) return rc;
+    if (m == 0) return AQ_OK;
+    if (!lhs || !S || !Smin) return fail(AQ_ERR_INVALID_ARG, "null argument");
+    if ((rc = use_device(ctx->device))) return rc;
+    const bool gemm = use_gemm(w, m);
+    CallLayout L = call_layout(w, m, true, true, gemm);
+    if ((rc = ensure_scratch(ctx, L.total))) return rc;
+    const size_t nblk = (size_t)(w->k / block_elems(w->type));
+    const size_t xin = (size_t)m * k * 4, sbytes = (size_t)m * w->n * nblk * 4;
+    if ((rc = ensure_pinned(ctx, xin > sbytes ? xin : sbytes))) return rc;
+    uint8_t *B = (uint8_t *)ctx->scratch;
+    float *d_x = (float *)(B + L.x), *d_y = (float *)(B + L.y);
+    int32_t *dS = (int32_t *)(B + L.s), *dSm = (int32_t *)(B + L.smin);
+    memcpy(ctx->pinned, lhs, xin);
+    HIP_TRY(hipMemcpyAsync(d_x, ctx->pinned, xin, hipMemcpyHostToDevice, ctx->stream));
+    if ((rc = run_matmul(ctx, w, d_x, m, d_y, B + L.act, dS, dSm, B + L.ws, L.total - L.ws))) return rc;
+    HIP_TRY(hipMemcpyAsync(ctx->pinned, dS, sbytes, hipMemcpyDeviceToHost, ctx->stream));
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    memcpy(S, ctx->pinned, sbytes);
+    HIP_TRY(hipMemcpyAsync(ctx->pinned, dSm, sbytes, hipMemcpyDeviceToHost, ctx->stream));
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    memcpy(Smin, ctx->pinned, sbytes);
+    return AQ_OK;
+}
+
+}  // extern "C"

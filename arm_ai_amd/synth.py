@@ -1,0 +1,173 @@
+"""Seeded synthetic GGUF block data for the quantized-matmul hot path.
+
+The reference publishes no fixture data for this path (its only model test
+needs a downloaded TinyLlama GGUF, test/llama_candle_model_test.exs:2-4), so
+every workload here is synthetic, with the value distributions the benchmark
+configurations prescribe:
+
+* Q4_K: d, dmin = f16(|N(0, 0.02)|); 6-bit scales and mins ~ U[0, 63];
+  4-bit quants ~ U[0, 15].
+* Q6_K: d = f16(|N(0, 0.02)|); int8 sub-scales ~ U[-32, 31]; 6-bit quants
+  ~ U[0, 63] (value q - 32).
+* Q8_0: d = f16(|N(0, 0.02)|); int8 quants ~ U[-127, 127].
+* activations: f32 N(0, 1).
+
+Generators draw element-level arrays from ``numpy.random.default_rng(seed)``
+(PCG64) and pack them into GGUF block bytes with the GGUF layout (block
+formats: Q4_K 144 B, Q6_K 210 B, Q8_0 34 B).  The element arrays are kept so
+tests can compute exact answers without going through any unpacking code.
+f32 -> f16 uses numpy's IEEE round-to-nearest-even conversion, the same
+rounding the reference's `half` crate uses (shape_ops.rs:1492-1503).
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import numpy as np
+
+QK_K = 256
+QK8_0 = 32
+TYPE_Q4_0 = 2
+TYPE_Q8_0 = 8
+TYPE_Q4_K = 12
+TYPE_Q6_K = 14
+TYPE_Q8_K = 15
+
+BLOCK_BYTES = {TYPE_Q4_K: 144, TYPE_Q6_K: 210, TYPE_Q8_0: 34, TYPE_Q8_K: 292}
+BLOCK_ELEMS = {TYPE_Q4_K: QK_K, TYPE_Q6_K: QK_K, TYPE_Q8_0: QK8_0, TYPE_Q8_K: QK_K}
+TYPE_NAMES = {TYPE_Q4_K: "q4_k", TYPE_Q6_K: "q6_k", TYPE_Q8_0: "q8_0", TYPE_Q8_K: "q8_k"}
+
+
+@dataclass
+class QWeight:
+    """A packed GGUF weight of `n` rows by `k` columns plus its element arrays."""
+
+    type: int
+    n: int
+    k: int
+    blocks: np.ndarray  # uint8 [n, nb * block_bytes], GGUF AoS layout
+    d: np.ndarray  # float16 [n, nb]
+    dmin: np.ndarray | None  # float16 [n, nb] (Q4_K only)
+    sc: np.ndarray | None  # Q4_K uint8 [n, nb, 8]; Q6_K int8 [n, nb, 16]
+    mn: np.ndarray | None  # Q4_K uint8 [n, nb, 8]
+    q: np.ndarray  # Q4_K uint8 [n,nb,256] in [0,15]; Q6_K int8 [n,nb,256] in [-32,31]; Q8_0 int8 [n,nb,32]
+
+    @property
+    def nbytes(self) -> int:
+        return int(self.blocks.nbytes)
+
+    def dequantize(self) -> np.ndarray:
+        """f64 [n, k] element values from the element arrays (GGML formulas)."""
+        d = self.d.astype(np.float64)[..., None]
+        if self.type == TYPE_Q4_K:
+            sc = np.repeat(self.sc.astype(np.float64), 32, axis=-1)
+            mn = np.repeat(self.mn.astype(np.float64), 32, axis=-1)
+            v = d * sc * self.q.astype(np.float64) - self.dmin.astype(np.float64)[..., None] * mn
+        elif self.type == TYPE_Q6_K:
+            sc = np.repeat(self.sc.astype(np.float64), 16, axis=-1)
+            v = d * sc * self.q.astype(np.float64)
+        else:
+            v = d * self.q.astype(np.float64)
+        return v.reshape(self.n, self.k)
+
+
+def _half_abs_normal(rng: np.random.Generator, shape, sigma: float = 0.02) -> np.ndarray:
+    return np.abs(rng.normal(0.0, sigma, size=shape)).astype(np.float32).astype(np.float16)
+
+
+def pack_q4k(d, dmin, sc, mn, q) -> np.ndarray:
+    """Pack Q4_K element arrays into 144-byte blocks.
+
+    6-bit scale/min packing (inverse of GGML's get_scale_min_k4), j < 4:
+      s[j]   = sc[j] | (sc[j+4] >> 4) << 6
+      s[j+4] = m[j]  | (m[j+4]  >> 4) << 6
+      s[j+8] = (sc[j+4] & 15) | (m[j+4] & 15) << 4
+    quants: qs[32c+l] = q[64c+l] | q[64c+32+l] << 4.
+    """
+    n, nb = d.shape
+    out = np.empty((n, nb, 144), dtype=np.uint8)
+    out[..., 0:2] = d.astype(np.float16).view(np.uint8).reshape(n, nb, 2)
+    out[..., 2:4] = dmin.astype(np.float16).view(np.uint8).reshape(n, nb, 2)
+    sc = sc.astype(np.uint8)
+    mn = mn.astype(np.uint8)
+    s = out[..., 4:16]
+    s[..., 0:4] = sc[..., 0:4] | ((sc[..., 4:8] >> 4) << 6)
+    s[..., 4:8] = mn[..., 0:4] | ((mn[..., 4:8] >> 4) << 6)
+    s[..., 8:12] = (sc[..., 4:8] & 15) | ((mn[..., 4:8] & 15) << 4)
+    qq = q.astype(np.uint8).reshape(n, nb, 4, 2, 32)  # [c][lo/hi][l]
+    out[..., 16:144] = (qq[..., 0, :] | (qq[..., 1, :] << 4)).reshape(n, nb, 128)
+    return out.reshape(n, nb * 144)
+
+
+def pack_q6k(d, sc, q) -> np.ndarray:
+    """Pack Q6_K element arrays (q in [-32, 31]) into 210-byte blocks.
+
+    For half h, l < 32, u = q + 32:
+      ql[64h+l]    = u[128h+l]    & 15 | (u[128h+64+l] & 15) << 4
+      ql[64h+32+l] = u[128h+32+l] & 15 | (u[128h+96+l] & 15) << 4
+      qh[32h+l]    = u[128h+l]>>4 | u[128h+32+l]>>4 << 2 | u[128h+64+l]>>4 << 4 | u[128h+96+l]>>4 << 6
+    """
+    n, nb = d.shape
+    out = np.empty((n, nb, 210), dtype=np.uint8)
+    u = (q.astype(np.int16) + 32).astype(np.uint8).reshape(n, nb, 2, 4, 32)  # [h][g][l]
+    ql = out[..., 0:128].reshape(n, nb, 2, 2, 32)  # [h][first/second 32][l]
+    ql[..., 0, :] = (u[..., 0, :] & 15) | ((u[..., 2, :] & 15) << 4)
+    ql[..., 1, :] = (u[..., 1, :] & 15) | ((u[..., 3, :] & 15) << 4)
+    qh = out[..., 128:192].reshape(n, nb, 2, 32)
+    qh[...] = (u[..., 0, :] >> 4) | ((u[..., 1, :] >> 4) << 2) | ((u[..., 2, :] >> 4) << 4) | ((u[..., 3, :] >> 4) << 6)
+    out[..., 192:208] = sc.astype(np.int8).view(np.uint8)
+    out[..., 208:210] = d.astype(np.float16).view(np.uint8).reshape(n, nb, 2)
+    return out.reshape(n, nb * 210)
+
+
+def pack_q8_0(d, q) -> np.ndarray:
+    n, nb = d.shape
+    out = np.empty((n, nb, 34), dtype=np.uint8)
+    out[..., 0:2] = d.astype(np.float16).view(np.uint8).reshape(n, nb, 2)
+    out[..., 2:34] = q.astype(np.int8).view(np.uint8)
+    return out.reshape(n, nb * 34)
+
+
+def make_weight(type_: int, n: int, k: int, seed: int = 0, rng: np.random.Generator | None = None) -> QWeight:
+    """A seeded random weight of `n` rows by `k` columns in GGUF block format."""
+    if rng is None:
+        rng = np.random.default_rng(seed)
+    blk = BLOCK_ELEMS[type_]
+    if k % blk:
+        raise ValueError(f"k={k} is not a multiple of the block size {blk}")
+    nb = k // blk
+    if type_ == TYPE_Q4_K:
+        d = _half_abs_normal(rng, (n, nb))
+        dmin = _half_abs_normal(rng, (n, nb))
+        sc = rng.integers(0, 64, size=(n, nb, 8), dtype=np.uint8)
+        mn = rng.integers(0, 64, size=(n, nb, 8), dtype=np.uint8)
+        q = rng.integers(0, 16, size=(n, nb, 256), dtype=np.uint8)
+        return QWeight(type_, n, k, pack_q4k(d, dmin, sc, mn, q), d, dmin, sc, mn, q)
+    if type_ == TYPE_Q6_K:
+        d = _half_abs_normal(rng, (n, nb))
+        sc = rng.integers(-32, 32, size=(n, nb, 16), dtype=np.int8)
+        q = (rng.integers(0, 64, size=(n, nb, 256), dtype=np.uint8).astype(np.int16) - 32).astype(np.int8)
+        return QWeight(type_, n, k, pack_q6k(d, sc, q), d, None, sc, None, q)
+    if type_ == TYPE_Q8_0:
+        d = _half_abs_normal(rng, (n, nb))
+        q = rng.integers(-127, 128, size=(n, nb, 32), dtype=np.int8)
+        return QWeight(type_, n, k, pack_q8_0(d, q), d, None, None, None, q)
+    raise ValueError(f"unsupported weight type {type_}")
+
+
+def make_activation(m: int, k: int, seed: int = 0, rng: np.random.Generator | None = None) -> np.ndarray:
+    """f32 [m, k] drawn from N(0, 1)."""
+    if rng is None:
+        rng = np.random.default_rng(seed)
+    return rng.standard_normal(size=(m, k), dtype=np.float32)
+
+
+def weight_bytes(type_: int, n: int, k: int) -> int:
+    return n * (k // BLOCK_ELEMS[type_]) * BLOCK_BYTES[type_]
+
+
+def act_bytes(type_: int, m: int, k: int) -> int:
+    """Bytes of the quantised activation a weight of `type_` is dotted with."""
+    if type_ == TYPE_Q8_0:
+        return m * (k // QK8_0) * 34
+    return m * (k // QK_K) * 292

@@ -1,0 +1,184 @@
+"""ctypes front end of the CPU oracle (oracle.c).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and
+bench.py's cpu_baseline leg, never by the product package.  The C code
+restates candle-core 0.8.4's quantized matmul (the path behind
+native/arm_ai_nif/src/llama_candle.rs:93, :119); see oracle.h for the
+per-function reference and how each is pinned.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+
+Q4_K, Q6_K, Q8_0, Q8_K = 12, 14, 8, 15
+BLOCK_BYTES = {Q4_K: 144, Q6_K: 210, Q8_0: 34, Q8_K: 292}
+BLOCK_ELEMS = {Q4_K: 256, Q6_K: 256, Q8_0: 32, Q8_K: 256}
+
+_lib = None
+
+
+def build() -> str:
+    """Compile liboracle.so with its Makefile (gcc; no GPU needed)."""
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+    return LIB_PATH
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = ctypes.CDLL(LIB_PATH)
+        P = ctypes.c_void_p
+        i64 = ctypes.c_int64
+        L.orc_f16_to_f32.argtypes = [ctypes.c_uint16]
+        L.orc_f16_to_f32.restype = ctypes.c_float
+        L.orc_f32_to_f16.argtypes = [ctypes.c_float]
+        L.orc_f32_to_f16.restype = ctypes.c_uint16
+        L.orc_f16_to_f32_n.argtypes = [P, i64, P]
+        L.orc_f16_to_f32_n.restype = None
+        L.orc_f32_to_f16_n.argtypes = [P, i64, P]
+        L.orc_f32_to_f16_n.restype = None
+        for f in ("orc_quantize_row_q8k", "orc_quantize_row_q8_0"):
+            getattr(L, f).argtypes = [P, i64, P]
+            getattr(L, f).restype = ctypes.c_int
+        for f in ("orc_vec_dot_q4k_q8k", "orc_vec_dot_q6k_q8k", "orc_vec_dot_q8_0_q8_0"):
+            getattr(L, f).argtypes = [i64, P, P]
+            getattr(L, f).restype = ctypes.c_float
+        L.orc_block_sums.argtypes = [ctypes.c_int, i64, P, P, P, P]
+        L.orc_block_sums.restype = None
+        L.orc_matmul.argtypes = [ctypes.c_int, i64, i64, i64, P, P, P, ctypes.c_int]
+        L.orc_matmul.restype = ctypes.c_int
+        L.orc_matmul_preq.argtypes = [ctypes.c_int, i64, i64, i64, P, P, P, ctypes.c_int]
+        L.orc_matmul_preq.restype = ctypes.c_int
+        L.orc_dequantize_row.argtypes = [ctypes.c_int, P, i64, P]
+        L.orc_dequantize_row.restype = ctypes.c_int
+        L.orc_max_threads.argtypes = []
+        L.orc_max_threads.restype = ctypes.c_int
+        _lib = L
+    return _lib
+
+
+def _p(a: np.ndarray) -> int:
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data
+
+
+def f16_to_f32(bits: np.ndarray) -> np.ndarray:
+    b = np.ascontiguousarray(bits, np.uint16).ravel()
+    out = np.empty(b.size, np.float32)
+    lib().orc_f16_to_f32_n(_p(b), b.size, _p(out))
+    return out
+
+
+def f32_to_f16(x: np.ndarray) -> np.ndarray:
+    f = np.ascontiguousarray(x, np.float32).ravel()
+    out = np.empty(f.size, np.uint16)
+    lib().orc_f32_to_f16_n(_p(f), f.size, _p(out))
+    return out
+
+
+def act_type(wtype: int) -> int:
+    return Q8_0 if wtype == Q8_0 else Q8_K
+
+
+def quantize(x: np.ndarray, atype: int = Q8_K) -> np.ndarray:
+    """Quantise f32 rows [m, k] to Q8_K (or Q8_0) block bytes [m, k/blk*bytes]."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    if x.ndim == 1:
+        x = x[None, :]
+    m, k = x.shape
+    blk, nbytes = BLOCK_ELEMS[atype], BLOCK_BYTES[atype]
+    if k % blk:
+        raise ValueError("k not a multiple of the block size")
+    out = np.zeros((m, k // blk * nbytes), np.uint8)
+    f = lib().orc_quantize_row_q8k if atype == Q8_K else lib().orc_quantize_row_q8_0
+    for r in range(m):
+        rc = f(_p(x[r]), k, out[r].ctypes.data)
+        assert rc == 0
+    return out
+
+
+def q8k_fields(blocks: np.ndarray):
+    """Split Q8_K block bytes [..., nb*292] into (d f32 [..,nb], qs i8 [..,nb,256], bsums i16 [..,nb,16])."""
+    b = np.ascontiguousarray(blocks).reshape(*blocks.shape[:-1], -1, 292)
+    d = b[..., 0:4].copy().view(np.float32)[..., 0]
+    qs = b[..., 4:260].copy().view(np.int8)
+    bs = b[..., 260:292].copy().view(np.int16)
+    return d, qs, bs
+
+
+def q8_0_fields(blocks: np.ndarray):
+    b = np.ascontiguousarray(blocks).reshape(*blocks.shape[:-1], -1, 34)
+    d = b[..., 0:2].copy().view(np.float16)[..., 0]
+    qs = b[..., 2:34].copy().view(np.int8)
+    return d, qs
+
+
+def vec_dot(wtype: int, k: int, wrow: np.ndarray, xq_row: np.ndarray) -> float:
+    L = lib()
+    f = {Q4_K: L.orc_vec_dot_q4k_q8k, Q6_K: L.orc_vec_dot_q6k_q8k, Q8_0: L.orc_vec_dot_q8_0_q8_0}[wtype]
+    wrow = np.ascontiguousarray(wrow)
+    xq_row = np.ascontiguousarray(xq_row)
+    return float(f(k, _p(wrow), _p(xq_row)))
+
+
+def block_sums(wtype: int, k: int, w: np.ndarray, xq: np.ndarray):
+    """Integer sums per (m, n, block): returns S, Smin int32 [m, n, nb]."""
+    w = np.ascontiguousarray(w)
+    xq = np.ascontiguousarray(xq)
+    n = w.shape[0]
+    m = xq.shape[0]
+    nb = k // BLOCK_ELEMS[wtype]
+    S = np.zeros((m, n, nb), np.int32)
+    Sm = np.zeros((m, n, nb), np.int32)
+    L = lib()
+    for i in range(m):
+        for j in range(n):
+            L.orc_block_sums(wtype, k, w[j].ctypes.data, xq[i].ctypes.data, S[i, j].ctypes.data, Sm[i, j].ctypes.data)
+    return S, Sm
+
+
+def matmul(wtype: int, x: np.ndarray, w: np.ndarray, n: int, k: int, nthreads: int = 0) -> np.ndarray:
+    """k_quants::matmul: f32 [m, k] x W[n, k]^T -> f32 [m, n]."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    if x.ndim == 1:
+        x = x[None, :]
+    m = x.shape[0]
+    w = np.ascontiguousarray(w)
+    dst = np.zeros((m, n), np.float32)
+    rc = lib().orc_matmul(wtype, m, k, n, _p(x), _p(w), _p(dst), nthreads)
+    if rc != 0:
+        raise ValueError(f"orc_matmul failed: {rc}")
+    return dst
+
+
+def matmul_preq(wtype: int, xq: np.ndarray, w: np.ndarray, n: int, k: int, nthreads: int = 0) -> np.ndarray:
+    xq = np.ascontiguousarray(xq)
+    w = np.ascontiguousarray(w)
+    m = xq.shape[0]
+    dst = np.zeros((m, n), np.float32)
+    rc = lib().orc_matmul_preq(wtype, m, k, n, _p(xq), _p(dst), _p(w), nthreads)
+    if rc != 0:
+        raise ValueError(f"orc_matmul_preq failed: {rc}")
+    return dst
+
+
+def dequantize(wtype: int, w: np.ndarray, k: int) -> np.ndarray:
+    w = np.ascontiguousarray(w)
+    out = np.zeros((w.shape[0], k), np.float32)
+    for r in range(w.shape[0]):
+        rc = lib().orc_dequantize_row(wtype, w[r].ctypes.data, k, out[r].ctypes.data)
+        assert rc == 0
+    return out
+
+
+def max_threads() -> int:
+    return int(lib().orc_max_threads())

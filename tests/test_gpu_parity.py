@@ -1,0 +1,221 @@
+"""GPU parity: the HIP kernels, called through the C ABI, against the oracle.
+
+Bars (task statement): Q8_K / Q8_0 activation quantisation and every integer
+block dot product bit-exact; f32 outputs within max relative error 1e-5
+(1e-4 for K >= 14336), measured as rel_max and rel_cond (tests/_metrics.py).
+"""
+import numpy as np
+import pytest
+
+import arm_ai_amd as A
+import oracle as O
+from arm_ai_amd import synth as S
+from tests._metrics import rel_cond, rel_max, tol_for_k
+
+pytestmark = pytest.mark.gpu
+
+
+def _xdeq_abs(x, wtype):
+    xq = O.quantize(x, O.act_type(wtype))
+    if wtype == O.Q8_0:
+        d, q = O.q8_0_fields(xq)
+    else:
+        d, q, _ = O.q8k_fields(xq)
+    return xq, np.abs(d.astype(np.float32)[..., None] * q).reshape(x.shape[0], -1)
+
+
+def check_matmul(ctx, W, x, *, sums=True, cond=True):
+    wtype = W.type
+    mm = A.QMatMul.from_qtensor(A.QTensor(wtype, (W.n, W.k), W.blocks), ctx)
+    y = mm.forward(x)
+    xq, xabs = _xdeq_abs(x, wtype)
+    r = O.matmul_preq(wtype, xq, W.blocks, W.n, W.k)
+    tol = tol_for_k(W.k)
+    rm = rel_max(y, r)
+    assert np.all(np.isfinite(y))
+    assert rm <= tol, f"rel_max {rm:.3e} > {tol}"
+    if cond:
+        rc = rel_cond(y, r, W, xabs)
+        assert rc <= tol, f"rel_cond {rc:.3e} > {tol}"
+    if sums:
+        gS, gSm = mm.block_sums(x)
+        oS, oSm = O.block_sums(wtype, W.k, W.blocks, xq)
+        assert np.array_equal(gS, oS), "integer block sums S differ"
+        assert np.array_equal(gSm, oSm), "integer block sums Smin differ"
+    mm.free()
+    return y, r
+
+
+# ------------------------------------------------------------ quantizers
+def _edge_rows(k):
+    rng = np.random.default_rng(17)
+    rows = [
+        np.zeros(k, np.float32),
+        rng.standard_normal(k).astype(np.float32) * 1e-30,  # tiny values
+        rng.standard_normal(k).astype(np.float32) * 1e30,
+        np.full(k, -2.0, np.float32),  # all equal: first element is the max
+    ]
+    r = np.zeros(k, np.float32)
+    r[0], r[1], r[2], r[3], r[4] = -128.0, 2.5, -2.5, 0.5, 1.5  # ties-away rounding
+    r[300 % k], r[301 % k] = 3.0, -3.0
+    rows.append(r)
+    r = rng.standard_normal(k).astype(np.float32)
+    r[5] = np.nan
+    rows.append(r)
+    r = np.zeros(k, np.float32)
+    r[::37] = np.float32(1e-40)  # f32 subnormals
+    rows.append(r)
+    return np.stack(rows)
+
+
+@pytest.mark.parametrize("m,k", [(1, 2048), (8, 4096), (3, 14336), (512, 2048), (2, 256)])
+def test_quantize_q8k_bitexact(ctx, m, k):
+    x = S.make_activation(m, k, seed=m * 7 + k)
+    x = np.concatenate([x, _edge_rows(k)])
+    got = A.quantize_q8k(ctx, x)
+    want = O.quantize(x, O.Q8_K)
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("m,k", [(1, 2048), (5, 4096), (64, 1024), (1, 32)])
+def test_quantize_q8_0_bitexact(ctx, m, k):
+    x = S.make_activation(m, k, seed=m + k)
+    x = np.concatenate([x, _edge_rows(k)])
+    x[-3, :] *= np.float32(65504.0 * 127)  # f16 overflow of d -> inf
+    got = A.quantize_q8_0(ctx, x)
+    want = O.quantize(x, O.Q8_0)
+    assert np.array_equal(got, want)
+
+
+# --------------------------------------------------- benchmark configurations
+def test_config0_q4k_tinyllama_ffn_up(ctx):
+    W = S.make_weight(S.TYPE_Q4_K, 5632, 2048, seed=0)
+    x = S.make_activation(1, 2048, seed=0)
+    check_matmul(ctx, W, x)
+
+
+def test_config1_q8_0(ctx):
+    W = S.make_weight(S.TYPE_Q8_0, 2048, 2048, seed=1)
+    x = S.make_activation(1, 2048, seed=1)
+    check_matmul(ctx, W, x)
+
+
+def test_config1_q6k_lm_head(ctx):
+    W = S.make_weight(S.TYPE_Q6_K, 32000, 2048, seed=1)
+    x = S.make_activation(1, 2048, seed=2)
+    check_matmul(ctx, W, x)
+
+
+@pytest.mark.parametrize("n,k", [(14336, 4096), (4096, 14336)])
+@pytest.mark.parametrize("m", [1, 8])
+def test_config4_llama3_ffn(ctx, n, k, m):
+    W = S.make_weight(S.TYPE_Q4_K, n, k, seed=4)
+    x = S.make_activation(m, k, seed=40 + m)
+    check_matmul(ctx, W, x, cond=(m == 1))
+
+
+def test_config4_llama3_lm_head_q6k(ctx):
+    W = S.make_weight(S.TYPE_Q6_K, 128256, 4096, seed=5)
+    x = S.make_activation(1, 4096, seed=50)
+    check_matmul(ctx, W, x, sums=False, cond=False)
+
+
+# ------------------------------------------------------ batch and K coverage
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 7, 8, 11])
+@pytest.mark.parametrize("wtype", [S.TYPE_Q4_K, S.TYPE_Q6_K, S.TYPE_Q8_0])
+def test_batches(ctx, wtype, m):
+    W = S.make_weight(wtype, 300, 2048, seed=m + wtype)
+    x = S.make_activation(m, 2048, seed=100 + m)
+    check_matmul(ctx, W, x)
+
+
+@pytest.mark.parametrize("k", [256, 512, 5632, 16384, 20480])
+@pytest.mark.parametrize("wtype", [S.TYPE_Q4_K, S.TYPE_Q6_K, S.TYPE_Q8_0])
+@pytest.mark.parametrize("m", [1, 8])
+def test_k_coverage(ctx, wtype, k, m):
+    W = S.make_weight(wtype, 70, k, seed=k + m)
+    x = S.make_activation(m, k, seed=k)
+    check_matmul(ctx, W, x)
+
+
+def test_single_row_weight(ctx):
+    W = S.make_weight(S.TYPE_Q4_K, 1, 256, seed=3)
+    x = S.make_activation(2, 256, seed=3)
+    check_matmul(ctx, W, x)
+
+
+@pytest.mark.parametrize("wtype", [S.TYPE_Q4_K, S.TYPE_Q6_K, S.TYPE_Q8_0])
+def test_subnormal_and_zero_scales(ctx, wtype):
+    W = S.make_weight(wtype, 128, 1024, seed=8)
+    rng = np.random.default_rng(8)
+    d = (rng.integers(1, 1024, size=W.d.shape).astype(np.uint16)).view(np.float16)  # f16 subnormals
+    d[::5] = 0
+    if wtype == S.TYPE_Q4_K:
+        W.blocks = S.pack_q4k(d, d[:, ::-1].copy(), W.sc, W.mn, W.q)
+        W.dmin = d[:, ::-1].copy()
+    elif wtype == S.TYPE_Q6_K:
+        W.blocks = S.pack_q6k(d, W.sc, W.q)
+    else:
+        W.blocks = S.pack_q8_0(d, W.q)
+    W.d = d
+    x = S.make_activation(3, 1024, seed=9)
+    check_matmul(ctx, W, x, cond=False)
+
+
+# ----------------------------------------------------------- API behaviour
+def test_m_zero_and_shape_errors(ctx):
+    W = S.make_weight(S.TYPE_Q4_K, 16, 512, seed=1)
+    mm = A.QMatMul.from_qtensor(A.QTensor(W.type, (16, 512), W.blocks), ctx)
+    y = mm.forward(np.zeros((0, 512), np.float32))
+    assert y.shape == (0, 16)
+    with pytest.raises(A.QMatMulError):
+        mm.forward(np.zeros((1, 256), np.float32))
+    L = A._lib.load()
+    x = np.zeros((1, 256), np.float32)
+    dst = np.zeros((1, 16), np.float32)
+    rc = L.aq_qmatmul_f32(ctx.handle, mm.handle, x.ctypes.data, 1, 256, dst.ctypes.data)
+    assert rc == A._lib.AQ_ERR_SHAPE
+    with pytest.raises(A.AqError):
+        A.QMatMul.from_device_blocks(ctx, 99, (16, 512), 1, 16 * 2 * 144)
+    mm.free()
+
+
+def test_higher_rank_input_and_determinism(ctx):
+    W = S.make_weight(S.TYPE_Q6_K, 96, 1024, seed=2)
+    mm = A.QMatMul.from_qtensor(A.QTensor(W.type, (96, 1024), W.blocks), ctx)
+    x = S.make_activation(6, 1024, seed=2).reshape(2, 3, 1024)
+    y1 = mm.forward(x)
+    y2 = mm.forward(x)
+    assert y1.shape == (2, 3, 96)
+    assert np.array_equal(y1, y2)
+    r = O.matmul(W.type, x.reshape(6, 1024), W.blocks, 96, 1024).reshape(2, 3, 96)
+    assert rel_max(y1, r) <= 1e-5
+    mm.free()
+
+
+@pytest.mark.parametrize("wtype,m", [(S.TYPE_Q4_K, 4), (S.TYPE_Q6_K, 1), (S.TYPE_Q8_0, 8), (S.TYPE_Q4_K, 40)])
+def test_device_pointer_entry_points(ctx, wtype, m):
+    from arm_ai_amd import hip
+
+    W = S.make_weight(wtype, 512, 2048, seed=12)
+    x = S.make_activation(m, 2048, seed=12)
+    mm = A.QMatMul.from_qtensor(A.QTensor(W.type, (512, 2048), W.blocks), ctx)
+    y_host = mm.forward(x)
+    dx = hip.to_device(x)
+    dy = hip.DeviceBuffer(m * 512 * 4)
+    mm.forward_device(dx.ptr, m, dy.ptr)
+    ctx.synchronize()
+    assert np.array_equal(dy.download(np.float32, (m, 512)), y_host)
+    # quantise once, reuse: same bytes as the fused call
+    act = hip.DeviceBuffer(A.act_bytes(mm.act_type, m, 2048))
+    A.quantize_act_device(ctx, mm.act_type, dx.ptr, m, 2048, act.ptr)
+    dy2 = hip.DeviceBuffer(m * 512 * 4)
+    mm.forward_preq_device(act.ptr, m, dy2.ptr)
+    ctx.synchronize()
+    assert np.array_equal(dy2.download(np.float32, (m, 512)), y_host)
+    # weights uploaded from device memory give the same result
+    dblocks = hip.to_device(W.blocks)
+    mm2 = A.QMatMul.from_device_blocks(ctx, W.type, (512, 2048), dblocks.ptr, W.blocks.size)
+    assert np.array_equal(mm2.forward(x), y_host)
+    mm.free()
+    mm2.free()

@@ -1,0 +1,296 @@
+"""Pins the CPU oracle (oracle/oracle.c) before anything is checked against it.
+
+The reference holds no golden vectors for this path (its only model test
+needs a downloaded GGUF, test/llama_candle_model_test.exs:2-4), and candle's
+source is not in this image.  The oracle is therefore pinned by
+* library routines (numpy IEEE f16 conversion),
+* closed-form known answers built so that the plausible mistakes (ties-to-even
+  instead of ties-away, last-max instead of first-max, missing clamp, wrong
+  sign of d, unrounded vs f16-rounded Q8_0 d) each give a different byte,
+* exact integer sums computed from the generator's element arrays, which never
+  go through the oracle's unpacking code (a swapped nibble, scale/min mix-up
+  or wrong sub-scale index changes them),
+* f64 dequantise-then-dot truth,
+* the reference's own Q6_K bit layout (shape_ops.rs:2848-2899), restated.
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+from arm_ai_amd import synth as S
+from tests._metrics import rel_cond, rel_max
+
+
+# ------------------------------------------------------------------ f16
+def test_f16_to_f32_all_half_values():
+    bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    got = O.f16_to_f32(bits)
+    want = bits.view(np.float16).astype(np.float32)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+
+
+def test_f32_to_f16_matches_numpy_rne():
+    rng = np.random.default_rng(0)
+    bits = rng.integers(0, 2**32, size=400_000, dtype=np.uint64).astype(np.uint32)
+    # dense coverage of the f16 range, halfway cases and subnormals
+    f16_all = np.arange(65536, dtype=np.uint32).astype(np.uint16).view(np.float16).astype(np.float32)
+    f16_all = f16_all[np.isfinite(f16_all)]
+    nxt = np.nextafter(f16_all.astype(np.float16), np.float16(np.inf)).astype(np.float32)
+    mids = ((f16_all.astype(np.float64) + nxt.astype(np.float64)) / 2).astype(np.float32)
+    extra = np.array([0.0, -0.0, 65504.0, 65520.0, 65519.99, 1e-8, 2.0**-25, 2.0**-24, 3 * 2.0**-26], np.float32)
+    x = np.concatenate([bits.view(np.float32), f16_all, mids, np.nextafter(mids, np.float32(0)), extra])
+    got = O.f32_to_f16(x)
+    want = x.astype(np.float16).view(np.uint16)
+    nan = np.isnan(x)
+    assert np.array_equal(got[~nan], want[~nan])
+    assert np.all((got[nan] & 0x7C00) == 0x7C00) and np.all((got[nan] & 0x03FF) != 0)
+
+
+# --------------------------------------------------------------- Q8_K
+def _q8k(x):
+    blocks = O.quantize(np.asarray(x, np.float32)[None, :], O.Q8_K)
+    d, qs, bs = O.q8k_fields(blocks)
+    return d[0], qs[0], bs[0]
+
+
+def test_q8k_known_answers_rounding_and_scale():
+    x = np.zeros(256, np.float32)
+    x[0] = -128.0  # max |x| -> max = -128 -> iscale = 1.0, d = 1.0
+    x[1], x[2], x[3], x[4], x[5] = 2.5, -2.5, 0.5, 1.5, 127.4
+    d, qs, bs = _q8k(x)
+    assert d[0] == np.float32(1.0)
+    # ties away from zero (Rust f32::round): 2.5 -> 3, -2.5 -> -3, 0.5 -> 1, 1.5 -> 2
+    assert list(qs[0, :6]) == [-128, 3, -3, 1, 2, 127]
+    assert bs[0, 0] == int(qs[0, :16].astype(np.int32).sum())
+
+
+def test_q8k_first_max_wins_and_clamp():
+    x = np.zeros(256, np.float32)
+    x[5], x[9] = 3.0, -3.0  # equal |x|: the first (+3) is `max`
+    x[17] = 1.0
+    d, qs, bs = _q8k(x)
+    iscale = np.float32(-128.0) / np.float32(3.0)
+    assert d[0] == np.float32(1.0) / iscale and d[0] < 0
+    assert qs[0, 5] == -128
+    assert qs[0, 9] == 127  # round(+128) clamped by min(127)
+    assert qs[0, 17] == int(np.round(np.float64(iscale * np.float32(1.0))))
+    assert bs[0, 0] == -1 and bs[0, 1] == qs[0, 17]
+
+
+def test_q8k_zero_block_and_nan():
+    x = np.zeros(512, np.float32)
+    x[256 + 3] = np.nan  # NaN never becomes the max; round(NaN).min(127) -> 127
+    x[256 + 7] = -2.0
+    d, qs, bs = _q8k(x)
+    assert d[0] == 0 and not qs[0].any() and not bs[0].any()
+    assert d[1] == np.float32(1.0) / (np.float32(-128.0) / np.float32(-2.0))
+    assert qs[1, 3] == 127 and qs[1, 7] == -128
+
+
+def test_q8k_invariants_random():
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((4, 4096), dtype=np.float32) * rng.uniform(0.01, 100, size=(4, 1)).astype(np.float32)
+    blocks = O.quantize(x, O.Q8_K)
+    d, qs, bs = O.q8k_fields(blocks)
+    xb = x.reshape(4, 16, 256)
+    assert np.array_equal(bs, qs.reshape(4, 16, 16, 16).astype(np.int32).sum(-1).astype(np.int16))
+    first = np.abs(xb).argmax(-1)  # numpy argmax returns the first maximum
+    assert np.all(np.take_along_axis(qs, first[..., None], -1) == -128)
+    mx = np.take_along_axis(xb, first[..., None], -1)[..., 0]
+    assert np.allclose(d, -mx / 128.0, rtol=1e-6)
+    err = np.abs(d[..., None].astype(np.float64) * qs - xb)
+    clamped = qs == 127
+    assert np.all(err[~clamped] <= np.abs(d[..., None].repeat(256, -1))[~clamped] * 0.5 * (1 + 1e-5))
+    assert np.all(err[clamped] <= np.abs(d[..., None].repeat(256, -1))[clamped] * 1.5)
+
+
+# --------------------------------------------------------------- Q8_0
+def test_q8_0_known_answers():
+    x = np.zeros(64, np.float32)
+    x[:4] = [127.0, 63.5, -63.5, 0.5]
+    x[32] = 1.0
+    x[33] = 0.5
+    blocks = O.quantize(x[None], O.Q8_0)
+    d, qs = O.q8_0_fields(blocks)
+    assert d[0, 0] == np.float16(1.0)
+    assert list(qs[0, 0, :4]) == [127, 64, -64, 1]
+    # d = 1/127 is stored f16-rounded; q uses the unrounded f32 id = 1/d
+    d1 = np.float32(1.0) / np.float32(127.0)
+    assert d[0, 1].view(np.uint16) == np.float32(d1).astype(np.float16).view(np.uint16)
+    id1 = np.float32(1.0) / d1
+    assert qs[0, 1, 0] == 127 and qs[0, 1, 1] == int(np.trunc(np.float64(np.float32(0.5) * id1) + 0.5))
+
+
+# -------------------------------------------------- weights: layouts and sums
+def _int_sums(W, xq, wtype):
+    """S, Smin [m, n, nb] from the generator's element arrays (no unpacking)."""
+    m = xq.shape[0]
+    if wtype == O.Q8_0:
+        _, qx = O.q8_0_fields(xq)  # [m, nb, 32]
+        Sx = np.einsum("nbe,mbe->mnb", W.q.astype(np.int64), qx.astype(np.int64))
+        return Sx, np.zeros_like(Sx)
+    _, qx, bs = O.q8k_fields(xq)  # [m, nb, 256], [m, nb, 16]
+    if wtype == O.Q4_K:
+        isum = np.einsum("nbje,mbje->mnbj", W.q.reshape(W.n, -1, 8, 32).astype(np.int64),
+                         qx.reshape(m, -1, 8, 32).astype(np.int64))
+        Sx = (isum * W.sc.astype(np.int64)[None]).sum(-1)
+        Sm = np.einsum("mbg,nbg->mnb", bs.astype(np.int64), np.repeat(W.mn.astype(np.int64), 2, axis=-1))
+        return Sx, Sm
+    isum = np.einsum("nbje,mbje->mnbj", W.q.reshape(W.n, -1, 16, 16).astype(np.int64),
+                     qx.reshape(m, -1, 16, 16).astype(np.int64))
+    Sx = (isum * W.sc.astype(np.int64)[None]).sum(-1)
+    return Sx, np.zeros_like(Sx)
+
+
+WTYPES = [O.Q4_K, O.Q6_K, O.Q8_0]
+
+
+@pytest.mark.parametrize("wtype", WTYPES)
+@pytest.mark.parametrize("k", [256, 2048, 5632])
+def test_block_sums_exact(wtype, k):
+    W = S.make_weight(wtype, 24, k, seed=k + wtype)
+    x = S.make_activation(3, k, seed=7)
+    xq = O.quantize(x, O.act_type(wtype))
+    got_S, got_Sm = O.block_sums(wtype, k, W.blocks, xq)
+    want_S, want_Sm = _int_sums(W, xq, wtype)
+    assert np.array_equal(got_S, want_S)
+    assert np.array_equal(got_Sm, want_Sm)
+
+
+@pytest.mark.parametrize("wtype", WTYPES)
+def test_dequantize_matches_element_arrays(wtype):
+    W = S.make_weight(wtype, 16, 1024, seed=11)
+    got = O.dequantize(wtype, W.blocks, 1024).astype(np.float64)
+    want = W.dequantize()
+    assert np.allclose(got, want, rtol=1e-6, atol=1e-7)
+
+
+@pytest.mark.parametrize("wtype", WTYPES)
+def test_matmul_vs_f64_truth(wtype):
+    k = 2048
+    W = S.make_weight(wtype, 96, k, seed=5)
+    x = S.make_activation(2, k, seed=6)
+    xq = O.quantize(x, O.act_type(wtype))
+    if wtype == O.Q8_0:
+        dx, qx = O.q8_0_fields(xq)
+    else:
+        dx, qx, _ = O.q8k_fields(xq)
+    xdeq = (dx.astype(np.float64)[..., None] * qx).reshape(2, k)
+    truth = xdeq @ W.dequantize().T
+    got = O.matmul(wtype, x, W.blocks, 96, k)
+    assert rel_max(got, truth) < 1e-6
+    assert rel_cond(got, truth, W, np.abs(xdeq)) < 1e-6
+
+
+def test_q4k_scale_unpack_two_formulations():
+    """GGML get_scale_min_k4 (restated here) must invert the generator's pack for all 64x64 values."""
+    sc = np.repeat(np.arange(64, dtype=np.uint8), 64).reshape(-1, 1, 1).repeat(8, axis=2)
+    mn = np.tile(np.arange(64, dtype=np.uint8), 64).reshape(-1, 1, 1).repeat(8, axis=2)
+    n = sc.shape[0]
+    one = np.ones((n, 1), np.float16)
+    blocks = S.pack_q4k(one, one, sc, mn, np.zeros((n, 1, 256), np.uint8)).reshape(n, 144)
+    q = blocks[:, 4:16].astype(np.int32)
+    for j in range(8):
+        if j < 4:
+            s, m = q[:, j] & 63, q[:, j + 4] & 63
+        else:
+            s = (q[:, j + 4] & 0xF) | ((q[:, j - 4] >> 6) << 4)
+            m = (q[:, j + 4] >> 4) | ((q[:, j] >> 6) << 4)
+        assert np.array_equal(s, sc[:, 0, j]) and np.array_equal(m, mn[:, 0, j])
+
+
+def _ref_dequantize_q6_k(block_bytes: np.ndarray) -> np.ndarray:
+    """Restatement of the reference's shape_ops.rs:2848-2899 (dequantize_q6_k),
+    including its sub-scale indexing (scales[8n + {0,2,4,6}] for all l)."""
+    out = np.zeros(256, np.float64)
+    ql, qh, scales = block_bytes[0:128], block_bytes[128:192], block_bytes[192:208].view(np.int8)
+    d = float(block_bytes[208:210].view(np.float16)[0])
+    for n in range(2):
+        for l in range(32):
+            qhi = int(qh[32 * n + l])
+            a, b = int(ql[64 * n + l]), int(ql[64 * n + l + 32])
+            q1 = ((a & 0xF) | (((qhi >> 0) & 3) << 4)) - 32
+            q2 = ((b & 0xF) | (((qhi >> 2) & 3) << 4)) - 32
+            q3 = (((a >> 4) & 0xF) | (((qhi >> 4) & 3) << 4)) - 32
+            q4 = (((b >> 4) & 0xF) | (((qhi >> 6) & 3) << 4)) - 32
+            s = [int(scales[8 * n + i]) for i in (0, 2, 4, 6)]
+            out[128 * n + l + 0] = d * s[0] * q1
+            out[128 * n + l + 32] = d * s[1] * q2
+            out[128 * n + l + 64] = d * s[2] * q3
+            out[128 * n + l + 96] = d * s[3] * q4
+    return out
+
+
+def test_q6k_layout_vs_reference_dequantizer():
+    rng = np.random.default_rng(21)
+    W = S.make_weight(O.Q6_K, 4, 512, seed=21)
+    # make odd sub-scales equal to the even ones, where the reference's
+    # indexing and GGML's agree, then repack
+    sc = W.sc.copy()
+    sc[..., 1::2] = sc[..., 0::2]
+    blocks = S.pack_q6k(W.d, sc, W.q).reshape(4, 2, 210)
+    ours = O.dequantize(O.Q6_K, blocks.reshape(4, -1), 512).reshape(4, 2, 256)
+    for r in range(4):
+        for b in range(2):
+            ref = _ref_dequantize_q6_k(blocks[r, b])
+            assert np.allclose(ours[r, b], ref, rtol=1e-6, atol=0), (r, b)
+    del rng
+
+
+def test_special_case_reduces_to_int8_dot():
+    """sc=1, m=0, d=1, dmin=0 turns Q4_K . Q8_K into d_x * sum q*qx."""
+    rng = np.random.default_rng(1)
+    n, k = 8, 512
+    nb = k // 256
+    q = rng.integers(0, 16, (n, nb, 256), dtype=np.uint8)
+    blocks = S.pack_q4k(np.ones((n, nb), np.float16), np.zeros((n, nb), np.float16),
+                        np.ones((n, nb, 8), np.uint8), np.zeros((n, nb, 8), np.uint8), q)
+    x = S.make_activation(1, k, seed=2)
+    xq = O.quantize(x, O.Q8_K)
+    dx, qx, _ = O.q8k_fields(xq)
+    want = (q.astype(np.int64) * qx[0].astype(np.int64)[None]).sum(-1)  # [n, nb]
+    want_f = (want * dx[0].astype(np.float64)[None]).sum(-1)
+    got = O.matmul_preq(O.Q4_K, xq, blocks, n, k)[0]
+    assert np.allclose(got, want_f, rtol=1e-6)
+
+
+def test_matmul_thread_count_independent_and_rowwise():
+    W = S.make_weight(O.Q4_K, 700, 1024, seed=9)
+    x = S.make_activation(3, 1024, seed=10)
+    a = O.matmul(O.Q4_K, x, W.blocks, 700, 1024, nthreads=1)
+    b = O.matmul(O.Q4_K, x, W.blocks, 700, 1024, nthreads=4)
+    assert np.array_equal(a, b)
+    for r in range(3):
+        assert np.array_equal(O.matmul(O.Q4_K, x[r], W.blocks, 700, 1024, nthreads=2)[0], a[r])
+
+
+def test_matmul_rejects_bad_shapes():
+    with pytest.raises(ValueError):
+        O.matmul(O.Q4_K, np.zeros((1, 300), np.float32), np.zeros((1, 144), np.uint8), 1, 300)
+    with pytest.raises(ValueError):
+        O.matmul(99, np.zeros((1, 256), np.float32), np.zeros((1, 144), np.uint8), 1, 256)
+
+
+def test_planted_mistakes_are_caught():
+    """Each check above fails for a plausible oracle mistake, planted here on the CPU."""
+    k = 512
+    W = S.make_weight(O.Q4_K, 8, k, seed=4)
+    x = S.make_activation(1, k, seed=5)
+    xq = O.quantize(x, O.Q8_K)
+    want_S, want_Sm = _int_sums(W, xq, O.Q4_K)
+    # (1) low/high nibble swapped in the unpack
+    swapped = W.blocks.reshape(8, 2, 144).copy()
+    qs = swapped[..., 16:]
+    swapped[..., 16:] = ((qs & 0x0F) << 4) | (qs >> 4)
+    S1, _ = O.block_sums(O.Q4_K, k, swapped.reshape(8, -1), xq)
+    assert not np.array_equal(S1, want_S)
+    # (2) scales and mins exchanged
+    sw = S.pack_q4k(W.d, W.dmin, W.mn, W.sc, W.q)
+    S2, Sm2 = O.block_sums(O.Q4_K, k, sw, xq)
+    assert not np.array_equal(S2, want_S) and not np.array_equal(Sm2, want_Sm)
+    # (3) ties-to-even instead of ties-away in Q8_K
+    xx = np.zeros(256, np.float32)
+    xx[0], xx[1] = -128.0, 2.5
+    assert _q8k(xx)[1][0, 1] != int(np.rint(2.5))
