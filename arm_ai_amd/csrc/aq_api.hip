@@ -3,9 +3,11 @@
 // Host-side replacement for candle-core 0.8.4's QMatMul / QTensor on the
 // CPU (reached from native/arm_ai_nif/src/llama_candle.rs:42 at load and
 // :93 / :119 at prefill / decode).  Weights are uploaded once, repacked into
-// HBM planes, and every matmul runs as: activation quantizer kernel (Q8_K, or
-// Q8_0 for Q8_0 weights) -> matvec (m <= 8) or MFMA GEMM (m > 8) on the
-// context's stream.  Errors are status codes plus a thread-local message;
+// the HBM slab layout (aq_internal.h), and every matmul runs on the context's
+// stream as either one matvec kernel that quantises the f32 activation itself
+// (m <= 8), or the activation quantizer kernel (Q8_K, or Q8_0 for Q8_0
+// weights) followed by the MFMA GEMM (m > 8).  Errors are status codes plus
+// a thread-local message;
 // nothing here aborts (the reference crate builds with panic = "abort",
 // Cargo.toml:33, which this library must not inherit).
 #include <hip/hip_runtime.h>
@@ -36,7 +38,7 @@ struct aq_qweight {
     int64_t n = 0, k = 0;
     void *base = nullptr;
     size_t bytes = 0;
-    WPlanes planes{};
+    WLayout layout{};
 };
 
 namespace {
@@ -74,14 +76,6 @@ int block_bytes(int type) {
     case AQ_TYPE_Q8_0: return 34;
     default: return 0;
     }
-}
-
-// Per-block bytes of each plane (qs, qh, meta, d), see aq_internal.h.
-void plane_bytes(int type, size_t pb[4]) {
-    pb[0] = pb[1] = pb[2] = pb[3] = 0;
-    if (type == AQ_TYPE_Q4_K) { pb[0] = 128; pb[2] = 16; }
-    if (type == AQ_TYPE_Q6_K) { pb[0] = 128; pb[1] = 64; pb[2] = 16; pb[3] = 2; }
-    if (type == AQ_TYPE_Q8_0) { pb[0] = 32; pb[3] = 2; }
 }
 
 int use_device(int device) {
@@ -164,20 +158,31 @@ int check_mm(aq_ctx *ctx, const aq_qweight *w, int64_t m, int64_t k) {
     return AQ_OK;
 }
 
-// Quantise d_x [m][k] into the activation planes at `act`, then run the
-// matmul into d_y.  All on ctx->stream.
+// The matmul of d_x [m][k] into d_y on ctx->stream.  m <= 8 (or no GEMM
+// for this shape): one matvec launch that quantises d_x itself.  m > 8: the
+// quantizer kernel writes the activation planes at `act`, then the GEMM.
 int run_matmul(aq_ctx *ctx, const aq_qweight *w, const float *d_x, int64_t m, float *d_y, void *act, int32_t *dS,
                int32_t *dSmin, void *ws, size_t ws_bytes) {
-    ActPlanes a = act_planes(act, m, w->k);
-    hipError_t e = w->type == AQ_TYPE_Q8_0 ? launch_quantize_q8_0(d_x, m, w->k, a, ctx->stream)
-                                           : launch_quantize_q8k(d_x, m, w->k, a, ctx->stream);
-    if (e != hipSuccess) return fail(AQ_ERR_HIP, "activation quantizer: %s", hipGetErrorString(e));
+    hipError_t e;
     if (use_gemm(w, m)) {
-        e = launch_gemm(w->type, w->planes, w->n, w->k, a, m, d_y, dS, dSmin, ws, ws_bytes, ctx->stream);
+        ActPlanes a = act_planes(act, m, w->k);
+        e = w->type == AQ_TYPE_Q8_0 ? launch_quantize_q8_0(d_x, m, w->k, a, ctx->stream)
+                                    : launch_quantize_q8k(d_x, m, w->k, a, ctx->stream);
+        if (e != hipSuccess) return fail(AQ_ERR_HIP, "activation quantizer: %s", hipGetErrorString(e));
+        e = launch_gemm(w->layout, w->n, w->k, a, m, d_y, dS, dSmin, ws, ws_bytes, ctx->stream);
         if (e == hipSuccess) return AQ_OK;
         if (e != hipErrorNotSupported) return fail(AQ_ERR_HIP, "gemm: %s", hipGetErrorString(e));
+        e = launch_matvec(w->layout, w->n, w->k, nullptr, &a, m, d_y, dS, dSmin, ctx->stream);
+    } else if (((uintptr_t)d_x & 15) == 0) {
+        e = launch_matvec(w->layout, w->n, w->k, d_x, nullptr, m, d_y, dS, dSmin, ctx->stream);
+    } else {
+        // the fused prologue reads float4; quantise separately instead
+        ActPlanes a = act_planes(act, m, w->k);
+        e = w->type == AQ_TYPE_Q8_0 ? launch_quantize_q8_0(d_x, m, w->k, a, ctx->stream)
+                                    : launch_quantize_q8k(d_x, m, w->k, a, ctx->stream);
+        if (e != hipSuccess) return fail(AQ_ERR_HIP, "activation quantizer: %s", hipGetErrorString(e));
+        e = launch_matvec(w->layout, w->n, w->k, nullptr, &a, m, d_y, dS, dSmin, ctx->stream);
     }
-    e = launch_matvec(w->type, w->planes, w->n, w->k, a, m, d_y, dS, dSmin, ctx->stream);
     if (e == hipErrorNotSupported) return fail(AQ_ERR_SHAPE, "k=%lld is larger than the matvec supports", (long long)w->k);
     if (e != hipSuccess) return fail(AQ_ERR_HIP, "matvec: %s", hipGetErrorString(e));
     return AQ_OK;
@@ -264,13 +269,12 @@ static int upload_impl(aq_ctx *ctx, int type, const void *blocks, size_t nbytes,
         return fail(AQ_ERR_SHAPE, "nbytes=%zu != n*k/%d*%d = %zu", nbytes, be, block_bytes(type), row_bytes * (size_t)n);
     int rc = use_device(ctx->device);
     if (rc) return rc;
-    size_t pb[4];
-    plane_bytes(type, pb);
-    size_t off[4], total = 0;
-    for (int i = 0; i < 4; i++) {
-        off[i] = total;
-        total += align_up(pb[i] * nb * (size_t)n, 256);
-    }
+    // slab layout (aq_internal.h): [n][slabs][ng][16] plus, for Q6_K, the d plane [n][ng]
+    const int ng = groups_of(type, k);
+    const int64_t slab_row = (int64_t)slabs_of(type) * ng * 16;
+    const size_t slab_bytes = align_up((size_t)slab_row * (size_t)n, 256);
+    const size_t d_bytes = type == AQ_TYPE_Q6_K ? align_up((size_t)n * ng * 2, 256) : 0;
+    const size_t total = slab_bytes + d_bytes;
     aq_qweight *w = new (std::nothrow) aq_qweight();
     if (!w) return fail(AQ_ERR_OOM, "out of host memory");
     if (hipMalloc(&w->base, total) != hipSuccess) {
@@ -284,10 +288,17 @@ static int upload_impl(aq_ctx *ctx, int type, const void *blocks, size_t nbytes,
     w->k = k;
     w->bytes = total;
     uint8_t *base = (uint8_t *)w->base;
-    w->planes.qs = base + off[0];
-    w->planes.qh = pb[1] ? base + off[1] : nullptr;
-    w->planes.meta = pb[2] ? base + off[2] : nullptr;
-    w->planes.d = pb[3] ? (const uint16_t *)(base + off[3]) : nullptr;
+    w->layout.slab = base;
+    w->layout.d = d_bytes ? (const uint16_t *)(base + slab_bytes) : nullptr;
+    w->layout.type = type;
+    w->layout.ng = ng;
+    w->layout.row_bytes = slab_row;
+
+    int status = AQ_OK;
+    // Q8_0 rows whose block count is not a multiple of 8 end in zero padding blocks
+    if (type == AQ_TYPE_Q8_0 && (k / QK8_0) % 8 != 0 &&
+        hipMemsetAsync(base, 0, slab_bytes, ctx->stream) != hipSuccess)
+        status = fail(AQ_ERR_HIP, "hipMemsetAsync of the weight padding failed");
 
     // Stage whole rows through a bounded device buffer (256 MiB) unless the
     // blocks are already on the device.
@@ -296,15 +307,12 @@ static int upload_impl(aq_ctx *ctx, int type, const void *blocks, size_t nbytes,
     if (rows_per < 1) rows_per = 1;
     if (rows_per > n) rows_per = n;
     void *stage = nullptr;
-    if (!src_on_device) {
+    if (!src_on_device && status == AQ_OK) {
         if (hipMalloc(&stage, (size_t)rows_per * row_bytes) != hipSuccess) {
             (void)hipGetLastError();
-            (void)hipFree(w->base);
-            delete w;
-            return fail(AQ_ERR_OOM, "hipMalloc of the upload staging buffer failed");
+            status = fail(AQ_ERR_OOM, "hipMalloc of the upload staging buffer failed");
         }
     }
-    int status = AQ_OK;
     for (int64_t r0 = 0; r0 < n && status == AQ_OK; r0 += rows_per) {
         const int64_t rows = (n - r0) < rows_per ? (n - r0) : rows_per;
         const uint8_t *src = (const uint8_t *)blocks + (size_t)r0 * row_bytes;
@@ -315,10 +323,8 @@ static int upload_impl(aq_ctx *ctx, int type, const void *blocks, size_t nbytes,
             }
             src = (const uint8_t *)stage;
         }
-        const size_t rb = (size_t)r0 * nb;
-        hipError_t e = launch_repack(type, src, rows, k, base + off[0] + rb * pb[0], pb[1] ? base + off[1] + rb * pb[1] : nullptr,
-                                     pb[2] ? base + off[2] + rb * pb[2] : nullptr, pb[3] ? base + off[3] + rb * pb[3] : nullptr,
-                                     ctx->stream);
+        hipError_t e = launch_repack(type, src, rows, k, base + (size_t)r0 * slab_row,
+                                     d_bytes ? (uint16_t *)(base + slab_bytes) + (size_t)r0 * ng : nullptr, ctx->stream);
         if (e != hipSuccess) status = fail(AQ_ERR_HIP, "repack: %s", hipGetErrorString(e));
         // the staging buffer is reused by the next chunk
         if (status == AQ_OK && hipStreamSynchronize(ctx->stream) != hipSuccess) status = fail(AQ_ERR_HIP, "upload sync failed");
@@ -425,15 +431,15 @@ int aq_qmatmul_preq_device(aq_ctx *ctx, const aq_qweight *w, const void *d_act, 
     if ((uintptr_t)d_act & 255) return fail(AQ_ERR_INVALID_ARG, "activation buffer must be 256-byte aligned");
     if ((rc = use_device(ctx->device))) return rc;
     ActPlanes a = act_planes((void *)d_act, m, k);
+    hipError_t e = hipErrorNotSupported;
     if (use_gemm(w, m)) {
         CallLayout L = call_layout(w, m, false, false, true);
         if ((rc = ensure_scratch(ctx, L.total))) return rc;
-        hipError_t e = launch_gemm(w->type, w->planes, w->n, w->k, a, m, d_dst, nullptr, nullptr,
-                                   (uint8_t *)ctx->scratch + L.ws, L.total - L.ws, ctx->stream);
-        if (e == hipSuccess) return AQ_OK;
-        if (e != hipErrorNotSupported) return fail(AQ_ERR_HIP, "gemm: %s", hipGetErrorString(e));
+        e = launch_gemm(w->layout, w->n, w->k, a, m, d_dst, nullptr, nullptr, (uint8_t *)ctx->scratch + L.ws,
+                        L.total - L.ws, ctx->stream);
+        if (e != hipSuccess && e != hipErrorNotSupported) return fail(AQ_ERR_HIP, "gemm: %s", hipGetErrorString(e));
     }
-    hipError_t e = launch_matvec(w->type, w->planes, w->n, w->k, a, m, d_dst, nullptr, nullptr, ctx->stream);
+    if (e == hipErrorNotSupported) e = launch_matvec(w->layout, w->n, w->k, nullptr, &a, m, d_dst, nullptr, nullptr, ctx->stream);
     if (e == hipErrorNotSupported) return fail(AQ_ERR_SHAPE, "k=%lld is larger than the matvec supports", (long long)w->k);
     if (e != hipSuccess) return fail(AQ_ERR_HIP, "matvec: %s", hipGetErrorString(e));
     return AQ_OK;

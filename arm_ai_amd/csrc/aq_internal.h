@@ -16,27 +16,36 @@ constexpr int TYPE_Q6_K = 14;
 constexpr int TYPE_Q8_K = 15;
 
 // ---------------------------------------------------------------------------
-// Weight layout in HBM.  GGUF blocks arrive array-of-structs (Q4_K 144 B,
-// Q6_K 210 B, Q8_0 34 B); Q6_K and Q8_0 blocks are not 16-byte multiples, so
-// every type is repacked once at upload into 16-byte aligned planes.  The
-// repack is lossless and moves no byte across rows; the planes hold exactly
-// the GGUF bytes (algorithmic bytes per block are unchanged):
-//   Q4_K: qs   [n][nb][128]  quants (GGUF order)
-//         meta [n][nb][16]   f16 d, f16 dmin, u8 scales[12]
-//   Q6_K: qs   [n][nb][128]  ql, 16-byte pieces in the order 0,2,1,3,4,6,5,7 so
-//                            that the 32 bytes one lane needs are contiguous
-//         qh   [n][nb][64]   (GGUF order)
-//         meta [n][nb][16]   i8 scales[16]
-//         d    [n][nb]       f16
-//   Q8_0: qs   [n][k]        i8 quants
-//         d    [n][nb]       f16
+// Weight layout in HBM ("slabs").  A weight row is cut into groups of 256
+// elements: one super-block for Q4_K / Q6_K, eight 32-element blocks for
+// Q8_0.  Each group is stored as 16-byte pieces, and piece i of every group of
+// a row is stored contiguously ("slab" i).  So a row is
+//     slab 0: piece 0 of groups 0..ng-1 | slab 1: piece 1 of groups 0..ng-1 | ...
+// and a wavefront whose lane L reads piece i of group L issues one fully
+// contiguous 16*ng-byte load.  The repack at upload is lossless:
+//   Q4_K (9 pieces = 144 B):  piece 0 = d f16, dmin f16, scales[12];
+//                             pieces 1..8 = qs[0..127] in GGUF order.
+//   Q6_K (13 pieces = 208 B + d plane): pieces 0..7 = ql[0..127],
+//                             8..11 = qh[0..63], 12 = scales[16];  the f16 d of
+//                             each super-block goes to a separate plane [n][ng].
+//   Q8_0 (17 pieces = 272 B): pieces 2j, 2j+1 = qs of block 8g+j, piece 16 =
+//                             the eight f16 d; a row whose block count is not a
+//                             multiple of 8 is padded with zero blocks.
 // ---------------------------------------------------------------------------
-struct WPlanes {
-    const uint8_t *qs;
-    const uint8_t *qh;
-    const uint8_t *meta;
-    const uint16_t *d;
+struct WLayout {
+    const uint8_t *slab = nullptr;  // [n][SLABS][ng][16]
+    const uint16_t *d = nullptr;    // Q6_K only: [n][ng] f16
+    int type = 0;
+    int ng = 0;                     // groups per row
+    int64_t row_bytes = 0;          // SLABS * ng * 16
 };
+
+__host__ __device__ constexpr int slabs_of(int type) {
+    return type == TYPE_Q4_K ? 9 : type == TYPE_Q6_K ? 13 : type == TYPE_Q8_0 ? 17 : 0;
+}
+inline int groups_of(int type, int64_t k) {
+    return type == TYPE_Q8_0 ? (int)((k / QK8_0 + 7) / 8) : (int)(k / QK_K);
+}
 
 // Quantised activation planes (written by the quantizer kernels):
 //   qs    [m][k]      i8
@@ -83,18 +92,21 @@ inline ActPlanes act_planes(void *base, int64_t m, int64_t k) {
 // ---------------------------------------------------------------------------
 hipError_t launch_quantize_q8k(const float *x, int64_t m, int64_t k, ActPlanes a, hipStream_t s);
 hipError_t launch_quantize_q8_0(const float *x, int64_t m, int64_t k, ActPlanes a, hipStream_t s);
-// GGUF blocks of n rows (device memory) -> the planes of those rows.
-hipError_t launch_repack(int type, const uint8_t *src, int64_t n, int64_t k, uint8_t *qs, uint8_t *qh,
-                         uint8_t *meta, uint8_t *dp, hipStream_t s);
-// Matvec for small m (the decode path); m may be any size, it is cut into
-// slices of at most 8 rows.  S/Smin non-null selects the integer-dump epilogue.
-hipError_t launch_matvec(int type, const WPlanes &w, int64_t n, int64_t k, const ActPlanes &x,
-                         int64_t m, float *y, int32_t *S, int32_t *Smin, hipStream_t s);
+// GGUF blocks of n rows (device memory) -> those rows of the slab layout.
+// dst_slab / dst_d point at the first destination row.  Q8_0 rows must be
+// zeroed beforehand (padding blocks are not written).
+hipError_t launch_repack(int type, const uint8_t *src, int64_t n, int64_t k, uint8_t *dst_slab, uint16_t *dst_d,
+                         hipStream_t s);
+// Decode matvec (any m; batch rows are processed up to 8 at a time).  The
+// activation is either f32 (x != nullptr: quantised inside the kernel,
+// bit-identical to the quantizer kernels) or pre-quantised planes.
+// S/Smin non-null selects the integer-dump variant ([m][n][blocks] int32).
+hipError_t launch_matvec(const WLayout &w, int64_t n, int64_t k, const float *x, const ActPlanes *act, int64_t m,
+                         float *y, int32_t *S, int32_t *Smin, hipStream_t s);
 // Prefill GEMM on MFMA (m > 8).  Returns hipErrorNotSupported for shapes it
 // does not take; the caller then uses launch_matvec.
-hipError_t launch_gemm(int type, const WPlanes &w, int64_t n, int64_t k, const ActPlanes &x,
-                       int64_t m, float *y, int32_t *S, int32_t *Smin, void *ws, size_t ws_bytes,
-                       hipStream_t s);
+hipError_t launch_gemm(const WLayout &w, int64_t n, int64_t k, const ActPlanes &x, int64_t m, float *y, int32_t *S,
+                       int32_t *Smin, void *ws, size_t ws_bytes, hipStream_t s);
 size_t gemm_workspace_bytes(int type, int64_t m, int64_t n, int64_t k);
 
 }  // namespace aq
@@ -112,37 +124,15 @@ template <int CTRL>
 __device__ __forceinline__ int dpp_i(int v) {
     return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
 }
-template <int CTRL>
-__device__ __forceinline__ float dpp_f(float v) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
-}
 constexpr int DPP_QUAD_XOR1 = 0xB1;  // quad_perm [1,0,3,2]
 constexpr int DPP_QUAD_XOR2 = 0x4E;  // quad_perm [2,3,0,1]
-constexpr int DPP_HALF_MIRROR = 0x141;
-constexpr int DPP_ROW_MIRROR = 0x140;
 
-// Sum over groups of 2^LOG consecutive lanes (LOG <= 4); every lane of the
-// group gets the group sum.  All 64 lanes must be active.
-template <int LOG>
-__device__ __forceinline__ int group_sum_i(int v) {
-    if (LOG >= 1) v += dpp_i<DPP_QUAD_XOR1>(v);
-    if (LOG >= 2) v += dpp_i<DPP_QUAD_XOR2>(v);
-    if (LOG >= 3) v += dpp_i<DPP_HALF_MIRROR>(v);
-    if (LOG >= 4) v += dpp_i<DPP_ROW_MIRROR>(v);
+// Sum over aligned groups of 4 lanes; every lane of the group gets the sum.
+// All lanes of each group must be active.
+__device__ __forceinline__ int quad_sum_i(int v) {
+    v += dpp_i<DPP_QUAD_XOR1>(v);
+    v += dpp_i<DPP_QUAD_XOR2>(v);
     return v;
-}
-
-// Sum over all 64 lanes; the result is uniform.  All lanes must be active.
-__device__ __forceinline__ float wave_sum(float v) {
-    v += dpp_f<DPP_QUAD_XOR1>(v);
-    v += dpp_f<DPP_QUAD_XOR2>(v);
-    v += dpp_f<DPP_HALF_MIRROR>(v);
-    v += dpp_f<DPP_ROW_MIRROR>(v);
-    float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
-    float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
-    float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
-    float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
-    return (r0 + r1) + (r2 + r3);
 }
 
 // f16 -> f32 (exact; v_cvt_f32_f16 with f16 denormals preserved, the HIP
@@ -182,6 +172,100 @@ __device__ __forceinline__ int sat_i8(float v) {
     if (v != v) return 0;
     v = fminf(fmaxf(v, -128.0f), 127.0f);
     return (int)v;
+}
+
+__device__ __forceinline__ uint32_t pack4_i8(const int q[4]) {
+    return (uint32_t)(q[0] & 0xff) | ((uint32_t)(q[1] & 0xff) << 8) | ((uint32_t)(q[2] & 0xff) << 16) |
+           ((uint32_t)(q[3] & 0xff) << 24);
+}
+
+constexpr int DPP_HALF_MIRROR = 0x141;  // lane i <-> 7-i within each 8 lanes
+constexpr int DPP_ROW_MIRROR = 0x140;   // lane i <-> 15-i within each 16 lanes
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float readlane_f(float v, int l) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+
+// Wave-uniform max / min over all 64 lanes (all lanes active): max within
+// each row of 16 lanes by DPP, then across the four rows by readlane.
+__device__ __forceinline__ float wave_max_f(float v) {
+    v = fmaxf(v, dpp_f<DPP_QUAD_XOR1>(v));
+    v = fmaxf(v, dpp_f<DPP_QUAD_XOR2>(v));
+    v = fmaxf(v, dpp_f<DPP_HALF_MIRROR>(v));
+    v = fmaxf(v, dpp_f<DPP_ROW_MIRROR>(v));
+    return fmaxf(fmaxf(readlane_f(v, 0), readlane_f(v, 16)), fmaxf(readlane_f(v, 32), readlane_f(v, 48)));
+}
+__device__ __forceinline__ int wave_min_i(int v) {
+    v = min(v, dpp_i<DPP_QUAD_XOR1>(v));
+    v = min(v, dpp_i<DPP_QUAD_XOR2>(v));
+    v = min(v, dpp_i<DPP_HALF_MIRROR>(v));
+    v = min(v, dpp_i<DPP_ROW_MIRROR>(v));
+    return min(min(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
+               min(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
+}
+
+// One Q8_K block (candle-core 0.8.4 BlockQ8K::from_float) quantised by one
+// full wavefront: lane l holds elements 4l..4l+3 in v.  Returns the four
+// quants packed in a dword; *bsum gets the sum of the 16 quants of lanes
+// 4(l/4)..4(l/4)+3 (every lane of the quad), *d the block's d (uniform).
+// candle scans the block in order with `if amax < x.abs() { amax = |x|; max = x }`,
+// so max is the FIRST element of largest |x| (NaN never wins); then
+// iscale = -128/max, q = min(round(iscale*x), 127) with ties away from zero,
+// d = 1/iscale; an all-zero block gives d = 0, q = 0.  Here: amax = max |x|
+// over the wave, then the smallest index attaining it, then that element.
+// IEEE division (the library is built without fast-math) keeps it bit-exact.
+__device__ __forceinline__ uint32_t q8k_block_wave(const float v[4], int lane, int *bsum, float *d) {
+    float ax[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float a = fabsf(v[i]);
+        ax[i] = a == a ? a : 0.0f;  // NaN never becomes the max
+    }
+    const float am = wave_max_f(fmaxf(fmaxf(ax[0], ax[1]), fmaxf(ax[2], ax[3])));
+    int q[4] = {0, 0, 0, 0};
+    float dd = 0.0f;
+    if (am != 0.0f) {  // uniform
+        int li = 1 << 30;
+#pragma unroll
+        for (int i = 3; i >= 0; i--)
+            if (ax[i] == am) li = 4 * lane + i;
+        const int idx = wave_min_i(li);
+        const int c = idx & 3;
+        const float mine = c == 0 ? v[0] : c == 1 ? v[1] : c == 2 ? v[2] : v[3];
+        const float mx = readlane_f(mine, idx >> 2);
+        const float iscale = -128.0f / mx;
+#pragma unroll
+        for (int i = 0; i < 4; i++) q[i] = sat_i8(fminf(roundf(iscale * v[i]), 127.0f));
+        dd = 1.0f / iscale;
+    }
+    *bsum = quad_sum_i(q[0] + q[1] + q[2] + q[3]);
+    *d = dd;
+    return pack4_i8(q);
+}
+
+// One Q8_0 block (BlockQ8_0::from_float) quantised by eight consecutive
+// lanes (lane sub = l%8 holds elements 4sub..4sub+3): d = amax/127, id = 1/d
+// (0 if d == 0), q = round(x*id) as i8, stored d = f16(d) (RNE).  Returns the
+// packed quants; *d16 gets the f16 bits (uniform over the 8 lanes).  All 64
+// lanes of the wave must be active.
+__device__ __forceinline__ uint32_t q8_0_block_8lanes(const float v[4], uint16_t *d16) {
+    float am = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) am = fmaxf(am, fabsf(v[i]));
+    am = fmaxf(am, dpp_f<DPP_QUAD_XOR1>(am));
+    am = fmaxf(am, dpp_f<DPP_QUAD_XOR2>(am));
+    am = fmaxf(am, dpp_f<DPP_HALF_MIRROR>(am));
+    const float d = am / 127.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    int q[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) q[i] = sat_i8(roundf(v[i] * id));
+    *d16 = f32_to_f16_rne(d);
+    return pack4_i8(q);
 }
 
 }  // namespace aq

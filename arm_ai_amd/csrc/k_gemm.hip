@@ -6,8 +6,8 @@ namespace aq {
 
 size_t gemm_workspace_bytes(int, int64_t, int64_t, int64_t) { return (size_t)-1; }
 
-hipError_t launch_gemm(int, const WPlanes &, int64_t, int64_t, const ActPlanes &, int64_t, float *, int32_t *,
-                       int32_t *, void *, size_t, hipStream_t) {
+hipError_t launch_gemm(const WLayout &, int64_t, int64_t, const ActPlanes &, int64_t, float *, int32_t *, int32_t *,
+                       void *, size_t, hipStream_t) {
     return hipErrorNotSupported;
 }
 

@@ -1,20 +1,16 @@
 // k_quantize.hip -- activation quantizers (Q8_K, Q8_0) and the one-time
-// weight repack, for gfx950.
+// weight repack into the slab layout, for gfx950.
 //
 // Q8_K follows candle-core 0.8.4 BlockQ8K::from_float (the quantize_row_q8k
 // step of k_quants::matmul, reached from native/arm_ai_nif/src/llama_candle.rs:93,
-// :119): per 256-element block, the element of largest |x| (first on ties)
-// gives iscale = -128/max, q = min(round(iscale*x), 127) with round-half-away,
-// bsums are sums of 16 quants, d = 1/iscale.  Q8_0 follows BlockQ8_0::from_float:
-// d = amax/127, id = 1/d (0 if d == 0), q = round(x*id), d stored as f16 (RNE).
-// Both are bit-exact restatements: IEEE division (no fast-math, no rcp), and
-// the (|x|, index) reduction reproduces the sequential first-max rule.
+// :119); Q8_0 follows BlockQ8_0::from_float.  The per-block arithmetic lives in
+// q8k_block_wave / q8_0_block_8lanes (aq_internal.h), which the fused matvec
+// prologue calls too, so both paths produce the same bytes.
 #include "aq_internal.h"
 
 namespace aq {
 
 // One wavefront per 256-element block, four blocks per 256-thread workgroup.
-// Lane l holds elements 4l..4l+3.
 template <bool VEC>
 __global__ __launch_bounds__(256) void quantize_q8k_kernel(const float *__restrict__ x, int64_t nblocks,
                                                            int64_t k, ActPlanes a) {
@@ -26,46 +22,16 @@ __global__ __launch_bounds__(256) void quantize_q8k_kernel(const float *__restri
     const float *xb = x + row * k + sb * QK_K + 4 * lane;
     float v[4];
     if (VEC) {
-        float4 t = *(const float4 *)xb;
+        const float4 t = *(const float4 *)xb;
         v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
     } else {
         for (int i = 0; i < 4; i++) v[i] = xb[i];
     }
-    // First index of the largest |x| (candle: `if amax < x.abs()` scanning
-    // in order); zeros and NaNs never win.
-    float am = 0.0f, mx = 0.0f;
-    int idx = 1 << 30;
-    for (int i = 0; i < 4; i++) {
-        float ax = fabsf(v[i]);
-        if (am < ax) {
-            am = ax;
-            mx = v[i];
-            idx = 4 * lane + i;
-        }
-    }
-    for (int off = 32; off >= 1; off >>= 1) {
-        float oam = __shfl_xor(am, off);
-        float omx = __shfl_xor(mx, off);
-        int oidx = __shfl_xor(idx, off);
-        if (oam > am || (oam == am && oidx < idx)) {
-            am = oam;
-            mx = omx;
-            idx = oidx;
-        }
-    }
-    int q[4] = {0, 0, 0, 0};
-    float d = 0.0f;
-    if (am != 0.0f) {
-        const float iscale = -128.0f / mx;
-        for (int i = 0; i < 4; i++) q[i] = sat_i8(fminf(roundf(iscale * v[i]), 127.0f));
-        d = 1.0f / iscale;
-    }
-    int s = q[0] + q[1] + q[2] + q[3];
-    s = group_sum_i<2>(s);  // 16 elements = 4 lanes
-    uint32_t packed = (uint32_t)(q[0] & 0xff) | ((uint32_t)(q[1] & 0xff) << 8) |
-                      ((uint32_t)(q[2] & 0xff) << 16) | ((uint32_t)(q[3] & 0xff) << 24);
+    int bsum;
+    float d;
+    const uint32_t packed = q8k_block_wave(v, lane, &bsum, &d);
     *(uint32_t *)(a.qs + row * k + sb * QK_K + 4 * lane) = packed;
-    if ((lane & 3) == 0) a.bsums[row * (k / 16) + sb * 16 + (lane >> 2)] = (int16_t)s;
+    if ((lane & 3) == 0) a.bsums[row * (k / 16) + sb * 16 + (lane >> 2)] = (int16_t)bsum;
     if (lane == 0) a.d[row * nb + sb] = d;
 }
 
@@ -82,25 +48,17 @@ __global__ __launch_bounds__(256) void quantize_q8_0_kernel(const float *__restr
     if (valid) {
         const float *xb = x + row * k + b * QK8_0 + 4 * sub;
         if (VEC) {
-            float4 t = *(const float4 *)xb;
+            const float4 t = *(const float4 *)xb;
             v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
         } else {
             for (int i = 0; i < 4; i++) v[i] = xb[i];
         }
     }
-    float am = 0.0f;
-    for (int i = 0; i < 4; i++) am = fmaxf(am, fabsf(v[i]));
-    am = fmaxf(am, __shfl_xor(am, 1));
-    am = fmaxf(am, __shfl_xor(am, 2));
-    am = fmaxf(am, __shfl_xor(am, 4));
-    const float d = am / 127.0f;
-    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    uint16_t h;
+    const uint32_t packed = q8_0_block_8lanes(v, &h);
     if (!valid) return;
-    uint32_t packed = 0;
-    for (int i = 0; i < 4; i++) packed |= (uint32_t)(sat_i8(roundf(v[i] * id)) & 0xff) << (8 * i);
     *(uint32_t *)(a.qs + row * k + b * QK8_0 + 4 * sub) = packed;
     if (sub == 0) {
-        const uint16_t h = f32_to_f16_rne(d);
         a.d16[row * nb + b] = h;
         a.d[row * nb + b] = f16_bits_to_f32(h);
     }
@@ -133,63 +91,61 @@ hipError_t launch_quantize_q8_0(const float *x, int64_t m, int64_t k, ActPlanes 
 }
 
 // ---------------------------------------------------------------------------
-// Weight repack: GGUF array-of-blocks -> planes (layout in aq_internal.h).
-// One thread per byte of a block; grid-stride over all bytes.
+// Weight repack: GGUF array-of-blocks -> slab layout (aq_internal.h).
+// One thread per source byte; grid-stride over all bytes of the n rows.
 // ---------------------------------------------------------------------------
 template <int TYPE>
-__global__ __launch_bounds__(256) void repack_kernel(const uint8_t *__restrict__ src, int64_t nblk,
-                                                     uint8_t *__restrict__ qs, uint8_t *__restrict__ qh,
-                                                     uint8_t *__restrict__ meta, uint8_t *__restrict__ dpl) {
+__global__ __launch_bounds__(256) void repack_kernel(const uint8_t *__restrict__ src, int64_t n, int64_t nblk,
+                                                     int ng, uint8_t *__restrict__ slab, uint16_t *__restrict__ dpl) {
     constexpr int BYTES = TYPE == TYPE_Q4_K ? 144 : TYPE == TYPE_Q6_K ? 210 : 34;
-    const int64_t total = nblk * BYTES;
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
-         i += (int64_t)gridDim.x * blockDim.x) {
-        const int64_t b = i / BYTES;
-        const int o = (int)(i - b * BYTES);
+    constexpr int S = slabs_of(TYPE);
+    const int64_t row_bytes = (int64_t)S * ng * 16;
+    const int64_t total = n * nblk * BYTES;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t blk = i / BYTES;  // block index over all rows
+        const int o = (int)(i - blk * BYTES);
+        const int64_t row = blk / nblk, b = blk - row * nblk;
+        uint8_t *rowp = slab + row * row_bytes;
         if (TYPE == TYPE_Q4_K) {
-            // bytes 0..15 -> meta (d, dmin, scales), 16..143 -> qs
-            if (o < 16) meta[b * 16 + o] = src[i];
-            else qs[b * 128 + (o - 16)] = src[i];
+            // bytes 0..15 (d, dmin, scales) -> piece 0; qs byte j -> piece 1 + j/16
+            const int piece = o < 16 ? 0 : 1 + (o - 16) / 16;
+            const int w = o < 16 ? o : (o - 16) & 15;
+            rowp[((int64_t)piece * ng + b) * 16 + w] = src[i];
         } else if (TYPE == TYPE_Q6_K) {
-            if (o < 128) {
-                // destination piece p takes source piece perm[p]
-                const int p = o >> 4, w = o & 15;
-                const int sp = (p & 4) | ((p & 1) << 1) | ((p >> 1) & 1);  // 0,2,1,3,4,6,5,7
-                qs[b * 128 + o] = src[b * BYTES + sp * 16 + w];
-            } else if (o < 192) {
-                qh[b * 64 + (o - 128)] = src[i];
-            } else if (o < 208) {
-                meta[b * 16 + (o - 192)] = src[i];
+            if (o < 208) {
+                // ql 0..127 -> pieces 0..7, qh 128..191 -> 8..11, scales 192..207 -> 12
+                rowp[((int64_t)(o >> 4) * ng + b) * 16 + (o & 15)] = src[i];
             } else {
-                dpl[b * 2 + (o - 208)] = src[i];
+                ((uint8_t *)(dpl + row * ng + b))[o - 208] = src[i];
             }
         } else {
-            if (o < 2) dpl[b * 2 + o] = src[i];
-            else qs[b * 32 + (o - 2)] = src[i];
+            // Q8_0 block b = 8g + j: d -> piece 16 bytes 2j..2j+1; qs byte q -> piece 2j + q/16
+            const int64_t g = b >> 3;
+            const int j = (int)(b & 7);
+            if (o < 2) rowp[((int64_t)16 * ng + g) * 16 + 2 * j + o] = src[i];
+            else {
+                const int q = o - 2;
+                rowp[((int64_t)(2 * j + (q >> 4)) * ng + g) * 16 + (q & 15)] = src[i];
+            }
         }
     }
 }
 
-hipError_t launch_repack(int type, const uint8_t *src, int64_t n, int64_t k, uint8_t *qs, uint8_t *qh,
-                         uint8_t *meta, uint8_t *dp, hipStream_t s) {
-    if (!src || n <= 0 || k <= 0) return hipErrorInvalidValue;
+hipError_t launch_repack(int type, const uint8_t *src, int64_t n, int64_t k, uint8_t *dst_slab, uint16_t *dst_d,
+                         hipStream_t s) {
+    if (!src || !dst_slab || n <= 0 || k <= 0) return hipErrorInvalidValue;
     const int blk = type == TYPE_Q8_0 ? QK8_0 : QK_K;
     if (k % blk) return hipErrorInvalidValue;
-    const int64_t nblk = n * (k / blk);
+    const int64_t nblk = k / blk;
+    const int ng = groups_of(type, k);
     const unsigned grid = 8192;
     switch (type) {
-    case TYPE_Q4_K:
-        if (!qs || !meta) return hipErrorInvalidValue;
-        repack_kernel<TYPE_Q4_K><<<grid, 256, 0, s>>>(src, nblk, qs, qh, meta, dp);
-        break;
+    case TYPE_Q4_K: repack_kernel<TYPE_Q4_K><<<grid, 256, 0, s>>>(src, n, nblk, ng, dst_slab, dst_d); break;
     case TYPE_Q6_K:
-        if (!qs || !qh || !meta || !dp) return hipErrorInvalidValue;
-        repack_kernel<TYPE_Q6_K><<<grid, 256, 0, s>>>(src, nblk, qs, qh, meta, dp);
+        if (!dst_d) return hipErrorInvalidValue;
+        repack_kernel<TYPE_Q6_K><<<grid, 256, 0, s>>>(src, n, nblk, ng, dst_slab, dst_d);
         break;
-    case TYPE_Q8_0:
-        if (!qs || !dp) return hipErrorInvalidValue;
-        repack_kernel<TYPE_Q8_0><<<grid, 256, 0, s>>>(src, nblk, qs, qh, meta, dp);
-        break;
+    case TYPE_Q8_0: repack_kernel<TYPE_Q8_0><<<grid, 256, 0, s>>>(src, n, nblk, ng, dst_slab, dst_d); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
