@@ -52,18 +52,21 @@ inline int groups_of(int type, int64_t k) {
 //   d     [m][k/256]  f32 (Q8_K) or [m][k/32] f32 value of the f16 d (Q8_0)
 //   d16   [m][k/32]   f16 bits of the Q8_0 d
 //   bsums [m][k/16]   i16 (Q8_K)
+//   bsum16 [m][k/16]  the same bsums as f16 bits (exact: |bsum| <= 2048), the
+//                     A operand of the GEMM's f16 MFMA for the min term
 struct ActPlanes {
     int8_t *qs;
     float *d;
     uint16_t *d16;
     int16_t *bsums;
+    uint16_t *bsum16;
 };
 
 inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
 // Sizes of the activation planes for m rows of k (bytes, each plane 256-B aligned).
 struct ActSizes {
-    size_t qs, d, d16, bsums, total;
+    size_t qs, d, d16, bsums, bsum16, total;
 };
 inline ActSizes act_sizes(int64_t m, int64_t k) {
     ActSizes s;
@@ -71,7 +74,8 @@ inline ActSizes act_sizes(int64_t m, int64_t k) {
     s.d = align_up((size_t)m * (k / 32) * 4, 256);  // large enough for Q8_K (k/256) and Q8_0 (k/32)
     s.d16 = align_up((size_t)m * (k / 32) * 2, 256);
     s.bsums = align_up((size_t)m * (k / 16) * 2, 256);
-    s.total = s.qs + s.d + s.d16 + s.bsums;
+    s.bsum16 = s.bsums;
+    s.total = s.qs + s.d + s.d16 + s.bsums + s.bsum16;
     return s;
 }
 inline ActPlanes act_planes(void *base, int64_t m, int64_t k) {
@@ -82,6 +86,7 @@ inline ActPlanes act_planes(void *base, int64_t m, int64_t k) {
     a.d = (float *)(p + s.qs);
     a.d16 = (uint16_t *)(p + s.qs + s.d);
     a.bsums = (int16_t *)(p + s.qs + s.d + s.d16);
+    a.bsum16 = (uint16_t *)(p + s.qs + s.d + s.d16 + s.bsums);
     return a;
 }
 
@@ -104,9 +109,14 @@ hipError_t launch_repack(int type, const uint8_t *src, int64_t n, int64_t k, uin
 hipError_t launch_matvec(const WLayout &w, int64_t n, int64_t k, const float *x, const ActPlanes *act, int64_t m,
                          float *y, int32_t *S, int32_t *Smin, hipStream_t s);
 // Prefill GEMM on MFMA (m > 8).  Returns hipErrorNotSupported for shapes it
-// does not take; the caller then uses launch_matvec.
+// does not take; the caller then uses launch_matvec.  ws: gemm_workspace_bytes
+// of scratch (split-K partials); counters: GEMM_MAX_TILES ints that are zero
+// before the launch and are zero again after it.
+constexpr int GEMM_MAX_TILES = 1 << 16;
 hipError_t launch_gemm(const WLayout &w, int64_t n, int64_t k, const ActPlanes &x, int64_t m, float *y, int32_t *S,
-                       int32_t *Smin, void *ws, size_t ws_bytes, hipStream_t s);
+                       int32_t *Smin, void *ws, size_t ws_bytes, int *counters, hipStream_t s);
+// Workspace bytes launch_gemm needs for this shape, or (size_t)-1 if the
+// weight type / shape has no GEMM (the matvec then serves m > 8 too).
 size_t gemm_workspace_bytes(int type, int64_t m, int64_t n, int64_t k);
 
 }  // namespace aq

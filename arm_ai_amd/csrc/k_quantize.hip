@@ -31,7 +31,10 @@ __global__ __launch_bounds__(256) void quantize_q8k_kernel(const float *__restri
     float d;
     const uint32_t packed = q8k_block_wave(v, lane, &bsum, &d);
     *(uint32_t *)(a.qs + row * k + sb * QK_K + 4 * lane) = packed;
-    if ((lane & 3) == 0) a.bsums[row * (k / 16) + sb * 16 + (lane >> 2)] = (int16_t)bsum;
+    if ((lane & 3) == 0) {
+        a.bsums[row * (k / 16) + sb * 16 + (lane >> 2)] = (int16_t)bsum;
+        a.bsum16[row * (k / 16) + sb * 16 + (lane >> 2)] = __builtin_bit_cast(uint16_t, (_Float16)(float)bsum);
+    }
     if (lane == 0) a.d[row * nb + sb] = d;
 }
 

@@ -181,6 +181,24 @@ def measure(ctx, wtype, n, k, m, steps, warmup, seed):
     return wl, step_ms, step_wall, kern_ms, out
 
 
+def measure_prefill(ctx, n, k, m, steps, warmup, seed):
+    """Prefill GEMM at m rows: quantiser kernel + int8 MFMA GEMM (step) and the GEMM alone."""
+    wl = Workload(ctx, 12, n, k, m, seed)
+    step_ms, _ = time_graph(ctx, wl.step, steps, warmup)
+    kern_ms, _ = time_graph(ctx, wl.kernel, steps, warmup)
+    ops = 2.0 * m * n * k
+    out = {
+        "n": n, "k": k, "m": m, "weight_type": "Q4_K",
+        "step_us": round(step_ms * 1e3, 3),
+        "step_TOPS": round(ops / (step_ms / 1e3) / 1e12, 1),
+        "gemm_us": round(kern_ms * 1e3, 3),
+        "gemm_TOPS": round(ops / (kern_ms / 1e3) / 1e12, 1),
+        "gemm_frac_int8_peak": round(ops / (kern_ms / 1e3) / 1e12 / INT8_PEAK_TOPS, 4),
+    }
+    wl.free()
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -274,6 +292,12 @@ def main() -> int:
             w2.free()
             extra[name] = out
             log(f"{name}: step {out['step_us']} us ({out['step_GBps']} GB/s), pre-quantised matvec {out['matvec_us']} us ({out['matvec_GBps']} GB/s)")
+        for name, n_, k_, m_, seed in [("c3_prefill_q4k_5632x2048_m512", 5632, 2048, 512, 3),
+                                        ("c3_prefill_q4k_2048x5632_m512", 2048, 5632, 512, 3),
+                                        ("c4_prefill_q4k_14336x4096_m512", 14336, 4096, 512, 4)]:
+            out = measure_prefill(ctx, n_, k_, m_, min(args.steps, 50), min(args.warmup, 5), seed)
+            extra[name] = out
+            log(f"{name}: step {out['step_us']} us ({out['step_TOPS']} TOPS), gemm {out['gemm_us']} us ({out['gemm_TOPS']} TOPS, {out['gemm_frac_int8_peak']} of int8 peak)")
         result["extra"] = extra
     else:
         result["extra"] = {}

@@ -54,6 +54,8 @@ def lib() -> ctypes.CDLL:
             getattr(L, f).restype = ctypes.c_float
         L.orc_block_sums.argtypes = [ctypes.c_int, i64, P, P, P, P]
         L.orc_block_sums.restype = None
+        L.orc_block_sums_mat.argtypes = [ctypes.c_int, i64, i64, i64, P, P, P, P, ctypes.c_int]
+        L.orc_block_sums_mat.restype = ctypes.c_int
         L.orc_matmul.argtypes = [ctypes.c_int, i64, i64, i64, P, P, P, ctypes.c_int]
         L.orc_matmul.restype = ctypes.c_int
         L.orc_matmul_preq.argtypes = [ctypes.c_int, i64, i64, i64, P, P, P, ctypes.c_int]
@@ -130,7 +132,7 @@ def vec_dot(wtype: int, k: int, wrow: np.ndarray, xq_row: np.ndarray) -> float:
     return float(f(k, _p(wrow), _p(xq_row)))
 
 
-def block_sums(wtype: int, k: int, w: np.ndarray, xq: np.ndarray):
+def block_sums(wtype: int, k: int, w: np.ndarray, xq: np.ndarray, nthreads: int = 0):
     """Integer sums per (m, n, block): returns S, Smin int32 [m, n, nb]."""
     w = np.ascontiguousarray(w)
     xq = np.ascontiguousarray(xq)
@@ -139,10 +141,9 @@ def block_sums(wtype: int, k: int, w: np.ndarray, xq: np.ndarray):
     nb = k // BLOCK_ELEMS[wtype]
     S = np.zeros((m, n, nb), np.int32)
     Sm = np.zeros((m, n, nb), np.int32)
-    L = lib()
-    for i in range(m):
-        for j in range(n):
-            L.orc_block_sums(wtype, k, w[j].ctypes.data, xq[i].ctypes.data, S[i, j].ctypes.data, Sm[i, j].ctypes.data)
+    rc = lib().orc_block_sums_mat(wtype, m, n, k, _p(w), _p(xq), _p(S), _p(Sm), nthreads)
+    if rc != 0:
+        raise ValueError(f"orc_block_sums_mat failed: {rc}")
     return S, Sm
 
 

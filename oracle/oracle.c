@@ -405,6 +405,27 @@ void orc_block_sums(int type, int64_t k, const uint8_t *w, const uint8_t *xq, in
     }
 }
 
+/* Block sums for every (row of xq, weight row): S and Smin [m][n][nblk],
+ * rows in parallel.  Same arithmetic as orc_block_sums. */
+int orc_block_sums_mat(int type, int64_t m, int64_t n, int64_t k, const uint8_t *w, const uint8_t *xq,
+                       int32_t *S, int32_t *Smin, int nthreads) {
+    if (type != ORC_Q4_K && type != ORC_Q6_K && type != ORC_Q8_0) return -2;
+    int64_t wblk = orc_type_block_elems(type);
+    if (k <= 0 || k % wblk != 0 || m < 0 || n < 0) return -3;
+    const int64_t nblk = k / wblk;
+    const size_t row_w = (size_t)nblk * orc_type_block_bytes(type);
+    const int at = type == ORC_Q8_0 ? ORC_Q8_0 : ORC_Q8_K;
+    const size_t row_x = (size_t)(k / orc_type_block_elems(at)) * orc_type_block_bytes(at);
+    if (nthreads <= 0) nthreads = orc_max_threads();
+#pragma omp parallel for schedule(dynamic, 64) num_threads(nthreads)
+    for (int64_t i = 0; i < m * n; i++) {
+        const int64_t r = i / n, c = i % n;
+        orc_block_sums(type, k, w + (size_t)c * row_w, xq + (size_t)r * row_x, S + (size_t)i * nblk,
+                       Smin + (size_t)i * nblk);
+    }
+    return 0;
+}
+
 /* ---------------------------------------------------------- matmul */
 
 static int act_type_for(int type) { return type == ORC_Q8_0 ? ORC_Q8_0 : ORC_Q8_K; }

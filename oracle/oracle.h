@@ -74,6 +74,11 @@ float orc_vec_dot_q8_0_q8_0(int64_t k, const uint8_t *w, const uint8_t *xq);
 void orc_block_sums(int type, int64_t k, const uint8_t *w, const uint8_t *xq,
                     int32_t *S, int32_t *Smin);
 
+/* orc_block_sums for all m x n (activation row, weight row) pairs:
+ * S, Smin [m][n][blocks].  OpenMP over the pairs. */
+int orc_block_sums_mat(int type, int64_t m, int64_t n, int64_t k, const uint8_t *w, const uint8_t *xq,
+                       int32_t *S, int32_t *Smin, int nthreads);
+
 /* k_quants::matmul<T>: dst[m][n] = lhs[m][k] . W[n][k]^T.
  * Serial per-row activation quantisation, then columns in parallel
  * (nthreads OpenMP threads, chunks of 256 columns).  Returns 0, or a

@@ -120,6 +120,43 @@ def test_config4_llama3_lm_head_q6k(ctx):
     check_matmul(ctx, W, x, sums=False, cond=False)
 
 
+# ----------------------------------------------- prefill GEMM (int8 MFMA, m > 8)
+@pytest.mark.parametrize("n,k", [(5632, 2048), (2048, 5632)])
+def test_config3_prefill_gemm(ctx, n, k):
+    W = S.make_weight(S.TYPE_Q4_K, n, k, seed=3)
+    x = S.make_activation(512, k, seed=30 + k)
+    check_matmul(ctx, W, x)
+
+
+def test_config4_prefill_gemm_llama3_ffn_up(ctx):
+    W = S.make_weight(S.TYPE_Q4_K, 14336, 4096, seed=4)
+    x = S.make_activation(512, 4096, seed=44)
+    check_matmul(ctx, W, x, sums=False, cond=False)
+
+
+@pytest.mark.parametrize("m,n,k", [(9, 100, 256), (63, 129, 768), (65, 300, 512), (130, 257, 1024), (200, 64, 2048)])
+def test_prefill_gemm_ragged_tiles(ctx, m, n, k):
+    W = S.make_weight(S.TYPE_Q4_K, n, k, seed=m + n)
+    x = S.make_activation(m, k, seed=m * n)
+    check_matmul(ctx, W, x)
+
+
+def test_prefill_gemm_extreme_values(ctx):
+    """Largest integer sums the Q4_K . Q8_K product can form: all quants 15,
+    all scales and mins 63, and activation blocks of equal values (every
+    quant -128)."""
+    n, k, m = 64, 1024, 16
+    rng = np.random.default_rng(5)
+    W = S.make_weight(S.TYPE_Q4_K, n, k, seed=5)
+    W.q[:] = 15
+    W.sc[:] = 63
+    W.mn[:] = 63
+    W.blocks = S.pack_q4k(W.d, W.dmin, W.sc, W.mn, W.q)
+    x = np.repeat(rng.standard_normal((m, k // 256)).astype(np.float32), 256, axis=1)
+    x[1::2] = -np.abs(x[1::2])
+    check_matmul(ctx, W, x, cond=False)
+
+
 # ------------------------------------------------------ batch and K coverage
 @pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 7, 8, 11])
 @pytest.mark.parametrize("wtype", [S.TYPE_Q4_K, S.TYPE_Q6_K, S.TYPE_Q8_0])
