@@ -3,7 +3,7 @@
 // Host-side replacement for candle-core 0.8.4's QMatMul / QTensor on the
 // CPU (reached from native/arm_ai_nif/src/llama_candle.rs:42 at load and
 // :93 / :119 at prefill / decode).  Weights are uploaded once, repacked into
-// the HBM slab layout (aq_internal.h), and every matmul runs on the context's
+// the HBM row-block tile layout (aq_internal.h), and every matmul runs on the context's
 // stream as either one matvec kernel that quantises the f32 activation itself
 // (m <= 8), or the activation quantizer kernel (Q8_K, or Q8_0 for Q8_0
 // weights) followed by the MFMA GEMM (m > 8).  Errors are status codes plus
@@ -279,11 +279,13 @@ static int upload_impl(aq_ctx *ctx, int type, const void *blocks, size_t nbytes,
         return fail(AQ_ERR_SHAPE, "nbytes=%zu != n*k/%d*%d = %zu", nbytes, be, block_bytes(type), row_bytes * (size_t)n);
     int rc = use_device(ctx->device);
     if (rc) return rc;
-    // slab layout (aq_internal.h): [n][slabs][ng][16] plus, for Q6_K, the d plane [n][ng]
+    // row-block tile layout (aq_internal.h): rows padded to a multiple of 8,
+    // plus, for Q6_K, the d plane [n/8][ng][8]
     const int ng = groups_of(type, k);
-    const int64_t slab_row = (int64_t)slabs_of(type) * ng * 16;
-    const size_t slab_bytes = align_up((size_t)slab_row * (size_t)n, 256);
-    const size_t d_bytes = type == AQ_TYPE_Q6_K ? align_up((size_t)n * ng * 2, 256) : 0;
+    const int64_t nrb = (n + RB - 1) / RB;
+    const int64_t rb_stride = (int64_t)slabs_of(type) * ng * 128;
+    const size_t slab_bytes = align_up((size_t)rb_stride * (size_t)nrb, 256);
+    const size_t d_bytes = type == AQ_TYPE_Q6_K ? align_up((size_t)nrb * ng * RB * 2, 256) : 0;
     const size_t total = slab_bytes + d_bytes;
     aq_qweight *w = new (std::nothrow) aq_qweight();
     if (!w) return fail(AQ_ERR_OOM, "out of host memory");
@@ -302,19 +304,19 @@ static int upload_impl(aq_ctx *ctx, int type, const void *blocks, size_t nbytes,
     w->layout.d = d_bytes ? (const uint16_t *)(base + slab_bytes) : nullptr;
     w->layout.type = type;
     w->layout.ng = ng;
-    w->layout.row_bytes = slab_row;
+    w->layout.rb_stride = rb_stride;
 
     int status = AQ_OK;
-    // Q8_0 rows whose block count is not a multiple of 8 end in zero padding blocks
-    if (type == AQ_TYPE_Q8_0 && (k / QK8_0) % 8 != 0 &&
-        hipMemsetAsync(base, 0, slab_bytes, ctx->stream) != hipSuccess)
+    // padding rows (n not a multiple of 8) and Q8_0 padding blocks must read as zeros
+    if ((n % RB != 0 || (type == AQ_TYPE_Q8_0 && (k / QK8_0) % 8 != 0)) &&
+        hipMemsetAsync(base, 0, total, ctx->stream) != hipSuccess)
         status = fail(AQ_ERR_HIP, "hipMemsetAsync of the weight padding failed");
 
     // Stage whole rows through a bounded device buffer (256 MiB) unless the
     // blocks are already on the device.
     const size_t stage_cap = (size_t)256 << 20;
-    int64_t rows_per = (int64_t)(stage_cap / row_bytes);
-    if (rows_per < 1) rows_per = 1;
+    int64_t rows_per = (int64_t)(stage_cap / row_bytes) / RB * RB;  // chunks start on a row block
+    if (rows_per < RB) rows_per = RB;
     if (rows_per > n) rows_per = n;
     void *stage = nullptr;
     if (!src_on_device && status == AQ_OK) {
@@ -333,8 +335,9 @@ static int upload_impl(aq_ctx *ctx, int type, const void *blocks, size_t nbytes,
             }
             src = (const uint8_t *)stage;
         }
-        hipError_t e = launch_repack(type, src, rows, k, base + (size_t)r0 * slab_row,
-                                     d_bytes ? (uint16_t *)(base + slab_bytes) + (size_t)r0 * ng : nullptr, ctx->stream);
+        hipError_t e = launch_repack(type, src, rows, k, base + (size_t)(r0 / RB) * rb_stride,
+                                     d_bytes ? (uint16_t *)(base + slab_bytes) + (size_t)(r0 / RB) * ng * RB : nullptr,
+                                     ctx->stream);
         if (e != hipSuccess) status = fail(AQ_ERR_HIP, "repack: %s", hipGetErrorString(e));
         // the staging buffer is reused by the next chunk
         if (status == AQ_OK && hipStreamSynchronize(ctx->stream) != hipSuccess) status = fail(AQ_ERR_HIP, "upload sync failed");

@@ -16,28 +16,37 @@ constexpr int TYPE_Q6_K = 14;
 constexpr int TYPE_Q8_K = 15;
 
 // ---------------------------------------------------------------------------
-// Weight layout in HBM ("slabs").  A weight row is cut into groups of 256
-// elements: one super-block for Q4_K / Q6_K, eight 32-element blocks for
-// Q8_0.  Each group is stored as 16-byte pieces, and piece i of every group of
-// a row is stored contiguously ("slab" i).  So a row is
-//     slab 0: piece 0 of groups 0..ng-1 | slab 1: piece 1 of groups 0..ng-1 | ...
-// and a wavefront whose lane L reads piece i of group L issues one fully
-// contiguous 16*ng-byte load.  The repack at upload is lossless:
+// Weight layout in HBM ("row-block tiles").  A weight row is cut into groups
+// of 256 elements: one super-block for Q4_K / Q6_K, eight 32-element blocks
+// for Q8_0.  Each group is a fixed number of 16-byte pieces (the repack at
+// upload is lossless; same bytes, moved):
 //   Q4_K (9 pieces = 144 B):  piece 0 = d f16, dmin f16, scales[12];
 //                             pieces 1..8 = qs[0..127] in GGUF order.
 //   Q6_K (13 pieces = 208 B + d plane): pieces 0..7 = ql[0..127],
-//                             8..11 = qh[0..63], 12 = scales[16];  the f16 d of
-//                             each super-block goes to a separate plane [n][ng].
+//                             8..11 = qh[0..63], 12 = scales[16]; the f16 d of
+//                             each super-block goes to a separate plane.
 //   Q8_0 (17 pieces = 272 B): pieces 2j, 2j+1 = qs of block 8g+j, piece 16 =
 //                             the eight f16 d; a row whose block count is not a
 //                             multiple of 8 is padded with zero blocks.
+// Rows are taken in blocks of 8 (the row count is padded with zero rows to a
+// multiple of 8), and for each (row block, group, piece) the 8 rows' pieces
+// are one 128-byte line:
+//   byte offset of piece p of group g of row r =
+//       (r/8) * rb_stride + (g * PIECES + p) * 128 + (r%8) * 16,
+//   rb_stride = groups * PIECES * 128;
+//   Q6_K d of (r, g): element ((r/8) * groups + g) * 8 + r%8 of the d plane.
+// The decode matvec reads a tile with lanes (group, row) of an 8 x 8 block of
+// a row block: eight full lines per load instruction.  The prefill GEMM reads
+// it with lanes over 32 consecutive rows (output columns) of one group: four
+// full lines per half-wavefront.
 // ---------------------------------------------------------------------------
+constexpr int RB = 8;  // rows per row block
 struct WLayout {
-    const uint8_t *slab = nullptr;  // [n][SLABS][ng][16]
-    const uint16_t *d = nullptr;    // Q6_K only: [n][ng] f16
+    const uint8_t *slab = nullptr;  // row-block tiles
+    const uint16_t *d = nullptr;    // Q6_K only: [n/8][groups][8] f16
     int type = 0;
     int ng = 0;                     // groups per row
-    int64_t row_bytes = 0;          // SLABS * ng * 16
+    int64_t rb_stride = 0;          // bytes per row block
 };
 
 __host__ __device__ constexpr int slabs_of(int type) {
@@ -97,9 +106,10 @@ inline ActPlanes act_planes(void *base, int64_t m, int64_t k) {
 // ---------------------------------------------------------------------------
 hipError_t launch_quantize_q8k(const float *x, int64_t m, int64_t k, ActPlanes a, hipStream_t s);
 hipError_t launch_quantize_q8_0(const float *x, int64_t m, int64_t k, ActPlanes a, hipStream_t s);
-// GGUF blocks of n rows (device memory) -> those rows of the slab layout.
-// dst_slab / dst_d point at the first destination row.  Q8_0 rows must be
-// zeroed beforehand (padding blocks are not written).
+// GGUF blocks of n rows (device memory) -> those rows of the row-block tile
+// layout.  dst_slab / dst_d point at the first destination row block (the
+// first source row is a multiple of 8).  Padding (rows past n in the last row
+// block, Q8_0 padding blocks) is not written: zero the tiles beforehand.
 hipError_t launch_repack(int type, const uint8_t *src, int64_t n, int64_t k, uint8_t *dst_slab, uint16_t *dst_d,
                          hipStream_t s);
 // Decode matvec (any m; batch rows are processed up to 8 at a time).  The
@@ -128,6 +138,23 @@ size_t gemm_workspace_bytes(int type, int64_t m, int64_t n, int64_t k);
 namespace aq {
 
 __device__ __forceinline__ int sdot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
+
+// Raw buffer accesses through a descriptor over [base, base + bytes): a lane
+// whose offset lies past the range reads zeros / drops its store without a
+// memory access, so the loads of a pipeline can be issued unconditionally
+// (no branches around them, hence exact s_waitcnt counts).  BUF_OOB is an
+// offset past every range (bytes < 2^31).
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+constexpr uint32_t BUF_OOB = 0x80000000u;
+constexpr int BUF_NT = 2;  // cache policy: nontemporal (streamed once)
+// Bit casts go through a by-value scalar: this clang's __builtin_bit_cast
+// applied directly to an ext_vector element (v.y) reads element 0.
+__device__ __forceinline__ float u32_as_f32(uint32_t u) { return __builtin_bit_cast(float, u); }
+__device__ __forceinline__ uint32_t f32_as_u32(float f) { return __builtin_bit_cast(uint32_t, f); }
+__device__ __forceinline__ rsrc_t buf_rsrc(const void *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
+}
 
 // DPP lane permutations within a row of 16 lanes.
 template <int CTRL>

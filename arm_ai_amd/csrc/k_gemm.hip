@@ -20,12 +20,14 @@
 //
 // Tiling.  A workgroup (4 wavefronts) owns a 32*MT (m) x 128 (n) output
 // tile; wavefront w owns columns 32w..32w+31 and all rows (MT 32x32 MFMA
-// tiles), so each weight digit operand it builds is used MT times.  Per
-// super-block the workgroup stages the activation rows (256 quant bytes, d,
-// 16 bsums) in LDS (double-buffered, row stride 272 B so the 16-byte reads of
-// consecutive rows hit distinct banks); each lane loads its own weight
-// column's pieces (slab layout: the meta piece and the four quant pieces of its
-// half of the super-block) straight into registers, one super-block ahead.
+// tiles), so each weight digit operand it builds is used MT times.  The
+// activation rows of two super-blocks at a time (quants, bsums, d) are copied
+// global -> LDS directly (global_load_lds, no registers), double-buffered, the
+// 16-byte quant chunks of each row XOR-swizzled so that 16 consecutive rows
+// read distinct banks.  Each lane loads its own weight column's pieces (the
+// meta piece and the four quant pieces of its half of the super-block) into
+// registers one stage ahead; in the row-block tile layout the 32 columns of a
+// wavefront's half read 4 full 128-byte lines per instruction.
 // Work items (tile, k-split) are numbered so that all m-tiles and k-splits of
 // one n-tile run on the same XCD (workgroups are dealt to the 8 XCDs
 // round-robin), where they share that XCD's L2 copy of the weight tile.
@@ -55,8 +57,8 @@ constexpr int NXCD = 8;
 constexpr int TARGET_WG = 256;  // at least one workgroup per CU
 
 struct GemmParams {
-    const uint8_t *w;  // slab plane
-    int64_t row_bytes;
+    const uint8_t *w;  // row-block tiles
+    int64_t rb_stride;
     int ng;            // super-blocks per row (= k / 256)
     const int8_t *xq;  // activation planes
     const float *xd;
@@ -166,12 +168,13 @@ __global__ __launch_bounds__(256, MT == 4 ? 1 : 2) void gemm_q4k_kernel(GemmPara
     };
     // ---- weight pieces of this lane's column (plain loads: the m-tiles of an
     // n-tile reuse them from L2).  Columns past n load column 0 (never stored).
-    const uint8_t *wrow = p.w + (int64_t)(col_ok ? col : 0) * p.row_bytes;
-    const int64_t slab = (int64_t)ng * 16;
+    const int wc = col_ok ? col : 0;
+    const uint8_t *wcol = p.w + (int64_t)(wc >> 3) * p.rb_stride + (wc & 7) * 16;  // + (9 b + piece) * 128
     auto load_b = [&](BStage &st, int b) {
-        st.meta = *(const uint4 *)(wrow + b * 16);
+        const uint8_t *wb = wcol + (int64_t)b * (9 * 128);
+        st.meta = *(const uint4 *)wb;
 #pragma unroll
-        for (int c = 0; c < 4; c++) st.q[c] = *(const uint4 *)(wrow + (1 + 2 * c + h) * slab + b * 16);
+        for (int c = 0; c < 4; c++) st.q[c] = *(const uint4 *)(wb + (1 + 2 * c + h) * 128);
     };
 
     v16f yacc[MT];
@@ -367,7 +370,7 @@ hipError_t launch_gemm(const WLayout &w, int64_t n, int64_t k, const ActPlanes &
     if (g.splits > 1 && (!ws || ws_bytes < g.ws || !counters)) return hipErrorInvalidValue;
     GemmParams p;
     p.w = w.slab;
-    p.row_bytes = w.row_bytes;
+    p.rb_stride = w.rb_stride;
     p.ng = w.ng;
     p.xq = x.qs;
     p.xd = x.d;

@@ -7,19 +7,25 @@
 // every block dot product is computed exactly (v_dot4_i32_i8 on 4 bytes at a
 // time); only the f32 combination order differs from candle's vec_dot_unopt.
 //
-// Mapping.  One lane owns one 256-element group (a Q4_K/Q6_K super-block, or
-// eight Q8_0 blocks) of one weight row per iteration.  The lanes of a "row
-// group" (lpr = next power of two >= groups per row, at most 64) cover a
-// whole row, so a wavefront covers 64/lpr rows, and the loads of piece i of
-// all its groups are one contiguous slab read (the weight layout is described
-// in aq_internal.h).  Each wavefront prefetches the weights of its next
-// iteration before computing the current one.  The activation (all batch rows
-// of the pass) sits in LDS as one 304-byte record per (row, group); the
-// records' stride spreads the 16-byte reads of consecutive lanes over
-// disjoint LDS banks.  With an f32 input the workgroup quantises it into LDS
-// itself (same device code as the quantizer kernels, so the same bytes)
-// while its first weight loads are in flight.
+// Mapping.  A wavefront works on one 8-row block of the weight (the
+// row-block tile layout of aq_internal.h) and a chunk of 8 of its 256-element
+// groups: lane (g_l, r_l) = (lane / 8, lane % 8) owns group 8*chunk + g_l of
+// row 8*block + r_l, so each 16-byte load instruction of the wavefront reads
+// eight full 128-byte lines (nontemporal: the weights are read once per call).
+// A workgroup iteration covers rbw = max(1, 8 / chunks) row blocks with
+// nw = min(8, rbw * chunks) wavefronts (no idle wavefronts below 8 chunks; above
+// 8, wavefront w takes chunks w, w + 8, ...).  A row's chunk partials are
+// reduced across the chunk's lanes (butterfly) and across wavefronts through
+// LDS, in chunk order.  Each wavefront prefetches its next step's weights
+// before computing the current one (ping-pong registers).  The activation (all batch rows of the
+// pass) sits in LDS as one 304-byte record per (row, group); the records'
+// stride spreads the 16-byte reads of consecutive lanes over disjoint LDS
+// banks.  With an f32 input the workgroup quantises it into LDS itself (same
+// device code as the quantizer kernels, so the same bytes) while its first
+// weight loads are in flight.
 #include "aq_internal.h"
+
+#include <mutex>
 
 namespace aq {
 
@@ -29,14 +35,15 @@ constexpr int REC = 304;           // LDS bytes per (batch row, group) activatio
 constexpr int REC_BSUMS = 256;     // Q8_K record: i16 bsums[16]
 constexpr int REC_D = 288;         // Q8_K record: f32 d
 constexpr int REC_D8 = 256;        // Q8_0 record: f32 d[8] (value of the f16 d)
-constexpr size_t LDS_CAP = 64 * 1024;
-constexpr int TARGET_WAVES = 4096;  // about 16 wavefronts per CU on 256 CUs
+constexpr size_t LDS_CAP = 144 * 1024;  // activation records per workgroup (gfx950: 160 KB of LDS per CU)
+constexpr int TARGET_WAVES = 8192;  // resident wavefronts aimed at: 32 per CU on 256 CUs
+constexpr int MIN_WAVES = 1536;     // split a row block over wavefronts below this many
 
 struct MvParams {
-    const uint8_t *w;    // slab plane
+    const uint8_t *w;    // row-block tiles
     const uint16_t *wd;  // Q6_K d plane
-    int64_t row_bytes;
-    int n, k, ng, lpr_log, m, iters, nwaves;
+    int64_t rb_stride;
+    int n, k, ng, nch, np, rbw, nw, nsub, m, iters;  // np: wavefronts per row block, nsub: chunks per wavefront
     const float *x;      // fused: f32 [m][k] of this pass, or null
     ActPlanes act;       // pre-quantised planes of this pass (when x is null)
     float *y;            // [m][n] of this pass
@@ -49,27 +56,24 @@ struct Wt {
     uint32_t d;  // Q6_K super-block d (f16 bits)
 };
 
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-
 // Weights are streamed once per call: nontemporal loads keep them from
-// displacing the (reused) activation in the caches.
+// displacing the (reused) activation in the caches.  Row block rb is
+// wave-uniform; a row block past the end (or a group past the row) reads zeros.
 template <int TYPE>
-__device__ __forceinline__ void load_w(Wt<TYPE> &W, const MvParams &p, int row, int g) {
-    const uint8_t *base = p.w + (int64_t)row * p.row_bytes + (int64_t)g * 16;
-    const int64_t stride = (int64_t)p.ng * 16;
+__device__ __forceinline__ void load_w(Wt<TYPE> &W, const MvParams &p, int rb, int nrb, int g, int r_l) {
+    constexpr int S = slabs_of(TYPE);
+    const bool rb_ok = rb < nrb;
+    const rsrc_t r = buf_rsrc(p.w + (int64_t)rb * p.rb_stride, rb_ok ? (uint32_t)p.rb_stride : 0u);
+    const uint32_t off = g < p.ng ? (uint32_t)(g * (S * 128) + r_l * 16) : BUF_OOB;
 #pragma unroll
-    for (int i = 0; i < slabs_of(TYPE); i++) {
-        const u32x4 t = __builtin_nontemporal_load((const u32x4 *)(base + i * stride));
+    for (int i = 0; i < S; i++) {
+        const u32x4 t = __builtin_amdgcn_raw_buffer_load_b128(r, off + i * 128, 0, BUF_NT);
         W.pc[i] = make_uint4(t.x, t.y, t.z, t.w);
     }
-    if (TYPE == TYPE_Q6_K) W.d = p.wd[(int64_t)row * p.ng + g];
-}
-
-template <int TYPE>
-__device__ __forceinline__ void zero_w(Wt<TYPE> &W) {
-#pragma unroll
-    for (int i = 0; i < slabs_of(TYPE); i++) W.pc[i] = make_uint4(0, 0, 0, 0);
-    W.d = 0;
+    if (TYPE == TYPE_Q6_K) {
+        const rsrc_t rd = buf_rsrc(p.wd + (int64_t)rb * p.ng * RB, rb_ok ? (uint32_t)(p.ng * RB * 2) : 0u);
+        W.d = __builtin_amdgcn_raw_buffer_load_b16(rd, g < p.ng ? (uint32_t)((g * RB + r_l) * 2) : BUF_OOB, 0, BUF_NT);
+    }
 }
 
 __device__ __forceinline__ int byte_u(uint32_t w, int i) { return (int)((w >> (8 * i)) & 0xffu); }
@@ -214,7 +218,7 @@ __device__ __forceinline__ void dot_q6k(const Wt<TYPE_Q6_K> &W, const uint8_t *l
 // eight f16 d.  candle: sumf += (sum_i qw*qx as f32) * f16(d_w) * f16(d_x).
 template <int B, bool DUMP>
 __device__ __forceinline__ void dot_q80(const Wt<TYPE_Q8_0> &W, const uint8_t *lds, int ng, int g, int m,
-                                        float (&f)[B], const MvParams &p, int row) {
+                                        float (&f)[B], const MvParams &p, int row, bool row_ok) {
     const uint32_t dwp[4] = {W.pc[16].x, W.pc[16].y, W.pc[16].z, W.pc[16].w};
     const int nblk = p.k / QK8_0;
 #pragma unroll
@@ -232,7 +236,7 @@ __device__ __forceinline__ void dot_q80(const Wt<TYPE_Q8_0> &W, const uint8_t *l
                 f[b] += ((float)isum * dw) * dx;
                 if (DUMP) {
                     const int blk = 8 * g + j;
-                    if (blk < nblk) {
+                    if (blk < nblk && row_ok) {
                         const int64_t o = ((int64_t)b * p.n + row) * nblk + blk;
                         p.S[o] = isum;
                         p.Smin[o] = 0;
@@ -247,8 +251,7 @@ template <int TYPE, int B, bool DUMP>
 __device__ __forceinline__ void group_dot(const Wt<TYPE> &W, const uint8_t *lds, const MvParams &p, int g, int row,
                                           bool valid, float (&f)[B]) {
     if (TYPE == TYPE_Q8_0) {
-        dot_q80<B, DUMP && true>(*(const Wt<TYPE_Q8_0> *)&W, lds, p.ng, g, p.m, f, p, row);
-        (void)valid;
+        dot_q80<B, DUMP>(*(const Wt<TYPE_Q8_0> *)&W, lds, p.ng, g, p.m, f, p, row, valid);
     } else {
         int So[B], Smo[B];
         if (TYPE == TYPE_Q4_K) dot_q4k<B, DUMP>(*(const Wt<TYPE_Q4_K> *)&W, lds, p.ng, g, p.m, f, So, Smo);
@@ -269,52 +272,61 @@ __device__ __forceinline__ void group_dot(const Wt<TYPE> &W, const uint8_t *lds,
 // Activation of this pass into LDS records.  The global loads of the first
 // PRE records of each wave (rec_load) are issued before the weight loads of
 // the first iteration, so quantising them (rec_store) waits only for them.
-constexpr int NW = 8;    // wavefronts per workgroup
+constexpr int NW = 8;    // wavefronts per workgroup, at most
 constexpr int PRE = 4;   // records per wave whose loads precede the weight loads
 
 struct ActStage {
-    float4 v[PRE];
-    int4 q[PRE];
+    u32x4 q[PRE];   // f32 inputs (fused) or quant bytes / bsums (pre-quantised)
     float dsc[PRE];
 };
 
-template <int TYPE>
+// Record t = (batch row b, group g) of this pass.  Every lane issues the same
+// loads whatever t is (records past the end read zeros).
+template <int TYPE, bool FUSED>
 __device__ __forceinline__ void rec_load(ActStage &st, int r, const MvParams &p, int t, int lane) {
-    const int ng = p.ng, k = p.k;
+    const int ng = p.ng, k = p.k, m = p.m;
+    const bool ok = t < m * ng;
     const int b = t / ng, g = t - b * ng;
-    if (p.x) {
+    if (FUSED) {
+        const rsrc_t rx = buf_rsrc(p.x, (uint32_t)(m * k * 4));
+        uint32_t off;
         if (TYPE != TYPE_Q8_0) {
-            st.v[r] = *(const float4 *)(p.x + (int64_t)b * k + g * QK_K + 4 * lane);
+            off = ok ? (uint32_t)((b * k + g * QK_K + 4 * lane) * 4) : BUF_OOB;
         } else {
             const int j = lane >> 3, sub = lane & 7;
-            st.v[r] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            if ((8 * g + j) * QK8_0 < k) st.v[r] = *(const float4 *)(p.x + (int64_t)b * k + (8 * g + j) * QK8_0 + 4 * sub);
+            off = ok && (8 * g + j) * QK8_0 < k ? (uint32_t)((b * k + (8 * g + j) * QK8_0 + 4 * sub) * 4) : BUF_OOB;
         }
+        st.q[r] = __builtin_amdgcn_raw_buffer_load_b128(rx, off, 0, 0);
+    } else if (TYPE != TYPE_Q8_0) {
+        const rsrc_t rq = buf_rsrc(p.act.qs, (uint32_t)(m * k));
+        const rsrc_t rs = buf_rsrc(p.act.bsums, (uint32_t)(m * (k / 16) * 2));
+        const rsrc_t rd = buf_rsrc(p.act.d, (uint32_t)(m * (k / QK_K) * 4));
+        const u32x4 q = __builtin_amdgcn_raw_buffer_load_b128(rq, ok && lane < 16 ? (uint32_t)(b * k + g * QK_K + 16 * lane) : BUF_OOB, 0, 0);
+        const u32x4 bs = __builtin_amdgcn_raw_buffer_load_b128(
+            rs, ok && (unsigned)(lane - 16) < 2u ? (uint32_t)((b * (k / 16) + g * 16 + 8 * (lane - 16)) * 2) : BUF_OOB, 0, 0);
+        const uint32_t d = __builtin_amdgcn_raw_buffer_load_b32(rd, ok && lane == 18 ? (uint32_t)((b * (k / QK_K) + g) * 4) : BUF_OOB, 0, 0);
+        st.q[r] = lane < 16 ? q : bs;
+        st.dsc[r] = u32_as_f32(d);
     } else {
-        st.q[r] = make_int4(0, 0, 0, 0);
-        st.dsc[r] = 0.0f;
-        if (TYPE != TYPE_Q8_0) {
-            if (lane < 16) st.q[r] = *(const int4 *)(p.act.qs + (int64_t)b * k + g * QK_K + 16 * lane);
-            else if (lane < 18) st.q[r] = *(const int4 *)(p.act.bsums + (int64_t)b * (k / 16) + g * 16 + 8 * (lane - 16));
-            else if (lane == 18) st.dsc[r] = p.act.d[(int64_t)b * (k / QK_K) + g];
-        } else {
-            const int nblk = k / QK8_0;
-            if (lane < 16) {
-                const int j = lane >> 1;
-                if (8 * g + j < nblk) st.q[r] = *(const int4 *)(p.act.qs + (int64_t)b * k + (8 * g + j) * QK8_0 + 16 * (lane & 1));
-            } else if (lane < 24) {
-                const int j = lane - 16;
-                if (8 * g + j < nblk) st.dsc[r] = p.act.d[(int64_t)b * nblk + 8 * g + j];
-            }
-        }
+        const int nblk = k / QK8_0;
+        const rsrc_t rq = buf_rsrc(p.act.qs, (uint32_t)(m * k));
+        const rsrc_t rd = buf_rsrc(p.act.d, (uint32_t)(m * nblk * 4));
+        const int jq = lane >> 1, jd = lane - 16;
+        const u32x4 q = __builtin_amdgcn_raw_buffer_load_b128(
+            rq, ok && lane < 16 && 8 * g + jq < nblk ? (uint32_t)(b * k + (8 * g + jq) * QK8_0 + 16 * (lane & 1)) : BUF_OOB, 0, 0);
+        const uint32_t d = __builtin_amdgcn_raw_buffer_load_b32(
+            rd, ok && (unsigned)jd < 8u && 8 * g + jd < nblk ? (uint32_t)((b * nblk + 8 * g + jd) * 4) : BUF_OOB, 0, 0);
+        st.q[r] = q;
+        st.dsc[r] = u32_as_f32(d);
     }
 }
 
-template <int TYPE>
-__device__ __forceinline__ void rec_store(const ActStage &st, int r, uint8_t *lds, const MvParams &p, int t, int lane) {
+template <int TYPE, bool FUSED>
+__device__ __forceinline__ void rec_store(const ActStage &st, int r, uint8_t *lds, int t, int lane) {
     uint8_t *rec = lds + t * REC;
-    if (p.x) {
-        const float v[4] = {st.v[r].x, st.v[r].y, st.v[r].z, st.v[r].w};
+    if (FUSED) {
+        const u32x4 u = st.q[r];
+        const float v[4] = {u32_as_f32(u.x), u32_as_f32(u.y), u32_as_f32(u.z), u32_as_f32(u.w)};
         if (TYPE != TYPE_Q8_0) {
             int bsum;
             float d;
@@ -331,120 +343,160 @@ __device__ __forceinline__ void rec_store(const ActStage &st, int r, uint8_t *ld
         }
     } else {
         if (TYPE != TYPE_Q8_0) {
-            if (lane < 16) *(int4 *)(rec + 16 * lane) = st.q[r];
-            else if (lane < 18) *(int4 *)(rec + REC_BSUMS + 16 * (lane - 16)) = st.q[r];
+            if (lane < 16) *(u32x4 *)(rec + 16 * lane) = st.q[r];
+            else if (lane < 18) *(u32x4 *)(rec + REC_BSUMS + 16 * (lane - 16)) = st.q[r];
             else if (lane == 18) *(float *)(rec + REC_D) = st.dsc[r];
         } else {
-            if (lane < 16) *(int4 *)(rec + 16 * lane) = st.q[r];
+            if (lane < 16) *(u32x4 *)(rec + 16 * lane) = st.q[r];
             else if (lane < 24) *(float *)(rec + REC_D8 + 4 * (lane - 16)) = st.dsc[r];
         }
     }
 }
 
-template <int TYPE, int B, bool DUMP, bool MULTI>
+template <int TYPE, int B, bool DUMP, bool FUSED>
 __global__ __launch_bounds__(NW * 64) void matvec_kernel(MvParams p) {
     extern __shared__ __align__(16) uint8_t lds[];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int lpr = 1 << p.lpr_log, rpw = 64 >> p.lpr_log;
-    const int sl = lane & (lpr - 1), grp = lane >> p.lpr_log;
-    const int gw = blockIdx.x * NW + wave;
-    const int iters = gw < p.nwaves ? p.iters : 0;
+    __shared__ float red[NW][B][RB];  // per-wavefront chunk partials of the 8 rows of a row block
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int g_l = lane >> 3, r_l = lane & 7;
+    const int nw = p.nw, nsub = p.nsub;
+    const int np = p.np;                     // wavefronts (chunk partials) per row block
+    const int rbo = wave / np;               // row block of this wavefront within an iteration
+    const int c0 = wave - rbo * np;          // its first chunk; step j takes chunk c0 + np * j
+    const int nrb = (p.n + RB - 1) / RB;
     const int nrec = p.m * p.ng;
+    const int nsteps = p.iters * nsub;
+    // a step past the last reads zeros: blockIdx + iters * gridDim >= workgroup iterations
+    auto rb_of = [&](int st) { return (int)(blockIdx.x + (st / nsub) * gridDim.x) * p.rbw + rbo; };
+    auto g_of = [&](int st) { return 8 * (c0 + np * (st % nsub)) + g_l; };
 
     // 1. activation loads of the first records, 2. weight loads of the first
-    // iteration, 3. quantise / copy into LDS (waits only for step 1).
-    ActStage st;
+    // step, 3. quantise / copy into LDS (waits only for step 1).
+    ActStage as;
 #pragma unroll
-    for (int r = 0; r < PRE; r++) {
-        const int t = wave + NW * r;
-        if (t < nrec) rec_load<TYPE>(st, r, p, t, lane);
-    }
+    for (int r = 0; r < PRE; r++) rec_load<TYPE, FUSED>(as, r, p, wave + nw * r, lane);
     Wt<TYPE> wa, wb;
-    int row = gw * rpw + grp;
-    bool valid = iters > 0 && row < p.n && sl < p.ng;
-    if (!MULTI) {
-        if (valid) load_w<TYPE>(wa, p, row, sl);
-        else zero_w<TYPE>(wa);
-    }
+    load_w<TYPE>(wa, p, rb_of(0), nrb, g_of(0), r_l);
 #pragma unroll
     for (int r = 0; r < PRE; r++) {
-        const int t = wave + NW * r;
-        if (t < nrec) rec_store<TYPE>(st, r, lds, p, t, lane);
+        const int t = wave + nw * r;
+        if (t < nrec) rec_store<TYPE, FUSED>(as, r, lds, t, lane);
     }
-    for (int t = wave + NW * PRE; t < nrec; t += NW) {
-        rec_load<TYPE>(st, 0, p, t, lane);
-        rec_store<TYPE>(st, 0, lds, p, t, lane);
+    for (int t = wave + nw * PRE; t < nrec; t += nw) {
+        rec_load<TYPE, FUSED>(as, 0, p, t, lane);
+        rec_store<TYPE, FUSED>(as, 0, lds, t, lane);
     }
     __syncthreads();
 
-    auto finish = [&](float (&f)[B], int r) {
-        // reduce over the lanes of the row group (aligned groups of lpr lanes)
+    float f[B];
 #pragma unroll
-        for (int b = 0; b < B; b++)
-            for (int off = lpr >> 1; off >= 1; off >>= 1) f[b] += __shfl_xor(f[b], off);
-        if (sl == 0 && r < p.n) {
+    for (int b = 0; b < B; b++) f[b] = 0.0f;
+    const rsrc_t ry = buf_rsrc(p.y, (uint32_t)(p.m * p.n * 4));
+
+    // Row block partials of iteration it: butterfly over the chunk's 8 groups
+    // of each row (lanes r_l, r_l + 8, ..., r_l + 56); with several wavefronts
+    // per row block, lane r of wavefront w < rbw then sums row r of row block
+    // w's partials in chunk order (the other lanes' stores are dropped).
+    auto finish = [&](int it) {
 #pragma unroll
-            for (int b = 0; b < B; b++)
-                if (b < p.m) p.y[(int64_t)b * p.n + r] = f[b];
+        for (int b = 0; b < B; b++) {
+            f[b] += __shfl_xor(f[b], 8);
+            f[b] += __shfl_xor(f[b], 16);
+            f[b] += __shfl_xor(f[b], 32);
         }
+        if (np == 1) {  // workgroup-uniform: this wavefront holds whole rows, lanes 0..7 store them
+            const int row = rb_of(it * nsub) * RB + r_l;
+            const bool ok = lane < RB && row < p.n;
+#pragma unroll
+            for (int b = 0; b < B; b++) {
+                __builtin_amdgcn_raw_buffer_store_b32(f32_as_u32(f[b]), ry,
+                                                      ok && b < p.m ? (uint32_t)((b * p.n + row) * 4) : BUF_OOB, 0, 0);
+                f[b] = 0.0f;
+            }
+            return;
+        }
+        if (g_l == 0) {
+#pragma unroll
+            for (int b = 0; b < B; b++) red[wave][b][r_l] = f[b];
+        }
+#pragma unroll
+        for (int b = 0; b < B; b++) f[b] = 0.0f;
+        __syncthreads();
+        const int wr = wave < p.rbw ? wave : 0;
+        const int row = ((int)(blockIdx.x + it * gridDim.x) * p.rbw + wr) * RB + r_l;
+        const bool ok = wave < p.rbw && lane < RB && row < p.n;
+#pragma unroll
+        for (int b = 0; b < B; b++) {
+            float s = 0.0f;
+            for (int c = 0; c < np; c++) s += red[wr * np + c][b][r_l];
+            __builtin_amdgcn_raw_buffer_store_b32(f32_as_u32(s), ry,
+                                                  ok && b < p.m ? (uint32_t)((b * p.n + row) * 4) : BUF_OOB, 0, 0);
+        }
+        __syncthreads();
+    };
+    // No branch around the dot product: a row block past the end holds zero
+    // weights (its loads read zeros), which add nothing, and keeping every
+    // path alike keeps the compiler's s_waitcnt counts exact.
+    auto step = [&](const Wt<TYPE> &W, int st) {
+        const int g = g_of(st), row = rb_of(st) * RB + r_l;
+        group_dot<TYPE, B, DUMP>(W, lds, p, g < p.ng ? g : p.ng - 1, row, row < p.n && g < p.ng, f);
+        if (st % nsub == nsub - 1) finish(st / nsub);  // workgroup-uniform
     };
 
-    if (!MULTI) {
-        // ping-pong: wa holds iteration it, wb iteration it + 1
-        for (int it = 0; it < iters; it += 2) {
-            const int row_b = (gw + (it + 1) * p.nwaves) * rpw + grp;
-            const bool valid_b = it + 1 < iters && row_b < p.n && sl < p.ng;
-            if (valid_b) load_w<TYPE>(wb, p, row_b, sl);
-            float f[B];
-#pragma unroll
-            for (int b = 0; b < B; b++) f[b] = 0.0f;
-            if (valid) group_dot<TYPE, B, DUMP>(wa, lds, p, sl, row, true, f);
-            finish(f, row);
-            if (it + 1 >= iters) break;
-            row = (gw + (it + 2) * p.nwaves) * rpw + grp;
-            valid = it + 2 < iters && row < p.n && sl < p.ng;
-            if (valid) load_w<TYPE>(wa, p, row, sl);
-#pragma unroll
-            for (int b = 0; b < B; b++) f[b] = 0.0f;
-            if (valid_b) group_dot<TYPE, B, DUMP>(wb, lds, p, sl, row_b, true, f);
-            finish(f, row_b);
-        }
-    } else {
-        for (int it = 0; it < iters; it++) {
-            float f[B];
-#pragma unroll
-            for (int b = 0; b < B; b++) f[b] = 0.0f;
-            if (row < p.n) {
-                for (int g = sl; g < p.ng; g += 64) {
-                    load_w<TYPE>(wb, p, row, g);
-                    group_dot<TYPE, B, DUMP>(wb, lds, p, g, row, true, f);
-                }
-            }
-            finish(f, row);
-            row = (gw + (it + 1) * p.nwaves) * rpw + grp;
-        }
+    // ping-pong: wa holds step st, wb step st + 1
+    for (int st = 0; st < nsteps; st += 2) {
+        load_w<TYPE>(wb, p, rb_of(st + 1), nrb, g_of(st + 1), r_l);
+        step(wa, st);
+        if (st + 1 >= nsteps) break;
+        load_w<TYPE>(wa, p, rb_of(st + 2), nrb, g_of(st + 2), r_l);
+        step(wb, st + 1);
     }
 }
 
+// Dynamic LDS above 64 KB has to be allowed per kernel, once.
 template <int TYPE, int B>
-hipError_t launch_tb(const MvParams &p, unsigned grid, size_t lds, bool dump, bool multi, hipStream_t s) {
-    if (dump) {
-        if (multi) matvec_kernel<TYPE, B, true, true><<<grid, NW * 64, lds, s>>>(p);
-        else matvec_kernel<TYPE, B, true, false><<<grid, NW * 64, lds, s>>>(p);
+hipError_t allow_lds() {
+    static std::once_flag once;
+    static hipError_t err = hipSuccess;
+    std::call_once(once, [] {
+        const int cap = (int)LDS_CAP;
+        const void *fns[4] = {(const void *)matvec_kernel<TYPE, B, false, false>,
+                              (const void *)matvec_kernel<TYPE, B, false, true>,
+                              (const void *)matvec_kernel<TYPE, B, true, false>,
+                              (const void *)matvec_kernel<TYPE, B, true, true>};
+        for (const void *f : fns) {
+            const hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, cap);
+            if (e != hipSuccess) err = e;
+        }
+    });
+    return err;
+}
+
+template <int TYPE, int B>
+hipError_t launch_tb(const MvParams &p, unsigned grid, size_t lds, bool dump, hipStream_t s) {
+    if (lds > 64 * 1024) {
+        const hipError_t e = allow_lds<TYPE, B>();
+        if (e != hipSuccess) return e;
+    }
+    const dim3 blk(p.nw * 64);
+    if (p.x) {
+        if (dump) matvec_kernel<TYPE, B, true, true><<<grid, blk, lds, s>>>(p);
+        else matvec_kernel<TYPE, B, false, true><<<grid, blk, lds, s>>>(p);
     } else {
-        if (multi) matvec_kernel<TYPE, B, false, true><<<grid, NW * 64, lds, s>>>(p);
-        else matvec_kernel<TYPE, B, false, false><<<grid, NW * 64, lds, s>>>(p);
+        if (dump) matvec_kernel<TYPE, B, true, false><<<grid, blk, lds, s>>>(p);
+        else matvec_kernel<TYPE, B, false, false><<<grid, blk, lds, s>>>(p);
     }
     return hipGetLastError();
 }
 
 template <int TYPE>
-hipError_t launch_t(int B, const MvParams &p, unsigned grid, size_t lds, bool dump, bool multi, hipStream_t s) {
+hipError_t launch_t(int B, const MvParams &p, unsigned grid, size_t lds, bool dump, hipStream_t s) {
     switch (B) {
-    case 1: return launch_tb<TYPE, 1>(p, grid, lds, dump, multi, s);
-    case 2: return launch_tb<TYPE, 2>(p, grid, lds, dump, multi, s);
-    case 4: return launch_tb<TYPE, 4>(p, grid, lds, dump, multi, s);
-    case 8: return launch_tb<TYPE, 8>(p, grid, lds, dump, multi, s);
+    case 1: return launch_tb<TYPE, 1>(p, grid, lds, dump, s);
+    case 2: return launch_tb<TYPE, 2>(p, grid, lds, dump, s);
+    case 4: return launch_tb<TYPE, 4>(p, grid, lds, dump, s);
+    case 8: return launch_tb<TYPE, 8>(p, grid, lds, dump, s);
     default: return hipErrorInvalidConfiguration;
     }
 }
@@ -465,15 +517,24 @@ hipError_t launch_matvec(const WLayout &w, int64_t n, int64_t k, const float *x,
     if ((S == nullptr) != (Smin == nullptr)) return hipErrorInvalidValue;
     if (m == 0) return hipSuccess;
     const int ng = w.ng;
-    if ((size_t)ng * REC > LDS_CAP) return hipErrorNotSupported;  // k > 55040
-    int lpr_log = 0;
-    while ((1 << lpr_log) < ng && lpr_log < 6) lpr_log++;
-    const bool multi = ng > 64;
-    const int rpw = 64 >> lpr_log;
-    const int64_t ri = (n + rpw - 1) / rpw;  // wavefront iterations
-    const int64_t iters = (ri + TARGET_WAVES - 1) / TARGET_WAVES;
-    const int64_t nwaves = (ri + iters - 1) / iters;
-    const int64_t grid = (nwaves + NW - 1) / NW;
+    if ((size_t)ng * REC > LDS_CAP) return hipErrorNotSupported;  // k > 124160
+    if ((int64_t)8 * n * 4 >= ((int64_t)1 << 31)) return hipErrorNotSupported;  // y of a pass: 32-bit buffer offsets
+    const int64_t nrb = (n + RB - 1) / RB;
+    // Wavefronts per row block: as few as give MIN_WAVES wavefronts in all
+    // (fewer, longer-lived wavefronts keep two steps of loads in flight and
+    // need no cross-wavefront reduction), at most one per chunk and NW.
+    const int nch = (ng + 7) / 8;  // 8-group chunks per row
+    int np = 1;
+    while (np < NW && np < nch && nrb * np < MIN_WAVES) np *= 2;
+    if (np > nch) np = nch;
+    const int rbw = NW / np;                // row blocks per workgroup iteration
+    const int nw = rbw * np;                // wavefronts per workgroup
+    const int nsub = (nch + np - 1) / np;   // chunks per wavefront per row block
+    const int64_t wg_iters = (nrb + rbw - 1) / rbw;  // workgroup iterations in total
+    const int64_t target_wg = TARGET_WAVES / nw;
+    const int64_t iters = (wg_iters + target_wg - 1) / target_wg;
+    const int64_t grid = (wg_iters + iters - 1) / iters;
+    if ((int64_t)iters * nsub > 0x7fffffff) return hipErrorInvalidValue;
     const int64_t nblk = k / blk;
     int64_t r0 = 0;
     while (r0 < m) {
@@ -484,14 +545,17 @@ hipError_t launch_matvec(const WLayout &w, int64_t n, int64_t k, const float *x,
         MvParams p;
         p.w = w.slab;
         p.wd = w.d;
-        p.row_bytes = w.row_bytes;
+        p.rb_stride = w.rb_stride;
         p.n = (int)n;
         p.k = (int)k;
         p.ng = ng;
-        p.lpr_log = lpr_log;
+        p.nch = nch;
+        p.np = np;
+        p.rbw = rbw;
+        p.nw = nw;
+        p.nsub = nsub;
         p.m = mb;
         p.iters = (int)iters;
-        p.nwaves = (int)nwaves;
         p.x = x ? x + r0 * k : nullptr;
         if (act) {
             p.act.qs = act->qs + r0 * k;
@@ -507,9 +571,9 @@ hipError_t launch_matvec(const WLayout &w, int64_t n, int64_t k, const float *x,
         const size_t lds = (size_t)B * ng * REC;
         hipError_t e;
         switch (type) {
-        case TYPE_Q4_K: e = launch_t<TYPE_Q4_K>(B, p, (unsigned)grid, lds, S != nullptr, multi, s); break;
-        case TYPE_Q6_K: e = launch_t<TYPE_Q6_K>(B, p, (unsigned)grid, lds, S != nullptr, multi, s); break;
-        default: e = launch_t<TYPE_Q8_0>(B, p, (unsigned)grid, lds, S != nullptr, multi, s); break;
+        case TYPE_Q4_K: e = launch_t<TYPE_Q4_K>(B, p, (unsigned)grid, lds, S != nullptr, s); break;
+        case TYPE_Q6_K: e = launch_t<TYPE_Q6_K>(B, p, (unsigned)grid, lds, S != nullptr, s); break;
+        default: e = launch_t<TYPE_Q8_0>(B, p, (unsigned)grid, lds, S != nullptr, s); break;
         }
         if (e != hipSuccess) return e;
         r0 += mb;

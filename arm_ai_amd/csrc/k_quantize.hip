@@ -1,5 +1,5 @@
 // k_quantize.hip -- activation quantizers (Q8_K, Q8_0) and the one-time
-// weight repack into the slab layout, for gfx950.
+// weight repack into the row-block tile layout, for gfx950.
 //
 // Q8_K follows candle-core 0.8.4 BlockQ8K::from_float (the quantize_row_q8k
 // step of k_quants::matmul, reached from native/arm_ai_nif/src/llama_candle.rs:93,
@@ -94,7 +94,7 @@ hipError_t launch_quantize_q8_0(const float *x, int64_t m, int64_t k, ActPlanes 
 }
 
 // ---------------------------------------------------------------------------
-// Weight repack: GGUF array-of-blocks -> slab layout (aq_internal.h).
+// Weight repack: GGUF array-of-blocks -> row-block tiles (aq_internal.h).
 // One thread per source byte; grid-stride over all bytes of the n rows.
 // ---------------------------------------------------------------------------
 template <int TYPE>
@@ -102,33 +102,33 @@ __global__ __launch_bounds__(256) void repack_kernel(const uint8_t *__restrict__
                                                      int ng, uint8_t *__restrict__ slab, uint16_t *__restrict__ dpl) {
     constexpr int BYTES = TYPE == TYPE_Q4_K ? 144 : TYPE == TYPE_Q6_K ? 210 : 34;
     constexpr int S = slabs_of(TYPE);
-    const int64_t row_bytes = (int64_t)S * ng * 16;
+    const int64_t rb_stride = (int64_t)ng * S * 128;
     const int64_t total = n * nblk * BYTES;
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
         const int64_t blk = i / BYTES;  // block index over all rows
         const int o = (int)(i - blk * BYTES);
         const int64_t row = blk / nblk, b = blk - row * nblk;
-        uint8_t *rowp = slab + row * row_bytes;
+        uint8_t *rbp = slab + (row >> 3) * rb_stride + (row & 7) * 16;  // + (g * S + piece) * 128 + byte
         if (TYPE == TYPE_Q4_K) {
             // bytes 0..15 (d, dmin, scales) -> piece 0; qs byte j -> piece 1 + j/16
             const int piece = o < 16 ? 0 : 1 + (o - 16) / 16;
             const int w = o < 16 ? o : (o - 16) & 15;
-            rowp[((int64_t)piece * ng + b) * 16 + w] = src[i];
+            rbp[(b * S + piece) * 128 + w] = src[i];
         } else if (TYPE == TYPE_Q6_K) {
             if (o < 208) {
                 // ql 0..127 -> pieces 0..7, qh 128..191 -> 8..11, scales 192..207 -> 12
-                rowp[((int64_t)(o >> 4) * ng + b) * 16 + (o & 15)] = src[i];
+                rbp[(b * S + (o >> 4)) * 128 + (o & 15)] = src[i];
             } else {
-                ((uint8_t *)(dpl + row * ng + b))[o - 208] = src[i];
+                ((uint8_t *)(dpl + ((row >> 3) * ng + b) * 8 + (row & 7)))[o - 208] = src[i];
             }
         } else {
             // Q8_0 block b = 8g + j: d -> piece 16 bytes 2j..2j+1; qs byte q -> piece 2j + q/16
             const int64_t g = b >> 3;
             const int j = (int)(b & 7);
-            if (o < 2) rowp[((int64_t)16 * ng + g) * 16 + 2 * j + o] = src[i];
+            if (o < 2) rbp[(g * S + 16) * 128 + 2 * j + o] = src[i];
             else {
                 const int q = o - 2;
-                rowp[((int64_t)(2 * j + (q >> 4)) * ng + g) * 16 + (q & 15)] = src[i];
+                rbp[(g * S + 2 * j + (q >> 4)) * 128 + (q & 15)] = src[i];
             }
         }
     }

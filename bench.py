@@ -28,6 +28,7 @@ and the Q4_K matvec, i.e. candle's QMatMul::forward for that call.  At batch
   profiles/traffic_matvec_q4k_14336x4096_b1.json, null if absent.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-extra] [--no-cpu]
+       python bench.py --case NAME          (one of the extra configurations alone, e.g. for a profile)
        python bench.py --copy-calibration   (ten 64 MiB device-to-device copies, for PMC scaling)
 """
 from __future__ import annotations
@@ -199,6 +200,34 @@ def measure_prefill(ctx, n, k, m, steps, warmup, seed):
     return out
 
 
+MATVEC_CASES = {  # name: (weight type, n, k, m, seed)
+    "c0_q4k_5632x2048_b1": (12, 5632, 2048, 1, 0),
+    "c1_q8_0_2048x2048_b1": (8, 2048, 2048, 1, 1),
+    "c1_q6k_32000x2048_b1": (14, 32000, 2048, 1, 2),
+    "c4_q4k_4096x14336_b1": (12, 4096, 14336, 1, 5),
+    "c4_q4k_14336x4096_b8": (12, 14336, 4096, 8, 6),
+    "c4_q6k_128256x4096_b1": (14, 128256, 4096, 1, 7),
+}
+PREFILL_CASES = {  # name: (n, k, m, seed), Q4_K weight
+    "c3_prefill_q4k_5632x2048_m512": (5632, 2048, 512, 3),
+    "c3_prefill_q4k_2048x5632_m512": (2048, 5632, 512, 3),
+    "c4_prefill_q4k_14336x4096_m512": (14336, 4096, 512, 4),
+}
+
+
+def run_case(ctx, name, steps, warmup):
+    if name in MATVEC_CASES:
+        wt, n_, k_, m_, seed = MATVEC_CASES[name]
+        w2, *_, out = measure(ctx, wt, n_, k_, m_, min(steps, 100), min(warmup, 10), seed)
+        w2.free()
+        log(f"{name}: step {out['step_us']} us ({out['step_GBps']} GB/s), pre-quantised matvec {out['matvec_us']} us ({out['matvec_GBps']} GB/s)")
+        return out
+    n_, k_, m_, seed = PREFILL_CASES[name]
+    out = measure_prefill(ctx, n_, k_, m_, min(steps, 50), min(warmup, 5), seed)
+    log(f"{name}: step {out['step_us']} us ({out['step_TOPS']} TOPS), gemm {out['gemm_us']} us ({out['gemm_TOPS']} TOPS, {out['gemm_frac_int8_peak']} of int8 peak)")
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -206,6 +235,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-extra", action="store_true", help="skip the other configurations")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--case", default=None, help="run only this extra configuration and print its JSON")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run ten 64 MiB device-to-device copies (known-size kernel for PMC scaling)")
     args = ap.parse_args()
@@ -230,8 +260,17 @@ def main() -> int:
         print(json.dumps({"copy_calibration_bytes": nbytes, "copies": 10}), flush=True)
         return 0
 
+    if args.case is not None and args.case not in MATVEC_CASES and args.case not in PREFILL_CASES:
+        print(f"unknown case {args.case!r}; cases: {', '.join(list(MATVEC_CASES) + list(PREFILL_CASES))}", file=sys.stderr)
+        return 2
+
     ctx = A.Context(0)
     log("context ready on device 0")
+    if args.case is not None:
+        out = run_case(ctx, args.case, args.steps, args.warmup)
+        ctx.close()
+        print(json.dumps({"case": args.case, **out}), flush=True)
+        return 0
     n, k, m = 14336, 4096, 1
     wl, step_ms, step_wall, kern_ms, head = measure(ctx, 12, n, k, m, args.steps, args.warmup, seed=4)
     log(f"headline: step {step_ms*1e3:.2f} us ({wl.step_bytes / step_ms / 1e6:.1f} GB/s), pre-quantised matvec {kern_ms*1e3:.2f} us ({head['matvec_GBps']} GB/s)")
@@ -266,7 +305,7 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic_from_profile(),
-            "kernel": "matvec_kernel<12, 1, false, false> (Q4_K, batch 1, Q8_K quantisation fused)",
+            "kernel": "matvec_kernel<12, 1, false, true> (Q4_K, batch 1, Q8_K quantisation fused)",
             "bytes_per_launch": wl.step_bytes,
             "avg_launch_us": round(step_ms * 1e3, 3),
         },
@@ -279,25 +318,10 @@ def main() -> int:
 
     if not args.no_extra:
         extra = {}
-        cases = [
-            ("c0_q4k_5632x2048_b1", 12, 5632, 2048, 1, 0),
-            ("c1_q8_0_2048x2048_b1", 8, 2048, 2048, 1, 1),
-            ("c1_q6k_32000x2048_b1", 14, 32000, 2048, 1, 2),
-            ("c4_q4k_4096x14336_b1", 12, 4096, 14336, 1, 5),
-            ("c4_q4k_14336x4096_b8", 12, 14336, 4096, 8, 6),
-            ("c4_q6k_128256x4096_b1", 14, 128256, 4096, 1, 7),
-        ]
-        for name, wt, n_, k_, m_, seed in cases:
-            w2, *_, out = measure(ctx, wt, n_, k_, m_, min(args.steps, 100), min(args.warmup, 10), seed)
-            w2.free()
-            extra[name] = out
-            log(f"{name}: step {out['step_us']} us ({out['step_GBps']} GB/s), pre-quantised matvec {out['matvec_us']} us ({out['matvec_GBps']} GB/s)")
-        for name, n_, k_, m_, seed in [("c3_prefill_q4k_5632x2048_m512", 5632, 2048, 512, 3),
-                                        ("c3_prefill_q4k_2048x5632_m512", 2048, 5632, 512, 3),
-                                        ("c4_prefill_q4k_14336x4096_m512", 14336, 4096, 512, 4)]:
-            out = measure_prefill(ctx, n_, k_, m_, min(args.steps, 50), min(args.warmup, 5), seed)
-            extra[name] = out
-            log(f"{name}: step {out['step_us']} us ({out['step_TOPS']} TOPS), gemm {out['gemm_us']} us ({out['gemm_TOPS']} TOPS, {out['gemm_frac_int8_peak']} of int8 peak)")
+        for name in MATVEC_CASES:
+            extra[name] = run_case(ctx, name, args.steps, args.warmup)
+        for name in PREFILL_CASES:
+            extra[name] = run_case(ctx, name, args.steps, args.warmup)
         result["extra"] = extra
     else:
         result["extra"] = {}

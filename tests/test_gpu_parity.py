@@ -175,6 +175,16 @@ def test_k_coverage(ctx, wtype, k, m):
     check_matmul(ctx, W, x)
 
 
+@pytest.mark.parametrize("k", [55296, 65536])
+@pytest.mark.parametrize("wtype", [S.TYPE_Q4_K, S.TYPE_Q8_0])
+@pytest.mark.parametrize("m", [1, 3])
+def test_long_rows_large_lds(ctx, wtype, k, m):
+    # activation records above 64 KB of LDS per workgroup, batch split into passes
+    W = S.make_weight(wtype, 24, k, seed=k + m + wtype)
+    x = S.make_activation(m, k, seed=k + 1)
+    check_matmul(ctx, W, x)
+
+
 def test_single_row_weight(ctx):
     W = S.make_weight(S.TYPE_Q4_K, 1, 256, seed=3)
     x = S.make_activation(2, 256, seed=3)
