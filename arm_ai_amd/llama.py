@@ -1,0 +1,387 @@
+"""The call sites of the quantized matmuls: a Llama decoder driven like ArmAI.LlamaCandle.
+
+In the reference, ``llama_candle_generate_op`` (native/arm_ai_nif/src/llama_candle.rs:58-139)
+runs candle-transformers' ``quantized_llama::ModelWeights::forward`` once over the
+prompt at offset 0 (prefill, :93) and then once per generated token (decode,
+:119), picking each next token by a first-maximum argmax (:154-176).  Each
+forward makes 7 ``QMatMul::forward`` calls per layer (wq, wk, wv, wo, w1, w3,
+w2) plus the output head: for TinyLlama-1.1B that is 155 quantized matmuls per
+token, which is where the time goes.
+
+Here those 155 calls are this library's GPU QMatMuls (the product, through the
+C ABI, device pointers, on the context's HIP stream).  The operations between
+them (token embedding, RMSNorm, interleaved RoPE, grouped-query attention with
+a KV cache, SiLU gate, residual adds, argmax) are not part of the quantized
+matmul path; they run as PyTorch f32 operations enqueued on the same stream,
+so the whole step stays on the GPU.  They follow candle-transformers 0.8.4
+``quantized_llama`` (a registry dependency of native/arm_ai_nif/Cargo.lock, not
+vendored in the reference):
+
+* ``forward(x, index_pos)``: embedding; per layer
+  ``h = x + wo(attn(rms_norm(x)))``, ``x = h + w2(silu(w1(n)) * w3(n))`` with
+  ``n = rms_norm(h)``; final ``rms_norm``; the output head on the last position
+  only.
+* attention: q, k, v reshaped to heads, ``rope_i`` (interleaved pairs) with
+  ``theta_i = base^(-2i/head_dim)`` at positions ``index_pos ..``, the new k, v
+  appended to the cache, k, v repeated ``n_head / n_kv_head`` times,
+  ``softmax(q k^T / sqrt(head_dim))`` with the causal mask ``j > i`` when more
+  than one position is fed, ``att v``, heads merged, wo.
+* ``rms_norm(x) = x / sqrt(mean(x^2) + eps) * w``; ``silu(x) = x / (1 + e^-x)``.
+
+The decode step (one token at a given position) can be captured once into a
+HIP graph and replayed per token (``Llama.generate(..., graph=True)``): the
+KV cache and the RoPE tables are preallocated for ``max_seq`` positions and the
+position lives in device memory, so every replay has the same shapes.
+"""
+from __future__ import annotations
+
+import math
+import time
+from dataclasses import dataclass, field
+
+import numpy as np
+
+from . import synth
+from .qmatmul import Context, GgmlDType, QMatMul, QTensor
+
+
+@dataclass
+class LlamaConfig:
+    """Hyper-parameters read from GGUF ``llama.*`` metadata in the reference."""
+
+    n_layer: int = 22
+    hidden: int = 2048
+    ffn: int = 5632
+    n_head: int = 32
+    n_kv_head: int = 4
+    vocab: int = 32000
+    rope_theta: float = 10000.0
+    rms_eps: float = 1e-5
+    max_seq: int = 1024
+
+    @property
+    def head_dim(self) -> int:
+        return self.hidden // self.n_head
+
+
+# TinyLlama-1.1B Q4_K_M tensor types (config 2): Q4_K everywhere except attn_v,
+# ffn_down in every other layer (11 of 22) and the output head, which are Q6_K.
+def tinyllama_q4km_types(cfg: LlamaConfig, layer: int) -> dict[str, int]:
+    return {
+        "wq": synth.TYPE_Q4_K,
+        "wk": synth.TYPE_Q4_K,
+        "wv": synth.TYPE_Q6_K,
+        "wo": synth.TYPE_Q4_K,
+        "w1": synth.TYPE_Q4_K,
+        "w3": synth.TYPE_Q4_K,
+        "w2": synth.TYPE_Q6_K if layer % 2 == 1 else synth.TYPE_Q4_K,
+    }
+
+
+def weight_shapes(cfg: LlamaConfig) -> dict[str, tuple[int, int]]:
+    """(n, k) of each per-layer projection (candle's (out, in))."""
+    hd = cfg.head_dim
+    return {
+        "wq": (cfg.n_head * hd, cfg.hidden),
+        "wk": (cfg.n_kv_head * hd, cfg.hidden),
+        "wv": (cfg.n_kv_head * hd, cfg.hidden),
+        "wo": (cfg.hidden, cfg.n_head * hd),
+        "w1": (cfg.ffn, cfg.hidden),
+        "w3": (cfg.ffn, cfg.hidden),
+        "w2": (cfg.hidden, cfg.ffn),
+    }
+
+
+@dataclass
+class HostWeights:
+    """A model's weights in host memory: GGUF blocks for the projections,
+    f32 for the embedding table and the norm weights."""
+
+    cfg: LlamaConfig
+    layers: list[dict[str, QTensor]] = field(default_factory=list)
+    attn_norm: list[np.ndarray] = field(default_factory=list)
+    ffn_norm: list[np.ndarray] = field(default_factory=list)
+    tok_embeddings: np.ndarray | None = None
+    norm: np.ndarray | None = None
+    output: QTensor | None = None
+
+
+def synthetic_weights(cfg: LlamaConfig, seed: int = 0, types=tinyllama_q4km_types,
+                      output_type: int = synth.TYPE_Q6_K) -> HostWeights:
+    """Random weights of the given architecture (block value distributions of
+    arm_ai_amd.synth; embedding ~ N(0, 1); norm weights ~ 1 + N(0, 0.05))."""
+    rng = np.random.default_rng(seed)
+    hw = HostWeights(cfg)
+    shapes = weight_shapes(cfg)
+    for layer in range(cfg.n_layer):
+        t = types(cfg, layer)
+        qt = {}
+        for name, (n, k) in shapes.items():
+            w = synth.make_weight(t[name], n, k, rng=rng)
+            qt[name] = QTensor(t[name], (n, k), w.blocks)
+        hw.layers.append(qt)
+        hw.attn_norm.append((1.0 + 0.05 * rng.standard_normal(cfg.hidden)).astype(np.float32))
+        hw.ffn_norm.append((1.0 + 0.05 * rng.standard_normal(cfg.hidden)).astype(np.float32))
+    hw.tok_embeddings = rng.standard_normal((cfg.vocab, cfg.hidden), dtype=np.float32)
+    hw.norm = (1.0 + 0.05 * rng.standard_normal(cfg.hidden)).astype(np.float32)
+    w = synth.make_weight(output_type, cfg.vocab, cfg.hidden, rng=rng)
+    hw.output = QTensor(output_type, (cfg.vocab, cfg.hidden), w.blocks)
+    return hw
+
+
+def rope_tables(cfg: LlamaConfig, n_pos: int) -> tuple[np.ndarray, np.ndarray]:
+    """cos, sin [n_pos][head_dim/2] as candle's precompute_freqs_cis (f32)."""
+    hd = cfg.head_dim
+    theta = np.array([1.0 / (cfg.rope_theta ** (i / hd)) for i in range(0, hd, 2)], dtype=np.float32)
+    idx = np.arange(n_pos, dtype=np.float32)[:, None] * theta[None, :]
+    return np.cos(idx).astype(np.float32), np.sin(idx).astype(np.float32)
+
+
+class GenerateResult:
+    def __init__(self, tokens: list[int], prefill_us: int, decode_us: int):
+        self.tokens = tokens
+        self.prefill_us = prefill_us
+        self.decode_us = decode_us
+
+    def stats(self, n_prompt: int) -> dict:
+        """The statistics ArmAI.LlamaCandle.generate reports (llama_candle.ex:92-101)."""
+        n_new = len(self.tokens)
+        return {
+            "n_prompt": n_prompt,
+            "n_new": n_new,
+            "prefill_ms": self.prefill_us / 1000.0,
+            "decode_total_ms": self.decode_us / 1000.0,
+            "decode_ms_per_tok": self.decode_us / 1000.0 / (n_new - 1) if n_new > 1 else None,
+            "prefill_tokens_per_sec": n_prompt * 1.0e6 / max(self.prefill_us, 1),
+        }
+
+
+class Llama:
+    """ModelWeights on one MI355X: quantized projections in HBM (this library),
+    f32 embedding / norms / KV cache as torch tensors on the same device."""
+
+    def __init__(self, ctx: Context, hw: HostWeights):
+        import torch
+
+        self.torch = torch
+        self.ctx = ctx
+        self.cfg = cfg = hw.cfg
+        if cfg.hidden % cfg.n_head or cfg.n_head % cfg.n_kv_head:
+            raise ValueError("hidden must divide into n_head heads and n_head into n_kv_head groups")
+        if not torch.cuda.is_available():
+            raise RuntimeError(
+                "torch sees no GPU: import torch before the first arm_ai_amd call in this process "
+                "(torch loads its own HIP runtime, and a process can use only one)")
+        self.dev = torch.device("cuda", ctx.device)
+        self.stream = torch.cuda.ExternalStream(ctx.stream, device=self.dev)
+        f32 = dict(dtype=torch.float32, device=self.dev)
+        with torch.cuda.stream(self.stream):
+            self.layers = [{name: QMatMul.from_qtensor(qt, ctx) for name, qt in layer.items()} for layer in hw.layers]
+            self.attn_norm = [torch.tensor(w, **f32) for w in hw.attn_norm]
+            self.ffn_norm = [torch.tensor(w, **f32) for w in hw.ffn_norm]
+            self.tok_embeddings = torch.tensor(hw.tok_embeddings, **f32)
+            self.norm = torch.tensor(hw.norm, **f32)
+            self.output = QMatMul.from_qtensor(hw.output, ctx)
+            cos, sin = rope_tables(cfg, cfg.max_seq)
+            self.cos = torch.tensor(cos, **f32)
+            self.sin = torch.tensor(sin, **f32)
+            hd = cfg.head_dim
+            self.k_cache = torch.zeros((cfg.n_layer, cfg.n_kv_head, cfg.max_seq, hd), **f32)
+            self.v_cache = torch.zeros((cfg.n_layer, cfg.n_kv_head, cfg.max_seq, hd), **f32)
+        self.ctx.synchronize()
+        self._graph = None
+
+    # ------------------------------------------------------------ pieces
+    # The work runs on the library's stream; the caller's current stream waits
+    # for it on the way out (and it for the caller's on the way in), so tensors
+    # handed back can be used on the caller's stream directly.
+    def _enter(self):
+        self.stream.wait_stream(self.torch.cuda.current_stream(self.dev))
+
+    def _leave(self):
+        self.torch.cuda.current_stream(self.dev).wait_stream(self.stream)
+
+    def _mm(self, w: QMatMul, x):
+        """QMatMul::forward on device memory: x f32 [m, k] -> f32 [m, n]."""
+        torch = self.torch
+        x = x.contiguous()
+        y = torch.empty((x.shape[0], w.n), dtype=torch.float32, device=self.dev)
+        w.forward_device(x.data_ptr(), x.shape[0], y.data_ptr())
+        return y
+
+    def _rms_norm(self, x, w):
+        torch = self.torch
+        return x * torch.rsqrt(torch.mean(x * x, dim=-1, keepdim=True) + self.cfg.rms_eps) * w
+
+    def _rope(self, x, cos, sin):
+        """rope_i: rotate interleaved pairs (x[2i], x[2i+1]); x [L, H, D], cos/sin [L, D/2]."""
+        L, H, D = x.shape
+        xp = x.reshape(L, H, D // 2, 2)
+        x0, x1 = xp[..., 0], xp[..., 1]
+        c, s = cos[:, None, :], sin[:, None, :]
+        return self.torch.stack((x0 * c - x1 * s, x0 * s + x1 * c), dim=-1).reshape(L, H, D)
+
+    def _attend(self, q, k, v, mask):
+        """q [H, Lq, D], k/v [Hkv, Lk, D]; mask [Lq, Lk] bool (True = masked) or None."""
+        torch = self.torch
+        cfg = self.cfg
+        rep = cfg.n_head // cfg.n_kv_head
+        k = k.repeat_interleave(rep, dim=0)
+        v = v.repeat_interleave(rep, dim=0)
+        att = torch.matmul(q, k.transpose(1, 2).contiguous()) / math.sqrt(cfg.head_dim)
+        if mask is not None:
+            att = att.masked_fill(mask, float("-inf"))
+        att = torch.softmax(att, dim=-1)
+        return torch.matmul(att, v.contiguous())
+
+    def _layer_tail(self, i, x, y):
+        """wo, residual, FFN and its residual for layer i; y = attention output [L, H*D]."""
+        lw = self.layers[i]
+        h = x + self._mm(lw["wo"], y)
+        n = self._rms_norm(h, self.ffn_norm[i])
+        g = self._mm(lw["w1"], n)
+        u = self._mm(lw["w3"], n)
+        return h + self._mm(lw["w2"], self.torch.nn.functional.silu(g) * u)
+
+    # ------------------------------------------------------------ forward
+    def forward(self, tokens, index_pos: int):
+        """ModelWeights::forward(&x[1, L], index_pos) -> logits f32 [vocab] of the last position.
+
+        tokens: a torch int64 tensor [L] on the device, or a sequence of ints."""
+        torch = self.torch
+        cfg = self.cfg
+        self._enter()
+        with torch.cuda.stream(self.stream):
+            if not torch.is_tensor(tokens):
+                tokens = torch.tensor(list(tokens), dtype=torch.int64, device=self.dev)
+            L = int(tokens.shape[0])
+            if L == 0 or index_pos + L > cfg.max_seq:
+                raise ValueError(f"positions {index_pos}..{index_pos + L} outside 0..{cfg.max_seq}")
+            H, Hkv, D = cfg.n_head, cfg.n_kv_head, cfg.head_dim
+            cos = self.cos[index_pos:index_pos + L]
+            sin = self.sin[index_pos:index_pos + L]
+            end = index_pos + L
+            mask = None
+            if L > 1:  # candle builds the causal mask whenever more than one position is fed
+                i = torch.arange(L, device=self.dev)[:, None]
+                j = torch.arange(end, device=self.dev)[None, :]
+                mask = j > (i + index_pos)
+            x = self.tok_embeddings[tokens]
+            for li, lw in enumerate(self.layers):
+                n = self._rms_norm(x, self.attn_norm[li])
+                q = self._rope(self._mm(lw["wq"], n).view(L, H, D), cos, sin)
+                k = self._rope(self._mm(lw["wk"], n).view(L, Hkv, D), cos, sin)
+                v = self._mm(lw["wv"], n).view(L, Hkv, D)
+                self.k_cache[li, :, index_pos:end] = k.transpose(0, 1)
+                self.v_cache[li, :, index_pos:end] = v.transpose(0, 1)
+                y = self._attend(q.transpose(0, 1), self.k_cache[li, :, :end], self.v_cache[li, :, :end], mask)
+                x = self._layer_tail(li, x, y.transpose(0, 1).reshape(L, H * D))
+            last = self._rms_norm(x[L - 1:L], self.norm)
+            logits = self._mm(self.output, last)[0]
+        self._leave()
+        return logits
+
+    # ------------------------------------------------------------ graph-captured decode step
+    def _decode_step_static(self):
+        """One decode step at the position in self._pos (device), token in self._tok.
+        All shapes are fixed (attention over max_seq with a position mask)."""
+        torch = self.torch
+        cfg = self.cfg
+        H, Hkv, D = cfg.n_head, cfg.n_kv_head, cfg.head_dim
+        pos = self._pos
+        cos = self.cos.index_select(0, pos)
+        sin = self.sin.index_select(0, pos)
+        mask = (self._ar > pos)[None, :]  # [1, max_seq]: positions after pos are masked
+        x = self.tok_embeddings.index_select(0, self._tok)
+        for li, lw in enumerate(self.layers):
+            n = self._rms_norm(x, self.attn_norm[li])
+            q = self._rope(self._mm(lw["wq"], n).view(1, H, D), cos, sin)
+            k = self._rope(self._mm(lw["wk"], n).view(1, Hkv, D), cos, sin)
+            v = self._mm(lw["wv"], n).view(1, Hkv, D)
+            self.k_cache[li].index_copy_(1, pos, k.transpose(0, 1))
+            self.v_cache[li].index_copy_(1, pos, v.transpose(0, 1))
+            y = self._attend(q.transpose(0, 1), self.k_cache[li], self.v_cache[li], mask)
+            x = self._layer_tail(li, x, y.transpose(0, 1).reshape(1, H * D))
+        logits = self._mm(self.output, self._rms_norm(x, self.norm))[0]
+        self._next.copy_(torch.argmax(logits).view(1))
+        self._logits.copy_(logits)
+
+    def _capture(self):
+        torch = self.torch
+        self._enter()
+        with torch.cuda.stream(self.stream):
+            self._pos = torch.zeros(1, dtype=torch.int64, device=self.dev)
+            self._tok = torch.zeros(1, dtype=torch.int64, device=self.dev)
+            self._next = torch.zeros(1, dtype=torch.int64, device=self.dev)
+            self._logits = torch.zeros(self.cfg.vocab, dtype=torch.float32, device=self.dev)
+            self._ar = torch.arange(self.cfg.max_seq, device=self.dev)
+        # Warm up on the capture stream (library first-call set-up, torch
+        # kernels) at the last cache slot: a step writes its own position's k, v
+        # before attending and masks later positions, so that slot is never read
+        # stale, and the cache entries of a sequence in progress stay intact.
+        with torch.cuda.stream(self.stream):
+            self._pos.fill_(self.cfg.max_seq - 1)
+            self._decode_step_static()
+        self.ctx.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=self.stream):
+            self._decode_step_static()
+        self._graph = g
+        self._leave()
+
+    def decode_step_graph(self, token: int, pos: int):
+        """Replay the captured decode step for `token` at position `pos`; returns the device logits."""
+        if self._graph is None:
+            self._capture()
+        if pos >= self.cfg.max_seq:
+            raise ValueError(f"position {pos} outside 0..{self.cfg.max_seq}")
+        self._enter()
+        with self.torch.cuda.stream(self.stream):
+            self._pos.fill_(pos)
+            self._tok.fill_(token)
+            self._graph.replay()
+        self._leave()
+        return self._logits
+
+    # ------------------------------------------------------------ generate
+    @staticmethod
+    def argmax_first(logits) -> int:
+        """First index of the maximum (llama_candle.rs:154-176 folds with a strict >)."""
+        return int(logits.argmax().item())
+
+    def generate(self, prompt: list[int], max_new: int, stop_tokens=(), graph: bool = False) -> GenerateResult:
+        """generate_greedy (llama_candle.rs:58-139): prefill at offset 0, then one
+        forward per new token; stops after emitting a stop token (kept in the output)."""
+        if max_new == 0 or len(prompt) == 0:
+            return GenerateResult([], 0, 0)
+        if len(prompt) + max_new - 1 > self.cfg.max_seq:
+            raise ValueError("prompt + max_new exceeds max_seq")
+        torch = self.torch
+        if graph and self._graph is None:
+            self._capture()
+        self.ctx.synchronize()
+        t0 = time.perf_counter()
+        logits = self.forward(prompt, 0)
+        nxt = self.argmax_first(logits)  # .item() synchronises
+        prefill_us = int((time.perf_counter() - t0) * 1e6)
+        generated = [nxt]
+        t1 = time.perf_counter()
+        offset = len(prompt)
+        for _ in range(1, max_new):
+            if nxt in stop_tokens:
+                break
+            if graph:
+                self.decode_step_graph(nxt, offset)
+                nxt = int(self._next.item())
+            else:
+                nxt = self.argmax_first(self.forward([nxt], offset))
+            generated.append(nxt)
+            offset += 1
+        decode_us = int((time.perf_counter() - t1) * 1e6)
+        return GenerateResult(generated, prefill_us, decode_us)
+
+    def free(self) -> None:
+        for lw in self.layers:
+            for w in lw.values():
+                w.free()
+        self.output.free()

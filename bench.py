@@ -208,6 +208,9 @@ MATVEC_CASES = {  # name: (weight type, n, k, m, seed)
     "c4_q4k_14336x4096_b8": (12, 14336, 4096, 8, 6),
     "c4_q6k_128256x4096_b1": (14, 128256, 4096, 1, 7),
 }
+DECODE_CASES = {  # name: (prompt tokens, new tokens, seed)
+    "c2_tinyllama_decode": (512, 128, 2),
+}
 PREFILL_CASES = {  # name: (n, k, m, seed), Q4_K weight
     "c3_prefill_q4k_5632x2048_m512": (5632, 2048, 512, 3),
     "c3_prefill_q4k_2048x5632_m512": (2048, 5632, 512, 3),
@@ -215,7 +218,64 @@ PREFILL_CASES = {  # name: (n, k, m, seed), Q4_K weight
 }
 
 
+def measure_decode(ctx, n_prompt, n_new, seed):
+    """Config 2: TinyLlama-1.1B-shaped Q4_K_M model with random weights, a prompt
+    of uniform-random ids, greedy decode with the decode step replayed from a HIP
+    graph; statistics as ArmAI.LlamaCandle.generate reports them."""
+    from arm_ai_amd.llama import Llama, LlamaConfig, synthetic_weights
+
+    cfg = LlamaConfig(max_seq=n_prompt + n_new)
+    t0 = time.perf_counter()
+    hw = synthetic_weights(cfg, seed)
+    wbytes = sum(qt.data.size for layer in hw.layers for qt in layer.values()) + hw.output.data.size
+    model = Llama(ctx, hw)
+    del hw
+    log(f"c2 model ready in {time.perf_counter() - t0:.1f} s")
+    rng = np.random.default_rng(seed)
+    prompt = rng.integers(0, cfg.vocab, size=n_prompt).tolist()
+    model.generate(prompt[:16], 4, graph=True)  # capture the step, first-call set-up
+    res = model.generate(prompt, n_new, graph=True)
+    st = res.stats(n_prompt)
+    eager = model.generate(prompt, 16)
+    est = eager.stats(n_prompt)
+    model.free()
+    out = {
+        "model": "TinyLlama-1.1B shape (22 layers, hidden 2048, FFN 5632, 32/4 heads, vocab 32000), Q4_K_M types, random weights",
+        "n_prompt": n_prompt,
+        "n_new": st["n_new"],
+        "decode_tok_s": round(1e3 / st["decode_ms_per_tok"], 1),
+        "decode_ms_per_tok": round(st["decode_ms_per_tok"], 4),
+        "prefill_ms": round(st["prefill_ms"], 3),
+        "prefill_tok_s": round(st["prefill_tokens_per_sec"], 1),
+        "eager_decode_tok_s": round(1e3 / est["decode_ms_per_tok"], 1),
+        "matmul_weight_bytes_per_token": int(wbytes),
+        "weight_GBps_at_decode": round(wbytes / (st["decode_ms_per_tok"] / 1e3) / 1e9, 1),
+        "graph_and_eager_tokens_agree": res.tokens[:16] == eager.tokens,
+        "timing": "wall clock around generate (llama_candle.rs:80-139 points); decode step replayed from a HIP graph",
+    }
+    return out
+
+
+def run_decode_child(name):
+    """Run a decode case in a child process: the driver's torch glue needs torch
+    imported before this library is loaded (one HIP runtime per process)."""
+    import subprocess
+
+    r = subprocess.run([sys.executable, "-u", os.path.abspath(__file__), "--case", name],
+                       stdout=subprocess.PIPE, text=True, cwd=ROOT)
+    if r.returncode != 0:
+        raise RuntimeError(f"{name} failed in its child process (exit {r.returncode})")
+    out = json.loads(r.stdout.strip().splitlines()[-1])
+    out.pop("case", None)
+    return out
+
+
 def run_case(ctx, name, steps, warmup):
+    if name in DECODE_CASES:
+        n_prompt, n_new, seed = DECODE_CASES[name]
+        out = measure_decode(ctx, n_prompt, n_new, seed)
+        log(f"{name}: decode {out['decode_tok_s']} tok/s ({out['decode_ms_per_tok']} ms/tok; eager {out['eager_decode_tok_s']} tok/s), prefill {out['prefill_ms']} ms ({out['prefill_tok_s']} tok/s)")
+        return out
     if name in MATVEC_CASES:
         wt, n_, k_, m_, seed = MATVEC_CASES[name]
         w2, *_, out = measure(ctx, wt, n_, k_, m_, min(steps, 100), min(warmup, 10), seed)
@@ -247,6 +307,9 @@ def main() -> int:
         print("--steps must be >= 1", file=sys.stderr)
         return 2
 
+    if args.case in DECODE_CASES:
+        import torch  # noqa: F401  (before the library: one HIP runtime per process)
+
     import arm_ai_amd as A
 
     if args.copy_calibration:
@@ -260,8 +323,9 @@ def main() -> int:
         print(json.dumps({"copy_calibration_bytes": nbytes, "copies": 10}), flush=True)
         return 0
 
-    if args.case is not None and args.case not in MATVEC_CASES and args.case not in PREFILL_CASES:
-        print(f"unknown case {args.case!r}; cases: {', '.join(list(MATVEC_CASES) + list(PREFILL_CASES))}", file=sys.stderr)
+    all_cases = list(MATVEC_CASES) + list(PREFILL_CASES) + list(DECODE_CASES)
+    if args.case is not None and args.case not in all_cases:
+        print(f"unknown case {args.case!r}; cases: {', '.join(all_cases)}", file=sys.stderr)
         return 2
 
     ctx = A.Context(0)
@@ -322,6 +386,8 @@ def main() -> int:
             extra[name] = run_case(ctx, name, args.steps, args.warmup)
         for name in PREFILL_CASES:
             extra[name] = run_case(ctx, name, args.steps, args.warmup)
+        for name in DECODE_CASES:
+            extra[name] = run_decode_child(name)
         result["extra"] = extra
     else:
         result["extra"] = {}

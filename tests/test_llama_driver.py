@@ -1,0 +1,148 @@
+"""The quantized matmuls' call sites (a Llama decoder driven like ArmAI.LlamaCandle).
+
+GPU tests: the driver (arm_ai_amd.llama, quantized projections on the GPU
+through the C ABI) against tests/_llama_ref.py (numpy glue + the oracle's
+k_quants::matmul) on a small model, teacher-forced: prefill logits, decode
+logits, the graph-captured decode step against the eager one, and greedy
+generation.  Tolerance: the activation quantisation is bit-exact, but the f32
+glue (torch on the GPU vs numpy) rounds differently and a Q8_K block whose
+input moved by one ulp can round a quant the other way, so logits are
+compared at 2e-3 of their largest magnitude.
+
+CPU test: the reference restatement's rope_i pairing against its closed form.
+"""
+import numpy as np
+import pytest
+
+from tests._llama_ref import RefLlama
+
+LOGIT_TOL = 2e-3
+
+
+def _tiny_cfg():
+    from arm_ai_amd.llama import LlamaConfig
+
+    return LlamaConfig(n_layer=2, hidden=256, ffn=512, n_head=4, n_kv_head=2, vocab=512, max_seq=64)
+
+
+def _rel(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.max(np.abs(a - b)) / max(np.max(np.abs(b)), 1e-30))
+
+
+# ---------------------------------------------------------------- CPU
+def test_ref_rope_closed_form():
+    from arm_ai_amd.llama import synthetic_weights
+
+    cfg = _tiny_cfg()
+    hw = synthetic_weights(cfg, seed=1)
+    ref = RefLlama(hw)
+    hd = cfg.hidden // cfg.n_head
+    # position 0 is the identity; a pair (1, 0) at position p becomes (cos, sin)(p * theta_i)
+    x = np.zeros((3, 1, hd), np.float32)
+    x[:, 0, 0::2] = 1.0
+    out = ref.rope(x, 5)
+    for L in range(3):
+        for i in range(hd // 2):
+            ang = (5 + L) * (cfg.rope_theta ** (-2.0 * i / hd))
+            assert abs(out[L, 0, 2 * i] - np.cos(ang)) < 2e-5
+            assert abs(out[L, 0, 2 * i + 1] - np.sin(ang)) < 2e-5
+    assert np.array_equal(ref.rope(x, 0)[0], x[0])
+
+
+# ---------------------------------------------------------------- GPU
+@pytest.fixture(scope="module")
+def tiny():
+    import torch
+
+    import arm_ai_amd as A
+
+    if not torch.cuda.is_available():
+        if A.device_count() > 0:
+            pytest.fail("the library sees a GPU but torch does not (torch must be imported first)")
+        pytest.skip("no GPU")
+    from arm_ai_amd.llama import Llama, synthetic_weights
+
+    cfg = _tiny_cfg()
+    hw = synthetic_weights(cfg, seed=3)
+    ctx = A.Context(0)
+    model = Llama(ctx, hw)
+    yield hw, model
+    model.free()
+    ctx.close()
+
+
+@pytest.mark.gpu
+def test_prefill_and_decode_logits_match_reference(tiny):
+    hw, model = tiny
+    ref = RefLlama(hw)
+    rng = np.random.default_rng(5)
+    prompt = rng.integers(0, hw.cfg.vocab, size=7).tolist()
+    g = model.forward(prompt, 0).cpu().numpy()
+    r = ref.forward(prompt, 0)
+    assert np.all(np.isfinite(g))
+    assert _rel(g, r) <= LOGIT_TOL, f"prefill logits rel {_rel(g, r):.3e}"
+    pos = len(prompt)
+    for step in range(3):  # teacher-forced: both sides see the same tokens
+        tok = int(rng.integers(0, hw.cfg.vocab))
+        g = model.forward([tok], pos).cpu().numpy()
+        r = ref.forward([tok], pos)
+        assert _rel(g, r) <= LOGIT_TOL, f"decode step {step} logits rel {_rel(g, r):.3e}"
+        pos += 1
+
+
+@pytest.mark.gpu
+def test_graph_decode_step_matches_eager(tiny):
+    hw, model = tiny
+    prompt = [1, 2, 3, 4, 5]
+    model.forward(prompt, 0)
+    eager = model.forward([9], 5).cpu().numpy()
+    model.forward(prompt, 0)  # same cache contents again
+    first = None
+    for rep in range(3):  # replays with eager work in between, each checked
+        graph = model.decode_step_graph(9, 5).cpu().numpy()
+        # the static step attends over max_seq positions (masked), so its f32
+        # sums may round differently from the eager step's, not from each other
+        assert _rel(graph, eager) <= LOGIT_TOL, f"replay {rep}: rel {_rel(graph, eager):.3e}"
+        if first is None:
+            first = graph
+        assert np.array_equal(graph, first), f"replay {rep} differs from the first replay"
+        model.forward(prompt, 0)
+
+
+@pytest.mark.gpu
+def test_generate_greedy_eager_and_graph_agree(tiny):
+    hw, model = tiny
+    ref = RefLlama(hw)
+    prompt = [7, 100, 33, 250, 3, 9]
+    a = model.generate(prompt, 6)
+    b = model.generate(prompt, 6, graph=True)
+    assert len(a.tokens) == 6
+    assert a.tokens == b.tokens
+    # the reference's greedy choice at each step, fed the GPU's tokens
+    toks = list(prompt)
+    logits = ref.forward(toks, 0)
+    margin_ok = []
+    for t in a.tokens:
+        top2 = np.sort(logits)[-2:]
+        if top2[1] - top2[0] > 1e-2 * np.max(np.abs(logits)):
+            assert t == int(np.argmax(logits))
+            margin_ok.append(True)
+        logits = ref.forward([t], len(toks))
+        toks.append(t)
+    assert margin_ok, "no step had a clear argmax"
+    st = a.stats(len(prompt))
+    assert st["n_new"] == 6 and st["n_prompt"] == len(prompt) and st["decode_ms_per_tok"] is not None
+
+
+@pytest.mark.gpu
+def test_generate_stops_after_stop_token_and_edge_cases(tiny):
+    hw, model = tiny
+    prompt = [11, 12, 13]
+    first = model.generate(prompt, 1).tokens
+    assert len(first) == 1
+    r = model.generate(prompt, 5, stop_tokens=(first[0],))
+    assert r.tokens == first  # the stop token is emitted, then generation ends
+    assert model.generate([], 5).tokens == []
+    assert model.generate(prompt, 0).tokens == []
