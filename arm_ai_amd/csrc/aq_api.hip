@@ -30,7 +30,6 @@ struct aq_ctx {
     size_t scratch_bytes = 0;
     void *pinned = nullptr;  // host staging, grow-only
     size_t pinned_bytes = 0;
-    int *counters = nullptr;  // GEMM split-K tile counters: zeroed once, left zero by every GEMM launch
 };
 
 struct aq_qweight {
@@ -170,7 +169,7 @@ int run_matmul(aq_ctx *ctx, const aq_qweight *w, const float *d_x, int64_t m, fl
         e = w->type == AQ_TYPE_Q8_0 ? launch_quantize_q8_0(d_x, m, w->k, a, ctx->stream)
                                     : launch_quantize_q8k(d_x, m, w->k, a, ctx->stream);
         if (e != hipSuccess) return fail(AQ_ERR_HIP, "activation quantizer: %s", hipGetErrorString(e));
-        e = launch_gemm(w->layout, w->n, w->k, a, m, d_y, dS, dSmin, ws, ws_bytes, ctx->counters, ctx->stream);
+        e = launch_gemm(w->layout, w->n, w->k, a, m, d_y, dS, dSmin, ws, ws_bytes, ctx->stream);
         if (e == hipSuccess) return AQ_OK;
         if (e != hipErrorNotSupported) return fail(AQ_ERR_HIP, "gemm: %s", hipGetErrorString(e));
         e = launch_matvec(w->layout, w->n, w->k, nullptr, &a, m, d_y, dS, dSmin, ctx->stream);
@@ -225,14 +224,6 @@ int aq_ctx_create(int device, aq_ctx **out) {
         delete c;
         return fail(AQ_ERR_HIP, "hipStreamCreateWithFlags failed");
     }
-    if (hipMalloc(&c->counters, sizeof(int) * GEMM_MAX_TILES) != hipSuccess ||
-        hipMemset(c->counters, 0, sizeof(int) * GEMM_MAX_TILES) != hipSuccess) {
-        (void)hipGetLastError();
-        if (c->counters) (void)hipFree(c->counters);
-        (void)hipStreamDestroy(c->stream);
-        delete c;
-        return fail(AQ_ERR_OOM, "allocating the GEMM tile counters failed");
-    }
     *out = c;
     return AQ_OK;
 }
@@ -243,7 +234,6 @@ int aq_ctx_destroy(aq_ctx *c) {
     if (c->stream) (void)hipStreamSynchronize(c->stream);
     if (c->scratch) (void)hipFree(c->scratch);
     if (c->pinned) (void)hipHostFree(c->pinned);
-    if (c->counters) (void)hipFree(c->counters);
     if (c->stream) (void)hipStreamDestroy(c->stream);
     delete c;
     return AQ_OK;
@@ -449,7 +439,7 @@ int aq_qmatmul_preq_device(aq_ctx *ctx, const aq_qweight *w, const void *d_act, 
         CallLayout L = call_layout(w, m, false, false, true);
         if ((rc = ensure_scratch(ctx, L.total))) return rc;
         e = launch_gemm(w->layout, w->n, w->k, a, m, d_dst, nullptr, nullptr, (uint8_t *)ctx->scratch + L.ws,
-                        L.total - L.ws, ctx->counters, ctx->stream);
+                        L.total - L.ws, ctx->stream);
         if (e != hipSuccess && e != hipErrorNotSupported) return fail(AQ_ERR_HIP, "gemm: %s", hipGetErrorString(e));
     }
     if (e == hipErrorNotSupported) e = launch_matvec(w->layout, w->n, w->k, nullptr, &a, m, d_dst, nullptr, nullptr, ctx->stream);

@@ -120,11 +120,10 @@ hipError_t launch_matvec(const WLayout &w, int64_t n, int64_t k, const float *x,
                          float *y, int32_t *S, int32_t *Smin, hipStream_t s);
 // Prefill GEMM on MFMA (m > 8).  Returns hipErrorNotSupported for shapes it
 // does not take; the caller then uses launch_matvec.  ws: gemm_workspace_bytes
-// of scratch (split-K partials); counters: GEMM_MAX_TILES ints that are zero
-// before the launch and are zero again after it.
-constexpr int GEMM_MAX_TILES = 1 << 16;
+// of scratch (split-K partials, summed by a second launch on the stream).
+constexpr int GEMM_MAX_TILES = 1 << 20;
 hipError_t launch_gemm(const WLayout &w, int64_t n, int64_t k, const ActPlanes &x, int64_t m, float *y, int32_t *S,
-                       int32_t *Smin, void *ws, size_t ws_bytes, int *counters, hipStream_t s);
+                       int32_t *Smin, void *ws, size_t ws_bytes, hipStream_t s);
 // Workspace bytes launch_gemm needs for this shape, or (size_t)-1 if the
 // weight type / shape has no GEMM (the matvec then serves m > 8 too).
 size_t gemm_workspace_bytes(int type, int64_t m, int64_t n, int64_t k);
