@@ -56,6 +56,26 @@ SIGNATURES = {
     "aq_quantize_q8k": (INT, [P, P, I64, I64, P]),
     "aq_quantize_q8_0": (INT, [P, P, I64, I64, P]),
     "aq_qmatmul_block_sums": (INT, [P, P, P, I64, I64, P, P]),
+    # crate kernels (shape_ops.rs)
+    "aq_int8_matmul_f32": (INT, [P, P, P, P, ctypes.c_float, I64, I64, I64, P]),
+    "aq_int8_matmul_f32_per_token": (INT, [P, P, P, P, P, I64, I64, I64, P]),
+    "aq_int8_matmul_f32_device": (INT, [P, P, P, P, ctypes.c_float, P, I64, I64, I64, P]),
+    "aq_quantize_int8_per_token": (INT, [P, P, I64, I64, P, P]),
+    "aq_quantize_int8_per_token_device": (INT, [P, P, I64, I64, P, P]),
+    "aq_dequant_matmul_int8_f32": (INT, [P, P, P, P, I64, I64, I64, I64, P]),
+    "aq_dequant_matmul_f16_f32": (INT, [P, P, P, I64, I64, I64, I64, P]),
+    "aq_int4_matmul_f32": (INT, [P, P, P, P, I64, I64, I64, P]),
+    "aq_int4_matmul_gemv": (INT, [P, P, P, P, I64, I64, P]),
+    "aq_weight_only_matmul_device": (INT, [P, INT, P, P, P, I64, I64, I64, P]),
+    "aq_int4_matmul_gemv_q4_x_q8": (INT, [P, P, P, P, I64, I64, P]),
+    "aq_q4_x_q8_act_bytes": (SZ, [I64]),
+    "aq_int4_matmul_gemv_q4_x_q8_device": (INT, [P, P, P, P, I64, I64, P, P, P, P]),
+    "aq_quantize_int4_q4_0": (INT, [P, P, I64, I64, P, P]),
+    "aq_dequantize_q6_k": (INT, [P, P, SZ, I64, P]),
+    "aq_dequantize_q6_k_device": (INT, [P, P, I64, P]),
+    "aq_q4_0_dequant_row": (INT, [P, P, P, I64, I64, I64, P]),
+    "aq_q8_0_dequant_row": (INT, [P, P, P, I64, I64, I64, P]),
+    "aq_dequant_rows_device": (INT, [P, INT, P, P, I64, P, I64, I64, P]),
 }
 
 

@@ -531,3 +531,291 @@ int aq_qmatmul_block_sums(aq_ctx *ctx, const aq_qweight *w, const float *lhs, in
 }
 
 }  // extern "C"
+
+// ===========================================================================
+// The NIF crate's own int8 / int4 kernels (shape_ops.rs; include/aq.h,
+// "crate kernels").  Each host-buffer entry copies its inputs into the
+// context's device scratch, runs the kernel on the context's stream and
+// copies the outputs back before returning; each _device entry takes device
+// pointers and returns with the work queued on the stream.
+// ===========================================================================
+namespace {
+
+struct ScratchPlan {
+    size_t total = 0;
+    size_t add(size_t bytes) {
+        const size_t o = total;
+        total += align_up(bytes ? bytes : 1, 256);
+        return o;
+    }
+};
+
+bool mul_ok(int64_t a, int64_t b, int64_t lim = ((int64_t)1 << 40)) { return a >= 0 && b >= 0 && (b == 0 || a <= lim / b); }
+
+int crate_prologue(aq_ctx *ctx, int64_t m, int64_t n, int64_t k) {
+    if (!ctx) return fail(AQ_ERR_INVALID_ARG, "null context");
+    if (m < 0 || n <= 0 || k <= 0 || m > 0x7fffffff || n > 0x7fffffff || !mul_ok(m, k) || !mul_ok(n, k) || !mul_ok(m, n))
+        return fail(AQ_ERR_SHAPE, "bad shape (m=%lld, n=%lld, k=%lld)", (long long)m, (long long)n, (long long)k);
+    return use_device(ctx->device);
+}
+
+int hip_status(hipError_t e, const char *what) {
+    if (e == hipSuccess) return AQ_OK;
+    if (e == hipErrorInvalidValue) return fail(AQ_ERR_SHAPE, "%s: invalid shape or argument", what);
+    return fail(AQ_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+int h2d(aq_ctx *c, void *dst, const void *src, size_t bytes) {
+    if (bytes) HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, c->stream));
+    return AQ_OK;
+}
+
+int d2h_sync(aq_ctx *c, void *dst, const void *src, size_t bytes) {
+    if (bytes) HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, c->stream));
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    return AQ_OK;
+}
+
+int int8_matmul_host(aq_ctx *ctx, const int8_t *a, const int8_t *w, const float *act_scales, float act_scale,
+                     const float *w_scales, int64_t m, int64_t n, int64_t k, float *out) {
+    int rc = crate_prologue(ctx, m, n, k);
+    if (rc) return rc;
+    if (m == 0) return AQ_OK;
+    if (!a || !w || !w_scales || !out) return fail(AQ_ERR_INVALID_ARG, "null argument");
+    ScratchPlan P;
+    const size_t oa = P.add(m * k), ow = P.add(n * k), osa = P.add(act_scales ? m * 4 : 0), osw = P.add(n * 4),
+                 oo = P.add(m * n * 4);
+    if ((rc = ensure_scratch(ctx, P.total))) return rc;
+    uint8_t *S = (uint8_t *)ctx->scratch;
+    if ((rc = h2d(ctx, S + oa, a, m * k)) || (rc = h2d(ctx, S + ow, w, n * k)) ||
+        (rc = h2d(ctx, S + osw, w_scales, n * 4)) || (act_scales && (rc = h2d(ctx, S + osa, act_scales, m * 4))))
+        return rc;
+    if ((rc = hip_status(launch_int8_matmul((int8_t *)(S + oa), (int8_t *)(S + ow), act_scales ? (float *)(S + osa) : nullptr,
+                                            act_scale, (float *)(S + osw), m, n, k, (float *)(S + oo), ctx->stream),
+                         "int8 matmul")))
+        return rc;
+    return d2h_sync(ctx, out, S + oo, m * n * 4);
+}
+
+int weight_only_host(aq_ctx *ctx, int wt, const float *act, const void *w, size_t w_bytes, const float *scales,
+                     size_t s_bytes, int64_t m, int64_t n, int64_t k, float *out) {
+    int rc = crate_prologue(ctx, m, n, k);
+    if (rc) return rc;
+    if (m == 0) return AQ_OK;
+    if (!act || !w || !out || (s_bytes && !scales)) return fail(AQ_ERR_INVALID_ARG, "null argument");
+    ScratchPlan P;
+    const size_t oa = P.add(m * k * 4), ow = P.add(w_bytes), os = P.add(s_bytes), oo = P.add(m * n * 4);
+    if ((rc = ensure_scratch(ctx, P.total))) return rc;
+    uint8_t *S = (uint8_t *)ctx->scratch;
+    if ((rc = h2d(ctx, S + oa, act, m * k * 4)) || (rc = h2d(ctx, S + ow, w, w_bytes)) ||
+        (rc = h2d(ctx, S + os, scales, s_bytes)))
+        return rc;
+    if ((rc = hip_status(launch_weight_only_matmul(wt, (float *)(S + oa), S + ow, s_bytes ? (float *)(S + os) : nullptr,
+                                                   m, n, k, (float *)(S + oo), ctx->stream),
+                         "weight-only matmul")))
+        return rc;
+    return d2h_sync(ctx, out, S + oo, m * n * 4);
+}
+
+}  // namespace
+
+int aq_int8_matmul_f32(aq_ctx *ctx, const int8_t *a, const int8_t *w, const float *w_scales, float act_scale, int64_t m,
+                       int64_t n, int64_t k, float *out) {
+    return int8_matmul_host(ctx, a, w, nullptr, act_scale, w_scales, m, n, k, out);
+}
+
+int aq_int8_matmul_f32_per_token(aq_ctx *ctx, const int8_t *a, const int8_t *w, const float *act_scales,
+                                 const float *w_scales, int64_t m, int64_t n, int64_t k, float *out) {
+    if (m > 0 && !act_scales) return fail(AQ_ERR_INVALID_ARG, "null act_scales");
+    return int8_matmul_host(ctx, a, w, act_scales, 0.0f, w_scales, m, n, k, out);
+}
+
+int aq_int8_matmul_f32_device(aq_ctx *ctx, const int8_t *d_a, const int8_t *d_w, const float *d_act_scales,
+                              float act_scale, const float *d_w_scales, int64_t m, int64_t n, int64_t k, float *d_out) {
+    int rc = crate_prologue(ctx, m, n, k);
+    if (rc) return rc;
+    return hip_status(launch_int8_matmul(d_a, d_w, d_act_scales, act_scale, d_w_scales, m, n, k, d_out, ctx->stream),
+                      "int8 matmul");
+}
+
+int aq_quantize_int8_per_token(aq_ctx *ctx, const float *a, int64_t m, int64_t k, int8_t *q, float *scales) {
+    int rc = crate_prologue(ctx, m, 1, k);
+    if (rc) return rc;
+    if (m == 0) return AQ_OK;
+    if (!a || !q || !scales) return fail(AQ_ERR_INVALID_ARG, "null argument");
+    ScratchPlan P;
+    const size_t oa = P.add(m * k * 4), oq = P.add(m * k), os = P.add(m * 4);
+    if ((rc = ensure_scratch(ctx, P.total))) return rc;
+    uint8_t *S = (uint8_t *)ctx->scratch;
+    if ((rc = h2d(ctx, S + oa, a, m * k * 4))) return rc;
+    if ((rc = hip_status(launch_quantize_int8_per_token((float *)(S + oa), m, k, (int8_t *)(S + oq), (float *)(S + os),
+                                                        ctx->stream),
+                         "quantize_int8_per_token")))
+        return rc;
+    HIP_TRY(hipMemcpyAsync(q, S + oq, m * k, hipMemcpyDeviceToHost, ctx->stream));
+    return d2h_sync(ctx, scales, S + os, m * 4);
+}
+
+int aq_quantize_int8_per_token_device(aq_ctx *ctx, const float *d_a, int64_t m, int64_t k, int8_t *d_q, float *d_scales) {
+    int rc = crate_prologue(ctx, m, 1, k);
+    if (rc) return rc;
+    return hip_status(launch_quantize_int8_per_token(d_a, m, k, d_q, d_scales, ctx->stream), "quantize_int8_per_token");
+}
+
+int aq_dequant_matmul_int8_f32(aq_ctx *ctx, const float *act, const int8_t *w, const float *scales, int64_t b, int64_t m,
+                               int64_t n, int64_t k, float *out) {
+    if (b < 0 || !mul_ok(b, m)) return fail(AQ_ERR_SHAPE, "bad batch");
+    return weight_only_host(ctx, CRATE_W_I8, act, w, (size_t)(n * k), scales, (size_t)n * 4, b * m, n, k, out);
+}
+
+int aq_dequant_matmul_f16_f32(aq_ctx *ctx, const float *act, const uint16_t *w, int64_t b, int64_t m, int64_t n,
+                              int64_t k, float *out) {
+    if (b < 0 || !mul_ok(b, m)) return fail(AQ_ERR_SHAPE, "bad batch");
+    return weight_only_host(ctx, CRATE_W_F16, act, w, (size_t)(n * k) * 2, nullptr, 0, b * m, n, k, out);
+}
+
+int aq_int4_matmul_f32(aq_ctx *ctx, const float *a, const uint8_t *w_packed, const float *w_scales, int64_t m, int64_t n,
+                       int64_t k, float *out) {
+    if (k <= 0 || k % 32) return fail(AQ_ERR_SHAPE, "int4_matmul: K=%lld must be a multiple of 32", (long long)k);
+    return weight_only_host(ctx, CRATE_W_Q4_0, a, w_packed, (size_t)(n * (k / 2)), w_scales, (size_t)(n * (k / 32)) * 4, m,
+                            n, k, out);
+}
+
+int aq_int4_matmul_gemv(aq_ctx *ctx, const float *a, const uint8_t *w_packed, const float *w_scales, int64_t n, int64_t k,
+                        float *out) {
+    return aq_int4_matmul_f32(ctx, a, w_packed, w_scales, 1, n, k, out);
+}
+
+int aq_weight_only_matmul_device(aq_ctx *ctx, int weight_format, const float *d_act, const void *d_w,
+                                 const float *d_scales, int64_t m, int64_t n, int64_t k, float *d_out) {
+    int rc = crate_prologue(ctx, m, n, k);
+    if (rc) return rc;
+    if (weight_format != AQ_CRATE_W_Q4_0 && weight_format != AQ_CRATE_W_I8 && weight_format != AQ_CRATE_W_F16)
+        return fail(AQ_ERR_UNSUPPORTED_TYPE, "unknown weight format %d", weight_format);
+    if (weight_format == AQ_CRATE_W_Q4_0 && k % 32)
+        return fail(AQ_ERR_SHAPE, "int4_matmul: K=%lld must be a multiple of 32", (long long)k);
+    const int wt = weight_format == AQ_CRATE_W_Q4_0 ? CRATE_W_Q4_0 : weight_format == AQ_CRATE_W_I8 ? CRATE_W_I8 : CRATE_W_F16;
+    return hip_status(launch_weight_only_matmul(wt, d_act, d_w, d_scales, m, n, k, d_out, ctx->stream),
+                      "weight-only matmul");
+}
+
+int aq_int4_matmul_gemv_q4_x_q8(aq_ctx *ctx, const float *a, const uint8_t *w_packed, const float *w_scales, int64_t n,
+                                int64_t k, float *out) {
+    int rc = crate_prologue(ctx, 1, n, k);
+    if (rc) return rc;
+    if (k % 32) return fail(AQ_ERR_SHAPE, "K=%lld must be a multiple of 32", (long long)k);
+    if (!a || !w_packed || !w_scales || !out) return fail(AQ_ERR_INVALID_ARG, "null argument");
+    ScratchPlan P;
+    const size_t oa = P.add(k * 4), ow = P.add(n * (k / 2)), os = P.add(n * (k / 32) * 4), oo = P.add(n * 4),
+                 orec = P.add(q4_x_q8_act_bytes(k));
+    if ((rc = ensure_scratch(ctx, P.total))) return rc;
+    uint8_t *S = (uint8_t *)ctx->scratch;
+    if ((rc = h2d(ctx, S + oa, a, k * 4)) || (rc = h2d(ctx, S + ow, w_packed, n * (k / 2))) ||
+        (rc = h2d(ctx, S + os, w_scales, n * (k / 32) * 4)))
+        return rc;
+    if ((rc = hip_status(launch_q4_x_q8_gemv((float *)(S + oa), S + ow, (float *)(S + os), n, k, (float *)(S + oo), S + orec,
+                                             nullptr, nullptr, ctx->stream),
+                         "q4 x q8 gemv")))
+        return rc;
+    return d2h_sync(ctx, out, S + oo, n * 4);
+}
+
+size_t aq_q4_x_q8_act_bytes(int64_t k) { return k > 0 && k % 32 == 0 ? q4_x_q8_act_bytes(k) : 0; }
+
+int aq_int4_matmul_gemv_q4_x_q8_device(aq_ctx *ctx, const float *d_a, const uint8_t *d_w_packed, const float *d_w_scales,
+                                       int64_t n, int64_t k, float *d_out, void *d_act, int8_t *d_q, float *d_qscales) {
+    int rc = crate_prologue(ctx, 1, n, k);
+    if (rc) return rc;
+    if (k % 32) return fail(AQ_ERR_SHAPE, "K=%lld must be a multiple of 32", (long long)k);
+    return hip_status(launch_q4_x_q8_gemv(d_a, d_w_packed, d_w_scales, n, k, d_out, d_act, d_q, d_qscales, ctx->stream),
+                      "q4 x q8 gemv");
+}
+
+int aq_quantize_int4_q4_0(aq_ctx *ctx, const float *w, int64_t n, int64_t k, uint8_t *packed, float *scales) {
+    int rc = crate_prologue(ctx, 1, n, k);
+    if (rc) return rc;
+    if (k % 32) return fail(AQ_ERR_SHAPE, "quantize_int4: K=%lld must be a multiple of 32", (long long)k);
+    if (!w || !packed || !scales) return fail(AQ_ERR_INVALID_ARG, "null argument");
+    ScratchPlan P;
+    const size_t ow = P.add(n * k * 4), op = P.add(n * (k / 2)), os = P.add(n * (k / 32) * 4);
+    if ((rc = ensure_scratch(ctx, P.total))) return rc;
+    uint8_t *S = (uint8_t *)ctx->scratch;
+    if ((rc = h2d(ctx, S + ow, w, n * k * 4))) return rc;
+    if ((rc = hip_status(launch_quantize_int4_q4_0((float *)(S + ow), n, k, S + op, (float *)(S + os), ctx->stream),
+                         "quantize_int4_q4_0")))
+        return rc;
+    HIP_TRY(hipMemcpyAsync(packed, S + op, n * (k / 2), hipMemcpyDeviceToHost, ctx->stream));
+    return d2h_sync(ctx, scales, S + os, n * (k / 32) * 4);
+}
+
+int aq_dequantize_q6_k(aq_ctx *ctx, const void *blocks, size_t nbytes, int64_t n_elements, float *out) {
+    if (!ctx) return fail(AQ_ERR_INVALID_ARG, "null context");
+    if (n_elements <= 0 || n_elements % 256 || nbytes != (size_t)(n_elements / 256) * 210)
+        return fail(AQ_ERR_SHAPE, "dequantize_q6_k: %zu bytes for %lld elements", nbytes, (long long)n_elements);
+    if (!blocks || !out) return fail(AQ_ERR_INVALID_ARG, "null argument");
+    int rc = use_device(ctx->device);
+    if (rc) return rc;
+    ScratchPlan P;
+    const size_t ob = P.add(nbytes), oo = P.add(n_elements * 4);
+    if ((rc = ensure_scratch(ctx, P.total))) return rc;
+    uint8_t *S = (uint8_t *)ctx->scratch;
+    if ((rc = h2d(ctx, S + ob, blocks, nbytes))) return rc;
+    if ((rc = hip_status(launch_dequantize_q6_k_crate(S + ob, n_elements, (float *)(S + oo), ctx->stream), "dequantize_q6_k")))
+        return rc;
+    return d2h_sync(ctx, out, S + oo, n_elements * 4);
+}
+
+int aq_dequantize_q6_k_device(aq_ctx *ctx, const void *d_blocks, int64_t n_elements, float *d_out) {
+    if (!ctx) return fail(AQ_ERR_INVALID_ARG, "null context");
+    int rc = use_device(ctx->device);
+    if (rc) return rc;
+    return hip_status(launch_dequantize_q6_k_crate((const uint8_t *)d_blocks, n_elements, d_out, ctx->stream),
+                      "dequantize_q6_k");
+}
+
+static int dequant_row_host(aq_ctx *ctx, int wt, const void *table, const float *scales, int64_t n_rows, int64_t row,
+                            int64_t k, float *out) {
+    if (!ctx) return fail(AQ_ERR_INVALID_ARG, "null context");
+    if (k <= 0 || k % 32) return fail(AQ_ERR_SHAPE, "K=%lld must be a multiple of 32", (long long)k);
+    if (row < 0 || row >= n_rows) return fail(AQ_ERR_SHAPE, "row %lld outside 0..%lld", (long long)row, (long long)n_rows);
+    if (!table || !scales || !out) return fail(AQ_ERR_INVALID_ARG, "null argument");
+    int rc = use_device(ctx->device);
+    if (rc) return rc;
+    const size_t rb = wt == CRATE_W_Q4_0 ? (size_t)k / 2 : (size_t)k, sb = (size_t)(k / 32) * 4;
+    ScratchPlan P;
+    const size_t ot = P.add(rb), os = P.add(sb), orow = P.add(8), oo = P.add(k * 4);
+    if ((rc = ensure_scratch(ctx, P.total))) return rc;
+    uint8_t *S = (uint8_t *)ctx->scratch;
+    const int64_t zero = 0;
+    // only the requested row travels: it becomes row 0 of a one-row table
+    if ((rc = h2d(ctx, S + ot, (const uint8_t *)table + (size_t)row * rb, rb)) ||
+        (rc = h2d(ctx, S + os, (const uint8_t *)scales + (size_t)row * sb, sb)) || (rc = h2d(ctx, S + orow, &zero, 8)))
+        return rc;
+    if ((rc = hip_status(launch_dequant_rows(wt, S + ot, (float *)(S + os), 1, (int64_t *)(S + orow), 1, k, (float *)(S + oo),
+                                             ctx->stream),
+                         "dequant row")))
+        return rc;
+    return d2h_sync(ctx, out, S + oo, k * 4);
+}
+
+int aq_q4_0_dequant_row(aq_ctx *ctx, const uint8_t *packed, const float *scales, int64_t n_rows, int64_t row, int64_t k,
+                        float *out) {
+    return dequant_row_host(ctx, CRATE_W_Q4_0, packed, scales, n_rows, row, k, out);
+}
+
+int aq_q8_0_dequant_row(aq_ctx *ctx, const int8_t *w, const float *scales, int64_t n_rows, int64_t row, int64_t k,
+                        float *out) {
+    return dequant_row_host(ctx, CRATE_W_I8, w, scales, n_rows, row, k, out);
+}
+
+int aq_dequant_rows_device(aq_ctx *ctx, int weight_format, const void *d_table, const float *d_scales, int64_t n_rows,
+                           const int64_t *d_rows, int64_t n_out, int64_t k, float *d_out) {
+    if (!ctx) return fail(AQ_ERR_INVALID_ARG, "null context");
+    if (weight_format != AQ_CRATE_W_Q4_0 && weight_format != AQ_CRATE_W_I8)
+        return fail(AQ_ERR_UNSUPPORTED_TYPE, "row tables are Q4_0-style or int8");
+    int rc = use_device(ctx->device);
+    if (rc) return rc;
+    return hip_status(launch_dequant_rows(weight_format == AQ_CRATE_W_Q4_0 ? CRATE_W_Q4_0 : CRATE_W_I8, d_table, d_scales,
+                                          n_rows, d_rows, n_out, k, d_out, ctx->stream),
+                      "dequant rows");
+}

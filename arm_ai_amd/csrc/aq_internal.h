@@ -128,6 +128,25 @@ hipError_t launch_gemm(const WLayout &w, int64_t n, int64_t k, const ActPlanes &
 // weight type / shape has no GEMM (the matvec then serves m > 8 too).
 size_t gemm_workspace_bytes(int type, int64_t m, int64_t n, int64_t k);
 
+// The NIF crate's own kernels (k_crate.hip; shape_ops.rs).
+enum { CRATE_W_Q4_0 = 0, CRATE_W_I8 = 1, CRATE_W_F16 = 2 };
+// out[i][j] = ((f32) sum_k a[i][k] w[j][k]) * (act_scales ? act_scales[i] : act_scale) * w_scales[j]
+hipError_t launch_int8_matmul(const int8_t *a, const int8_t *w, const float *act_scales, float act_scale,
+                              const float *w_scales, int64_t m, int64_t n, int64_t k, float *out, hipStream_t s);
+hipError_t launch_quantize_int8_per_token(const float *a, int64_t m, int64_t k, int8_t *q, float *scales, hipStream_t s);
+// f32 activations [m][k] x weights [n][k] (Q4_0-style, int8 or f16) -> [m][n]
+hipError_t launch_weight_only_matmul(int wt, const float *a, const void *w, const float *w_scales, int64_t m, int64_t n,
+                                     int64_t k, float *out, hipStream_t s);
+// Q4_0 x Q8 GEMV; act: q4_x_q8_act_bytes(k) of scratch; q_out / s_out (optional)
+// receive the quantised activation [k] i8 and its group scales [k/32].
+size_t q4_x_q8_act_bytes(int64_t k);
+hipError_t launch_q4_x_q8_gemv(const float *a, const uint8_t *w_packed, const float *w_scales, int64_t n, int64_t k,
+                               float *out, void *act, int8_t *q_out, float *s_out, hipStream_t s);
+hipError_t launch_quantize_int4_q4_0(const float *w, int64_t n, int64_t k, uint8_t *packed, float *scales, hipStream_t s);
+hipError_t launch_dequantize_q6_k_crate(const uint8_t *blocks, int64_t nel, float *out, hipStream_t s);
+hipError_t launch_dequant_rows(int wt, const void *table, const float *scales, int64_t ntab, const int64_t *rows,
+                               int64_t nr, int64_t k, float *out, hipStream_t s);
+
 }  // namespace aq
 
 // ---------------------------------------------------------------------------

@@ -211,6 +211,12 @@ MATVEC_CASES = {  # name: (weight type, n, k, m, seed)
 DECODE_CASES = {  # name: (prompt tokens, new tokens, seed)
     "c2_tinyllama_decode": (512, 128, 2),
 }
+CRATE_CASES = {  # the NIF crate's own kernels: name: (kind, m, n, k)
+    "crate_q4_x_q8_gemv_4096x4096": ("q4_x_q8", 1, 4096, 4096),
+    "crate_int4_gemv_f32_4096x4096": ("q4_0", 1, 4096, 4096),
+    "crate_int8_weight_gemv_4096x4096": ("i8w", 1, 4096, 4096),
+    "crate_int8_per_token_m512_4096x4096": ("i8i8", 512, 4096, 4096),
+}
 PREFILL_CASES = {  # name: (n, k, m, seed), Q4_K weight
     "c3_prefill_q4k_5632x2048_m512": (5632, 2048, 512, 3),
     "c3_prefill_q4k_2048x5632_m512": (2048, 5632, 512, 3),
@@ -256,6 +262,59 @@ def measure_decode(ctx, n_prompt, n_new, seed):
     return out
 
 
+def measure_crate(ctx, kind, m, n, k, steps, warmup):
+    """One of the NIF crate's kernels on device memory (weights rotated over
+    enough copies to exceed the Infinity Cache); GB/s of algorithmic bytes, or
+    int8 TOPS for the int8 x int8 matmul."""
+    import arm_ai_amd as A
+    from arm_ai_amd import hip
+
+    L = A._lib.load()
+    rng = np.random.default_rng(11)
+    if kind in ("q4_x_q8", "q4_0"):
+        wbytes = n * (k // 2) + n * (k // 32) * 4
+    elif kind == "i8w":
+        wbytes = n * k + n * 4
+    else:
+        wbytes = n * k + n * 4
+    copies = copies_for(wbytes)
+    ws = []
+    for _ in range(copies):
+        if kind in ("q4_x_q8", "q4_0"):
+            ws.append((hip.to_device(rng.integers(0, 256, (n, k // 2)).astype(np.uint8)),
+                       hip.to_device(rng.uniform(1e-3, 0.05, (n, k // 32)).astype(np.float32))))
+        else:
+            ws.append((hip.to_device(rng.integers(-127, 128, (n, k)).astype(np.int8)),
+                       hip.to_device(rng.uniform(1e-3, 0.05, n).astype(np.float32))))
+    dout = hip.DeviceBuffer(m * n * 4)
+    if kind == "i8i8":
+        da = hip.to_device(rng.integers(-127, 128, (m, k)).astype(np.int8))
+        das = hip.to_device(rng.uniform(1e-3, 0.05, m).astype(np.float32))
+        fn = lambda i: L.aq_int8_matmul_f32_device(ctx.handle, da.ptr, ws[i % copies][0].ptr, das.ptr, 0.0,
+                                                   ws[i % copies][1].ptr, m, n, k, dout.ptr)
+    else:
+        da = hip.to_device(rng.standard_normal((m, k)).astype(np.float32))
+        if kind == "q4_x_q8":
+            act = hip.DeviceBuffer(int(L.aq_q4_x_q8_act_bytes(k)))
+            fn = lambda i: L.aq_int4_matmul_gemv_q4_x_q8_device(ctx.handle, da.ptr, ws[i % copies][0].ptr,
+                                                                ws[i % copies][1].ptr, n, k, dout.ptr, act.ptr, None, None)
+        else:
+            fmt = 0 if kind == "q4_0" else 1
+            fn = lambda i: L.aq_weight_only_matmul_device(ctx.handle, fmt, da.ptr, ws[i % copies][0].ptr,
+                                                          ws[i % copies][1].ptr, m, n, k, dout.ptr)
+    assert fn(0) == 0
+    ms, _ = time_graph(ctx, fn, min(steps, 100), min(warmup, 10))
+    out = {"kind": kind, "m": m, "n": n, "k": k, "us": round(ms * 1e3, 3), "rotating_weight_copies": copies}
+    if kind == "i8i8":
+        out["TOPS"] = round(2.0 * m * n * k / (ms / 1e3) / 1e12, 1)
+        out["frac_int8_peak"] = round(out["TOPS"] / INT8_PEAK_TOPS, 4)
+    else:
+        nbytes = wbytes + m * k * 4 + m * n * 4
+        out["GBps"] = round(nbytes / (ms / 1e3) / 1e9, 1)
+        out["frac_hbm"] = round(out["GBps"] / HBM_PEAK_GBS, 4)
+    return out
+
+
 def run_decode_child(name):
     """Run a decode case in a child process: the driver's torch glue needs torch
     imported before this library is loaded (one HIP runtime per process)."""
@@ -271,6 +330,10 @@ def run_decode_child(name):
 
 
 def run_case(ctx, name, steps, warmup):
+    if name in CRATE_CASES:
+        out = measure_crate(ctx, *CRATE_CASES[name], steps, warmup)
+        log(f"{name}: {out['us']} us ({out.get('GBps', out.get('TOPS'))} {'GB/s' if 'GBps' in out else 'TOPS'})")
+        return out
     if name in DECODE_CASES:
         n_prompt, n_new, seed = DECODE_CASES[name]
         out = measure_decode(ctx, n_prompt, n_new, seed)
@@ -323,7 +386,7 @@ def main() -> int:
         print(json.dumps({"copy_calibration_bytes": nbytes, "copies": 10}), flush=True)
         return 0
 
-    all_cases = list(MATVEC_CASES) + list(PREFILL_CASES) + list(DECODE_CASES)
+    all_cases = list(MATVEC_CASES) + list(PREFILL_CASES) + list(CRATE_CASES) + list(DECODE_CASES)
     if args.case is not None and args.case not in all_cases:
         print(f"unknown case {args.case!r}; cases: {', '.join(all_cases)}", file=sys.stderr)
         return 2
@@ -385,6 +448,8 @@ def main() -> int:
         for name in MATVEC_CASES:
             extra[name] = run_case(ctx, name, args.steps, args.warmup)
         for name in PREFILL_CASES:
+            extra[name] = run_case(ctx, name, args.steps, args.warmup)
+        for name in CRATE_CASES:
             extra[name] = run_case(ctx, name, args.steps, args.warmup)
         for name in DECODE_CASES:
             extra[name] = run_decode_child(name)

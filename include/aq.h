@@ -128,6 +128,95 @@ int aq_quantize_q8_0(aq_ctx *ctx, const float *x, int64_t m, int64_t k, void *ou
 int aq_qmatmul_block_sums(aq_ctx *ctx, const aq_qweight *w, const float *lhs, int64_t m,
                           int64_t k, int32_t *S, int32_t *Smin);
 
+/* ===================================================================
+ * Crate kernels: the NIF crate's own int8 / int4 kernels
+ * (native/arm_ai_nif/src/shape_ops.rs), the secondary quantized matmuls that
+ * the NIFs in native/arm_ai_nif/src/lib.rs expose next to candle's QMatMul.
+ * Arguments keep the NIFs' meaning and order (binaries become pointers plus
+ * the sizes the NIFs derive).  Integer dots, the int8 matmul scalings, the
+ * quantizers and the dequantizers are bit-identical to the crate's scalar
+ * code; the weight-only matmuls' f32 sums are reordered (tolerance-bound).
+ * =================================================================== */
+
+/* Weight formats of aq_weight_only_matmul_device / aq_dequant_rows_device. */
+typedef enum aq_crate_weight {
+    AQ_CRATE_W_Q4_0 = 0, /* [N][K/2] packed nibbles (low = even k), [N][K/32] f32 scales; value (q - 8) * s */
+    AQ_CRATE_W_I8 = 1,   /* [N][K] int8, [N] f32 per-row scales (matmul) or [N][K/32] (row tables) */
+    AQ_CRATE_W_F16 = 2   /* [N][K] IEEE binary16 */
+} aq_crate_weight;
+
+/* int8_matmul_f32 (shape_ops.rs:1169-1211; NIF int8_matmul_f32_op, lib.rs:216-236):
+ * out[m][n] = (f32)(sum_k a[m][k] * w[n][k]) * act_scale * w_scales[n]. */
+int aq_int8_matmul_f32(aq_ctx *ctx, const int8_t *a, const int8_t *w, const float *w_scales, float act_scale,
+                       int64_t m, int64_t n, int64_t k, float *out);
+/* int8_matmul_f32_per_token (shape_ops.rs:1222-1264; NIF lib.rs:240-266):
+ * as above with act_scales[m] per row. */
+int aq_int8_matmul_f32_per_token(aq_ctx *ctx, const int8_t *a, const int8_t *w, const float *act_scales,
+                                 const float *w_scales, int64_t m, int64_t n, int64_t k, float *out);
+/* Both, on device memory (d_act_scales null: act_scale for every row). */
+int aq_int8_matmul_f32_device(aq_ctx *ctx, const int8_t *d_a, const int8_t *d_w, const float *d_act_scales,
+                              float act_scale, const float *d_w_scales, int64_t m, int64_t n, int64_t k, float *d_out);
+
+/* quantize_int8_per_token (shape_ops.rs:1273-1292; NIF lib.rs:269-296):
+ * per row scale = max|x| / 127 (1 for a zero row), q = clamp(round(x / scale), -127, 127). */
+int aq_quantize_int8_per_token(aq_ctx *ctx, const float *a, int64_t m, int64_t k, int8_t *q, float *scales);
+int aq_quantize_int8_per_token_device(aq_ctx *ctx, const float *d_a, int64_t m, int64_t k, int8_t *d_q,
+                                      float *d_scales);
+
+/* dequant_matmul_int8_f32 (shape_ops.rs:1525-1582; NIF lib.rs:508-532):
+ * out[b][m][n] = (sum_k act[b][m][k] * (f32)w[n][k]) * scales[n]. */
+int aq_dequant_matmul_int8_f32(aq_ctx *ctx, const float *act, const int8_t *w, const float *scales, int64_t b,
+                               int64_t m, int64_t n, int64_t k, float *out);
+/* dequant_matmul_f16_f32 (shape_ops.rs:1386-1490; NIF lib.rs:176-195): f16 weights. */
+int aq_dequant_matmul_f16_f32(aq_ctx *ctx, const float *act, const uint16_t *w, int64_t b, int64_t m, int64_t n,
+                              int64_t k, float *out);
+/* int4_matmul_f32 (shape_ops.rs:3175-3236; NIF lib.rs:451-475) and its M = 1
+ * form int4_matmul_gemv_neon (shape_ops.rs:3059-3166; NIF lib.rs:428-448):
+ * Q4_0-style weights, K a multiple of 32. */
+int aq_int4_matmul_f32(aq_ctx *ctx, const float *a, const uint8_t *w_packed, const float *w_scales, int64_t m,
+                       int64_t n, int64_t k, float *out);
+int aq_int4_matmul_gemv(aq_ctx *ctx, const float *a, const uint8_t *w_packed, const float *w_scales, int64_t n,
+                        int64_t k, float *out);
+/* The three weight-only matmuls on device memory (d_scales: per-group for
+ * Q4_0, per-row for I8, unused for F16). */
+int aq_weight_only_matmul_device(aq_ctx *ctx, int weight_format, const float *d_act, const void *d_w,
+                                 const float *d_scales, int64_t m, int64_t n, int64_t k, float *d_out);
+
+/* int4_matmul_gemv_q4_x_q8_neon (shape_ops.rs:2923-3028; NIF lib.rs:404-425):
+ * the activation quantised per group of 32 (scale = max|x| / 127, 1 for a
+ * zero group; q = clamp(round(x / scale), -128, 127)), exact integer group
+ * dots with the (nibble - 8) weights, out[n] = sum_g (f32)dot * w_scale * a_scale. */
+int aq_int4_matmul_gemv_q4_x_q8(aq_ctx *ctx, const float *a, const uint8_t *w_packed, const float *w_scales,
+                                int64_t n, int64_t k, float *out);
+/* Device form; d_act: aq_q4_x_q8_act_bytes(k) of scratch; d_q [k] and
+ * d_qscales [k/32] (optional, may be null) receive the quantised activation. */
+size_t aq_q4_x_q8_act_bytes(int64_t k);
+int aq_int4_matmul_gemv_q4_x_q8_device(aq_ctx *ctx, const float *d_a, const uint8_t *d_w_packed,
+                                       const float *d_w_scales, int64_t n, int64_t k, float *d_out, void *d_act,
+                                       int8_t *d_q, float *d_qscales);
+
+/* quantize_int4_q4_0 (shape_ops.rs:3242-3275; NIF lib.rs:478-505): per group of
+ * 32, scale = max|x| / 7 (1 for a zero group), q = clamp(round(x / scale), -8, 7) + 8,
+ * byte j = (q[2j+1] << 4) | q[2j]. */
+int aq_quantize_int4_q4_0(aq_ctx *ctx, const float *w, int64_t n, int64_t k, uint8_t *packed, float *scales);
+
+/* dequantize_q6_k as the crate has it (shape_ops.rs:2848-2899; NIF
+ * dequantize_q6_k_op, lib.rs:346-355), including its sub-scale index
+ * (8h + {0,2,4,6} for all 32 elements of a group; GGML uses 8h + l/16 + ...). */
+int aq_dequantize_q6_k(aq_ctx *ctx, const void *blocks, size_t nbytes, int64_t n_elements, float *out);
+int aq_dequantize_q6_k_device(aq_ctx *ctx, const void *d_blocks, int64_t n_elements, float *d_out);
+
+/* q4_0_dequant_row_f32 / q8_0_dequant_row_f32 (shape_ops.rs:2780-2808,
+ * :2812-2832; NIFs lib.rs:358-399): one row of an n_rows-row table. */
+int aq_q4_0_dequant_row(aq_ctx *ctx, const uint8_t *packed, const float *scales, int64_t n_rows, int64_t row,
+                        int64_t k, float *out);
+int aq_q8_0_dequant_row(aq_ctx *ctx, const int8_t *w, const float *scales, int64_t n_rows, int64_t row, int64_t k,
+                        float *out);
+/* Batched device form (an embedding lookup): out[i] = row d_rows[i] of the
+ * table; an index outside 0..n_rows-1 yields a zero row. */
+int aq_dequant_rows_device(aq_ctx *ctx, int weight_format, const void *d_table, const float *d_scales, int64_t n_rows,
+                           const int64_t *d_rows, int64_t n_out, int64_t k, float *d_out);
+
 #ifdef __cplusplus
 }
 #endif

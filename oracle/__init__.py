@@ -183,3 +183,138 @@ def dequantize(wtype: int, w: np.ndarray, k: int) -> np.ndarray:
 
 def max_threads() -> int:
     return int(lib().orc_max_threads())
+
+
+# ---------------------------------------------------------------------------
+# The NIF crate's own int8 / int4 kernels (crate_ops.c, restating
+# native/arm_ai_nif/src/shape_ops.rs; see the C comments for line numbers).
+# ---------------------------------------------------------------------------
+def _crate_lib() -> ctypes.CDLL:
+    L = lib()
+    if getattr(L, "_crate_ready", False):
+        return L
+    P, i64, f32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_float
+    sigs = {
+        "orc_int8_matmul_f32": [P, P, f32, P, i64, i64, i64, P],
+        "orc_int8_matmul_f32_per_token": [P, P, P, P, i64, i64, i64, P],
+        "orc_quantize_int8_per_token": [P, i64, i64, P, P],
+        "orc_dequant_matmul_int8_f32": [P, P, P, i64, i64, i64, i64, P],
+        "orc_dequant_matmul_f16_f32": [P, P, i64, i64, i64, i64, P],
+        "orc_int4_matmul_f32": [P, P, P, i64, i64, i64, P],
+        "orc_int4_matmul_gemv": [P, P, P, i64, i64, P],
+        "orc_quantize_q8_groups": [P, i64, P, P],
+        "orc_int4_matmul_gemv_q4_x_q8": [P, P, P, i64, i64, P, P, P],
+        "orc_quantize_int4_q4_0": [P, i64, i64, P, P],
+        "orc_dequantize_q6_k_crate": [P, i64, P],
+        "orc_q4_0_dequant_row": [P, P, i64, i64, P],
+        "orc_q8_0_dequant_row": [P, P, i64, i64, P],
+    }
+    for name, args in sigs.items():
+        f = getattr(L, name)
+        f.argtypes = args
+        f.restype = None
+    L._crate_ready = True
+    return L
+
+
+def _c(a, dt):
+    return np.ascontiguousarray(a, dtype=dt)
+
+
+def int8_matmul_f32(a, w, act_scale, w_scales, m, n, k):
+    a, w, ws = _c(a, np.int8), _c(w, np.int8), _c(w_scales, np.float32)
+    out = np.zeros((m, n), np.float32)
+    _crate_lib().orc_int8_matmul_f32(_p(a), _p(w), float(act_scale), _p(ws), m, n, k, _p(out))
+    return out
+
+
+def int8_matmul_f32_per_token(a, w, act_scales, w_scales, m, n, k):
+    a, w = _c(a, np.int8), _c(w, np.int8)
+    as_, ws = _c(act_scales, np.float32), _c(w_scales, np.float32)
+    out = np.zeros((m, n), np.float32)
+    _crate_lib().orc_int8_matmul_f32_per_token(_p(a), _p(w), _p(as_), _p(ws), m, n, k, _p(out))
+    return out
+
+
+def quantize_int8_per_token(a, m, k):
+    a = _c(a, np.float32)
+    q = np.zeros((m, k), np.int8)
+    s = np.zeros(m, np.float32)
+    _crate_lib().orc_quantize_int8_per_token(_p(a), m, k, _p(q), _p(s))
+    return q, s
+
+
+def dequant_matmul_int8_f32(act, w, scales, b, m, n, k):
+    act, w, s = _c(act, np.float32), _c(w, np.int8), _c(scales, np.float32)
+    out = np.zeros((b, m, n), np.float32)
+    _crate_lib().orc_dequant_matmul_int8_f32(_p(act), _p(w), _p(s), b, m, n, k, _p(out))
+    return out
+
+
+def dequant_matmul_f16_f32(act, w_f16bits, b, m, n, k):
+    act, w = _c(act, np.float32), _c(w_f16bits, np.uint16)
+    out = np.zeros((b, m, n), np.float32)
+    _crate_lib().orc_dequant_matmul_f16_f32(_p(act), _p(w), b, m, n, k, _p(out))
+    return out
+
+
+def int4_matmul_f32(a, w_packed, w_scales, m, n, k):
+    a, wp, ws = _c(a, np.float32), _c(w_packed, np.uint8), _c(w_scales, np.float32)
+    out = np.zeros((m, n), np.float32)
+    _crate_lib().orc_int4_matmul_f32(_p(a), _p(wp), _p(ws), m, n, k, _p(out))
+    return out
+
+
+def int4_matmul_gemv(a, w_packed, w_scales, n, k):
+    a, wp, ws = _c(a, np.float32), _c(w_packed, np.uint8), _c(w_scales, np.float32)
+    out = np.zeros(n, np.float32)
+    _crate_lib().orc_int4_matmul_gemv(_p(a), _p(wp), _p(ws), n, k, _p(out))
+    return out
+
+
+def quantize_q8_groups(a, k):
+    a = _c(a, np.float32)
+    q = np.zeros(k, np.int8)
+    s = np.zeros(k // 32, np.float32)
+    _crate_lib().orc_quantize_q8_groups(_p(a), k, _p(q), _p(s))
+    return q, s
+
+
+def int4_matmul_gemv_q4_x_q8(a, w_packed, w_scales, n, k):
+    """Returns (out [n], quantised activation i8 [k], its group scales [k/32])."""
+    a, wp, ws = _c(a, np.float32), _c(w_packed, np.uint8), _c(w_scales, np.float32)
+    out = np.zeros(n, np.float32)
+    q = np.zeros(k, np.int8)
+    s = np.zeros(k // 32, np.float32)
+    _crate_lib().orc_int4_matmul_gemv_q4_x_q8(_p(a), _p(wp), _p(ws), n, k, _p(out), _p(q), _p(s))
+    return out, q, s
+
+
+def quantize_int4_q4_0(w, n, k):
+    w = _c(w, np.float32)
+    packed = np.zeros((n, k // 2), np.uint8)
+    scales = np.zeros((n, k // 32), np.float32)
+    _crate_lib().orc_quantize_int4_q4_0(_p(w), n, k, _p(packed), _p(scales))
+    return packed, scales
+
+
+def dequantize_q6_k_crate(blocks, n_elements):
+    b = _c(blocks, np.uint8).ravel()
+    nb = n_elements // 256
+    out = np.zeros(nb * 256, np.float32)
+    _crate_lib().orc_dequantize_q6_k_crate(_p(b), nb, _p(out))
+    return out
+
+
+def q4_0_dequant_row(packed, scales, row, k):
+    p, s = _c(packed, np.uint8), _c(scales, np.float32)
+    out = np.zeros(k, np.float32)
+    _crate_lib().orc_q4_0_dequant_row(_p(p), _p(s), row, k, _p(out))
+    return out
+
+
+def q8_0_dequant_row(w, scales, row, k):
+    w, s = _c(w, np.int8), _c(scales, np.float32)
+    out = np.zeros(k, np.float32)
+    _crate_lib().orc_q8_0_dequant_row(_p(w), _p(s), row, k, _p(out))
+    return out

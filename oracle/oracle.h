@@ -97,6 +97,29 @@ int orc_dequantize_row(int type, const uint8_t *w, int64_t k, float *out);
 /* Number of OpenMP threads the library would use by default. */
 int orc_max_threads(void);
 
+/* ---- the NIF crate's own int8 / int4 kernels (crate_ops.c;
+ *      native/arm_ai_nif/src/shape_ops.rs) ---- */
+void orc_int8_matmul_f32(const int8_t *a, const int8_t *w, float act_scale, const float *w_scales, int64_t m,
+                         int64_t n, int64_t k, float *out);
+void orc_int8_matmul_f32_per_token(const int8_t *a, const int8_t *w, const float *act_scales, const float *w_scales,
+                                   int64_t m, int64_t n, int64_t k, float *out);
+void orc_quantize_int8_per_token(const float *a, int64_t m, int64_t k, int8_t *q, float *scales);
+void orc_dequant_matmul_int8_f32(const float *act, const int8_t *w, const float *scales, int64_t b, int64_t m,
+                                 int64_t n, int64_t k, float *out);
+void orc_dequant_matmul_f16_f32(const float *act, const uint16_t *w, int64_t b, int64_t m, int64_t n, int64_t k,
+                                float *out);
+void orc_int4_matmul_f32(const float *a, const uint8_t *w_packed, const float *w_scales, int64_t m, int64_t n,
+                         int64_t k, float *out);
+void orc_int4_matmul_gemv(const float *a, const uint8_t *w_packed, const float *w_scales, int64_t n, int64_t k,
+                          float *out);
+void orc_quantize_q8_groups(const float *a, int64_t k, int8_t *q, float *scales);
+void orc_int4_matmul_gemv_q4_x_q8(const float *a, const uint8_t *w_packed, const float *w_scales, int64_t n,
+                                  int64_t k, float *out, int8_t *aq, float *as);
+void orc_quantize_int4_q4_0(const float *w, int64_t n, int64_t k, uint8_t *packed, float *scales);
+void orc_dequantize_q6_k_crate(const uint8_t *in, int64_t n_blocks, float *out);
+void orc_q4_0_dequant_row(const uint8_t *packed, const float *scales, int64_t row, int64_t k, float *out);
+void orc_q8_0_dequant_row(const int8_t *w, const float *scales, int64_t row, int64_t k, float *out);
+
 #ifdef __cplusplus
 }
 #endif
