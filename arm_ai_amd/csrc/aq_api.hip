@@ -148,6 +148,11 @@ CallLayout call_layout(const aq_qweight *w, int64_t m, bool host_io, bool dump, 
 }
 
 bool use_gemm(const aq_qweight *w, int64_t m) { return m > 8 && gemm_workspace_bytes(w->type, m, w->n, w->k) != (size_t)-1; }
+// 2 or more rows of Q4_K / Q6_K without a GEMM: quantizer kernel, then the
+// matrix-core matvec
+bool use_mmv(const aq_qweight *w, int64_t m) {
+    return m >= 2 && (w->type == AQ_TYPE_Q4_K || w->type == AQ_TYPE_Q6_K) && w->k <= mmv_max_k();
+}
 
 int check_mm(aq_ctx *ctx, const aq_qweight *w, int64_t m, int64_t k) {
     if (!ctx) return fail(AQ_ERR_INVALID_ARG, "null context");
@@ -158,9 +163,11 @@ int check_mm(aq_ctx *ctx, const aq_qweight *w, int64_t m, int64_t k) {
     return AQ_OK;
 }
 
-// The matmul of d_x [m][k] into d_y on ctx->stream.  m <= 8 (or no GEMM
-// for this shape): one matvec launch that quantises d_x itself.  m > 8: the
-// quantizer kernel writes the activation planes at `act`, then the GEMM.
+// The matmul of d_x [m][k] into d_y on ctx->stream.  m > 8 with a GEMM for
+// the shape: the quantizer kernel writes the activation planes at `act`, then
+// the GEMM.  Other m >= 2 of Q4_K / Q6_K: the quantizer, then the
+// matrix-core matvec (passes of 8 rows).  Otherwise (m = 1, Q8_0): one matvec
+// launch that quantises d_x itself.
 int run_matmul(aq_ctx *ctx, const aq_qweight *w, const float *d_x, int64_t m, float *d_y, void *act, int32_t *dS,
                int32_t *dSmin, void *ws, size_t ws_bytes) {
     hipError_t e;
@@ -173,6 +180,12 @@ int run_matmul(aq_ctx *ctx, const aq_qweight *w, const float *d_x, int64_t m, fl
         if (e == hipSuccess) return AQ_OK;
         if (e != hipErrorNotSupported) return fail(AQ_ERR_HIP, "gemm: %s", hipGetErrorString(e));
         e = launch_matvec(w->layout, w->n, w->k, nullptr, &a, m, d_y, dS, dSmin, ctx->stream);
+    } else if (use_mmv(w, m)) {
+        ActPlanes a = act_planes(act, m, w->k);
+        e = launch_quantize_q8k(d_x, m, w->k, a, ctx->stream);
+        if (e != hipSuccess) return fail(AQ_ERR_HIP, "activation quantizer: %s", hipGetErrorString(e));
+        e = launch_mmv(w->layout, w->n, w->k, a, m, d_y, dS, dSmin, ctx->stream);
+        if (e == hipErrorNotSupported) e = launch_matvec(w->layout, w->n, w->k, nullptr, &a, m, d_y, dS, dSmin, ctx->stream);
     } else if (((uintptr_t)d_x & 15) == 0) {
         e = launch_matvec(w->layout, w->n, w->k, d_x, nullptr, m, d_y, dS, dSmin, ctx->stream);
     } else {
@@ -442,6 +455,8 @@ int aq_qmatmul_preq_device(aq_ctx *ctx, const aq_qweight *w, const void *d_act, 
                         L.total - L.ws, ctx->stream);
         if (e != hipSuccess && e != hipErrorNotSupported) return fail(AQ_ERR_HIP, "gemm: %s", hipGetErrorString(e));
     }
+    if (e == hipErrorNotSupported && use_mmv(w, m))
+        e = launch_mmv(w->layout, w->n, w->k, a, m, d_dst, nullptr, nullptr, ctx->stream);
     if (e == hipErrorNotSupported) e = launch_matvec(w->layout, w->n, w->k, nullptr, &a, m, d_dst, nullptr, nullptr, ctx->stream);
     if (e == hipErrorNotSupported) return fail(AQ_ERR_SHAPE, "k=%lld is larger than the matvec supports", (long long)w->k);
     if (e != hipSuccess) return fail(AQ_ERR_HIP, "matvec: %s", hipGetErrorString(e));

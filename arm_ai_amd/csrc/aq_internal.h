@@ -118,6 +118,12 @@ hipError_t launch_repack(int type, const uint8_t *src, int64_t n, int64_t k, uin
 // S/Smin non-null selects the integer-dump variant ([m][n][blocks] int32).
 hipError_t launch_matvec(const WLayout &w, int64_t n, int64_t k, const float *x, const ActPlanes *act, int64_t m,
                          float *y, int32_t *S, int32_t *Smin, hipStream_t s);
+// Matvec of pre-quantised (Q8_K) rows on the int8 matrix cores, 8 rows per
+// launch, Q4_K / Q6_K weights, k <= mmv_max_k().  Returns hipErrorNotSupported
+// for other types and shapes (the caller then uses launch_matvec).
+int mmv_max_k();
+hipError_t launch_mmv(const WLayout &w, int64_t n, int64_t k, const ActPlanes &act, int64_t m, float *y, int32_t *S,
+                      int32_t *Smin, hipStream_t s);
 // Prefill GEMM on MFMA (m > 8).  Returns hipErrorNotSupported for shapes it
 // does not take; the caller then uses launch_matvec.  ws: gemm_workspace_bytes
 // of scratch (split-K partials, summed by a second launch on the stream).
@@ -172,6 +178,40 @@ __device__ __forceinline__ float u32_as_f32(uint32_t u) { return __builtin_bit_c
 __device__ __forceinline__ uint32_t f32_as_u32(float f) { return __builtin_bit_cast(uint32_t, f); }
 __device__ __forceinline__ rsrc_t buf_rsrc(const void *base, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+// Raw buffer loads of 16 (4) bytes per lane straight into LDS: lane i's bytes
+// land at lds + 16 * i (4 * i); lds must be wave-uniform.  (Kept in
+// non-template functions: used directly inside a kernel template, this
+// builtin stopped the host-side launch stubs from being emitted.)
+typedef __attribute__((address_space(3))) void lds_void;
+__device__ __forceinline__ void buf_to_lds16(rsrc_t r, uint8_t *lds, uint32_t voff, int soff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)lds, 16, voff, soff, 0, 0);
+}
+__device__ __forceinline__ void buf_to_lds4(rsrc_t r, uint8_t *lds, uint32_t voff, int soff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)lds, 4, voff, soff, 0, 0);
+}
+
+// s_waitcnt with only vmcnt constrained (gfx9 encoding: vmcnt[3:0], expcnt[6:4],
+// lgkmcnt[11:8], vmcnt[5:4] at [15:14]).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt is six bits");
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+// Workgroup barrier without the memory fence __syncthreads() adds (that
+// fence would wait for every outstanding load, including the ones issued
+// ahead for later stages).  The "memory" clobber keeps the compiler from
+// moving loads and stores across it; completion of the copies a stage needs
+// is waited for explicitly with wait_vmcnt before it.
+__device__ __forceinline__ void stage_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
+// Barrier after LDS writes only: waits for this wavefront's LDS accesses
+// (lgkmcnt 0), not for its outstanding global loads.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14));
+    asm volatile("s_barrier" ::: "memory");
 }
 
 // DPP lane permutations within a row of 16 lanes.

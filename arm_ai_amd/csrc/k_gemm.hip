@@ -80,17 +80,6 @@ __device__ __forceinline__ int pkmul(uint32_t x, uint32_t s) {
     return (int)__builtin_bit_cast(uint32_t, r);
 }
 
-typedef __attribute__((address_space(3))) void lds_void;
-
-// Raw buffer loads of 16 (4) bytes per lane straight into LDS: lane i's bytes
-// land at lds + 16 * i (4 * i).
-__device__ __forceinline__ void buf_to_lds16(rsrc_t r, uint8_t *lds, uint32_t voff, int soff) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)lds, 16, voff, soff, 0, 0);
-}
-__device__ __forceinline__ void buf_to_lds4(rsrc_t r, uint8_t *lds, uint32_t voff, int soff) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)lds, 4, voff, soff, 0, 0);
-}
-
 // LDS of one workgroup (a tile of 32*MT rows x GBN columns):
 //   two main stages, one super-block each:
 //     quants [rows][256] i8, 16-byte chunk c of row r at chunk c ^ (r & 15), so
@@ -115,20 +104,6 @@ struct TileLds {
     static constexpr int RING0 = 2 * MAIN;
     static constexpr int BYTES = RING0 + 3 * SMALL;
 };
-
-// s_waitcnt with only vmcnt constrained (gfx9 encoding: vmcnt[3:0], expcnt[6:4],
-// lgkmcnt[11:8], vmcnt[5:4] at [15:14]).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
-}
-
-// Workgroup barrier without the memory fence __syncthreads() adds (that
-// fence would wait for every outstanding copy, including the ones issued
-// ahead for later stages).  The "memory" clobber keeps the compiler from
-// moving loads and stores across it; completion of the copies a stage needs
-// is waited for explicitly with wait_vmcnt before it.
-__device__ __forceinline__ void stage_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
 template <int MT, bool DUMP>
 __global__ __launch_bounds__(256, 2) void gemm_q4k_kernel(GemmParams p) {

@@ -206,7 +206,9 @@ MATVEC_CASES = {  # name: (weight type, n, k, m, seed)
     "c1_q6k_32000x2048_b1": (14, 32000, 2048, 1, 2),
     "c4_q4k_4096x14336_b1": (12, 4096, 14336, 1, 5),
     "c4_q4k_14336x4096_b8": (12, 14336, 4096, 8, 6),
+    "c4_q4k_4096x14336_b8": (12, 4096, 14336, 8, 8),
     "c4_q6k_128256x4096_b1": (14, 128256, 4096, 1, 7),
+    "c4_q6k_128256x4096_b8": (14, 128256, 4096, 8, 9),
 }
 DECODE_CASES = {  # name: (prompt tokens, new tokens, seed)
     "c2_tinyllama_decode": (512, 128, 2),
