@@ -132,12 +132,27 @@ def vec_dot(wtype: int, k: int, wrow: np.ndarray, xq_row: np.ndarray) -> float:
     return float(f(k, _p(wrow), _p(xq_row)))
 
 
+def _row_bytes(wtype: int, k: int) -> int:
+    if wtype not in BLOCK_ELEMS:
+        raise ValueError(f"unsupported GGML type {wtype}")
+    if k <= 0 or k % BLOCK_ELEMS[wtype]:
+        raise ValueError(f"k={k} is not a multiple of the block size {BLOCK_ELEMS[wtype]}")
+    return k // BLOCK_ELEMS[wtype] * BLOCK_BYTES[wtype]
+
+
+def _rows_of(buf: np.ndarray, row_bytes: int, what: str) -> int:
+    """Row count of a buffer of whole rows (any shape); the C code trusts it."""
+    if buf.nbytes % row_bytes:
+        raise ValueError(f"{what}: {buf.nbytes} bytes is not a whole number of {row_bytes}-byte rows")
+    return buf.nbytes // row_bytes
+
+
 def block_sums(wtype: int, k: int, w: np.ndarray, xq: np.ndarray, nthreads: int = 0):
     """Integer sums per (m, n, block): returns S, Smin int32 [m, n, nb]."""
     w = np.ascontiguousarray(w)
     xq = np.ascontiguousarray(xq)
-    n = w.shape[0]
-    m = xq.shape[0]
+    n = _rows_of(w, _row_bytes(wtype, k), "weight")
+    m = _rows_of(xq, _row_bytes(act_type(wtype), k), "quantised activation")
     nb = k // BLOCK_ELEMS[wtype]
     S = np.zeros((m, n, nb), np.int32)
     Sm = np.zeros((m, n, nb), np.int32)
@@ -153,7 +168,11 @@ def matmul(wtype: int, x: np.ndarray, w: np.ndarray, n: int, k: int, nthreads: i
     if x.ndim == 1:
         x = x[None, :]
     m = x.shape[0]
+    if x.shape[1] != k:
+        raise ValueError(f"x has {x.shape[1]} columns, k={k}")
     w = np.ascontiguousarray(w)
+    if w.nbytes != n * _row_bytes(wtype, k):
+        raise ValueError(f"weight has {w.nbytes} bytes, {n} rows of k={k} need {n * _row_bytes(wtype, k)}")
     dst = np.zeros((m, n), np.float32)
     rc = lib().orc_matmul(wtype, m, k, n, _p(x), _p(w), _p(dst), nthreads)
     if rc != 0:
@@ -164,7 +183,9 @@ def matmul(wtype: int, x: np.ndarray, w: np.ndarray, n: int, k: int, nthreads: i
 def matmul_preq(wtype: int, xq: np.ndarray, w: np.ndarray, n: int, k: int, nthreads: int = 0) -> np.ndarray:
     xq = np.ascontiguousarray(xq)
     w = np.ascontiguousarray(w)
-    m = xq.shape[0]
+    m = _rows_of(xq, _row_bytes(act_type(wtype), k), "quantised activation")
+    if w.nbytes != n * _row_bytes(wtype, k):
+        raise ValueError(f"weight has {w.nbytes} bytes, {n} rows of k={k} need {n * _row_bytes(wtype, k)}")
     dst = np.zeros((m, n), np.float32)
     rc = lib().orc_matmul_preq(wtype, m, k, n, _p(xq), _p(dst), _p(w), nthreads)
     if rc != 0:
