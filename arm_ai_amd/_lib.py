@@ -76,6 +76,12 @@ SIGNATURES = {
     "aq_q4_0_dequant_row": (INT, [P, P, P, I64, I64, I64, P]),
     "aq_q8_0_dequant_row": (INT, [P, P, P, I64, I64, I64, P]),
     "aq_dequant_rows_device": (INT, [P, INT, P, P, I64, P, I64, I64, P]),
+    # decode-step glue (k_decode.hip)
+    "aq_llama_embed": (INT, [P, P, I64, P, I64, P]),
+    "aq_llama_rmsnorm": (INT, [P, P, P, P, I64, I64, ctypes.c_float, P]),
+    "aq_llama_silu_mul": (INT, [P, P, I64, P]),
+    "aq_llama_attn_decode": (INT, [P, P, P, P, P, P, P, P, I64, I64, I64, I64, P]),
+    "aq_llama_argmax": (INT, [P, P, I64, P, P, P, I64]),
 }
 
 

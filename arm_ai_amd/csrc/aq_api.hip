@@ -834,3 +834,47 @@ int aq_dequant_rows_device(aq_ctx *ctx, int weight_format, const void *d_table, 
                                           n_rows, d_rows, n_out, k, d_out, ctx->stream),
                       "dequant rows");
 }
+
+// ---------------------------------------------------------------- decode-step glue
+int aq_llama_embed(aq_ctx *ctx, const float *d_table, int64_t vocab, const int64_t *d_tok, int64_t hidden,
+                   float *d_out) {
+    if (!ctx) return fail(AQ_ERR_INVALID_ARG, "null context");
+    int rc = use_device(ctx->device);
+    if (rc) return rc;
+    return hip_status(launch_embed(d_table, vocab, d_tok, hidden, d_out, ctx->stream), "embed");
+}
+
+int aq_llama_rmsnorm(aq_ctx *ctx, float *d_x, const float *d_delta, const float *d_w, int64_t m, int64_t n, float eps,
+                     float *d_out) {
+    if (!ctx) return fail(AQ_ERR_INVALID_ARG, "null context");
+    if (m == 0) return AQ_OK;
+    int rc = use_device(ctx->device);
+    if (rc) return rc;
+    return hip_status(launch_rmsnorm(d_x, d_delta, d_w, m, n, eps, d_out, ctx->stream), "rmsnorm");
+}
+
+int aq_llama_silu_mul(aq_ctx *ctx, const float *d_gu, int64_t n, float *d_out) {
+    if (!ctx) return fail(AQ_ERR_INVALID_ARG, "null context");
+    int rc = use_device(ctx->device);
+    if (rc) return rc;
+    return hip_status(launch_silu_mul(d_gu, n, d_out, ctx->stream), "silu_mul");
+}
+
+int aq_llama_attn_decode(aq_ctx *ctx, const float *d_qk, const float *d_v, const float *d_cos, const float *d_sin,
+                         const int64_t *d_pos, float *d_kcache, float *d_vcache, int64_t n_head, int64_t n_kv,
+                         int64_t head_dim, int64_t max_seq, float *d_out) {
+    if (!ctx) return fail(AQ_ERR_INVALID_ARG, "null context");
+    int rc = use_device(ctx->device);
+    if (rc) return rc;
+    return hip_status(launch_attn_decode(d_qk, d_v, d_cos, d_sin, d_pos, d_kcache, d_vcache, n_head, n_kv, head_dim,
+                                         max_seq, d_out, ctx->stream),
+                      "attn_decode");
+}
+
+int aq_llama_argmax(aq_ctx *ctx, const float *d_x, int64_t n, int64_t *d_tok, int64_t *d_pos, int64_t *d_hist,
+                    int64_t hist_len) {
+    if (!ctx) return fail(AQ_ERR_INVALID_ARG, "null context");
+    int rc = use_device(ctx->device);
+    if (rc) return rc;
+    return hip_status(launch_argmax(d_x, n, d_tok, d_pos, d_hist, hist_len, ctx->stream), "argmax");
+}

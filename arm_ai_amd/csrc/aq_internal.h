@@ -153,6 +153,18 @@ hipError_t launch_dequantize_q6_k_crate(const uint8_t *blocks, int64_t nel, floa
 hipError_t launch_dequant_rows(int wt, const void *table, const float *scales, int64_t ntab, const int64_t *rows,
                                int64_t nr, int64_t k, float *out, hipStream_t s);
 
+// Decode-step glue (k_decode.hip).
+hipError_t launch_embed(const float *table, int64_t vocab, const int64_t *d_tok, int64_t hidden, float *out,
+                        hipStream_t s);
+hipError_t launch_rmsnorm(float *x, const float *delta, const float *w, int64_t m, int64_t n, float eps, float *out,
+                          hipStream_t s);
+hipError_t launch_silu_mul(const float *gu, int64_t n, float *out, hipStream_t s);
+hipError_t launch_attn_decode(const float *qk, const float *v, const float *cosb, const float *sinb,
+                              const int64_t *d_pos, float *kc, float *vc, int64_t n_head, int64_t n_kv, int64_t hd,
+                              int64_t max_seq, float *out, hipStream_t s);
+hipError_t launch_argmax(const float *x, int64_t n, int64_t *d_tok, int64_t *d_pos, int64_t *hist, int64_t hist_len,
+                         hipStream_t s);
+
 }  // namespace aq
 
 // ---------------------------------------------------------------------------

@@ -29,12 +29,22 @@ vendored in the reference):
 * ``rms_norm(x) = x / sqrt(mean(x^2) + eps) * w``; ``silu(x) = x / (1 + e^-x)``.
 
 The decode step (one token at a given position) can be captured once into a
-HIP graph and replayed per token (``Llama.generate(..., graph=True)``): the
-KV cache and the RoPE tables are preallocated for ``max_seq`` positions and the
-position lives in device memory, so every replay has the same shapes.
+HIP graph and replayed per token (``Llama.generate(..., graph=True)``).  That
+step does not use torch ops: it is this library's decode-step glue kernels
+(k_decode.hip: embedding, residual add + RMSNorm, RoPE + KV-cache write +
+grouped-query attention in one launch, SiLU * up, and a first-maximum argmax
+that writes the next token and advances the device-side position) around the
+GPU QMatMuls, 9 launches per layer.  Projections that share an input and a
+type are uploaded as one weight (wq|wk, w1|w3: rows concatenated), so each
+pair is one matmul launch.  The KV cache, the RoPE tables and every
+intermediate buffer are preallocated for ``max_seq`` positions, so every
+replay has the same shapes, and because the step feeds its own next token and
+position, several steps can be replayed back to back without a host round
+trip.
 """
 from __future__ import annotations
 
+import ctypes
 import math
 import time
 from dataclasses import dataclass, field
@@ -176,7 +186,7 @@ class Llama:
         self.stream = torch.cuda.ExternalStream(ctx.stream, device=self.dev)
         f32 = dict(dtype=torch.float32, device=self.dev)
         with torch.cuda.stream(self.stream):
-            self.layers = [{name: QMatMul.from_qtensor(qt, ctx) for name, qt in layer.items()} for layer in hw.layers]
+            self.layers = [self._upload_layer(layer) for layer in hw.layers]
             self.attn_norm = [torch.tensor(w, **f32) for w in hw.attn_norm]
             self.ffn_norm = [torch.tensor(w, **f32) for w in hw.ffn_norm]
             self.tok_embeddings = torch.tensor(hw.tok_embeddings, **f32)
@@ -189,7 +199,33 @@ class Llama:
             self.k_cache = torch.zeros((cfg.n_layer, cfg.n_kv_head, cfg.max_seq, hd), **f32)
             self.v_cache = torch.zeros((cfg.n_layer, cfg.n_kv_head, cfg.max_seq, hd), **f32)
         self.ctx.synchronize()
+        self._n_second = {"wqk": cfg.n_kv_head * cfg.head_dim, "w13": cfg.ffn}
         self._graph = None
+
+    def _upload_layer(self, layer: dict[str, QTensor]) -> dict[str, QMatMul]:
+        """The layer's projections in HBM; wq|wk and w1|w3 become one weight each
+        (rows concatenated) when the pair has one type, so one launch serves both."""
+        out = {}
+        for a, b, name in (("wq", "wk", "wqk"), ("w1", "w3", "w13")):
+            qa, qb = layer[a], layer[b]
+            if qa.dtype == qb.dtype and qa.shape[1] == qb.shape[1]:
+                cat = QTensor(qa.dtype, (qa.shape[0] + qb.shape[0], qa.shape[1]),
+                              np.concatenate([qa.data.reshape(-1), qb.data.reshape(-1)]))
+                out[name] = QMatMul.from_qtensor(cat, self.ctx)
+            else:
+                out[a] = QMatMul.from_qtensor(qa, self.ctx)
+                out[b] = QMatMul.from_qtensor(qb, self.ctx)
+        for name in ("wv", "wo", "w2"):
+            out[name] = QMatMul.from_qtensor(layer[name], self.ctx)
+        return out
+
+    def _pair(self, lw, merged, a, b, x):
+        """Outputs of projections a and b of x: one launch on the merged weight, or two."""
+        if merged in lw:
+            y = self._mm(lw[merged], x)
+            na = y.shape[1] - self._n_second[merged]
+            return y[:, :na], y[:, na:]
+        return self._mm(lw[a], x), self._mm(lw[b], x)
 
     # ------------------------------------------------------------ pieces
     # The work runs on the library's stream; the caller's current stream waits
@@ -239,8 +275,7 @@ class Llama:
         lw = self.layers[i]
         h = x + self._mm(lw["wo"], y)
         n = self._rms_norm(h, self.ffn_norm[i])
-        g = self._mm(lw["w1"], n)
-        u = self._mm(lw["w3"], n)
+        g, u = self._pair(lw, "w13", "w1", "w3", n)
         return h + self._mm(lw["w2"], self.torch.nn.functional.silu(g) * u)
 
     # ------------------------------------------------------------ forward
@@ -269,8 +304,9 @@ class Llama:
             x = self.tok_embeddings[tokens]
             for li, lw in enumerate(self.layers):
                 n = self._rms_norm(x, self.attn_norm[li])
-                q = self._rope(self._mm(lw["wq"], n).view(L, H, D), cos, sin)
-                k = self._rope(self._mm(lw["wk"], n).view(L, Hkv, D), cos, sin)
+                q, k = self._pair(lw, "wqk", "wq", "wk", n)
+                q = self._rope(q.reshape(L, H, D), cos, sin)
+                k = self._rope(k.reshape(L, Hkv, D), cos, sin)
                 v = self._mm(lw["wv"], n).view(L, Hkv, D)
                 self.k_cache[li, :, index_pos:end] = k.transpose(0, 1)
                 self.v_cache[li, :, index_pos:end] = v.transpose(0, 1)
@@ -282,43 +318,76 @@ class Llama:
         return logits
 
     # ------------------------------------------------------------ graph-captured decode step
-    def _decode_step_static(self):
-        """One decode step at the position in self._pos (device), token in self._tok.
-        All shapes are fixed (attention over max_seq with a position mask)."""
+    def _decode_buffers(self):
         torch = self.torch
         cfg = self.cfg
-        H, Hkv, D = cfg.n_head, cfg.n_kv_head, cfg.head_dim
-        pos = self._pos
-        cos = self.cos.index_select(0, pos)
-        sin = self.sin.index_select(0, pos)
-        mask = (self._ar > pos)[None, :]  # [1, max_seq]: positions after pos are masked
-        x = self.tok_embeddings.index_select(0, self._tok)
+        hd = cfg.head_dim
+        f32 = dict(dtype=torch.float32, device=self.dev)
+        i64 = dict(dtype=torch.int64, device=self.dev)
+        self._pos = torch.zeros(1, **i64)
+        self._tok = torch.zeros(1, **i64)
+        self._hist = torch.zeros(cfg.max_seq, **i64)  # token generated at each position
+        self._x = torch.zeros(cfg.hidden, **f32)       # residual stream
+        self._n = torch.zeros(cfg.hidden, **f32)
+        self._qk = torch.zeros((cfg.n_head + cfg.n_kv_head) * hd, **f32)
+        self._v = torch.zeros(cfg.n_kv_head * hd, **f32)
+        self._att = torch.zeros(cfg.n_head * hd, **f32)
+        self._o = torch.zeros(cfg.hidden, **f32)       # wo / w2 output (the next residual delta)
+        self._gu = torch.zeros(2 * cfg.ffn, **f32)
+        self._a = torch.zeros(cfg.ffn, **f32)
+        self._logits = torch.zeros(cfg.vocab, **f32)
+
+    def _decode_step_static(self):
+        """One decode step for the token in self._tok at the position in self._pos
+        (both device memory), through the library's glue kernels and QMatMuls;
+        leaves the logits in self._logits, the next token in self._tok and in
+        self._hist[pos], and pos + 1 in self._pos."""
+        from . import _lib
+
+        L = _lib.load()
+        cfg = self.cfg
+        c = self.ctx.handle
+        hd = cfg.head_dim
+        ptr = lambda t: t.data_ptr()
+        chk = _lib.check
+        eps = ctypes.c_float(cfg.rms_eps)
+        chk(L.aq_llama_embed(c, ptr(self.tok_embeddings), cfg.vocab, ptr(self._tok), cfg.hidden, ptr(self._x)))
+        delta = None
         for li, lw in enumerate(self.layers):
-            n = self._rms_norm(x, self.attn_norm[li])
-            q = self._rope(self._mm(lw["wq"], n).view(1, H, D), cos, sin)
-            k = self._rope(self._mm(lw["wk"], n).view(1, Hkv, D), cos, sin)
-            v = self._mm(lw["wv"], n).view(1, Hkv, D)
-            self.k_cache[li].index_copy_(1, pos, k.transpose(0, 1))
-            self.v_cache[li].index_copy_(1, pos, v.transpose(0, 1))
-            y = self._attend(q.transpose(0, 1), self.k_cache[li], self.v_cache[li], mask)
-            x = self._layer_tail(li, x, y.transpose(0, 1).reshape(1, H * D))
-        logits = self._mm(self.output, self._rms_norm(x, self.norm))[0]
-        self._next.copy_(torch.argmax(logits).view(1))
-        self._logits.copy_(logits)
+            chk(L.aq_llama_rmsnorm(c, ptr(self._x), delta, ptr(self.attn_norm[li]), 1, cfg.hidden, eps, ptr(self._n)))
+            if "wqk" in lw:
+                lw["wqk"].forward_device(ptr(self._n), 1, ptr(self._qk))
+            else:
+                lw["wq"].forward_device(ptr(self._n), 1, ptr(self._qk))
+                lw["wk"].forward_device(ptr(self._n), 1, ptr(self._qk) + 4 * cfg.n_head * hd)
+            lw["wv"].forward_device(ptr(self._n), 1, ptr(self._v))
+            chk(L.aq_llama_attn_decode(c, ptr(self._qk), ptr(self._v), ptr(self.cos), ptr(self.sin), ptr(self._pos),
+                                       ptr(self.k_cache[li]), ptr(self.v_cache[li]), cfg.n_head, cfg.n_kv_head, hd,
+                                       cfg.max_seq, ptr(self._att)))
+            lw["wo"].forward_device(ptr(self._att), 1, ptr(self._o))
+            chk(L.aq_llama_rmsnorm(c, ptr(self._x), ptr(self._o), ptr(self.ffn_norm[li]), 1, cfg.hidden, eps,
+                                   ptr(self._n)))
+            if "w13" in lw:
+                lw["w13"].forward_device(ptr(self._n), 1, ptr(self._gu))
+            else:
+                lw["w1"].forward_device(ptr(self._n), 1, ptr(self._gu))
+                lw["w3"].forward_device(ptr(self._n), 1, ptr(self._gu) + 4 * cfg.ffn)
+            chk(L.aq_llama_silu_mul(c, ptr(self._gu), cfg.ffn, ptr(self._a)))
+            lw["w2"].forward_device(ptr(self._a), 1, ptr(self._o))
+            delta = ptr(self._o)
+        chk(L.aq_llama_rmsnorm(c, ptr(self._x), delta, ptr(self.norm), 1, cfg.hidden, eps, ptr(self._n)))
+        self.output.forward_device(ptr(self._n), 1, ptr(self._logits))
+        chk(L.aq_llama_argmax(c, ptr(self._logits), cfg.vocab, ptr(self._tok), ptr(self._pos), ptr(self._hist),
+                              cfg.max_seq))
 
     def _capture(self):
         torch = self.torch
         self._enter()
         with torch.cuda.stream(self.stream):
-            self._pos = torch.zeros(1, dtype=torch.int64, device=self.dev)
-            self._tok = torch.zeros(1, dtype=torch.int64, device=self.dev)
-            self._next = torch.zeros(1, dtype=torch.int64, device=self.dev)
-            self._logits = torch.zeros(self.cfg.vocab, dtype=torch.float32, device=self.dev)
-            self._ar = torch.arange(self.cfg.max_seq, device=self.dev)
-        # Warm up on the capture stream (library first-call set-up, torch
-        # kernels) at the last cache slot: a step writes its own position's k, v
-        # before attending and masks later positions, so that slot is never read
-        # stale, and the cache entries of a sequence in progress stay intact.
+            self._decode_buffers()
+        # Warm up on the capture stream (library first-call set-up) at the last
+        # cache slot: a step writes only its own position's k, v, so the cache
+        # entries of a sequence in progress stay intact.
         with torch.cuda.stream(self.stream):
             self._pos.fill_(self.cfg.max_seq - 1)
             self._decode_step_static()
@@ -333,7 +402,7 @@ class Llama:
         """Replay the captured decode step for `token` at position `pos`; returns the device logits."""
         if self._graph is None:
             self._capture()
-        if pos >= self.cfg.max_seq:
+        if not 0 <= pos < self.cfg.max_seq:
             raise ValueError(f"position {pos} outside 0..{self.cfg.max_seq}")
         self._enter()
         with self.torch.cuda.stream(self.stream):
@@ -349,14 +418,19 @@ class Llama:
         """First index of the maximum (llama_candle.rs:154-176 folds with a strict >)."""
         return int(logits.argmax().item())
 
-    def generate(self, prompt: list[int], max_new: int, stop_tokens=(), graph: bool = False) -> GenerateResult:
+    def generate(self, prompt: list[int], max_new: int, stop_tokens=(), graph: bool = False,
+                 chunk: int = 16) -> GenerateResult:
         """generate_greedy (llama_candle.rs:58-139): prefill at offset 0, then one
-        forward per new token; stops after emitting a stop token (kept in the output)."""
+        forward per new token; stops after emitting a stop token (kept in the output).
+
+        With graph=True the captured step is replayed `chunk` times back to back
+        (each replay feeds the next from device memory), then the chunk's tokens
+        are read and checked for a stop token; tokens after the first stop token
+        are dropped, so the output is the same as stepping one token at a time."""
         if max_new == 0 or len(prompt) == 0:
             return GenerateResult([], 0, 0)
         if len(prompt) + max_new - 1 > self.cfg.max_seq:
             raise ValueError("prompt + max_new exceeds max_seq")
-        torch = self.torch
         if graph and self._graph is None:
             self._capture()
         self.ctx.synchronize()
@@ -367,16 +441,32 @@ class Llama:
         generated = [nxt]
         t1 = time.perf_counter()
         offset = len(prompt)
-        for _ in range(1, max_new):
-            if nxt in stop_tokens:
-                break
-            if graph:
-                self.decode_step_graph(nxt, offset)
-                nxt = int(self._next.item())
-            else:
+        if graph and max_new > 1 and nxt not in stop_tokens:
+            self._enter()
+            with self.torch.cuda.stream(self.stream):
+                self._pos.fill_(offset)
+                self._tok.fill_(nxt)
+            done = False
+            while not done and len(generated) < max_new:
+                n = min(chunk, max_new - len(generated))
+                with self.torch.cuda.stream(self.stream):
+                    for _ in range(n):
+                        self._graph.replay()
+                    toks = self._hist[offset:offset + n].tolist()  # copies on the stream, then synchronises
+                for t in toks:
+                    generated.append(int(t))
+                    if t in stop_tokens:
+                        done = True
+                        break
+                offset += n
+            self._leave()
+        else:
+            for _ in range(1, max_new):
+                if nxt in stop_tokens:
+                    break
                 nxt = self.argmax_first(self.forward([nxt], offset))
-            generated.append(nxt)
-            offset += 1
+                generated.append(nxt)
+                offset += 1
         decode_us = int((time.perf_counter() - t1) * 1e6)
         return GenerateResult(generated, prefill_us, decode_us)
 

@@ -217,6 +217,43 @@ int aq_q8_0_dequant_row(aq_ctx *ctx, const int8_t *w, const float *scales, int64
 int aq_dequant_rows_device(aq_ctx *ctx, int weight_format, const void *d_table, const float *d_scales, int64_t n_rows,
                            const int64_t *d_rows, int64_t n_out, int64_t k, float *d_out);
 
+/* ===================================================================
+ * Decode-step glue: the f32 operations between the quantized matmuls of
+ * one Llama decode step, as candle-transformers 0.8.4 quantized_llama runs
+ * them per generated token (reached from llama_candle.rs:119; next-token
+ * pick as llama_candle.rs:154-176).  They are not QMatMul replacements: they
+ * let a caller keep the whole step on the GPU (and capture it in a HIP
+ * graph) around aq_qmatmul_f32_device.  Device pointers, asynchronous on the
+ * context stream.  f32 sums are reordered relative to candle's CPU loops
+ * (tolerance-bound, not bit-exact).
+ * =================================================================== */
+/* d_out[hidden] = row *d_tok of the f32 table [vocab][hidden] (zeros for an
+ * id outside 0..vocab-1). */
+int aq_llama_embed(aq_ctx *ctx, const float *d_table, int64_t vocab, const int64_t *d_tok, int64_t hidden,
+                   float *d_out);
+/* Per row of m rows of n: d_x += d_delta when d_delta is non-null (the
+ * residual add, written back to d_x), then
+ * d_out = d_x / sqrt(sum(d_x^2) / n + eps) * d_w (candle rms_norm). */
+int aq_llama_rmsnorm(aq_ctx *ctx, float *d_x, const float *d_delta, const float *d_w, int64_t m, int64_t n, float eps,
+                     float *d_out);
+/* d_out[i] = silu(g[i]) * u[i] for i < n, with d_gu = [g (n) | u (n)]. */
+int aq_llama_silu_mul(aq_ctx *ctx, const float *d_gu, int64_t n, float *d_out);
+/* Attention of one query position *d_pos (0 <= pos < max_seq): d_qk =
+ * [q (n_head*head_dim) | k (n_kv*head_dim)], d_v (n_kv*head_dim), before
+ * rotary embedding; d_cos / d_sin [max_seq][head_dim/2]; caches
+ * [n_kv][max_seq][head_dim] for one layer.  Rotates q and k (interleaved
+ * pairs), stores k and v at pos, and writes softmax(q.k/sqrt(head_dim)).v
+ * over positions 0..pos for each query head to d_out (n_head*head_dim).
+ * head_dim must divide 256 and be a multiple of 4; max_seq <= 8192. */
+int aq_llama_attn_decode(aq_ctx *ctx, const float *d_qk, const float *d_v, const float *d_cos, const float *d_sin,
+                         const int64_t *d_pos, float *d_kcache, float *d_vcache, int64_t n_head, int64_t n_kv,
+                         int64_t head_dim, int64_t max_seq, float *d_out);
+/* Greedy pick: the first index of the largest of d_x[0..n) goes to *d_tok
+ * and, when d_hist is non-null and 0 <= *d_pos < hist_len, to
+ * d_hist[*d_pos]; then *d_pos += 1. */
+int aq_llama_argmax(aq_ctx *ctx, const float *d_x, int64_t n, int64_t *d_tok, int64_t *d_pos, int64_t *d_hist,
+                    int64_t hist_len);
+
 #ifdef __cplusplus
 }
 #endif

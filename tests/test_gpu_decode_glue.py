@@ -1,0 +1,182 @@
+"""GPU tests of the decode-step glue kernels (k_decode.hip) through the C ABI,
+each against a numpy restatement of the candle-transformers quantized_llama
+operation it stands for (rms_norm, silu, rope_i + grouped-query attention
+over a KV cache, first-maximum argmax).  f32 sums are reordered on the GPU, so
+values are compared at 1e-5 relative; argmax and the cache writes are exact.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def env():
+    import torch
+
+    import arm_ai_amd as A
+
+    if not torch.cuda.is_available():
+        pytest.fail("GPU tests need torch to see the GPU (import torch before the library)")
+    ctx = A.Context(0)
+    yield torch, A._lib, ctx
+    ctx.close()
+
+
+def _dev(torch, a):
+    """A device copy, complete before the library's stream uses it."""
+    t = torch.from_numpy(np.ascontiguousarray(a)).to("cuda:0")
+    torch.cuda.synchronize()
+    return t
+
+
+def _rel(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.max(np.abs(a - b)) / max(np.max(np.abs(b)), 1e-30))
+
+
+def test_rmsnorm_with_and_without_residual(env):
+    torch, lib, ctx = env
+    L = lib.load()
+    rng = np.random.default_rng(0)
+    m, n, eps = 3, 2048, 1e-5
+    x = rng.standard_normal((m, n)).astype(np.float32)
+    d = rng.standard_normal((m, n)).astype(np.float32)
+    w = (1 + 0.05 * rng.standard_normal(n)).astype(np.float32)
+    dx, dd, dw = _dev(torch, x), _dev(torch, d), _dev(torch, w)
+    out = torch.empty((m, n), dtype=torch.float32, device="cuda:0")
+    torch.cuda.synchronize()
+    lib.check(L.aq_llama_rmsnorm(ctx.handle, dx.data_ptr(), None, dw.data_ptr(), m, n, ctypes.c_float(eps),
+                                 out.data_ptr()))
+    ctx.synchronize()
+    ms = np.mean(x.astype(np.float64) ** 2, axis=-1, keepdims=True)
+    assert _rel(out.cpu().numpy(), x / np.sqrt(ms + eps) * w) <= 1e-5
+    assert np.array_equal(dx.cpu().numpy(), x)  # no delta: x untouched
+    lib.check(L.aq_llama_rmsnorm(ctx.handle, dx.data_ptr(), dd.data_ptr(), dw.data_ptr(), m, n, ctypes.c_float(eps),
+                                 out.data_ptr()))
+    ctx.synchronize()
+    h = x + d
+    assert np.array_equal(dx.cpu().numpy(), h)  # the residual add is written back exactly
+    ms = np.mean(h.astype(np.float64) ** 2, axis=-1, keepdims=True)
+    assert _rel(out.cpu().numpy(), h / np.sqrt(ms + eps) * w) <= 1e-5
+
+
+def test_silu_mul(env):
+    torch, lib, ctx = env
+    L = lib.load()
+    rng = np.random.default_rng(1)
+    n = 5632
+    gu = (4 * rng.standard_normal(2 * n)).astype(np.float32)
+    gu[0], gu[1] = -100.0, 100.0  # exp overflow / underflow ends
+    dgu = _dev(torch, gu)
+    out = torch.empty(n, dtype=torch.float32, device="cuda:0")
+    lib.check(L.aq_llama_silu_mul(ctx.handle, dgu.data_ptr(), n, out.data_ptr()))
+    ctx.synchronize()
+    g, u = gu[:n].astype(np.float64), gu[n:].astype(np.float64)
+    want = g / (1 + np.exp(-g)) * u
+    got = out.cpu().numpy()
+    assert np.all(np.isfinite(got))
+    assert _rel(got, want) <= 1e-5
+
+
+def _rope(x, c, s):
+    out = np.empty_like(x)
+    a, b = x[..., 0::2], x[..., 1::2]
+    out[..., 0::2] = a * c - b * s
+    out[..., 1::2] = a * s + b * c
+    return out
+
+
+@pytest.mark.parametrize("n_head,n_kv,hd,pos", [(32, 4, 64, 0), (32, 4, 64, 517), (8, 8, 128, 300), (4, 2, 32, 1023)])
+def test_attn_decode_against_numpy(env, n_head, n_kv, hd, pos):
+    torch, lib, ctx = env
+    L = lib.load()
+    rng = np.random.default_rng(pos + hd)
+    max_seq = 1024
+    qk = rng.standard_normal((n_head + n_kv) * hd).astype(np.float32)
+    v = rng.standard_normal(n_kv * hd).astype(np.float32)
+    kc = rng.standard_normal((n_kv, max_seq, hd)).astype(np.float32)
+    vc = rng.standard_normal((n_kv, max_seq, hd)).astype(np.float32)
+    theta = 1.0 / (10000.0 ** (np.arange(0, hd, 2, dtype=np.float32) / hd))
+    ang = np.arange(max_seq, dtype=np.float32)[:, None] * theta[None, :]
+    cos, sin = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+    dqk, dv, dkc, dvc = _dev(torch, qk), _dev(torch, v), _dev(torch, kc), _dev(torch, vc)
+    dcos, dsin = _dev(torch, cos), _dev(torch, sin)
+    dpos = torch.tensor([pos], dtype=torch.int64, device="cuda:0")
+    out = torch.empty(n_head * hd, dtype=torch.float32, device="cuda:0")
+    torch.cuda.synchronize()
+    lib.check(L.aq_llama_attn_decode(ctx.handle, dqk.data_ptr(), dv.data_ptr(), dcos.data_ptr(), dsin.data_ptr(),
+                                     dpos.data_ptr(), dkc.data_ptr(), dvc.data_ptr(), n_head, n_kv, hd, max_seq,
+                                     out.data_ptr()))
+    ctx.synchronize()
+    q = _rope(qk[:n_head * hd].reshape(n_head, hd), cos[pos], sin[pos])
+    k = _rope(qk[n_head * hd:].reshape(n_kv, hd), cos[pos], sin[pos])
+    kc2, vc2 = kc.copy(), vc.copy()
+    kc2[:, pos], vc2[:, pos] = k, v.reshape(n_kv, hd)
+    rep = n_head // n_kv
+    want = np.empty((n_head, hd))
+    for h in range(n_head):
+        kk = kc2[h // rep, :pos + 1].astype(np.float64)
+        s = kk @ q[h].astype(np.float64) / np.sqrt(hd)
+        p = np.exp(s - s.max())
+        p /= p.sum()
+        want[h] = p @ vc2[h // rep, :pos + 1].astype(np.float64)
+    assert _rel(out.cpu().numpy().reshape(n_head, hd), want) <= 1e-5
+    # k, v stored at pos; every other cache entry untouched
+    assert np.array_equal(dkc.cpu().numpy()[:, pos], k)
+    assert np.array_equal(dvc.cpu().numpy(), vc2)
+    got_k = dkc.cpu().numpy()
+    got_k[:, pos] = kc[:, pos]
+    assert np.array_equal(got_k, kc)
+
+
+def test_argmax_first_max_history_and_position(env):
+    torch, lib, ctx = env
+    L = lib.load()
+    rng = np.random.default_rng(2)
+    x = rng.standard_normal(32000).astype(np.float32)
+    x[777] = x[31000] = 50.0  # tie: the first index wins
+    x[5] = np.nan  # a NaN never wins
+    dx = _dev(torch, x)
+    tok = torch.zeros(1, dtype=torch.int64, device="cuda:0")
+    pos = torch.tensor([10], dtype=torch.int64, device="cuda:0")
+    hist = torch.full((16,), -1, dtype=torch.int64, device="cuda:0")
+    torch.cuda.synchronize()
+    lib.check(L.aq_llama_argmax(ctx.handle, dx.data_ptr(), x.size, tok.data_ptr(), pos.data_ptr(), hist.data_ptr(), 16))
+    ctx.synchronize()
+    assert int(tok.item()) == 777
+    assert int(pos.item()) == 11
+    h = hist.cpu().numpy()
+    assert h[10] == 777 and np.all(np.delete(h, 10) == -1)
+
+
+def test_embed_lookup_and_out_of_range(env):
+    torch, lib, ctx = env
+    L = lib.load()
+    rng = np.random.default_rng(3)
+    table = rng.standard_normal((100, 64)).astype(np.float32)
+    dt = _dev(torch, table)
+    out = torch.empty(64, dtype=torch.float32, device="cuda:0")
+    for t, want in ((42, table[42]), (100, np.zeros(64, np.float32)), (-1, np.zeros(64, np.float32))):
+        tok = torch.tensor([t], dtype=torch.int64, device="cuda:0")
+        torch.cuda.synchronize()
+        lib.check(L.aq_llama_embed(ctx.handle, dt.data_ptr(), 100, tok.data_ptr(), 64, out.data_ptr()))
+        ctx.synchronize()
+        assert np.array_equal(out.cpu().numpy(), want)
+
+
+def test_glue_argument_errors(env):
+    torch, lib, ctx = env
+    L = lib.load()
+    buf = torch.zeros(1024, dtype=torch.float32, device="cuda:0")
+    pos = torch.zeros(1, dtype=torch.int64, device="cuda:0")
+    p = buf.data_ptr()
+    # head_dim that does not divide the workgroup, n_head not a multiple of n_kv, max_seq too large
+    for n_head, n_kv, hd, ms in ((4, 2, 48, 16), (6, 4, 64, 16), (4, 2, 64, 9000)):
+        rc = L.aq_llama_attn_decode(ctx.handle, p, p, p, p, pos.data_ptr(), p, p, n_head, n_kv, hd, ms, p)
+        assert rc != 0
+    assert L.aq_llama_silu_mul(ctx.handle, None, 4, p) != 0
+    assert L.aq_llama_argmax(ctx.handle, p, 0, pos.data_ptr(), pos.data_ptr(), None, 0) != 0
