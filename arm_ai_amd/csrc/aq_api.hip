@@ -878,3 +878,26 @@ int aq_llama_argmax(aq_ctx *ctx, const float *d_x, int64_t n, int64_t *d_tok, in
     if (rc) return rc;
     return hip_status(launch_argmax(d_x, n, d_tok, d_pos, d_hist, hist_len, ctx->stream), "argmax");
 }
+
+int aq_qmatmul_rmsnorm_f32_device(aq_ctx *ctx, const aq_qweight *w, const float *d_x, const float *d_delta,
+                                  const float *d_norm_w, float eps, int64_t k, float *d_h_out, float *d_dst) {
+    int rc = check_mm(ctx, w, 1, k);
+    if (rc) return rc;
+    if (!d_x || !d_norm_w || !d_dst) return fail(AQ_ERR_INVALID_ARG, "null pointer");
+    if (d_h_out && (d_h_out == d_x || d_h_out == d_delta)) return fail(AQ_ERR_INVALID_ARG, "d_h_out aliases an input");
+    if ((rc = use_device(ctx->device))) return rc;
+    const hipError_t e = launch_matvec_rmsnorm(w->layout, w->n, w->k, d_x, d_delta, d_norm_w, eps, d_h_out, d_dst,
+                                               ctx->stream);
+    if (e == hipErrorNotSupported) return fail(AQ_ERR_SHAPE, "k=%lld is too long for the fused norm", (long long)k);
+    return hip_status(e, "matvec rmsnorm");
+}
+
+int aq_qmatmul_silu_mul_f32_device(aq_ctx *ctx, const aq_qweight *w, const float *d_gu, int64_t k, float *d_dst) {
+    int rc = check_mm(ctx, w, 1, k);
+    if (rc) return rc;
+    if (!d_gu || !d_dst) return fail(AQ_ERR_INVALID_ARG, "null pointer");
+    if ((rc = use_device(ctx->device))) return rc;
+    const hipError_t e = launch_matvec_silu(w->layout, w->n, w->k, d_gu, d_dst, ctx->stream);
+    if (e == hipErrorNotSupported) return fail(AQ_ERR_SHAPE, "k=%lld is larger than the matvec supports", (long long)k);
+    return hip_status(e, "matvec silu");
+}

@@ -153,6 +153,14 @@ hipError_t launch_dequantize_q6_k_crate(const uint8_t *blocks, int64_t nel, floa
 hipError_t launch_dequant_rows(int wt, const void *table, const float *scales, int64_t ntab, const int64_t *rows,
                                int64_t nr, int64_t k, float *out, hipStream_t s);
 
+// Decode matvec (m = 1, f32 input) with a fused input transform (k_matvec.hip):
+// rms_norm(x + delta) * norm (workgroup 0 also writes x + delta to xout), or
+// silu(g) * u with gu = [g (k) | u (k)].  hipErrorNotSupported when the row
+// is too long for the fused norm (the caller then runs the two steps apart).
+hipError_t launch_matvec_rmsnorm(const WLayout &w, int64_t n, int64_t k, const float *x, const float *delta,
+                                 const float *norm, float eps, float *xout, float *y, hipStream_t s);
+hipError_t launch_matvec_silu(const WLayout &w, int64_t n, int64_t k, const float *gu, float *y, hipStream_t s);
+
 // Decode-step glue (k_decode.hip).
 hipError_t launch_embed(const float *table, int64_t vocab, const int64_t *d_tok, int64_t hidden, float *out,
                         hipStream_t s);

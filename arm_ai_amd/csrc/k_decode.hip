@@ -21,61 +21,99 @@ namespace aq {
 
 namespace {
 
-constexpr int DEC_THREADS = 256;
+constexpr int DEC_THREADS = 256;   // row kernels (embedding, RMSNorm, SiLU)
+constexpr int WIDE_THREADS = 1024; // one-workgroup kernels that stream a long vector (attention, argmax)
 
-// sum over a 256-thread block; every thread gets the result.  red: >= 4 floats of LDS.
+// Sum / max over a block of NT threads (NT/64 wavefronts); every thread gets
+// the result.  red: NT/64 floats of LDS.  The leading barrier lets red be
+// reused by consecutive calls; the trailing one publishes it (and any LDS
+// written before the call).
+template <int NT>
 __device__ __forceinline__ float block_sum(float v, float *red) {
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
-    const int w = threadIdx.x >> 6;
-    __syncthreads();  // red may still be read by a previous call
-    if ((threadIdx.x & 63) == 0) red[w] = v;
     __syncthreads();
-    return (red[0] + red[1]) + (red[2] + red[3]);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float s = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NT / 64; w++) s += red[w];
+    return s;
 }
-
+template <int NT>
 __device__ __forceinline__ float block_max(float v, float *red) {
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-    const int w = threadIdx.x >> 6;
     __syncthreads();
-    if ((threadIdx.x & 63) == 0) red[w] = v;
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
     __syncthreads();
-    return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    float s = red[0];
+#pragma unroll
+    for (int w = 1; w < NT / 64; w++) s = fmaxf(s, red[w]);
+    return s;
 }
 
-// out[row] = embedding row *d_tok (a token id outside [0, vocab) gives zeros).
+// out = embedding row *d_tok (a token id outside [0, vocab) gives zeros).
+// hidden % 4 == 0 (checked by the launcher): float4 copies.
 __global__ __launch_bounds__(DEC_THREADS) void embed_kernel(const float *__restrict__ table, int64_t vocab,
                                                             const int64_t *__restrict__ d_tok, int hidden,
                                                             float *__restrict__ out) {
     const int64_t t = *d_tok;
     const bool ok = t >= 0 && t < vocab;
-    for (int i = threadIdx.x; i < hidden; i += DEC_THREADS) out[i] = ok ? table[t * hidden + i] : 0.0f;
+    const float4 *src = (const float4 *)(table + (ok ? t : 0) * hidden);
+    for (int i = threadIdx.x; i < hidden / 4; i += DEC_THREADS)
+        ((float4 *)out)[i] = ok ? src[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 }
 
 // One row per workgroup: x += delta (when delta is given, written back to x:
-// the residual stream), then out = x / sqrt(sum(x^2)/n + eps) * w.
+// the residual stream), then out = x / sqrt(sum(x^2)/n + eps) * w.  The row
+// (n % 4 == 0, n <= 4 * RMS_V * DEC_THREADS) is held in registers, so x is
+// read once and every load is issued before the first use.
+constexpr int RMS_V = 8;
 __global__ __launch_bounds__(DEC_THREADS) void rmsnorm_kernel(float *__restrict__ x, const float *__restrict__ delta,
                                                               const float *__restrict__ w, int n, float eps,
                                                               float *__restrict__ out) {
-    __shared__ float red[4];
-    float *xr = x + (int64_t)blockIdx.x * n;
-    const float *dr = delta ? delta + (int64_t)blockIdx.x * n : nullptr;
-    float *orow = out + (int64_t)blockIdx.x * n;
-    float ss = 0.0f;
-    for (int i = threadIdx.x; i < n; i += DEC_THREADS) {
-        float v = xr[i];
-        if (dr) {
-            v += dr[i];
-            xr[i] = v;
-        }
-        ss = __builtin_fmaf(v, v, ss);
+    __shared__ float red[DEC_THREADS / 64];
+    float4 *xr = (float4 *)(x + (int64_t)blockIdx.x * n);
+    const float4 *dr = delta ? (const float4 *)(delta + (int64_t)blockIdx.x * n) : nullptr;
+    float4 *orow = (float4 *)(out + (int64_t)blockIdx.x * n);
+    const float4 *w4 = (const float4 *)w;
+    const int n4 = n / 4;
+    float4 v[RMS_V], d[RMS_V];
+#pragma unroll
+    for (int j = 0; j < RMS_V; j++) {
+        const int i = threadIdx.x + j * DEC_THREADS;
+        v[j] = i < n4 ? xr[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        d[j] = (dr && i < n4) ? dr[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
-    const float m = sqrtf(block_sum(ss, red) / (float)n + eps);
-    for (int i = threadIdx.x; i < n; i += DEC_THREADS) orow[i] = (xr[i] / m) * w[i];
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < RMS_V; j++) {
+        const int i = threadIdx.x + j * DEC_THREADS;
+        if (dr) {
+            v[j].x += d[j].x;
+            v[j].y += d[j].y;
+            v[j].z += d[j].z;
+            v[j].w += d[j].w;
+            if (i < n4) xr[i] = v[j];
+        }
+        ss = __builtin_fmaf(v[j].x, v[j].x, ss);
+        ss = __builtin_fmaf(v[j].y, v[j].y, ss);
+        ss = __builtin_fmaf(v[j].z, v[j].z, ss);
+        ss = __builtin_fmaf(v[j].w, v[j].w, ss);
+    }
+    const float m = sqrtf(block_sum<DEC_THREADS>(ss, red) / (float)n + eps);
+#pragma unroll
+    for (int j = 0; j < RMS_V; j++) {
+        const int i = threadIdx.x + j * DEC_THREADS;
+        if (i < n4) {
+            const float4 ww = w4[i];
+            orow[i] = make_float4((v[j].x / m) * ww.x, (v[j].y / m) * ww.y, (v[j].z / m) * ww.z, (v[j].w / m) * ww.w);
+        }
+    }
 }
 
-// out = silu(g) * u.  gu = [g (n) | u (n)] per row (the merged w1|w3 output).
+// out = silu(g) * u.  gu = [g (n) | u (n)] (the merged w1|w3 output).
 __global__ __launch_bounds__(DEC_THREADS) void silu_mul_kernel(const float *__restrict__ gu, int64_t n,
                                                                float *__restrict__ out) {
     const int64_t i = (int64_t)blockIdx.x * DEC_THREADS + threadIdx.x;
@@ -84,32 +122,42 @@ __global__ __launch_bounds__(DEC_THREADS) void silu_mul_kernel(const float *__re
     out[i] = (g / (1.0f + expf(-g))) * gu[n + i];
 }
 
-// Attention for one query position at *d_pos, one workgroup per query head.
-// qk = [q (n_head*hd) | k (n_kv*hd)] before rotation, v (n_kv*hd); the
-// caches are [n_kv][max_seq][hd] for this layer.  Each workgroup rotates its
-// q head and its group's k (rope_i: pairs (2i, 2i+1) by pos * theta_i, from
-// the cos/sin tables [max_seq][hd/2]); the first workgroup of each group
-// stores the rotated k and v at pos for later steps, and every workgroup uses
-// its own registers for position pos, so no workgroup waits for another.
+// Attention for one query position at *d_pos, one 1024-thread workgroup per
+// query head.  qk = [q (n_head*hd) | k (n_kv*hd)] before rotation, v
+// (n_kv*hd); the caches are [n_kv][max_seq][hd] for this layer.  Each
+// workgroup rotates its q head and its group's k (rope_i: pairs (2i, 2i+1) by
+// pos * theta_i, from the cos/sin tables [max_seq][hd/2]); the first
+// workgroup of each group stores the rotated k and v at pos for later steps,
+// and every workgroup uses its own LDS copy for position pos, so no
+// workgroup waits for another.
+//   scores: one position per thread (q broadcast from LDS, k_p as float4s);
+//   softmax: block max, exp, block sum, p = e / sum;
+//   output: thread (d4, g) sums positions p = g (mod 4096/hd) of p * v_p[d]
+//     for four consecutive d (float4 reads, four positions in flight), the
+//     groups' partials then summed in LDS in two levels.
 constexpr int ATT_MAX_SEQ = 8192;
 constexpr int ATT_MAX_HD = 256;
-__global__ __launch_bounds__(DEC_THREADS) void attn_decode_kernel(
+__global__ __launch_bounds__(WIDE_THREADS) void attn_decode_kernel(
     const float *__restrict__ qk, const float *__restrict__ v, const float *__restrict__ cosb,
     const float *__restrict__ sinb, const int64_t *__restrict__ d_pos, float *__restrict__ kc, float *__restrict__ vc,
     int n_head, int n_kv, int hd, int max_seq, float *__restrict__ out) {
-    __shared__ float qs[ATT_MAX_HD], ks[ATT_MAX_HD], vs[ATT_MAX_HD];
+    __shared__ __align__(16) float qs[ATT_MAX_HD];
+    __shared__ __align__(16) float ks[ATT_MAX_HD];
+    __shared__ __align__(16) float vs[ATT_MAX_HD];
     __shared__ float sc[ATT_MAX_SEQ];
-    __shared__ float red[4];
-    __shared__ float part[DEC_THREADS];
-    const int head = blockIdx.x, tid = threadIdx.x;
+    __shared__ float red[WIDE_THREADS / 64];
+    __shared__ float4 part4[WIDE_THREADS];
+    __shared__ float4 sc4[16 * ATT_MAX_HD / 4];
+    const int head = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int rep = n_head / n_kv, kvh = head / rep;
-    const int64_t pos = *d_pos;
-    if (pos < 0 || pos >= max_seq) return;  // the host checks; never index out of the cache
+    const int pos = (int)*d_pos;
+    if (pos < 0 || pos >= max_seq) return;  // uniform; the host checks, this never indexes out of the cache
     const float *q0 = qk + (int64_t)head * hd;
     const float *k0 = qk + (int64_t)n_head * hd + (int64_t)kvh * hd;
     const float *v0 = v + (int64_t)kvh * hd;
-    const float *cr = cosb + pos * (hd / 2), *sr = sinb + pos * (hd / 2);
-    for (int i = tid; i < hd / 2; i += DEC_THREADS) {
+    const float *cr = cosb + (int64_t)pos * (hd / 2), *sr = sinb + (int64_t)pos * (hd / 2);
+    if (tid < hd / 2) {
+        const int i = tid;
         const float c = cr[i], s = sr[i];
         const float a = q0[2 * i], b = q0[2 * i + 1];
         qs[2 * i] = a * c - b * s;
@@ -117,84 +165,136 @@ __global__ __launch_bounds__(DEC_THREADS) void attn_decode_kernel(
         const float ka = k0[2 * i], kb = k0[2 * i + 1];
         ks[2 * i] = ka * c - kb * s;
         ks[2 * i + 1] = ka * s + kb * c;
+    } else if (tid >= 512 && tid < 512 + hd) {
+        vs[tid - 512] = v0[tid - 512];
     }
-    for (int i = tid; i < hd; i += DEC_THREADS) vs[i] = v0[i];
     __syncthreads();
     float *kh = kc + (int64_t)kvh * max_seq * hd;
     float *vh = vc + (int64_t)kvh * max_seq * hd;
-    if (head % rep == 0)
-        for (int i = tid; i < hd; i += DEC_THREADS) {
-            kh[pos * hd + i] = ks[i];
-            vh[pos * hd + i] = vs[i];
-        }
-    // scores q . k_p / sqrt(hd) for p = 0..pos (k_pos from LDS)
+    if (head % rep == 0 && tid < hd) {
+        kh[(int64_t)pos * hd + tid] = ks[tid];
+        vh[(int64_t)pos * hd + tid] = vs[tid];
+    }
+    // scores q . k_p / sqrt(hd), p = 0..pos (k_pos from LDS): one position per
+    // thread, q read from LDS by broadcast, k_p as hd/4 float4 loads
     const float rs = sqrtf((float)hd);
     float mx = -INFINITY;
-    for (int64_t p = tid; p <= pos; p += DEC_THREADS) {
-        const float *kp = p == pos ? ks : kh + p * hd;
-        float d = 0.0f;
-        for (int i = 0; i < hd; i += 4) {
-            const float4 kv4 = *(const float4 *)(kp + i);
-            d = __builtin_fmaf(qs[i], kv4.x, d);
-            d = __builtin_fmaf(qs[i + 1], kv4.y, d);
-            d = __builtin_fmaf(qs[i + 2], kv4.z, d);
-            d = __builtin_fmaf(qs[i + 3], kv4.w, d);
+    for (int p = tid; p <= pos; p += WIDE_THREADS) {
+        const float4 *kp = (const float4 *)(p == pos ? ks : kh + (int64_t)p * hd);
+        const float4 *q4 = (const float4 *)qs;
+        float d0 = 0.0f, d1 = 0.0f;
+        for (int i = 0; i < hd / 4; i += 2) {
+            const float4 a0 = kp[i], a1 = kp[i + 1];
+            const float4 b0 = q4[i], b1 = q4[i + 1];
+            d0 = __builtin_fmaf(b0.x, a0.x, __builtin_fmaf(b0.y, a0.y, __builtin_fmaf(b0.z, a0.z, __builtin_fmaf(b0.w, a0.w, d0))));
+            d1 = __builtin_fmaf(b1.x, a1.x, __builtin_fmaf(b1.y, a1.y, __builtin_fmaf(b1.z, a1.z, __builtin_fmaf(b1.w, a1.w, d1))));
         }
-        const float s = d / rs;
-        sc[p] = s;
-        mx = fmaxf(mx, s);
+        const float sv = (d0 + d1) / rs;
+        sc[p] = sv;
+        mx = fmaxf(mx, sv);
     }
-    mx = block_max(mx, red);
+    mx = block_max<WIDE_THREADS>(mx, red);  // its barriers publish sc[]
     float sum = 0.0f;
-    for (int64_t p = tid; p <= pos; p += DEC_THREADS) {
+    for (int p = tid; p <= pos; p += WIDE_THREADS) {
         const float e = expf(sc[p] - mx);
         sc[p] = e;
         sum += e;
     }
-    sum = block_sum(sum, red);  // its barriers also publish sc[]
-    // out[d] = sum_p (e_p / sum) v_p[d]: thread (d, g) takes positions p = g mod groups
-    const int groups = DEC_THREADS / hd;
-    const int d = tid % hd, g = tid / hd;
-    float acc = 0.0f;
-    if (g < groups)
-        for (int64_t p = g; p <= pos; p += groups) {
-            const float vv = p == pos ? vs[d] : vh[p * hd + d];
-            acc = __builtin_fmaf(sc[p] / sum, vv, acc);
+    sum = block_sum<WIDE_THREADS>(sum, red);
+    for (int p = tid; p <= pos; p += WIDE_THREADS) sc[p] = sc[p] / sum;
+    __syncthreads();
+    // output: thread (d4, g) takes dims 4*d4..4*d4+3 of positions p = g (mod G)
+    constexpr int SU = 4;  // positions per thread with loads in flight together
+    const int nd4 = hd / 4, G = WIDE_THREADS / nd4;
+    const int d4 = tid % nd4, g = tid / nd4;
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (int p0 = g; p0 <= pos; p0 += SU * G) {
+        float4 v4[SU];
+#pragma unroll
+        for (int u = 0; u < SU; u++) {
+            const int p = p0 + u * G;
+            v4[u] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if (p < pos) v4[u] = *(const float4 *)(vh + (int64_t)p * hd + 4 * d4);
+            else if (p == pos) v4[u] = *(const float4 *)(vs + 4 * d4);
         }
-    part[tid] = acc;
+#pragma unroll
+        for (int u = 0; u < SU; u++) {
+            const int p = p0 + u * G;
+            const float w = p <= pos ? sc[p] : 0.0f;
+            acc.x = __builtin_fmaf(w, v4[u].x, acc.x);
+            acc.y = __builtin_fmaf(w, v4[u].y, acc.y);
+            acc.z = __builtin_fmaf(w, v4[u].z, acc.z);
+            acc.w = __builtin_fmaf(w, v4[u].w, acc.w);
+        }
+    }
+    part4[tid] = acc;
+    __syncthreads();
+    // sum the G groups: 16 threads per float4 column first add G/16 groups each
+    // (G is a multiple of 16: hd <= 256), then 64-thread columns add the 16 results
+    if (tid < 16 * nd4) {
+        const int c4 = tid % nd4, sl = tid / nd4, per = G / 16;
+        float4 t = part4[(sl * per) * nd4 + c4];
+        for (int j = 1; j < per; j++) {
+            const float4 u4 = part4[(sl * per + j) * nd4 + c4];
+            t.x += u4.x;
+            t.y += u4.y;
+            t.z += u4.z;
+            t.w += u4.w;
+        }
+        sc4[tid] = t;
+    }
     __syncthreads();
     if (tid < hd) {
+        const int dd = tid >> 2, c = tid & 3;
         float o = 0.0f;
-        for (int j = 0; j < groups; j++) o += part[j * hd + tid];
+        for (int sl = 0; sl < 16; sl++) {
+            const float4 t4 = sc4[sl * nd4 + dd];
+            o += c == 0 ? t4.x : c == 1 ? t4.y : c == 2 ? t4.z : t4.w;
+        }
         out[(int64_t)head * hd + tid] = o;
     }
 }
 
 // Greedy pick: the first index of the largest value (a NaN never wins; all
 // NaN gives 0).  Writes it to *d_tok (the next step's input), to
-// hist[*d_pos] when hist is given, and advances *d_pos by one.
-__global__ __launch_bounds__(DEC_THREADS) void argmax_kernel(const float *__restrict__ x, int n,
-                                                             int64_t *__restrict__ d_tok, int64_t *__restrict__ d_pos,
-                                                             int64_t *__restrict__ hist, int64_t hist_len) {
-    __shared__ float bv[4];
-    __shared__ int bi[4];
+// hist[*d_pos] when hist is given, and advances *d_pos by one.  One
+// 1024-thread workgroup, float4 loads (n % 4 == 0), several in flight.
+__device__ __forceinline__ void better(float v, int i, float &best, int &idx) {
+    if (v > best || (v == best && i < idx)) {  // NaN compares false
+        best = v;
+        idx = i;
+    }
+}
+__global__ __launch_bounds__(WIDE_THREADS) void argmax_kernel(const float *__restrict__ x, int n,
+                                                              int64_t *__restrict__ d_tok, int64_t *__restrict__ d_pos,
+                                                              int64_t *__restrict__ hist, int64_t hist_len) {
+    __shared__ float bv[WIDE_THREADS / 64];
+    __shared__ int bi[WIDE_THREADS / 64];
     float best = -INFINITY;
     int idx = 0x7fffffff;
-    for (int i = threadIdx.x; i < n; i += DEC_THREADS) {
-        const float v = x[i];
-        if (v > best || (v == best && i < idx)) {  // NaN compares false
-            best = v;
-            idx = i;
+    const float4 *x4 = (const float4 *)x;
+    const int n4 = n / 4;
+    for (int i0 = threadIdx.x; i0 < n4; i0 += 4 * WIDE_THREADS) {
+        float4 v[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int i = i0 + u * WIDE_THREADS;
+            v[u] = i < n4 ? x4[i] : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int i = 4 * (i0 + u * WIDE_THREADS);
+            better(v[u].x, i, best, idx);
+            better(v[u].y, i + 1, best, idx);
+            better(v[u].z, i + 2, best, idx);
+            better(v[u].w, i + 3, best, idx);
         }
     }
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) {
         const float ov = __shfl_xor(best, o);
         const int oi = __shfl_xor(idx, o);
-        if (ov > best || (ov == best && oi < idx)) {
-            best = ov;
-            idx = oi;
-        }
+        better(ov, oi, best, idx);
     }
     if ((threadIdx.x & 63) == 0) {
         bv[threadIdx.x >> 6] = best;
@@ -202,11 +302,7 @@ __global__ __launch_bounds__(DEC_THREADS) void argmax_kernel(const float *__rest
     }
     __syncthreads();
     if (threadIdx.x == 0) {
-        for (int w = 1; w < 4; w++)
-            if (bv[w] > best || (bv[w] == best && bi[w] < idx)) {
-                best = bv[w];
-                idx = bi[w];
-            }
+        for (int w = 1; w < WIDE_THREADS / 64; w++) better(bv[w], bi[w], best, idx);
         if (idx == 0x7fffffff) idx = 0;
         const int64_t pos = *d_pos;
         *d_tok = idx;
@@ -219,14 +315,16 @@ __global__ __launch_bounds__(DEC_THREADS) void argmax_kernel(const float *__rest
 
 hipError_t launch_embed(const float *table, int64_t vocab, const int64_t *d_tok, int64_t hidden, float *out,
                         hipStream_t s) {
-    if (!table || !d_tok || !out || vocab <= 0 || hidden <= 0 || hidden > 0x7fffffff) return hipErrorInvalidValue;
+    if (!table || !d_tok || !out || vocab <= 0 || hidden <= 0 || hidden % 4 || hidden > 0x7fffffff)
+        return hipErrorInvalidValue;
     embed_kernel<<<1, DEC_THREADS, 0, s>>>(table, vocab, d_tok, (int)hidden, out);
     return hipGetLastError();
 }
 
 hipError_t launch_rmsnorm(float *x, const float *delta, const float *w, int64_t m, int64_t n, float eps, float *out,
                           hipStream_t s) {
-    if (!x || !w || !out || m <= 0 || n <= 0 || n > 0x7fffffff || m > 0x7fffffff) return hipErrorInvalidValue;
+    if (!x || !w || !out || m <= 0 || n <= 0 || n % 4 || n > 4 * RMS_V * DEC_THREADS || m > 0x7fffffff)
+        return hipErrorInvalidValue;
     rmsnorm_kernel<<<(unsigned)m, DEC_THREADS, 0, s>>>(x, delta, w, (int)n, eps, out);
     return hipGetLastError();
 }
@@ -241,18 +339,19 @@ hipError_t launch_attn_decode(const float *qk, const float *v, const float *cosb
                               const int64_t *d_pos, float *kc, float *vc, int64_t n_head, int64_t n_kv, int64_t hd,
                               int64_t max_seq, float *out, hipStream_t s) {
     if (!qk || !v || !cosb || !sinb || !d_pos || !kc || !vc || !out) return hipErrorInvalidValue;
-    if (n_head <= 0 || n_kv <= 0 || n_head % n_kv || hd <= 0 || hd % 4 || hd > ATT_MAX_HD || DEC_THREADS % hd ||
+    // hd: a multiple of 8 whose quarter is a power of two (lanes per position), dividing the workgroup
+    if (n_head <= 0 || n_kv <= 0 || n_head % n_kv || hd < 8 || hd > ATT_MAX_HD || (hd / 4) & (hd / 4 - 1) || hd % 4 ||
         max_seq <= 0 || max_seq > ATT_MAX_SEQ)
         return hipErrorInvalidValue;
-    attn_decode_kernel<<<(unsigned)n_head, DEC_THREADS, 0, s>>>(qk, v, cosb, sinb, d_pos, kc, vc, (int)n_head,
+    attn_decode_kernel<<<(unsigned)n_head, WIDE_THREADS, 0, s>>>(qk, v, cosb, sinb, d_pos, kc, vc, (int)n_head,
                                                                 (int)n_kv, (int)hd, (int)max_seq, out);
     return hipGetLastError();
 }
 
 hipError_t launch_argmax(const float *x, int64_t n, int64_t *d_tok, int64_t *d_pos, int64_t *hist, int64_t hist_len,
                          hipStream_t s) {
-    if (!x || !d_tok || !d_pos || n <= 0 || n > 0x7fffffff) return hipErrorInvalidValue;
-    argmax_kernel<<<1, DEC_THREADS, 0, s>>>(x, (int)n, d_tok, d_pos, hist, hist_len);
+    if (!x || !d_tok || !d_pos || n <= 0 || n % 4 || n > 0x7fffffff) return hipErrorInvalidValue;
+    argmax_kernel<<<1, WIDE_THREADS, 0, s>>>(x, (int)n, d_tok, d_pos, hist, hist_len);
     return hipGetLastError();
 }
 

@@ -45,6 +45,13 @@ struct MvParams {
     int64_t rb_stride;
     int n, k, ng, nch, np, rbw, nw, nsub, m, iters;  // np: wavefronts per row block, nsub: chunks per wavefront
     const float *x;      // fused: f32 [m][k] of this pass, or null
+    // fused input transforms (m = 1; the XF template argument selects one):
+    //   XF_NORM: quantise rms_norm(x + xdelta) * xnorm, and workgroup 0 writes
+    //            x + xdelta to xout (xdelta, xout may be null);
+    //   XF_SILU: x = [g (k) | u (k)]: quantise silu(g) * u.
+    const float *xdelta, *xnorm;
+    float *xout;
+    float eps;
     ActPlanes act;       // pre-quantised planes of this pass (when x is null)
     float *y;            // [m][n] of this pass
     int32_t *S, *Smin;   // [m][n][blocks] of this pass, or null
@@ -275,14 +282,18 @@ __device__ __forceinline__ void group_dot(const Wt<TYPE> &W, const uint8_t *lds,
 constexpr int NW = 8;    // wavefronts per workgroup, at most
 constexpr int PRE = 4;   // records per wave whose loads precede the weight loads
 
+constexpr int XF_NONE = 0, XF_NORM = 1, XF_SILU = 2;
+
 struct ActStage {
     u32x4 q[PRE];   // f32 inputs (fused) or quant bytes / bsums (pre-quantised)
+    u32x4 q2[PRE];  // XF_NORM: the residual delta; XF_SILU: u
+    u32x4 q3[PRE];  // XF_NORM: the norm weight
     float dsc[PRE];
 };
 
 // Record t = (batch row b, group g) of this pass.  Every lane issues the same
 // loads whatever t is (records past the end read zeros).
-template <int TYPE, bool FUSED>
+template <int TYPE, bool FUSED, int XF = XF_NONE>
 __device__ __forceinline__ void rec_load(ActStage &st, int r, const MvParams &p, int t, int lane) {
     const int ng = p.ng, k = p.k, m = p.m;
     const bool ok = t < m * ng;
@@ -297,6 +308,15 @@ __device__ __forceinline__ void rec_load(ActStage &st, int r, const MvParams &p,
             off = ok && (8 * g + j) * QK8_0 < k ? (uint32_t)((b * k + (8 * g + j) * QK8_0 + 4 * sub) * 4) : BUF_OOB;
         }
         st.q[r] = __builtin_amdgcn_raw_buffer_load_b128(rx, off, 0, 0);
+        if (XF == XF_NORM) {  // m = 1: the same offsets address delta and the norm weight
+            const rsrc_t rdl = buf_rsrc(p.xdelta, p.xdelta ? (uint32_t)(k * 4) : 0u);
+            const rsrc_t rnw = buf_rsrc(p.xnorm, (uint32_t)(k * 4));
+            st.q2[r] = __builtin_amdgcn_raw_buffer_load_b128(rdl, off, 0, 0);
+            st.q3[r] = __builtin_amdgcn_raw_buffer_load_b128(rnw, off, 0, 0);
+        } else if (XF == XF_SILU) {
+            const rsrc_t ru = buf_rsrc(p.x + k, (uint32_t)(k * 4));
+            st.q2[r] = __builtin_amdgcn_raw_buffer_load_b128(ru, off, 0, 0);
+        }
     } else if (TYPE != TYPE_Q8_0) {
         const rsrc_t rq = buf_rsrc(p.act.qs, (uint32_t)(m * k));
         const rsrc_t rs = buf_rsrc(p.act.bsums, (uint32_t)(m * (k / 16) * 2));
@@ -353,10 +373,22 @@ __device__ __forceinline__ void rec_store(const ActStage &st, int r, uint8_t *ld
     }
 }
 
-template <int TYPE, int B, bool DUMP, bool FUSED>
+// silu(g) * u of four elements (candle: x / (1 + e^-x)).
+__device__ __forceinline__ u32x4 silu_mul4(u32x4 g, u32x4 u) {
+    const float gv[4] = {u32_as_f32(g.x), u32_as_f32(g.y), u32_as_f32(g.z), u32_as_f32(g.w)};
+    const float uv[4] = {u32_as_f32(u.x), u32_as_f32(u.y), u32_as_f32(u.z), u32_as_f32(u.w)};
+    float o[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) o[i] = (gv[i] / (1.0f + expf(-gv[i]))) * uv[i];
+    return (u32x4){f32_as_u32(o[0]), f32_as_u32(o[1]), f32_as_u32(o[2]), f32_as_u32(o[3])};
+}
+
+template <int TYPE, int B, bool DUMP, bool FUSED, int XF = XF_NONE>
 __global__ __launch_bounds__(NW * 64) void matvec_kernel(MvParams p) {
+    static_assert(XF == XF_NONE || (FUSED && B == 1), "input transforms are for one f32 row");
     extern __shared__ __align__(16) uint8_t lds[];
     __shared__ float red[NW][B][RB];  // per-wavefront chunk partials of the 8 rows of a row block
+    __shared__ float nred[NW];        // XF_NORM: per-wavefront sums of squares
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int g_l = lane >> 3, r_l = lane & 7;
@@ -375,16 +407,60 @@ __global__ __launch_bounds__(NW * 64) void matvec_kernel(MvParams p) {
     // step, 3. quantise / copy into LDS (waits only for step 1).
     ActStage as;
 #pragma unroll
-    for (int r = 0; r < PRE; r++) rec_load<TYPE, FUSED>(as, r, p, wave + nw * r, lane);
+    for (int r = 0; r < PRE; r++) rec_load<TYPE, FUSED, XF>(as, r, p, wave + nw * r, lane);
     Wt<TYPE> wa, wb;
     load_w<TYPE>(wa, p, rb_of(0), nrb, g_of(0), r_l);
+    if (XF == XF_NORM) {
+        // every record of the row is among the first PRE per wavefront (the
+        // launcher checks), so the row's sum of squares is known before any
+        // record is quantised; records past the end loaded zeros
+        float ss = 0.0f;
+#pragma unroll
+        for (int r = 0; r < PRE; r++) {
+            const u32x4 x4 = as.q[r], d4 = as.q2[r];
+            const float h[4] = {u32_as_f32(x4.x) + u32_as_f32(d4.x), u32_as_f32(x4.y) + u32_as_f32(d4.y),
+                                u32_as_f32(x4.z) + u32_as_f32(d4.z), u32_as_f32(x4.w) + u32_as_f32(d4.w)};
+            as.q[r] = (u32x4){f32_as_u32(h[0]), f32_as_u32(h[1]), f32_as_u32(h[2]), f32_as_u32(h[3])};
+#pragma unroll
+            for (int i = 0; i < 4; i++) ss = __builtin_fmaf(h[i], h[i], ss);
+        }
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
+        if (lane == 0) nred[wave] = ss;
+        __syncthreads();
+        float tot = 0.0f;
+        for (int w = 0; w < nw; w++) tot += nred[w];
+        const float mden = sqrtf(tot / (float)p.k + p.eps);
+        const rsrc_t rxo = buf_rsrc(p.xout, p.xout && blockIdx.x == 0 ? (uint32_t)(p.k * 4) : 0u);
+#pragma unroll
+        for (int r = 0; r < PRE; r++) {
+            const int t = wave + nw * r;
+            uint32_t off = BUF_OOB;
+            if (TYPE != TYPE_Q8_0) {
+                if (t < nrec) off = (uint32_t)((t * QK_K + 4 * lane) * 4);
+            } else {
+                const int j = lane >> 3, sub = lane & 7;
+                if (t < nrec && (8 * t + j) * QK8_0 < p.k) off = (uint32_t)(((8 * t + j) * QK8_0 + 4 * sub) * 4);
+            }
+            __builtin_amdgcn_raw_buffer_store_b128(as.q[r], rxo, off, 0, 0);  // the residual stream x + delta
+            const u32x4 h4 = as.q[r], w4 = as.q3[r];
+            as.q[r] = (u32x4){f32_as_u32((u32_as_f32(h4.x) / mden) * u32_as_f32(w4.x)),
+                              f32_as_u32((u32_as_f32(h4.y) / mden) * u32_as_f32(w4.y)),
+                              f32_as_u32((u32_as_f32(h4.z) / mden) * u32_as_f32(w4.z)),
+                              f32_as_u32((u32_as_f32(h4.w) / mden) * u32_as_f32(w4.w))};
+        }
+    } else if (XF == XF_SILU) {
+#pragma unroll
+        for (int r = 0; r < PRE; r++) as.q[r] = silu_mul4(as.q[r], as.q2[r]);
+    }
 #pragma unroll
     for (int r = 0; r < PRE; r++) {
         const int t = wave + nw * r;
         if (t < nrec) rec_store<TYPE, FUSED>(as, r, lds, t, lane);
     }
-    for (int t = wave + nw * PRE; t < nrec; t += nw) {
-        rec_load<TYPE, FUSED>(as, 0, p, t, lane);
+    for (int t = wave + nw * PRE; t < nrec; t += nw) {  // none with XF_NORM
+        rec_load<TYPE, FUSED, XF>(as, 0, p, t, lane);
+        if (XF == XF_SILU) as.q[0] = silu_mul4(as.q[0], as.q2[0]);
         rec_store<TYPE, FUSED>(as, 0, lds, t, lane);
     }
     __syncthreads();
@@ -473,13 +549,39 @@ hipError_t allow_lds() {
     return err;
 }
 
+template <int TYPE>
+hipError_t allow_lds_xf() {
+    static std::once_flag once;
+    static hipError_t err = hipSuccess;
+    std::call_once(once, [] {
+        const int cap = (int)LDS_CAP;
+        const void *fns[2] = {(const void *)matvec_kernel<TYPE, 1, false, true, XF_NORM>,
+                              (const void *)matvec_kernel<TYPE, 1, false, true, XF_SILU>};
+        for (const void *f : fns) {
+            const hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, cap);
+            if (e != hipSuccess) err = e;
+        }
+    });
+    return err;
+}
+
 template <int TYPE, int B>
-hipError_t launch_tb(const MvParams &p, unsigned grid, size_t lds, bool dump, hipStream_t s) {
+hipError_t launch_tb(const MvParams &p, unsigned grid, size_t lds, bool dump, int xf, hipStream_t s) {
+    const dim3 blk(p.nw * 64);
+    if (xf != XF_NONE) {
+        if (B != 1 || dump || !p.x) return hipErrorInvalidValue;
+        if (lds > 64 * 1024) {
+            const hipError_t e = allow_lds_xf<TYPE>();
+            if (e != hipSuccess) return e;
+        }
+        if (xf == XF_NORM) matvec_kernel<TYPE, 1, false, true, XF_NORM><<<grid, blk, lds, s>>>(p);
+        else matvec_kernel<TYPE, 1, false, true, XF_SILU><<<grid, blk, lds, s>>>(p);
+        return hipGetLastError();
+    }
     if (lds > 64 * 1024) {
         const hipError_t e = allow_lds<TYPE, B>();
         if (e != hipSuccess) return e;
     }
-    const dim3 blk(p.nw * 64);
     if (p.x) {
         if (dump) matvec_kernel<TYPE, B, true, true><<<grid, blk, lds, s>>>(p);
         else matvec_kernel<TYPE, B, false, true><<<grid, blk, lds, s>>>(p);
@@ -491,20 +593,28 @@ hipError_t launch_tb(const MvParams &p, unsigned grid, size_t lds, bool dump, hi
 }
 
 template <int TYPE>
-hipError_t launch_t(int B, const MvParams &p, unsigned grid, size_t lds, bool dump, hipStream_t s) {
+hipError_t launch_t(int B, const MvParams &p, unsigned grid, size_t lds, bool dump, int xf, hipStream_t s) {
     switch (B) {
-    case 1: return launch_tb<TYPE, 1>(p, grid, lds, dump, s);
-    case 2: return launch_tb<TYPE, 2>(p, grid, lds, dump, s);
-    case 4: return launch_tb<TYPE, 4>(p, grid, lds, dump, s);
-    case 8: return launch_tb<TYPE, 8>(p, grid, lds, dump, s);
+    case 1: return launch_tb<TYPE, 1>(p, grid, lds, dump, xf, s);
+    case 2: return launch_tb<TYPE, 2>(p, grid, lds, dump, xf, s);
+    case 4: return launch_tb<TYPE, 4>(p, grid, lds, dump, xf, s);
+    case 8: return launch_tb<TYPE, 8>(p, grid, lds, dump, xf, s);
     default: return hipErrorInvalidConfiguration;
     }
 }
 
-}  // namespace
+struct XfArgs {
+    int xf = XF_NONE;
+    const float *delta = nullptr, *norm = nullptr;
+    float eps = 0.0f;
+    float *xout = nullptr;
+};
 
-hipError_t launch_matvec(const WLayout &w, int64_t n, int64_t k, const float *x, const ActPlanes *act, int64_t m,
-                         float *y, int32_t *S, int32_t *Smin, hipStream_t s) {
+hipError_t matvec_impl(const WLayout &w, int64_t n, int64_t k, const float *x, const ActPlanes *act, int64_t m,
+                       float *y, int32_t *S, int32_t *Smin, const XfArgs &xa, hipStream_t s);
+
+hipError_t matvec_impl(const WLayout &w, int64_t n, int64_t k, const float *x, const ActPlanes *act, int64_t m,
+                       float *y, int32_t *S, int32_t *Smin, const XfArgs &xa, hipStream_t s) {
     const int type = w.type;
     if (type != TYPE_Q4_K && type != TYPE_Q6_K && type != TYPE_Q8_0) return hipErrorInvalidValue;
     const int blk = type == TYPE_Q8_0 ? QK8_0 : QK_K;
@@ -516,6 +626,7 @@ hipError_t launch_matvec(const WLayout &w, int64_t n, int64_t k, const float *x,
     if (x && ((uintptr_t)x & 15)) return hipErrorInvalidValue;  // the fused prologue reads float4
     if ((S == nullptr) != (Smin == nullptr)) return hipErrorInvalidValue;
     if (m == 0) return hipSuccess;
+    if (xa.xf != XF_NONE && (m != 1 || !x || S || (xa.xf == XF_NORM && !xa.norm))) return hipErrorInvalidValue;
     const int ng = w.ng;
     if ((size_t)ng * REC > LDS_CAP) return hipErrorNotSupported;  // k > 124160
     if ((int64_t)8 * n * 4 >= ((int64_t)1 << 31)) return hipErrorNotSupported;  // y of a pass: 32-bit buffer offsets
@@ -535,6 +646,8 @@ hipError_t launch_matvec(const WLayout &w, int64_t n, int64_t k, const float *x,
     const int64_t iters = (wg_iters + target_wg - 1) / target_wg;
     const int64_t grid = (wg_iters + iters - 1) / iters;
     if ((int64_t)iters * nsub > 0x7fffffff) return hipErrorInvalidValue;
+    // the fused norm needs the whole row among each wavefront's first PRE records
+    if (xa.xf == XF_NORM && ng > PRE * nw) return hipErrorNotSupported;
     const int64_t nblk = k / blk;
     int64_t r0 = 0;
     while (r0 < m) {
@@ -557,6 +670,10 @@ hipError_t launch_matvec(const WLayout &w, int64_t n, int64_t k, const float *x,
         p.m = mb;
         p.iters = (int)iters;
         p.x = x ? x + r0 * k : nullptr;
+        p.xdelta = xa.delta;
+        p.xnorm = xa.norm;
+        p.xout = xa.xout;
+        p.eps = xa.eps;
         if (act) {
             p.act.qs = act->qs + r0 * k;
             p.act.d = act->d + r0 * (k / blk);
@@ -571,14 +688,40 @@ hipError_t launch_matvec(const WLayout &w, int64_t n, int64_t k, const float *x,
         const size_t lds = (size_t)B * ng * REC;
         hipError_t e;
         switch (type) {
-        case TYPE_Q4_K: e = launch_t<TYPE_Q4_K>(B, p, (unsigned)grid, lds, S != nullptr, s); break;
-        case TYPE_Q6_K: e = launch_t<TYPE_Q6_K>(B, p, (unsigned)grid, lds, S != nullptr, s); break;
-        default: e = launch_t<TYPE_Q8_0>(B, p, (unsigned)grid, lds, S != nullptr, s); break;
+        case TYPE_Q4_K: e = launch_t<TYPE_Q4_K>(B, p, (unsigned)grid, lds, S != nullptr, xa.xf, s); break;
+        case TYPE_Q6_K: e = launch_t<TYPE_Q6_K>(B, p, (unsigned)grid, lds, S != nullptr, xa.xf, s); break;
+        default: e = launch_t<TYPE_Q8_0>(B, p, (unsigned)grid, lds, S != nullptr, xa.xf, s); break;
         }
         if (e != hipSuccess) return e;
         r0 += mb;
     }
     return hipSuccess;
+}
+
+}  // namespace
+
+hipError_t launch_matvec(const WLayout &w, int64_t n, int64_t k, const float *x, const ActPlanes *act, int64_t m,
+                         float *y, int32_t *S, int32_t *Smin, hipStream_t s) {
+    return matvec_impl(w, n, k, x, act, m, y, S, Smin, XfArgs{}, s);
+}
+
+hipError_t launch_matvec_rmsnorm(const WLayout &w, int64_t n, int64_t k, const float *x, const float *delta,
+                                 const float *norm, float eps, float *xout, float *y, hipStream_t s) {
+    if ((delta && ((uintptr_t)delta & 15)) || !norm || ((uintptr_t)norm & 15) || (xout && ((uintptr_t)xout & 15)))
+        return hipErrorInvalidValue;
+    XfArgs xa;
+    xa.xf = XF_NORM;
+    xa.delta = delta;
+    xa.norm = norm;
+    xa.eps = eps;
+    xa.xout = xout;
+    return matvec_impl(w, n, k, x, nullptr, 1, y, nullptr, nullptr, xa, s);
+}
+
+hipError_t launch_matvec_silu(const WLayout &w, int64_t n, int64_t k, const float *gu, float *y, hipStream_t s) {
+    XfArgs xa;
+    xa.xf = XF_SILU;
+    return matvec_impl(w, n, k, gu, nullptr, 1, y, nullptr, nullptr, xa, s);
 }
 
 }  // namespace aq

@@ -32,9 +32,10 @@ The decode step (one token at a given position) can be captured once into a
 HIP graph and replayed per token (``Llama.generate(..., graph=True)``).  That
 step does not use torch ops: it is this library's decode-step glue kernels
 (k_decode.hip: embedding, residual add + RMSNorm, RoPE + KV-cache write +
-grouped-query attention in one launch, SiLU * up, and a first-maximum argmax
-that writes the next token and advances the device-side position) around the
-GPU QMatMuls, 9 launches per layer.  Projections that share an input and a
+grouped-query attention in one launch, and a first-maximum argmax that writes
+the next token and advances the device-side position) around the GPU
+QMatMuls, whose matvec forms its own input where that input is
+rms_norm(x + delta) or silu(g) * u: 6 launches per layer.  Projections that share an input and a
 type are uploaded as one weight (wq|wk, w1|w3: rows concatenated), so each
 pair is one matmul launch.  The KV cache, the RoPE tables and every
 intermediate buffer are preallocated for ``max_seq`` positions, so every
@@ -327,21 +328,25 @@ class Llama:
         self._pos = torch.zeros(1, **i64)
         self._tok = torch.zeros(1, **i64)
         self._hist = torch.zeros(cfg.max_seq, **i64)  # token generated at each position
-        self._x = torch.zeros(cfg.hidden, **f32)       # residual stream
-        self._n = torch.zeros(cfg.hidden, **f32)
+        self._ra = torch.zeros(cfg.hidden, **f32)      # residual stream, two buffers in turn
+        self._rb = torch.zeros(cfg.hidden, **f32)
         self._qk = torch.zeros((cfg.n_head + cfg.n_kv_head) * hd, **f32)
         self._v = torch.zeros(cfg.n_kv_head * hd, **f32)
         self._att = torch.zeros(cfg.n_head * hd, **f32)
-        self._o = torch.zeros(cfg.hidden, **f32)       # wo / w2 output (the next residual delta)
+        self._o = torch.zeros(cfg.hidden, **f32)       # wo output
         self._gu = torch.zeros(2 * cfg.ffn, **f32)
-        self._a = torch.zeros(cfg.ffn, **f32)
+        self._d = torch.zeros(cfg.hidden, **f32)       # w2 output (the pending residual delta)
         self._logits = torch.zeros(cfg.vocab, **f32)
 
     def _decode_step_static(self):
         """One decode step for the token in self._tok at the position in self._pos
-        (both device memory), through the library's glue kernels and QMatMuls;
-        leaves the logits in self._logits, the next token in self._tok and in
-        self._hist[pos], and pos + 1 in self._pos."""
+        (both device memory); leaves the logits in self._logits, the next token
+        in self._tok and in self._hist[pos], and pos + 1 in self._pos.
+
+        Per layer six launches: the QMatMuls of wq|wk and wv take
+        rms_norm(x + delta) as their input (formed inside the matvec, which also
+        writes the residual x + delta once), attention (RoPE, KV write, GQA),
+        wo, w1|w3 on rms_norm(h + wo), w2 on silu(g) * u."""
         from . import _lib
 
         L = _lib.load()
@@ -351,32 +356,35 @@ class Llama:
         ptr = lambda t: t.data_ptr()
         chk = _lib.check
         eps = ctypes.c_float(cfg.rms_eps)
-        chk(L.aq_llama_embed(c, ptr(self.tok_embeddings), cfg.vocab, ptr(self._tok), cfg.hidden, ptr(self._x)))
+
+        def mm_norm(w, x, delta, norm, out, h_out=None):
+            chk(L.aq_qmatmul_rmsnorm_f32_device(c, w.handle, ptr(x), delta, ptr(norm), eps, w.k,
+                                                ptr(h_out) if h_out is not None else None, out))
+
+        chk(L.aq_llama_embed(c, ptr(self.tok_embeddings), cfg.vocab, ptr(self._tok), cfg.hidden, ptr(self._ra)))
+        cur, other = self._ra, self._rb
         delta = None
         for li, lw in enumerate(self.layers):
-            chk(L.aq_llama_rmsnorm(c, ptr(self._x), delta, ptr(self.attn_norm[li]), 1, cfg.hidden, eps, ptr(self._n)))
+            an = self.attn_norm[li]
             if "wqk" in lw:
-                lw["wqk"].forward_device(ptr(self._n), 1, ptr(self._qk))
+                mm_norm(lw["wqk"], cur, delta, an, ptr(self._qk), h_out=other)
             else:
-                lw["wq"].forward_device(ptr(self._n), 1, ptr(self._qk))
-                lw["wk"].forward_device(ptr(self._n), 1, ptr(self._qk) + 4 * cfg.n_head * hd)
-            lw["wv"].forward_device(ptr(self._n), 1, ptr(self._v))
+                mm_norm(lw["wq"], cur, delta, an, ptr(self._qk), h_out=other)
+                mm_norm(lw["wk"], cur, delta, an, ptr(self._qk) + 4 * cfg.n_head * hd)
+            mm_norm(lw["wv"], cur, delta, an, ptr(self._v))
             chk(L.aq_llama_attn_decode(c, ptr(self._qk), ptr(self._v), ptr(self.cos), ptr(self.sin), ptr(self._pos),
                                        ptr(self.k_cache[li]), ptr(self.v_cache[li]), cfg.n_head, cfg.n_kv_head, hd,
                                        cfg.max_seq, ptr(self._att)))
             lw["wo"].forward_device(ptr(self._att), 1, ptr(self._o))
-            chk(L.aq_llama_rmsnorm(c, ptr(self._x), ptr(self._o), ptr(self.ffn_norm[li]), 1, cfg.hidden, eps,
-                                   ptr(self._n)))
+            fn = self.ffn_norm[li]
             if "w13" in lw:
-                lw["w13"].forward_device(ptr(self._n), 1, ptr(self._gu))
+                mm_norm(lw["w13"], other, ptr(self._o), fn, ptr(self._gu), h_out=cur)
             else:
-                lw["w1"].forward_device(ptr(self._n), 1, ptr(self._gu))
-                lw["w3"].forward_device(ptr(self._n), 1, ptr(self._gu) + 4 * cfg.ffn)
-            chk(L.aq_llama_silu_mul(c, ptr(self._gu), cfg.ffn, ptr(self._a)))
-            lw["w2"].forward_device(ptr(self._a), 1, ptr(self._o))
-            delta = ptr(self._o)
-        chk(L.aq_llama_rmsnorm(c, ptr(self._x), delta, ptr(self.norm), 1, cfg.hidden, eps, ptr(self._n)))
-        self.output.forward_device(ptr(self._n), 1, ptr(self._logits))
+                mm_norm(lw["w1"], other, ptr(self._o), fn, ptr(self._gu), h_out=cur)
+                mm_norm(lw["w3"], other, ptr(self._o), fn, ptr(self._gu) + 4 * cfg.ffn)
+            chk(L.aq_qmatmul_silu_mul_f32_device(c, lw["w2"].handle, ptr(self._gu), cfg.ffn, ptr(self._d)))
+            delta = ptr(self._d)  # the residual is now x + wo + w2 = cur + d
+        mm_norm(self.output, cur, delta, self.norm, ptr(self._logits))
         chk(L.aq_llama_argmax(c, ptr(self._logits), cfg.vocab, ptr(self._tok), ptr(self._pos), ptr(self._hist),
                               cfg.max_seq))
 

@@ -248,6 +248,19 @@ int aq_llama_silu_mul(aq_ctx *ctx, const float *d_gu, int64_t n, float *d_out);
 int aq_llama_attn_decode(aq_ctx *ctx, const float *d_qk, const float *d_v, const float *d_cos, const float *d_sin,
                          const int64_t *d_pos, float *d_kcache, float *d_vcache, int64_t n_head, int64_t n_kv,
                          int64_t head_dim, int64_t max_seq, float *d_out);
+/* aq_qmatmul_f32_device for one row (m = 1) whose input is formed inside the
+ * matmul kernel, so the step needs no separate launch for it:
+ * rmsnorm: input = rms_norm(d_x + d_delta) * d_norm_w (eps as aq_llama_rmsnorm;
+ *   d_delta may be null), and when d_h_out is non-null it receives
+ *   d_x + d_delta (the residual stream), written once.  d_h_out must not
+ *   alias d_x or d_delta.  AQ_ERR_SHAPE when k is too long to fuse
+ *   (k > 8192 for Q4_K / Q6_K); then run aq_llama_rmsnorm and
+ *   aq_qmatmul_f32_device instead.
+ * silu_mul: d_gu = [g (k) | u (k)], input = silu(g) * u.
+ * All pointers 16-byte aligned. */
+int aq_qmatmul_rmsnorm_f32_device(aq_ctx *ctx, const aq_qweight *w, const float *d_x, const float *d_delta,
+                                  const float *d_norm_w, float eps, int64_t k, float *d_h_out, float *d_dst);
+int aq_qmatmul_silu_mul_f32_device(aq_ctx *ctx, const aq_qweight *w, const float *d_gu, int64_t k, float *d_dst);
 /* Greedy pick: the first index of the largest of d_x[0..n) goes to *d_tok
  * and, when d_hist is non-null and 0 <= *d_pos < hist_len, to
  * d_hist[*d_pos]; then *d_pos += 1. */

@@ -180,3 +180,90 @@ def test_glue_argument_errors(env):
         assert rc != 0
     assert L.aq_llama_silu_mul(ctx.handle, None, 4, p) != 0
     assert L.aq_llama_argmax(ctx.handle, p, 0, pos.data_ptr(), pos.data_ptr(), None, 0) != 0
+
+
+# ------------------------------------------------ matvec with a fused input transform
+def _weight(A, S, wtype, n, k, ctx, seed):
+    W = S.make_weight(wtype, n, k, seed=seed)
+    return W, A.QMatMul.from_qtensor(A.QTensor(wtype, (n, k), W.blocks), ctx)
+
+
+@pytest.mark.parametrize("wtype,n,k,with_delta", [(12, 2304, 2048, True), (14, 256, 2048, False),
+                                                  (12, 1000, 4096, True), (8, 300, 1024, True)])
+def test_matvec_fused_rmsnorm(env, wtype, n, k, with_delta):
+    """y = W . rms_norm(x + delta) * w_norm in one launch, against the oracle's
+    matmul of the same input formed in numpy; h_out = x + delta exactly."""
+    import oracle as O
+
+    import arm_ai_amd as A
+    from arm_ai_amd import synth as S
+
+    torch, lib, ctx = env
+    L = lib.load()
+    rng = np.random.default_rng(n + k)
+    W, mm = _weight(A, S, wtype, n, k, ctx, seed=n)
+    x = rng.standard_normal(k).astype(np.float32)
+    d = rng.standard_normal(k).astype(np.float32) if with_delta else np.zeros(k, np.float32)
+    wn = (1 + 0.05 * rng.standard_normal(k)).astype(np.float32)
+    dx, dd, dwn = _dev(torch, x), _dev(torch, d), _dev(torch, wn)
+    hout = torch.full((k,), np.nan, dtype=torch.float32, device="cuda:0")
+    y = torch.empty(n, dtype=torch.float32, device="cuda:0")
+    torch.cuda.synchronize()
+    lib.check(L.aq_qmatmul_rmsnorm_f32_device(ctx.handle, mm.handle, dx.data_ptr(),
+                                              dd.data_ptr() if with_delta else None, dwn.data_ptr(),
+                                              ctypes.c_float(1e-5), k, hout.data_ptr(), y.data_ptr()))
+    ctx.synchronize()
+    h = x + d
+    assert np.array_equal(hout.cpu().numpy(), h)
+    ms = np.float32(np.mean(h.astype(np.float64) ** 2))
+    xin = ((h / np.sqrt(ms + np.float32(1e-5))) * wn).astype(np.float32)[None, :]
+    r = O.matmul(wtype, xin, W.blocks, n, k)[0]
+    # the row's sum of squares is reduced in another order, which can move a
+    # Q8_K quant by one step: compare at 1e-3 of the output's scale
+    assert _rel(y.cpu().numpy(), r) <= 1e-3
+    mm.free()
+
+
+@pytest.mark.parametrize("wtype,n,k", [(12, 2048, 5632), (14, 2048, 5632), (12, 300, 256)])
+def test_matvec_fused_silu_mul(env, wtype, n, k):
+    import oracle as O
+
+    import arm_ai_amd as A
+    from arm_ai_amd import synth as S
+
+    torch, lib, ctx = env
+    L = lib.load()
+    rng = np.random.default_rng(k)
+    W, mm = _weight(A, S, wtype, n, k, ctx, seed=k)
+    gu = (2 * rng.standard_normal(2 * k)).astype(np.float32)
+    dgu = _dev(torch, gu)
+    y = torch.empty(n, dtype=torch.float32, device="cuda:0")
+    torch.cuda.synchronize()
+    lib.check(L.aq_qmatmul_silu_mul_f32_device(ctx.handle, mm.handle, dgu.data_ptr(), k, y.data_ptr()))
+    ctx.synchronize()
+    g, u = gu[:k], gu[k:]
+    xin = ((g / (np.float32(1) + np.exp(-g))) * u).astype(np.float32)[None, :]
+    r = O.matmul(wtype, xin, W.blocks, n, k)[0]
+    assert _rel(y.cpu().numpy(), r) <= 1e-3
+    mm.free()
+
+
+def test_matvec_fused_errors(env):
+    import arm_ai_amd as A
+    from arm_ai_amd import synth as S
+
+    torch, lib, ctx = env
+    L = lib.load()
+    W, mm = _weight(A, S, 12, 64, 16384, ctx, seed=1)
+    buf = torch.zeros(2 * 16384, dtype=torch.float32, device="cuda:0")
+    torch.cuda.synchronize()
+    p = buf.data_ptr()
+    # too long a row for the fused norm: a clean AQ_ERR_SHAPE, nothing launched
+    assert L.aq_qmatmul_rmsnorm_f32_device(ctx.handle, mm.handle, p, None, p, ctypes.c_float(1e-5), 16384, None,
+                                           p) == lib.AQ_ERR_SHAPE
+    # wrong k, aliased residual output
+    assert L.aq_qmatmul_rmsnorm_f32_device(ctx.handle, mm.handle, p, None, p, ctypes.c_float(1e-5), 8192, None,
+                                           p) == lib.AQ_ERR_SHAPE
+    assert L.aq_qmatmul_rmsnorm_f32_device(ctx.handle, mm.handle, p, None, p, ctypes.c_float(1e-5), 16384, p,
+                                           p) == lib.AQ_ERR_INVALID_ARG
+    mm.free()
