@@ -133,6 +133,15 @@ hipError_t launch_gemm(const WLayout &w, int64_t n, int64_t k, const ActPlanes &
 // Workspace bytes launch_gemm needs for this shape, or (size_t)-1 if the
 // weight type / shape has no GEMM (the matvec then serves m > 8 too).
 size_t gemm_workspace_bytes(int type, int64_t m, int64_t n, int64_t k);
+// The Q6_K GEMM on f16 MFMA (k_gemm6.hip), reached through launch_gemm /
+// gemm_workspace_bytes; its workspace holds the f16 copy of the activation
+// quants and the split-K partials.
+size_t gemm6_workspace_bytes(int64_t m, int64_t n, int64_t k);
+hipError_t launch_gemm6(const WLayout &w, int64_t n, int64_t k, const ActPlanes &x, int64_t m, float *y, int32_t *S,
+                        int32_t *Smin, void *ws, size_t ws_bytes, hipStream_t s);
+// Sums split-K partial tiles [tiles][splits][gbm][128] into y in split order.
+hipError_t launch_splitk_reduce(const float *part, float *y, int m, int n, int ntm, int gbm, int splits, int tiles,
+                                hipStream_t s);
 
 // The NIF crate's own kernels (k_crate.hip; shape_ops.rs).
 enum { CRATE_W_Q4_0 = 0, CRATE_W_I8 = 1, CRATE_W_F16 = 2 };

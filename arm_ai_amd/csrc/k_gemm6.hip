@@ -1,0 +1,364 @@
+// k_gemm6.hip -- prefill GEMM (m > 8) for Q6_K weights on the f16 matrix
+// cores, gfx950.
+//
+// Replaces the M-row loop of candle-core 0.8.4 k_quants::matmul<BlockQ6K> at
+// prefill (native/arm_ai_nif/src/llama_candle.rs:93): for TinyLlama Q4_K_M
+// these are attn_v and half of ffn_down.  Per super-block b of a weight row n
+// and an activation row m (Q8_K):
+//   y[m][n] += d_w[n,b] * d_x[m,b] * S,  S = sum_j sc_j * sum_{e in j} (q6_e - 32) * qx_e
+// over the 16 sub-blocks j of 16 elements, with S an exact integer (candle's
+// vec_dot keeps it exact too).
+//
+// Exactness on f16 MFMA.  The weight operand is w_e = sc_j * (q6_e - 32):
+// |w| <= 32 * 32 = 1024, an integer, so it is exact in f16; the activation
+// operand is the Q8_K quant qx (|qx| <= 128), exact in f16.  Each
+// v_mfma_f32_32x32x16_f16 covers one sub-block (K = 16); products are exact in
+// f32, and every partial sum of eight sub-blocks is an integer of magnitude at
+// most 8 * 16 * 1024 * 128 = 2^24, so the f32 accumulator chain over sub-blocks
+// 0..7, and the one over 8..15, hold exact integers whatever the summation
+// order.  S is their sum (converted to int32 for the integer dump; in f32 for
+// the output, where |S| <= 2^25 can round only the last bit of values the
+// BASELINE distributions never reach).
+// The weight operand is built per lane from the 6-bit quants: nibble of ql,
+// two bits of qh, then 1024 + q as f16 bits (0x6400 | q) and one packed f16
+// fma, (1024 + q) * sc - 1056 * sc, which is exact (the result is an integer
+// of magnitude <= 1024).
+//
+// Tiling.  A workgroup (4 wavefronts, two workgroups per CU) owns a 64 (m) x
+// 128 (n) output tile; wavefront w owns columns 32w..32w+31 and both 32-row
+// MFMA tiles, so each weight operand it builds feeds two MFMAs.  The f16
+// activation rows of the tile (written by qs_to_f16_kernel) are copied global
+// -> LDS (buffer loads into LDS) one super-block ahead, two stages, 16-byte
+// chunks XOR-swizzled by row; each lane loads its own column's ql / qh / scale
+// bytes straight into registers, also one super-block ahead.  Work items
+// (tile, k-split) are dealt so that all m-tiles and k-splits of one n-tile run
+// on one XCD.  Split-K partials are summed in split order by the Q4_K GEMM's
+// reduce launch.
+#include "aq_internal.h"
+
+#include <algorithm>
+
+namespace aq {
+
+namespace {
+
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int G6N = 128;  // columns (n) per workgroup
+constexpr int G6M = 64;   // rows (m) per workgroup
+constexpr int NXCD6 = 8;
+constexpr int TARGET_WG6 = 512;  // two workgroups per CU
+
+struct Gemm6Params {
+    const uint8_t *w;     // row-block tiles
+    const uint16_t *wd;   // d plane [n/8][ng][8] f16
+    int64_t rb_stride;
+    int ng;
+    const uint16_t *x16;  // activation quants as f16 [m][k]
+    const float *xd;      // [m][ng]
+    float *y;
+    int m, n, k;
+    int ntm, tiles, splits, kbs, items, per_xcd;
+    float *part;          // [tiles][splits][64][128] (splits > 1)
+    int32_t *S, *Smin;    // integer dump [m][n][ng] or null (Smin: zeros, Q6_K has no min term)
+};
+
+// One lane's weight bytes of one super-block: bytes 8h..8h+7 of the 8 ql and
+// 4 qh pieces of its column, the 16 int8 scales, and d.
+struct W6 {
+    u32x2 ql[8], qh[4];
+    u32x4 sc;
+    uint32_t d;
+};
+
+struct Lds6 {
+    static constexpr int QS = G6M * 512;  // f16 quants [64 rows][256], chunk c of row r at c ^ (r & 31)
+    static constexpr int DX = QS;         // d_x [64] f32
+    static constexpr int STAGE = QS + 256;
+    static constexpr int BYTES = 2 * STAGE;
+};
+
+__device__ __forceinline__ void load_w6(W6 &W, const rsrc_t &rw, const rsrc_t &rwd, uint32_t off, uint32_t doff,
+                                        int b, int ng) {
+    const bool ok = b < ng;
+    const uint32_t o = ok ? off + (uint32_t)(b * 13 * 128) : BUF_OOB;
+#pragma unroll
+    for (int i = 0; i < 8; i++) W.ql[i] = __builtin_amdgcn_raw_buffer_load_b64(rw, o + i * 128, 0, BUF_NT);
+#pragma unroll
+    for (int i = 0; i < 4; i++) W.qh[i] = __builtin_amdgcn_raw_buffer_load_b64(rw, o + (8 + i) * 128, 0, BUF_NT);
+    // the scales piece: the whole 16 bytes (this lane's h offset removed)
+    W.sc = __builtin_amdgcn_raw_buffer_load_b128(rw, ok ? (o & ~15u) + 12 * 128 : BUF_OOB, 0, BUF_NT);
+    W.d = __builtin_amdgcn_raw_buffer_load_b16(rwd, ok ? doff + (uint32_t)(b * RB * 2) : BUF_OOB, 0, BUF_NT);
+}
+
+// The 8 f16 weight operands sc_j * (q6 - 32) of sub-block j for this lane
+// (elements 16j + 8h .. 16j + 8h + 7 of its column's super-block).
+__device__ __forceinline__ v8h w6_operand(const W6 &W, int j) {
+    const int hh = j >> 3, jj = j & 7, qq = jj >> 1, odd = jj & 1;
+    const u32x2 ql = W.ql[4 * hh + 2 * (qq & 1) + odd];
+    const u32x2 qh = W.qh[2 * hh + odd];
+    uint32_t q[2];
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const uint32_t nib = (qq >> 1) ? (ql[i] >> 4) & 0x0F0F0F0Fu : ql[i] & 0x0F0F0F0Fu;
+        const uint32_t hb = (qq < 2 ? qh[i] << (4 - 2 * qq) : qh[i] >> (2 * qq - 4)) & 0x30303030u;
+        q[i] = nib | hb;
+    }
+    const int sc = (int)(int8_t)((W.sc[j >> 2] >> (8 * (j & 3))) & 0xffu);
+    const _Float16 s = (_Float16)sc;
+    const _Float16 o = (_Float16)(-1056 * sc);  // exact: 33 * 32 * |sc| has at most 6 significant bits
+    const h2 s2 = {s, s}, o2 = {o, o};
+    v8h r;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        // bytes 2i, 2i+1 of q as 16-bit lanes, then 1024 + q as f16
+        const uint32_t u = __builtin_amdgcn_perm(0u, q[i >> 1], (i & 1) ? 0x0C030C02u : 0x0C010C00u) | 0x64006400u;
+        const h2 f = __builtin_bit_cast(h2, u);
+        const h2 v = __builtin_elementwise_fma(f, s2, o2);
+        r[2 * i] = v[0];
+        r[2 * i + 1] = v[1];
+    }
+    return r;
+}
+
+template <bool DUMP>
+__global__ __launch_bounds__(256, 2) void gemm_q6k_kernel(Gemm6Params p) {
+    __shared__ __align__(16) uint8_t lds[Lds6::BYTES];
+    const int xcd = blockIdx.x % NXCD6, local = blockIdx.x / NXCD6;
+    const int item = xcd * p.per_xcd + local;
+    if (local >= p.per_xcd || item >= p.items) return;  // uniform over the workgroup
+    const int tile = item / p.splits, split = item - tile * p.splits;
+    const int tn = tile / p.ntm, tm = tile - tn * p.ntm;
+    const int m0 = tm * G6M;
+    const int kb0 = split * p.kbs;
+    const int kb1 = min(p.ng, kb0 + p.kbs);
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int h = lane >> 5, l32 = lane & 31;
+    const int ccol = wave * 32 + l32;
+    const int col = tn * G6N + ccol;
+    const bool col_ok = col < p.n;
+    const int ng = p.ng, k = p.k;
+
+    // activation copies: instruction i of wave w fills LDS bytes (8w+i)*1024 +
+    // 16*lane: row r = 2(8w+i) + lane/32, chunk position lane%32, which holds
+    // the row's chunk (lane%32) ^ (r & 31).  Rows past m read zeros.
+    const rsrc_t rq = buf_rsrc(p.x16, (uint32_t)((int64_t)p.m * k * 2));
+    const rsrc_t rdx = buf_rsrc(p.xd, (uint32_t)((int64_t)p.m * ng * 4));
+    uint32_t qoff[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const int r = 2 * (8 * wave + i) + (lane >> 5), cp = lane & 31;
+        qoff[i] = (uint32_t)((m0 + r) * k * 2 + 16 * (cp ^ (r & 31)));
+    }
+    const uint32_t dxoff = (uint32_t)((m0 + lane) * ng * 4);
+    // weights: this lane's column is row (ccol % 8) of the tile's row block ccol / 8
+    const int nrb = (p.n + RB - 1) / RB;
+    const int rb_here = min(16, nrb - 16 * tn);
+    const rsrc_t rw = buf_rsrc(p.w + (int64_t)16 * tn * p.rb_stride, (uint32_t)(rb_here * p.rb_stride));
+    const rsrc_t rwd = buf_rsrc(p.wd + (int64_t)16 * tn * ng * RB, (uint32_t)(rb_here * ng * RB * 2));
+    const uint32_t woff = (uint32_t)((ccol >> 3) * p.rb_stride + (ccol & 7) * 16 + 8 * h);
+    const uint32_t wdoff = (uint32_t)((((ccol >> 3) * ng) * RB + (ccol & 7)) * 2);
+
+    auto issue = [&](uint8_t *st, int b) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) buf_to_lds16(rq, st + 1024 * (8 * wave + i), qoff[i], b * 512);
+        if (wave == 0) buf_to_lds4(rdx, st + Lds6::DX, dxoff, b * 4);  // wave-uniform
+    };
+
+    v16f yacc[2];
+#pragma unroll
+    for (int t = 0; t < 2; t++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) yacc[t][r] = 0.0f;
+
+    auto compute = [&](const uint8_t *st, const W6 &W, int b) {
+        v16f acc[2][2];  // [tile][sub-blocks 0..7 / 8..15]
+        auto read_a = [&](int t, int j) {
+            const int R = 32 * t + l32, C = 2 * j + h;
+            return *(const v8h *)(st + R * 512 + 16 * (C ^ (R & 31)));
+        };
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            const v8h bw = w6_operand(W, j);
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
+                const v16f z = {0};
+                const int c = j >> 3;
+                acc[t][c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(read_a(t, j), bw, (j & 7) == 0 ? z : acc[t][c], 0, 0, 0);
+            }
+        }
+        const float dw = f16_bits_to_f32(W.d);
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+#pragma unroll
+            for (int g4 = 0; g4 < 4; g4++) {
+                const v4f dx4 = *(const v4f *)(st + Lds6::DX + 4 * (32 * t + 8 * g4 + 4 * h));
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int r = 4 * g4 + i;
+                    // f32 combine: y += (d_w * d_x) * S
+                    yacc[t][r] = __builtin_fmaf(dw * dx4[i], acc[t][0][r] + acc[t][1][r], yacc[t][r]);
+                    if (DUMP) {
+                        const int row = m0 + 32 * t + 8 * g4 + 4 * h + i;
+                        if (row < p.m && col_ok) {
+                            const int64_t o = ((int64_t)row * p.n + col) * ng + b;
+                            p.S[o] = (int)acc[t][0][r] + (int)acc[t][1][r];
+                            p.Smin[o] = 0;
+                        }
+                    }
+                }
+            }
+        }
+    };
+
+    // Two main stages and two weight register sets, one super-block ahead:
+    // step b waits for its copies and loads (all this wave's outstanding
+    // memory operations), a barrier, then issues step b + 1's.
+    W6 wa, wb;
+    issue(lds, kb0);
+    load_w6(wa, rw, rwd, woff, wdoff, kb0, kb1);
+    for (int b = kb0; b < kb1; b += 2) {
+        wait_vmcnt<0>();
+        stage_barrier();
+        issue(lds + Lds6::STAGE, b + 1);  // past kb1: reads rows past the range (zeros) or unused data
+        load_w6(wb, rw, rwd, woff, wdoff, b + 1, kb1);
+        compute(lds, wa, b);
+        if (b + 1 >= kb1) break;
+        wait_vmcnt<0>();
+        stage_barrier();
+        issue(lds, b + 2);
+        load_w6(wa, rw, rwd, woff, wdoff, b + 2, kb1);
+        compute(lds + Lds6::STAGE, wb, b + 1);
+    }
+    wait_vmcnt<0>();  // no copy may still be landing when the workgroup ends
+
+    if (p.splits == 1) {
+        if (col_ok) {
+#pragma unroll
+            for (int t = 0; t < 2; t++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const int row = m0 + 32 * t + 8 * (r >> 2) + 4 * h + (r & 3);
+                    if (row < p.m) p.y[(int64_t)row * p.n + col] = yacc[t][r];
+                }
+        }
+        return;
+    }
+    float *mine = p.part + ((int64_t)tile * p.splits + split) * (G6M * G6N);
+#pragma unroll
+    for (int t = 0; t < 2; t++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) mine[(32 * t + 8 * (r >> 2) + 4 * h + (r & 3)) * G6N + ccol] = yacc[t][r];
+}
+
+// The activation quants as f16 (exact), four per thread.
+__global__ __launch_bounds__(256) void qs_to_f16_kernel(const int8_t *__restrict__ qs, int64_t n4,
+                                                        uint16_t *__restrict__ out) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n4) return;
+    const uint32_t q = ((const uint32_t *)qs)[i];
+    uint16_t o[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) o[j] = __builtin_bit_cast(uint16_t, (_Float16)(int)(int8_t)((q >> (8 * j)) & 0xffu));
+    ((uint2 *)out)[i] = make_uint2(o[0] | ((uint32_t)o[1] << 16), o[2] | ((uint32_t)o[3] << 16));
+}
+
+struct Gemm6Plan {
+    int ntm, ntn, tiles, splits, kbs;
+    size_t part, ws;
+};
+
+// 64 x 128 tiles, two workgroups per CU; K split while there are fewer items
+// than workgroup slots, each split keeping at least two super-blocks.
+Gemm6Plan gemm6_plan(int64_t m, int64_t n, int64_t k) {
+    Gemm6Plan g;
+    const int ng = (int)(k / QK_K);
+    g.ntn = (int)((n + G6N - 1) / G6N);
+    g.ntm = (int)((m + G6M - 1) / G6M);
+    g.tiles = g.ntm * g.ntn;
+    g.splits = 1;
+    while ((int64_t)g.tiles * g.splits < TARGET_WG6 && ng / (2 * g.splits) >= 2) g.splits *= 2;
+    g.kbs = (ng + g.splits - 1) / g.splits;
+    g.splits = (ng + g.kbs - 1) / g.kbs;
+    g.part = g.splits > 1 ? (size_t)g.tiles * g.splits * G6M * G6N * 4 : 0;
+    g.ws = align_up(g.part, 256) + align_up((size_t)m * k * 2, 256);  // partials, then the f16 activation
+    return g;
+}
+
+int64_t gemm6_chunk_rows(int64_t k) {
+    const int64_t cap = (((int64_t)1 << 31) - 1) / (2 * k) / 64 * 64;  // f16 activation offsets in 32 bits
+    return cap;
+}
+
+}  // namespace
+
+size_t gemm6_workspace_bytes(int64_t m, int64_t n, int64_t k) {
+    if (m <= 0 || n <= 0 || k <= 0 || k % QK_K || k > (1 << 24)) return (size_t)-1;
+    const int64_t mc = std::min(m, gemm6_chunk_rows(k));
+    if (mc <= 0) return (size_t)-1;
+    Gemm6Plan g = gemm6_plan(mc, n, k);
+    if (g.tiles > GEMM_MAX_TILES) return (size_t)-1;
+    size_t ws = g.ws;
+    if (m % mc) ws = std::max(ws, gemm6_plan(m % mc, n, k).ws);
+    return ws;
+}
+
+hipError_t launch_gemm6(const WLayout &w, int64_t n, int64_t k, const ActPlanes &x, int64_t m, float *y, int32_t *S,
+                        int32_t *Smin, void *ws, size_t ws_bytes, hipStream_t s) {
+    if (w.type != TYPE_Q6_K) return hipErrorNotSupported;
+    if (!w.slab || !w.d || !y || !x.qs || !x.d || m <= 0 || n <= 0 || k <= 0 || k % QK_K) return hipErrorInvalidValue;
+    if (m > 0x7fffffff || n > 0x7fffffff || k > (1 << 24) || w.ng != k / QK_K) return hipErrorInvalidValue;
+    if ((int64_t)16 * w.rb_stride >= ((int64_t)1 << 31)) return hipErrorNotSupported;
+    if ((S == nullptr) != (Smin == nullptr)) return hipErrorInvalidValue;
+    const int64_t mc = std::min(m, gemm6_chunk_rows(k));
+    if (mc <= 0) return hipErrorNotSupported;
+    const int ng = w.ng;
+    for (int64_t r0 = 0; r0 < m; r0 += mc) {
+        const int64_t mm = std::min(mc, m - r0);
+        const Gemm6Plan g = gemm6_plan(mm, n, k);
+        if (g.tiles > GEMM_MAX_TILES) return hipErrorNotSupported;
+        if (!ws || ws_bytes < g.ws) return hipErrorInvalidValue;
+        uint16_t *x16 = (uint16_t *)((uint8_t *)ws + align_up(g.part, 256));
+        const int64_t n4 = mm * k / 4;
+        qs_to_f16_kernel<<<(unsigned)((n4 + 255) / 256), 256, 0, s>>>(x.qs + r0 * k, n4, x16);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        Gemm6Params p;
+        p.w = w.slab;
+        p.wd = w.d;
+        p.rb_stride = w.rb_stride;
+        p.ng = ng;
+        p.x16 = x16;
+        p.xd = x.d + r0 * ng;
+        p.y = y + r0 * n;
+        p.m = (int)mm;
+        p.n = (int)n;
+        p.k = (int)k;
+        p.ntm = g.ntm;
+        p.tiles = g.tiles;
+        p.splits = g.splits;
+        p.kbs = g.kbs;
+        p.items = g.tiles * g.splits;
+        p.per_xcd = (p.items + NXCD6 - 1) / NXCD6;
+        p.part = (float *)ws;
+        p.S = S ? S + r0 * n * ng : nullptr;
+        p.Smin = Smin ? Smin + r0 * n * ng : nullptr;
+        const unsigned grid = (unsigned)(p.per_xcd * NXCD6);
+        if (S) gemm_q6k_kernel<true><<<grid, 256, 0, s>>>(p);
+        else gemm_q6k_kernel<false><<<grid, 256, 0, s>>>(p);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+        if (g.splits > 1) {
+            e = launch_splitk_reduce(p.part, p.y, p.m, p.n, g.ntm, G6M, g.splits, g.tiles, s);
+            if (e != hipSuccess) return e;
+        }
+    }
+    return hipSuccess;
+}
+
+}  // namespace aq

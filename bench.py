@@ -182,14 +182,15 @@ def measure(ctx, wtype, n, k, m, steps, warmup, seed):
     return wl, step_ms, step_wall, kern_ms, out
 
 
-def measure_prefill(ctx, n, k, m, steps, warmup, seed):
-    """Prefill GEMM at m rows: quantiser kernel + int8 MFMA GEMM (step) and the GEMM alone."""
-    wl = Workload(ctx, 12, n, k, m, seed)
+def measure_prefill(ctx, wtype, n, k, m, steps, warmup, seed):
+    """Prefill GEMM at m rows: quantiser kernel + GEMM (step) and the GEMM alone
+    (Q4_K: int8 MFMA; Q6_K: f16 MFMA after its f16 copy of the quants)."""
+    wl = Workload(ctx, wtype, n, k, m, seed)
     step_ms, _ = time_graph(ctx, wl.step, steps, warmup)
     kern_ms, _ = time_graph(ctx, wl.kernel, steps, warmup)
     ops = 2.0 * m * n * k
     out = {
-        "n": n, "k": k, "m": m, "weight_type": "Q4_K",
+        "n": n, "k": k, "m": m, "weight_type": {12: "Q4_K", 14: "Q6_K"}[wtype],
         "step_us": round(step_ms * 1e3, 3),
         "step_TOPS": round(ops / (step_ms / 1e3) / 1e12, 1),
         "gemm_us": round(kern_ms * 1e3, 3),
@@ -219,10 +220,12 @@ CRATE_CASES = {  # the NIF crate's own kernels: name: (kind, m, n, k)
     "crate_int8_weight_gemv_4096x4096": ("i8w", 1, 4096, 4096),
     "crate_int8_per_token_m512_4096x4096": ("i8i8", 512, 4096, 4096),
 }
-PREFILL_CASES = {  # name: (n, k, m, seed), Q4_K weight
-    "c3_prefill_q4k_5632x2048_m512": (5632, 2048, 512, 3),
-    "c3_prefill_q4k_2048x5632_m512": (2048, 5632, 512, 3),
-    "c4_prefill_q4k_14336x4096_m512": (14336, 4096, 512, 4),
+PREFILL_CASES = {  # name: (weight type, n, k, m, seed)
+    "c3_prefill_q4k_5632x2048_m512": (12, 5632, 2048, 512, 3),
+    "c3_prefill_q4k_2048x5632_m512": (12, 2048, 5632, 512, 3),
+    "c4_prefill_q4k_14336x4096_m512": (12, 14336, 4096, 512, 4),
+    "c2_prefill_q6k_2048x5632_m512": (14, 2048, 5632, 512, 10),  # TinyLlama ffn_down (Q6_K layers)
+    "c2_prefill_q6k_256x2048_m512": (14, 256, 2048, 512, 11),    # TinyLlama attn_v
 }
 
 
@@ -347,8 +350,8 @@ def run_case(ctx, name, steps, warmup):
         w2.free()
         log(f"{name}: step {out['step_us']} us ({out['step_GBps']} GB/s), pre-quantised matvec {out['matvec_us']} us ({out['matvec_GBps']} GB/s)")
         return out
-    n_, k_, m_, seed = PREFILL_CASES[name]
-    out = measure_prefill(ctx, n_, k_, m_, min(steps, 50), min(warmup, 5), seed)
+    wt, n_, k_, m_, seed = PREFILL_CASES[name]
+    out = measure_prefill(ctx, wt, n_, k_, m_, min(steps, 50), min(warmup, 5), seed)
     log(f"{name}: step {out['step_us']} us ({out['step_TOPS']} TOPS), gemm {out['gemm_us']} us ({out['gemm_TOPS']} TOPS, {out['gemm_frac_int8_peak']} of int8 peak)")
     return out
 

@@ -157,6 +157,38 @@ def test_prefill_gemm_extreme_values(ctx):
     check_matmul(ctx, W, x, cond=False)
 
 
+# ----------------------------------------- Q6_K prefill GEMM (f16 MFMA, m > 8)
+@pytest.mark.parametrize("n,k,m", [(256, 2048, 512), (2048, 5632, 512), (32000, 2048, 16)])
+def test_prefill_gemm_q6k(ctx, n, k, m):
+    """TinyLlama attn_v and ffn_down at a 512-token prefill, and the lm_head
+    shape at 16 rows: integer block sums bit-exact, outputs within tolerance."""
+    W = S.make_weight(S.TYPE_Q6_K, n, k, seed=n + k)
+    x = S.make_activation(m, k, seed=m + k)
+    check_matmul(ctx, W, x)
+
+
+@pytest.mark.parametrize("m,n,k", [(9, 100, 256), (63, 129, 768), (65, 300, 512), (130, 257, 1024), (200, 64, 2048)])
+def test_prefill_gemm_q6k_ragged_tiles(ctx, m, n, k):
+    W = S.make_weight(S.TYPE_Q6_K, n, k, seed=m + n + 1)
+    x = S.make_activation(m, k, seed=m * n + 1)
+    check_matmul(ctx, W, x)
+
+
+def test_prefill_gemm_q6k_extreme_values(ctx):
+    """Largest Q6_K . Q8_K sums: every weight value -32 * -32 = 1024 and
+    activation blocks of equal values (every quant -128): each half
+    super-block's f32 MFMA chain reaches exactly -2^24."""
+    n, k, m = 64, 1024, 16
+    rng = np.random.default_rng(6)
+    W = S.make_weight(S.TYPE_Q6_K, n, k, seed=6)
+    W.q[:] = -32
+    W.sc[:] = -32
+    W.blocks = S.pack_q6k(W.d, W.sc, W.q)
+    x = np.repeat(np.abs(rng.standard_normal((m, k // 256))).astype(np.float32) + 0.5, 256, axis=1)
+    x[1::2] = -x[1::2]
+    check_matmul(ctx, W, x, cond=False)
+
+
 # ------------------------------------------------------ batch and K coverage
 @pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 7, 8, 11])
 @pytest.mark.parametrize("wtype", [S.TYPE_Q4_K, S.TYPE_Q6_K, S.TYPE_Q8_0])
