@@ -228,6 +228,15 @@ class Llama:
             return y[:, :na], y[:, na:]
         return self._mm(lw[a], x), self._mm(lw[b], x)
 
+    @classmethod
+    def from_gguf(cls, ctx: Context, path: str, max_seq: int = 4096) -> "Llama":
+        """ArmAI.LlamaCandle.load (llama_candle.rs:35-48): read a llama GGUF file
+        (arm_ai_amd.gguf) and upload its projections to HBM."""
+        from .gguf import load_llama
+
+        _, hw = load_llama(path, max_seq=max_seq)
+        return cls(ctx, hw)
+
     # ------------------------------------------------------------ pieces
     # The work runs on the library's stream; the caller's current stream waits
     # for it on the way out (and it for the caller's on the way in), so tensors
