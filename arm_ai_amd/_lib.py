@@ -84,6 +84,7 @@ SIGNATURES = {
     "aq_llama_argmax": (INT, [P, P, I64, P, P, P, I64]),
     "aq_qmatmul_rmsnorm_f32_device": (INT, [P, P, P, P, P, ctypes.c_float, I64, P, P]),
     "aq_qmatmul_silu_mul_f32_device": (INT, [P, P, P, I64, P]),
+    "aq_qmatmul2_rmsnorm_f32_device": (INT, [P, P, P, P, P, P, ctypes.c_float, I64, P, P, P]),
 }
 
 

@@ -901,3 +901,19 @@ int aq_qmatmul_silu_mul_f32_device(aq_ctx *ctx, const aq_qweight *w, const float
     if (e == hipErrorNotSupported) return fail(AQ_ERR_SHAPE, "k=%lld is larger than the matvec supports", (long long)k);
     return hip_status(e, "matvec silu");
 }
+
+int aq_qmatmul2_rmsnorm_f32_device(aq_ctx *ctx, const aq_qweight *w1, const aq_qweight *w2, const float *d_x,
+                                   const float *d_delta, const float *d_norm_w, float eps, int64_t k, float *d_h_out,
+                                   float *d_dst1, float *d_dst2) {
+    int rc = check_mm(ctx, w1, 1, k);
+    if (rc) return rc;
+    if ((rc = check_mm(ctx, w2, 1, k))) return rc;
+    if (!d_x || !d_norm_w || !d_dst1 || !d_dst2) return fail(AQ_ERR_INVALID_ARG, "null pointer");
+    if (d_h_out && (d_h_out == d_x || d_h_out == d_delta)) return fail(AQ_ERR_INVALID_ARG, "d_h_out aliases an input");
+    if ((rc = use_device(ctx->device))) return rc;
+    const hipError_t e = launch_matvec2_rmsnorm(w1->layout, w1->n, d_dst1, w2->layout, w2->n, d_dst2, k, d_x, d_delta,
+                                                d_norm_w, eps, d_h_out, ctx->stream);
+    if (e == hipErrorNotSupported)
+        return fail(AQ_ERR_SHAPE, "the two-weight fused norm takes Q4_K / Q6_K weights with k <= 8192");
+    return hip_status(e, "matvec2 rmsnorm");
+}

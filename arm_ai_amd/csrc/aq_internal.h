@@ -169,6 +169,12 @@ hipError_t launch_dequant_rows(int wt, const void *table, const float *scales, i
 hipError_t launch_matvec_rmsnorm(const WLayout &w, int64_t n, int64_t k, const float *x, const float *delta,
                                  const float *norm, float eps, float *xout, float *y, hipStream_t s);
 hipError_t launch_matvec_silu(const WLayout &w, int64_t n, int64_t k, const float *gu, float *y, hipStream_t s);
+// Two fused-norm matvecs of the same row in one launch (Q4_K / Q6_K weights
+// w1 and w2, outputs y1 and y2); xout is written once.  hipErrorNotSupported
+// for other types or rows too long to fuse.
+hipError_t launch_matvec2_rmsnorm(const WLayout &w1, int64_t n1, float *y1, const WLayout &w2, int64_t n2, float *y2,
+                                  int64_t k, const float *x, const float *delta, const float *norm, float eps,
+                                  float *xout, hipStream_t s);
 
 // Decode-step glue (k_decode.hip).
 hipError_t launch_embed(const float *table, int64_t vocab, const int64_t *d_tok, int64_t hidden, float *out,

@@ -383,10 +383,12 @@ __device__ __forceinline__ u32x4 silu_mul4(u32x4 g, u32x4 u) {
     return (u32x4){f32_as_u32(o[0]), f32_as_u32(o[1]), f32_as_u32(o[2]), f32_as_u32(o[3])};
 }
 
-template <int TYPE, int B, bool DUMP, bool FUSED, int XF = XF_NONE>
-__global__ __launch_bounds__(NW * 64) void matvec_kernel(MvParams p) {
+// The matvec of one workgroup (bid of nblk): the kernel body, shared by
+// matvec_kernel and by matvec2_kernel, which runs two weights' matvecs on the
+// same input in one launch.
+template <int TYPE, int B, bool DUMP, bool FUSED, int XF>
+__device__ __forceinline__ void matvec_body(const MvParams &p, const int bid, const int nblk, uint8_t *lds) {
     static_assert(XF == XF_NONE || (FUSED && B == 1), "input transforms are for one f32 row");
-    extern __shared__ __align__(16) uint8_t lds[];
     __shared__ float red[NW][B][RB];  // per-wavefront chunk partials of the 8 rows of a row block
     __shared__ float nred[NW];        // XF_NORM: per-wavefront sums of squares
     const int lane = threadIdx.x & 63;
@@ -400,7 +402,7 @@ __global__ __launch_bounds__(NW * 64) void matvec_kernel(MvParams p) {
     const int nrec = p.m * p.ng;
     const int nsteps = p.iters * nsub;
     // a step past the last reads zeros: blockIdx + iters * gridDim >= workgroup iterations
-    auto rb_of = [&](int st) { return (int)(blockIdx.x + (st / nsub) * gridDim.x) * p.rbw + rbo; };
+    auto rb_of = [&](int st) { return (int)(bid + (st / nsub) * nblk) * p.rbw + rbo; };
     auto g_of = [&](int st) { return 8 * (c0 + np * (st % nsub)) + g_l; };
 
     // 1. activation loads of the first records, 2. weight loads of the first
@@ -431,7 +433,7 @@ __global__ __launch_bounds__(NW * 64) void matvec_kernel(MvParams p) {
         float tot = 0.0f;
         for (int w = 0; w < nw; w++) tot += nred[w];
         const float mden = sqrtf(tot / (float)p.k + p.eps);
-        const rsrc_t rxo = buf_rsrc(p.xout, p.xout && blockIdx.x == 0 ? (uint32_t)(p.k * 4) : 0u);
+        const rsrc_t rxo = buf_rsrc(p.xout, p.xout && bid == 0 ? (uint32_t)(p.k * 4) : 0u);
 #pragma unroll
         for (int r = 0; r < PRE; r++) {
             const int t = wave + nw * r;
@@ -500,7 +502,7 @@ __global__ __launch_bounds__(NW * 64) void matvec_kernel(MvParams p) {
         for (int b = 0; b < B; b++) f[b] = 0.0f;
         __syncthreads();
         const int wr = wave < p.rbw ? wave : 0;
-        const int row = ((int)(blockIdx.x + it * gridDim.x) * p.rbw + wr) * RB + r_l;
+        const int row = ((int)(bid + it * nblk) * p.rbw + wr) * RB + r_l;
         const bool ok = wave < p.rbw && lane < RB && row < p.n;
 #pragma unroll
         for (int b = 0; b < B; b++) {
@@ -528,6 +530,23 @@ __global__ __launch_bounds__(NW * 64) void matvec_kernel(MvParams p) {
         load_w<TYPE>(wa, p, rb_of(st + 2), nrb, g_of(st + 2), r_l);
         step(wb, st + 1);
     }
+}
+
+template <int TYPE, int B, bool DUMP, bool FUSED, int XF = XF_NONE>
+__global__ __launch_bounds__(NW * 64) void matvec_kernel(MvParams p) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    matvec_body<TYPE, B, DUMP, FUSED, XF>(p, (int)blockIdx.x, (int)gridDim.x, lds);
+}
+
+// Two matvecs of one f32 row (m = 1) in one launch: workgroups below grid1
+// run weight 1 (type T1, p1), the rest weight 2 (T2, p2).  Both plans use
+// NW wavefronts per workgroup; the dynamic LDS is the larger of the two.
+template <int T1, int T2, int XF>
+__global__ __launch_bounds__(NW * 64) void matvec2_kernel(MvParams p1, MvParams p2, int grid1) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    const int bid = (int)blockIdx.x;
+    if (bid < grid1) matvec_body<T1, 1, false, true, XF>(p1, bid, grid1, lds);  // uniform over the workgroup
+    else matvec_body<T2, 1, false, true, XF>(p2, bid - grid1, (int)gridDim.x - grid1, lds);
 }
 
 // Dynamic LDS above 64 KB has to be allowed per kernel, once.
@@ -610,6 +629,31 @@ struct XfArgs {
     float *xout = nullptr;
 };
 
+// Launch shape of a matvec over n rows of ng groups.
+struct MvPlan {
+    int nch, np, rbw, nw, nsub;
+    int64_t iters, grid;
+};
+MvPlan mv_plan(int64_t n, int ng) {
+    MvPlan P;
+    const int64_t nrb = (n + RB - 1) / RB;
+    // Wavefronts per row block: as few as give MIN_WAVES wavefronts in all
+    // (fewer, longer-lived wavefronts keep two steps of loads in flight and
+    // need no cross-wavefront reduction), at most one per chunk and NW.
+    P.nch = (ng + 7) / 8;  // 8-group chunks per row
+    P.np = 1;
+    while (P.np < NW && P.np < P.nch && nrb * P.np < MIN_WAVES) P.np *= 2;
+    if (P.np > P.nch) P.np = P.nch;
+    P.rbw = NW / P.np;                        // row blocks per workgroup iteration
+    P.nw = P.rbw * P.np;                      // wavefronts per workgroup
+    P.nsub = (P.nch + P.np - 1) / P.np;       // chunks per wavefront per row block
+    const int64_t wg_iters = (nrb + P.rbw - 1) / P.rbw;  // workgroup iterations in total
+    const int64_t target_wg = TARGET_WAVES / P.nw;
+    P.iters = (wg_iters + target_wg - 1) / target_wg;
+    P.grid = (wg_iters + P.iters - 1) / P.iters;
+    return P;
+}
+
 hipError_t matvec_impl(const WLayout &w, int64_t n, int64_t k, const float *x, const ActPlanes *act, int64_t m,
                        float *y, int32_t *S, int32_t *Smin, const XfArgs &xa, hipStream_t s);
 
@@ -630,21 +674,9 @@ hipError_t matvec_impl(const WLayout &w, int64_t n, int64_t k, const float *x, c
     const int ng = w.ng;
     if ((size_t)ng * REC > LDS_CAP) return hipErrorNotSupported;  // k > 124160
     if ((int64_t)8 * n * 4 >= ((int64_t)1 << 31)) return hipErrorNotSupported;  // y of a pass: 32-bit buffer offsets
-    const int64_t nrb = (n + RB - 1) / RB;
-    // Wavefronts per row block: as few as give MIN_WAVES wavefronts in all
-    // (fewer, longer-lived wavefronts keep two steps of loads in flight and
-    // need no cross-wavefront reduction), at most one per chunk and NW.
-    const int nch = (ng + 7) / 8;  // 8-group chunks per row
-    int np = 1;
-    while (np < NW && np < nch && nrb * np < MIN_WAVES) np *= 2;
-    if (np > nch) np = nch;
-    const int rbw = NW / np;                // row blocks per workgroup iteration
-    const int nw = rbw * np;                // wavefronts per workgroup
-    const int nsub = (nch + np - 1) / np;   // chunks per wavefront per row block
-    const int64_t wg_iters = (nrb + rbw - 1) / rbw;  // workgroup iterations in total
-    const int64_t target_wg = TARGET_WAVES / nw;
-    const int64_t iters = (wg_iters + target_wg - 1) / target_wg;
-    const int64_t grid = (wg_iters + iters - 1) / iters;
+    const MvPlan P = mv_plan(n, ng);
+    const int nch = P.nch, np = P.np, rbw = P.rbw, nw = P.nw, nsub = P.nsub;
+    const int64_t iters = P.iters, grid = P.grid;
     if ((int64_t)iters * nsub > 0x7fffffff) return hipErrorInvalidValue;
     // the fused norm needs the whole row among each wavefront's first PRE records
     if (xa.xf == XF_NORM && ng > PRE * nw) return hipErrorNotSupported;
@@ -722,6 +754,87 @@ hipError_t launch_matvec_silu(const WLayout &w, int64_t n, int64_t k, const floa
     XfArgs xa;
     xa.xf = XF_SILU;
     return matvec_impl(w, n, k, gu, nullptr, 1, y, nullptr, nullptr, xa, s);
+}
+
+namespace {
+// MvParams of a one-row fused-norm matvec, or an error.
+hipError_t norm_params(const WLayout &w, int64_t n, int64_t k, const float *x, const XfArgs &xa, float *y,
+                       MvParams &p, int64_t &grid, size_t &lds) {
+    const int type = w.type;
+    if (type != TYPE_Q4_K && type != TYPE_Q6_K) return hipErrorNotSupported;
+    if (!w.slab || n <= 0 || k <= 0 || k % QK_K || n > 0x7fffffff || k > 0x7fffffff || !y || !x) return hipErrorInvalidValue;
+    if (type == TYPE_Q6_K && !w.d) return hipErrorInvalidValue;
+    if (w.ng != groups_of(type, k) || ((uintptr_t)x & 15) || !xa.norm) return hipErrorInvalidValue;
+    const int ng = w.ng;
+    if ((int64_t)8 * n * 4 >= ((int64_t)1 << 31)) return hipErrorNotSupported;
+    const MvPlan P = mv_plan(n, ng);
+    if (ng > PRE * P.nw || P.nw != NW || P.iters * P.nsub > 0x7fffffff) return hipErrorNotSupported;
+    p = MvParams{};
+    p.w = w.slab;
+    p.wd = w.d;
+    p.rb_stride = w.rb_stride;
+    p.n = (int)n;
+    p.k = (int)k;
+    p.ng = ng;
+    p.nch = P.nch;
+    p.np = P.np;
+    p.rbw = P.rbw;
+    p.nw = P.nw;
+    p.nsub = P.nsub;
+    p.m = 1;
+    p.iters = (int)P.iters;
+    p.x = x;
+    p.xdelta = xa.delta;
+    p.xnorm = xa.norm;
+    p.xout = xa.xout;
+    p.eps = xa.eps;
+    p.y = y;
+    grid = P.grid;
+    lds = (size_t)ng * REC;
+    return hipSuccess;
+}
+
+template <int T1, int T2>
+hipError_t launch_two(const MvParams &p1, const MvParams &p2, int64_t g1, int64_t g2, size_t lds, hipStream_t s) {
+    if (lds > 64 * 1024) {
+        static std::once_flag once;
+        static hipError_t err = hipSuccess;
+        std::call_once(once, [] {
+            err = hipFuncSetAttribute((const void *)matvec2_kernel<T1, T2, XF_NORM>,
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)LDS_CAP);
+        });
+        if (err != hipSuccess) return err;
+    }
+    matvec2_kernel<T1, T2, XF_NORM><<<(unsigned)(g1 + g2), NW * 64, lds, s>>>(p1, p2, (int)g1);
+    return hipGetLastError();
+}
+}  // namespace
+
+hipError_t launch_matvec2_rmsnorm(const WLayout &w1, int64_t n1, float *y1, const WLayout &w2, int64_t n2, float *y2,
+                                  int64_t k, const float *x, const float *delta, const float *norm, float eps,
+                                  float *xout, hipStream_t s) {
+    if ((delta && ((uintptr_t)delta & 15)) || !norm || ((uintptr_t)norm & 15) || (xout && ((uintptr_t)xout & 15)))
+        return hipErrorInvalidValue;
+    XfArgs xa;
+    xa.xf = XF_NORM;
+    xa.delta = delta;
+    xa.norm = norm;
+    xa.eps = eps;
+    xa.xout = xout;
+    MvParams p1, p2;
+    int64_t g1, g2;
+    size_t l1, l2;
+    hipError_t e = norm_params(w1, n1, k, x, xa, y1, p1, g1, l1);
+    if (e != hipSuccess) return e;
+    xa.xout = nullptr;  // the residual is written once, by weight 1's workgroup 0
+    if ((e = norm_params(w2, n2, k, x, xa, y2, p2, g2, l2)) != hipSuccess) return e;
+    if (g1 + g2 > 0x7fffffff) return hipErrorNotSupported;
+    const size_t lds = l1 > l2 ? l1 : l2;
+    const int t1 = w1.type, t2 = w2.type;
+    if (t1 == TYPE_Q4_K && t2 == TYPE_Q6_K) return launch_two<TYPE_Q4_K, TYPE_Q6_K>(p1, p2, g1, g2, lds, s);
+    if (t1 == TYPE_Q4_K && t2 == TYPE_Q4_K) return launch_two<TYPE_Q4_K, TYPE_Q4_K>(p1, p2, g1, g2, lds, s);
+    if (t1 == TYPE_Q6_K && t2 == TYPE_Q4_K) return launch_two<TYPE_Q6_K, TYPE_Q4_K>(p1, p2, g1, g2, lds, s);
+    return launch_two<TYPE_Q6_K, TYPE_Q6_K>(p1, p2, g1, g2, lds, s);
 }
 
 }  // namespace aq

@@ -35,7 +35,7 @@ step does not use torch ops: it is this library's decode-step glue kernels
 grouped-query attention in one launch, and a first-maximum argmax that writes
 the next token and advances the device-side position) around the GPU
 QMatMuls, whose matvec forms its own input where that input is
-rms_norm(x + delta) or silu(g) * u: 6 launches per layer.  Projections that share an input and a
+rms_norm(x + delta) or silu(g) * u: 5 launches per layer (wq|wk and wv share one).  Projections that share an input and a
 type are uploaded as one weight (wq|wk, w1|w3: rows concatenated), so each
 pair is one matmul launch.  The KV cache, the RoPE tables and every
 intermediate buffer are preallocated for ``max_seq`` positions, so every
@@ -54,6 +54,8 @@ import numpy as np
 
 from . import synth
 from .qmatmul import Context, GgmlDType, QMatMul, QTensor
+
+_NORM2 = (GgmlDType.Q4K, GgmlDType.Q6K)  # types the two-weight fused-norm launch takes
 
 
 @dataclass
@@ -352,10 +354,11 @@ class Llama:
         (both device memory); leaves the logits in self._logits, the next token
         in self._tok and in self._hist[pos], and pos + 1 in self._pos.
 
-        Per layer six launches: the QMatMuls of wq|wk and wv take
-        rms_norm(x + delta) as their input (formed inside the matvec, which also
-        writes the residual x + delta once), attention (RoPE, KV write, GQA),
-        wo, w1|w3 on rms_norm(h + wo), w2 on silu(g) * u."""
+        Per layer five launches: the QMatMuls of wq|wk and wv, one launch for
+        both, take rms_norm(x + delta) as their input (formed inside the
+        matvec, which also writes the residual x + delta once), attention
+        (RoPE, KV write, GQA), wo, w1|w3 on rms_norm(h + wo), w2 on
+        silu(g) * u."""
         from . import _lib
 
         L = _lib.load()
@@ -375,12 +378,17 @@ class Llama:
         delta = None
         for li, lw in enumerate(self.layers):
             an = self.attn_norm[li]
-            if "wqk" in lw:
-                mm_norm(lw["wqk"], cur, delta, an, ptr(self._qk), h_out=other)
+            if "wqk" in lw and lw["wqk"].dtype in _NORM2 and lw["wv"].dtype in _NORM2:
+                # wq|wk and wv in one launch
+                chk(L.aq_qmatmul2_rmsnorm_f32_device(c, lw["wqk"].handle, lw["wv"].handle, ptr(cur), delta, ptr(an),
+                                                     eps, cfg.hidden, ptr(other), ptr(self._qk), ptr(self._v)))
             else:
-                mm_norm(lw["wq"], cur, delta, an, ptr(self._qk), h_out=other)
-                mm_norm(lw["wk"], cur, delta, an, ptr(self._qk) + 4 * cfg.n_head * hd)
-            mm_norm(lw["wv"], cur, delta, an, ptr(self._v))
+                if "wqk" in lw:
+                    mm_norm(lw["wqk"], cur, delta, an, ptr(self._qk), h_out=other)
+                else:
+                    mm_norm(lw["wq"], cur, delta, an, ptr(self._qk), h_out=other)
+                    mm_norm(lw["wk"], cur, delta, an, ptr(self._qk) + 4 * cfg.n_head * hd)
+                mm_norm(lw["wv"], cur, delta, an, ptr(self._v))
             chk(L.aq_llama_attn_decode(c, ptr(self._qk), ptr(self._v), ptr(self.cos), ptr(self.sin), ptr(self._pos),
                                        ptr(self.k_cache[li]), ptr(self.v_cache[li]), cfg.n_head, cfg.n_kv_head, hd,
                                        cfg.max_seq, ptr(self._att)))

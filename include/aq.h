@@ -261,6 +261,14 @@ int aq_llama_attn_decode(aq_ctx *ctx, const float *d_qk, const float *d_v, const
 int aq_qmatmul_rmsnorm_f32_device(aq_ctx *ctx, const aq_qweight *w, const float *d_x, const float *d_delta,
                                   const float *d_norm_w, float eps, int64_t k, float *d_h_out, float *d_dst);
 int aq_qmatmul_silu_mul_f32_device(aq_ctx *ctx, const aq_qweight *w, const float *d_gu, int64_t k, float *d_dst);
+/* Two aq_qmatmul_rmsnorm_f32_device calls on the same input (w1 -> d_dst1,
+ * w2 -> d_dst2, both k columns, Q4_K or Q6_K) in one kernel launch, with the
+ * same results as the two calls; d_h_out is written once.  For the
+ * projections that share an input but not a type (TinyLlama Q4_K_M: wq|wk
+ * and wv). */
+int aq_qmatmul2_rmsnorm_f32_device(aq_ctx *ctx, const aq_qweight *w1, const aq_qweight *w2, const float *d_x,
+                                   const float *d_delta, const float *d_norm_w, float eps, int64_t k, float *d_h_out,
+                                   float *d_dst1, float *d_dst2);
 /* Greedy pick: the first index of the largest of d_x[0..n) goes to *d_tok
  * and, when d_hist is non-null and 0 <= *d_pos < hist_len, to
  * d_hist[*d_pos]; then *d_pos += 1. */

@@ -267,3 +267,40 @@ def test_matvec_fused_errors(env):
     assert L.aq_qmatmul_rmsnorm_f32_device(ctx.handle, mm.handle, p, None, p, ctypes.c_float(1e-5), 16384, p,
                                            p) == lib.AQ_ERR_INVALID_ARG
     mm.free()
+
+
+@pytest.mark.parametrize("t1,n1,t2,n2,k", [(12, 2304, 14, 256, 2048), (12, 1000, 12, 300, 4096), (14, 512, 14, 96, 1024)])
+def test_matvec2_fused_rmsnorm_equals_two_calls(env, t1, n1, t2, n2, k):
+    """One launch over two weights gives the bytes the two single calls give."""
+    import arm_ai_amd as A
+    from arm_ai_amd import synth as S
+
+    torch, lib, ctx = env
+    L = lib.load()
+    rng = np.random.default_rng(n1 + n2)
+    _, m1 = _weight(A, S, t1, n1, k, ctx, seed=n1)
+    _, m2 = _weight(A, S, t2, n2, k, ctx, seed=n2 + 1)
+    x, d = _dev(torch, rng.standard_normal(k).astype(np.float32)), _dev(torch, rng.standard_normal(k).astype(np.float32))
+    wn = _dev(torch, (1 + 0.05 * rng.standard_normal(k)).astype(np.float32))
+    outs = [torch.full((n,), np.nan, dtype=torch.float32, device="cuda:0") for n in (n1, n2, n1, n2)]
+    h1 = torch.full((k,), np.nan, dtype=torch.float32, device="cuda:0")
+    h2 = torch.full((k,), np.nan, dtype=torch.float32, device="cuda:0")
+    torch.cuda.synchronize()
+    eps = ctypes.c_float(1e-5)
+    lib.check(L.aq_qmatmul2_rmsnorm_f32_device(ctx.handle, m1.handle, m2.handle, x.data_ptr(), d.data_ptr(),
+                                               wn.data_ptr(), eps, k, h1.data_ptr(), outs[0].data_ptr(),
+                                               outs[1].data_ptr()))
+    lib.check(L.aq_qmatmul_rmsnorm_f32_device(ctx.handle, m1.handle, x.data_ptr(), d.data_ptr(), wn.data_ptr(), eps,
+                                              k, h2.data_ptr(), outs[2].data_ptr()))
+    lib.check(L.aq_qmatmul_rmsnorm_f32_device(ctx.handle, m2.handle, x.data_ptr(), d.data_ptr(), wn.data_ptr(), eps,
+                                              k, None, outs[3].data_ptr()))
+    ctx.synchronize()
+    o = [t.cpu().numpy() for t in outs]
+    assert np.array_equal(o[0], o[2]) and np.array_equal(o[1], o[3])
+    assert np.array_equal(h1.cpu().numpy(), h2.cpu().numpy())
+    # a Q8_0 weight is not taken by the two-weight launch
+    _, m3 = _weight(A, S, 8, 64, k, ctx, seed=3)
+    assert L.aq_qmatmul2_rmsnorm_f32_device(ctx.handle, m1.handle, m3.handle, x.data_ptr(), None, wn.data_ptr(), eps,
+                                            k, None, outs[0].data_ptr(), outs[1].data_ptr()) == lib.AQ_ERR_SHAPE
+    for mm in (m1, m2, m3):
+        mm.free()
