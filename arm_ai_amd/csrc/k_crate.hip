@@ -163,6 +163,112 @@ __global__ __launch_bounds__(256) void int8_mfma_kernel(const int8_t *__restrict
 }
 
 // ---------------------------------------------------------------------------
+// int8 x int8 -> f32, m >= 32 and k a multiple of 64: a 128 x 128 output tile
+// per 4-wavefront workgroup (two per CU), each wavefront a 64 x 64 block of
+// four v_mfma_i32_32x32x32_i8 tiles.  Both operands (row-major, k
+// contiguous) are copied global -> LDS by buffer loads into LDS, 64 k-bytes
+// of the tile's 128 activation rows and 128 weight rows per stage, in a ring
+// of four stages issued three steps ahead.  A row's four 16-byte chunks sit at
+// positions c ^ ((r >> 2) & 3), so the 16-byte reads of 16 consecutive rows
+// (64-byte row stride) fall on distinct banks.  Work items are numbered so
+// that all m-tiles of one n-tile run on one XCD (workgroups are dealt to the
+// 8 XCDs round-robin) and share its L2 copy of the weight rows.
+// The i32 sums are exact; out = ((f32)acc * sa) * sw as the crate.
+// ---------------------------------------------------------------------------
+constexpr int I8T = 128, I8K = 64, I8NST = 4, I8XCD = 8;
+constexpr int I8STAGE = 2 * I8T * I8K;  // activation rows, then weight rows
+constexpr int I8COPIES = 4;             // copy instructions per wavefront and stage
+
+__global__ __launch_bounds__(256, 2) void int8_gemm_kernel(const int8_t *__restrict__ a, const int8_t *__restrict__ w,
+                                                           const float *__restrict__ act_scales, float act_scale,
+                                                           const float *__restrict__ w_scales, int m, int n, int k,
+                                                           float *__restrict__ out, int ntm, int items, int per_xcd) {
+    __shared__ __align__(16) uint8_t lds[I8NST * I8STAGE];
+    const int xcd = blockIdx.x % I8XCD, local = blockIdx.x / I8XCD;
+    const int item = xcd * per_xcd + local;
+    if (local >= per_xcd || item >= items) return;  // uniform over the workgroup
+    const int tn = item / ntm, tm = item - tn * ntm;
+    const int m0 = tm * I8T, n0 = tn * I8T;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1, wn = wave & 1, h = lane >> 5, l32 = lane & 31;
+
+    const rsrc_t ra = buf_rsrc(a, (uint32_t)((int64_t)m * k));
+    const rsrc_t rw = buf_rsrc(w, (uint32_t)((int64_t)n * k));
+    // copy instruction i of this wavefront fills chunks (2*wave + i)*64 + lane
+    // of a 128 x 64-byte region: row r = chunk / 4, position chunk % 4
+    uint32_t aoff[2], woff[2];
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const int t = (2 * wave + i) * 64 + lane, r = t >> 2, cp = t & 3;
+        const int c = cp ^ ((r >> 2) & 3);
+        aoff[i] = (uint32_t)((m0 + r) * k + 16 * c);
+        woff[i] = (uint32_t)((n0 + r) * k + 16 * c);
+    }
+    auto issue = [&](int ks) {  // step ks's copies (past k: unused data or zeros)
+        uint8_t *st = lds + (ks & (I8NST - 1)) * I8STAGE;
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            buf_to_lds16(ra, st + 1024 * (2 * wave + i), aoff[i], ks * I8K);
+            buf_to_lds16(rw, st + I8T * I8K + 1024 * (2 * wave + i), woff[i], ks * I8K);
+        }
+    };
+    auto frag = [&](const uint8_t *base, int R, int s) {  // 16 k-bytes of row R, slice s, half h
+        const int C = 2 * s + h;
+        return *(const v4i *)(base + R * I8K + 16 * (C ^ ((R >> 2) & 3)));
+    };
+
+    v16i acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[i][j][r] = 0;
+
+    const int nk = k / I8K;
+    issue(0);
+    issue(1);
+    issue(2);
+    for (int ks = 0; ks < nk; ks++) {
+        wait_vmcnt<2 * I8COPIES>();  // this step's copies have landed (two later steps' may be in flight)
+        stage_barrier();             // ... for every wavefront; and step ks - 1's stage is free
+        issue(ks + 3);
+        const uint8_t *st = lds + (ks & (I8NST - 1)) * I8STAGE;
+#pragma unroll
+        for (int s2 = 0; s2 < 2; s2++) {
+            v4i af[2], bf[2];
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
+                af[t] = frag(st, 64 * wm + 32 * t + l32, s2);
+                bf[t] = frag(st + I8T * I8K, 64 * wn + 32 * t + l32, s2);
+            }
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+#pragma unroll
+                for (int j = 0; j < 2; j++) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
+        }
+    }
+    wait_vmcnt<0>();  // no copy may still be landing when the workgroup ends
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const int col = n0 + 64 * wn + 32 * j + l32;
+        if (col >= n) continue;
+        const float sw = w_scales[col];
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int row = m0 + 64 * wm + 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
+                if (row < m) {
+                    const float sa = act_scales ? act_scales[row] : act_scale;
+                    out[(int64_t)row * n + col] = ((float)acc[i][j][r] * sa) * sw;
+                }
+            }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // quantize_int8_per_token: one workgroup per row.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void quantize_int8_per_token_kernel(const float *__restrict__ a, int64_t k,
@@ -451,6 +557,13 @@ hipError_t launch_int8_matmul(const int8_t *a, const int8_t *w, const float *act
                               const float *w_scales, int64_t m, int64_t n, int64_t k, float *out, hipStream_t s) {
     if (!a || !w || !w_scales || !out || !dims_ok(m, n, k)) return hipErrorInvalidValue;
     if (m == 0) return hipSuccess;
+    if (m >= 32 && k % I8K == 0 && k <= 0x7fffffff && m * k < ((int64_t)1 << 31) && n * k < ((int64_t)1 << 31)) {
+        const int ntm = (int)blocks_for(m, I8T), ntn = (int)blocks_for(n, I8T);
+        const int items = ntm * ntn, per_xcd = (items + I8XCD - 1) / I8XCD;
+        int8_gemm_kernel<<<(unsigned)(per_xcd * I8XCD), 256, 0, s>>>(a, w, act_scales, act_scale, w_scales, (int)m,
+                                                                     (int)n, (int)k, out, ntm, items, per_xcd);
+        return hipGetLastError();
+    }
     if (m >= 32) {
         const dim3 grid(blocks_for(n, 128), blocks_for(m, 128));
         if (grid.y > 65535) return hipErrorInvalidValue;

@@ -25,7 +25,8 @@ def _rel(a, b):
 
 
 @pytest.mark.parametrize("m,n,k", [(1, 300, 256), (3, 65, 37), (8, 128, 1000), (9, 40, 64), (40, 200, 96),
-                                   (130, 70, 4096), (64, 4096, 4096)])
+                                   (130, 70, 4096), (64, 4096, 4096), (33, 129, 64), (257, 300, 128),
+                                   (512, 384, 1024)])
 def test_int8_matmuls_bitexact(ctx, m, n, k):
     a = RNG.integers(-127, 128, (m, k)).astype(np.int8)
     w = RNG.integers(-127, 128, (n, k)).astype(np.int8)
