@@ -139,6 +139,11 @@ size_t gemm_workspace_bytes(int type, int64_t m, int64_t n, int64_t k);
 size_t gemm6_workspace_bytes(int64_t m, int64_t n, int64_t k);
 hipError_t launch_gemm6(const WLayout &w, int64_t n, int64_t k, const ActPlanes &x, int64_t m, float *y, int32_t *S,
                         int32_t *Smin, void *ws, size_t ws_bytes, hipStream_t s);
+// The Q8_0 GEMM on int8 MFMA (k_gemm8.hip), reached through launch_gemm /
+// gemm_workspace_bytes; its workspace holds the split-K partial tiles.
+size_t gemm8_workspace_bytes(int64_t m, int64_t n, int64_t k);
+hipError_t launch_gemm8(const WLayout &w, int64_t n, int64_t k, const ActPlanes &x, int64_t m, float *y, int32_t *S,
+                        int32_t *Smin, void *ws, size_t ws_bytes, hipStream_t s);
 // Sums split-K partial tiles [tiles][splits][gbm][128] into y in split order.
 hipError_t launch_splitk_reduce(const float *part, float *y, int m, int n, int ntm, int gbm, int splits, int tiles,
                                 hipStream_t s);

@@ -202,11 +202,16 @@ __global__ __launch_bounds__(256, 2) void int8_gemm_kernel(const int8_t *__restr
     for (int i = 0; i < 2; i++) {
         const int t = (2 * wave + i) * 64 + lane, r = t >> 2, cp = t & 3;
         const int c = cp ^ ((r >> 2) & 3);
-        aoff[i] = (uint32_t)((m0 + r) * k + 16 * c);
-        woff[i] = (uint32_t)((n0 + r) * k + 16 * c);
+        aoff[i] = m0 + r < m ? (uint32_t)((int64_t)(m0 + r) * k + 16 * c) : BUF_OOB;  // rows past m / n read zeros
+        woff[i] = n0 + r < n ? (uint32_t)((int64_t)(n0 + r) * k + 16 * c) : BUF_OOB;
     }
-    auto issue = [&](int ks) {  // step ks's copies (past k: unused data or zeros)
-        uint8_t *st = lds + (ks & (I8NST - 1)) * I8STAGE;
+    const int nk = k / I8K;
+    auto issue = [&](int slot_ks) {
+        // stage slot_ks % 4 gets step slot_ks's data; a step past k (issued
+        // ahead, never read) reloads the last step, so no copy addresses
+        // memory past the rows
+        uint8_t *st = lds + (slot_ks & (I8NST - 1)) * I8STAGE;
+        const int ks = min(slot_ks, nk - 1);
 #pragma unroll
         for (int i = 0; i < 2; i++) {
             buf_to_lds16(ra, st + 1024 * (2 * wave + i), aoff[i], ks * I8K);
@@ -226,7 +231,6 @@ __global__ __launch_bounds__(256, 2) void int8_gemm_kernel(const int8_t *__restr
 #pragma unroll
             for (int r = 0; r < 16; r++) acc[i][j][r] = 0;
 
-    const int nk = k / I8K;
     issue(0);
     issue(1);
     issue(2);

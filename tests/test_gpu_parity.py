@@ -223,6 +223,56 @@ def test_single_row_weight(ctx):
     check_matmul(ctx, W, x)
 
 
+# ------------------------------------------ Q8_0 prefill GEMM (int8 MFMA, m > 8)
+@pytest.mark.parametrize("n,k,m", [(768, 2048, 256), (4096, 4096, 16)])
+def test_prefill_gemm_q8_0(ctx, n, k, m):
+    """A 256-token prefill and a 16-row batch (four k-splits per tile):
+    integer block sums bit-exact, outputs within tolerance."""
+    W = S.make_weight(S.TYPE_Q8_0, n, k, seed=n + k + 2)
+    x = S.make_activation(m, k, seed=m + k + 2)
+    check_matmul(ctx, W, x)
+
+
+@pytest.mark.parametrize(
+    "m,n,k",
+    [(9, 100, 256), (63, 129, 768), (65, 300, 512), (130, 257, 1024), (200, 64, 2048),
+     (33, 50, 32), (40, 70, 96), (17, 130, 1056)],
+)
+def test_prefill_gemm_q8_0_ragged_tiles(ctx, m, n, k):
+    """Partial tiles in m and n, and k an odd number of blocks (32, 96, 1056:
+    the last step's second block is padding)."""
+    W = S.make_weight(S.TYPE_Q8_0, n, k, seed=m + n + 2)
+    x = S.make_activation(m, k, seed=m * n + 2)
+    check_matmul(ctx, W, x)
+
+
+def test_prefill_gemm_q8_0_extreme_values(ctx):
+    """Largest Q8_0 . Q8_0 block sums: every weight quant -128 and activation
+    blocks of equal values (every quant +-127), |S| = 32 * 128 * 127, the
+    widest sum the GEMM's offset accumulator (1.5 * 2^23 + S read as f32)
+    must hold exactly."""
+    n, k, m = 64, 1024, 16
+    rng = np.random.default_rng(7)
+    W = S.make_weight(S.TYPE_Q8_0, n, k, seed=7)
+    W.q[:] = -128
+    W.blocks = S.pack_q8_0(W.d, W.q)
+    x = np.repeat(rng.standard_normal((m, k // 32)).astype(np.float32), 32, axis=1)
+    x[1::2] = -np.abs(x[1::2])
+    x[::2] = np.abs(x[::2])
+    check_matmul(ctx, W, x, cond=False)
+
+
+def test_prefill_gemm_q8_0_subnormal_and_zero_scales(ctx):
+    W = S.make_weight(S.TYPE_Q8_0, 128, 1024, seed=18)
+    rng = np.random.default_rng(18)
+    d = (rng.integers(1, 1024, size=W.d.shape).astype(np.uint16)).view(np.float16)
+    d[::5] = 0
+    W.blocks = S.pack_q8_0(d, W.q)
+    W.d = d
+    x = S.make_activation(40, 1024, seed=19)
+    check_matmul(ctx, W, x, cond=False)
+
+
 @pytest.mark.parametrize("wtype", [S.TYPE_Q4_K, S.TYPE_Q6_K, S.TYPE_Q8_0])
 def test_subnormal_and_zero_scales(ctx, wtype):
     W = S.make_weight(wtype, 128, 1024, seed=8)
