@@ -130,25 +130,34 @@ __global__ __launch_bounds__(DEC_THREADS) void silu_mul_kernel(const float *__re
 // workgroup of each group stores the rotated k and v at pos for later steps,
 // and every workgroup uses its own LDS copy for position pos, so no
 // workgroup waits for another.
-//   scores: one position per thread (q broadcast from LDS, k_p as float4s);
-//   softmax: block max, exp, block sum, p = e / sum;
-//   output: thread (d4, g) sums positions p = g (mod 4096/hd) of p * v_p[d]
-//     for four consecutive d (float4 reads, four positions in flight), the
-//     groups' partials then summed in LDS in two levels.
+//   scores: HD4 = hd/4 lanes per position, each a float4 of q and of k_p, the
+//     partial dots summed over the lanes (coalesced 1 KB key reads);
+//   softmax: block max, e_p = exp(s_p - max), block sum;
+//   output: thread (d4, g) sums positions p = g (mod 4096/hd) of e_p * v_p[d]
+//     for four consecutive d (float4 reads), the groups' partials are summed
+//     in LDS in two levels, and the result is divided by the sum of the e_p.
+// The value rows do not depend on the scores: each thread's first ones are
+// loaded before the softmax's barriers.
 constexpr int ATT_MAX_SEQ = 8192;
 constexpr int ATT_MAX_HD = 256;
+template <int HD4>
 __global__ __launch_bounds__(WIDE_THREADS) void attn_decode_kernel(
     const float *__restrict__ qk, const float *__restrict__ v, const float *__restrict__ cosb,
     const float *__restrict__ sinb, const int64_t *__restrict__ d_pos, float *__restrict__ kc, float *__restrict__ vc,
-    int n_head, int n_kv, int hd, int max_seq, float *__restrict__ out) {
-    __shared__ __align__(16) float qs[ATT_MAX_HD];
-    __shared__ __align__(16) float ks[ATT_MAX_HD];
-    __shared__ __align__(16) float vs[ATT_MAX_HD];
+    int n_head, int n_kv, int max_seq, float *__restrict__ out) {
+    constexpr int hd = 4 * HD4;
+    // value rows loaded ahead into registers, in flight across the softmax
+    // (fewer for wide heads: a 1024-thread workgroup has 128 VGPRs per lane)
+    constexpr int VPRE = HD4 <= 16 ? 8 : 4;
+    constexpr int G = WIDE_THREADS / HD4;    // position groups of the output pass
+    __shared__ __align__(16) float qs[hd];
+    __shared__ __align__(16) float ks[hd];
+    __shared__ __align__(16) float vs[hd];
     __shared__ float sc[ATT_MAX_SEQ];
     __shared__ float red[WIDE_THREADS / 64];
     __shared__ float4 part4[WIDE_THREADS];
-    __shared__ float4 sc4[16 * ATT_MAX_HD / 4];
-    const int head = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    __shared__ float4 sc4[16 * HD4];
+    const int head = blockIdx.x, tid = threadIdx.x;
     const int rep = n_head / n_kv, kvh = head / rep;
     const int pos = (int)*d_pos;
     if (pos < 0 || pos >= max_seq) return;  // uniform; the host checks, this never indexes out of the cache
@@ -156,42 +165,78 @@ __global__ __launch_bounds__(WIDE_THREADS) void attn_decode_kernel(
     const float *k0 = qk + (int64_t)n_head * hd + (int64_t)kvh * hd;
     const float *v0 = v + (int64_t)kvh * hd;
     const float *cr = cosb + (int64_t)pos * (hd / 2), *sr = sinb + (int64_t)pos * (hd / 2);
-    if (tid < hd / 2) {
-        const int i = tid;
-        const float c = cr[i], s = sr[i];
-        const float a = q0[2 * i], b = q0[2 * i + 1];
-        qs[2 * i] = a * c - b * s;
-        qs[2 * i + 1] = a * s + b * c;
-        const float ka = k0[2 * i], kb = k0[2 * i + 1];
-        ks[2 * i] = ka * c - kb * s;
-        ks[2 * i + 1] = ka * s + kb * c;
-    } else if (tid >= 512 && tid < 512 + hd) {
-        vs[tid - 512] = v0[tid - 512];
-    }
-    __syncthreads();
     float *kh = kc + (int64_t)kvh * max_seq * hd;
     float *vh = vc + (int64_t)kvh * max_seq * hd;
+
+    // rotation inputs
+    float ra = 0.0f, rb = 0.0f, rka = 0.0f, rkb = 0.0f, rc = 0.0f, rsn = 0.0f, rv = 0.0f;
+    if (tid < hd / 2) {
+        rc = cr[tid];
+        rsn = sr[tid];
+        ra = q0[2 * tid];
+        rb = q0[2 * tid + 1];
+        rka = k0[2 * tid];
+        rkb = k0[2 * tid + 1];
+    } else if (tid >= 512 && tid < 512 + hd) {
+        rv = v0[tid - 512];
+    }
+    if (tid < hd / 2) {
+        qs[2 * tid] = ra * rc - rb * rsn;
+        qs[2 * tid + 1] = ra * rsn + rb * rc;
+        ks[2 * tid] = rka * rc - rkb * rsn;
+        ks[2 * tid + 1] = rka * rsn + rkb * rc;
+    } else if (tid >= 512 && tid < 512 + hd) {
+        vs[tid - 512] = rv;
+    }
+    __syncthreads();
     if (head % rep == 0 && tid < hd) {
         kh[(int64_t)pos * hd + tid] = ks[tid];
         vh[(int64_t)pos * hd + tid] = vs[tid];
     }
-    // scores q . k_p / sqrt(hd), p = 0..pos (k_pos from LDS): one position per
-    // thread, q read from LDS by broadcast, k_p as hd/4 float4 loads
+
+    // scores q . k_p / sqrt(hd), p = 0..pos: HD4 lanes share a key row (lane
+    // c holds float4 c of q), so one load instruction reads 64 / HD4
+    // consecutive rows, 1 KB contiguous; the row's dot is summed over its
+    // lanes by a butterfly within the lane group
+    constexpr int RPI = 64 / HD4;  // rows per load instruction
+    constexpr int SU_K = 4;        // rows per lane with loads in flight together
+    const int lane = tid & 63, wave = tid >> 6;
+    const int c = lane % HD4;
+    const float4 qv = ((const float4 *)qs)[c];
+    const float4 *kpos = (const float4 *)ks;
     const float rs = sqrtf((float)hd);
     float mx = -INFINITY;
-    for (int p = tid; p <= pos; p += WIDE_THREADS) {
-        const float4 *kp = (const float4 *)(p == pos ? ks : kh + (int64_t)p * hd);
-        const float4 *q4 = (const float4 *)qs;
-        float d0 = 0.0f, d1 = 0.0f;
-        for (int i = 0; i < hd / 4; i += 2) {
-            const float4 a0 = kp[i], a1 = kp[i + 1];
-            const float4 b0 = q4[i], b1 = q4[i + 1];
-            d0 = __builtin_fmaf(b0.x, a0.x, __builtin_fmaf(b0.y, a0.y, __builtin_fmaf(b0.z, a0.z, __builtin_fmaf(b0.w, a0.w, d0))));
-            d1 = __builtin_fmaf(b1.x, a1.x, __builtin_fmaf(b1.y, a1.y, __builtin_fmaf(b1.z, a1.z, __builtin_fmaf(b1.w, a1.w, d1))));
+    for (int p0 = wave * RPI + lane / HD4; p0 <= pos; p0 += SU_K * (WIDE_THREADS / 64) * RPI) {
+        float4 kv[SU_K];
+#pragma unroll
+        for (int u = 0; u < SU_K; u++) {
+            const int p = p0 + u * (WIDE_THREADS / 64) * RPI;
+            kv[u] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if (p < pos) kv[u] = ((const float4 *)(kh + (int64_t)p * hd))[c];
+            else if (p == pos) kv[u] = kpos[c];
         }
-        const float sv = (d0 + d1) / rs;
-        sc[p] = sv;
-        mx = fmaxf(mx, sv);
+#pragma unroll
+        for (int u = 0; u < SU_K; u++) {
+            const int p = p0 + u * (WIDE_THREADS / 64) * RPI;
+            float d = __builtin_fmaf(qv.x, kv[u].x, __builtin_fmaf(qv.y, kv[u].y,
+                      __builtin_fmaf(qv.z, kv[u].z, qv.w * kv[u].w)));
+#pragma unroll
+            for (int o = HD4 / 2; o >= 1; o >>= 1) d += __shfl_xor(d, o);
+            if (p <= pos) {
+                const float sv = d / rs;
+                if (c == 0) sc[p] = sv;
+                mx = fmaxf(mx, sv);
+            }
+        }
+    }
+
+    // the output pass's first value rows, in flight across the softmax
+    const int d4 = tid % HD4, g = tid / HD4;
+    float4 vp4[VPRE];
+#pragma unroll
+    for (int u = 0; u < VPRE; u++) {
+        const int p = g + u * G;
+        vp4[u] = p < pos ? *(const float4 *)(vh + (int64_t)p * hd + 4 * d4) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
     mx = block_max<WIDE_THREADS>(mx, red);  // its barriers publish sc[]
     float sum = 0.0f;
@@ -200,15 +245,24 @@ __global__ __launch_bounds__(WIDE_THREADS) void attn_decode_kernel(
         sc[p] = e;
         sum += e;
     }
-    sum = block_sum<WIDE_THREADS>(sum, red);
-    for (int p = tid; p <= pos; p += WIDE_THREADS) sc[p] = sc[p] / sum;
-    __syncthreads();
+    sum = block_sum<WIDE_THREADS>(sum, red);  // ... and the e_p
+
     // output: thread (d4, g) takes dims 4*d4..4*d4+3 of positions p = g (mod G)
-    constexpr int SU = 4;  // positions per thread with loads in flight together
-    const int nd4 = hd / 4, G = WIDE_THREADS / nd4;
-    const int d4 = tid % nd4, g = tid / nd4;
     float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    for (int p0 = g; p0 <= pos; p0 += SU * G) {
+    auto axpy = [&](float w, const float4 x) {
+        acc.x = __builtin_fmaf(w, x.x, acc.x);
+        acc.y = __builtin_fmaf(w, x.y, acc.y);
+        acc.z = __builtin_fmaf(w, x.z, acc.z);
+        acc.w = __builtin_fmaf(w, x.w, acc.w);
+    };
+#pragma unroll
+    for (int u = 0; u < VPRE; u++) {
+        const int p = g + u * G;
+        if (p < pos) axpy(sc[p], vp4[u]);
+        else if (p == pos) axpy(sc[p], *(const float4 *)(vs + 4 * d4));
+    }
+    constexpr int SU = 4;  // positions per thread with loads in flight together
+    for (int p0 = g + VPRE * G; p0 <= pos; p0 += SU * G) {
         float4 v4[SU];
 #pragma unroll
         for (int u = 0; u < SU; u++) {
@@ -220,22 +274,18 @@ __global__ __launch_bounds__(WIDE_THREADS) void attn_decode_kernel(
 #pragma unroll
         for (int u = 0; u < SU; u++) {
             const int p = p0 + u * G;
-            const float w = p <= pos ? sc[p] : 0.0f;
-            acc.x = __builtin_fmaf(w, v4[u].x, acc.x);
-            acc.y = __builtin_fmaf(w, v4[u].y, acc.y);
-            acc.z = __builtin_fmaf(w, v4[u].z, acc.z);
-            acc.w = __builtin_fmaf(w, v4[u].w, acc.w);
+            axpy(p <= pos ? sc[p] : 0.0f, v4[u]);
         }
     }
     part4[tid] = acc;
     __syncthreads();
     // sum the G groups: 16 threads per float4 column first add G/16 groups each
     // (G is a multiple of 16: hd <= 256), then 64-thread columns add the 16 results
-    if (tid < 16 * nd4) {
-        const int c4 = tid % nd4, sl = tid / nd4, per = G / 16;
-        float4 t = part4[(sl * per) * nd4 + c4];
+    if (tid < 16 * HD4) {
+        const int c4 = tid % HD4, sl = tid / HD4, per = G / 16;
+        float4 t = part4[(sl * per) * HD4 + c4];
         for (int j = 1; j < per; j++) {
-            const float4 u4 = part4[(sl * per + j) * nd4 + c4];
+            const float4 u4 = part4[(sl * per + j) * HD4 + c4];
             t.x += u4.x;
             t.y += u4.y;
             t.z += u4.z;
@@ -248,10 +298,10 @@ __global__ __launch_bounds__(WIDE_THREADS) void attn_decode_kernel(
         const int dd = tid >> 2, c = tid & 3;
         float o = 0.0f;
         for (int sl = 0; sl < 16; sl++) {
-            const float4 t4 = sc4[sl * nd4 + dd];
+            const float4 t4 = sc4[sl * HD4 + dd];
             o += c == 0 ? t4.x : c == 1 ? t4.y : c == 2 ? t4.z : t4.w;
         }
-        out[(int64_t)head * hd + tid] = o;
+        out[(int64_t)head * hd + tid] = o / sum;
     }
 }
 
@@ -343,8 +393,16 @@ hipError_t launch_attn_decode(const float *qk, const float *v, const float *cosb
     if (n_head <= 0 || n_kv <= 0 || n_head % n_kv || hd < 8 || hd > ATT_MAX_HD || (hd / 4) & (hd / 4 - 1) || hd % 4 ||
         max_seq <= 0 || max_seq > ATT_MAX_SEQ)
         return hipErrorInvalidValue;
-    attn_decode_kernel<<<(unsigned)n_head, WIDE_THREADS, 0, s>>>(qk, v, cosb, sinb, d_pos, kc, vc, (int)n_head,
-                                                                (int)n_kv, (int)hd, (int)max_seq, out);
+    const unsigned grid = (unsigned)n_head;
+    switch (hd / 4) {
+    case 2: attn_decode_kernel<2><<<grid, WIDE_THREADS, 0, s>>>(qk, v, cosb, sinb, d_pos, kc, vc, (int)n_head, (int)n_kv, (int)max_seq, out); break;
+    case 4: attn_decode_kernel<4><<<grid, WIDE_THREADS, 0, s>>>(qk, v, cosb, sinb, d_pos, kc, vc, (int)n_head, (int)n_kv, (int)max_seq, out); break;
+    case 8: attn_decode_kernel<8><<<grid, WIDE_THREADS, 0, s>>>(qk, v, cosb, sinb, d_pos, kc, vc, (int)n_head, (int)n_kv, (int)max_seq, out); break;
+    case 16: attn_decode_kernel<16><<<grid, WIDE_THREADS, 0, s>>>(qk, v, cosb, sinb, d_pos, kc, vc, (int)n_head, (int)n_kv, (int)max_seq, out); break;
+    case 32: attn_decode_kernel<32><<<grid, WIDE_THREADS, 0, s>>>(qk, v, cosb, sinb, d_pos, kc, vc, (int)n_head, (int)n_kv, (int)max_seq, out); break;
+    case 64: attn_decode_kernel<64><<<grid, WIDE_THREADS, 0, s>>>(qk, v, cosb, sinb, d_pos, kc, vc, (int)n_head, (int)n_kv, (int)max_seq, out); break;
+    default: return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 

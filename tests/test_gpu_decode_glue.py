@@ -90,12 +90,17 @@ def _rope(x, c, s):
     return out
 
 
-@pytest.mark.parametrize("n_head,n_kv,hd,pos", [(32, 4, 64, 0), (32, 4, 64, 517), (8, 8, 128, 300), (4, 2, 32, 1023)])
-def test_attn_decode_against_numpy(env, n_head, n_kv, hd, pos):
+@pytest.mark.parametrize(
+    "n_head,n_kv,hd,pos,max_seq",
+    [(32, 4, 64, 0, 1024), (32, 4, 64, 517, 1024), (8, 8, 128, 300, 1024), (4, 2, 32, 1023, 1024),
+     # contexts past the rows each thread loads ahead (one key row, up to
+     # eight value rows per thread), the narrowest and widest heads
+     (32, 4, 64, 4095, 4096), (8, 2, 256, 2500, 4096), (16, 4, 8, 3000, 4096), (8, 1, 128, 1800, 2048)],
+)
+def test_attn_decode_against_numpy(env, n_head, n_kv, hd, pos, max_seq):
     torch, lib, ctx = env
     L = lib.load()
     rng = np.random.default_rng(pos + hd)
-    max_seq = 1024
     qk = rng.standard_normal((n_head + n_kv) * hd).astype(np.float32)
     v = rng.standard_normal(n_kv * hd).astype(np.float32)
     kc = rng.standard_normal((n_kv, max_seq, hd)).astype(np.float32)
