@@ -122,6 +122,30 @@ __global__ __launch_bounds__(DEC_THREADS) void silu_mul_kernel(const float *__re
     out[i] = (g / (1.0f + expf(-g))) * gu[n + i];
 }
 
+// Sum over aligned groups of N lanes (N = 2, 4, 8, 16, 32 or 64), every lane
+// of a group getting the same value: DPP moves within 16-lane rows (quad
+// swaps, half-row mirror, row rotations), cross-lane permutes only between
+// rows.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return u32_as_f32((uint32_t)__builtin_amdgcn_update_dpp(0, (int)f32_as_u32(v), CTRL, 0xF, 0xF, false));
+}
+template <int N>
+__device__ __forceinline__ float lane_group_sum(float v) {
+    static_assert(N == 2 || N == 4 || N == 8 || N == 16 || N == 32 || N == 64, "group of 2..64 lanes");
+    if (N >= 16) {
+        v += dpp_f<0x128>(v);  // row_ror:8
+        v += dpp_f<0x124>(v);  // row_ror:4
+    } else if (N == 8) {
+        v += dpp_f<0x141>(v);  // row_half_mirror: lanes l and 7 - l of each half row
+    }
+    if (N >= 4) v += dpp_f<0x4E>(v);  // quad_perm [2,3,0,1]
+    v += dpp_f<0xB1>(v);              // quad_perm [1,0,3,2]
+    if (N >= 32) v += __shfl_xor(v, 16);
+    if (N >= 64) v += __shfl_xor(v, 32);
+    return v;
+}
+
 // Attention for one query position at *d_pos, one 1024-thread workgroup per
 // query head.  qk = [q (n_head*hd) | k (n_kv*hd)] before rotation, v
 // (n_kv*hd); the caches are [n_kv][max_seq][hd] for this layer.  Each
@@ -220,8 +244,7 @@ __global__ __launch_bounds__(WIDE_THREADS) void attn_decode_kernel(
             const int p = p0 + u * (WIDE_THREADS / 64) * RPI;
             float d = __builtin_fmaf(qv.x, kv[u].x, __builtin_fmaf(qv.y, kv[u].y,
                       __builtin_fmaf(qv.z, kv[u].z, qv.w * kv[u].w)));
-#pragma unroll
-            for (int o = HD4 / 2; o >= 1; o >>= 1) d += __shfl_xor(d, o);
+            d = lane_group_sum<HD4>(d);
             if (p <= pos) {
                 const float sv = d / rs;
                 if (c == 0) sc[p] = sv;
