@@ -211,6 +211,15 @@ MATVEC_CASES = {  # name: (weight type, n, k, m, seed)
     "c4_q6k_128256x4096_b1": (14, 128256, 4096, 1, 7),
     "c4_q6k_128256x4096_b8": (14, 128256, 4096, 8, 9),
 }
+# Reference points, not this library: the vendor's plain int8 x int8 -> int32
+# GEMM (hipBLASLt through torch._int_mm) at the prefill GEMMs' shapes, with no
+# dequantisation work at all -- what the int8 matrix cores reach at M = 512 on
+# this GPU without Q4_K decoding.
+VENDOR_CASES = {  # name: (m, n, k)
+    "ref_vendor_int8_gemm_512x14336x4096": (512, 14336, 4096),
+    "ref_vendor_int8_gemm_512x5632x2048": (512, 5632, 2048),
+    "ref_vendor_int8_gemm_512x2048x5632": (512, 2048, 5632),
+}
 DECODE_CASES = {  # name: (prompt tokens, new tokens, seed)
     "c2_tinyllama_decode": (512, 128, 2),
 }
@@ -321,9 +330,36 @@ def measure_crate(ctx, kind, m, n, k, steps, warmup):
     return out
 
 
+def measure_vendor_int8(m, n, k, steps, warmup):
+    """torch._int_mm (hipBLASLt) on int8 operands of the given shape, the weight
+    rotated over enough copies to exceed the Infinity Cache; HIP events around
+    `steps` back-to-back calls."""
+    import torch
+
+    dev = torch.device("cuda:0")
+    copies = copies_for(n * k)
+    a = torch.randint(-127, 128, (m, k), dtype=torch.int8, device=dev)
+    bs = [torch.randint(-127, 128, (n, k), dtype=torch.int8, device=dev).t() for _ in range(copies)]
+    for i in range(warmup):
+        torch._int_mm(a, bs[i % copies])
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(steps):
+        torch._int_mm(a, bs[i % copies])
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / steps
+    tops = 2.0 * m * n * k / us / 1e6
+    return {"library": "hipBLASLt via torch._int_mm (int8 x int8 -> int32, no dequantisation)", "m": m, "n": n,
+            "k": k, "us": round(us, 3), "TOPS": round(tops, 1), "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4),
+            "rotating_weight_copies": copies}
+
+
 def run_decode_child(name):
-    """Run a decode case in a child process: the driver's torch glue needs torch
-    imported before this library is loaded (one HIP runtime per process)."""
+    """Run a decode (or vendor reference) case in a child process: the driver's
+    torch glue needs torch imported before this library is loaded (one HIP
+    runtime per process)."""
     import subprocess
 
     r = subprocess.run([sys.executable, "-u", os.path.abspath(__file__), "--case", name],
@@ -339,6 +375,10 @@ def run_case(ctx, name, steps, warmup):
     if name in CRATE_CASES:
         out = measure_crate(ctx, *CRATE_CASES[name], steps, warmup)
         log(f"{name}: {out['us']} us ({out.get('GBps', out.get('TOPS'))} {'GB/s' if 'GBps' in out else 'TOPS'})")
+        return out
+    if name in VENDOR_CASES:
+        out = measure_vendor_int8(*VENDOR_CASES[name], min(steps, 50), min(warmup, 5))
+        log(f"{name}: {out['us']} us ({out['TOPS']} TOPS, {out['frac_int8_peak']} of int8 peak)")
         return out
     if name in DECODE_CASES:
         n_prompt, n_new, seed = DECODE_CASES[name]
@@ -376,7 +416,7 @@ def main() -> int:
         print("--steps must be >= 1", file=sys.stderr)
         return 2
 
-    if args.case in DECODE_CASES:
+    if args.case in DECODE_CASES or args.case in VENDOR_CASES:
         import torch  # noqa: F401  (before the library: one HIP runtime per process)
 
     import arm_ai_amd as A
@@ -392,7 +432,7 @@ def main() -> int:
         print(json.dumps({"copy_calibration_bytes": nbytes, "copies": 10}), flush=True)
         return 0
 
-    all_cases = list(MATVEC_CASES) + list(PREFILL_CASES) + list(CRATE_CASES) + list(DECODE_CASES)
+    all_cases = list(MATVEC_CASES) + list(PREFILL_CASES) + list(CRATE_CASES) + list(DECODE_CASES) + list(VENDOR_CASES)
     if args.case is not None and args.case not in all_cases:
         print(f"unknown case {args.case!r}; cases: {', '.join(all_cases)}", file=sys.stderr)
         return 2
@@ -458,6 +498,8 @@ def main() -> int:
         for name in CRATE_CASES:
             extra[name] = run_case(ctx, name, args.steps, args.warmup)
         for name in DECODE_CASES:
+            extra[name] = run_decode_child(name)
+        for name in VENDOR_CASES:
             extra[name] = run_decode_child(name)
         result["extra"] = extra
     else:
