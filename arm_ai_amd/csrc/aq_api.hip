@@ -64,6 +64,7 @@ int fail(int code, const char *fmt, ...) {
 int block_elems(int type) {
     switch (type) {
     case AQ_TYPE_Q4_K:
+    case AQ_TYPE_Q5_K:
     case AQ_TYPE_Q6_K: return QK_K;
     case AQ_TYPE_Q8_0: return QK8_0;
     default: return 0;
@@ -72,6 +73,7 @@ int block_elems(int type) {
 int block_bytes(int type) {
     switch (type) {
     case AQ_TYPE_Q4_K: return 144;
+    case AQ_TYPE_Q5_K: return 176;
     case AQ_TYPE_Q6_K: return 210;
     case AQ_TYPE_Q8_0: return 34;
     default: return 0;

@@ -12,6 +12,7 @@ constexpr int QK_K = 256;
 constexpr int QK8_0 = 32;
 constexpr int TYPE_Q8_0 = 8;
 constexpr int TYPE_Q4_K = 12;
+constexpr int TYPE_Q5_K = 13;
 constexpr int TYPE_Q6_K = 14;
 constexpr int TYPE_Q8_K = 15;
 
@@ -22,6 +23,8 @@ constexpr int TYPE_Q8_K = 15;
 // upload is lossless; same bytes, moved):
 //   Q4_K (9 pieces = 144 B):  piece 0 = d f16, dmin f16, scales[12];
 //                             pieces 1..8 = qs[0..127] in GGUF order.
+//   Q5_K (11 pieces = 176 B): the GGUF block in order: piece 0 as Q4_K,
+//                             pieces 1..2 = qh[0..31], 3..10 = qs[0..127].
 //   Q6_K (13 pieces = 208 B + d plane): pieces 0..7 = ql[0..127],
 //                             8..11 = qh[0..63], 12 = scales[16]; the f16 d of
 //                             each super-block goes to a separate plane.
@@ -50,7 +53,7 @@ struct WLayout {
 };
 
 __host__ __device__ constexpr int slabs_of(int type) {
-    return type == TYPE_Q4_K ? 9 : type == TYPE_Q6_K ? 13 : type == TYPE_Q8_0 ? 17 : 0;
+    return type == TYPE_Q4_K ? 9 : type == TYPE_Q5_K ? 11 : type == TYPE_Q6_K ? 13 : type == TYPE_Q8_0 ? 17 : 0;
 }
 inline int groups_of(int type, int64_t k) {
     return type == TYPE_Q8_0 ? (int)((k / QK8_0 + 7) / 8) : (int)(k / QK_K);

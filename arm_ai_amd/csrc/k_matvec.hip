@@ -96,13 +96,18 @@ __device__ __forceinline__ int dot16(const uint32_t q[4], const int4 x, int acc)
     return acc;
 }
 
-// ------------------------------------------------------------------ Q4_K
-// Super-block: piece 0 = d, dmin, 12 scale bytes; piece 1 + 2c + h = qs bytes
+// ------------------------------------------------------------ Q4_K, Q5_K
+// Super-block: piece 0 = d, dmin, 12 scale bytes; piece QP + 2c + h = qs bytes
 // 32c + 16h .. +15, whose low nibbles are elements 64c + 16h + i (sub-block
 // 2c) and high nibbles elements 64c + 32 + 16h + i (sub-block 2c + 1).
-template <int B, bool DUMP>
-__device__ __forceinline__ void dot_q4k(const Wt<TYPE_Q4_K> &W, const uint8_t *lds, int ng, int g, int m,
-                                        float (&f)[B], int (&So)[B], int (&Smo)[B]) {
+// Q4_K: QP = 1.  Q5_K: QP = 3, pieces 1 + h = qh bytes 16h .. +15, and bit s
+// of qh[l] is bit 4 of element 32s + l (bit 2c for the low nibbles of chunk
+// c, bit 2c + 1 for its high nibbles).
+template <int B, bool DUMP, int TYPE>
+__device__ __forceinline__ void dot_q45k(const Wt<TYPE> &W, const uint8_t *lds, int ng, int g, int m,
+                                         float (&f)[B], int (&So)[B], int (&Smo)[B]) {
+    constexpr bool FIVE = TYPE == TYPE_Q5_K;
+    constexpr int QP = FIVE ? 3 : 1;
     const uint32_t u0 = W.pc[0].y, u1 = W.pc[0].z, u2 = W.pc[0].w;
     // candle's utmp form of GGML get_scale_min_k4 (6-bit scales and mins)
     const uint32_t sc03 = u0 & 0x3F3F3F3Fu;
@@ -120,10 +125,19 @@ __device__ __forceinline__ void dot_q4k(const Wt<TYPE_Q4_K> &W, const uint8_t *l
         for (int b = 0; b < B; b++) il[b] = ih[b] = 0;
 #pragma unroll
         for (int h = 0; h < 2; h++) {
-            const uint4 q = W.pc[1 + 2 * c + h];
-            const uint32_t lo[4] = {q.x & 0x0F0F0F0Fu, q.y & 0x0F0F0F0Fu, q.z & 0x0F0F0F0Fu, q.w & 0x0F0F0F0Fu};
-            const uint32_t hi[4] = {(q.x >> 4) & 0x0F0F0F0Fu, (q.y >> 4) & 0x0F0F0F0Fu, (q.z >> 4) & 0x0F0F0F0Fu,
-                                    (q.w >> 4) & 0x0F0F0F0Fu};
+            const uint4 q = W.pc[QP + 2 * c + h];
+            uint32_t lo[4] = {q.x & 0x0F0F0F0Fu, q.y & 0x0F0F0F0Fu, q.z & 0x0F0F0F0Fu, q.w & 0x0F0F0F0Fu};
+            uint32_t hi[4] = {(q.x >> 4) & 0x0F0F0F0Fu, (q.y >> 4) & 0x0F0F0F0Fu, (q.z >> 4) & 0x0F0F0F0Fu,
+                              (q.w >> 4) & 0x0F0F0F0Fu};
+            if (FIVE) {
+                const uint4 qh = W.pc[1 + h];
+                const uint32_t hw[4] = {qh.x, qh.y, qh.z, qh.w};
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    lo[i] |= ((hw[i] >> (2 * c)) & 0x01010101u) << 4;
+                    hi[i] |= ((hw[i] >> (2 * c + 1)) & 0x01010101u) << 4;
+                }
+            }
 #pragma unroll
             for (int b = 0; b < B; b++) {
                 if (b < m) {
@@ -261,7 +275,8 @@ __device__ __forceinline__ void group_dot(const Wt<TYPE> &W, const uint8_t *lds,
         dot_q80<B, DUMP>(*(const Wt<TYPE_Q8_0> *)&W, lds, p.ng, g, p.m, f, p, row, valid);
     } else {
         int So[B], Smo[B];
-        if (TYPE == TYPE_Q4_K) dot_q4k<B, DUMP>(*(const Wt<TYPE_Q4_K> *)&W, lds, p.ng, g, p.m, f, So, Smo);
+        if (TYPE == TYPE_Q4_K) dot_q45k<B, DUMP, TYPE_Q4_K>(*(const Wt<TYPE_Q4_K> *)&W, lds, p.ng, g, p.m, f, So, Smo);
+        else if (TYPE == TYPE_Q5_K) dot_q45k<B, DUMP, TYPE_Q5_K>(*(const Wt<TYPE_Q5_K> *)&W, lds, p.ng, g, p.m, f, So, Smo);
         else dot_q6k<B, DUMP>(*(const Wt<TYPE_Q6_K> *)&W, lds, p.ng, g, p.m, f, So, Smo);
         if (DUMP && valid) {
 #pragma unroll
@@ -660,7 +675,7 @@ hipError_t matvec_impl(const WLayout &w, int64_t n, int64_t k, const float *x, c
 hipError_t matvec_impl(const WLayout &w, int64_t n, int64_t k, const float *x, const ActPlanes *act, int64_t m,
                        float *y, int32_t *S, int32_t *Smin, const XfArgs &xa, hipStream_t s) {
     const int type = w.type;
-    if (type != TYPE_Q4_K && type != TYPE_Q6_K && type != TYPE_Q8_0) return hipErrorInvalidValue;
+    if (type != TYPE_Q4_K && type != TYPE_Q5_K && type != TYPE_Q6_K && type != TYPE_Q8_0) return hipErrorInvalidValue;
     const int blk = type == TYPE_Q8_0 ? QK8_0 : QK_K;
     if (!w.slab || m < 0 || n <= 0 || k <= 0 || k % blk || n > 0x7fffffff || k > 0x7fffffff || !y)
         return hipErrorInvalidValue;
@@ -721,6 +736,7 @@ hipError_t matvec_impl(const WLayout &w, int64_t n, int64_t k, const float *x, c
         hipError_t e;
         switch (type) {
         case TYPE_Q4_K: e = launch_t<TYPE_Q4_K>(B, p, (unsigned)grid, lds, S != nullptr, xa.xf, s); break;
+        case TYPE_Q5_K: e = launch_t<TYPE_Q5_K>(B, p, (unsigned)grid, lds, S != nullptr, xa.xf, s); break;
         case TYPE_Q6_K: e = launch_t<TYPE_Q6_K>(B, p, (unsigned)grid, lds, S != nullptr, xa.xf, s); break;
         default: e = launch_t<TYPE_Q8_0>(B, p, (unsigned)grid, lds, S != nullptr, xa.xf, s); break;
         }

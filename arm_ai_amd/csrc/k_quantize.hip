@@ -100,7 +100,7 @@ hipError_t launch_quantize_q8_0(const float *x, int64_t m, int64_t k, ActPlanes 
 template <int TYPE>
 __global__ __launch_bounds__(256) void repack_kernel(const uint8_t *__restrict__ src, int64_t n, int64_t nblk,
                                                      int ng, uint8_t *__restrict__ slab, uint16_t *__restrict__ dpl) {
-    constexpr int BYTES = TYPE == TYPE_Q4_K ? 144 : TYPE == TYPE_Q6_K ? 210 : 34;
+    constexpr int BYTES = TYPE == TYPE_Q4_K ? 144 : TYPE == TYPE_Q5_K ? 176 : TYPE == TYPE_Q6_K ? 210 : 34;
     constexpr int S = slabs_of(TYPE);
     const int64_t rb_stride = (int64_t)ng * S * 128;
     const int64_t total = n * nblk * BYTES;
@@ -114,6 +114,9 @@ __global__ __launch_bounds__(256) void repack_kernel(const uint8_t *__restrict__
             const int piece = o < 16 ? 0 : 1 + (o - 16) / 16;
             const int w = o < 16 ? o : (o - 16) & 15;
             rbp[(b * S + piece) * 128 + w] = src[i];
+        } else if (TYPE == TYPE_Q5_K) {
+            // the 176 bytes are 11 pieces in order: byte o -> piece o / 16
+            rbp[(b * S + (o >> 4)) * 128 + (o & 15)] = src[i];
         } else if (TYPE == TYPE_Q6_K) {
             if (o < 208) {
                 // ql 0..127 -> pieces 0..7, qh 128..191 -> 8..11, scales 192..207 -> 12
@@ -144,6 +147,7 @@ hipError_t launch_repack(int type, const uint8_t *src, int64_t n, int64_t k, uin
     const unsigned grid = 8192;
     switch (type) {
     case TYPE_Q4_K: repack_kernel<TYPE_Q4_K><<<grid, 256, 0, s>>>(src, n, nblk, ng, dst_slab, dst_d); break;
+    case TYPE_Q5_K: repack_kernel<TYPE_Q5_K><<<grid, 256, 0, s>>>(src, n, nblk, ng, dst_slab, dst_d); break;
     case TYPE_Q6_K:
         if (!dst_d) return hipErrorInvalidValue;
         repack_kernel<TYPE_Q6_K><<<grid, 256, 0, s>>>(src, n, nblk, ng, dst_slab, dst_d);

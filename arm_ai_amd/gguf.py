@@ -22,7 +22,7 @@ the quantized projections as raw GGUF blocks (memory-mapped, uploaded to HBM
 by aq_qweight_upload), the norm weights as f32, and the token embedding
 dequantized to f32 as candle does for its embedding table.  Dequantization
 follows candle's ``to_float`` f32 formulas (restated from the GGML block
-definitions: Q4_K d*sc*q - dmin*m, Q6_K d*sc*(q-32), Q8_0 d*q); the
+definitions: Q4_K and Q5_K d*sc*q - dmin*m, Q6_K d*sc*(q-32), Q8_0 d*q); the
 embedding only feeds the f32 glue, which is tolerance-checked.
 """
 from __future__ import annotations
@@ -47,8 +47,8 @@ _SCALAR = {T_U8: "<B", T_I8: "<b", T_U16: "<H", T_I16: "<h", T_U32: "<I", T_I32:
 # ggml tensor types read here: (elements per block, bytes per block)
 GGML_F32, GGML_F16 = 0, 1
 TYPE_SIZES = {GGML_F32: (1, 4), GGML_F16: (1, 2), synth.TYPE_Q8_0: (32, 34), synth.TYPE_Q4_K: (256, 144),
-              synth.TYPE_Q6_K: (256, 210)}
-QUANT_TYPES = (synth.TYPE_Q4_K, synth.TYPE_Q6_K, synth.TYPE_Q8_0)
+              synth.TYPE_Q5_K: (256, 176), synth.TYPE_Q6_K: (256, 210)}
+QUANT_TYPES = (synth.TYPE_Q4_K, synth.TYPE_Q5_K, synth.TYPE_Q6_K, synth.TYPE_Q8_0)
 
 
 class GGUFError(ValueError):
@@ -176,7 +176,7 @@ class GGUFFile:
         """A 2-D quantized weight as candle's QTensor (n rows, k columns)."""
         ti = self.tensor(name)
         if ti.type not in QUANT_TYPES or len(ti.dims) != 2:
-            raise GGUFError(f"tensor {name}: a 2-D Q4_K / Q6_K / Q8_0 weight is needed, got type {ti.type} "
+            raise GGUFError(f"tensor {name}: a 2-D Q4_K / Q5_K / Q6_K / Q8_0 weight is needed, got type {ti.type} "
                             f"with dims {ti.dims}")
         k, n = ti.dims
         return QTensor(GgmlDType(ti.type), (n, k), self.raw(name))
@@ -217,8 +217,9 @@ def dequantize(type_: int, raw: np.ndarray, n_elements: int) -> np.ndarray:
         d = _f16(b[:, 0:2])
         q = b[:, 2:34].view(np.int8).astype(np.float32)
         return (q * d[:, None]).reshape(-1)[:n_elements]
-    if type_ == synth.TYPE_Q4_K:
-        b = raw.reshape(-1, 144)
+    if type_ in (synth.TYPE_Q4_K, synth.TYPE_Q5_K):
+        five = type_ == synth.TYPE_Q5_K
+        b = raw.reshape(-1, 176 if five else 144)
         d, dmin = _f16(b[:, 0:2]), _f16(b[:, 2:4])
         s = b[:, 4:16].astype(np.uint32)
         sc = np.empty((b.shape[0], 8), np.uint32)
@@ -227,8 +228,12 @@ def dequantize(type_: int, raw: np.ndarray, n_elements: int) -> np.ndarray:
         mn[:, 0:4] = s[:, 4:8] & 63
         sc[:, 4:8] = (s[:, 8:12] & 0xF) | ((s[:, 0:4] >> 6) << 4)
         mn[:, 4:8] = (s[:, 8:12] >> 4) | ((s[:, 4:8] >> 6) << 4)
-        qs = b[:, 16:144].reshape(-1, 4, 32)
-        q = np.stack([qs & 0xF, qs >> 4], axis=2).reshape(-1, 8, 32).astype(np.float32)  # [blk][sub][l]
+        qs = b[:, 48:176].reshape(-1, 4, 32) if five else b[:, 16:144].reshape(-1, 4, 32)
+        q = np.stack([qs & 0xF, qs >> 4], axis=2).reshape(-1, 8, 32).astype(np.int32)  # [blk][sub][l]
+        if five:  # bit s of qh[l] is bit 4 of element 32s + l
+            qh = b[:, 16:48].astype(np.int32)
+            q = q + 16 * ((qh[:, None, :] >> np.arange(8)[None, :, None]) & 1)
+        q = q.astype(np.float32)
         d1 = d[:, None] * sc.astype(np.float32)
         m1 = dmin[:, None] * mn.astype(np.float32)
         return (d1[:, :, None] * q - m1[:, :, None]).reshape(-1)[:n_elements]

@@ -91,6 +91,12 @@ def tinyllama_q4km_types(cfg: LlamaConfig, layer: int) -> dict[str, int]:
     }
 
 
+# The Q5_K_M files of the same models: Q5_K where Q4_K_M has Q4_K.
+def tinyllama_q5km_types(cfg: LlamaConfig, layer: int) -> dict[str, int]:
+    return {name: (synth.TYPE_Q5_K if t == synth.TYPE_Q4_K else t)
+            for name, t in tinyllama_q4km_types(cfg, layer).items()}
+
+
 def weight_shapes(cfg: LlamaConfig) -> dict[str, tuple[int, int]]:
     """(n, k) of each per-layer projection (candle's (out, in))."""
     hd = cfg.head_dim

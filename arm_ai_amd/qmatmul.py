@@ -30,6 +30,7 @@ class GgmlDType(IntEnum):
 
     Q8_0 = 8
     Q4K = 12
+    Q5K = 13
     Q6K = 14
     Q8K = 15
 
@@ -39,7 +40,8 @@ class GgmlDType(IntEnum):
 
     @property
     def type_size(self) -> int:
-        return {GgmlDType.Q8_0: 34, GgmlDType.Q4K: 144, GgmlDType.Q6K: 210, GgmlDType.Q8K: 292}[self]
+        return {GgmlDType.Q8_0: 34, GgmlDType.Q4K: 144, GgmlDType.Q5K: 176, GgmlDType.Q6K: 210,
+                GgmlDType.Q8K: 292}[self]
 
 
 class QMatMulError(ValueError):

@@ -7,6 +7,7 @@ configurations prescribe:
 
 * Q4_K: d, dmin = f16(|N(0, 0.02)|); 6-bit scales and mins ~ U[0, 63];
   4-bit quants ~ U[0, 15].
+* Q5_K: as Q4_K with 5-bit quants ~ U[0, 31].
 * Q6_K: d = f16(|N(0, 0.02)|); int8 sub-scales ~ U[-32, 31]; 6-bit quants
   ~ U[0, 63] (value q - 32).
 * Q8_0: d = f16(|N(0, 0.02)|); int8 quants ~ U[-127, 127].
@@ -14,7 +15,7 @@ configurations prescribe:
 
 Generators draw element-level arrays from ``numpy.random.default_rng(seed)``
 (PCG64) and pack them into GGUF block bytes with the GGUF layout (block
-formats: Q4_K 144 B, Q6_K 210 B, Q8_0 34 B).  The element arrays are kept so
+formats: Q4_K 144 B, Q5_K 176 B, Q6_K 210 B, Q8_0 34 B).  The element arrays are kept so
 tests can compute exact answers without going through any unpacking code.
 f32 -> f16 uses numpy's IEEE round-to-nearest-even conversion, the same
 rounding the reference's `half` crate uses (shape_ops.rs:1492-1503).
@@ -30,12 +31,13 @@ QK8_0 = 32
 TYPE_Q4_0 = 2
 TYPE_Q8_0 = 8
 TYPE_Q4_K = 12
+TYPE_Q5_K = 13
 TYPE_Q6_K = 14
 TYPE_Q8_K = 15
 
-BLOCK_BYTES = {TYPE_Q4_K: 144, TYPE_Q6_K: 210, TYPE_Q8_0: 34, TYPE_Q8_K: 292}
-BLOCK_ELEMS = {TYPE_Q4_K: QK_K, TYPE_Q6_K: QK_K, TYPE_Q8_0: QK8_0, TYPE_Q8_K: QK_K}
-TYPE_NAMES = {TYPE_Q4_K: "q4_k", TYPE_Q6_K: "q6_k", TYPE_Q8_0: "q8_0", TYPE_Q8_K: "q8_k"}
+BLOCK_BYTES = {TYPE_Q4_K: 144, TYPE_Q5_K: 176, TYPE_Q6_K: 210, TYPE_Q8_0: 34, TYPE_Q8_K: 292}
+BLOCK_ELEMS = {TYPE_Q4_K: QK_K, TYPE_Q5_K: QK_K, TYPE_Q6_K: QK_K, TYPE_Q8_0: QK8_0, TYPE_Q8_K: QK_K}
+TYPE_NAMES = {TYPE_Q4_K: "q4_k", TYPE_Q5_K: "q5_k", TYPE_Q6_K: "q6_k", TYPE_Q8_0: "q8_0", TYPE_Q8_K: "q8_k"}
 
 
 @dataclass
@@ -47,10 +49,10 @@ class QWeight:
     k: int
     blocks: np.ndarray  # uint8 [n, nb * block_bytes], GGUF AoS layout
     d: np.ndarray  # float16 [n, nb]
-    dmin: np.ndarray | None  # float16 [n, nb] (Q4_K only)
-    sc: np.ndarray | None  # Q4_K uint8 [n, nb, 8]; Q6_K int8 [n, nb, 16]
-    mn: np.ndarray | None  # Q4_K uint8 [n, nb, 8]
-    q: np.ndarray  # Q4_K uint8 [n,nb,256] in [0,15]; Q6_K int8 [n,nb,256] in [-32,31]; Q8_0 int8 [n,nb,32]
+    dmin: np.ndarray | None  # float16 [n, nb] (Q4_K, Q5_K)
+    sc: np.ndarray | None  # Q4_K / Q5_K uint8 [n, nb, 8]; Q6_K int8 [n, nb, 16]
+    mn: np.ndarray | None  # Q4_K / Q5_K uint8 [n, nb, 8]
+    q: np.ndarray  # Q4_K uint8 [n,nb,256] in [0,15]; Q5_K in [0,31]; Q6_K int8 in [-32,31]; Q8_0 int8 [n,nb,32]
 
     @property
     def nbytes(self) -> int:
@@ -59,7 +61,7 @@ class QWeight:
     def dequantize(self) -> np.ndarray:
         """f64 [n, k] element values from the element arrays (GGML formulas)."""
         d = self.d.astype(np.float64)[..., None]
-        if self.type == TYPE_Q4_K:
+        if self.type in (TYPE_Q4_K, TYPE_Q5_K):
             sc = np.repeat(self.sc.astype(np.float64), 32, axis=-1)
             mn = np.repeat(self.mn.astype(np.float64), 32, axis=-1)
             v = d * sc * self.q.astype(np.float64) - self.dmin.astype(np.float64)[..., None] * mn
@@ -97,6 +99,26 @@ def pack_q4k(d, dmin, sc, mn, q) -> np.ndarray:
     qq = q.astype(np.uint8).reshape(n, nb, 4, 2, 32)  # [c][lo/hi][l]
     out[..., 16:144] = (qq[..., 0, :] | (qq[..., 1, :] << 4)).reshape(n, nb, 128)
     return out.reshape(n, nb * 144)
+
+
+def pack_q5k(d, dmin, sc, mn, q) -> np.ndarray:
+    """Pack Q5_K element arrays (q in [0, 31]) into 176-byte blocks:
+    d f16 @0, dmin f16 @2, the 12 scale/min bytes @4 packed as Q4_K's,
+    qh @16: bit s of qh[l] = bit 4 of element 32s + l,
+    qs @48: qs[32c+l] = (q[64c+l] & 15) | (q[64c+32+l] & 15) << 4.
+    """
+    n, nb = d.shape
+    q = q.astype(np.uint8)
+    q4 = pack_q4k(d, dmin, sc, mn, q & 15).reshape(n, nb, 144)
+    out = np.empty((n, nb, 176), dtype=np.uint8)
+    out[..., 0:16] = q4[..., 0:16]
+    hb = ((q >> 4) & 1).reshape(n, nb, 8, 32)  # [sub-block s][l]
+    qh = np.zeros((n, nb, 32), dtype=np.uint8)
+    for s_ in range(8):
+        qh |= hb[..., s_, :] << s_
+    out[..., 16:48] = qh
+    out[..., 48:176] = q4[..., 16:144]
+    return out.reshape(n, nb * 176)
 
 
 def pack_q6k(d, sc, q) -> np.ndarray:
@@ -143,6 +165,13 @@ def make_weight(type_: int, n: int, k: int, seed: int = 0, rng: np.random.Genera
         mn = rng.integers(0, 64, size=(n, nb, 8), dtype=np.uint8)
         q = rng.integers(0, 16, size=(n, nb, 256), dtype=np.uint8)
         return QWeight(type_, n, k, pack_q4k(d, dmin, sc, mn, q), d, dmin, sc, mn, q)
+    if type_ == TYPE_Q5_K:
+        d = _half_abs_normal(rng, (n, nb))
+        dmin = _half_abs_normal(rng, (n, nb))
+        sc = rng.integers(0, 64, size=(n, nb, 8), dtype=np.uint8)
+        mn = rng.integers(0, 64, size=(n, nb, 8), dtype=np.uint8)
+        q = rng.integers(0, 32, size=(n, nb, 256), dtype=np.uint8)
+        return QWeight(type_, n, k, pack_q5k(d, dmin, sc, mn, q), d, dmin, sc, mn, q)
     if type_ == TYPE_Q6_K:
         d = _half_abs_normal(rng, (n, nb))
         sc = rng.integers(-32, 32, size=(n, nb, 16), dtype=np.int8)

@@ -122,6 +122,7 @@ static inline int8_t sat_i8(float v) {
 size_t orc_type_block_bytes(int type) {
     switch (type) {
     case ORC_Q4_K: return ORC_Q4K_BYTES;
+    case ORC_Q5_K: return ORC_Q5K_BYTES;
     case ORC_Q6_K: return ORC_Q6K_BYTES;
     case ORC_Q8_0: return ORC_Q8_0_BYTES;
     case ORC_Q8_K: return ORC_Q8K_BYTES;
@@ -132,6 +133,7 @@ size_t orc_type_block_bytes(int type) {
 int64_t orc_type_block_elems(int type) {
     switch (type) {
     case ORC_Q4_K:
+    case ORC_Q5_K:
     case ORC_Q6_K:
     case ORC_Q8_K: return ORC_QK_K;
     case ORC_Q8_0: return ORC_QK8_0;
@@ -241,6 +243,16 @@ static void q4k_unpack(const uint8_t *qs, int8_t aux8[256]) {
         }
 }
 
+/* Q5_K (GGML block_q5_K; candle BlockQ5K): the Q4_K nibbles plus a fifth
+ * bit, bit s of qh[l] for element 32s + l (sub-block s):
+ *   element 64c + l      = (qs[32c+l] & 0xF) + 16 * (qh[l] >> 2c & 1)
+ *   element 64c + 32 + l = (qs[32c+l] >> 4)  + 16 * (qh[l] >> (2c+1) & 1) */
+static void q5k_unpack(const uint8_t *qh, const uint8_t *qs, int8_t aux8[256]) {
+    q4k_unpack(qs, aux8);
+    for (int s = 0; s < 8; s++)
+        for (int l = 0; l < 32; l++) aux8[32 * s + l] = (int8_t)(aux8[32 * s + l] + 16 * ((qh[l] >> s) & 1));
+}
+
 /* Q6_K element order (h<2, l<32; QL = ql+64h, QH = qh+32h, base 128h):
  * e = base+l    : (QL[l]    & 0xF) | ((QH[l] >> 0 & 3) << 4)
  * e = base+32+l : (QL[l+32] & 0xF) | ((QH[l] >> 2 & 3) << 4)
@@ -267,17 +279,20 @@ static void q6k_unpack(const uint8_t *ql, const uint8_t *qh, int8_t aux8[256]) {
  * per block, 8 i32 lane sums aux32[l] += scale * (q8*q4) over groups of 8;
  * sums[l] += (f16(d_w)*d_x) * aux32[l]; sumf -= (f16(dmin_w)*d_x) * sumi
  * with sumi = sum_{j<16} bsums[j]*mins[j/2]; return sumf + sum(sums). */
-float orc_vec_dot_q4k_q8k(int64_t k, const uint8_t *w, const uint8_t *xq) {
+static float q45k_vec_dot(int five, int64_t k, const uint8_t *w, const uint8_t *xq) {
     int64_t nb = k / ORC_QK_K;
     int8_t aux8[256];
     float sums[8] = {0};
     float sumf = 0.0f;
     for (int64_t b = 0; b < nb; b++) {
-        const uint8_t *x = w + b * ORC_Q4K_BYTES;
+        const uint8_t *x = w + b * (five ? ORC_Q5K_BYTES : ORC_Q4K_BYTES);
         const uint8_t *y = xq + b * ORC_Q8K_BYTES;
         const int8_t *q8 = (const int8_t *)(y + 4);
         int32_t aux32[8] = {0};
-        q4k_unpack(x + 16, aux8);
+        if (five)
+            q5k_unpack(x + 16, x + 48, aux8);
+        else
+            q4k_unpack(x + 16, aux8);
         uint8_t scales[8], mins[8];
         q4k_scales_mins(x + 4, scales, mins);
         int32_t sumi = 0;
@@ -304,6 +319,12 @@ float orc_vec_dot_q4k_q8k(int64_t k, const uint8_t *w, const uint8_t *xq) {
     for (int l = 0; l < 8; l++) t += sums[l];
     return sumf + t;
 }
+
+float orc_vec_dot_q4k_q8k(int64_t k, const uint8_t *w, const uint8_t *xq) { return q45k_vec_dot(0, k, w, xq); }
+
+/* BlockQ5K::vec_dot_unopt (vec_dot_q5k_q8k): the same order as Q4_K's with
+ * the 5-bit quants of q5k_unpack (|q8*q5| <= 3968 still fits the i16 aux16). */
+float orc_vec_dot_q5k_q8k(int64_t k, const uint8_t *w, const uint8_t *xq) { return q45k_vec_dot(1, k, w, xq); }
 
 /* BlockQ6K::vec_dot_unopt (vec_dot_q6k_q8k): per 16-element sub-block j,
  * two 8-lane halves, aux32[l] += (f32)scale_j * (f32)(q8*q6) kept in f32
@@ -356,15 +377,19 @@ float orc_vec_dot_q8_0_q8_0(int64_t k, const uint8_t *w, const uint8_t *xq) {
 void orc_block_sums(int type, int64_t k, const uint8_t *w, const uint8_t *xq, int32_t *S,
                     int32_t *Smin) {
     int8_t aux8[256];
-    if (type == ORC_Q4_K) {
+    if (type == ORC_Q4_K || type == ORC_Q5_K) {
+        const int five = type == ORC_Q5_K;
         int64_t nb = k / ORC_QK_K;
         for (int64_t b = 0; b < nb; b++) {
-            const uint8_t *x = w + b * ORC_Q4K_BYTES;
+            const uint8_t *x = w + b * (five ? ORC_Q5K_BYTES : ORC_Q4K_BYTES);
             const uint8_t *y = xq + b * ORC_Q8K_BYTES;
             const int8_t *q8 = (const int8_t *)(y + 4);
             uint8_t scales[8], mins[8];
             q4k_scales_mins(x + 4, scales, mins);
-            q4k_unpack(x + 16, aux8);
+            if (five)
+                q5k_unpack(x + 16, x + 48, aux8);
+            else
+                q4k_unpack(x + 16, aux8);
             int32_t s = 0, sm = 0;
             for (int j = 0; j < 8; j++) {
                 int32_t isum = 0;
@@ -409,7 +434,7 @@ void orc_block_sums(int type, int64_t k, const uint8_t *w, const uint8_t *xq, in
  * rows in parallel.  Same arithmetic as orc_block_sums. */
 int orc_block_sums_mat(int type, int64_t m, int64_t n, int64_t k, const uint8_t *w, const uint8_t *xq,
                        int32_t *S, int32_t *Smin, int nthreads) {
-    if (type != ORC_Q4_K && type != ORC_Q6_K && type != ORC_Q8_0) return -2;
+    if (type != ORC_Q4_K && type != ORC_Q5_K && type != ORC_Q6_K && type != ORC_Q8_0) return -2;
     int64_t wblk = orc_type_block_elems(type);
     if (k <= 0 || k % wblk != 0 || m < 0 || n < 0) return -3;
     const int64_t nblk = k / wblk;
@@ -433,6 +458,7 @@ static int act_type_for(int type) { return type == ORC_Q8_0 ? ORC_Q8_0 : ORC_Q8_
 static float vec_dot(int type, int64_t k, const uint8_t *w, const uint8_t *xq) {
     switch (type) {
     case ORC_Q4_K: return orc_vec_dot_q4k_q8k(k, w, xq);
+    case ORC_Q5_K: return orc_vec_dot_q5k_q8k(k, w, xq);
     case ORC_Q6_K: return orc_vec_dot_q6k_q8k(k, w, xq);
     default: return orc_vec_dot_q8_0_q8_0(k, w, xq);
     }
@@ -451,7 +477,7 @@ int orc_max_threads(void) {
  * with_max_len(512); here OpenMP dynamic chunks of 256 columns). */
 int orc_matmul_preq(int type, int64_t m, int64_t k, int64_t n, const uint8_t *xq, float *dst,
                     const uint8_t *w, int nthreads) {
-    if (type != ORC_Q4_K && type != ORC_Q6_K && type != ORC_Q8_0) return -2;
+    if (type != ORC_Q4_K && type != ORC_Q5_K && type != ORC_Q6_K && type != ORC_Q8_0) return -2;
     int64_t wblk = orc_type_block_elems(type);
     if (k <= 0 || k % wblk != 0 || m < 0 || n < 0) return -3;
     size_t row_w = (size_t)(k / wblk) * orc_type_block_bytes(type);
@@ -471,7 +497,7 @@ int orc_matmul_preq(int type, int64_t m, int64_t k, int64_t n, const uint8_t *xq
  * serially with T::VecDotType::from_float, then the column loop. */
 int orc_matmul(int type, int64_t m, int64_t k, int64_t n, const float *lhs, const uint8_t *w,
                float *dst, int nthreads) {
-    if (type != ORC_Q4_K && type != ORC_Q6_K && type != ORC_Q8_0) return -2;
+    if (type != ORC_Q4_K && type != ORC_Q5_K && type != ORC_Q6_K && type != ORC_Q8_0) return -2;
     int64_t wblk = orc_type_block_elems(type);
     if (k <= 0 || k % wblk != 0 || m < 0 || n < 0) return -3;
     int at = act_type_for(type);
@@ -490,7 +516,7 @@ int orc_matmul(int type, int64_t m, int64_t k, int64_t n, const float *lhs, cons
 }
 
 /* GGML dequantisation of one weight row (value = d*sc*q - dmin*m for
- * Q4_K, d*sc*q6 for Q6_K, d*q for Q8_0), f32. */
+ * Q4_K and Q5_K, d*sc*q6 for Q6_K, d*q for Q8_0), f32. */
 int orc_dequantize_row(int type, const uint8_t *w, int64_t k, float *out) {
     int8_t aux8[256];
     if (type == ORC_Q4_K) {
@@ -500,6 +526,19 @@ int orc_dequantize_row(int type, const uint8_t *w, int64_t k, float *out) {
             uint8_t sc[8], mn[8];
             q4k_scales_mins(x + 4, sc, mn);
             q4k_unpack(x + 16, aux8);
+            float d = orc_f16_to_f32(rd_u16(x)), dmin = orc_f16_to_f32(rd_u16(x + 2));
+            for (int e = 0; e < 256; e++)
+                out[b * 256 + e] = d * (float)sc[e / 32] * (float)aux8[e] - dmin * (float)mn[e / 32];
+        }
+        return 0;
+    }
+    if (type == ORC_Q5_K) {
+        if (k % ORC_QK_K) return -3;
+        for (int64_t b = 0; b < k / ORC_QK_K; b++) {
+            const uint8_t *x = w + b * ORC_Q5K_BYTES;
+            uint8_t sc[8], mn[8];
+            q4k_scales_mins(x + 4, sc, mn);
+            q5k_unpack(x + 16, x + 48, aux8);
             float d = orc_f16_to_f32(rd_u16(x)), dmin = orc_f16_to_f32(rd_u16(x + 2));
             for (int e = 0; e < 256; e++)
                 out[b * 256 + e] = d * (float)sc[e / 32] * (float)aux8[e] - dmin * (float)mn[e / 32];

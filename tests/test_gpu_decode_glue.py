@@ -194,7 +194,8 @@ def _weight(A, S, wtype, n, k, ctx, seed):
 
 
 @pytest.mark.parametrize("wtype,n,k,with_delta", [(12, 2304, 2048, True), (14, 256, 2048, False),
-                                                  (12, 1000, 4096, True), (8, 300, 1024, True)])
+                                                  (12, 1000, 4096, True), (8, 300, 1024, True),
+                                                  (13, 2304, 2048, True)])
 def test_matvec_fused_rmsnorm(env, wtype, n, k, with_delta):
     """y = W . rms_norm(x + delta) * w_norm in one launch, against the oracle's
     matmul of the same input formed in numpy; h_out = x + delta exactly."""
@@ -229,7 +230,7 @@ def test_matvec_fused_rmsnorm(env, wtype, n, k, with_delta):
     mm.free()
 
 
-@pytest.mark.parametrize("wtype,n,k", [(12, 2048, 5632), (14, 2048, 5632), (12, 300, 256)])
+@pytest.mark.parametrize("wtype,n,k", [(12, 2048, 5632), (14, 2048, 5632), (12, 300, 256), (13, 2048, 5632)])
 def test_matvec_fused_silu_mul(env, wtype, n, k):
     import oracle as O
 

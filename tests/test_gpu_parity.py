@@ -191,7 +191,7 @@ def test_prefill_gemm_q6k_extreme_values(ctx):
 
 # ------------------------------------------------------ batch and K coverage
 @pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 7, 8, 11])
-@pytest.mark.parametrize("wtype", [S.TYPE_Q4_K, S.TYPE_Q6_K, S.TYPE_Q8_0])
+@pytest.mark.parametrize("wtype", [S.TYPE_Q4_K, S.TYPE_Q5_K, S.TYPE_Q6_K, S.TYPE_Q8_0])
 def test_batches(ctx, wtype, m):
     W = S.make_weight(wtype, 300, 2048, seed=m + wtype)
     x = S.make_activation(m, 2048, seed=100 + m)
@@ -199,7 +199,7 @@ def test_batches(ctx, wtype, m):
 
 
 @pytest.mark.parametrize("k", [256, 512, 5632, 16384, 20480])
-@pytest.mark.parametrize("wtype", [S.TYPE_Q4_K, S.TYPE_Q6_K, S.TYPE_Q8_0])
+@pytest.mark.parametrize("wtype", [S.TYPE_Q4_K, S.TYPE_Q5_K, S.TYPE_Q6_K, S.TYPE_Q8_0])
 @pytest.mark.parametrize("m", [1, 8])
 def test_k_coverage(ctx, wtype, k, m):
     W = S.make_weight(wtype, 70, k, seed=k + m)
@@ -221,6 +221,31 @@ def test_single_row_weight(ctx):
     W = S.make_weight(S.TYPE_Q4_K, 1, 256, seed=3)
     x = S.make_activation(2, 256, seed=3)
     check_matmul(ctx, W, x)
+
+
+# ------------------------------------------------------------ Q5_K (matvec at any m)
+@pytest.mark.parametrize("n,k,m", [(5632, 2048, 1), (2048, 5632, 1), (14336, 4096, 1), (4096, 14336, 8),
+                                   (2048, 2048, 40)])
+def test_q5k_matvec(ctx, n, k, m):
+    """TinyLlama / Llama-3 FFN shapes of a Q5_K_M file, batch 1 and 8, and a
+    40-row prefill (five passes of 8 rows): block sums bit-exact."""
+    W = S.make_weight(S.TYPE_Q5_K, n, k, seed=n + k + 5)
+    x = S.make_activation(m, k, seed=m + k + 5)
+    check_matmul(ctx, W, x, cond=(m <= 8 and k < 14336))
+
+
+def test_q5k_extreme_values(ctx):
+    """Largest Q5_K . Q8_K sums: every quant 31 (all five bits set), scales
+    and mins 63, activation blocks of equal values (quants -128)."""
+    n, k, m = 40, 1024, 3
+    rng = np.random.default_rng(25)
+    W = S.make_weight(S.TYPE_Q5_K, n, k, seed=25)
+    W.q[:] = 31
+    W.sc[:] = 63
+    W.mn[:] = 63
+    W.blocks = S.pack_q5k(W.d, W.dmin, W.sc, W.mn, W.q)
+    x = np.repeat(rng.standard_normal((m, k // 256)).astype(np.float32), 256, axis=1)
+    check_matmul(ctx, W, x, cond=False)
 
 
 # ------------------------------------------ Q8_0 prefill GEMM (int8 MFMA, m > 8)
@@ -273,14 +298,15 @@ def test_prefill_gemm_q8_0_subnormal_and_zero_scales(ctx):
     check_matmul(ctx, W, x, cond=False)
 
 
-@pytest.mark.parametrize("wtype", [S.TYPE_Q4_K, S.TYPE_Q6_K, S.TYPE_Q8_0])
+@pytest.mark.parametrize("wtype", [S.TYPE_Q4_K, S.TYPE_Q5_K, S.TYPE_Q6_K, S.TYPE_Q8_0])
 def test_subnormal_and_zero_scales(ctx, wtype):
     W = S.make_weight(wtype, 128, 1024, seed=8)
     rng = np.random.default_rng(8)
     d = (rng.integers(1, 1024, size=W.d.shape).astype(np.uint16)).view(np.float16)  # f16 subnormals
     d[::5] = 0
-    if wtype == S.TYPE_Q4_K:
-        W.blocks = S.pack_q4k(d, d[:, ::-1].copy(), W.sc, W.mn, W.q)
+    if wtype in (S.TYPE_Q4_K, S.TYPE_Q5_K):
+        pack = S.pack_q4k if wtype == S.TYPE_Q4_K else S.pack_q5k
+        W.blocks = pack(d, d[:, ::-1].copy(), W.sc, W.mn, W.q)
         W.dmin = d[:, ::-1].copy()
     elif wtype == S.TYPE_Q6_K:
         W.blocks = S.pack_q6k(d, W.sc, W.q)
@@ -322,7 +348,8 @@ def test_higher_rank_input_and_determinism(ctx):
     mm.free()
 
 
-@pytest.mark.parametrize("wtype,m", [(S.TYPE_Q4_K, 4), (S.TYPE_Q6_K, 1), (S.TYPE_Q8_0, 8), (S.TYPE_Q4_K, 40)])
+@pytest.mark.parametrize("wtype,m", [(S.TYPE_Q4_K, 4), (S.TYPE_Q6_K, 1), (S.TYPE_Q8_0, 8), (S.TYPE_Q4_K, 40),
+                                     (S.TYPE_Q5_K, 3)])
 def test_device_pointer_entry_points(ctx, wtype, m):
     from arm_ai_amd import hip
 

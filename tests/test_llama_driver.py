@@ -92,6 +92,48 @@ def test_prefill_and_decode_logits_match_reference(tiny):
         pos += 1
 
 
+@pytest.fixture(scope="module")
+def tiny_q5km():
+    """The same architecture with the Q5_K_M type mix (Q5_K projections; wv,
+    half the w2 and the output head Q6_K): the decode step's one-weight
+    fused-norm path, since the two-weight launch takes Q4_K / Q6_K only."""
+    import torch
+
+    import arm_ai_amd as A
+
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from arm_ai_amd.llama import Llama, synthetic_weights, tinyllama_q5km_types
+
+    hw = synthetic_weights(_tiny_cfg(), seed=13, types=tinyllama_q5km_types)
+    ctx = A.Context(0)
+    model = Llama(ctx, hw)
+    yield hw, model
+    model.free()
+    ctx.close()
+
+
+@pytest.mark.gpu
+def test_q5km_logits_and_graph_step_match_reference(tiny_q5km):
+    hw, model = tiny_q5km
+    ref = RefLlama(hw)
+    rng = np.random.default_rng(15)
+    prompt = rng.integers(0, hw.cfg.vocab, size=9).tolist()
+    g = model.forward(prompt, 0).cpu().numpy()
+    r = ref.forward(prompt, 0)
+    assert _rel(g, r) <= LOGIT_TOL, f"prefill logits rel {_rel(g, r):.3e}"
+    pos = len(prompt)
+    for step in range(2):  # teacher-forced decode
+        tok = int(rng.integers(0, hw.cfg.vocab))
+        g = model.forward([tok], pos).cpu().numpy()
+        r = ref.forward([tok], pos)
+        assert _rel(g, r) <= LOGIT_TOL, f"decode step {step} logits rel {_rel(g, r):.3e}"
+        pos += 1
+    toks_e = model.generate(prompt, 6, graph=False).tokens
+    toks_g = model.generate(prompt, 6, graph=True).tokens
+    assert toks_e == toks_g
+
+
 @pytest.mark.gpu
 def test_graph_decode_step_matches_eager(tiny):
     hw, model = tiny

@@ -132,7 +132,7 @@ def _int_sums(W, xq, wtype):
         Sx = np.einsum("nbe,mbe->mnb", W.q.astype(np.int64), qx.astype(np.int64))
         return Sx, np.zeros_like(Sx)
     _, qx, bs = O.q8k_fields(xq)  # [m, nb, 256], [m, nb, 16]
-    if wtype == O.Q4_K:
+    if wtype in (O.Q4_K, O.Q5_K):
         isum = np.einsum("nbje,mbje->mnbj", W.q.reshape(W.n, -1, 8, 32).astype(np.int64),
                          qx.reshape(m, -1, 8, 32).astype(np.int64))
         Sx = (isum * W.sc.astype(np.int64)[None]).sum(-1)
@@ -144,7 +144,7 @@ def _int_sums(W, xq, wtype):
     return Sx, np.zeros_like(Sx)
 
 
-WTYPES = [O.Q4_K, O.Q6_K, O.Q8_0]
+WTYPES = [O.Q4_K, O.Q5_K, O.Q6_K, O.Q8_0]
 
 
 @pytest.mark.parametrize("wtype", WTYPES)
@@ -294,3 +294,66 @@ def test_planted_mistakes_are_caught():
     xx = np.zeros(256, np.float32)
     xx[0], xx[1] = -128.0, 2.5
     assert _q8k(xx)[1][0, 1] != int(np.rint(2.5))
+
+
+def _q5k_block(qh=None, qs=None, sc=1, d=1.0):
+    """One Q5_K block built byte by byte (not by the generator's packer):
+    d, dmin = 0, every 6-bit scale = sc and min = 0 (the Q4_K packing of a
+    constant scale below 16: bytes 0-3 = sc, 4-7 = 0, 8-11 = sc)."""
+    b = np.zeros(176, np.uint8)
+    b[0:2] = np.array([d], np.float16).view(np.uint8)
+    b[4:8] = sc
+    b[12:16] = sc
+    if qh is not None:
+        b[16:48] = qh
+    if qs is not None:
+        b[48:176] = qs
+    return b
+
+
+@pytest.mark.parametrize("s,l", [(0, 0), (1, 5), (2, 31), (5, 17), (7, 9)])
+def test_q5k_fifth_bit_lands_on_element_32s_plus_l(s, l):
+    """GGML dequantize_row_q5_K: chunk c uses qh bit 2c for its low nibbles
+    (elements 64c + l) and bit 2c+1 for its high nibbles (64c + 32 + l), i.e.
+    bit s of qh[l] is bit 4 of element 32s + l."""
+    qh = np.zeros(32, np.uint8)
+    qh[l] = 1 << s
+    got = O.dequantize(O.Q5_K, _q5k_block(qh=qh)[None], 256)[0]
+    want = np.zeros(256)
+    want[32 * s + l] = 16.0
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("c,l,hi", [(0, 3, False), (0, 3, True), (3, 30, True), (2, 0, False)])
+def test_q5k_nibbles_land_like_q4k(c, l, hi):
+    qs = np.zeros(128, np.uint8)
+    qs[32 * c + l] = 0x50 if hi else 0x05
+    got = O.dequantize(O.Q5_K, _q5k_block(qs=qs)[None], 256)[0]
+    want = np.zeros(256)
+    want[64 * c + 32 * hi + l] = 5.0
+    assert np.array_equal(got, want)
+
+
+def test_q5k_dot_is_plain_int8_dot_for_unit_scales():
+    """sc = 1, m = 0, d = 1: Q5_K . Q8_K reduces to d_x * sum q5 * qx."""
+    rng = np.random.default_rng(21)
+    q = rng.integers(0, 32, 256)
+    qs = ((q[np.r_[0:32, 64:96, 128:160, 192:224]] & 15) |
+          ((q[np.r_[32:64, 96:128, 160:192, 224:256]] & 15) << 4)).astype(np.uint8)
+    qh = np.zeros(32, np.uint8)
+    for s in range(8):
+        qh |= (((q[32 * s:32 * s + 32] >> 4) & 1) << s).astype(np.uint8)
+    w = _q5k_block(qh=qh, qs=qs)[None]
+    x = rng.standard_normal((1, 256)).astype(np.float32)
+    xq = O.quantize(x, O.Q8_K)
+    dx, qx, _ = O.q8k_fields(xq)
+    got = O.matmul_preq(O.Q5_K, xq, w, 1, 256)[0, 0]
+    # candle's order: eight i32 lanes (element e goes to lane e % 8), each
+    # scaled by d = f16(d_w) * d_x in f32, then summed in lane order
+    lanes = (q * qx[0, 0].astype(np.int64)).reshape(32, 8).sum(0)
+    d = np.float32(1.0) * np.float32(dx[0, 0])
+    t = np.float32(0.0)
+    for l in range(8):
+        t = np.float32(t + np.float32(d * np.float32(lanes[l])))
+    assert int(lanes.sum()) == int((q * qx[0, 0].astype(np.int64)).sum())
+    assert got == np.float32(np.float32(-0.0) + t)
