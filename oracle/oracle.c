@@ -23,6 +23,9 @@
  *    same unpacked arrays; Q6_K bit layout also against a restatement of
  *    the reference's own dequantize_q6_k (shape_ops.rs:2848-2899) on blocks
  *    where its sub-scale indexing quirk cannot matter.
+ *  - Q5_K (GGML block_q5_K, restated; the reference holds no source for
+ *    it): hand-built blocks whose single qh bit or nibble must land on the
+ *    element dequantize_row_q5_K assigns it, and the unit-scale case.
  *  - the f32 combine order (candle vec_dot_unopt) is pinned only by the
  *    candle source, which is not in this image: "parity unpinned" for the
  *    exact f32 rounding sequence; the value is pinned to f64 truth.
