@@ -66,7 +66,8 @@ int block_elems(int type) {
     case AQ_TYPE_Q4_K:
     case AQ_TYPE_Q5_K:
     case AQ_TYPE_Q6_K: return QK_K;
-    case AQ_TYPE_Q8_0: return QK8_0;
+    case AQ_TYPE_Q8_0:
+    case AQ_TYPE_Q4_0: return QK8_0;
     default: return 0;
     }
 }
@@ -76,6 +77,7 @@ int block_bytes(int type) {
     case AQ_TYPE_Q5_K: return 176;
     case AQ_TYPE_Q6_K: return 210;
     case AQ_TYPE_Q8_0: return 34;
+    case AQ_TYPE_Q4_0: return 18;
     default: return 0;
     }
 }
@@ -175,7 +177,7 @@ int run_matmul(aq_ctx *ctx, const aq_qweight *w, const float *d_x, int64_t m, fl
     hipError_t e;
     if (use_gemm(w, m)) {
         ActPlanes a = act_planes(act, m, w->k);
-        e = w->type == AQ_TYPE_Q8_0 ? launch_quantize_q8_0(d_x, m, w->k, a, ctx->stream)
+        e = act_q80(w->type) ? launch_quantize_q8_0(d_x, m, w->k, a, ctx->stream)
                                     : launch_quantize_q8k(d_x, m, w->k, a, ctx->stream);
         if (e != hipSuccess) return fail(AQ_ERR_HIP, "activation quantizer: %s", hipGetErrorString(e));
         e = launch_gemm(w->layout, w->n, w->k, a, m, d_y, dS, dSmin, ws, ws_bytes, ctx->stream);
@@ -193,7 +195,7 @@ int run_matmul(aq_ctx *ctx, const aq_qweight *w, const float *d_x, int64_t m, fl
     } else {
         // the fused prologue reads float4; quantise separately instead
         ActPlanes a = act_planes(act, m, w->k);
-        e = w->type == AQ_TYPE_Q8_0 ? launch_quantize_q8_0(d_x, m, w->k, a, ctx->stream)
+        e = act_q80(w->type) ? launch_quantize_q8_0(d_x, m, w->k, a, ctx->stream)
                                     : launch_quantize_q8k(d_x, m, w->k, a, ctx->stream);
         if (e != hipSuccess) return fail(AQ_ERR_HIP, "activation quantizer: %s", hipGetErrorString(e));
         e = launch_matvec(w->layout, w->n, w->k, nullptr, &a, m, d_y, dS, dSmin, ctx->stream);
@@ -313,7 +315,7 @@ static int upload_impl(aq_ctx *ctx, int type, const void *blocks, size_t nbytes,
 
     int status = AQ_OK;
     // padding rows (n not a multiple of 8) and Q8_0 padding blocks must read as zeros
-    if ((n % RB != 0 || (type == AQ_TYPE_Q8_0 && (k / QK8_0) % 8 != 0)) &&
+    if ((n % RB != 0 || (act_q80(type) && (k / QK8_0) % 8 != 0)) &&
         hipMemsetAsync(base, 0, total, ctx->stream) != hipSuccess)
         status = fail(AQ_ERR_HIP, "hipMemsetAsync of the weight padding failed");
 

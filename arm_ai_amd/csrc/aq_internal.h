@@ -10,6 +10,7 @@ namespace aq {
 
 constexpr int QK_K = 256;
 constexpr int QK8_0 = 32;
+constexpr int TYPE_Q4_0 = 2;
 constexpr int TYPE_Q8_0 = 8;
 constexpr int TYPE_Q4_K = 12;
 constexpr int TYPE_Q5_K = 13;
@@ -31,6 +32,8 @@ constexpr int TYPE_Q8_K = 15;
 //   Q8_0 (17 pieces = 272 B): pieces 2j, 2j+1 = qs of block 8g+j, piece 16 =
 //                             the eight f16 d; a row whose block count is not a
 //                             multiple of 8 is padded with zero blocks.
+//   Q4_0 (9 pieces = 144 B):  piece j = the 16 qs bytes of block 8g+j, piece 8
+//                             = the eight f16 d; padded like Q8_0.
 // Rows are taken in blocks of 8 (the row count is padded with zero rows to a
 // multiple of 8), and for each (row block, group, piece) the 8 rows' pieces
 // are one 128-byte line:
@@ -53,10 +56,14 @@ struct WLayout {
 };
 
 __host__ __device__ constexpr int slabs_of(int type) {
-    return type == TYPE_Q4_K ? 9 : type == TYPE_Q5_K ? 11 : type == TYPE_Q6_K ? 13 : type == TYPE_Q8_0 ? 17 : 0;
+    return type == TYPE_Q4_K ? 9 : type == TYPE_Q5_K ? 11 : type == TYPE_Q6_K ? 13 : type == TYPE_Q8_0 ? 17
+         : type == TYPE_Q4_0 ? 9 : 0;
 }
+// Weights whose activation is quantised to Q8_0 blocks of 32 (candle's
+// VecDotType): Q8_0 and Q4_0.  The others use Q8_K.
+__host__ __device__ constexpr bool act_q80(int type) { return type == TYPE_Q8_0 || type == TYPE_Q4_0; }
 inline int groups_of(int type, int64_t k) {
-    return type == TYPE_Q8_0 ? (int)((k / QK8_0 + 7) / 8) : (int)(k / QK_K);
+    return act_q80(type) ? (int)((k / QK8_0 + 7) / 8) : (int)(k / QK_K);
 }
 
 // Quantised activation planes (written by the quantizer kernels):

@@ -268,11 +268,56 @@ __device__ __forceinline__ void dot_q80(const Wt<TYPE_Q8_0> &W, const uint8_t *l
     }
 }
 
+// ------------------------------------------------------------------ Q4_0
+// Group of eight blocks: piece j = the 16 qs bytes of block j (low nibbles
+// elements 0..15, high nibbles 16..31, value q - 8), piece 8 = the eight f16
+// d.  candle: sum_i ((q - 8) * qx) as f32 * f16(d_w) * f16(d_x); the integer
+// sum is formed as sum q*qx - 8 * sum qx.
+template <int B, bool DUMP>
+__device__ __forceinline__ void dot_q40(const Wt<TYPE_Q4_0> &W, const uint8_t *lds, int ng, int g, int m,
+                                        float (&f)[B], const MvParams &p, int row, bool row_ok) {
+    const uint32_t dwp[4] = {W.pc[8].x, W.pc[8].y, W.pc[8].z, W.pc[8].w};
+    const uint32_t ones[4] = {0x01010101u, 0x01010101u, 0x01010101u, 0x01010101u};
+    const int nblk = p.k / QK8_0;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const uint4 q = W.pc[j];
+        const uint32_t lo[4] = {q.x & 0x0F0F0F0Fu, q.y & 0x0F0F0F0Fu, q.z & 0x0F0F0F0Fu, q.w & 0x0F0F0F0Fu};
+        const uint32_t hi[4] = {(q.x >> 4) & 0x0F0F0F0Fu, (q.y >> 4) & 0x0F0F0F0Fu, (q.z >> 4) & 0x0F0F0F0Fu,
+                                (q.w >> 4) & 0x0F0F0F0Fu};
+        const float dw = f16_bits_to_f32(dwp[j >> 1] >> (16 * (j & 1)));
+#pragma unroll
+        for (int b = 0; b < B; b++) {
+            if (b < m) {
+                const uint8_t *rec = lds + (b * ng + g) * REC;
+                const int4 x0 = *(const int4 *)(rec + 32 * j), x1 = *(const int4 *)(rec + 32 * j + 16);
+                int isum = dot16(lo, x0, 0);
+                isum = dot16(hi, x1, isum);
+                int xs = dot16(ones, x0, 0);
+                xs = dot16(ones, x1, xs);
+                isum -= 8 * xs;
+                const float dx = *(const float *)(rec + REC_D8 + 4 * j);
+                f[b] += ((float)isum * dw) * dx;
+                if (DUMP) {
+                    const int blk = 8 * g + j;
+                    if (blk < nblk && row_ok) {
+                        const int64_t o = ((int64_t)b * p.n + row) * nblk + blk;
+                        p.S[o] = isum;
+                        p.Smin[o] = 0;
+                    }
+                }
+            }
+        }
+    }
+}
+
 template <int TYPE, int B, bool DUMP>
 __device__ __forceinline__ void group_dot(const Wt<TYPE> &W, const uint8_t *lds, const MvParams &p, int g, int row,
                                           bool valid, float (&f)[B]) {
     if (TYPE == TYPE_Q8_0) {
         dot_q80<B, DUMP>(*(const Wt<TYPE_Q8_0> *)&W, lds, p.ng, g, p.m, f, p, row, valid);
+    } else if (TYPE == TYPE_Q4_0) {
+        dot_q40<B, DUMP>(*(const Wt<TYPE_Q4_0> *)&W, lds, p.ng, g, p.m, f, p, row, valid);
     } else {
         int So[B], Smo[B];
         if (TYPE == TYPE_Q4_K) dot_q45k<B, DUMP, TYPE_Q4_K>(*(const Wt<TYPE_Q4_K> *)&W, lds, p.ng, g, p.m, f, So, Smo);
@@ -316,7 +361,7 @@ __device__ __forceinline__ void rec_load(ActStage &st, int r, const MvParams &p,
     if (FUSED) {
         const rsrc_t rx = buf_rsrc(p.x, (uint32_t)(m * k * 4));
         uint32_t off;
-        if (TYPE != TYPE_Q8_0) {
+        if (!act_q80(TYPE)) {
             off = ok ? (uint32_t)((b * k + g * QK_K + 4 * lane) * 4) : BUF_OOB;
         } else {
             const int j = lane >> 3, sub = lane & 7;
@@ -332,7 +377,7 @@ __device__ __forceinline__ void rec_load(ActStage &st, int r, const MvParams &p,
             const rsrc_t ru = buf_rsrc(p.x + k, (uint32_t)(k * 4));
             st.q2[r] = __builtin_amdgcn_raw_buffer_load_b128(ru, off, 0, 0);
         }
-    } else if (TYPE != TYPE_Q8_0) {
+    } else if (!act_q80(TYPE)) {
         const rsrc_t rq = buf_rsrc(p.act.qs, (uint32_t)(m * k));
         const rsrc_t rs = buf_rsrc(p.act.bsums, (uint32_t)(m * (k / 16) * 2));
         const rsrc_t rd = buf_rsrc(p.act.d, (uint32_t)(m * (k / QK_K) * 4));
@@ -362,7 +407,7 @@ __device__ __forceinline__ void rec_store(const ActStage &st, int r, uint8_t *ld
     if (FUSED) {
         const u32x4 u = st.q[r];
         const float v[4] = {u32_as_f32(u.x), u32_as_f32(u.y), u32_as_f32(u.z), u32_as_f32(u.w)};
-        if (TYPE != TYPE_Q8_0) {
+        if (!act_q80(TYPE)) {
             int bsum;
             float d;
             const uint32_t packed = q8k_block_wave(v, lane, &bsum, &d);
@@ -377,7 +422,7 @@ __device__ __forceinline__ void rec_store(const ActStage &st, int r, uint8_t *ld
             if (sub == 0) *(float *)(rec + REC_D8 + 4 * j) = f16_bits_to_f32(h);
         }
     } else {
-        if (TYPE != TYPE_Q8_0) {
+        if (!act_q80(TYPE)) {
             if (lane < 16) *(u32x4 *)(rec + 16 * lane) = st.q[r];
             else if (lane < 18) *(u32x4 *)(rec + REC_BSUMS + 16 * (lane - 16)) = st.q[r];
             else if (lane == 18) *(float *)(rec + REC_D) = st.dsc[r];
@@ -453,7 +498,7 @@ __device__ __forceinline__ void matvec_body(const MvParams &p, const int bid, co
         for (int r = 0; r < PRE; r++) {
             const int t = wave + nw * r;
             uint32_t off = BUF_OOB;
-            if (TYPE != TYPE_Q8_0) {
+            if (!act_q80(TYPE)) {
                 if (t < nrec) off = (uint32_t)((t * QK_K + 4 * lane) * 4);
             } else {
                 const int j = lane >> 3, sub = lane & 7;
@@ -675,8 +720,9 @@ hipError_t matvec_impl(const WLayout &w, int64_t n, int64_t k, const float *x, c
 hipError_t matvec_impl(const WLayout &w, int64_t n, int64_t k, const float *x, const ActPlanes *act, int64_t m,
                        float *y, int32_t *S, int32_t *Smin, const XfArgs &xa, hipStream_t s) {
     const int type = w.type;
-    if (type != TYPE_Q4_K && type != TYPE_Q5_K && type != TYPE_Q6_K && type != TYPE_Q8_0) return hipErrorInvalidValue;
-    const int blk = type == TYPE_Q8_0 ? QK8_0 : QK_K;
+    if (type != TYPE_Q4_K && type != TYPE_Q5_K && type != TYPE_Q6_K && type != TYPE_Q8_0 && type != TYPE_Q4_0)
+        return hipErrorInvalidValue;
+    const int blk = act_q80(type) ? QK8_0 : QK_K;
     if (!w.slab || m < 0 || n <= 0 || k <= 0 || k % blk || n > 0x7fffffff || k > 0x7fffffff || !y)
         return hipErrorInvalidValue;
     if (type == TYPE_Q6_K && !w.d) return hipErrorInvalidValue;
@@ -738,6 +784,7 @@ hipError_t matvec_impl(const WLayout &w, int64_t n, int64_t k, const float *x, c
         case TYPE_Q4_K: e = launch_t<TYPE_Q4_K>(B, p, (unsigned)grid, lds, S != nullptr, xa.xf, s); break;
         case TYPE_Q5_K: e = launch_t<TYPE_Q5_K>(B, p, (unsigned)grid, lds, S != nullptr, xa.xf, s); break;
         case TYPE_Q6_K: e = launch_t<TYPE_Q6_K>(B, p, (unsigned)grid, lds, S != nullptr, xa.xf, s); break;
+        case TYPE_Q4_0: e = launch_t<TYPE_Q4_0>(B, p, (unsigned)grid, lds, S != nullptr, xa.xf, s); break;
         default: e = launch_t<TYPE_Q8_0>(B, p, (unsigned)grid, lds, S != nullptr, xa.xf, s); break;
         }
         if (e != hipSuccess) return e;

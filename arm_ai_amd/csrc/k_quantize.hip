@@ -100,7 +100,8 @@ hipError_t launch_quantize_q8_0(const float *x, int64_t m, int64_t k, ActPlanes 
 template <int TYPE>
 __global__ __launch_bounds__(256) void repack_kernel(const uint8_t *__restrict__ src, int64_t n, int64_t nblk,
                                                      int ng, uint8_t *__restrict__ slab, uint16_t *__restrict__ dpl) {
-    constexpr int BYTES = TYPE == TYPE_Q4_K ? 144 : TYPE == TYPE_Q5_K ? 176 : TYPE == TYPE_Q6_K ? 210 : 34;
+    constexpr int BYTES = TYPE == TYPE_Q4_K ? 144 : TYPE == TYPE_Q5_K ? 176 : TYPE == TYPE_Q6_K ? 210
+                        : TYPE == TYPE_Q4_0 ? 18 : 34;
     constexpr int S = slabs_of(TYPE);
     const int64_t rb_stride = (int64_t)ng * S * 128;
     const int64_t total = n * nblk * BYTES;
@@ -114,6 +115,12 @@ __global__ __launch_bounds__(256) void repack_kernel(const uint8_t *__restrict__
             const int piece = o < 16 ? 0 : 1 + (o - 16) / 16;
             const int w = o < 16 ? o : (o - 16) & 15;
             rbp[(b * S + piece) * 128 + w] = src[i];
+        } else if (TYPE == TYPE_Q4_0) {
+            // Q4_0 block b = 8g + j: d -> piece 8 bytes 2j..2j+1; qs byte q -> piece j byte q
+            const int64_t g = b >> 3;
+            const int j = (int)(b & 7);
+            if (o < 2) rbp[(g * S + 8) * 128 + 2 * j + o] = src[i];
+            else rbp[(g * S + j) * 128 + (o - 2)] = src[i];
         } else if (TYPE == TYPE_Q5_K) {
             // the 176 bytes are 11 pieces in order: byte o -> piece o / 16
             rbp[(b * S + (o >> 4)) * 128 + (o & 15)] = src[i];
@@ -140,7 +147,7 @@ __global__ __launch_bounds__(256) void repack_kernel(const uint8_t *__restrict__
 hipError_t launch_repack(int type, const uint8_t *src, int64_t n, int64_t k, uint8_t *dst_slab, uint16_t *dst_d,
                          hipStream_t s) {
     if (!src || !dst_slab || n <= 0 || k <= 0) return hipErrorInvalidValue;
-    const int blk = type == TYPE_Q8_0 ? QK8_0 : QK_K;
+    const int blk = act_q80(type) ? QK8_0 : QK_K;
     if (k % blk) return hipErrorInvalidValue;
     const int64_t nblk = k / blk;
     const int ng = groups_of(type, k);
@@ -153,6 +160,7 @@ hipError_t launch_repack(int type, const uint8_t *src, int64_t n, int64_t k, uin
         repack_kernel<TYPE_Q6_K><<<grid, 256, 0, s>>>(src, n, nblk, ng, dst_slab, dst_d);
         break;
     case TYPE_Q8_0: repack_kernel<TYPE_Q8_0><<<grid, 256, 0, s>>>(src, n, nblk, ng, dst_slab, dst_d); break;
+    case TYPE_Q4_0: repack_kernel<TYPE_Q4_0><<<grid, 256, 0, s>>>(src, n, nblk, ng, dst_slab, dst_d); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

@@ -22,7 +22,8 @@ the quantized projections as raw GGUF blocks (memory-mapped, uploaded to HBM
 by aq_qweight_upload), the norm weights as f32, and the token embedding
 dequantized to f32 as candle does for its embedding table.  Dequantization
 follows candle's ``to_float`` f32 formulas (restated from the GGML block
-definitions: Q4_K and Q5_K d*sc*q - dmin*m, Q6_K d*sc*(q-32), Q8_0 d*q); the
+definitions: Q4_K and Q5_K d*sc*q - dmin*m, Q6_K d*sc*(q-32), Q8_0 d*q,
+Q4_0 d*(q-8)); the
 embedding only feeds the f32 glue, which is tolerance-checked.
 """
 from __future__ import annotations
@@ -46,9 +47,9 @@ _SCALAR = {T_U8: "<B", T_I8: "<b", T_U16: "<H", T_I16: "<h", T_U32: "<I", T_I32:
 
 # ggml tensor types read here: (elements per block, bytes per block)
 GGML_F32, GGML_F16 = 0, 1
-TYPE_SIZES = {GGML_F32: (1, 4), GGML_F16: (1, 2), synth.TYPE_Q8_0: (32, 34), synth.TYPE_Q4_K: (256, 144),
-              synth.TYPE_Q5_K: (256, 176), synth.TYPE_Q6_K: (256, 210)}
-QUANT_TYPES = (synth.TYPE_Q4_K, synth.TYPE_Q5_K, synth.TYPE_Q6_K, synth.TYPE_Q8_0)
+TYPE_SIZES = {GGML_F32: (1, 4), GGML_F16: (1, 2), synth.TYPE_Q8_0: (32, 34), synth.TYPE_Q4_0: (32, 18),
+              synth.TYPE_Q4_K: (256, 144), synth.TYPE_Q5_K: (256, 176), synth.TYPE_Q6_K: (256, 210)}
+QUANT_TYPES = (synth.TYPE_Q4_K, synth.TYPE_Q5_K, synth.TYPE_Q6_K, synth.TYPE_Q8_0, synth.TYPE_Q4_0)
 
 
 class GGUFError(ValueError):
@@ -176,7 +177,7 @@ class GGUFFile:
         """A 2-D quantized weight as candle's QTensor (n rows, k columns)."""
         ti = self.tensor(name)
         if ti.type not in QUANT_TYPES or len(ti.dims) != 2:
-            raise GGUFError(f"tensor {name}: a 2-D Q4_K / Q5_K / Q6_K / Q8_0 weight is needed, got type {ti.type} "
+            raise GGUFError(f"tensor {name}: a 2-D Q4_K / Q5_K / Q6_K / Q8_0 / Q4_0 weight is needed, got type {ti.type} "
                             f"with dims {ti.dims}")
         k, n = ti.dims
         return QTensor(GgmlDType(ti.type), (n, k), self.raw(name))
@@ -212,6 +213,12 @@ def _f16(b: np.ndarray) -> np.ndarray:
 def dequantize(type_: int, raw: np.ndarray, n_elements: int) -> np.ndarray:
     """GGUF blocks -> f32 [n_elements], candle to_float's f32 operation order."""
     raw = np.asarray(raw, np.uint8)
+    if type_ == synth.TYPE_Q4_0:
+        b = raw.reshape(-1, 18)
+        d = _f16(b[:, 0:2])
+        qs = b[:, 2:18]
+        q = np.concatenate([qs & 0xF, qs >> 4], axis=1).astype(np.float32) - 8.0  # elements 0..15, 16..31
+        return (q * d[:, None]).reshape(-1)[:n_elements]
     if type_ == synth.TYPE_Q8_0:
         b = raw.reshape(-1, 34)
         d = _f16(b[:, 0:2])

@@ -10,7 +10,7 @@ keeps those names and their argument meaning:
 * ``QMatMul.from_qtensor(qt, ctx)``: uploads the blocks to HBM once.
 * ``QMatMul.forward(xs)``: xs is f32 ``[..., k]`` (rank >= 2, C-contiguous),
   returns f32 ``[..., n]``; the activation is quantised to Q8_K (Q8_0 for
-  Q8_0 weights) and the dot products run on the GPU.
+  Q8_0 and Q4_0 weights) and the dot products run on the GPU.
 
 candle's checks are kept with the same outcome (an error, never a crash):
 a non-contiguous input, rank < 2, or a last dimension different from k.
@@ -28,6 +28,7 @@ from . import _lib
 class GgmlDType(IntEnum):
     """GGUF/GGML dtype ids, named as in candle's `GgmlDType`."""
 
+    Q4_0 = 2
     Q8_0 = 8
     Q4K = 12
     Q5K = 13
@@ -36,11 +37,11 @@ class GgmlDType(IntEnum):
 
     @property
     def block_size(self) -> int:
-        return 32 if self is GgmlDType.Q8_0 else 256
+        return 32 if self in (GgmlDType.Q8_0, GgmlDType.Q4_0) else 256
 
     @property
     def type_size(self) -> int:
-        return {GgmlDType.Q8_0: 34, GgmlDType.Q4K: 144, GgmlDType.Q5K: 176, GgmlDType.Q6K: 210,
+        return {GgmlDType.Q4_0: 18, GgmlDType.Q8_0: 34, GgmlDType.Q4K: 144, GgmlDType.Q5K: 176, GgmlDType.Q6K: 210,
                 GgmlDType.Q8K: 292}[self]
 
 
@@ -179,7 +180,7 @@ class QMatMul:
 
     @property
     def act_type(self) -> GgmlDType:
-        return GgmlDType.Q8_0 if self.dtype is GgmlDType.Q8_0 else GgmlDType.Q8K
+        return GgmlDType.Q8_0 if self.dtype in (GgmlDType.Q8_0, GgmlDType.Q4_0) else GgmlDType.Q8K
 
     def forward_preq_device(self, d_act: int, m: int, d_y: int) -> None:
         """Matmul on an activation quantised by quantize_act_device (asynchronous)."""

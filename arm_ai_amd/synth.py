@@ -11,11 +11,12 @@ configurations prescribe:
 * Q6_K: d = f16(|N(0, 0.02)|); int8 sub-scales ~ U[-32, 31]; 6-bit quants
   ~ U[0, 63] (value q - 32).
 * Q8_0: d = f16(|N(0, 0.02)|); int8 quants ~ U[-127, 127].
+* Q4_0: d = f16(|N(0, 0.02)|); 4-bit quants ~ U[0, 15] (value q - 8).
 * activations: f32 N(0, 1).
 
 Generators draw element-level arrays from ``numpy.random.default_rng(seed)``
 (PCG64) and pack them into GGUF block bytes with the GGUF layout (block
-formats: Q4_K 144 B, Q5_K 176 B, Q6_K 210 B, Q8_0 34 B).  The element arrays are kept so
+formats: Q4_K 144 B, Q5_K 176 B, Q6_K 210 B, Q8_0 34 B, Q4_0 18 B).  The element arrays are kept so
 tests can compute exact answers without going through any unpacking code.
 f32 -> f16 uses numpy's IEEE round-to-nearest-even conversion, the same
 rounding the reference's `half` crate uses (shape_ops.rs:1492-1503).
@@ -35,9 +36,11 @@ TYPE_Q5_K = 13
 TYPE_Q6_K = 14
 TYPE_Q8_K = 15
 
-BLOCK_BYTES = {TYPE_Q4_K: 144, TYPE_Q5_K: 176, TYPE_Q6_K: 210, TYPE_Q8_0: 34, TYPE_Q8_K: 292}
-BLOCK_ELEMS = {TYPE_Q4_K: QK_K, TYPE_Q5_K: QK_K, TYPE_Q6_K: QK_K, TYPE_Q8_0: QK8_0, TYPE_Q8_K: QK_K}
-TYPE_NAMES = {TYPE_Q4_K: "q4_k", TYPE_Q5_K: "q5_k", TYPE_Q6_K: "q6_k", TYPE_Q8_0: "q8_0", TYPE_Q8_K: "q8_k"}
+BLOCK_BYTES = {TYPE_Q4_K: 144, TYPE_Q5_K: 176, TYPE_Q6_K: 210, TYPE_Q8_0: 34, TYPE_Q4_0: 18, TYPE_Q8_K: 292}
+BLOCK_ELEMS = {TYPE_Q4_K: QK_K, TYPE_Q5_K: QK_K, TYPE_Q6_K: QK_K, TYPE_Q8_0: QK8_0, TYPE_Q4_0: QK8_0,
+               TYPE_Q8_K: QK_K}
+TYPE_NAMES = {TYPE_Q4_K: "q4_k", TYPE_Q5_K: "q5_k", TYPE_Q6_K: "q6_k", TYPE_Q8_0: "q8_0", TYPE_Q4_0: "q4_0",
+              TYPE_Q8_K: "q8_k"}
 
 
 @dataclass
@@ -52,7 +55,8 @@ class QWeight:
     dmin: np.ndarray | None  # float16 [n, nb] (Q4_K, Q5_K)
     sc: np.ndarray | None  # Q4_K / Q5_K uint8 [n, nb, 8]; Q6_K int8 [n, nb, 16]
     mn: np.ndarray | None  # Q4_K / Q5_K uint8 [n, nb, 8]
-    q: np.ndarray  # Q4_K uint8 [n,nb,256] in [0,15]; Q5_K in [0,31]; Q6_K int8 in [-32,31]; Q8_0 int8 [n,nb,32]
+    q: np.ndarray  # Q4_K uint8 [n,nb,256] in [0,15]; Q5_K in [0,31]; Q6_K int8 in [-32,31]; Q8_0 int8 [n,nb,32];
+    #               Q4_0 uint8 [n,nb,32] in [0,15] (value q - 8)
 
     @property
     def nbytes(self) -> int:
@@ -68,6 +72,8 @@ class QWeight:
         elif self.type == TYPE_Q6_K:
             sc = np.repeat(self.sc.astype(np.float64), 16, axis=-1)
             v = d * sc * self.q.astype(np.float64)
+        elif self.type == TYPE_Q4_0:
+            v = d * (self.q.astype(np.float64) - 8.0)
         else:
             v = d * self.q.astype(np.float64)
         return v.reshape(self.n, self.k)
@@ -150,6 +156,17 @@ def pack_q8_0(d, q) -> np.ndarray:
     return out.reshape(n, nb * 34)
 
 
+def pack_q4_0(d, q) -> np.ndarray:
+    """Pack Q4_0 element arrays (q in [0, 15]) into 18-byte blocks: f16 d @0,
+    qs @2 with qs[j] = q[j] | q[j + 16] << 4."""
+    n, nb = d.shape
+    out = np.empty((n, nb, 18), dtype=np.uint8)
+    out[..., 0:2] = d.astype(np.float16).view(np.uint8).reshape(n, nb, 2)
+    q = q.astype(np.uint8)
+    out[..., 2:18] = (q[..., 0:16] & 15) | ((q[..., 16:32] & 15) << 4)
+    return out.reshape(n, nb * 18)
+
+
 def make_weight(type_: int, n: int, k: int, seed: int = 0, rng: np.random.Generator | None = None) -> QWeight:
     """A seeded random weight of `n` rows by `k` columns in GGUF block format."""
     if rng is None:
@@ -181,6 +198,10 @@ def make_weight(type_: int, n: int, k: int, seed: int = 0, rng: np.random.Genera
         d = _half_abs_normal(rng, (n, nb))
         q = rng.integers(-127, 128, size=(n, nb, 32), dtype=np.int8)
         return QWeight(type_, n, k, pack_q8_0(d, q), d, None, None, None, q)
+    if type_ == TYPE_Q4_0:
+        d = _half_abs_normal(rng, (n, nb))
+        q = rng.integers(0, 16, size=(n, nb, 32), dtype=np.uint8)
+        return QWeight(type_, n, k, pack_q4_0(d, q), d, None, None, None, q)
     raise ValueError(f"unsupported weight type {type_}")
 
 
@@ -197,6 +218,6 @@ def weight_bytes(type_: int, n: int, k: int) -> int:
 
 def act_bytes(type_: int, m: int, k: int) -> int:
     """Bytes of the quantised activation a weight of `type_` is dotted with."""
-    if type_ == TYPE_Q8_0:
+    if type_ in (TYPE_Q8_0, TYPE_Q4_0):
         return m * (k // QK8_0) * 34
     return m * (k // QK_K) * 292

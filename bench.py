@@ -91,7 +91,7 @@ class Workload:
         A.quantize_act_device(ctx, at, self.dx.ptr, m, k, self.dact.ptr)
         ctx.synchronize()
         self.ctx = ctx
-        act_q = m * (k // 32) * 34 if wtype == 8 else m * (k // 256) * 292
+        act_q = m * (k // 32) * 34 if wtype in (8, 2) else m * (k // 256) * 292
         self.weight_bytes = self.W.nbytes
         self.step_bytes = self.W.nbytes + m * k * 4 + m * n * 4  # quantizer fused into the step
         self.kernel_bytes = self.W.nbytes + act_q + m * n * 4  # matvec kernel alone
@@ -171,7 +171,7 @@ def measure(ctx, wtype, n, k, m, steps, warmup, seed):
     step_ms, step_wall = time_graph(ctx, wl.step, steps, warmup)
     kern_ms, _ = time_graph(ctx, wl.kernel, steps, warmup)
     out = {
-        "n": n, "k": k, "m": m, "weight_type": {12: "Q4_K", 13: "Q5_K", 14: "Q6_K", 8: "Q8_0"}[wtype],
+        "n": n, "k": k, "m": m, "weight_type": {12: "Q4_K", 13: "Q5_K", 14: "Q6_K", 8: "Q8_0", 2: "Q4_0"}[wtype],
         "step_us": round(step_ms * 1e3, 3),
         "step_GBps": round(wl.step_bytes / (step_ms / 1e3) / 1e9, 1),
         "matvec_us": round(kern_ms * 1e3, 3),
@@ -211,6 +211,7 @@ MATVEC_CASES = {  # name: (weight type, n, k, m, seed)
     "c4_q6k_128256x4096_b1": (14, 128256, 4096, 1, 7),
     "c4_q6k_128256x4096_b8": (14, 128256, 4096, 8, 9),
     "q5k_14336x4096_b1": (13, 14336, 4096, 1, 13),  # a Q5_K_M file's ffn_up, batch 1
+    "q4_0_14336x4096_b1": (2, 14336, 4096, 1, 14),  # a Q4_0 file's ffn_up, batch 1
 }
 # Reference points, not this library: the vendor's plain int8 x int8 -> int32
 # GEMM (hipBLASLt through torch._int_mm) at the prefill GEMMs' shapes, with no

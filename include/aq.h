@@ -3,7 +3,7 @@
  * (libarm_ai_amd.so).
  *
  * This is the drop-in boundary for the hot path of mlainez/arm_ai's
- * ArmAI.LlamaCandle: GGUF block-quantized weights (Q4_K, Q5_K, Q6_K, Q8_0) times
+ * ArmAI.LlamaCandle: GGUF block-quantized weights (Q4_K, Q5_K, Q6_K, Q8_0, Q4_0) times
  * f32 activations that are quantized to Q8_K (Q8_0 for Q8_0 weights), as
  * candle-core 0.8.4's QMatMul does on the CPU.  The reference reaches that
  * code through
@@ -18,9 +18,10 @@
  *  - Every function returns an aq_status (0 = AQ_OK, negative = error) and
  *    never aborts the process; aq_last_error() gives the calling thread's
  *    last message.
- *  - Weight type ids are GGUF/GGML dtype ids (Q8_0 = 8, Q4_K = 12, Q5_K = 13,
- *    Q6_K = 14).  Q5_K runs the batch-1..8 matvec at any m (batches of more
- *    than 8 rows in passes of 8); the prefill GEMMs take Q4_K, Q6_K and Q8_0.
+ *  - Weight type ids are GGUF/GGML dtype ids (Q4_0 = 2, Q8_0 = 8, Q4_K = 12,
+ *    Q5_K = 13, Q6_K = 14).  Q5_K and Q4_0 run the batch-1..8 matvec at any m
+ *    (batches of more than 8 rows in passes of 8); the prefill GEMMs take
+ *    Q4_K, Q6_K and Q8_0.
  *  - A weight is n rows (output features) by k columns (input features),
  *    row-major blocks, exactly candle's QTensor storage of shape (n, k).
  *  - Host-pointer entry points are synchronous at return.  Device-pointer
@@ -50,6 +51,7 @@ typedef enum aq_status {
 } aq_status;
 
 typedef enum aq_type {
+    AQ_TYPE_Q4_0 = 2,
     AQ_TYPE_Q8_0 = 8,
     AQ_TYPE_Q4_K = 12,
     AQ_TYPE_Q5_K = 13,
@@ -107,7 +109,7 @@ int aq_qmatmul_f32_device(aq_ctx *ctx, const aq_qweight *w, const float *d_lhs, 
  * k_quants::matmul; these two calls let a caller quantise once on the device
  * and run several matmuls on the result.  The activation buffer layout is
  * private to this library; size it with aq_act_bytes.
- *   act_type: AQ_TYPE_Q8_K (for Q4_K / Q5_K / Q6_K weights) or AQ_TYPE_Q8_0 (for Q8_0). */
+ *   act_type: AQ_TYPE_Q8_K (for Q4_K / Q5_K / Q6_K weights) or AQ_TYPE_Q8_0 (for Q8_0 / Q4_0). */
 size_t aq_act_bytes(int act_type, int64_t m, int64_t k);
 int aq_quantize_act_device(aq_ctx *ctx, int act_type, const float *d_x, int64_t m, int64_t k, void *d_act);
 int aq_qmatmul_preq_device(aq_ctx *ctx, const aq_qweight *w, const void *d_act, int64_t m, int64_t k,
@@ -126,6 +128,7 @@ int aq_quantize_q8_0(aq_ctx *ctx, const float *x, int64_t m, int64_t k, void *ou
  *   Q4_K, Q5_K: S = sum_j sc_j * sum_{e in sub-block j} q_e*qx_e,  Smin = sum_g bsums_g * m_{g/2}
  *   Q6_K: S = sum_j sc_j * sum_{e in sub-block j} q6_e*qx_e, Smin = 0
  *   Q8_0: S = sum_{32} qw*qx per 32-block,                    Smin = 0
+ *   Q4_0: S = sum_{32} (q-8)*qx per 32-block,                 Smin = 0
  * computed by the same kernel code as aq_qmatmul_f32 (batch <= 8 path)
  * or the prefill GEMM (m > 8) with an integer epilogue.  Host buffers. */
 int aq_qmatmul_block_sums(aq_ctx *ctx, const aq_qweight *w, const float *lhs, int64_t m,

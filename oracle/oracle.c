@@ -23,6 +23,8 @@
  *    same unpacked arrays; Q6_K bit layout also against a restatement of
  *    the reference's own dequantize_q6_k (shape_ops.rs:2848-2899) on blocks
  *    where its sub-scale indexing quirk cannot matter.
+ *  - Q4_0 (GGML block_q4_0, restated): hand-built blocks whose single
+ *    nibble must land on element j or j + 16 with value q - 8.
  *  - Q5_K (GGML block_q5_K, restated; the reference holds no source for
  *    it): hand-built blocks whose single qh bit or nibble must land on the
  *    element dequantize_row_q5_K assigns it, and the unit-scale case.
@@ -128,6 +130,7 @@ size_t orc_type_block_bytes(int type) {
     case ORC_Q5_K: return ORC_Q5K_BYTES;
     case ORC_Q6_K: return ORC_Q6K_BYTES;
     case ORC_Q8_0: return ORC_Q8_0_BYTES;
+    case ORC_Q4_0: return ORC_Q4_0_BYTES;
     case ORC_Q8_K: return ORC_Q8K_BYTES;
     default: return 0;
     }
@@ -139,7 +142,8 @@ int64_t orc_type_block_elems(int type) {
     case ORC_Q5_K:
     case ORC_Q6_K:
     case ORC_Q8_K: return ORC_QK_K;
-    case ORC_Q8_0: return ORC_QK8_0;
+    case ORC_Q8_0:
+    case ORC_Q4_0: return ORC_QK8_0;
     default: return 0;
     }
 }
@@ -377,6 +381,25 @@ float orc_vec_dot_q8_0_q8_0(int64_t k, const uint8_t *w, const uint8_t *xq) {
     return sumf;
 }
 
+/* BlockQ4_0::vec_dot_unopt (Q4_0 . Q8_0): per 32-block
+ * sum_i = sum_{j<16} ((qs[j] & 15) - 8) * qx[j] + ((qs[j] >> 4) - 8) * qx[j+16]
+ * (i32), sumf += (f32)sum_i * f16(d_w) * f16(d_x). */
+float orc_vec_dot_q4_0_q8_0(int64_t k, const uint8_t *w, const uint8_t *xq) {
+    int64_t nb = k / ORC_QK8_0;
+    float sumf = 0.0f;
+    for (int64_t b = 0; b < nb; b++) {
+        const uint8_t *x = w + b * ORC_Q4_0_BYTES;
+        const uint8_t *y = xq + b * ORC_Q8_0_BYTES;
+        int32_t s = 0;
+        for (int j = 0; j < 16; j++) {
+            const int32_t v0 = (int32_t)(x[2 + j] & 0x0F) - 8, v1 = (int32_t)(x[2 + j] >> 4) - 8;
+            s += v0 * (int32_t)(int8_t)y[2 + j] + v1 * (int32_t)(int8_t)y[2 + 16 + j];
+        }
+        sumf += (float)s * orc_f16_to_f32(rd_u16(x)) * orc_f16_to_f32(rd_u16(y));
+    }
+    return sumf;
+}
+
 void orc_block_sums(int type, int64_t k, const uint8_t *w, const uint8_t *xq, int32_t *S,
                     int32_t *Smin) {
     int8_t aux8[256];
@@ -420,6 +443,18 @@ void orc_block_sums(int type, int64_t k, const uint8_t *w, const uint8_t *xq, in
             S[b] = s;
             if (Smin) Smin[b] = 0;
         }
+    } else if (type == ORC_Q4_0) {
+        int64_t nb = k / ORC_QK8_0;
+        for (int64_t b = 0; b < nb; b++) {
+            const uint8_t *x = w + b * ORC_Q4_0_BYTES;
+            const uint8_t *y = xq + b * ORC_Q8_0_BYTES;
+            int32_t s = 0;
+            for (int j = 0; j < 16; j++)
+                s += ((int32_t)(x[2 + j] & 0x0F) - 8) * (int32_t)(int8_t)y[2 + j] +
+                     ((int32_t)(x[2 + j] >> 4) - 8) * (int32_t)(int8_t)y[2 + 16 + j];
+            S[b] = s;
+            if (Smin) Smin[b] = 0;
+        }
     } else if (type == ORC_Q8_0) {
         int64_t nb = k / ORC_QK8_0;
         for (int64_t b = 0; b < nb; b++) {
@@ -437,12 +472,12 @@ void orc_block_sums(int type, int64_t k, const uint8_t *w, const uint8_t *xq, in
  * rows in parallel.  Same arithmetic as orc_block_sums. */
 int orc_block_sums_mat(int type, int64_t m, int64_t n, int64_t k, const uint8_t *w, const uint8_t *xq,
                        int32_t *S, int32_t *Smin, int nthreads) {
-    if (type != ORC_Q4_K && type != ORC_Q5_K && type != ORC_Q6_K && type != ORC_Q8_0) return -2;
+    if (type != ORC_Q4_K && type != ORC_Q5_K && type != ORC_Q6_K && type != ORC_Q8_0 && type != ORC_Q4_0) return -2;
     int64_t wblk = orc_type_block_elems(type);
     if (k <= 0 || k % wblk != 0 || m < 0 || n < 0) return -3;
     const int64_t nblk = k / wblk;
     const size_t row_w = (size_t)nblk * orc_type_block_bytes(type);
-    const int at = type == ORC_Q8_0 ? ORC_Q8_0 : ORC_Q8_K;
+    const int at = type == ORC_Q8_0 || type == ORC_Q4_0 ? ORC_Q8_0 : ORC_Q8_K;
     const size_t row_x = (size_t)(k / orc_type_block_elems(at)) * orc_type_block_bytes(at);
     if (nthreads <= 0) nthreads = orc_max_threads();
 #pragma omp parallel for schedule(dynamic, 64) num_threads(nthreads)
@@ -456,12 +491,13 @@ int orc_block_sums_mat(int type, int64_t m, int64_t n, int64_t k, const uint8_t 
 
 /* ---------------------------------------------------------- matmul */
 
-static int act_type_for(int type) { return type == ORC_Q8_0 ? ORC_Q8_0 : ORC_Q8_K; }
+static int act_type_for(int type) { return type == ORC_Q8_0 || type == ORC_Q4_0 ? ORC_Q8_0 : ORC_Q8_K; }
 
 static float vec_dot(int type, int64_t k, const uint8_t *w, const uint8_t *xq) {
     switch (type) {
     case ORC_Q4_K: return orc_vec_dot_q4k_q8k(k, w, xq);
     case ORC_Q5_K: return orc_vec_dot_q5k_q8k(k, w, xq);
+    case ORC_Q4_0: return orc_vec_dot_q4_0_q8_0(k, w, xq);
     case ORC_Q6_K: return orc_vec_dot_q6k_q8k(k, w, xq);
     default: return orc_vec_dot_q8_0_q8_0(k, w, xq);
     }
@@ -480,7 +516,7 @@ int orc_max_threads(void) {
  * with_max_len(512); here OpenMP dynamic chunks of 256 columns). */
 int orc_matmul_preq(int type, int64_t m, int64_t k, int64_t n, const uint8_t *xq, float *dst,
                     const uint8_t *w, int nthreads) {
-    if (type != ORC_Q4_K && type != ORC_Q5_K && type != ORC_Q6_K && type != ORC_Q8_0) return -2;
+    if (type != ORC_Q4_K && type != ORC_Q5_K && type != ORC_Q6_K && type != ORC_Q8_0 && type != ORC_Q4_0) return -2;
     int64_t wblk = orc_type_block_elems(type);
     if (k <= 0 || k % wblk != 0 || m < 0 || n < 0) return -3;
     size_t row_w = (size_t)(k / wblk) * orc_type_block_bytes(type);
@@ -500,7 +536,7 @@ int orc_matmul_preq(int type, int64_t m, int64_t k, int64_t n, const uint8_t *xq
  * serially with T::VecDotType::from_float, then the column loop. */
 int orc_matmul(int type, int64_t m, int64_t k, int64_t n, const float *lhs, const uint8_t *w,
                float *dst, int nthreads) {
-    if (type != ORC_Q4_K && type != ORC_Q5_K && type != ORC_Q6_K && type != ORC_Q8_0) return -2;
+    if (type != ORC_Q4_K && type != ORC_Q5_K && type != ORC_Q6_K && type != ORC_Q8_0 && type != ORC_Q4_0) return -2;
     int64_t wblk = orc_type_block_elems(type);
     if (k <= 0 || k % wblk != 0 || m < 0 || n < 0) return -3;
     int at = act_type_for(type);
@@ -556,6 +592,18 @@ int orc_dequantize_row(int type, const uint8_t *w, int64_t k, float *out) {
             q6k_unpack(x, x + 128, aux8);
             float d = orc_f16_to_f32(rd_u16(x + 208));
             for (int e = 0; e < 256; e++) out[b * 256 + e] = d * (float)(sc[e / 16] * aux8[e]);
+        }
+        return 0;
+    }
+    if (type == ORC_Q4_0) {
+        if (k % ORC_QK8_0) return -3;
+        for (int64_t b = 0; b < k / ORC_QK8_0; b++) {
+            const uint8_t *x = w + b * ORC_Q4_0_BYTES;
+            float d = orc_f16_to_f32(rd_u16(x));
+            for (int j = 0; j < 16; j++) {
+                out[b * 32 + j] = (float)((int32_t)(x[2 + j] & 0x0F) - 8) * d;
+                out[b * 32 + j + 16] = (float)((int32_t)(x[2 + j] >> 4) - 8) * d;
+            }
         }
         return 0;
     }

@@ -22,6 +22,7 @@
  *   Q5_K 176 B: f16 d @0, f16 dmin @2, u8 scales[12] @4, u8 qh[32] @16, u8 qs[128] @48
  *   Q6_K 210 B: u8 ql[128] @0, u8 qh[64] @128, i8 scales[16] @192, f16 d @208
  *   Q8_0  34 B: f16 d @0, i8 qs[32] @2
+ *   Q4_0  18 B: f16 d @0, u8 qs[16] @2 (element j = qs[j] & 15, j+16 = qs[j] >> 4; value d*(q-8))
  *   Q8_K 292 B: f32 d @0, i8 qs[256] @4, i16 bsums[16] @260
  */
 #ifndef ARM_AI_ORACLE_H
@@ -49,6 +50,7 @@ enum {
 #define ORC_Q5K_BYTES 176
 #define ORC_Q6K_BYTES 210
 #define ORC_Q8_0_BYTES 34
+#define ORC_Q4_0_BYTES 18
 #define ORC_Q8K_BYTES 292
 
 /* IEEE binary16 <-> binary32 as the `half` crate does it (RNE). */
@@ -70,11 +72,13 @@ float orc_vec_dot_q4k_q8k(int64_t k, const uint8_t *w, const uint8_t *xq);
 float orc_vec_dot_q5k_q8k(int64_t k, const uint8_t *w, const uint8_t *xq);
 float orc_vec_dot_q6k_q8k(int64_t k, const uint8_t *w, const uint8_t *xq);
 float orc_vec_dot_q8_0_q8_0(int64_t k, const uint8_t *w, const uint8_t *xq);
+float orc_vec_dot_q4_0_q8_0(int64_t k, const uint8_t *w, const uint8_t *xq);
 
 /* Integer intermediates per block (the bit-exact gate).
  * Q4_K, Q5_K: S[b] = sum_j sc_j * sum_{e in j} q_e*qx_e ; Smin[b] = sum_g bsums_g * m_{g/2}
  * Q6_K: S[b] = sum_j sc_j * sum_{e in j} q6_e*qx_e ; Smin unused
- * Q8_0: S[b] = sum_{32} qw*qx (per 32-block)                                     */
+ * Q8_0: S[b] = sum_{32} qw*qx (per 32-block)
+ * Q4_0: S[b] = sum_{32} (q-8)*qx (per 32-block)                                 */
 void orc_block_sums(int type, int64_t k, const uint8_t *w, const uint8_t *xq,
                     int32_t *S, int32_t *Smin);
 

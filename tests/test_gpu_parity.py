@@ -17,7 +17,7 @@ pytestmark = pytest.mark.gpu
 
 def _xdeq_abs(x, wtype):
     xq = O.quantize(x, O.act_type(wtype))
-    if wtype == O.Q8_0:
+    if wtype in (O.Q8_0, O.Q4_0):
         d, q = O.q8_0_fields(xq)
     else:
         d, q, _ = O.q8k_fields(xq)
@@ -191,7 +191,7 @@ def test_prefill_gemm_q6k_extreme_values(ctx):
 
 # ------------------------------------------------------ batch and K coverage
 @pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 7, 8, 11])
-@pytest.mark.parametrize("wtype", [S.TYPE_Q4_K, S.TYPE_Q5_K, S.TYPE_Q6_K, S.TYPE_Q8_0])
+@pytest.mark.parametrize("wtype", [S.TYPE_Q4_K, S.TYPE_Q5_K, S.TYPE_Q6_K, S.TYPE_Q8_0, S.TYPE_Q4_0])
 def test_batches(ctx, wtype, m):
     W = S.make_weight(wtype, 300, 2048, seed=m + wtype)
     x = S.make_activation(m, 2048, seed=100 + m)
@@ -199,7 +199,7 @@ def test_batches(ctx, wtype, m):
 
 
 @pytest.mark.parametrize("k", [256, 512, 5632, 16384, 20480])
-@pytest.mark.parametrize("wtype", [S.TYPE_Q4_K, S.TYPE_Q5_K, S.TYPE_Q6_K, S.TYPE_Q8_0])
+@pytest.mark.parametrize("wtype", [S.TYPE_Q4_K, S.TYPE_Q5_K, S.TYPE_Q6_K, S.TYPE_Q8_0, S.TYPE_Q4_0])
 @pytest.mark.parametrize("m", [1, 8])
 def test_k_coverage(ctx, wtype, k, m):
     W = S.make_weight(wtype, 70, k, seed=k + m)
@@ -246,6 +246,31 @@ def test_q5k_extreme_values(ctx):
     W.blocks = S.pack_q5k(W.d, W.dmin, W.sc, W.mn, W.q)
     x = np.repeat(rng.standard_normal((m, k // 256)).astype(np.float32), 256, axis=1)
     check_matmul(ctx, W, x, cond=False)
+
+
+# ------------------------------------------------------------ Q4_0 (matvec at any m)
+@pytest.mark.parametrize("n,k,m", [(4096, 4096, 1), (14336, 4096, 1), (4096, 14336, 8), (300, 96, 3),
+                                   (129, 1056, 5), (2048, 2048, 20)])
+def test_q4_0_matvec(ctx, n, k, m):
+    """Llama-3 FFN shapes of a Q4_0 file, rows whose block count is not a
+    multiple of 8 (96 and 1056 columns: padding blocks in the tile layout),
+    and a 20-row batch (passes of 8): block sums bit-exact."""
+    W = S.make_weight(S.TYPE_Q4_0, n, k, seed=n + k + 7)
+    x = S.make_activation(m, k, seed=m + k + 7)
+    check_matmul(ctx, W, x, cond=(k < 14336))
+
+
+def test_q4_0_extreme_values(ctx):
+    """Every quant 0 (value -8) against activation blocks of equal values
+    (quants +-127): |S| = 32 * 8 * 127 per block, and every quant 15."""
+    n, k, m = 64, 512, 2
+    rng = np.random.default_rng(27)
+    for qv in (0, 15):
+        W = S.make_weight(S.TYPE_Q4_0, n, k, seed=27)
+        W.q[:] = qv
+        W.blocks = S.pack_q4_0(W.d, W.q)
+        x = np.repeat(rng.standard_normal((m, k // 32)).astype(np.float32), 32, axis=1)
+        check_matmul(ctx, W, x, cond=False)
 
 
 # ------------------------------------------ Q8_0 prefill GEMM (int8 MFMA, m > 8)
@@ -298,7 +323,7 @@ def test_prefill_gemm_q8_0_subnormal_and_zero_scales(ctx):
     check_matmul(ctx, W, x, cond=False)
 
 
-@pytest.mark.parametrize("wtype", [S.TYPE_Q4_K, S.TYPE_Q5_K, S.TYPE_Q6_K, S.TYPE_Q8_0])
+@pytest.mark.parametrize("wtype", [S.TYPE_Q4_K, S.TYPE_Q5_K, S.TYPE_Q6_K, S.TYPE_Q8_0, S.TYPE_Q4_0])
 def test_subnormal_and_zero_scales(ctx, wtype):
     W = S.make_weight(wtype, 128, 1024, seed=8)
     rng = np.random.default_rng(8)
@@ -310,6 +335,8 @@ def test_subnormal_and_zero_scales(ctx, wtype):
         W.dmin = d[:, ::-1].copy()
     elif wtype == S.TYPE_Q6_K:
         W.blocks = S.pack_q6k(d, W.sc, W.q)
+    elif wtype == S.TYPE_Q4_0:
+        W.blocks = S.pack_q4_0(d, W.q)
     else:
         W.blocks = S.pack_q8_0(d, W.q)
     W.d = d
@@ -349,7 +376,7 @@ def test_higher_rank_input_and_determinism(ctx):
 
 
 @pytest.mark.parametrize("wtype,m", [(S.TYPE_Q4_K, 4), (S.TYPE_Q6_K, 1), (S.TYPE_Q8_0, 8), (S.TYPE_Q4_K, 40),
-                                     (S.TYPE_Q5_K, 3)])
+                                     (S.TYPE_Q5_K, 3), (S.TYPE_Q4_0, 2)])
 def test_device_pointer_entry_points(ctx, wtype, m):
     from arm_ai_amd import hip
 

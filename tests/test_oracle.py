@@ -127,9 +127,10 @@ def test_q8_0_known_answers():
 def _int_sums(W, xq, wtype):
     """S, Smin [m, n, nb] from the generator's element arrays (no unpacking)."""
     m = xq.shape[0]
-    if wtype == O.Q8_0:
+    if wtype in (O.Q8_0, O.Q4_0):
         _, qx = O.q8_0_fields(xq)  # [m, nb, 32]
-        Sx = np.einsum("nbe,mbe->mnb", W.q.astype(np.int64), qx.astype(np.int64))
+        qw = W.q.astype(np.int64) - (8 if wtype == O.Q4_0 else 0)
+        Sx = np.einsum("nbe,mbe->mnb", qw, qx.astype(np.int64))
         return Sx, np.zeros_like(Sx)
     _, qx, bs = O.q8k_fields(xq)  # [m, nb, 256], [m, nb, 16]
     if wtype in (O.Q4_K, O.Q5_K):
@@ -144,7 +145,7 @@ def _int_sums(W, xq, wtype):
     return Sx, np.zeros_like(Sx)
 
 
-WTYPES = [O.Q4_K, O.Q5_K, O.Q6_K, O.Q8_0]
+WTYPES = [O.Q4_K, O.Q5_K, O.Q6_K, O.Q8_0, O.Q4_0]
 
 
 @pytest.mark.parametrize("wtype", WTYPES)
@@ -173,7 +174,7 @@ def test_matmul_vs_f64_truth(wtype):
     W = S.make_weight(wtype, 96, k, seed=5)
     x = S.make_activation(2, k, seed=6)
     xq = O.quantize(x, O.act_type(wtype))
-    if wtype == O.Q8_0:
+    if wtype in (O.Q8_0, O.Q4_0):
         dx, qx = O.q8_0_fields(xq)
     else:
         dx, qx, _ = O.q8k_fields(xq)
@@ -357,3 +358,17 @@ def test_q5k_dot_is_plain_int8_dot_for_unit_scales():
         t = np.float32(t + np.float32(d * np.float32(lanes[l])))
     assert int(lanes.sum()) == int((q * qx[0, 0].astype(np.int64)).sum())
     assert got == np.float32(np.float32(-0.0) + t)
+
+
+@pytest.mark.parametrize("j,hi", [(0, False), (0, True), (7, True), (15, False), (15, True)])
+def test_q4_0_nibble_lands_on_element_j_or_j_plus_16(j, hi):
+    """GGML dequantize_row_q4_0: qs[j] & 15 is element j, qs[j] >> 4 element
+    j + 16, value d * (q - 8); the block is built byte by byte."""
+    b = np.zeros(18, np.uint8)
+    b[0:2] = np.array([2.0], np.float16).view(np.uint8)
+    b[2:18] = 0x88  # every quant 8 -> value 0
+    b[2 + j] = 0x8D if not hi else 0xD8  # q = 13 -> value 2 * 5 = 10
+    got = O.dequantize(O.Q4_0, b[None], 32)[0]
+    want = np.zeros(32)
+    want[j + 16 * hi] = 10.0
+    assert np.array_equal(got, want)
