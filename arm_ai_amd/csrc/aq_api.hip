@@ -39,6 +39,10 @@ struct aq_qweight {
     void *base = nullptr;
     size_t bytes = 0;
     WLayout layout{};
+    // the layout the prefill GEMM reads: the same tiles, except for Q4_0,
+    // whose GEMM runs on an expanded copy in the Q8_0 tile layout (values
+    // q - 8 as int8), kept after the decode tiles in the same allocation
+    WLayout glayout{};
 };
 
 namespace {
@@ -146,12 +150,14 @@ CallLayout call_layout(const aq_qweight *w, int64_t m, bool host_io, bool dump, 
     L.smin = off;
     if (dump) off += align_up((size_t)m * w->n * nblk * 4, 256);
     L.ws = off;
-    if (gemm) off += align_up(gemm_workspace_bytes(w->type, m, w->n, w->k), 256);
+    if (gemm) off += align_up(gemm_workspace_bytes(w->glayout.type, m, w->n, w->k), 256);
     L.total = off;
     return L;
 }
 
-bool use_gemm(const aq_qweight *w, int64_t m) { return m > 8 && gemm_workspace_bytes(w->type, m, w->n, w->k) != (size_t)-1; }
+bool use_gemm(const aq_qweight *w, int64_t m) {
+    return m > 8 && gemm_workspace_bytes(w->glayout.type, m, w->n, w->k) != (size_t)-1;
+}
 // 2 or more rows of Q4_K / Q6_K without a GEMM: quantizer kernel, then the
 // matrix-core matvec
 bool use_mmv(const aq_qweight *w, int64_t m) {
@@ -180,7 +186,7 @@ int run_matmul(aq_ctx *ctx, const aq_qweight *w, const float *d_x, int64_t m, fl
         e = act_q80(w->type) ? launch_quantize_q8_0(d_x, m, w->k, a, ctx->stream)
                                     : launch_quantize_q8k(d_x, m, w->k, a, ctx->stream);
         if (e != hipSuccess) return fail(AQ_ERR_HIP, "activation quantizer: %s", hipGetErrorString(e));
-        e = launch_gemm(w->layout, w->n, w->k, a, m, d_y, dS, dSmin, ws, ws_bytes, ctx->stream);
+        e = launch_gemm(w->glayout, w->n, w->k, a, m, d_y, dS, dSmin, ws, ws_bytes, ctx->stream);
         if (e == hipSuccess) return AQ_OK;
         if (e != hipErrorNotSupported) return fail(AQ_ERR_HIP, "gemm: %s", hipGetErrorString(e));
         e = launch_matvec(w->layout, w->n, w->k, nullptr, &a, m, d_y, dS, dSmin, ctx->stream);
@@ -293,7 +299,10 @@ static int upload_impl(aq_ctx *ctx, int type, const void *blocks, size_t nbytes,
     const int64_t rb_stride = (int64_t)slabs_of(type) * ng * 128;
     const size_t slab_bytes = align_up((size_t)rb_stride * (size_t)nrb, 256);
     const size_t d_bytes = type == AQ_TYPE_Q6_K ? align_up((size_t)nrb * ng * RB * 2, 256) : 0;
-    const size_t total = slab_bytes + d_bytes;
+    // Q4_0: the GEMM's expanded copy in the Q8_0 tile layout
+    const int64_t g_stride = type == AQ_TYPE_Q4_0 ? (int64_t)slabs_of(TYPE_Q8_0) * ng * 128 : 0;
+    const size_t g_bytes = align_up((size_t)g_stride * (size_t)nrb, 256);
+    const size_t total = slab_bytes + d_bytes + g_bytes;
     aq_qweight *w = new (std::nothrow) aq_qweight();
     if (!w) return fail(AQ_ERR_OOM, "out of host memory");
     if (hipMalloc(&w->base, total) != hipSuccess) {
@@ -312,6 +321,14 @@ static int upload_impl(aq_ctx *ctx, int type, const void *blocks, size_t nbytes,
     w->layout.type = type;
     w->layout.ng = ng;
     w->layout.rb_stride = rb_stride;
+    w->glayout = w->layout;
+    uint8_t *gslab = base + slab_bytes + d_bytes;
+    if (g_bytes) {
+        w->glayout.slab = gslab;
+        w->glayout.d = nullptr;
+        w->glayout.type = TYPE_Q8_0;
+        w->glayout.rb_stride = g_stride;
+    }
 
     int status = AQ_OK;
     // padding rows (n not a multiple of 8) and Q8_0 padding blocks must read as zeros
@@ -346,6 +363,9 @@ static int upload_impl(aq_ctx *ctx, int type, const void *blocks, size_t nbytes,
                                      d_bytes ? (uint16_t *)(base + slab_bytes) + (size_t)(r0 / RB) * ng * RB : nullptr,
                                      ctx->stream);
         if (e != hipSuccess) status = fail(AQ_ERR_HIP, "repack: %s", hipGetErrorString(e));
+        if (status == AQ_OK && g_bytes &&
+            (e = launch_expand_q4_0(src, rows, k, gslab + (size_t)(r0 / RB) * g_stride, ctx->stream)) != hipSuccess)
+            status = fail(AQ_ERR_HIP, "Q4_0 expansion: %s", hipGetErrorString(e));
         // the staging buffer is reused by the next chunk
         if (status == AQ_OK && hipStreamSynchronize(ctx->stream) != hipSuccess) status = fail(AQ_ERR_HIP, "upload sync failed");
     }
@@ -455,7 +475,7 @@ int aq_qmatmul_preq_device(aq_ctx *ctx, const aq_qweight *w, const void *d_act, 
     if (use_gemm(w, m)) {
         CallLayout L = call_layout(w, m, false, false, true);
         if ((rc = ensure_scratch(ctx, L.total))) return rc;
-        e = launch_gemm(w->layout, w->n, w->k, a, m, d_dst, nullptr, nullptr, (uint8_t *)ctx->scratch + L.ws,
+        e = launch_gemm(w->glayout, w->n, w->k, a, m, d_dst, nullptr, nullptr, (uint8_t *)ctx->scratch + L.ws,
                         L.total - L.ws, ctx->stream);
         if (e != hipSuccess && e != hipErrorNotSupported) return fail(AQ_ERR_HIP, "gemm: %s", hipGetErrorString(e));
     }

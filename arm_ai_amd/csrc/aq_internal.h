@@ -122,6 +122,10 @@ hipError_t launch_quantize_q8_0(const float *x, int64_t m, int64_t k, ActPlanes 
 // block, Q8_0 padding blocks) is not written: zero the tiles beforehand.
 hipError_t launch_repack(int type, const uint8_t *src, int64_t n, int64_t k, uint8_t *dst_slab, uint16_t *dst_d,
                          hipStream_t s);
+// GGUF Q4_0 blocks of n rows -> those rows of a Q8_0 row-block tile layout
+// holding the values q - 8 as int8 and the same f16 d (what the Q8_0 GEMM
+// reads).  Padding is not written: zero the tiles beforehand.
+hipError_t launch_expand_q4_0(const uint8_t *src, int64_t n, int64_t k, uint8_t *dst_slab, hipStream_t s);
 // Decode matvec (any m; batch rows are processed up to 8 at a time).  The
 // activation is either f32 (x != nullptr: quantised inside the kernel,
 // bit-identical to the quantizer kernels) or pre-quantised planes.

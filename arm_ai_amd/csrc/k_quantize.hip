@@ -144,6 +144,42 @@ __global__ __launch_bounds__(256) void repack_kernel(const uint8_t *__restrict__
     }
 }
 
+// Q4_0 -> Q8_0 tiles: one thread per source byte.  Block b = 8g + j of a
+// row: d -> piece 16 bytes 2j, 2j+1; qs byte t (elements t and t + 16) ->
+// piece 2j byte t = (qs & 15) - 8 and piece 2j + 1 byte t = (qs >> 4) - 8.
+__global__ __launch_bounds__(256) void expand_q4_0_kernel(const uint8_t *__restrict__ src, int64_t n, int64_t nblk,
+                                                          int ng, uint8_t *__restrict__ slab) {
+    constexpr int S = slabs_of(TYPE_Q8_0);
+    const int64_t rb_stride = (int64_t)ng * S * 128;
+    const int64_t total = n * nblk * 18;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t blk = i / 18;
+        const int o = (int)(i - blk * 18);
+        const int64_t row = blk / nblk, b = blk - row * nblk;
+        uint8_t *rbp = slab + (row >> 3) * rb_stride + (row & 7) * 16;
+        const int64_t g = b >> 3;
+        const int j = (int)(b & 7);
+        const uint8_t v = src[i];
+        if (o < 2) {
+            rbp[(g * S + 16) * 128 + 2 * j + o] = v;
+        } else {
+            const int t = o - 2;
+            rbp[(g * S + 2 * j) * 128 + t] = (uint8_t)(int8_t)((int)(v & 15) - 8);
+            rbp[(g * S + 2 * j + 1) * 128 + t] = (uint8_t)(int8_t)((int)(v >> 4) - 8);
+        }
+    }
+}
+
+hipError_t launch_expand_q4_0(const uint8_t *src, int64_t n, int64_t k, uint8_t *dst_slab, hipStream_t s) {
+    if (!src || !dst_slab || n <= 0 || k <= 0 || k % QK8_0) return hipErrorInvalidValue;
+    const int64_t nblk = k / QK8_0;
+    const int ng = groups_of(TYPE_Q4_0, k);
+    const int64_t total = n * nblk * 18;
+    const int64_t blocks = (total + 255) / 256, grid = blocks < 65536 ? blocks : 65536;
+    expand_q4_0_kernel<<<(unsigned)grid, 256, 0, s>>>(src, n, nblk, ng, dst_slab);
+    return hipGetLastError();
+}
+
 hipError_t launch_repack(int type, const uint8_t *src, int64_t n, int64_t k, uint8_t *dst_slab, uint16_t *dst_d,
                          hipStream_t s) {
     if (!src || !dst_slab || n <= 0 || k <= 0) return hipErrorInvalidValue;

@@ -190,7 +190,7 @@ def measure_prefill(ctx, wtype, n, k, m, steps, warmup, seed):
     kern_ms, _ = time_graph(ctx, wl.kernel, steps, warmup)
     ops = 2.0 * m * n * k
     out = {
-        "n": n, "k": k, "m": m, "weight_type": {12: "Q4_K", 14: "Q6_K", 8: "Q8_0"}[wtype],
+        "n": n, "k": k, "m": m, "weight_type": {12: "Q4_K", 14: "Q6_K", 8: "Q8_0", 2: "Q4_0"}[wtype],
         "step_us": round(step_ms * 1e3, 3),
         "step_TOPS": round(ops / (step_ms / 1e3) / 1e12, 1),
         "gemm_us": round(kern_ms * 1e3, 3),
@@ -238,6 +238,7 @@ PREFILL_CASES = {  # name: (weight type, n, k, m, seed)
     "c2_prefill_q6k_2048x5632_m512": (14, 2048, 5632, 512, 10),  # TinyLlama ffn_down (Q6_K layers)
     "c2_prefill_q6k_256x2048_m512": (14, 256, 2048, 512, 11),    # TinyLlama attn_v
     "prefill_q8_0_4096x4096_m512": (8, 4096, 4096, 512, 12),     # a Q8_0 GGUF's projection
+    "prefill_q4_0_4096x4096_m512": (2, 4096, 4096, 512, 15),     # Q4_0: the Q8_0 GEMM on the expanded copy
 }
 
 

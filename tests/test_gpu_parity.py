@@ -260,6 +260,15 @@ def test_q4_0_matvec(ctx, n, k, m):
     check_matmul(ctx, W, x, cond=(k < 14336))
 
 
+@pytest.mark.parametrize("n,k,m", [(1024, 2048, 64), (300, 1056, 40), (2048, 96, 17)])
+def test_q4_0_prefill_gemm(ctx, n, k, m):
+    """m > 8: the Q8_0 GEMM on the upload's expanded copy (values q - 8 as
+    int8), including rows with padding blocks: block sums bit-exact."""
+    W = S.make_weight(S.TYPE_Q4_0, n, k, seed=n + k + 9)
+    x = S.make_activation(m, k, seed=m + k + 9)
+    check_matmul(ctx, W, x, cond=False)
+
+
 def test_q4_0_extreme_values(ctx):
     """Every quant 0 (value -8) against activation blocks of equal values
     (quants +-127): |S| = 32 * 8 * 127 per block, and every quant 15."""
