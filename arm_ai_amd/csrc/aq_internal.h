@@ -126,6 +126,11 @@ hipError_t launch_repack(int type, const uint8_t *src, int64_t n, int64_t k, uin
 // holding the values q - 8 as int8 and the same f16 d (what the Q8_0 GEMM
 // reads).  Padding is not written: zero the tiles beforehand.
 hipError_t launch_expand_q4_0(const uint8_t *src, int64_t n, int64_t k, uint8_t *dst_slab, hipStream_t s);
+// Measurement aid (k_probe.hip): stream `bytes` of buf (16-byte aligned, a
+// multiple of 16) through a read-only kernel; out needs stream_read_grid()
+// entries.
+int stream_read_grid();
+hipError_t launch_stream_read(const void *buf, size_t bytes, uint32_t *out, hipStream_t s);
 // Decode matvec (any m; batch rows are processed up to 8 at a time).  The
 // activation is either f32 (x != nullptr: quantised inside the kernel,
 // bit-identical to the quantizer kernels) or pre-quantised planes.

@@ -359,6 +359,27 @@ def measure_vendor_int8(m, n, k, steps, warmup):
             "rotating_weight_copies": copies}
 
 
+def measure_stream_read(ctx, nbytes, steps, warmup):
+    """The read rate of a kernel that only streams nbytes (aq_stream_read_probe),
+    over enough rotating buffers to exceed the Infinity Cache: the practical
+    ceiling for a single launch of that many bytes on this GPU."""
+    import arm_ai_amd as A
+    from arm_ai_amd import hip
+
+    L = A._lib.load()
+    nbytes = nbytes // 16 * 16
+    copies = copies_for(nbytes)
+    bufs = [hip.DeviceBuffer(nbytes) for _ in range(copies)]  # contents do not matter to a read
+    out = hip.DeviceBuffer(4 * int(L.aq_stream_read_probe_out_words()))
+    fn = lambda i: L.aq_stream_read_probe(ctx.handle, bufs[i % copies].ptr, nbytes, out.ptr)
+    assert fn(0) == 0
+    ms, _ = time_graph(ctx, fn, steps, warmup)
+    gbps = nbytes / (ms / 1e3) / 1e9
+    return {"kernel": "stream_read_kernel (reads only; 512 x 512 threads, 2 x 16 B in flight per thread)",
+            "bytes": nbytes, "us": round(ms * 1e3, 3), "GBps": round(gbps, 1),
+            "frac_hbm": round(gbps / HBM_PEAK_GBS, 4), "rotating_copies": copies}
+
+
 def run_decode_child(name):
     """Run a decode (or vendor reference) case in a child process: the driver's
     torch glue needs torch imported before this library is loaded (one HIP
@@ -486,6 +507,10 @@ def main() -> int:
             "avg_launch_us": round(step_ms * 1e3, 3),
         },
     }
+    ref = measure_stream_read(ctx, wl.step_bytes, args.steps, args.warmup)
+    log(f"read-only kernel on the same {ref['bytes']} bytes: {ref['us']} us ({ref['GBps']} GB/s, {ref['frac_hbm']} of peak)")
+    result["roofline"]["read_only_reference"] = ref
+    result["roofline"]["frac_of_read_only_reference"] = round(achieved / ref["GBps"], 4)
     if not args.no_cpu:
         log("cpu baseline ...")
         result["cpu_baseline"] = cpu_baseline(wl)
