@@ -152,7 +152,7 @@ hipError_t launch_gemm(const WLayout &w, int64_t n, int64_t k, const ActPlanes &
 // Workspace bytes launch_gemm needs for this shape, or (size_t)-1 if the
 // weight type / shape has no GEMM (the matvec then serves m > 8 too).
 size_t gemm_workspace_bytes(int type, int64_t m, int64_t n, int64_t k);
-// The Q6_K GEMM on f16 MFMA (k_gemm6.hip), reached through launch_gemm /
+// The Q6_K and Q5_K GEMM on f16 MFMA (k_gemm6.hip), reached through launch_gemm /
 // gemm_workspace_bytes; its workspace holds the f16 copy of the activation
 // quants and the split-K partials.
 size_t gemm6_workspace_bytes(int64_t m, int64_t n, int64_t k);

@@ -388,7 +388,7 @@ hipError_t launch_splitk_reduce(const float *part, float *y, int m, int n, int n
 }
 
 size_t gemm_workspace_bytes(int type, int64_t m, int64_t n, int64_t k) {
-    if (type == TYPE_Q6_K) return gemm6_workspace_bytes(m, n, k);
+    if (type == TYPE_Q6_K || type == TYPE_Q5_K) return gemm6_workspace_bytes(m, n, k);
     if (type == TYPE_Q8_0) return gemm8_workspace_bytes(m, n, k);
     if (type != TYPE_Q4_K || m <= 0 || n <= 0 || k <= 0 || k % QK_K || k > (1 << 24)) return (size_t)-1;
     const int64_t mc = gemm_chunk_rows(m, k);
@@ -401,7 +401,7 @@ size_t gemm_workspace_bytes(int type, int64_t m, int64_t n, int64_t k) {
 
 hipError_t launch_gemm(const WLayout &w, int64_t n, int64_t k, const ActPlanes &x, int64_t m, float *y, int32_t *S,
                        int32_t *Smin, void *ws, size_t ws_bytes, hipStream_t s) {
-    if (w.type == TYPE_Q6_K) return launch_gemm6(w, n, k, x, m, y, S, Smin, ws, ws_bytes, s);
+    if (w.type == TYPE_Q6_K || w.type == TYPE_Q5_K) return launch_gemm6(w, n, k, x, m, y, S, Smin, ws, ws_bytes, s);
     if (w.type == TYPE_Q8_0) return launch_gemm8(w, n, k, x, m, y, S, Smin, ws, ws_bytes, s);
     if (w.type != TYPE_Q4_K) return hipErrorNotSupported;
     if (!w.slab || !y || !x.qs || !x.d || !x.bsum16 || m <= 0 || n <= 0 || k <= 0 || k % QK_K) return hipErrorInvalidValue;

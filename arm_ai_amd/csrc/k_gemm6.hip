@@ -1,5 +1,5 @@
-// k_gemm6.hip -- prefill GEMM (m > 8) for Q6_K weights on the f16 matrix
-// cores, gfx950.
+// k_gemm6.hip -- prefill GEMM (m > 8) for Q6_K and Q5_K weights on the f16
+// matrix cores, gfx950.
 //
 // Replaces the M-row loop of candle-core 0.8.4 k_quants::matmul<BlockQ6K> at
 // prefill (native/arm_ai_nif/src/llama_candle.rs:93): for TinyLlama Q4_K_M
@@ -34,9 +34,25 @@
 // (tile, k-split) are dealt so that all m-tiles and k-splits of one n-tile run
 // on one XCD.  Split-K partials are summed in split order by the Q4_K GEMM's
 // reduce launch.
+//
+// Q5_K (candle-core 0.8.4 k_quants::matmul<BlockQ5K>).  Per super-block
+//   y[m][n] += d_x * (d_w * S - dmin_w * Smin),
+//   S    = sum_j sc_j * sum_{e in j} q5_e * qx_e   (8 sub-blocks of 32, q5 in 0..31)
+//   Smin = sum_g bsums[m,g] * mn_{g/2}              (16 groups of 16)
+// The weight operand sc_j * q5 <= 63 * 31 = 1953 is an integer exact in f16,
+// built as (1024 + q5) * sc - 1024 * sc in one fma (one rounding, of an exact
+// integer); every partial sum of two sub-blocks (64 elements) is at most
+// 64 * 1953 * 128 < 2^24, so four accumulator chains of four MFMAs each hold
+// exact integers, and S is their sum (exact in int32 for the dump; in f32 for
+// the output).  Smin is one M x 16 by 16 x N f16 MFMA per super-block of
+// bsums (|.| <= 2048, exact in f16) and mins (<= 63), every partial sum below
+// 16 * 2048 * 63 < 2^24, so exact.  Piece 0 of the group (d, dmin, the twelve
+// packed scale bytes) is loaded whole by each lane; the bsums rows of the tile
+// are copied into LDS beside the quants.
 #include "aq_internal.h"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace aq {
 
@@ -60,11 +76,12 @@ struct Gemm6Params {
     int ng;
     const uint16_t *x16;  // activation quants as f16 [m][k]
     const float *xd;      // [m][ng]
+    const uint16_t *xbs;  // Q5_K: bsums as f16 [m][k/16]
     float *y;
     int m, n, k;
     int ntm, tiles, splits, kbs, items, per_xcd;
     float *part;          // [tiles][splits][64][128] (splits > 1)
-    int32_t *S, *Smin;    // integer dump [m][n][ng] or null (Smin: zeros, Q6_K has no min term)
+    int32_t *S, *Smin;    // integer dump [m][n][ng] or null (Q6_K has no min term: Smin zeros)
 };
 
 // One lane's weight bytes of one super-block: bytes 8h..8h+7 of the 8 ql and
@@ -75,10 +92,18 @@ struct W6 {
     uint32_t d;
 };
 
+// One lane's weight bytes of one Q5_K super-block: bytes 8h..8h+7 of the 8 qs
+// and 2 qh pieces of its column, and the whole of piece 0 (d, dmin, scales).
+struct W5 {
+    u32x2 qs[8], qh[2];
+    u32x4 meta;
+};
+
 struct Lds6 {
     static constexpr int QS = G6M * 512;  // f16 quants [64 rows][256], chunk c of row r at c ^ (r & 31)
     static constexpr int DX = QS;         // d_x [64] f32
-    static constexpr int STAGE = QS + 256;
+    static constexpr int BS = QS + 256;   // Q5_K: bsums [64 rows][16] f16
+    static constexpr int STAGE = BS + G6M * 32;
     static constexpr int BYTES = 2 * STAGE;
 };
 
@@ -125,8 +150,49 @@ __device__ __forceinline__ v8h w6_operand(const W6 &W, int j) {
     return r;
 }
 
-template <bool DUMP>
-__global__ __launch_bounds__(256, 2) void gemm_q6k_kernel(Gemm6Params p) {
+__device__ __forceinline__ void load_w5(W5 &W, const rsrc_t &rw, uint32_t off, int b, int ng) {
+    const bool ok = b < ng;
+    const uint32_t o = ok ? off + (uint32_t)(b * 11 * 128) : BUF_OOB;
+    // piece 0 whole (this lane's h offset removed), then qh, then qs
+    W.meta = __builtin_amdgcn_raw_buffer_load_b128(rw, ok ? o & ~15u : BUF_OOB, 0, BUF_NT);
+#pragma unroll
+    for (int i = 0; i < 2; i++) W.qh[i] = __builtin_amdgcn_raw_buffer_load_b64(rw, o + (1 + i) * 128, 0, BUF_NT);
+#pragma unroll
+    for (int i = 0; i < 8; i++) W.qs[i] = __builtin_amdgcn_raw_buffer_load_b64(rw, o + (3 + i) * 128, 0, BUF_NT);
+}
+
+// The 8 f16 weight operands sc * q5 of MFMA j, elements 16j + 8h .. 16j + 8h + 7
+// of this lane's column's super-block: chunk c = j / 4 of 64 elements, low
+// nibbles of qs[32c ..] for its first 32 elements and high nibbles for the
+// rest, the fifth bit from qh bit 2c (low) or 2c + 1 (high); sub-block j / 2.
+__device__ __forceinline__ v8h w5_operand(const W5 &W, int j, uint32_t sc) {
+    const int c = j >> 2, hi = (j >> 1) & 1, odd = j & 1;
+    const u32x2 qs = W.qs[2 * c + odd];
+    const u32x2 qh = W.qh[odd];
+    uint32_t q[2];
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const uint32_t nib = hi ? (qs[i] >> 4) & 0x0F0F0F0Fu : qs[i] & 0x0F0F0F0Fu;
+        q[i] = nib | (((qh[i] >> (2 * c + hi)) & 0x01010101u) << 4);
+    }
+    const _Float16 s = (_Float16)(int)sc;
+    const _Float16 o = (_Float16)(-1024 * (int)sc);  // exact: sc * 2^10 <= 64512
+    const h2 s2 = {s, s}, o2 = {o, o};
+    v8h r;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint32_t u = __builtin_amdgcn_perm(0u, q[i >> 1], (i & 1) ? 0x0C030C02u : 0x0C010C00u) | 0x64006400u;
+        const h2 f = __builtin_bit_cast(h2, u);
+        const h2 v = __builtin_elementwise_fma(f, s2, o2);
+        r[2 * i] = v[0];
+        r[2 * i + 1] = v[1];
+    }
+    return r;
+}
+
+template <int TYPE, bool DUMP>
+__global__ __launch_bounds__(256, 2) void gemm_f16w_kernel(Gemm6Params p) {
+    constexpr bool Q5 = TYPE == TYPE_Q5_K;
     __shared__ __align__(16) uint8_t lds[Lds6::BYTES];
     const int xcd = blockIdx.x % NXCD6, local = blockIdx.x / NXCD6;
     const int item = xcd * p.per_xcd + local;
@@ -157,18 +223,26 @@ __global__ __launch_bounds__(256, 2) void gemm_q6k_kernel(Gemm6Params p) {
         qoff[i] = (uint32_t)((m0 + r) * k * 2 + 16 * (cp ^ (r & 31)));
     }
     const uint32_t dxoff = (uint32_t)((m0 + lane) * ng * 4);
+    // Q5_K bsums: waves 1 and 2 copy rows 0..31 and 32..63, lane L row L / 2,
+    // groups 8 (L % 2) .. 8 (L % 2) + 7
+    const rsrc_t rbs = buf_rsrc(p.xbs, Q5 ? (uint32_t)((int64_t)p.m * (k / 16) * 2) : 0u);
+    const uint32_t bsoff = (uint32_t)(((m0 + 32 * ((wave - 1) & 1) + (lane >> 1)) * (k / 16) + 8 * (lane & 1)) * 2);
     // weights: this lane's column is row (ccol % 8) of the tile's row block ccol / 8
     const int nrb = (p.n + RB - 1) / RB;
     const int rb_here = min(16, nrb - 16 * tn);
     const rsrc_t rw = buf_rsrc(p.w + (int64_t)16 * tn * p.rb_stride, (uint32_t)(rb_here * p.rb_stride));
-    const rsrc_t rwd = buf_rsrc(p.wd + (int64_t)16 * tn * ng * RB, (uint32_t)(rb_here * ng * RB * 2));
+    const rsrc_t rwd = Q5 ? rw : buf_rsrc(p.wd + (int64_t)16 * tn * ng * RB, (uint32_t)(rb_here * ng * RB * 2));
     const uint32_t woff = (uint32_t)((ccol >> 3) * p.rb_stride + (ccol & 7) * 16 + 8 * h);
     const uint32_t wdoff = (uint32_t)((((ccol >> 3) * ng) * RB + (ccol & 7)) * 2);
 
+    // b past the range (the step after the last) re-reads the last super-block:
+    // the scalar offset is kept inside the buffers
     auto issue = [&](uint8_t *st, int b) {
+        b = min(b, kb1 - 1);
 #pragma unroll
         for (int i = 0; i < 8; i++) buf_to_lds16(rq, st + 1024 * (8 * wave + i), qoff[i], b * 512);
         if (wave == 0) buf_to_lds4(rdx, st + Lds6::DX, dxoff, b * 4);  // wave-uniform
+        if (Q5 && (wave == 1 || wave == 2)) buf_to_lds16(rbs, st + Lds6::BS + 1024 * (wave - 1), bsoff, b * 32);
     };
 
     v16f yacc[2];
@@ -177,12 +251,13 @@ __global__ __launch_bounds__(256, 2) void gemm_q6k_kernel(Gemm6Params p) {
 #pragma unroll
         for (int r = 0; r < 16; r++) yacc[t][r] = 0.0f;
 
-    auto compute = [&](const uint8_t *st, const W6 &W, int b) {
+    auto read_a = [&](const uint8_t *st, int t, int j) {
+        const int R = 32 * t + l32, C = 2 * j + h;
+        return *(const v8h *)(st + R * 512 + 16 * (C ^ (R & 31)));
+    };
+
+    auto compute6 = [&](const uint8_t *st, const W6 &W, int b) {
         v16f acc[2][2];  // [tile][sub-blocks 0..7 / 8..15]
-        auto read_a = [&](int t, int j) {
-            const int R = 32 * t + l32, C = 2 * j + h;
-            return *(const v8h *)(st + R * 512 + 16 * (C ^ (R & 31)));
-        };
 #pragma unroll
         for (int j = 0; j < 16; j++) {
             const v8h bw = w6_operand(W, j);
@@ -190,7 +265,7 @@ __global__ __launch_bounds__(256, 2) void gemm_q6k_kernel(Gemm6Params p) {
             for (int t = 0; t < 2; t++) {
                 const v16f z = {0};
                 const int c = j >> 3;
-                acc[t][c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(read_a(t, j), bw, (j & 7) == 0 ? z : acc[t][c], 0, 0, 0);
+                acc[t][c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(read_a(st, t, j), bw, (j & 7) == 0 ? z : acc[t][c], 0, 0, 0);
             }
         }
         const float dw = f16_bits_to_f32(W.d);
@@ -217,23 +292,97 @@ __global__ __launch_bounds__(256, 2) void gemm_q6k_kernel(Gemm6Params p) {
         }
     };
 
+    auto compute5 = [&](const uint8_t *st, const W5 &W, int b) {
+        // scales / mins of this lane's column (candle's utmp form of get_scale_min_k4)
+        const uint32_t u0 = W.meta.y, u1 = W.meta.z, u2 = W.meta.w;
+        const uint32_t sc03 = u0 & 0x3F3F3F3Fu;
+        const uint32_t sc47 = (u2 & 0x0F0F0F0Fu) | (((u0 >> 6) & 0x03030303u) << 4);
+        const uint32_t mn03 = u1 & 0x3F3F3F3Fu;
+        const uint32_t mn47 = ((u2 >> 4) & 0x0F0F0F0Fu) | (((u1 >> 6) & 0x03030303u) << 4);
+        // chain c (sub-blocks 2c, 2c + 1) is exact; S in f32 = ((c0 + c1) + c2) + c3,
+        // folded as each chain ends; the dump keeps the chains for the int32 sum
+        v16f cur[2], tot[2], keep[2][DUMP ? 4 : 1];
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            const int sb = j >> 1;
+            const uint32_t sc = ((sb < 4 ? sc03 : sc47) >> (8 * (sb & 3))) & 0xffu;
+            const v8h bw = w5_operand(W, j, sc);
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
+                const v16f z = {0};
+                cur[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(read_a(st, t, j), bw, (j & 3) == 0 ? z : cur[t], 0, 0, 0);
+                if ((j & 3) == 3) {
+                    tot[t] = j == 3 ? cur[t] : tot[t] + cur[t];
+                    if (DUMP) keep[t][DUMP ? j >> 2 : 0] = cur[t];
+                }
+            }
+        }
+        // Smin: A[m][g] = bsums (g = 8h + i), B[g][n] = mn[g/2]
+        const uint32_t mw = h ? mn47 : mn03;
+        v8h bmn;
+#pragma unroll
+        for (int i = 0; i < 8; i++) bmn[i] = (_Float16)(int)((mw >> (8 * (i >> 1))) & 0xffu);
+        v16f sm[2];
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            const v8h abs = *(const v8h *)(st + Lds6::BS + (32 * t + l32) * 32 + 16 * h);
+            const v16f z = {0};
+            sm[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(abs, bmn, z, 0, 0, 0);
+        }
+        const float dw = f16_bits_to_f32(W.meta.x), dmw = f16_bits_to_f32(W.meta.x >> 16);
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+#pragma unroll
+            for (int g4 = 0; g4 < 4; g4++) {
+                const v4f dx4 = *(const v4f *)(st + Lds6::DX + 4 * (32 * t + 8 * g4 + 4 * h));
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int r = 4 * g4 + i;
+                    // f32 combine: y += d_x * (d_w * S - dmin_w * Smin)
+                    yacc[t][r] = __builtin_fmaf(dx4[i], __builtin_fmaf(-dmw, sm[t][r], dw * tot[t][r]), yacc[t][r]);
+                    if (DUMP) {
+                        const int row = m0 + 32 * t + 8 * g4 + 4 * h + i;
+                        if (row < p.m && col_ok) {
+                            const int64_t o = ((int64_t)row * p.n + col) * ng + b;
+                            int si = 0;
+#pragma unroll
+                            for (int c = 0; c < (DUMP ? 4 : 1); c++) si += (int)keep[t][c][r];
+                            p.S[o] = si;
+                            p.Smin[o] = (int)sm[t][r];
+                        }
+                    }
+                }
+            }
+        }
+    };
+
+    using WR = typename std::conditional<Q5, W5, W6>::type;
+    auto load_w = [&](WR &W, int b) {
+        if constexpr (Q5) load_w5(W, rw, woff, b, kb1);
+        else load_w6(W, rw, rwd, woff, wdoff, b, kb1);
+    };
+    auto compute = [&](const uint8_t *st, const WR &W, int b) {
+        if constexpr (Q5) compute5(st, W, b);
+        else compute6(st, W, b);
+    };
+
     // Two main stages and two weight register sets, one super-block ahead:
     // step b waits for its copies and loads (all this wave's outstanding
     // memory operations), a barrier, then issues step b + 1's.
-    W6 wa, wb;
+    WR wa, wb;
     issue(lds, kb0);
-    load_w6(wa, rw, rwd, woff, wdoff, kb0, kb1);
+    load_w(wa, kb0);
     for (int b = kb0; b < kb1; b += 2) {
         wait_vmcnt<0>();
         stage_barrier();
-        issue(lds + Lds6::STAGE, b + 1);  // past kb1: reads rows past the range (zeros) or unused data
-        load_w6(wb, rw, rwd, woff, wdoff, b + 1, kb1);
+        issue(lds + Lds6::STAGE, b + 1);
+        load_w(wb, b + 1);  // past kb1: zeros
         compute(lds, wa, b);
         if (b + 1 >= kb1) break;
         wait_vmcnt<0>();
         stage_barrier();
         issue(lds, b + 2);
-        load_w6(wa, rw, rwd, woff, wdoff, b + 2, kb1);
+        load_w(wa, b + 2);
         compute(lds + Lds6::STAGE, wb, b + 1);
     }
     wait_vmcnt<0>();  // no copy may still be landing when the workgroup ends
@@ -311,8 +460,10 @@ size_t gemm6_workspace_bytes(int64_t m, int64_t n, int64_t k) {
 
 hipError_t launch_gemm6(const WLayout &w, int64_t n, int64_t k, const ActPlanes &x, int64_t m, float *y, int32_t *S,
                         int32_t *Smin, void *ws, size_t ws_bytes, hipStream_t s) {
-    if (w.type != TYPE_Q6_K) return hipErrorNotSupported;
-    if (!w.slab || !w.d || !y || !x.qs || !x.d || m <= 0 || n <= 0 || k <= 0 || k % QK_K) return hipErrorInvalidValue;
+    if (w.type != TYPE_Q6_K && w.type != TYPE_Q5_K) return hipErrorNotSupported;
+    const bool q5 = w.type == TYPE_Q5_K;
+    if (!w.slab || (!q5 && !w.d) || (q5 && !x.bsum16) || !y || !x.qs || !x.d || m <= 0 || n <= 0 || k <= 0 || k % QK_K)
+        return hipErrorInvalidValue;
     if (m > 0x7fffffff || n > 0x7fffffff || k > (1 << 24) || w.ng != k / QK_K) return hipErrorInvalidValue;
     if ((int64_t)16 * w.rb_stride >= ((int64_t)1 << 31)) return hipErrorNotSupported;
     if ((S == nullptr) != (Smin == nullptr)) return hipErrorInvalidValue;
@@ -336,6 +487,7 @@ hipError_t launch_gemm6(const WLayout &w, int64_t n, int64_t k, const ActPlanes 
         p.ng = ng;
         p.x16 = x16;
         p.xd = x.d + r0 * ng;
+        p.xbs = q5 ? x.bsum16 + r0 * (k / 16) : nullptr;
         p.y = y + r0 * n;
         p.m = (int)mm;
         p.n = (int)n;
@@ -350,8 +502,13 @@ hipError_t launch_gemm6(const WLayout &w, int64_t n, int64_t k, const ActPlanes 
         p.S = S ? S + r0 * n * ng : nullptr;
         p.Smin = Smin ? Smin + r0 * n * ng : nullptr;
         const unsigned grid = (unsigned)(p.per_xcd * NXCD6);
-        if (S) gemm_q6k_kernel<true><<<grid, 256, 0, s>>>(p);
-        else gemm_q6k_kernel<false><<<grid, 256, 0, s>>>(p);
+        if (q5) {
+            if (S) gemm_f16w_kernel<TYPE_Q5_K, true><<<grid, 256, 0, s>>>(p);
+            else gemm_f16w_kernel<TYPE_Q5_K, false><<<grid, 256, 0, s>>>(p);
+        } else {
+            if (S) gemm_f16w_kernel<TYPE_Q6_K, true><<<grid, 256, 0, s>>>(p);
+            else gemm_f16w_kernel<TYPE_Q6_K, false><<<grid, 256, 0, s>>>(p);
+        }
         if ((e = hipGetLastError()) != hipSuccess) return e;
         if (g.splits > 1) {
             e = launch_splitk_reduce(p.part, p.y, p.m, p.n, g.ntm, G6M, g.splits, g.tiles, s);

@@ -47,6 +47,7 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
 INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA
+F16_PEAK_TFLOPS = 2500.0  # MI355X dense f16 MFMA
 MALL_BYTES = 256 << 20
 METRIC = "Q4_K matvec HBM GB/s (% of peak) + prefill int8 TOPS; decode tok/s"
 
@@ -184,19 +185,22 @@ def measure(ctx, wtype, n, k, m, steps, warmup, seed):
 
 def measure_prefill(ctx, wtype, n, k, m, steps, warmup, seed):
     """Prefill GEMM at m rows: quantiser kernel + GEMM (step) and the GEMM alone
-    (Q4_K: int8 MFMA; Q6_K: f16 MFMA after its f16 copy of the quants)."""
+    (Q4_K, Q8_0, Q4_0: int8 MFMA; Q5_K, Q6_K: f16 MFMA after the f16 copy of
+    the quants, which the GEMM time includes)."""
     wl = Workload(ctx, wtype, n, k, m, seed)
     step_ms, _ = time_graph(ctx, wl.step, steps, warmup)
     kern_ms, _ = time_graph(ctx, wl.kernel, steps, warmup)
     ops = 2.0 * m * n * k
     out = {
-        "n": n, "k": k, "m": m, "weight_type": {12: "Q4_K", 14: "Q6_K", 8: "Q8_0", 2: "Q4_0"}[wtype],
+        "n": n, "k": k, "m": m, "weight_type": {12: "Q4_K", 13: "Q5_K", 14: "Q6_K", 8: "Q8_0", 2: "Q4_0"}[wtype],
         "step_us": round(step_ms * 1e3, 3),
         "step_TOPS": round(ops / (step_ms / 1e3) / 1e12, 1),
         "gemm_us": round(kern_ms * 1e3, 3),
         "gemm_TOPS": round(ops / (kern_ms / 1e3) / 1e12, 1),
         "gemm_frac_int8_peak": round(ops / (kern_ms / 1e3) / 1e12 / INT8_PEAK_TOPS, 4),
     }
+    if wtype in (13, 14):  # the kernel runs on the f16 matrix cores
+        out["gemm_frac_f16_peak"] = round(ops / (kern_ms / 1e3) / 1e12 / F16_PEAK_TFLOPS, 4)
     wl.free()
     return out
 
@@ -239,6 +243,7 @@ PREFILL_CASES = {  # name: (weight type, n, k, m, seed)
     "c2_prefill_q6k_256x2048_m512": (14, 256, 2048, 512, 11),    # TinyLlama attn_v
     "prefill_q8_0_4096x4096_m512": (8, 4096, 4096, 512, 12),     # a Q8_0 GGUF's projection
     "prefill_q4_0_4096x4096_m512": (2, 4096, 4096, 512, 15),     # Q4_0: the Q8_0 GEMM on the expanded copy
+    "prefill_q5k_5632x2048_m512": (13, 5632, 2048, 512, 16),     # a Q5_K_M file's TinyLlama ffn_up
 }
 
 

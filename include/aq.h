@@ -19,11 +19,10 @@
  *    never aborts the process; aq_last_error() gives the calling thread's
  *    last message.
  *  - Weight type ids are GGUF/GGML dtype ids (Q4_0 = 2, Q8_0 = 8, Q4_K = 12,
- *    Q5_K = 13, Q6_K = 14).  Q5_K runs the batch-1..8 matvec at any m
- *    (batches of more than 8 rows in passes of 8); the prefill GEMMs take
- *    Q4_K, Q6_K, Q8_0 and Q4_0 (the last on an int8 copy that the upload
- *    expands into the Q8_0 layout, 34 bytes per 32 weights beside its
- *    18-byte decode tiles).
+ *    Q5_K = 13, Q6_K = 14).  Every type runs the batch-1..8 matvec and, for
+ *    m > 8, a prefill GEMM (Q4_0 on an int8 copy that the upload expands
+ *    into the Q8_0 layout, 34 bytes per 32 weights beside its 18-byte
+ *    decode tiles).
  *  - A weight is n rows (output features) by k columns (input features),
  *    row-major blocks, exactly candle's QTensor storage of shape (n, k).
  *  - Host-pointer entry points are synchronous at return.  Device-pointer

@@ -223,12 +223,12 @@ def test_single_row_weight(ctx):
     check_matmul(ctx, W, x)
 
 
-# ------------------------------------------------------------ Q5_K (matvec at any m)
+# ------------------------------------ Q5_K (matvec m <= 8, f16 MFMA GEMM m > 8)
 @pytest.mark.parametrize("n,k,m", [(5632, 2048, 1), (2048, 5632, 1), (14336, 4096, 1), (4096, 14336, 8),
                                    (2048, 2048, 40)])
 def test_q5k_matvec(ctx, n, k, m):
     """TinyLlama / Llama-3 FFN shapes of a Q5_K_M file, batch 1 and 8, and a
-    40-row prefill (five passes of 8 rows): block sums bit-exact."""
+    40-row prefill (the GEMM): block sums bit-exact."""
     W = S.make_weight(S.TYPE_Q5_K, n, k, seed=n + k + 5)
     x = S.make_activation(m, k, seed=m + k + 5)
     check_matmul(ctx, W, x, cond=(m <= 8 and k < 14336))
@@ -245,6 +245,40 @@ def test_q5k_extreme_values(ctx):
     W.mn[:] = 63
     W.blocks = S.pack_q5k(W.d, W.dmin, W.sc, W.mn, W.q)
     x = np.repeat(rng.standard_normal((m, k // 256)).astype(np.float32), 256, axis=1)
+    check_matmul(ctx, W, x, cond=False)
+
+
+@pytest.mark.parametrize("n,k,m", [(2048, 2048, 512), (5632, 2048, 64), (2048, 5632, 33), (32000, 2048, 16)])
+def test_prefill_gemm_q5k(ctx, n, k, m):
+    """TinyLlama attn_q / ffn_up / ffn_down shapes of a Q5_K_M file at
+    prefill (k-splits of two super-blocks at 512 rows) and the lm_head shape
+    at 16 rows: integer block sums S and Smin bit-exact."""
+    W = S.make_weight(S.TYPE_Q5_K, n, k, seed=n + k + 13)
+    x = S.make_activation(m, k, seed=m + k + 13)
+    check_matmul(ctx, W, x, cond=(k < 14336))
+
+
+@pytest.mark.parametrize("m,n,k", [(9, 100, 256), (63, 129, 768), (65, 300, 512), (130, 257, 1024), (200, 64, 2048)])
+def test_prefill_gemm_q5k_ragged_tiles(ctx, m, n, k):
+    W = S.make_weight(S.TYPE_Q5_K, n, k, seed=m + n + 13)
+    x = S.make_activation(m, k, seed=m * n + 13)
+    check_matmul(ctx, W, x)
+
+
+def test_prefill_gemm_q5k_extreme_values(ctx):
+    """Largest Q5_K . Q8_K sums on the GEMM: every quant 31, scales and mins
+    63, activation blocks of equal values (quants +-128 / 127): each
+    64-element f32 MFMA chain reaches 64 * 1953 * 128 < 2^24 and S four times
+    that; Smin 16 * 2048 * 63."""
+    n, k, m = 64, 1024, 16
+    rng = np.random.default_rng(26)
+    W = S.make_weight(S.TYPE_Q5_K, n, k, seed=26)
+    W.q[:] = 31
+    W.sc[:] = 63
+    W.mn[:] = 63
+    W.blocks = S.pack_q5k(W.d, W.dmin, W.sc, W.mn, W.q)
+    x = np.repeat(np.abs(rng.standard_normal((m, k // 256))).astype(np.float32) + 0.5, 256, axis=1)
+    x[1::2] = -x[1::2]
     check_matmul(ctx, W, x, cond=False)
 
 
@@ -332,8 +366,11 @@ def test_prefill_gemm_q8_0_subnormal_and_zero_scales(ctx):
     check_matmul(ctx, W, x, cond=False)
 
 
+@pytest.mark.parametrize("m", [3, 20])
 @pytest.mark.parametrize("wtype", [S.TYPE_Q4_K, S.TYPE_Q5_K, S.TYPE_Q6_K, S.TYPE_Q8_0, S.TYPE_Q4_0])
-def test_subnormal_and_zero_scales(ctx, wtype):
+def test_subnormal_and_zero_scales(ctx, wtype, m):
+    """f16 subnormal and zero d / dmin through the matvec (3 rows) and the
+    GEMMs (20 rows)."""
     W = S.make_weight(wtype, 128, 1024, seed=8)
     rng = np.random.default_rng(8)
     d = (rng.integers(1, 1024, size=W.d.shape).astype(np.uint16)).view(np.float16)  # f16 subnormals
@@ -349,7 +386,7 @@ def test_subnormal_and_zero_scales(ctx, wtype):
     else:
         W.blocks = S.pack_q8_0(d, W.q)
     W.d = d
-    x = S.make_activation(3, 1024, seed=9)
+    x = S.make_activation(m, 1024, seed=9)
     check_matmul(ctx, W, x, cond=False)
 
 
@@ -385,7 +422,7 @@ def test_higher_rank_input_and_determinism(ctx):
 
 
 @pytest.mark.parametrize("wtype,m", [(S.TYPE_Q4_K, 4), (S.TYPE_Q6_K, 1), (S.TYPE_Q8_0, 8), (S.TYPE_Q4_K, 40),
-                                     (S.TYPE_Q5_K, 3), (S.TYPE_Q4_0, 2)])
+                                     (S.TYPE_Q5_K, 3), (S.TYPE_Q5_K, 24), (S.TYPE_Q4_0, 2)])
 def test_device_pointer_entry_points(ctx, wtype, m):
     from arm_ai_amd import hip
 
