@@ -183,6 +183,7 @@ int run_matmul(aq_ctx *ctx, const aq_qweight *w, const float *d_x, int64_t m, fl
     hipError_t e;
     if (use_gemm(w, m)) {
         ActPlanes a = act_planes(act, m, w->k);
+        a.q16 = gemm_q16_plane(w->glayout.type, m, w->n, w->k, ws);  // f16-MFMA GEMMs: quants as f16 too
         e = act_q80(w->type) ? launch_quantize_q8_0(d_x, m, w->k, a, ctx->stream)
                                     : launch_quantize_q8k(d_x, m, w->k, a, ctx->stream);
         if (e != hipSuccess) return fail(AQ_ERR_HIP, "activation quantizer: %s", hipGetErrorString(e));

@@ -79,6 +79,7 @@ struct ActPlanes {
     uint16_t *d16;
     int16_t *bsums;
     uint16_t *bsum16;
+    uint16_t *q16 = nullptr;  // optional: the qs as f16 [m][k], written by the Q8_K quantizer when set
 };
 
 inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
@@ -156,6 +157,12 @@ size_t gemm_workspace_bytes(int type, int64_t m, int64_t n, int64_t k);
 // gemm_workspace_bytes; its workspace holds the f16 copy of the activation
 // quants and the split-K partials.
 size_t gemm6_workspace_bytes(int64_t m, int64_t n, int64_t k);
+// Where in ws the GEMM for this weight type reads f16 activation quants, or
+// null if it reads none (or converts them per launch chunk).  A Q8_K
+// quantizer given this plane as ActPlanes::q16 writes them there, and the
+// GEMM then skips its own conversion launch.
+uint16_t *gemm_q16_plane(int type, int64_t m, int64_t n, int64_t k, void *ws);
+uint16_t *gemm6_q16_plane(int64_t m, int64_t n, int64_t k, void *ws);
 hipError_t launch_gemm6(const WLayout &w, int64_t n, int64_t k, const ActPlanes &x, int64_t m, float *y, int32_t *S,
                         int32_t *Smin, void *ws, size_t ws_bytes, hipStream_t s);
 // The Q8_0 GEMM on int8 MFMA (k_gemm8.hip), reached through launch_gemm /

@@ -399,6 +399,10 @@ size_t gemm_workspace_bytes(int type, int64_t m, int64_t n, int64_t k) {
     return ws;
 }
 
+uint16_t *gemm_q16_plane(int type, int64_t m, int64_t n, int64_t k, void *ws) {
+    return type == TYPE_Q6_K || type == TYPE_Q5_K ? gemm6_q16_plane(m, n, k, ws) : nullptr;
+}
+
 hipError_t launch_gemm(const WLayout &w, int64_t n, int64_t k, const ActPlanes &x, int64_t m, float *y, int32_t *S,
                        int32_t *Smin, void *ws, size_t ws_bytes, hipStream_t s) {
     if (w.type == TYPE_Q6_K || w.type == TYPE_Q5_K) return launch_gemm6(w, n, k, x, m, y, S, Smin, ws, ws_bytes, s);

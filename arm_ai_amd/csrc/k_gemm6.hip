@@ -27,7 +27,8 @@
 // Tiling.  A workgroup (4 wavefronts, two workgroups per CU) owns a 64 (m) x
 // 128 (n) output tile; wavefront w owns columns 32w..32w+31 and both 32-row
 // MFMA tiles, so each weight operand it builds feeds two MFMAs.  The f16
-// activation rows of the tile (written by qs_to_f16_kernel) are copied global
+// activation rows of the tile (written by the Q8_K quantizer when it runs in
+// the same call, else by qs_to_f16_kernel) are copied global
 // -> LDS (buffer loads into LDS) one super-block ahead, two stages, 16-byte
 // chunks XOR-swizzled by row; each lane loads its own column's ql / qh / scale
 // bytes straight into registers, also one super-block ahead.  Work items
@@ -424,7 +425,10 @@ struct Gemm6Plan {
 };
 
 // 64 x 128 tiles, two workgroups per CU; K split while there are fewer items
-// than workgroup slots, each split keeping at least two super-blocks.
+// than workgroup slots, each split keeping at least two super-blocks.  (The
+// kernel is latency-bound at one workgroup per CU: a split that leaves the
+// same number of rounds still pays for itself, e.g. 352 tiles x 8
+// super-blocks in 30 us with two splits plus a 10 us reduce, 44 us without.)
 Gemm6Plan gemm6_plan(int64_t m, int64_t n, int64_t k) {
     Gemm6Plan g;
     const int ng = (int)(k / QK_K);
@@ -458,6 +462,11 @@ size_t gemm6_workspace_bytes(int64_t m, int64_t n, int64_t k) {
     return ws;
 }
 
+uint16_t *gemm6_q16_plane(int64_t m, int64_t n, int64_t k, void *ws) {
+    if (!ws || m <= 0 || n <= 0 || k <= 0 || k % QK_K || m > gemm6_chunk_rows(k)) return nullptr;  // one launch only
+    return (uint16_t *)((uint8_t *)ws + align_up(gemm6_plan(m, n, k).part, 256));
+}
+
 hipError_t launch_gemm6(const WLayout &w, int64_t n, int64_t k, const ActPlanes &x, int64_t m, float *y, int32_t *S,
                         int32_t *Smin, void *ws, size_t ws_bytes, hipStream_t s) {
     if (w.type != TYPE_Q6_K && w.type != TYPE_Q5_K) return hipErrorNotSupported;
@@ -476,10 +485,12 @@ hipError_t launch_gemm6(const WLayout &w, int64_t n, int64_t k, const ActPlanes 
         if (g.tiles > GEMM_MAX_TILES) return hipErrorNotSupported;
         if (!ws || ws_bytes < g.ws) return hipErrorInvalidValue;
         uint16_t *x16 = (uint16_t *)((uint8_t *)ws + align_up(g.part, 256));
-        const int64_t n4 = mm * k / 4;
-        qs_to_f16_kernel<<<(unsigned)((n4 + 255) / 256), 256, 0, s>>>(x.qs + r0 * k, n4, x16);
-        hipError_t e = hipGetLastError();
-        if (e != hipSuccess) return e;
+        hipError_t e;
+        if (!(r0 == 0 && mm == m && x.q16 == x16)) {  // not already written there by the quantizer
+            const int64_t n4 = mm * k / 4;
+            qs_to_f16_kernel<<<(unsigned)((n4 + 255) / 256), 256, 0, s>>>(x.qs + r0 * k, n4, x16);
+            if ((e = hipGetLastError()) != hipSuccess) return e;
+        }
         Gemm6Params p;
         p.w = w.slab;
         p.wd = w.d;

@@ -31,6 +31,13 @@ __global__ __launch_bounds__(256) void quantize_q8k_kernel(const float *__restri
     float d;
     const uint32_t packed = q8k_block_wave(v, lane, &bsum, &d);
     *(uint32_t *)(a.qs + row * k + sb * QK_K + 4 * lane) = packed;
+    if (a.q16) {  // uniform: the f16 copy for the f16-MFMA GEMMs
+        uint32_t o[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            o[j] = __builtin_bit_cast(uint16_t, (_Float16)(int)(int8_t)((packed >> (8 * j)) & 0xffu));
+        *(uint2 *)(a.q16 + row * k + sb * QK_K + 4 * lane) = make_uint2(o[0] | (o[1] << 16), o[2] | (o[3] << 16));
+    }
     if ((lane & 3) == 0) {
         a.bsums[row * (k / 16) + sb * 16 + (lane >> 2)] = (int16_t)bsum;
         a.bsum16[row * (k / 16) + sb * 16 + (lane >> 2)] = __builtin_bit_cast(uint16_t, (_Float16)(float)bsum);
