@@ -48,8 +48,10 @@ _SCALAR = {T_U8: "<B", T_I8: "<b", T_U16: "<H", T_I16: "<h", T_U32: "<I", T_I32:
 # ggml tensor types read here: (elements per block, bytes per block)
 GGML_F32, GGML_F16 = 0, 1
 TYPE_SIZES = {GGML_F32: (1, 4), GGML_F16: (1, 2), synth.TYPE_Q8_0: (32, 34), synth.TYPE_Q4_0: (32, 18),
-              synth.TYPE_Q4_K: (256, 144), synth.TYPE_Q5_K: (256, 176), synth.TYPE_Q6_K: (256, 210)}
-QUANT_TYPES = (synth.TYPE_Q4_K, synth.TYPE_Q5_K, synth.TYPE_Q6_K, synth.TYPE_Q8_0, synth.TYPE_Q4_0)
+              synth.TYPE_Q4_K: (256, 144), synth.TYPE_Q5_K: (256, 176), synth.TYPE_Q6_K: (256, 210),
+              synth.TYPE_Q2_K: (256, 84), synth.TYPE_Q3_K: (256, 110)}
+QUANT_TYPES = (synth.TYPE_Q4_K, synth.TYPE_Q5_K, synth.TYPE_Q6_K, synth.TYPE_Q8_0, synth.TYPE_Q4_0, synth.TYPE_Q2_K,
+               synth.TYPE_Q3_K)
 
 
 class GGUFError(ValueError):
@@ -177,7 +179,7 @@ class GGUFFile:
         """A 2-D quantized weight as candle's QTensor (n rows, k columns)."""
         ti = self.tensor(name)
         if ti.type not in QUANT_TYPES or len(ti.dims) != 2:
-            raise GGUFError(f"tensor {name}: a 2-D Q4_K / Q5_K / Q6_K / Q8_0 / Q4_0 weight is needed, got type {ti.type} "
+            raise GGUFError(f"tensor {name}: a 2-D Q2_K / Q3_K / Q4_K / Q5_K / Q6_K / Q8_0 / Q4_0 weight is needed, got type {ti.type} "
                             f"with dims {ti.dims}")
         k, n = ti.dims
         return QTensor(GgmlDType(ti.type), (n, k), self.raw(name))
@@ -244,6 +246,30 @@ def dequantize(type_: int, raw: np.ndarray, n_elements: int) -> np.ndarray:
         d1 = d[:, None] * sc.astype(np.float32)
         m1 = dmin[:, None] * mn.astype(np.float32)
         return (d1[:, :, None] * q - m1[:, :, None]).reshape(-1)[:n_elements]
+    if type_ == synth.TYPE_Q2_K:
+        b = raw.reshape(-1, 84)
+        d, dmin = _f16(b[:, 80:82]), _f16(b[:, 82:84])
+        sc = (b[:, 0:16] & 0xF).astype(np.float32)
+        mn = (b[:, 0:16] >> 4).astype(np.float32)
+        qs = b[:, 16:80].reshape(-1, 2, 1, 32)
+        q = ((qs >> (2 * np.arange(4)[None, None, :, None])) & 3).reshape(-1, 16, 16).astype(np.float32)
+        return ((d[:, None] * sc)[:, :, None] * q - (dmin[:, None] * mn)[:, :, None]).reshape(-1)[:n_elements]
+    if type_ == synth.TYPE_Q3_K:
+        b = raw.reshape(-1, 110)
+        hm = b[:, 0:32].astype(np.int32)
+        qs = b[:, 32:96].reshape(-1, 2, 1, 32).astype(np.int32)
+        sh = np.arange(4)[None, None, :, None]
+        q2 = (qs >> (2 * sh)) & 3                                          # [blk][hf][j][l]
+        hb = (hm[:, None, None, :] >> (4 * np.arange(2)[None, :, None, None] + sh)) & 1
+        q = (q2 - 4 * (1 - hb)).reshape(-1, 16, 16).astype(np.float32)
+        a = b[:, 96:108].astype(np.int32)
+        s6 = np.empty((b.shape[0], 16), np.int32)
+        s6[:, 0:4] = (a[:, 0:4] & 15) | ((a[:, 8:12] & 3) << 4)
+        s6[:, 4:8] = (a[:, 4:8] & 15) | (((a[:, 8:12] >> 2) & 3) << 4)
+        s6[:, 8:12] = (a[:, 0:4] >> 4) | (((a[:, 8:12] >> 4) & 3) << 4)
+        s6[:, 12:16] = (a[:, 4:8] >> 4) | (((a[:, 8:12] >> 6) & 3) << 4)
+        d = _f16(b[:, 108:110])
+        return ((d[:, None] * (s6 - 32).astype(np.float32))[:, :, None] * q).reshape(-1)[:n_elements]
     if type_ == synth.TYPE_Q6_K:
         b = raw.reshape(-1, 210)
         ql = b[:, 0:128].reshape(-1, 2, 64)

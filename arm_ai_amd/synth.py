@@ -12,11 +12,16 @@ configurations prescribe:
   ~ U[0, 63] (value q - 32).
 * Q8_0: d = f16(|N(0, 0.02)|); int8 quants ~ U[-127, 127].
 * Q4_0: d = f16(|N(0, 0.02)|); 4-bit quants ~ U[0, 15] (value q - 8).
+* Q2_K: d, dmin = f16(|N(0, 0.02)|); 4-bit scales and mins ~ U[0, 15];
+  2-bit quants ~ U[0, 3].
+* Q3_K: d = f16(|N(0, 0.02)|); 6-bit scales ~ U[0, 63] (value s - 32);
+  3-bit quants ~ U[-4, 3].
 * activations: f32 N(0, 1).
 
 Generators draw element-level arrays from ``numpy.random.default_rng(seed)``
 (PCG64) and pack them into GGUF block bytes with the GGUF layout (block
-formats: Q4_K 144 B, Q5_K 176 B, Q6_K 210 B, Q8_0 34 B, Q4_0 18 B).  The element arrays are kept so
+formats: Q4_K 144 B, Q5_K 176 B, Q6_K 210 B, Q8_0 34 B, Q4_0 18 B, Q2_K 84 B,
+Q3_K 110 B).  The element arrays are kept so
 tests can compute exact answers without going through any unpacking code.
 f32 -> f16 uses numpy's IEEE round-to-nearest-even conversion, the same
 rounding the reference's `half` crate uses (shape_ops.rs:1492-1503).
@@ -31,16 +36,19 @@ QK_K = 256
 QK8_0 = 32
 TYPE_Q4_0 = 2
 TYPE_Q8_0 = 8
+TYPE_Q2_K = 10
+TYPE_Q3_K = 11
 TYPE_Q4_K = 12
 TYPE_Q5_K = 13
 TYPE_Q6_K = 14
 TYPE_Q8_K = 15
 
-BLOCK_BYTES = {TYPE_Q4_K: 144, TYPE_Q5_K: 176, TYPE_Q6_K: 210, TYPE_Q8_0: 34, TYPE_Q4_0: 18, TYPE_Q8_K: 292}
+BLOCK_BYTES = {TYPE_Q4_K: 144, TYPE_Q5_K: 176, TYPE_Q6_K: 210, TYPE_Q8_0: 34, TYPE_Q4_0: 18, TYPE_Q2_K: 84,
+               TYPE_Q3_K: 110, TYPE_Q8_K: 292}
 BLOCK_ELEMS = {TYPE_Q4_K: QK_K, TYPE_Q5_K: QK_K, TYPE_Q6_K: QK_K, TYPE_Q8_0: QK8_0, TYPE_Q4_0: QK8_0,
-               TYPE_Q8_K: QK_K}
+               TYPE_Q2_K: QK_K, TYPE_Q3_K: QK_K, TYPE_Q8_K: QK_K}
 TYPE_NAMES = {TYPE_Q4_K: "q4_k", TYPE_Q5_K: "q5_k", TYPE_Q6_K: "q6_k", TYPE_Q8_0: "q8_0", TYPE_Q4_0: "q4_0",
-              TYPE_Q8_K: "q8_k"}
+              TYPE_Q2_K: "q2_k", TYPE_Q3_K: "q3_k", TYPE_Q8_K: "q8_k"}
 
 
 @dataclass
@@ -52,11 +60,11 @@ class QWeight:
     k: int
     blocks: np.ndarray  # uint8 [n, nb * block_bytes], GGUF AoS layout
     d: np.ndarray  # float16 [n, nb]
-    dmin: np.ndarray | None  # float16 [n, nb] (Q4_K, Q5_K)
-    sc: np.ndarray | None  # Q4_K / Q5_K uint8 [n, nb, 8]; Q6_K int8 [n, nb, 16]
-    mn: np.ndarray | None  # Q4_K / Q5_K uint8 [n, nb, 8]
+    dmin: np.ndarray | None  # float16 [n, nb] (Q2_K, Q4_K, Q5_K)
+    sc: np.ndarray | None  # Q4_K / Q5_K uint8 [n, nb, 8]; Q2_K uint8 [n, nb, 16]; Q3_K (value), Q6_K int8 [n, nb, 16]
+    mn: np.ndarray | None  # Q4_K / Q5_K uint8 [n, nb, 8]; Q2_K uint8 [n, nb, 16]
     q: np.ndarray  # Q4_K uint8 [n,nb,256] in [0,15]; Q5_K in [0,31]; Q6_K int8 in [-32,31]; Q8_0 int8 [n,nb,32];
-    #               Q4_0 uint8 [n,nb,32] in [0,15] (value q - 8)
+    #               Q4_0 uint8 [n,nb,32] in [0,15] (value q - 8); Q2_K uint8 in [0,3]; Q3_K int8 in [-4,3]
 
     @property
     def nbytes(self) -> int:
@@ -69,7 +77,11 @@ class QWeight:
             sc = np.repeat(self.sc.astype(np.float64), 32, axis=-1)
             mn = np.repeat(self.mn.astype(np.float64), 32, axis=-1)
             v = d * sc * self.q.astype(np.float64) - self.dmin.astype(np.float64)[..., None] * mn
-        elif self.type == TYPE_Q6_K:
+        elif self.type == TYPE_Q2_K:
+            sc = np.repeat(self.sc.astype(np.float64), 16, axis=-1)
+            mn = np.repeat(self.mn.astype(np.float64), 16, axis=-1)
+            v = d * sc * self.q.astype(np.float64) - self.dmin.astype(np.float64)[..., None] * mn
+        elif self.type in (TYPE_Q3_K, TYPE_Q6_K):
             sc = np.repeat(self.sc.astype(np.float64), 16, axis=-1)
             v = d * sc * self.q.astype(np.float64)
         elif self.type == TYPE_Q4_0:
@@ -148,6 +160,52 @@ def pack_q6k(d, sc, q) -> np.ndarray:
     return out.reshape(n, nb * 210)
 
 
+def pack_q2k(d, dmin, sc, mn, q) -> np.ndarray:
+    """Pack Q2_K element arrays (sc, mn in [0, 15] per 16-element group, q in
+    [0, 3]) into 84-byte blocks: scales[g] = sc[g] | mn[g] << 4 @0,
+    qs @16 with qs[32hf + l] = sum_j q[128hf + 32j + l] << 2j, d f16 @80,
+    dmin f16 @82."""
+    n, nb = d.shape
+    out = np.empty((n, nb, 84), dtype=np.uint8)
+    out[..., 0:16] = (sc.astype(np.uint8) & 15) | ((mn.astype(np.uint8) & 15) << 4)
+    qq = q.astype(np.uint8).reshape(n, nb, 2, 4, 32)  # [hf][j][l]
+    qs = np.zeros((n, nb, 2, 32), dtype=np.uint8)
+    for j in range(4):
+        qs |= (qq[..., j, :] & 3) << (2 * j)
+    out[..., 16:80] = qs.reshape(n, nb, 64)
+    out[..., 80:82] = d.astype(np.float16).view(np.uint8).reshape(n, nb, 2)
+    out[..., 82:84] = dmin.astype(np.float16).view(np.uint8).reshape(n, nb, 2)
+    return out.reshape(n, nb * 84)
+
+
+def pack_q3k(d, sc, q) -> np.ndarray:
+    """Pack Q3_K element arrays (sc in [-32, 31] per 16-element group, q in
+    [-4, 3]) into 110-byte blocks.  With u = q + 4: hmask @0, bit 4hf + j of
+    hmask[l] = u[128hf + 32j + l] >> 2; qs @32, qs[32hf + l] = sum_j
+    (u[128hf + 32j + l] & 3) << 2j; the 6-bit s = sc + 32 @96: byte i < 4 =
+    s[i] & 15 | (s[8+i] & 15) << 4, byte 4 + i = s[4+i] & 15 | (s[12+i] & 15)
+    << 4, byte 8 + i = s[i] >> 4 | s[4+i] >> 4 << 2 | s[8+i] >> 4 << 4 |
+    s[12+i] >> 4 << 6; d f16 @108."""
+    n, nb = d.shape
+    out = np.empty((n, nb, 110), dtype=np.uint8)
+    u = (q.astype(np.int16) + 4).astype(np.uint8).reshape(n, nb, 2, 4, 32)  # [hf][j][l]
+    hm = np.zeros((n, nb, 32), dtype=np.uint8)
+    qs = np.zeros((n, nb, 2, 32), dtype=np.uint8)
+    for hf in range(2):
+        for j in range(4):
+            hm |= (u[..., hf, j, :] >> 2) << (4 * hf + j)
+            qs[..., hf, :] |= (u[..., hf, j, :] & 3) << (2 * j)
+    out[..., 0:32] = hm
+    out[..., 32:96] = qs.reshape(n, nb, 64)
+    s6 = (sc.astype(np.int16) + 32).astype(np.uint8)
+    b = out[..., 96:108]
+    b[..., 0:4] = (s6[..., 0:4] & 15) | ((s6[..., 8:12] & 15) << 4)
+    b[..., 4:8] = (s6[..., 4:8] & 15) | ((s6[..., 12:16] & 15) << 4)
+    b[..., 8:12] = (s6[..., 0:4] >> 4) | ((s6[..., 4:8] >> 4) << 2) | ((s6[..., 8:12] >> 4) << 4) | ((s6[..., 12:16] >> 4) << 6)
+    out[..., 108:110] = d.astype(np.float16).view(np.uint8).reshape(n, nb, 2)
+    return out.reshape(n, nb * 110)
+
+
 def pack_q8_0(d, q) -> np.ndarray:
     n, nb = d.shape
     out = np.empty((n, nb, 34), dtype=np.uint8)
@@ -202,6 +260,18 @@ def make_weight(type_: int, n: int, k: int, seed: int = 0, rng: np.random.Genera
         d = _half_abs_normal(rng, (n, nb))
         q = rng.integers(0, 16, size=(n, nb, 32), dtype=np.uint8)
         return QWeight(type_, n, k, pack_q4_0(d, q), d, None, None, None, q)
+    if type_ == TYPE_Q2_K:
+        d = _half_abs_normal(rng, (n, nb))
+        dmin = _half_abs_normal(rng, (n, nb))
+        sc = rng.integers(0, 16, size=(n, nb, 16), dtype=np.uint8)
+        mn = rng.integers(0, 16, size=(n, nb, 16), dtype=np.uint8)
+        q = rng.integers(0, 4, size=(n, nb, 256), dtype=np.uint8)
+        return QWeight(type_, n, k, pack_q2k(d, dmin, sc, mn, q), d, dmin, sc, mn, q)
+    if type_ == TYPE_Q3_K:
+        d = _half_abs_normal(rng, (n, nb))
+        sc = rng.integers(-32, 32, size=(n, nb, 16), dtype=np.int8)
+        q = rng.integers(-4, 4, size=(n, nb, 256), dtype=np.int8)
+        return QWeight(type_, n, k, pack_q3k(d, sc, q), d, None, sc, None, q)
     raise ValueError(f"unsupported weight type {type_}")
 
 

@@ -28,6 +28,11 @@
  *  - Q5_K (GGML block_q5_K, restated; the reference holds no source for
  *    it): hand-built blocks whose single qh bit or nibble must land on the
  *    element dequantize_row_q5_K assigns it, and the unit-scale case.
+ *  - Q2_K and Q3_K (GGML block_q2_K / block_q3_K, restated; no source for
+ *    them in the reference): hand-built blocks whose single 2-bit quant,
+ *    hmask bit or scale must land on the element and sub-block
+ *    dequantize_row_q2_K / q3_K assign it, closed-form sums of uniform
+ *    blocks, and the f64 dequantize-then-dot of the generator's arrays.
  *  - the f32 combine order (candle vec_dot_unopt) is pinned only by the
  *    candle source, which is not in this image: "parity unpinned" for the
  *    exact f32 rounding sequence; the value is pinned to f64 truth.
@@ -126,6 +131,8 @@ static inline int8_t sat_i8(float v) {
 
 size_t orc_type_block_bytes(int type) {
     switch (type) {
+    case ORC_Q2_K: return ORC_Q2K_BYTES;
+    case ORC_Q3_K: return ORC_Q3K_BYTES;
     case ORC_Q4_K: return ORC_Q4K_BYTES;
     case ORC_Q5_K: return ORC_Q5K_BYTES;
     case ORC_Q6_K: return ORC_Q6K_BYTES;
@@ -138,6 +145,8 @@ size_t orc_type_block_bytes(int type) {
 
 int64_t orc_type_block_elems(int type) {
     switch (type) {
+    case ORC_Q2_K:
+    case ORC_Q3_K:
     case ORC_Q4_K:
     case ORC_Q5_K:
     case ORC_Q6_K:
@@ -280,6 +289,46 @@ static void q6k_unpack(const uint8_t *ql, const uint8_t *qh, int8_t aux8[256]) {
     }
 }
 
+/* Q2_K (GGML block_q2_K: scales[16] @0, qs[64] @16, f16 d @80, f16 dmin
+ * @82; candle BlockQ2K).  For half hf < 2, shift j < 4, l < 32:
+ *   element 128hf + 32j + l = (qs[32hf + l] >> 2j) & 3,
+ * in 16-element group 8hf + 2j + l/16, whose scales byte holds the scale
+ * (low nibble) and the min (high nibble). */
+static void q2k_unpack(const uint8_t *qs, int8_t aux8[256]) {
+    for (int hf = 0; hf < 2; hf++)
+        for (int j = 0; j < 4; j++)
+            for (int l = 0; l < 32; l++) aux8[128 * hf + 32 * j + l] = (int8_t)((qs[32 * hf + l] >> (2 * j)) & 3);
+}
+
+/* Q3_K (GGML block_q3_K: hmask[32] @0, qs[64] @32, scales[12] @96, f16 d
+ * @108; candle BlockQ3K).  For half hf < 2, shift j < 4, l < 32:
+ *   element 128hf + 32j + l = ((qs[32hf + l] >> 2j) & 3) - (hmask[l] bit (4hf + j) ? 0 : 4),
+ * 16-element group g = e/16 with the 6-bit scale of candle's auxs form
+ * (low nibbles of bytes 0..7, then their high nibbles, each with two bits
+ * of bytes 8..11 on top), used as scale - 32. */
+static void q3k_unpack(const uint8_t *hm, const uint8_t *qs, int8_t aux8[256]) {
+    for (int hf = 0; hf < 2; hf++)
+        for (int j = 0; j < 4; j++)
+            for (int l = 0; l < 32; l++) {
+                const int q = (qs[32 * hf + l] >> (2 * j)) & 3;
+                const int h = (hm[l] >> (4 * hf + j)) & 1;
+                aux8[128 * hf + 32 * j + l] = (int8_t)(q - (h ? 0 : 4));
+            }
+}
+
+static void q3k_scales(const uint8_t *sc12, int8_t scales[16]) {
+    const uint32_t KMASK1 = 0x03030303u, KMASK2 = 0x0f0f0f0fu;
+    uint32_t a[4];
+    a[0] = rd_u32(sc12);
+    a[1] = rd_u32(sc12 + 4);
+    const uint32_t tmp = rd_u32(sc12 + 8);
+    a[2] = ((a[0] >> 4) & KMASK2) | (((tmp >> 4) & KMASK1) << 4);
+    a[3] = ((a[1] >> 4) & KMASK2) | (((tmp >> 6) & KMASK1) << 4);
+    a[0] = (a[0] & KMASK2) | ((tmp & KMASK1) << 4);
+    a[1] = (a[1] & KMASK2) | (((tmp >> 2) & KMASK1) << 4);
+    for (int i = 0; i < 16; i++) scales[i] = (int8_t)((int)((a[i / 4] >> (8 * (i % 4))) & 0xffu) - 32);
+}
+
 /* --------------------------------------------------------- vec dots */
 
 /* BlockQ4K::vec_dot_unopt (vec_dot_q4k_q8k), candle's generic order:
@@ -328,6 +377,63 @@ static float q45k_vec_dot(int five, int64_t k, const uint8_t *w, const uint8_t *
 }
 
 float orc_vec_dot_q4k_q8k(int64_t k, const uint8_t *w, const uint8_t *xq) { return q45k_vec_dot(0, k, w, xq); }
+
+/* BlockQ2K::vec_dot_unopt (vec_dot_q2k_q8k): per block
+ * summs = sum_g bsums[g] * (scales[g] >> 4), isum = sum_g (scales[g] & 15) *
+ * sum_{e in g} q8 * q2 (i32), sumf += (d_x * f16(d_w)) * isum - (d_x *
+ * f16(dmin_w)) * summs. */
+float orc_vec_dot_q2k_q8k(int64_t k, const uint8_t *w, const uint8_t *xq) {
+    int64_t nb = k / ORC_QK_K;
+    int8_t aux8[256];
+    float sumf = 0.0f;
+    for (int64_t b = 0; b < nb; b++) {
+        const uint8_t *x = w + b * ORC_Q2K_BYTES;
+        const uint8_t *y = xq + b * ORC_Q8K_BYTES;
+        const int8_t *q8 = (const int8_t *)(y + 4);
+        int32_t summs = 0, isum = 0;
+        for (int g = 0; g < 16; g++) summs += (int32_t)rd_i16(y + 260 + 2 * g) * (int32_t)(x[g] >> 4);
+        q2k_unpack(x + 16, aux8);
+        for (int g = 0; g < 16; g++) {
+            int32_t isuml = 0;
+            for (int e = 16 * g; e < 16 * g + 16; e++) isuml += (int32_t)q8[e] * aux8[e];
+            isum += (int32_t)(x[g] & 0xF) * isuml;
+        }
+        const float yd = rd_f32(y);
+        const float dall = yd * orc_f16_to_f32(rd_u16(x + 80));
+        const float dmin = yd * orc_f16_to_f32(rd_u16(x + 82));
+        sumf += dall * (float)isum - dmin * (float)summs;
+    }
+    return sumf;
+}
+
+/* BlockQ3K::vec_dot_unopt (vec_dot_q3k_q8k): the 8-lane order of Q4_K's,
+ * aux32[l] += (scale_g - 32) * (q8 * q3) per half group of 8, sums[l] +=
+ * (f16(d_w) * d_x) * aux32[l]; return sum(sums). */
+float orc_vec_dot_q3k_q8k(int64_t k, const uint8_t *w, const uint8_t *xq) {
+    int64_t nb = k / ORC_QK_K;
+    int8_t aux8[256], sc[16];
+    float sums[8] = {0};
+    for (int64_t b = 0; b < nb; b++) {
+        const uint8_t *x = w + b * ORC_Q3K_BYTES;
+        const uint8_t *y = xq + b * ORC_Q8K_BYTES;
+        const int8_t *q8 = (const int8_t *)(y + 4);
+        int32_t aux32[8] = {0};
+        q3k_unpack(x, x + 32, aux8);
+        q3k_scales(x + 96, sc);
+        for (int g = 0; g < 16; g++)
+            for (int hh = 0; hh < 2; hh++)
+                for (int l = 0; l < 8; l++) {
+                    const int e = 16 * g + 8 * hh + l;
+                    int16_t aux16 = (int16_t)(q8[e] * aux8[e]);
+                    aux32[l] += (int32_t)sc[g] * (int32_t)aux16;
+                }
+        const float d = orc_f16_to_f32(rd_u16(x + 108)) * rd_f32(y);
+        for (int l = 0; l < 8; l++) sums[l] += d * (float)aux32[l];
+    }
+    float t = 0.0f;
+    for (int l = 0; l < 8; l++) t += sums[l];
+    return t;
+}
 
 /* BlockQ5K::vec_dot_unopt (vec_dot_q5k_q8k): the same order as Q4_K's with
  * the 5-bit quants of q5k_unpack (|q8*q5| <= 3968 still fits the i16 aux16). */
@@ -426,6 +532,41 @@ void orc_block_sums(int type, int64_t k, const uint8_t *w, const uint8_t *xq, in
             S[b] = s;
             if (Smin) Smin[b] = sm;
         }
+    } else if (type == ORC_Q2_K) {
+        int64_t nb = k / ORC_QK_K;
+        for (int64_t b = 0; b < nb; b++) {
+            const uint8_t *x = w + b * ORC_Q2K_BYTES;
+            const uint8_t *y = xq + b * ORC_Q8K_BYTES;
+            const int8_t *q8 = (const int8_t *)(y + 4);
+            q2k_unpack(x + 16, aux8);
+            int32_t s = 0, sm = 0;
+            for (int g = 0; g < 16; g++) {
+                int32_t isum = 0;
+                for (int e = 16 * g; e < 16 * g + 16; e++) isum += (int32_t)q8[e] * aux8[e];
+                s += (int32_t)(x[g] & 0xF) * isum;
+                sm += (int32_t)rd_i16(y + 260 + 2 * g) * (int32_t)(x[g] >> 4);
+            }
+            S[b] = s;
+            if (Smin) Smin[b] = sm;
+        }
+    } else if (type == ORC_Q3_K) {
+        int64_t nb = k / ORC_QK_K;
+        int8_t sc[16];
+        for (int64_t b = 0; b < nb; b++) {
+            const uint8_t *x = w + b * ORC_Q3K_BYTES;
+            const uint8_t *y = xq + b * ORC_Q8K_BYTES;
+            const int8_t *q8 = (const int8_t *)(y + 4);
+            q3k_unpack(x, x + 32, aux8);
+            q3k_scales(x + 96, sc);
+            int32_t s = 0;
+            for (int g = 0; g < 16; g++) {
+                int32_t isum = 0;
+                for (int e = 16 * g; e < 16 * g + 16; e++) isum += (int32_t)q8[e] * aux8[e];
+                s += (int32_t)sc[g] * isum;
+            }
+            S[b] = s;
+            if (Smin) Smin[b] = 0;
+        }
     } else if (type == ORC_Q6_K) {
         int64_t nb = k / ORC_QK_K;
         for (int64_t b = 0; b < nb; b++) {
@@ -472,7 +613,7 @@ void orc_block_sums(int type, int64_t k, const uint8_t *w, const uint8_t *xq, in
  * rows in parallel.  Same arithmetic as orc_block_sums. */
 int orc_block_sums_mat(int type, int64_t m, int64_t n, int64_t k, const uint8_t *w, const uint8_t *xq,
                        int32_t *S, int32_t *Smin, int nthreads) {
-    if (type != ORC_Q4_K && type != ORC_Q5_K && type != ORC_Q6_K && type != ORC_Q8_0 && type != ORC_Q4_0) return -2;
+    if (!orc_known_type(type)) return -2;
     int64_t wblk = orc_type_block_elems(type);
     if (k <= 0 || k % wblk != 0 || m < 0 || n < 0) return -3;
     const int64_t nblk = k / wblk;
@@ -491,10 +632,17 @@ int orc_block_sums_mat(int type, int64_t m, int64_t n, int64_t k, const uint8_t 
 
 /* ---------------------------------------------------------- matmul */
 
+int orc_known_type(int type) {
+    return type == ORC_Q2_K || type == ORC_Q3_K || type == ORC_Q4_K || type == ORC_Q5_K || type == ORC_Q6_K ||
+           type == ORC_Q8_0 || type == ORC_Q4_0;
+}
+
 static int act_type_for(int type) { return type == ORC_Q8_0 || type == ORC_Q4_0 ? ORC_Q8_0 : ORC_Q8_K; }
 
 static float vec_dot(int type, int64_t k, const uint8_t *w, const uint8_t *xq) {
     switch (type) {
+    case ORC_Q2_K: return orc_vec_dot_q2k_q8k(k, w, xq);
+    case ORC_Q3_K: return orc_vec_dot_q3k_q8k(k, w, xq);
     case ORC_Q4_K: return orc_vec_dot_q4k_q8k(k, w, xq);
     case ORC_Q5_K: return orc_vec_dot_q5k_q8k(k, w, xq);
     case ORC_Q4_0: return orc_vec_dot_q4_0_q8_0(k, w, xq);
@@ -516,7 +664,7 @@ int orc_max_threads(void) {
  * with_max_len(512); here OpenMP dynamic chunks of 256 columns). */
 int orc_matmul_preq(int type, int64_t m, int64_t k, int64_t n, const uint8_t *xq, float *dst,
                     const uint8_t *w, int nthreads) {
-    if (type != ORC_Q4_K && type != ORC_Q5_K && type != ORC_Q6_K && type != ORC_Q8_0 && type != ORC_Q4_0) return -2;
+    if (!orc_known_type(type)) return -2;
     int64_t wblk = orc_type_block_elems(type);
     if (k <= 0 || k % wblk != 0 || m < 0 || n < 0) return -3;
     size_t row_w = (size_t)(k / wblk) * orc_type_block_bytes(type);
@@ -536,7 +684,7 @@ int orc_matmul_preq(int type, int64_t m, int64_t k, int64_t n, const uint8_t *xq
  * serially with T::VecDotType::from_float, then the column loop. */
 int orc_matmul(int type, int64_t m, int64_t k, int64_t n, const float *lhs, const uint8_t *w,
                float *dst, int nthreads) {
-    if (type != ORC_Q4_K && type != ORC_Q5_K && type != ORC_Q6_K && type != ORC_Q8_0 && type != ORC_Q4_0) return -2;
+    if (!orc_known_type(type)) return -2;
     int64_t wblk = orc_type_block_elems(type);
     if (k <= 0 || k % wblk != 0 || m < 0 || n < 0) return -3;
     int at = act_type_for(type);
@@ -555,7 +703,7 @@ int orc_matmul(int type, int64_t m, int64_t k, int64_t n, const float *lhs, cons
 }
 
 /* GGML dequantisation of one weight row (value = d*sc*q - dmin*m for
- * Q4_K and Q5_K, d*sc*q6 for Q6_K, d*q for Q8_0), f32. */
+ * Q2_K, Q4_K and Q5_K, d*sc*q for Q3_K and Q6_K, d*q for Q8_0), f32. */
 int orc_dequantize_row(int type, const uint8_t *w, int64_t k, float *out) {
     int8_t aux8[256];
     if (type == ORC_Q4_K) {
@@ -581,6 +729,29 @@ int orc_dequantize_row(int type, const uint8_t *w, int64_t k, float *out) {
             float d = orc_f16_to_f32(rd_u16(x)), dmin = orc_f16_to_f32(rd_u16(x + 2));
             for (int e = 0; e < 256; e++)
                 out[b * 256 + e] = d * (float)sc[e / 32] * (float)aux8[e] - dmin * (float)mn[e / 32];
+        }
+        return 0;
+    }
+    if (type == ORC_Q2_K) {
+        if (k % ORC_QK_K) return -3;
+        for (int64_t b = 0; b < k / ORC_QK_K; b++) {
+            const uint8_t *x = w + b * ORC_Q2K_BYTES;
+            q2k_unpack(x + 16, aux8);
+            float d = orc_f16_to_f32(rd_u16(x + 80)), dmin = orc_f16_to_f32(rd_u16(x + 82));
+            for (int e = 0; e < 256; e++)
+                out[b * 256 + e] = d * (float)(x[e / 16] & 0xF) * (float)aux8[e] - dmin * (float)(x[e / 16] >> 4);
+        }
+        return 0;
+    }
+    if (type == ORC_Q3_K) {
+        if (k % ORC_QK_K) return -3;
+        int8_t sc[16];
+        for (int64_t b = 0; b < k / ORC_QK_K; b++) {
+            const uint8_t *x = w + b * ORC_Q3K_BYTES;
+            q3k_unpack(x, x + 32, aux8);
+            q3k_scales(x + 96, sc);
+            float d = orc_f16_to_f32(rd_u16(x + 108));
+            for (int e = 0; e < 256; e++) out[b * 256 + e] = d * (float)(sc[e / 16] * aux8[e]);
         }
         return 0;
     }

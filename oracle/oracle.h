@@ -38,6 +38,8 @@ extern "C" {
 enum {
     ORC_Q4_0 = 2,
     ORC_Q8_0 = 8,
+    ORC_Q2_K = 10,
+    ORC_Q3_K = 11,
     ORC_Q4_K = 12,
     ORC_Q5_K = 13,
     ORC_Q6_K = 14,
@@ -46,6 +48,8 @@ enum {
 
 #define ORC_QK_K 256
 #define ORC_QK8_0 32
+#define ORC_Q2K_BYTES 84
+#define ORC_Q3K_BYTES 110
 #define ORC_Q4K_BYTES 144
 #define ORC_Q5K_BYTES 176
 #define ORC_Q6K_BYTES 210
@@ -61,6 +65,7 @@ void orc_f32_to_f16_n(const float *f, int64_t n, uint16_t *out);
 
 /* Bytes of one block and elements per block for a GGUF type id; 0 if unknown. */
 size_t orc_type_block_bytes(int type);
+int orc_known_type(int type); /* 1 for the weight types below */
 int64_t orc_type_block_elems(int type);
 
 /* Activation quantizers (one row of k floats -> k/blk blocks). Return 0 or -1 (k % blk != 0). */
@@ -68,6 +73,8 @@ int orc_quantize_row_q8k(const float *x, int64_t k, uint8_t *out);
 int orc_quantize_row_q8_0(const float *x, int64_t k, uint8_t *out);
 
 /* vec_dot_unopt: one weight row (k elements, packed) . one quantized activation row. */
+float orc_vec_dot_q2k_q8k(int64_t k, const uint8_t *w, const uint8_t *xq);
+float orc_vec_dot_q3k_q8k(int64_t k, const uint8_t *w, const uint8_t *xq);
 float orc_vec_dot_q4k_q8k(int64_t k, const uint8_t *w, const uint8_t *xq);
 float orc_vec_dot_q5k_q8k(int64_t k, const uint8_t *w, const uint8_t *xq);
 float orc_vec_dot_q6k_q8k(int64_t k, const uint8_t *w, const uint8_t *xq);

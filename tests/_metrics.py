@@ -33,8 +33,9 @@ def abs_weight_magnitude(W) -> np.ndarray:
     """f32 [n, k]: |d*sc*q| + |dmin*m| per element, from the generator's element arrays."""
     d = np.abs(W.d.astype(np.float32))[..., None]
     if W.dmin is not None:
-        sc = np.repeat(W.sc.astype(np.float32), 32, axis=-1)
-        mn = np.repeat(W.mn.astype(np.float32), 32, axis=-1)
+        per = W.k // W.d.shape[1] // W.sc.shape[-1]  # elements per scale: 32 (Q4_K, Q5_K) or 16 (Q2_K)
+        sc = np.repeat(W.sc.astype(np.float32), per, axis=-1)
+        mn = np.repeat(W.mn.astype(np.float32), per, axis=-1)
         v = d * sc * W.q.astype(np.float32) + np.abs(W.dmin.astype(np.float32))[..., None] * mn
     elif W.sc is not None:
         sc = np.repeat(np.abs(W.sc.astype(np.float32)), 16, axis=-1)

@@ -133,6 +133,12 @@ def _int_sums(W, xq, wtype):
         Sx = np.einsum("nbe,mbe->mnb", qw, qx.astype(np.int64))
         return Sx, np.zeros_like(Sx)
     _, qx, bs = O.q8k_fields(xq)  # [m, nb, 256], [m, nb, 16]
+    if wtype == O.Q2_K:
+        isum = np.einsum("nbje,mbje->mnbj", W.q.reshape(W.n, -1, 16, 16).astype(np.int64),
+                         qx.reshape(m, -1, 16, 16).astype(np.int64))
+        Sx = (isum * W.sc.astype(np.int64)[None]).sum(-1)
+        Sm = np.einsum("mbg,nbg->mnb", bs.astype(np.int64), W.mn.astype(np.int64))
+        return Sx, Sm
     if wtype in (O.Q4_K, O.Q5_K):
         isum = np.einsum("nbje,mbje->mnbj", W.q.reshape(W.n, -1, 8, 32).astype(np.int64),
                          qx.reshape(m, -1, 8, 32).astype(np.int64))
@@ -145,7 +151,7 @@ def _int_sums(W, xq, wtype):
     return Sx, np.zeros_like(Sx)
 
 
-WTYPES = [O.Q4_K, O.Q5_K, O.Q6_K, O.Q8_0, O.Q4_0]
+WTYPES = [O.Q4_K, O.Q5_K, O.Q6_K, O.Q8_0, O.Q4_0, O.Q2_K, O.Q3_K]
 
 
 @pytest.mark.parametrize("wtype", WTYPES)
@@ -371,4 +377,103 @@ def test_q4_0_nibble_lands_on_element_j_or_j_plus_16(j, hi):
     got = O.dequantize(O.Q4_0, b[None], 32)[0]
     want = np.zeros(32)
     want[j + 16 * hi] = 10.0
+    assert np.array_equal(got, want)
+
+
+# ------------------------------------------ Q2_K / Q3_K: hand-built blocks
+def _q2k_block(scales=0x01, qs=None, d=1.0, dmin=0.0):
+    """One Q2_K block built byte by byte: scales[16] @0 (low nibble scale,
+    high nibble min), qs[64] @16, f16 d @80, f16 dmin @82."""
+    b = np.zeros(84, np.uint8)
+    b[0:16] = scales
+    if qs is not None:
+        b[16:80] = qs
+    b[80:82] = np.array([d], np.float16).view(np.uint8)
+    b[82:84] = np.array([dmin], np.float16).view(np.uint8)
+    return b
+
+
+@pytest.mark.parametrize("hf,j,l", [(0, 0, 0), (0, 3, 31), (1, 1, 7), (1, 2, 16), (0, 2, 15)])
+def test_q2k_quant_lands_on_element_128hf_32j_l(hf, j, l):
+    """GGML dequantize_row_q2_K: bits 2j..2j+1 of qs[32hf + l] are element
+    128hf + 32j + l."""
+    qs = np.zeros(64, np.uint8)
+    qs[32 * hf + l] = 3 << (2 * j)
+    got = O.dequantize(O.Q2_K, _q2k_block(qs=qs)[None], 256)[0]
+    want = np.zeros(256)
+    want[128 * hf + 32 * j + l] = 3.0
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("g", [0, 5, 8, 15])
+def test_q2k_scale_and_min_of_group_g(g):
+    """scales[g] holds the scale (low nibble) and min (high nibble) of
+    elements 16g .. 16g + 15: value d * sc * q - dmin * mn."""
+    sc = np.zeros(16, np.uint8)
+    sc[g] = 0x75  # scale 5, min 7
+    qs = np.full(64, 0x55, np.uint8)  # every quant 1
+    got = O.dequantize(O.Q2_K, _q2k_block(scales=sc, qs=qs, d=2.0, dmin=0.5)[None], 256)[0]
+    want = np.zeros(256)
+    want[16 * g:16 * g + 16] = 2.0 * 5 * 1 - 0.5 * 7
+    assert np.array_equal(got, want)
+
+
+def test_q2k_dot_closed_form():
+    """Every quant 3, scale 15, min 15, d = 1, dmin = 1, activation all ones
+    (quants -128 after Q8_K: the first max maps to -128): per block
+    S = 16 * 15 * (3 * -128 * 16), Smin = 16 * 15 * (-128 * 16)."""
+    w = _q2k_block(scales=0xFF, qs=np.full(64, 0xFF, np.uint8), d=1.0, dmin=1.0)[None]
+    x = np.ones((1, 256), np.float32)
+    xq = O.quantize(x, O.Q8_K)
+    S_, Sm = O.block_sums(O.Q2_K, 256, w, xq)
+    assert S_[0, 0, 0] == 16 * 15 * 3 * -128 * 16
+    assert Sm[0, 0, 0] == 16 * 15 * -128 * 16
+    dx = O.q8k_fields(xq)[0][0, 0]
+    got = O.matmul_preq(O.Q2_K, xq, w, 1, 256)[0, 0]
+    assert got == np.float32(np.float32(dx * np.float32(S_[0, 0, 0])) - np.float32(dx * np.float32(Sm[0, 0, 0])))
+
+
+def _q3k_block(hmask=0xFF, qs=None, scale_bytes=None, d=1.0):
+    """One Q3_K block built byte by byte: hmask[32] @0, qs[64] @32,
+    scales[12] @96, f16 d @108.  Default scale bytes give every group the
+    6-bit scale 32 (value 0): low nibbles 0, two-bit fields 0b10."""
+    b = np.zeros(110, np.uint8)
+    b[0:32] = hmask
+    if qs is not None:
+        b[32:96] = qs
+    b[96:108] = scale_bytes if scale_bytes is not None else np.r_[np.zeros(8, np.uint8), np.full(4, 0xAA, np.uint8)]
+    b[108:110] = np.array([d], np.float16).view(np.uint8)
+    return b
+
+
+@pytest.mark.parametrize("g,nib_byte,nib_hi,bits_byte,bits_shift", [
+    (0, 0, False, 8, 0), (3, 3, False, 11, 0), (5, 5, False, 9, 2), (9, 1, True, 9, 4), (14, 6, True, 10, 6)])
+def test_q3k_scale_of_group_g(g, nib_byte, nib_hi, bits_byte, bits_shift):
+    """candle's auxs form: scales 0-3 = low nibbles of bytes 0-3 + bits 0-1
+    of bytes 8-11; 4-7 = low nibbles of bytes 4-7 + bits 2-3; 8-11 = high
+    nibbles of bytes 0-3 + bits 4-5; 12-15 = high nibbles of bytes 4-7 +
+    bits 6-7; value scale - 32.  Group g gets 63 (value 31), every other 32."""
+    sb = np.r_[np.zeros(8, np.uint8), np.full(4, 0xAA, np.uint8)]
+    sb[nib_byte] |= 0xF0 if nib_hi else 0x0F
+    sb[bits_byte] |= 3 << bits_shift
+    qs = np.full(64, 0x55, np.uint8)  # every 2-bit field 1, hmask set: value 1
+    got = O.dequantize(O.Q3_K, _q3k_block(qs=qs, scale_bytes=sb)[None], 256)[0]
+    want = np.zeros(256)
+    want[16 * g:16 * g + 16] = 31.0
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("hf,j,l", [(0, 0, 0), (0, 3, 20), (1, 0, 31), (1, 3, 9)])
+def test_q3k_hmask_bit_lands_on_element(hf, j, l):
+    """GGML dequantize_row_q3_K: bit 4hf + j of hmask[l] clear subtracts 4
+    from element 128hf + 32j + l; bits 2j..2j+1 of qs[32hf + l] are its low
+    two bits.  All scales 33 (value 1)."""
+    sb = np.r_[np.full(8, 0x11, np.uint8), np.full(4, 0xAA, np.uint8)]  # 0b10_0001 = 33
+    hm = np.full(32, 0xFF, np.uint8)
+    hm[l] &= ~np.uint8(1 << (4 * hf + j))
+    qs = np.zeros(64, np.uint8)
+    qs[32 * hf + l] = 2 << (2 * j)
+    got = O.dequantize(O.Q3_K, _q3k_block(hmask=hm, qs=qs, scale_bytes=sb)[None], 256)[0]
+    want = np.zeros(256)
+    want[128 * hf + 32 * j + l] = 2.0 - 4.0
     assert np.array_equal(got, want)
