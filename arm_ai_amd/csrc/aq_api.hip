@@ -67,6 +67,8 @@ int fail(int code, const char *fmt, ...) {
 
 int block_elems(int type) {
     switch (type) {
+    case AQ_TYPE_Q2_K:
+    case AQ_TYPE_Q3_K:
     case AQ_TYPE_Q4_K:
     case AQ_TYPE_Q5_K:
     case AQ_TYPE_Q6_K: return QK_K;
@@ -77,6 +79,8 @@ int block_elems(int type) {
 }
 int block_bytes(int type) {
     switch (type) {
+    case AQ_TYPE_Q2_K: return 84;
+    case AQ_TYPE_Q3_K: return 110;
     case AQ_TYPE_Q4_K: return 144;
     case AQ_TYPE_Q5_K: return 176;
     case AQ_TYPE_Q6_K: return 210;
@@ -299,7 +303,9 @@ static int upload_impl(aq_ctx *ctx, int type, const void *blocks, size_t nbytes,
     const int64_t nrb = (n + RB - 1) / RB;
     const int64_t rb_stride = (int64_t)slabs_of(type) * ng * 128;
     const size_t slab_bytes = align_up((size_t)rb_stride * (size_t)nrb, 256);
-    const size_t d_bytes = type == AQ_TYPE_Q6_K ? align_up((size_t)nrb * ng * RB * 2, 256) : 0;
+    const size_t d_bytes = type == AQ_TYPE_Q6_K   ? align_up((size_t)nrb * ng * RB * 2, 256)
+                           : type == AQ_TYPE_Q2_K ? align_up((size_t)nrb * ng * RB * 4, 256)
+                                                  : 0;
     // Q4_0: the GEMM's expanded copy in the Q8_0 tile layout
     const int64_t g_stride = type == AQ_TYPE_Q4_0 ? (int64_t)slabs_of(TYPE_Q8_0) * ng * 128 : 0;
     const size_t g_bytes = align_up((size_t)g_stride * (size_t)nrb, 256);
@@ -332,8 +338,9 @@ static int upload_impl(aq_ctx *ctx, int type, const void *blocks, size_t nbytes,
     }
 
     int status = AQ_OK;
-    // padding rows (n not a multiple of 8) and Q8_0 padding blocks must read as zeros
-    if ((n % RB != 0 || (act_q80(type) && (k / QK8_0) % 8 != 0)) &&
+    // padding rows (n not a multiple of 8) and Q8_0 padding blocks must read as
+    // zeros; Q3_K's two padding bytes per group are cleared too
+    if ((n % RB != 0 || (act_q80(type) && (k / QK8_0) % 8 != 0) || type == AQ_TYPE_Q3_K) &&
         hipMemsetAsync(base, 0, total, ctx->stream) != hipSuccess)
         status = fail(AQ_ERR_HIP, "hipMemsetAsync of the weight padding failed");
 

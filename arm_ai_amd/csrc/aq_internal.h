@@ -12,6 +12,8 @@ constexpr int QK_K = 256;
 constexpr int QK8_0 = 32;
 constexpr int TYPE_Q4_0 = 2;
 constexpr int TYPE_Q8_0 = 8;
+constexpr int TYPE_Q2_K = 10;
+constexpr int TYPE_Q3_K = 11;
 constexpr int TYPE_Q4_K = 12;
 constexpr int TYPE_Q5_K = 13;
 constexpr int TYPE_Q6_K = 14;
@@ -34,13 +36,20 @@ constexpr int TYPE_Q8_K = 15;
 //                             multiple of 8 is padded with zero blocks.
 //   Q4_0 (9 pieces = 144 B):  piece j = the 16 qs bytes of block 8g+j, piece 8
 //                             = the eight f16 d; padded like Q8_0.
+//   Q2_K (5 pieces = 80 B + d plane): piece 0 = scales[16], 1..4 = qs[0..63];
+//                             d and dmin (f16 each) go to a plane of 32-bit
+//                             entries, d in the low half.
+//   Q3_K (7 pieces = 112 B):  the GGUF block in order: pieces 0..1 = hmask,
+//                             2..5 = qs, 6 = scales[12] then f16 d (2 bytes
+//                             of padding).
 // Rows are taken in blocks of 8 (the row count is padded with zero rows to a
 // multiple of 8), and for each (row block, group, piece) the 8 rows' pieces
 // are one 128-byte line:
 //   byte offset of piece p of group g of row r =
 //       (r/8) * rb_stride + (g * PIECES + p) * 128 + (r%8) * 16,
 //   rb_stride = groups * PIECES * 128;
-//   Q6_K d of (r, g): element ((r/8) * groups + g) * 8 + r%8 of the d plane.
+//   Q6_K d of (r, g): element ((r/8) * groups + g) * 8 + r%8 of the d plane
+//   (16-bit entries; Q2_K: 32-bit entries at the same index).
 // The decode matvec reads a tile with lanes (group, row) of an 8 x 8 block of
 // a row block: eight full lines per load instruction.  The prefill GEMM reads
 // it with lanes over 32 consecutive rows (output columns) of one group: four
@@ -49,7 +58,7 @@ constexpr int TYPE_Q8_K = 15;
 constexpr int RB = 8;  // rows per row block
 struct WLayout {
     const uint8_t *slab = nullptr;  // row-block tiles
-    const uint16_t *d = nullptr;    // Q6_K only: [n/8][groups][8] f16
+    const uint16_t *d = nullptr;    // Q6_K: [n/8][groups][8] f16; Q2_K: [n/8][groups][8] (f16 d, f16 dmin)
     int type = 0;
     int ng = 0;                     // groups per row
     int64_t rb_stride = 0;          // bytes per row block
@@ -57,7 +66,7 @@ struct WLayout {
 
 __host__ __device__ constexpr int slabs_of(int type) {
     return type == TYPE_Q4_K ? 9 : type == TYPE_Q5_K ? 11 : type == TYPE_Q6_K ? 13 : type == TYPE_Q8_0 ? 17
-         : type == TYPE_Q4_0 ? 9 : 0;
+         : type == TYPE_Q4_0 ? 9 : type == TYPE_Q2_K ? 5 : type == TYPE_Q3_K ? 7 : 0;
 }
 // Weights whose activation is quantised to Q8_0 blocks of 32 (candle's
 // VecDotType): Q8_0 and Q4_0.  The others use Q8_K.

@@ -60,7 +60,7 @@ struct MvParams {
 template <int TYPE>
 struct Wt {
     uint4 pc[slabs_of(TYPE)];
-    uint32_t d;  // Q6_K super-block d (f16 bits)
+    uint32_t d;  // Q6_K super-block d (f16 bits); Q2_K d | dmin << 16
 };
 
 // Weights are streamed once per call: nontemporal loads keep them from
@@ -80,6 +80,10 @@ __device__ __forceinline__ void load_w(Wt<TYPE> &W, const MvParams &p, int rb, i
     if (TYPE == TYPE_Q6_K) {
         const rsrc_t rd = buf_rsrc(p.wd + (int64_t)rb * p.ng * RB, rb_ok ? (uint32_t)(p.ng * RB * 2) : 0u);
         W.d = __builtin_amdgcn_raw_buffer_load_b16(rd, g < p.ng ? (uint32_t)((g * RB + r_l) * 2) : BUF_OOB, 0, BUF_NT);
+    }
+    if (TYPE == TYPE_Q2_K) {  // d | dmin << 16
+        const rsrc_t rd = buf_rsrc(p.wd + (int64_t)rb * p.ng * RB * 2, rb_ok ? (uint32_t)(p.ng * RB * 4) : 0u);
+        W.d = __builtin_amdgcn_raw_buffer_load_b32(rd, g < p.ng ? (uint32_t)((g * RB + r_l) * 4) : BUF_OOB, 0, BUF_NT);
     }
 }
 
@@ -234,6 +238,120 @@ __device__ __forceinline__ void dot_q6k(const Wt<TYPE_Q6_K> &W, const uint8_t *l
     }
 }
 
+// ------------------------------------------------------------- Q2_K, Q3_K
+// Both: element 128hf + 32j + 16t + i (half hf, shift j, 16-element half t)
+// is bits 2j..2j+1 of qs byte 32hf + 16t + i, in 16-element group
+// 8hf + 2j + t.  Q2_K: pieces 0 = scales (scale | min << 4 per group),
+// 1 + 2hf + t = qs.  Q3_K: pieces t = hmask bytes 16t.., 2 + 2hf + t = qs,
+// 6 = scales[12] then d; bit 4hf + j of the hmask byte set means the value
+// is the two bits, clear means the two bits - 4, and the 6-bit group scale
+// (candle's auxs form) is used as scale - 32.
+template <int B, bool DUMP>
+__device__ __forceinline__ void dot_q2k(const Wt<TYPE_Q2_K> &W, const uint8_t *lds, int ng, int g, int m,
+                                        float (&f)[B], int (&So)[B], int (&Smo)[B]) {
+    const uint32_t scw[4] = {W.pc[0].x, W.pc[0].y, W.pc[0].z, W.pc[0].w};
+    int S[B];
+#pragma unroll
+    for (int b = 0; b < B; b++) S[b] = 0;
+#pragma unroll
+    for (int hf = 0; hf < 2; hf++) {
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            const uint4 Q = W.pc[1 + 2 * hf + t];
+            const uint32_t qv[4] = {Q.x, Q.y, Q.z, Q.w};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                uint32_t q[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) q[i] = (qv[i] >> (2 * j)) & 0x03030303u;
+                const int grp = 8 * hf + 2 * j + t;
+                const int sc = byte_u(scw[grp >> 2], grp & 3) & 15;
+#pragma unroll
+                for (int b = 0; b < B; b++) {
+                    if (b < m) {
+                        const uint8_t *rec = lds + (b * ng + g) * REC;
+                        S[b] += sc * dot16(q, *(const int4 *)(rec + 128 * hf + 32 * j + 16 * t), 0);
+                    }
+                }
+            }
+        }
+    }
+    const float dw = f16_bits_to_f32(W.d), dmw = f16_bits_to_f32(W.d >> 16);
+#pragma unroll
+    for (int b = 0; b < B; b++) {
+        if (b < m) {
+            const uint8_t *rec = lds + (b * ng + g) * REC;
+            const int4 p0 = *(const int4 *)(rec + REC_BSUMS), p1 = *(const int4 *)(rec + REC_BSUMS + 16);
+            const uint32_t pw[8] = {(uint32_t)p0.x, (uint32_t)p0.y, (uint32_t)p0.z, (uint32_t)p0.w,
+                                    (uint32_t)p1.x, (uint32_t)p1.y, (uint32_t)p1.z, (uint32_t)p1.w};
+            int smin = 0;
+#pragma unroll
+            for (int w = 0; w < 8; w++) {  // bsums dword w: groups 2w, 2w + 1
+                smin += (byte_u(scw[w >> 1], 2 * (w & 1)) >> 4) * lo16(pw[w]);
+                smin += (byte_u(scw[w >> 1], 2 * (w & 1) + 1) >> 4) * hi16(pw[w]);
+            }
+            const float dx = *(const float *)(rec + REC_D);
+            f[b] += (dw * dx) * (float)S[b] - (dmw * dx) * (float)smin;
+            if (DUMP) {
+                So[b] = S[b];
+                Smo[b] = smin;
+            }
+        }
+    }
+}
+
+template <int B, bool DUMP>
+__device__ __forceinline__ void dot_q3k(const Wt<TYPE_Q3_K> &W, const uint8_t *lds, int ng, int g, int m,
+                                        float (&f)[B], int (&So)[B], int (&Smo)[B]) {
+    const uint32_t a0 = W.pc[6].x, a1 = W.pc[6].y, tmp = W.pc[6].z;
+    const uint32_t scw[4] = {(a0 & 0x0F0F0F0Fu) | ((tmp & 0x03030303u) << 4),
+                             (a1 & 0x0F0F0F0Fu) | (((tmp >> 2) & 0x03030303u) << 4),
+                             ((a0 >> 4) & 0x0F0F0F0Fu) | (((tmp >> 4) & 0x03030303u) << 4),
+                             ((a1 >> 4) & 0x0F0F0F0Fu) | (((tmp >> 6) & 0x03030303u) << 4)};
+    int S[B];
+#pragma unroll
+    for (int b = 0; b < B; b++) S[b] = 0;
+#pragma unroll
+    for (int hf = 0; hf < 2; hf++) {
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            const uint4 Q = W.pc[2 + 2 * hf + t], H = W.pc[t];
+            const uint32_t qv[4] = {Q.x, Q.y, Q.z, Q.w}, hv[4] = {H.x, H.y, H.z, H.w};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                uint32_t q[4];  // value + 4, in 0..7
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    q[i] = ((qv[i] >> (2 * j)) & 0x03030303u) | (((hv[i] >> (4 * hf + j)) & 0x01010101u) << 2);
+                const int grp = 8 * hf + 2 * j + t;
+                const int sc = byte_u(scw[grp >> 2], grp & 3) - 32;
+#pragma unroll
+                for (int b = 0; b < B; b++) {
+                    if (b < m) {
+                        const uint8_t *rec = lds + (b * ng + g) * REC;
+                        const int isum = dot16(q, *(const int4 *)(rec + 128 * hf + 32 * j + 16 * t), 0);
+                        const int bs = (int)*(const int16_t *)(rec + REC_BSUMS + 2 * grp);
+                        // sum (u - 4) * x = sum u * x - 4 * (sum of the same 16 x)
+                        S[b] += sc * (isum - 4 * bs);
+                    }
+                }
+            }
+        }
+    }
+    const float dw = f16_bits_to_f32(W.pc[6].w);
+#pragma unroll
+    for (int b = 0; b < B; b++) {
+        if (b < m) {
+            const float dx = *(const float *)(lds + (b * ng + g) * REC + REC_D);
+            f[b] += (dw * dx) * (float)S[b];
+            if (DUMP) {
+                So[b] = S[b];
+                Smo[b] = 0;
+            }
+        }
+    }
+}
+
 // ------------------------------------------------------------------ Q8_0
 // Group of eight blocks: pieces 2j, 2j+1 = qs of block j, piece 16 = the
 // eight f16 d.  candle: sumf += (sum_i qw*qx as f32) * f16(d_w) * f16(d_x).
@@ -322,6 +440,8 @@ __device__ __forceinline__ void group_dot(const Wt<TYPE> &W, const uint8_t *lds,
         int So[B], Smo[B];
         if (TYPE == TYPE_Q4_K) dot_q45k<B, DUMP, TYPE_Q4_K>(*(const Wt<TYPE_Q4_K> *)&W, lds, p.ng, g, p.m, f, So, Smo);
         else if (TYPE == TYPE_Q5_K) dot_q45k<B, DUMP, TYPE_Q5_K>(*(const Wt<TYPE_Q5_K> *)&W, lds, p.ng, g, p.m, f, So, Smo);
+        else if (TYPE == TYPE_Q2_K) dot_q2k<B, DUMP>(*(const Wt<TYPE_Q2_K> *)&W, lds, p.ng, g, p.m, f, So, Smo);
+        else if (TYPE == TYPE_Q3_K) dot_q3k<B, DUMP>(*(const Wt<TYPE_Q3_K> *)&W, lds, p.ng, g, p.m, f, So, Smo);
         else dot_q6k<B, DUMP>(*(const Wt<TYPE_Q6_K> *)&W, lds, p.ng, g, p.m, f, So, Smo);
         if (DUMP && valid) {
 #pragma unroll
@@ -720,12 +840,13 @@ hipError_t matvec_impl(const WLayout &w, int64_t n, int64_t k, const float *x, c
 hipError_t matvec_impl(const WLayout &w, int64_t n, int64_t k, const float *x, const ActPlanes *act, int64_t m,
                        float *y, int32_t *S, int32_t *Smin, const XfArgs &xa, hipStream_t s) {
     const int type = w.type;
-    if (type != TYPE_Q4_K && type != TYPE_Q5_K && type != TYPE_Q6_K && type != TYPE_Q8_0 && type != TYPE_Q4_0)
+    if (type != TYPE_Q4_K && type != TYPE_Q5_K && type != TYPE_Q6_K && type != TYPE_Q8_0 && type != TYPE_Q4_0 &&
+        type != TYPE_Q2_K && type != TYPE_Q3_K)
         return hipErrorInvalidValue;
     const int blk = act_q80(type) ? QK8_0 : QK_K;
     if (!w.slab || m < 0 || n <= 0 || k <= 0 || k % blk || n > 0x7fffffff || k > 0x7fffffff || !y)
         return hipErrorInvalidValue;
-    if (type == TYPE_Q6_K && !w.d) return hipErrorInvalidValue;
+    if ((type == TYPE_Q6_K || type == TYPE_Q2_K) && !w.d) return hipErrorInvalidValue;
     if (w.ng != groups_of(type, k)) return hipErrorInvalidValue;
     if (!x && !act) return hipErrorInvalidValue;
     if (x && ((uintptr_t)x & 15)) return hipErrorInvalidValue;  // the fused prologue reads float4
@@ -785,6 +906,8 @@ hipError_t matvec_impl(const WLayout &w, int64_t n, int64_t k, const float *x, c
         case TYPE_Q5_K: e = launch_t<TYPE_Q5_K>(B, p, (unsigned)grid, lds, S != nullptr, xa.xf, s); break;
         case TYPE_Q6_K: e = launch_t<TYPE_Q6_K>(B, p, (unsigned)grid, lds, S != nullptr, xa.xf, s); break;
         case TYPE_Q4_0: e = launch_t<TYPE_Q4_0>(B, p, (unsigned)grid, lds, S != nullptr, xa.xf, s); break;
+        case TYPE_Q2_K: e = launch_t<TYPE_Q2_K>(B, p, (unsigned)grid, lds, S != nullptr, xa.xf, s); break;
+        case TYPE_Q3_K: e = launch_t<TYPE_Q3_K>(B, p, (unsigned)grid, lds, S != nullptr, xa.xf, s); break;
         default: e = launch_t<TYPE_Q8_0>(B, p, (unsigned)grid, lds, S != nullptr, xa.xf, s); break;
         }
         if (e != hipSuccess) return e;
@@ -826,7 +949,7 @@ hipError_t norm_params(const WLayout &w, int64_t n, int64_t k, const float *x, c
     const int type = w.type;
     if (type != TYPE_Q4_K && type != TYPE_Q6_K) return hipErrorNotSupported;
     if (!w.slab || n <= 0 || k <= 0 || k % QK_K || n > 0x7fffffff || k > 0x7fffffff || !y || !x) return hipErrorInvalidValue;
-    if (type == TYPE_Q6_K && !w.d) return hipErrorInvalidValue;
+    if ((type == TYPE_Q6_K || type == TYPE_Q2_K) && !w.d) return hipErrorInvalidValue;
     if (w.ng != groups_of(type, k) || ((uintptr_t)x & 15) || !xa.norm) return hipErrorInvalidValue;
     const int ng = w.ng;
     if ((int64_t)8 * n * 4 >= ((int64_t)1 << 31)) return hipErrorNotSupported;

@@ -108,7 +108,7 @@ template <int TYPE>
 __global__ __launch_bounds__(256) void repack_kernel(const uint8_t *__restrict__ src, int64_t n, int64_t nblk,
                                                      int ng, uint8_t *__restrict__ slab, uint16_t *__restrict__ dpl) {
     constexpr int BYTES = TYPE == TYPE_Q4_K ? 144 : TYPE == TYPE_Q5_K ? 176 : TYPE == TYPE_Q6_K ? 210
-                        : TYPE == TYPE_Q4_0 ? 18 : 34;
+                        : TYPE == TYPE_Q4_0 ? 18 : TYPE == TYPE_Q2_K ? 84 : TYPE == TYPE_Q3_K ? 110 : 34;
     constexpr int S = slabs_of(TYPE);
     const int64_t rb_stride = (int64_t)ng * S * 128;
     const int64_t total = n * nblk * BYTES;
@@ -128,8 +128,12 @@ __global__ __launch_bounds__(256) void repack_kernel(const uint8_t *__restrict__
             const int j = (int)(b & 7);
             if (o < 2) rbp[(g * S + 8) * 128 + 2 * j + o] = src[i];
             else rbp[(g * S + j) * 128 + (o - 2)] = src[i];
-        } else if (TYPE == TYPE_Q5_K) {
-            // the 176 bytes are 11 pieces in order: byte o -> piece o / 16
+        } else if (TYPE == TYPE_Q2_K) {
+            // scales 0..15 -> piece 0, qs 16..79 -> pieces 1..4, d / dmin 80..83 -> the plane's 32-bit entry
+            if (o < 80) rbp[(b * S + (o >> 4)) * 128 + (o & 15)] = src[i];
+            else ((uint8_t *)(dpl + (((row >> 3) * ng + b) * 8 + (row & 7)) * 2))[o - 80] = src[i];
+        } else if (TYPE == TYPE_Q5_K || TYPE == TYPE_Q3_K) {
+            // the block's bytes are its pieces in order: byte o -> piece o / 16
             rbp[(b * S + (o >> 4)) * 128 + (o & 15)] = src[i];
         } else if (TYPE == TYPE_Q6_K) {
             if (o < 208) {
@@ -204,6 +208,11 @@ hipError_t launch_repack(int type, const uint8_t *src, int64_t n, int64_t k, uin
         break;
     case TYPE_Q8_0: repack_kernel<TYPE_Q8_0><<<grid, 256, 0, s>>>(src, n, nblk, ng, dst_slab, dst_d); break;
     case TYPE_Q4_0: repack_kernel<TYPE_Q4_0><<<grid, 256, 0, s>>>(src, n, nblk, ng, dst_slab, dst_d); break;
+    case TYPE_Q2_K:
+        if (!dst_d) return hipErrorInvalidValue;
+        repack_kernel<TYPE_Q2_K><<<grid, 256, 0, s>>>(src, n, nblk, ng, dst_slab, dst_d);
+        break;
+    case TYPE_Q3_K: repack_kernel<TYPE_Q3_K><<<grid, 256, 0, s>>>(src, n, nblk, ng, dst_slab, dst_d); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

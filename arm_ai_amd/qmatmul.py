@@ -30,6 +30,8 @@ class GgmlDType(IntEnum):
 
     Q4_0 = 2
     Q8_0 = 8
+    Q2K = 10
+    Q3K = 11
     Q4K = 12
     Q5K = 13
     Q6K = 14
@@ -41,8 +43,8 @@ class GgmlDType(IntEnum):
 
     @property
     def type_size(self) -> int:
-        return {GgmlDType.Q4_0: 18, GgmlDType.Q8_0: 34, GgmlDType.Q4K: 144, GgmlDType.Q5K: 176, GgmlDType.Q6K: 210,
-                GgmlDType.Q8K: 292}[self]
+        return {GgmlDType.Q4_0: 18, GgmlDType.Q8_0: 34, GgmlDType.Q2K: 84, GgmlDType.Q3K: 110, GgmlDType.Q4K: 144,
+                GgmlDType.Q5K: 176, GgmlDType.Q6K: 210, GgmlDType.Q8K: 292}[self]
 
 
 class QMatMulError(ValueError):

@@ -172,7 +172,7 @@ def measure(ctx, wtype, n, k, m, steps, warmup, seed):
     step_ms, step_wall = time_graph(ctx, wl.step, steps, warmup)
     kern_ms, _ = time_graph(ctx, wl.kernel, steps, warmup)
     out = {
-        "n": n, "k": k, "m": m, "weight_type": {12: "Q4_K", 13: "Q5_K", 14: "Q6_K", 8: "Q8_0", 2: "Q4_0"}[wtype],
+        "n": n, "k": k, "m": m, "weight_type": {12: "Q4_K", 13: "Q5_K", 14: "Q6_K", 8: "Q8_0", 2: "Q4_0", 10: "Q2_K", 11: "Q3_K"}[wtype],
         "step_us": round(step_ms * 1e3, 3),
         "step_GBps": round(wl.step_bytes / (step_ms / 1e3) / 1e9, 1),
         "matvec_us": round(kern_ms * 1e3, 3),
@@ -192,7 +192,7 @@ def measure_prefill(ctx, wtype, n, k, m, steps, warmup, seed):
     kern_ms, _ = time_graph(ctx, wl.kernel, steps, warmup)
     ops = 2.0 * m * n * k
     out = {
-        "n": n, "k": k, "m": m, "weight_type": {12: "Q4_K", 13: "Q5_K", 14: "Q6_K", 8: "Q8_0", 2: "Q4_0"}[wtype],
+        "n": n, "k": k, "m": m, "weight_type": {12: "Q4_K", 13: "Q5_K", 14: "Q6_K", 8: "Q8_0", 2: "Q4_0", 10: "Q2_K", 11: "Q3_K"}[wtype],
         "step_us": round(step_ms * 1e3, 3),
         "step_TOPS": round(ops / (step_ms / 1e3) / 1e12, 1),
         "gemm_us": round(kern_ms * 1e3, 3),
@@ -216,6 +216,8 @@ MATVEC_CASES = {  # name: (weight type, n, k, m, seed)
     "c4_q6k_128256x4096_b8": (14, 128256, 4096, 8, 9),
     "q5k_14336x4096_b1": (13, 14336, 4096, 1, 13),  # a Q5_K_M file's ffn_up, batch 1
     "q4_0_14336x4096_b1": (2, 14336, 4096, 1, 14),  # a Q4_0 file's ffn_up, batch 1
+    "q3k_14336x4096_b1": (11, 14336, 4096, 1, 17),  # a Q3_K_M file's ffn_up, batch 1
+    "q2k_14336x4096_b1": (10, 14336, 4096, 1, 18),  # a Q2_K file's ffn_up, batch 1
 }
 # Reference points, not this library: the vendor's plain int8 x int8 -> int32
 # GEMM (hipBLASLt through torch._int_mm) at the prefill GEMMs' shapes, with no

@@ -191,7 +191,8 @@ def test_prefill_gemm_q6k_extreme_values(ctx):
 
 # ------------------------------------------------------ batch and K coverage
 @pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 7, 8, 11])
-@pytest.mark.parametrize("wtype", [S.TYPE_Q4_K, S.TYPE_Q5_K, S.TYPE_Q6_K, S.TYPE_Q8_0, S.TYPE_Q4_0])
+@pytest.mark.parametrize("wtype", [S.TYPE_Q4_K, S.TYPE_Q5_K, S.TYPE_Q6_K, S.TYPE_Q8_0, S.TYPE_Q4_0, S.TYPE_Q2_K,
+                                   S.TYPE_Q3_K])
 def test_batches(ctx, wtype, m):
     W = S.make_weight(wtype, 300, 2048, seed=m + wtype)
     x = S.make_activation(m, 2048, seed=100 + m)
@@ -199,7 +200,8 @@ def test_batches(ctx, wtype, m):
 
 
 @pytest.mark.parametrize("k", [256, 512, 5632, 16384, 20480])
-@pytest.mark.parametrize("wtype", [S.TYPE_Q4_K, S.TYPE_Q5_K, S.TYPE_Q6_K, S.TYPE_Q8_0, S.TYPE_Q4_0])
+@pytest.mark.parametrize("wtype", [S.TYPE_Q4_K, S.TYPE_Q5_K, S.TYPE_Q6_K, S.TYPE_Q8_0, S.TYPE_Q4_0, S.TYPE_Q2_K,
+                                   S.TYPE_Q3_K])
 @pytest.mark.parametrize("m", [1, 8])
 def test_k_coverage(ctx, wtype, k, m):
     W = S.make_weight(wtype, 70, k, seed=k + m)
@@ -316,6 +318,45 @@ def test_q4_0_extreme_values(ctx):
         check_matmul(ctx, W, x, cond=False)
 
 
+# ------------------------------------------- Q2_K, Q3_K (matvec at any m)
+@pytest.mark.parametrize("wtype", [S.TYPE_Q2_K, S.TYPE_Q3_K])
+@pytest.mark.parametrize("n,k,m", [(14336, 4096, 1), (4096, 14336, 8), (5632, 2048, 1), (300, 2048, 20)])
+def test_q2k_q3k_matvec(ctx, wtype, n, k, m):
+    """Llama-3 and TinyLlama FFN shapes of Q2_K / Q3_K files, batch 1 and 8,
+    and 20 rows (passes of 8): block sums bit-exact."""
+    W = S.make_weight(wtype, n, k, seed=n + k + wtype)
+    x = S.make_activation(m, k, seed=m + k + wtype)
+    check_matmul(ctx, W, x, cond=(k < 14336))
+
+
+def test_q2k_extreme_values(ctx):
+    """Every quant 3, scales and mins 15, activation blocks of equal values
+    (quants +-128 / 127): the largest |S| and |Smin| a Q2_K block reaches."""
+    n, k, m = 40, 1024, 3
+    rng = np.random.default_rng(31)
+    W = S.make_weight(S.TYPE_Q2_K, n, k, seed=31)
+    W.q[:] = 3
+    W.sc[:] = 15
+    W.mn[:] = 15
+    W.blocks = S.pack_q2k(W.d, W.dmin, W.sc, W.mn, W.q)
+    x = np.repeat(rng.standard_normal((m, k // 256)).astype(np.float32), 256, axis=1)
+    check_matmul(ctx, W, x, cond=False)
+
+
+@pytest.mark.parametrize("qv,scv", [(-4, -32), (3, 31), (-4, 31)])
+def test_q3k_extreme_values(ctx, qv, scv):
+    """Every quant -4 (hmask bits clear) or 3, every scale -32 or 31,
+    activation blocks of equal values."""
+    n, k, m = 40, 1024, 3
+    rng = np.random.default_rng(32)
+    W = S.make_weight(S.TYPE_Q3_K, n, k, seed=32)
+    W.q[:] = qv
+    W.sc[:] = scv
+    W.blocks = S.pack_q3k(W.d, W.sc, W.q)
+    x = np.repeat(rng.standard_normal((m, k // 256)).astype(np.float32), 256, axis=1)
+    check_matmul(ctx, W, x, cond=False)
+
+
 # ------------------------------------------ Q8_0 prefill GEMM (int8 MFMA, m > 8)
 @pytest.mark.parametrize("n,k,m", [(768, 2048, 256), (4096, 4096, 16)])
 def test_prefill_gemm_q8_0(ctx, n, k, m):
@@ -367,7 +408,8 @@ def test_prefill_gemm_q8_0_subnormal_and_zero_scales(ctx):
 
 
 @pytest.mark.parametrize("m", [3, 20])
-@pytest.mark.parametrize("wtype", [S.TYPE_Q4_K, S.TYPE_Q5_K, S.TYPE_Q6_K, S.TYPE_Q8_0, S.TYPE_Q4_0])
+@pytest.mark.parametrize("wtype", [S.TYPE_Q4_K, S.TYPE_Q5_K, S.TYPE_Q6_K, S.TYPE_Q8_0, S.TYPE_Q4_0, S.TYPE_Q2_K,
+                                   S.TYPE_Q3_K])
 def test_subnormal_and_zero_scales(ctx, wtype, m):
     """f16 subnormal and zero d / dmin through the matvec (3 rows) and the
     GEMMs (20 rows)."""
@@ -383,6 +425,11 @@ def test_subnormal_and_zero_scales(ctx, wtype, m):
         W.blocks = S.pack_q6k(d, W.sc, W.q)
     elif wtype == S.TYPE_Q4_0:
         W.blocks = S.pack_q4_0(d, W.q)
+    elif wtype == S.TYPE_Q2_K:
+        W.blocks = S.pack_q2k(d, d[:, ::-1].copy(), W.sc, W.mn, W.q)
+        W.dmin = d[:, ::-1].copy()
+    elif wtype == S.TYPE_Q3_K:
+        W.blocks = S.pack_q3k(d, W.sc, W.q)
     else:
         W.blocks = S.pack_q8_0(d, W.q)
     W.d = d
@@ -422,7 +469,8 @@ def test_higher_rank_input_and_determinism(ctx):
 
 
 @pytest.mark.parametrize("wtype,m", [(S.TYPE_Q4_K, 4), (S.TYPE_Q6_K, 1), (S.TYPE_Q8_0, 8), (S.TYPE_Q4_K, 40),
-                                     (S.TYPE_Q5_K, 3), (S.TYPE_Q5_K, 24), (S.TYPE_Q4_0, 2)])
+                                     (S.TYPE_Q5_K, 3), (S.TYPE_Q5_K, 24), (S.TYPE_Q4_0, 2), (S.TYPE_Q2_K, 3),
+                                     (S.TYPE_Q3_K, 12)])
 def test_device_pointer_entry_points(ctx, wtype, m):
     from arm_ai_amd import hip
 
