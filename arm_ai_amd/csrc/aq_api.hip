@@ -73,7 +73,8 @@ int block_elems(int type) {
     case AQ_TYPE_Q5_K:
     case AQ_TYPE_Q6_K: return QK_K;
     case AQ_TYPE_Q8_0:
-    case AQ_TYPE_Q4_0: return QK8_0;
+    case AQ_TYPE_Q4_0:
+    case AQ_TYPE_Q5_0: return QK8_0;
     default: return 0;
     }
 }
@@ -86,6 +87,7 @@ int block_bytes(int type) {
     case AQ_TYPE_Q6_K: return 210;
     case AQ_TYPE_Q8_0: return 34;
     case AQ_TYPE_Q4_0: return 18;
+    case AQ_TYPE_Q5_0: return 22;
     default: return 0;
     }
 }
@@ -306,9 +308,10 @@ static int upload_impl(aq_ctx *ctx, int type, const void *blocks, size_t nbytes,
     const size_t d_bytes = type == AQ_TYPE_Q6_K   ? align_up((size_t)nrb * ng * RB * 2, 256)
                            : type == AQ_TYPE_Q2_K ? align_up((size_t)nrb * ng * RB * 4, 256)
                                                   : 0;
-    // Q4_0: the GEMM's expanded copy in the Q8_0 tile layout
-    const int64_t g_stride = type == AQ_TYPE_Q4_0 ? (int64_t)slabs_of(TYPE_Q8_0) * ng * 128 : 0;
+    // Q4_0, Q5_0: the GEMM's expanded copy in the Q8_0 tile layout
+    const int64_t g_stride = type == AQ_TYPE_Q4_0 || type == AQ_TYPE_Q5_0 ? (int64_t)slabs_of(TYPE_Q8_0) * ng * 128 : 0;
     const size_t g_bytes = align_up((size_t)g_stride * (size_t)nrb, 256);
+    const size_t d_u16 = type == AQ_TYPE_Q2_K ? 2 : 1;  // 16-bit units per d-plane entry
     const size_t total = slab_bytes + d_bytes + g_bytes;
     aq_qweight *w = new (std::nothrow) aq_qweight();
     if (!w) return fail(AQ_ERR_OOM, "out of host memory");
@@ -368,12 +371,12 @@ static int upload_impl(aq_ctx *ctx, int type, const void *blocks, size_t nbytes,
             src = (const uint8_t *)stage;
         }
         hipError_t e = launch_repack(type, src, rows, k, base + (size_t)(r0 / RB) * rb_stride,
-                                     d_bytes ? (uint16_t *)(base + slab_bytes) + (size_t)(r0 / RB) * ng * RB : nullptr,
+                                     d_bytes ? (uint16_t *)(base + slab_bytes) + (size_t)(r0 / RB) * ng * RB * d_u16 : nullptr,
                                      ctx->stream);
         if (e != hipSuccess) status = fail(AQ_ERR_HIP, "repack: %s", hipGetErrorString(e));
         if (status == AQ_OK && g_bytes &&
-            (e = launch_expand_q4_0(src, rows, k, gslab + (size_t)(r0 / RB) * g_stride, ctx->stream)) != hipSuccess)
-            status = fail(AQ_ERR_HIP, "Q4_0 expansion: %s", hipGetErrorString(e));
+            (e = launch_expand_q80(type, src, rows, k, gslab + (size_t)(r0 / RB) * g_stride, ctx->stream)) != hipSuccess)
+            status = fail(AQ_ERR_HIP, "expansion to the Q8_0 layout: %s", hipGetErrorString(e));
         // the staging buffer is reused by the next chunk
         if (status == AQ_OK && hipStreamSynchronize(ctx->stream) != hipSuccess) status = fail(AQ_ERR_HIP, "upload sync failed");
     }

@@ -11,6 +11,7 @@ namespace aq {
 constexpr int QK_K = 256;
 constexpr int QK8_0 = 32;
 constexpr int TYPE_Q4_0 = 2;
+constexpr int TYPE_Q5_0 = 6;
 constexpr int TYPE_Q8_0 = 8;
 constexpr int TYPE_Q2_K = 10;
 constexpr int TYPE_Q3_K = 11;
@@ -35,6 +36,9 @@ constexpr int TYPE_Q8_K = 15;
 //                             the eight f16 d; a row whose block count is not a
 //                             multiple of 8 is padded with zero blocks.
 //   Q4_0 (9 pieces = 144 B):  piece j = the 16 qs bytes of block 8g+j, piece 8
+//                             = the eight f16 d; padded like Q8_0.
+//   Q5_0 (11 pieces = 176 B): piece j = the 16 qs bytes of block 8g+j, pieces
+//                             8 + j/4 bytes 4(j%4).. = its 32-bit qh, piece 10
 //                             = the eight f16 d; padded like Q8_0.
 //   Q2_K (5 pieces = 80 B + d plane): piece 0 = scales[16], 1..4 = qs[0..63];
 //                             d and dmin (f16 each) go to a plane of 32-bit
@@ -66,11 +70,11 @@ struct WLayout {
 
 __host__ __device__ constexpr int slabs_of(int type) {
     return type == TYPE_Q4_K ? 9 : type == TYPE_Q5_K ? 11 : type == TYPE_Q6_K ? 13 : type == TYPE_Q8_0 ? 17
-         : type == TYPE_Q4_0 ? 9 : type == TYPE_Q2_K ? 5 : type == TYPE_Q3_K ? 7 : 0;
+         : type == TYPE_Q4_0 ? 9 : type == TYPE_Q2_K ? 5 : type == TYPE_Q3_K ? 7 : type == TYPE_Q5_0 ? 11 : 0;
 }
 // Weights whose activation is quantised to Q8_0 blocks of 32 (candle's
-// VecDotType): Q8_0 and Q4_0.  The others use Q8_K.
-__host__ __device__ constexpr bool act_q80(int type) { return type == TYPE_Q8_0 || type == TYPE_Q4_0; }
+// VecDotType): Q8_0, Q4_0 and Q5_0.  The others use Q8_K.
+__host__ __device__ constexpr bool act_q80(int type) { return type == TYPE_Q8_0 || type == TYPE_Q4_0 || type == TYPE_Q5_0; }
 inline int groups_of(int type, int64_t k) {
     return act_q80(type) ? (int)((k / QK8_0 + 7) / 8) : (int)(k / QK_K);
 }
@@ -132,10 +136,10 @@ hipError_t launch_quantize_q8_0(const float *x, int64_t m, int64_t k, ActPlanes 
 // block, Q8_0 padding blocks) is not written: zero the tiles beforehand.
 hipError_t launch_repack(int type, const uint8_t *src, int64_t n, int64_t k, uint8_t *dst_slab, uint16_t *dst_d,
                          hipStream_t s);
-// GGUF Q4_0 blocks of n rows -> those rows of a Q8_0 row-block tile layout
-// holding the values q - 8 as int8 and the same f16 d (what the Q8_0 GEMM
-// reads).  Padding is not written: zero the tiles beforehand.
-hipError_t launch_expand_q4_0(const uint8_t *src, int64_t n, int64_t k, uint8_t *dst_slab, hipStream_t s);
+// GGUF Q4_0 / Q5_0 blocks of n rows -> those rows of a Q8_0 row-block tile
+// layout holding the values (q - 8, q - 16) as int8 and the same f16 d (what
+// the Q8_0 GEMM reads).  Padding is not written: zero the tiles beforehand.
+hipError_t launch_expand_q80(int type, const uint8_t *src, int64_t n, int64_t k, uint8_t *dst_slab, hipStream_t s);
 // Measurement aid (k_probe.hip): stream `bytes` of buf (16-byte aligned, a
 // multiple of 16) through a read-only kernel; out needs stream_read_grid()
 // entries.

@@ -429,6 +429,62 @@ __device__ __forceinline__ void dot_q40(const Wt<TYPE_Q4_0> &W, const uint8_t *l
     }
 }
 
+// ------------------------------------------------------------------ Q5_0
+// Group of eight blocks: piece j = the 16 qs bytes of block j, pieces 8, 9 =
+// the 32-bit qh of blocks 0..3, 4..7, piece 10 = the eight f16 d.  Element
+// e < 16: (qs[e] & 15) | bit e of qh << 4; element 16 + e: (qs[e] >> 4) |
+// bit 16 + e of qh << 4; value - 16 (GGML dequantize_row_q5_0).  candle:
+// sum_i (x * qx) as f32 * f16(d_w) * f16(d_x), the integer sum formed as
+// sum q*qx - 16 * sum qx.  Four qh bits go to bit 4 of four bytes with one
+// 24-bit multiply: n * 0x204081 places bit i of n at bit 9i (no overlap).
+__device__ __forceinline__ uint32_t spread4(uint32_t n) {
+    return ((n * 0x204081u) & 0x01010101u) << 4;  // n < 16: a 24-bit multiply
+}
+
+template <int B, bool DUMP>
+__device__ __forceinline__ void dot_q50(const Wt<TYPE_Q5_0> &W, const uint8_t *lds, int ng, int g, int m,
+                                        float (&f)[B], const MvParams &p, int row, bool row_ok) {
+    const uint32_t dwp[4] = {W.pc[10].x, W.pc[10].y, W.pc[10].z, W.pc[10].w};
+    const uint32_t qhw[8] = {W.pc[8].x, W.pc[8].y, W.pc[8].z, W.pc[8].w, W.pc[9].x, W.pc[9].y, W.pc[9].z, W.pc[9].w};
+    const uint32_t ones[4] = {0x01010101u, 0x01010101u, 0x01010101u, 0x01010101u};
+    const int nblk = p.k / QK8_0;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const uint4 q = W.pc[j];
+        const uint32_t qv[4] = {q.x, q.y, q.z, q.w};
+        const uint32_t h = qhw[j];
+        uint32_t lo[4], hi[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            lo[i] = (qv[i] & 0x0F0F0F0Fu) | spread4((h >> (4 * i)) & 0xFu);
+            hi[i] = ((qv[i] >> 4) & 0x0F0F0F0Fu) | spread4((h >> (16 + 4 * i)) & 0xFu);
+        }
+        const float dw = f16_bits_to_f32(dwp[j >> 1] >> (16 * (j & 1)));
+#pragma unroll
+        for (int b = 0; b < B; b++) {
+            if (b < m) {
+                const uint8_t *rec = lds + (b * ng + g) * REC;
+                const int4 x0 = *(const int4 *)(rec + 32 * j), x1 = *(const int4 *)(rec + 32 * j + 16);
+                int isum = dot16(lo, x0, 0);
+                isum = dot16(hi, x1, isum);
+                int xs = dot16(ones, x0, 0);
+                xs = dot16(ones, x1, xs);
+                isum -= 16 * xs;
+                const float dx = *(const float *)(rec + REC_D8 + 4 * j);
+                f[b] += ((float)isum * dw) * dx;
+                if (DUMP) {
+                    const int blk = 8 * g + j;
+                    if (blk < nblk && row_ok) {
+                        const int64_t o = ((int64_t)b * p.n + row) * nblk + blk;
+                        p.S[o] = isum;
+                        p.Smin[o] = 0;
+                    }
+                }
+            }
+        }
+    }
+}
+
 template <int TYPE, int B, bool DUMP>
 __device__ __forceinline__ void group_dot(const Wt<TYPE> &W, const uint8_t *lds, const MvParams &p, int g, int row,
                                           bool valid, float (&f)[B]) {
@@ -436,6 +492,8 @@ __device__ __forceinline__ void group_dot(const Wt<TYPE> &W, const uint8_t *lds,
         dot_q80<B, DUMP>(*(const Wt<TYPE_Q8_0> *)&W, lds, p.ng, g, p.m, f, p, row, valid);
     } else if (TYPE == TYPE_Q4_0) {
         dot_q40<B, DUMP>(*(const Wt<TYPE_Q4_0> *)&W, lds, p.ng, g, p.m, f, p, row, valid);
+    } else if (TYPE == TYPE_Q5_0) {
+        dot_q50<B, DUMP>(*(const Wt<TYPE_Q5_0> *)&W, lds, p.ng, g, p.m, f, p, row, valid);
     } else {
         int So[B], Smo[B];
         if (TYPE == TYPE_Q4_K) dot_q45k<B, DUMP, TYPE_Q4_K>(*(const Wt<TYPE_Q4_K> *)&W, lds, p.ng, g, p.m, f, So, Smo);
@@ -841,7 +899,7 @@ hipError_t matvec_impl(const WLayout &w, int64_t n, int64_t k, const float *x, c
                        float *y, int32_t *S, int32_t *Smin, const XfArgs &xa, hipStream_t s) {
     const int type = w.type;
     if (type != TYPE_Q4_K && type != TYPE_Q5_K && type != TYPE_Q6_K && type != TYPE_Q8_0 && type != TYPE_Q4_0 &&
-        type != TYPE_Q2_K && type != TYPE_Q3_K)
+        type != TYPE_Q2_K && type != TYPE_Q3_K && type != TYPE_Q5_0)
         return hipErrorInvalidValue;
     const int blk = act_q80(type) ? QK8_0 : QK_K;
     if (!w.slab || m < 0 || n <= 0 || k <= 0 || k % blk || n > 0x7fffffff || k > 0x7fffffff || !y)
@@ -908,6 +966,7 @@ hipError_t matvec_impl(const WLayout &w, int64_t n, int64_t k, const float *x, c
         case TYPE_Q4_0: e = launch_t<TYPE_Q4_0>(B, p, (unsigned)grid, lds, S != nullptr, xa.xf, s); break;
         case TYPE_Q2_K: e = launch_t<TYPE_Q2_K>(B, p, (unsigned)grid, lds, S != nullptr, xa.xf, s); break;
         case TYPE_Q3_K: e = launch_t<TYPE_Q3_K>(B, p, (unsigned)grid, lds, S != nullptr, xa.xf, s); break;
+        case TYPE_Q5_0: e = launch_t<TYPE_Q5_0>(B, p, (unsigned)grid, lds, S != nullptr, xa.xf, s); break;
         default: e = launch_t<TYPE_Q8_0>(B, p, (unsigned)grid, lds, S != nullptr, xa.xf, s); break;
         }
         if (e != hipSuccess) return e;

@@ -108,7 +108,8 @@ template <int TYPE>
 __global__ __launch_bounds__(256) void repack_kernel(const uint8_t *__restrict__ src, int64_t n, int64_t nblk,
                                                      int ng, uint8_t *__restrict__ slab, uint16_t *__restrict__ dpl) {
     constexpr int BYTES = TYPE == TYPE_Q4_K ? 144 : TYPE == TYPE_Q5_K ? 176 : TYPE == TYPE_Q6_K ? 210
-                        : TYPE == TYPE_Q4_0 ? 18 : TYPE == TYPE_Q2_K ? 84 : TYPE == TYPE_Q3_K ? 110 : 34;
+                        : TYPE == TYPE_Q4_0 ? 18 : TYPE == TYPE_Q2_K ? 84 : TYPE == TYPE_Q3_K ? 110
+                        : TYPE == TYPE_Q5_0 ? 22 : 34;
     constexpr int S = slabs_of(TYPE);
     const int64_t rb_stride = (int64_t)ng * S * 128;
     const int64_t total = n * nblk * BYTES;
@@ -128,6 +129,14 @@ __global__ __launch_bounds__(256) void repack_kernel(const uint8_t *__restrict__
             const int j = (int)(b & 7);
             if (o < 2) rbp[(g * S + 8) * 128 + 2 * j + o] = src[i];
             else rbp[(g * S + j) * 128 + (o - 2)] = src[i];
+        } else if (TYPE == TYPE_Q5_0) {
+            // Q5_0 block b = 8g + j: d -> piece 10 bytes 2j..2j+1; qh -> piece 8 + j/4 bytes 4(j%4)..;
+            // qs byte q -> piece j byte q
+            const int64_t g = b >> 3;
+            const int j = (int)(b & 7);
+            if (o < 2) rbp[(g * S + 10) * 128 + 2 * j + o] = src[i];
+            else if (o < 6) rbp[(g * S + 8 + (j >> 2)) * 128 + 4 * (j & 3) + (o - 2)] = src[i];
+            else rbp[(g * S + j) * 128 + (o - 6)] = src[i];
         } else if (TYPE == TYPE_Q2_K) {
             // scales 0..15 -> piece 0, qs 16..79 -> pieces 1..4, d / dmin 80..83 -> the plane's 32-bit entry
             if (o < 80) rbp[(b * S + (o >> 4)) * 128 + (o & 15)] = src[i];
@@ -155,17 +164,20 @@ __global__ __launch_bounds__(256) void repack_kernel(const uint8_t *__restrict__
     }
 }
 
-// Q4_0 -> Q8_0 tiles: one thread per source byte.  Block b = 8g + j of a
-// row: d -> piece 16 bytes 2j, 2j+1; qs byte t (elements t and t + 16) ->
-// piece 2j byte t = (qs & 15) - 8 and piece 2j + 1 byte t = (qs >> 4) - 8.
-__global__ __launch_bounds__(256) void expand_q4_0_kernel(const uint8_t *__restrict__ src, int64_t n, int64_t nblk,
-                                                          int ng, uint8_t *__restrict__ slab) {
+// Q4_0 / Q5_0 -> Q8_0 tiles: one thread per source byte.  Block b = 8g + j
+// of a row: d -> piece 16 bytes 2j, 2j+1; qs byte t (elements t and t + 16)
+// -> piece 2j byte t and piece 2j + 1 byte t, the values q - 8 (Q4_0) or,
+// with bits t and t + 16 of qh as the fifth bits, q - 16 (Q5_0).
+template <int TYPE>
+__global__ __launch_bounds__(256) void expand_q80_kernel(const uint8_t *__restrict__ src, int64_t n, int64_t nblk,
+                                                         int ng, uint8_t *__restrict__ slab) {
     constexpr int S = slabs_of(TYPE_Q8_0);
+    constexpr int BYTES = TYPE == TYPE_Q5_0 ? 22 : 18, QS = TYPE == TYPE_Q5_0 ? 6 : 2;
     const int64_t rb_stride = (int64_t)ng * S * 128;
-    const int64_t total = n * nblk * 18;
+    const int64_t total = n * nblk * BYTES;
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
-        const int64_t blk = i / 18;
-        const int o = (int)(i - blk * 18);
+        const int64_t blk = i / BYTES;
+        const int o = (int)(i - blk * BYTES);
         const int64_t row = blk / nblk, b = blk - row * nblk;
         uint8_t *rbp = slab + (row >> 3) * rb_stride + (row & 7) * 16;
         const int64_t g = b >> 3;
@@ -173,21 +185,33 @@ __global__ __launch_bounds__(256) void expand_q4_0_kernel(const uint8_t *__restr
         const uint8_t v = src[i];
         if (o < 2) {
             rbp[(g * S + 16) * 128 + 2 * j + o] = v;
-        } else {
-            const int t = o - 2;
-            rbp[(g * S + 2 * j) * 128 + t] = (uint8_t)(int8_t)((int)(v & 15) - 8);
-            rbp[(g * S + 2 * j + 1) * 128 + t] = (uint8_t)(int8_t)((int)(v >> 4) - 8);
+        } else if (o >= QS) {
+            const int t = o - QS;
+            int lo = v & 15, hi = v >> 4;
+            if (TYPE == TYPE_Q5_0) {
+                const uint8_t *qh = src + blk * BYTES + 2;
+                const uint32_t h = (uint32_t)qh[0] | ((uint32_t)qh[1] << 8) | ((uint32_t)qh[2] << 16) | ((uint32_t)qh[3] << 24);
+                lo = (lo | (((h >> t) & 1) << 4)) - 16;
+                hi = (hi | (((h >> (t + 16)) & 1) << 4)) - 16;
+            } else {
+                lo -= 8;
+                hi -= 8;
+            }
+            rbp[(g * S + 2 * j) * 128 + t] = (uint8_t)(int8_t)lo;
+            rbp[(g * S + 2 * j + 1) * 128 + t] = (uint8_t)(int8_t)hi;
         }
     }
 }
 
-hipError_t launch_expand_q4_0(const uint8_t *src, int64_t n, int64_t k, uint8_t *dst_slab, hipStream_t s) {
+hipError_t launch_expand_q80(int type, const uint8_t *src, int64_t n, int64_t k, uint8_t *dst_slab, hipStream_t s) {
     if (!src || !dst_slab || n <= 0 || k <= 0 || k % QK8_0) return hipErrorInvalidValue;
+    if (type != TYPE_Q4_0 && type != TYPE_Q5_0) return hipErrorInvalidValue;
     const int64_t nblk = k / QK8_0;
-    const int ng = groups_of(TYPE_Q4_0, k);
-    const int64_t total = n * nblk * 18;
+    const int ng = groups_of(type, k);
+    const int64_t total = n * nblk * (type == TYPE_Q5_0 ? 22 : 18);
     const int64_t blocks = (total + 255) / 256, grid = blocks < 65536 ? blocks : 65536;
-    expand_q4_0_kernel<<<(unsigned)grid, 256, 0, s>>>(src, n, nblk, ng, dst_slab);
+    if (type == TYPE_Q5_0) expand_q80_kernel<TYPE_Q5_0><<<(unsigned)grid, 256, 0, s>>>(src, n, nblk, ng, dst_slab);
+    else expand_q80_kernel<TYPE_Q4_0><<<(unsigned)grid, 256, 0, s>>>(src, n, nblk, ng, dst_slab);
     return hipGetLastError();
 }
 
@@ -213,6 +237,7 @@ hipError_t launch_repack(int type, const uint8_t *src, int64_t n, int64_t k, uin
         repack_kernel<TYPE_Q2_K><<<grid, 256, 0, s>>>(src, n, nblk, ng, dst_slab, dst_d);
         break;
     case TYPE_Q3_K: repack_kernel<TYPE_Q3_K><<<grid, 256, 0, s>>>(src, n, nblk, ng, dst_slab, dst_d); break;
+    case TYPE_Q5_0: repack_kernel<TYPE_Q5_0><<<grid, 256, 0, s>>>(src, n, nblk, ng, dst_slab, dst_d); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

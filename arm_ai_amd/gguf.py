@@ -47,11 +47,11 @@ _SCALAR = {T_U8: "<B", T_I8: "<b", T_U16: "<H", T_I16: "<h", T_U32: "<I", T_I32:
 
 # ggml tensor types read here: (elements per block, bytes per block)
 GGML_F32, GGML_F16 = 0, 1
-TYPE_SIZES = {GGML_F32: (1, 4), GGML_F16: (1, 2), synth.TYPE_Q8_0: (32, 34), synth.TYPE_Q4_0: (32, 18),
+TYPE_SIZES = {GGML_F32: (1, 4), GGML_F16: (1, 2), synth.TYPE_Q8_0: (32, 34), synth.TYPE_Q4_0: (32, 18), synth.TYPE_Q5_0: (32, 22),
               synth.TYPE_Q4_K: (256, 144), synth.TYPE_Q5_K: (256, 176), synth.TYPE_Q6_K: (256, 210),
               synth.TYPE_Q2_K: (256, 84), synth.TYPE_Q3_K: (256, 110)}
 QUANT_TYPES = (synth.TYPE_Q4_K, synth.TYPE_Q5_K, synth.TYPE_Q6_K, synth.TYPE_Q8_0, synth.TYPE_Q4_0, synth.TYPE_Q2_K,
-               synth.TYPE_Q3_K)
+               synth.TYPE_Q3_K, synth.TYPE_Q5_0)
 
 
 class GGUFError(ValueError):
@@ -179,7 +179,7 @@ class GGUFFile:
         """A 2-D quantized weight as candle's QTensor (n rows, k columns)."""
         ti = self.tensor(name)
         if ti.type not in QUANT_TYPES or len(ti.dims) != 2:
-            raise GGUFError(f"tensor {name}: a 2-D Q2_K / Q3_K / Q4_K / Q5_K / Q6_K / Q8_0 / Q4_0 weight is needed, got type {ti.type} "
+            raise GGUFError(f"tensor {name}: a 2-D Q2_K / Q3_K / Q4_K / Q5_K / Q6_K / Q8_0 / Q4_0 / Q5_0 weight is needed, got type {ti.type} "
                             f"with dims {ti.dims}")
         k, n = ti.dims
         return QTensor(GgmlDType(ti.type), (n, k), self.raw(name))
@@ -221,6 +221,13 @@ def dequantize(type_: int, raw: np.ndarray, n_elements: int) -> np.ndarray:
         qs = b[:, 2:18]
         q = np.concatenate([qs & 0xF, qs >> 4], axis=1).astype(np.float32) - 8.0  # elements 0..15, 16..31
         return (q * d[:, None]).reshape(-1)[:n_elements]
+    if type_ == synth.TYPE_Q5_0:
+        b = raw.reshape(-1, 22)
+        d = _f16(b[:, 0:2])
+        qh = b[:, 2:6].copy().view("<u4")[:, 0].astype(np.int64)
+        qs = b[:, 6:22].astype(np.int64)
+        q = np.concatenate([qs & 0xF, qs >> 4], axis=1) | (((qh[:, None] >> np.arange(32)[None, :]) & 1) << 4)
+        return ((q - 16).astype(np.float32) * d[:, None]).reshape(-1)[:n_elements]
     if type_ == synth.TYPE_Q8_0:
         b = raw.reshape(-1, 34)
         d = _f16(b[:, 0:2])

@@ -29,6 +29,7 @@ class GgmlDType(IntEnum):
     """GGUF/GGML dtype ids, named as in candle's `GgmlDType`."""
 
     Q4_0 = 2
+    Q5_0 = 6
     Q8_0 = 8
     Q2K = 10
     Q3K = 11
@@ -39,11 +40,11 @@ class GgmlDType(IntEnum):
 
     @property
     def block_size(self) -> int:
-        return 32 if self in (GgmlDType.Q8_0, GgmlDType.Q4_0) else 256
+        return 32 if self in (GgmlDType.Q8_0, GgmlDType.Q4_0, GgmlDType.Q5_0) else 256
 
     @property
     def type_size(self) -> int:
-        return {GgmlDType.Q4_0: 18, GgmlDType.Q8_0: 34, GgmlDType.Q2K: 84, GgmlDType.Q3K: 110, GgmlDType.Q4K: 144,
+        return {GgmlDType.Q4_0: 18, GgmlDType.Q5_0: 22, GgmlDType.Q8_0: 34, GgmlDType.Q2K: 84, GgmlDType.Q3K: 110, GgmlDType.Q4K: 144,
                 GgmlDType.Q5K: 176, GgmlDType.Q6K: 210, GgmlDType.Q8K: 292}[self]
 
 
@@ -182,7 +183,7 @@ class QMatMul:
 
     @property
     def act_type(self) -> GgmlDType:
-        return GgmlDType.Q8_0 if self.dtype in (GgmlDType.Q8_0, GgmlDType.Q4_0) else GgmlDType.Q8K
+        return GgmlDType.Q8_0 if self.dtype in (GgmlDType.Q8_0, GgmlDType.Q4_0, GgmlDType.Q5_0) else GgmlDType.Q8K
 
     def forward_preq_device(self, d_act: int, m: int, d_y: int) -> None:
         """Matmul on an activation quantised by quantize_act_device (asynchronous)."""

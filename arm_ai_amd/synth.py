@@ -12,6 +12,7 @@ configurations prescribe:
   ~ U[0, 63] (value q - 32).
 * Q8_0: d = f16(|N(0, 0.02)|); int8 quants ~ U[-127, 127].
 * Q4_0: d = f16(|N(0, 0.02)|); 4-bit quants ~ U[0, 15] (value q - 8).
+* Q5_0: d = f16(|N(0, 0.02)|); 5-bit quants ~ U[0, 31] (value q - 16).
 * Q2_K: d, dmin = f16(|N(0, 0.02)|); 4-bit scales and mins ~ U[0, 15];
   2-bit quants ~ U[0, 3].
 * Q3_K: d = f16(|N(0, 0.02)|); 6-bit scales ~ U[0, 63] (value s - 32);
@@ -20,8 +21,8 @@ configurations prescribe:
 
 Generators draw element-level arrays from ``numpy.random.default_rng(seed)``
 (PCG64) and pack them into GGUF block bytes with the GGUF layout (block
-formats: Q4_K 144 B, Q5_K 176 B, Q6_K 210 B, Q8_0 34 B, Q4_0 18 B, Q2_K 84 B,
-Q3_K 110 B).  The element arrays are kept so
+formats: Q4_K 144 B, Q5_K 176 B, Q6_K 210 B, Q8_0 34 B, Q4_0 18 B, Q5_0 22 B,
+Q2_K 84 B, Q3_K 110 B).  The element arrays are kept so
 tests can compute exact answers without going through any unpacking code.
 f32 -> f16 uses numpy's IEEE round-to-nearest-even conversion, the same
 rounding the reference's `half` crate uses (shape_ops.rs:1492-1503).
@@ -35,6 +36,7 @@ import numpy as np
 QK_K = 256
 QK8_0 = 32
 TYPE_Q4_0 = 2
+TYPE_Q5_0 = 6
 TYPE_Q8_0 = 8
 TYPE_Q2_K = 10
 TYPE_Q3_K = 11
@@ -43,12 +45,12 @@ TYPE_Q5_K = 13
 TYPE_Q6_K = 14
 TYPE_Q8_K = 15
 
-BLOCK_BYTES = {TYPE_Q4_K: 144, TYPE_Q5_K: 176, TYPE_Q6_K: 210, TYPE_Q8_0: 34, TYPE_Q4_0: 18, TYPE_Q2_K: 84,
+BLOCK_BYTES = {TYPE_Q4_K: 144, TYPE_Q5_K: 176, TYPE_Q6_K: 210, TYPE_Q8_0: 34, TYPE_Q4_0: 18, TYPE_Q5_0: 22, TYPE_Q2_K: 84,
                TYPE_Q3_K: 110, TYPE_Q8_K: 292}
 BLOCK_ELEMS = {TYPE_Q4_K: QK_K, TYPE_Q5_K: QK_K, TYPE_Q6_K: QK_K, TYPE_Q8_0: QK8_0, TYPE_Q4_0: QK8_0,
-               TYPE_Q2_K: QK_K, TYPE_Q3_K: QK_K, TYPE_Q8_K: QK_K}
+               TYPE_Q5_0: QK8_0, TYPE_Q2_K: QK_K, TYPE_Q3_K: QK_K, TYPE_Q8_K: QK_K}
 TYPE_NAMES = {TYPE_Q4_K: "q4_k", TYPE_Q5_K: "q5_k", TYPE_Q6_K: "q6_k", TYPE_Q8_0: "q8_0", TYPE_Q4_0: "q4_0",
-              TYPE_Q2_K: "q2_k", TYPE_Q3_K: "q3_k", TYPE_Q8_K: "q8_k"}
+              TYPE_Q5_0: "q5_0", TYPE_Q2_K: "q2_k", TYPE_Q3_K: "q3_k", TYPE_Q8_K: "q8_k"}
 
 
 @dataclass
@@ -64,7 +66,7 @@ class QWeight:
     sc: np.ndarray | None  # Q4_K / Q5_K uint8 [n, nb, 8]; Q2_K uint8 [n, nb, 16]; Q3_K (value), Q6_K int8 [n, nb, 16]
     mn: np.ndarray | None  # Q4_K / Q5_K uint8 [n, nb, 8]; Q2_K uint8 [n, nb, 16]
     q: np.ndarray  # Q4_K uint8 [n,nb,256] in [0,15]; Q5_K in [0,31]; Q6_K int8 in [-32,31]; Q8_0 int8 [n,nb,32];
-    #               Q4_0 uint8 [n,nb,32] in [0,15] (value q - 8); Q2_K uint8 in [0,3]; Q3_K int8 in [-4,3]
+    #               Q4_0 uint8 [n,nb,32] in [0,15] (value q - 8); Q5_0 in [0,31] (value q - 16); Q2_K uint8 in [0,3]; Q3_K int8 in [-4,3]
 
     @property
     def nbytes(self) -> int:
@@ -86,6 +88,8 @@ class QWeight:
             v = d * sc * self.q.astype(np.float64)
         elif self.type == TYPE_Q4_0:
             v = d * (self.q.astype(np.float64) - 8.0)
+        elif self.type == TYPE_Q5_0:
+            v = d * (self.q.astype(np.float64) - 16.0)
         else:
             v = d * self.q.astype(np.float64)
         return v.reshape(self.n, self.k)
@@ -158,6 +162,20 @@ def pack_q6k(d, sc, q) -> np.ndarray:
     out[..., 192:208] = sc.astype(np.int8).view(np.uint8)
     out[..., 208:210] = d.astype(np.float16).view(np.uint8).reshape(n, nb, 2)
     return out.reshape(n, nb * 210)
+
+
+def pack_q5_0(d, q) -> np.ndarray:
+    """Pack Q5_0 element arrays (q in [0, 31]) into 22-byte blocks: f16 d @0,
+    qh @2 (u32, bit e = bit 4 of element e), qs @6 with qs[j] = q[j] & 15 |
+    (q[j + 16] & 15) << 4."""
+    n, nb = d.shape
+    out = np.empty((n, nb, 22), dtype=np.uint8)
+    out[..., 0:2] = d.astype(np.float16).view(np.uint8).reshape(n, nb, 2)
+    q = q.astype(np.uint32)
+    qh = ((q >> 4) & 1) << np.arange(32, dtype=np.uint32)
+    out[..., 2:6] = qh.sum(axis=-1, dtype=np.uint32).astype("<u4").view(np.uint8).reshape(n, nb, 4)
+    out[..., 6:22] = ((q[..., 0:16] & 15) | ((q[..., 16:32] & 15) << 4)).astype(np.uint8)
+    return out.reshape(n, nb * 22)
 
 
 def pack_q2k(d, dmin, sc, mn, q) -> np.ndarray:
@@ -260,6 +278,10 @@ def make_weight(type_: int, n: int, k: int, seed: int = 0, rng: np.random.Genera
         d = _half_abs_normal(rng, (n, nb))
         q = rng.integers(0, 16, size=(n, nb, 32), dtype=np.uint8)
         return QWeight(type_, n, k, pack_q4_0(d, q), d, None, None, None, q)
+    if type_ == TYPE_Q5_0:
+        d = _half_abs_normal(rng, (n, nb))
+        q = rng.integers(0, 32, size=(n, nb, 32), dtype=np.uint8)
+        return QWeight(type_, n, k, pack_q5_0(d, q), d, None, None, None, q)
     if type_ == TYPE_Q2_K:
         d = _half_abs_normal(rng, (n, nb))
         dmin = _half_abs_normal(rng, (n, nb))
@@ -288,6 +310,6 @@ def weight_bytes(type_: int, n: int, k: int) -> int:
 
 def act_bytes(type_: int, m: int, k: int) -> int:
     """Bytes of the quantised activation a weight of `type_` is dotted with."""
-    if type_ in (TYPE_Q8_0, TYPE_Q4_0):
+    if type_ in (TYPE_Q8_0, TYPE_Q4_0, TYPE_Q5_0):
         return m * (k // QK8_0) * 34
     return m * (k // QK_K) * 292

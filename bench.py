@@ -92,7 +92,7 @@ class Workload:
         A.quantize_act_device(ctx, at, self.dx.ptr, m, k, self.dact.ptr)
         ctx.synchronize()
         self.ctx = ctx
-        act_q = m * (k // 32) * 34 if wtype in (8, 2) else m * (k // 256) * 292
+        act_q = m * (k // 32) * 34 if wtype in (8, 2, 6) else m * (k // 256) * 292
         self.weight_bytes = self.W.nbytes
         self.step_bytes = self.W.nbytes + m * k * 4 + m * n * 4  # quantizer fused into the step
         self.kernel_bytes = self.W.nbytes + act_q + m * n * 4  # matvec kernel alone
@@ -172,7 +172,7 @@ def measure(ctx, wtype, n, k, m, steps, warmup, seed):
     step_ms, step_wall = time_graph(ctx, wl.step, steps, warmup)
     kern_ms, _ = time_graph(ctx, wl.kernel, steps, warmup)
     out = {
-        "n": n, "k": k, "m": m, "weight_type": {12: "Q4_K", 13: "Q5_K", 14: "Q6_K", 8: "Q8_0", 2: "Q4_0", 10: "Q2_K", 11: "Q3_K"}[wtype],
+        "n": n, "k": k, "m": m, "weight_type": {12: "Q4_K", 13: "Q5_K", 14: "Q6_K", 8: "Q8_0", 2: "Q4_0", 6: "Q5_0", 10: "Q2_K", 11: "Q3_K"}[wtype],
         "step_us": round(step_ms * 1e3, 3),
         "step_GBps": round(wl.step_bytes / (step_ms / 1e3) / 1e9, 1),
         "matvec_us": round(kern_ms * 1e3, 3),
@@ -192,7 +192,7 @@ def measure_prefill(ctx, wtype, n, k, m, steps, warmup, seed):
     kern_ms, _ = time_graph(ctx, wl.kernel, steps, warmup)
     ops = 2.0 * m * n * k
     out = {
-        "n": n, "k": k, "m": m, "weight_type": {12: "Q4_K", 13: "Q5_K", 14: "Q6_K", 8: "Q8_0", 2: "Q4_0", 10: "Q2_K", 11: "Q3_K"}[wtype],
+        "n": n, "k": k, "m": m, "weight_type": {12: "Q4_K", 13: "Q5_K", 14: "Q6_K", 8: "Q8_0", 2: "Q4_0", 6: "Q5_0", 10: "Q2_K", 11: "Q3_K"}[wtype],
         "step_us": round(step_ms * 1e3, 3),
         "step_TOPS": round(ops / (step_ms / 1e3) / 1e12, 1),
         "gemm_us": round(kern_ms * 1e3, 3),
@@ -218,6 +218,7 @@ MATVEC_CASES = {  # name: (weight type, n, k, m, seed)
     "q4_0_14336x4096_b1": (2, 14336, 4096, 1, 14),  # a Q4_0 file's ffn_up, batch 1
     "q3k_14336x4096_b1": (11, 14336, 4096, 1, 17),  # a Q3_K_M file's ffn_up, batch 1
     "q2k_14336x4096_b1": (10, 14336, 4096, 1, 18),  # a Q2_K file's ffn_up, batch 1
+    "q5_0_14336x4096_b1": (6, 14336, 4096, 1, 19),  # a Q5_0 file's ffn_up, batch 1
 }
 # Reference points, not this library: the vendor's plain int8 x int8 -> int32
 # GEMM (hipBLASLt through torch._int_mm) at the prefill GEMMs' shapes, with no
@@ -246,6 +247,7 @@ PREFILL_CASES = {  # name: (weight type, n, k, m, seed)
     "prefill_q8_0_4096x4096_m512": (8, 4096, 4096, 512, 12),     # a Q8_0 GGUF's projection
     "prefill_q4_0_4096x4096_m512": (2, 4096, 4096, 512, 15),     # Q4_0: the Q8_0 GEMM on the expanded copy
     "prefill_q5k_5632x2048_m512": (13, 5632, 2048, 512, 16),     # a Q5_K_M file's TinyLlama ffn_up
+    "prefill_q5_0_4096x4096_m512": (6, 4096, 4096, 512, 20),     # Q5_0: the Q8_0 GEMM on the expanded copy
 }
 
 

@@ -18,11 +18,12 @@
  *  - Every function returns an aq_status (0 = AQ_OK, negative = error) and
  *    never aborts the process; aq_last_error() gives the calling thread's
  *    last message.
- *  - Weight type ids are GGUF/GGML dtype ids (Q4_0 = 2, Q8_0 = 8, Q2_K = 10,
- *    Q3_K = 11, Q4_K = 12, Q5_K = 13, Q6_K = 14).  Every type runs the
- *    batch-1..8 matvec.  For m > 8, Q4_K, Q5_K, Q6_K, Q8_0 and Q4_0 run a
- *    prefill GEMM (Q4_0 on an int8 copy that the upload expands into the
- *    Q8_0 layout, 34 bytes per 32 weights beside its 18-byte decode tiles);
+ *  - Weight type ids are GGUF/GGML dtype ids (Q4_0 = 2, Q5_0 = 6, Q8_0 = 8,
+ *    Q2_K = 10, Q3_K = 11, Q4_K = 12, Q5_K = 13, Q6_K = 14).  Every type
+ *    runs the batch-1..8 matvec.  For m > 8, Q4_K, Q5_K, Q6_K, Q8_0, Q4_0
+ *    and Q5_0 run a prefill GEMM (Q4_0 and Q5_0 on an int8 copy that the
+ *    upload expands into the Q8_0 layout, 34 bytes per 32 weights beside
+ *    their 18- or 22-byte decode tiles);
  *    Q2_K and Q3_K run the matvec in passes of 8 rows.
  *  - A weight is n rows (output features) by k columns (input features),
  *    row-major blocks, exactly candle's QTensor storage of shape (n, k).
@@ -54,6 +55,7 @@ typedef enum aq_status {
 
 typedef enum aq_type {
     AQ_TYPE_Q4_0 = 2,
+    AQ_TYPE_Q5_0 = 6,
     AQ_TYPE_Q8_0 = 8,
     AQ_TYPE_Q2_K = 10,
     AQ_TYPE_Q3_K = 11,

@@ -17,9 +17,9 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "liboracle.so")
 
-Q2_K, Q3_K, Q4_0, Q4_K, Q5_K, Q6_K, Q8_0, Q8_K = 10, 11, 2, 12, 13, 14, 8, 15
-BLOCK_BYTES = {Q2_K: 84, Q3_K: 110, Q4_0: 18, Q4_K: 144, Q5_K: 176, Q6_K: 210, Q8_0: 34, Q8_K: 292}
-BLOCK_ELEMS = {Q2_K: 256, Q3_K: 256, Q4_0: 32, Q4_K: 256, Q5_K: 256, Q6_K: 256, Q8_0: 32, Q8_K: 256}
+Q2_K, Q3_K, Q4_0, Q5_0, Q4_K, Q5_K, Q6_K, Q8_0, Q8_K = 10, 11, 2, 6, 12, 13, 14, 8, 15
+BLOCK_BYTES = {Q2_K: 84, Q3_K: 110, Q4_0: 18, Q5_0: 22, Q4_K: 144, Q5_K: 176, Q6_K: 210, Q8_0: 34, Q8_K: 292}
+BLOCK_ELEMS = {Q2_K: 256, Q3_K: 256, Q4_0: 32, Q5_0: 32, Q4_K: 256, Q5_K: 256, Q6_K: 256, Q8_0: 32, Q8_K: 256}
 
 _lib = None
 
@@ -50,7 +50,7 @@ def lib() -> ctypes.CDLL:
             getattr(L, f).argtypes = [P, i64, P]
             getattr(L, f).restype = ctypes.c_int
         for f in ("orc_vec_dot_q2k_q8k", "orc_vec_dot_q3k_q8k", "orc_vec_dot_q4k_q8k", "orc_vec_dot_q5k_q8k", "orc_vec_dot_q6k_q8k", "orc_vec_dot_q8_0_q8_0",
-                  "orc_vec_dot_q4_0_q8_0"):
+                  "orc_vec_dot_q4_0_q8_0", "orc_vec_dot_q5_0_q8_0"):
             getattr(L, f).argtypes = [i64, P, P]
             getattr(L, f).restype = ctypes.c_float
         L.orc_block_sums.argtypes = [ctypes.c_int, i64, P, P, P, P]
@@ -89,7 +89,7 @@ def f32_to_f16(x: np.ndarray) -> np.ndarray:
 
 
 def act_type(wtype: int) -> int:
-    return Q8_0 if wtype in (Q8_0, Q4_0) else Q8_K
+    return Q8_0 if wtype in (Q8_0, Q4_0, Q5_0) else Q8_K
 
 
 def quantize(x: np.ndarray, atype: int = Q8_K) -> np.ndarray:
@@ -128,7 +128,7 @@ def q8_0_fields(blocks: np.ndarray):
 def vec_dot(wtype: int, k: int, wrow: np.ndarray, xq_row: np.ndarray) -> float:
     L = lib()
     f = {Q2_K: L.orc_vec_dot_q2k_q8k, Q3_K: L.orc_vec_dot_q3k_q8k, Q4_K: L.orc_vec_dot_q4k_q8k, Q5_K: L.orc_vec_dot_q5k_q8k, Q6_K: L.orc_vec_dot_q6k_q8k,
-         Q8_0: L.orc_vec_dot_q8_0_q8_0, Q4_0: L.orc_vec_dot_q4_0_q8_0}[wtype]
+         Q8_0: L.orc_vec_dot_q8_0_q8_0, Q4_0: L.orc_vec_dot_q4_0_q8_0, Q5_0: L.orc_vec_dot_q5_0_q8_0}[wtype]
     wrow = np.ascontiguousarray(wrow)
     xq_row = np.ascontiguousarray(xq_row)
     return float(f(k, _p(wrow), _p(xq_row)))

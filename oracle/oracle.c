@@ -28,6 +28,8 @@
  *  - Q5_K (GGML block_q5_K, restated; the reference holds no source for
  *    it): hand-built blocks whose single qh bit or nibble must land on the
  *    element dequantize_row_q5_K assigns it, and the unit-scale case.
+ *  - Q5_0 (GGML block_q5_0, restated): hand-built blocks whose single qh
+ *    bit or nibble must land on element j or j + 16 with value q - 16.
  *  - Q2_K and Q3_K (GGML block_q2_K / block_q3_K, restated; no source for
  *    them in the reference): hand-built blocks whose single 2-bit quant,
  *    hmask bit or scale must land on the element and sub-block
@@ -138,6 +140,7 @@ size_t orc_type_block_bytes(int type) {
     case ORC_Q6_K: return ORC_Q6K_BYTES;
     case ORC_Q8_0: return ORC_Q8_0_BYTES;
     case ORC_Q4_0: return ORC_Q4_0_BYTES;
+    case ORC_Q5_0: return ORC_Q5_0_BYTES;
     case ORC_Q8_K: return ORC_Q8K_BYTES;
     default: return 0;
     }
@@ -152,7 +155,8 @@ int64_t orc_type_block_elems(int type) {
     case ORC_Q6_K:
     case ORC_Q8_K: return ORC_QK_K;
     case ORC_Q8_0:
-    case ORC_Q4_0: return ORC_QK8_0;
+    case ORC_Q4_0:
+    case ORC_Q5_0: return ORC_QK8_0;
     default: return 0;
     }
 }
@@ -506,6 +510,32 @@ float orc_vec_dot_q4_0_q8_0(int64_t k, const uint8_t *w, const uint8_t *xq) {
     return sumf;
 }
 
+/* Q5_0 (GGML block_q5_0: f16 d @0, u32 qh @2, qs[16] @6; candle BlockQ5_0):
+ * element j < 16 = (qs[j] & 15) | (qh >> j & 1) << 4, element j + 16 =
+ * (qs[j] >> 4) | (qh >> (j + 16) & 1) << 4, each minus 16. */
+static int32_t q5_0_block_sum(const uint8_t *x, const uint8_t *y) {
+    const uint32_t qh = rd_u32(x + 2);
+    int32_t s = 0;
+    for (int j = 0; j < 16; j++) {
+        const int32_t v0 = (int32_t)((x[6 + j] & 0x0F) | (((qh >> j) & 1) << 4)) - 16;
+        const int32_t v1 = (int32_t)((x[6 + j] >> 4) | (((qh >> (j + 16)) & 1) << 4)) - 16;
+        s += v0 * (int32_t)(int8_t)y[2 + j] + v1 * (int32_t)(int8_t)y[2 + 16 + j];
+    }
+    return s;
+}
+
+/* BlockQ5_0::vec_dot_unopt (Q5_0 . Q8_0): sumf += (f32)sum_i * f16(d_w) * f16(d_x). */
+float orc_vec_dot_q5_0_q8_0(int64_t k, const uint8_t *w, const uint8_t *xq) {
+    int64_t nb = k / ORC_QK8_0;
+    float sumf = 0.0f;
+    for (int64_t b = 0; b < nb; b++) {
+        const uint8_t *x = w + b * ORC_Q5_0_BYTES;
+        const uint8_t *y = xq + b * ORC_Q8_0_BYTES;
+        sumf += (float)q5_0_block_sum(x, y) * orc_f16_to_f32(rd_u16(x)) * orc_f16_to_f32(rd_u16(y));
+    }
+    return sumf;
+}
+
 void orc_block_sums(int type, int64_t k, const uint8_t *w, const uint8_t *xq, int32_t *S,
                     int32_t *Smin) {
     int8_t aux8[256];
@@ -596,6 +626,12 @@ void orc_block_sums(int type, int64_t k, const uint8_t *w, const uint8_t *xq, in
             S[b] = s;
             if (Smin) Smin[b] = 0;
         }
+    } else if (type == ORC_Q5_0) {
+        int64_t nb = k / ORC_QK8_0;
+        for (int64_t b = 0; b < nb; b++) {
+            S[b] = q5_0_block_sum(w + b * ORC_Q5_0_BYTES, xq + b * ORC_Q8_0_BYTES);
+            if (Smin) Smin[b] = 0;
+        }
     } else if (type == ORC_Q8_0) {
         int64_t nb = k / ORC_QK8_0;
         for (int64_t b = 0; b < nb; b++) {
@@ -618,7 +654,7 @@ int orc_block_sums_mat(int type, int64_t m, int64_t n, int64_t k, const uint8_t 
     if (k <= 0 || k % wblk != 0 || m < 0 || n < 0) return -3;
     const int64_t nblk = k / wblk;
     const size_t row_w = (size_t)nblk * orc_type_block_bytes(type);
-    const int at = type == ORC_Q8_0 || type == ORC_Q4_0 ? ORC_Q8_0 : ORC_Q8_K;
+    const int at = type == ORC_Q8_0 || type == ORC_Q4_0 || type == ORC_Q5_0 ? ORC_Q8_0 : ORC_Q8_K;
     const size_t row_x = (size_t)(k / orc_type_block_elems(at)) * orc_type_block_bytes(at);
     if (nthreads <= 0) nthreads = orc_max_threads();
 #pragma omp parallel for schedule(dynamic, 64) num_threads(nthreads)
@@ -634,10 +670,10 @@ int orc_block_sums_mat(int type, int64_t m, int64_t n, int64_t k, const uint8_t 
 
 int orc_known_type(int type) {
     return type == ORC_Q2_K || type == ORC_Q3_K || type == ORC_Q4_K || type == ORC_Q5_K || type == ORC_Q6_K ||
-           type == ORC_Q8_0 || type == ORC_Q4_0;
+           type == ORC_Q8_0 || type == ORC_Q4_0 || type == ORC_Q5_0;
 }
 
-static int act_type_for(int type) { return type == ORC_Q8_0 || type == ORC_Q4_0 ? ORC_Q8_0 : ORC_Q8_K; }
+static int act_type_for(int type) { return type == ORC_Q8_0 || type == ORC_Q4_0 || type == ORC_Q5_0 ? ORC_Q8_0 : ORC_Q8_K; }
 
 static float vec_dot(int type, int64_t k, const uint8_t *w, const uint8_t *xq) {
     switch (type) {
@@ -646,6 +682,7 @@ static float vec_dot(int type, int64_t k, const uint8_t *w, const uint8_t *xq) {
     case ORC_Q4_K: return orc_vec_dot_q4k_q8k(k, w, xq);
     case ORC_Q5_K: return orc_vec_dot_q5k_q8k(k, w, xq);
     case ORC_Q4_0: return orc_vec_dot_q4_0_q8_0(k, w, xq);
+    case ORC_Q5_0: return orc_vec_dot_q5_0_q8_0(k, w, xq);
     case ORC_Q6_K: return orc_vec_dot_q6k_q8k(k, w, xq);
     default: return orc_vec_dot_q8_0_q8_0(k, w, xq);
     }
@@ -774,6 +811,19 @@ int orc_dequantize_row(int type, const uint8_t *w, int64_t k, float *out) {
             for (int j = 0; j < 16; j++) {
                 out[b * 32 + j] = (float)((int32_t)(x[2 + j] & 0x0F) - 8) * d;
                 out[b * 32 + j + 16] = (float)((int32_t)(x[2 + j] >> 4) - 8) * d;
+            }
+        }
+        return 0;
+    }
+    if (type == ORC_Q5_0) {
+        if (k % ORC_QK8_0) return -3;
+        for (int64_t b = 0; b < k / ORC_QK8_0; b++) {
+            const uint8_t *x = w + b * ORC_Q5_0_BYTES;
+            const uint32_t qh = rd_u32(x + 2);
+            float d = orc_f16_to_f32(rd_u16(x));
+            for (int j = 0; j < 16; j++) {
+                out[b * 32 + j] = (float)((int32_t)((x[6 + j] & 0x0F) | (((qh >> j) & 1) << 4)) - 16) * d;
+                out[b * 32 + j + 16] = (float)((int32_t)((x[6 + j] >> 4) | (((qh >> (j + 16)) & 1) << 4)) - 16) * d;
             }
         }
         return 0;

@@ -37,6 +37,7 @@ extern "C" {
 
 enum {
     ORC_Q4_0 = 2,
+    ORC_Q5_0 = 6,
     ORC_Q8_0 = 8,
     ORC_Q2_K = 10,
     ORC_Q3_K = 11,
@@ -55,6 +56,7 @@ enum {
 #define ORC_Q6K_BYTES 210
 #define ORC_Q8_0_BYTES 34
 #define ORC_Q4_0_BYTES 18
+#define ORC_Q5_0_BYTES 22
 #define ORC_Q8K_BYTES 292
 
 /* IEEE binary16 <-> binary32 as the `half` crate does it (RNE). */
@@ -80,6 +82,7 @@ float orc_vec_dot_q5k_q8k(int64_t k, const uint8_t *w, const uint8_t *xq);
 float orc_vec_dot_q6k_q8k(int64_t k, const uint8_t *w, const uint8_t *xq);
 float orc_vec_dot_q8_0_q8_0(int64_t k, const uint8_t *w, const uint8_t *xq);
 float orc_vec_dot_q4_0_q8_0(int64_t k, const uint8_t *w, const uint8_t *xq);
+float orc_vec_dot_q5_0_q8_0(int64_t k, const uint8_t *w, const uint8_t *xq);
 
 /* Integer intermediates per block (the bit-exact gate).
  * Q4_K, Q5_K: S[b] = sum_j sc_j * sum_{e in j} q_e*qx_e ; Smin[b] = sum_g bsums_g * m_{g/2}

@@ -17,7 +17,7 @@ pytestmark = pytest.mark.gpu
 
 def _xdeq_abs(x, wtype):
     xq = O.quantize(x, O.act_type(wtype))
-    if wtype in (O.Q8_0, O.Q4_0):
+    if wtype in (O.Q8_0, O.Q4_0, O.Q5_0):
         d, q = O.q8_0_fields(xq)
     else:
         d, q, _ = O.q8k_fields(xq)
@@ -192,7 +192,7 @@ def test_prefill_gemm_q6k_extreme_values(ctx):
 # ------------------------------------------------------ batch and K coverage
 @pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 7, 8, 11])
 @pytest.mark.parametrize("wtype", [S.TYPE_Q4_K, S.TYPE_Q5_K, S.TYPE_Q6_K, S.TYPE_Q8_0, S.TYPE_Q4_0, S.TYPE_Q2_K,
-                                   S.TYPE_Q3_K])
+                                   S.TYPE_Q3_K, S.TYPE_Q5_0])
 def test_batches(ctx, wtype, m):
     W = S.make_weight(wtype, 300, 2048, seed=m + wtype)
     x = S.make_activation(m, 2048, seed=100 + m)
@@ -201,7 +201,7 @@ def test_batches(ctx, wtype, m):
 
 @pytest.mark.parametrize("k", [256, 512, 5632, 16384, 20480])
 @pytest.mark.parametrize("wtype", [S.TYPE_Q4_K, S.TYPE_Q5_K, S.TYPE_Q6_K, S.TYPE_Q8_0, S.TYPE_Q4_0, S.TYPE_Q2_K,
-                                   S.TYPE_Q3_K])
+                                   S.TYPE_Q3_K, S.TYPE_Q5_0])
 @pytest.mark.parametrize("m", [1, 8])
 def test_k_coverage(ctx, wtype, k, m):
     W = S.make_weight(wtype, 70, k, seed=k + m)
@@ -318,6 +318,31 @@ def test_q4_0_extreme_values(ctx):
         check_matmul(ctx, W, x, cond=False)
 
 
+# ----------------------------- Q5_0 (matvec m <= 8, Q8_0 GEMM on a copy m > 8)
+@pytest.mark.parametrize("n,k,m", [(14336, 4096, 1), (4096, 14336, 8), (300, 96, 3), (1024, 2048, 64),
+                                   (300, 1056, 40)])
+def test_q5_0_matvec_and_gemm(ctx, n, k, m):
+    """Llama-3 FFN shapes of a Q5_0 file, rows whose block count is not a
+    multiple of 8 (padding blocks), and m > 8 through the Q8_0 GEMM on the
+    upload's expanded copy (values q - 16): block sums bit-exact."""
+    W = S.make_weight(S.TYPE_Q5_0, n, k, seed=n + k + 6)
+    x = S.make_activation(m, k, seed=m + k + 6)
+    check_matmul(ctx, W, x, cond=(k < 14336 and m <= 8))
+
+
+@pytest.mark.parametrize("qv,m", [(0, 2), (31, 2), (0, 20), (31, 20)])
+def test_q5_0_extreme_values(ctx, qv, m):
+    """Every quant 0 (value -16) or 31 (value 15) against activation blocks of
+    equal values, on the matvec (2 rows) and the GEMM (20 rows)."""
+    n, k = 64, 512
+    rng = np.random.default_rng(33)
+    W = S.make_weight(S.TYPE_Q5_0, n, k, seed=33)
+    W.q[:] = qv
+    W.blocks = S.pack_q5_0(W.d, W.q)
+    x = np.repeat(rng.standard_normal((m, k // 32)).astype(np.float32), 32, axis=1)
+    check_matmul(ctx, W, x, cond=False)
+
+
 # ------------------------------------------- Q2_K, Q3_K (matvec at any m)
 @pytest.mark.parametrize("wtype", [S.TYPE_Q2_K, S.TYPE_Q3_K])
 @pytest.mark.parametrize("n,k,m", [(14336, 4096, 1), (4096, 14336, 8), (5632, 2048, 1), (300, 2048, 20)])
@@ -409,7 +434,7 @@ def test_prefill_gemm_q8_0_subnormal_and_zero_scales(ctx):
 
 @pytest.mark.parametrize("m", [3, 20])
 @pytest.mark.parametrize("wtype", [S.TYPE_Q4_K, S.TYPE_Q5_K, S.TYPE_Q6_K, S.TYPE_Q8_0, S.TYPE_Q4_0, S.TYPE_Q2_K,
-                                   S.TYPE_Q3_K])
+                                   S.TYPE_Q3_K, S.TYPE_Q5_0])
 def test_subnormal_and_zero_scales(ctx, wtype, m):
     """f16 subnormal and zero d / dmin through the matvec (3 rows) and the
     GEMMs (20 rows)."""
@@ -425,6 +450,8 @@ def test_subnormal_and_zero_scales(ctx, wtype, m):
         W.blocks = S.pack_q6k(d, W.sc, W.q)
     elif wtype == S.TYPE_Q4_0:
         W.blocks = S.pack_q4_0(d, W.q)
+    elif wtype == S.TYPE_Q5_0:
+        W.blocks = S.pack_q5_0(d, W.q)
     elif wtype == S.TYPE_Q2_K:
         W.blocks = S.pack_q2k(d, d[:, ::-1].copy(), W.sc, W.mn, W.q)
         W.dmin = d[:, ::-1].copy()
@@ -470,7 +497,7 @@ def test_higher_rank_input_and_determinism(ctx):
 
 @pytest.mark.parametrize("wtype,m", [(S.TYPE_Q4_K, 4), (S.TYPE_Q6_K, 1), (S.TYPE_Q8_0, 8), (S.TYPE_Q4_K, 40),
                                      (S.TYPE_Q5_K, 3), (S.TYPE_Q5_K, 24), (S.TYPE_Q4_0, 2), (S.TYPE_Q2_K, 3),
-                                     (S.TYPE_Q3_K, 12)])
+                                     (S.TYPE_Q3_K, 12), (S.TYPE_Q5_0, 5), (S.TYPE_Q5_0, 40)])
 def test_device_pointer_entry_points(ctx, wtype, m):
     from arm_ai_amd import hip
 

@@ -127,9 +127,9 @@ def test_q8_0_known_answers():
 def _int_sums(W, xq, wtype):
     """S, Smin [m, n, nb] from the generator's element arrays (no unpacking)."""
     m = xq.shape[0]
-    if wtype in (O.Q8_0, O.Q4_0):
+    if wtype in (O.Q8_0, O.Q4_0, O.Q5_0):
         _, qx = O.q8_0_fields(xq)  # [m, nb, 32]
-        qw = W.q.astype(np.int64) - (8 if wtype == O.Q4_0 else 0)
+        qw = W.q.astype(np.int64) - {O.Q4_0: 8, O.Q5_0: 16}.get(wtype, 0)
         Sx = np.einsum("nbe,mbe->mnb", qw, qx.astype(np.int64))
         return Sx, np.zeros_like(Sx)
     _, qx, bs = O.q8k_fields(xq)  # [m, nb, 256], [m, nb, 16]
@@ -151,7 +151,7 @@ def _int_sums(W, xq, wtype):
     return Sx, np.zeros_like(Sx)
 
 
-WTYPES = [O.Q4_K, O.Q5_K, O.Q6_K, O.Q8_0, O.Q4_0, O.Q2_K, O.Q3_K]
+WTYPES = [O.Q4_K, O.Q5_K, O.Q6_K, O.Q8_0, O.Q4_0, O.Q2_K, O.Q3_K, O.Q5_0]
 
 
 @pytest.mark.parametrize("wtype", WTYPES)
@@ -180,7 +180,7 @@ def test_matmul_vs_f64_truth(wtype):
     W = S.make_weight(wtype, 96, k, seed=5)
     x = S.make_activation(2, k, seed=6)
     xq = O.quantize(x, O.act_type(wtype))
-    if wtype in (O.Q8_0, O.Q4_0):
+    if wtype in (O.Q8_0, O.Q4_0, O.Q5_0):
         dx, qx = O.q8_0_fields(xq)
     else:
         dx, qx, _ = O.q8k_fields(xq)
@@ -476,4 +476,22 @@ def test_q3k_hmask_bit_lands_on_element(hf, j, l):
     got = O.dequantize(O.Q3_K, _q3k_block(hmask=hm, qs=qs, scale_bytes=sb)[None], 256)[0]
     want = np.zeros(256)
     want[128 * hf + 32 * j + l] = 2.0 - 4.0
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("e", [0, 5, 15, 16, 22, 31])
+def test_q5_0_fifth_bit_and_nibble_land_on_element(e):
+    """GGML dequantize_row_q5_0: bit e of the u32 qh is bit 4 of element e;
+    qs[j] & 15 is element j, qs[j] >> 4 element j + 16; value d * (q - 16).
+    The block is built byte by byte: every quant 16 (value 0) except e."""
+    b = np.zeros(22, np.uint8)
+    b[0:2] = np.array([0.5], np.float16).view(np.uint8)
+    qh = np.uint32(0xFFFFFFFF) & ~np.uint32(1 << e)  # every fifth bit set (16) except e's
+    b[2:6] = np.array([qh], "<u4").view(np.uint8)
+    b[6:22] = 0
+    j, hi = e % 16, e >= 16
+    b[6 + j] = 0x70 if hi else 0x07  # e: q = 7 (fifth bit clear) -> value -9
+    got = O.dequantize(O.Q5_0, b[None], 32)[0]
+    want = np.zeros(32)
+    want[e] = 0.5 * (7 - 16)
     assert np.array_equal(got, want)
