@@ -134,6 +134,50 @@ def test_q5km_logits_and_graph_step_match_reference(tiny_q5km):
     assert toks_e == toks_g
 
 
+def _low_bit_types(cfg, layer):
+    """A Q3_K_M / Q2_K-style mix over the types with no fused two-weight
+    launch: Q3_K attention and FFN projections, Q5_0 wv, Q2_K wo, and w2
+    alternating Q2_K / Q5_0."""
+    from arm_ai_amd import synth
+
+    return {"wq": synth.TYPE_Q3_K, "wk": synth.TYPE_Q3_K, "wv": synth.TYPE_Q5_0, "wo": synth.TYPE_Q2_K,
+            "w1": synth.TYPE_Q3_K, "w3": synth.TYPE_Q3_K, "w2": synth.TYPE_Q2_K if layer % 2 else synth.TYPE_Q5_0}
+
+
+@pytest.mark.gpu
+def test_low_bit_types_logits_and_graph_step_match_reference():
+    """Prefill (GEMMs for Q5_0, matvec passes for Q2_K / Q3_K), eager decode
+    and the graph-captured decode step on Q2_K, Q3_K and Q5_0 weights."""
+    import torch
+
+    import arm_ai_amd as A
+    from arm_ai_amd.llama import Llama, synthetic_weights
+
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    hw = synthetic_weights(_tiny_cfg(), seed=17, types=_low_bit_types)
+    ctx = A.Context(0)
+    model = Llama(ctx, hw)
+    try:
+        ref = RefLlama(hw)
+        rng = np.random.default_rng(17)
+        prompt = rng.integers(0, hw.cfg.vocab, size=12).tolist()
+        g = model.forward(prompt, 0).cpu().numpy()
+        r = ref.forward(prompt, 0)
+        assert _rel(g, r) <= LOGIT_TOL, f"prefill logits rel {_rel(g, r):.3e}"
+        pos = len(prompt)
+        for step in range(2):
+            tok = int(rng.integers(0, hw.cfg.vocab))
+            g = model.forward([tok], pos).cpu().numpy()
+            r = ref.forward([tok], pos)
+            assert _rel(g, r) <= LOGIT_TOL, f"decode step {step} logits rel {_rel(g, r):.3e}"
+            pos += 1
+        assert model.generate(prompt, 6, graph=False).tokens == model.generate(prompt, 6, graph=True).tokens
+    finally:
+        model.free()
+        ctx.close()
+
+
 @pytest.mark.gpu
 def test_graph_decode_step_matches_eager(tiny):
     hw, model = tiny
