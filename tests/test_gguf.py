@@ -44,7 +44,8 @@ def test_round_trip_bytes_and_config(tmp_path):
     assert np.array_equal(hw.output.data, hw2.output.data) and hw2.output.shape == hw.output.shape
 
 
-@pytest.mark.parametrize("wtype", [synth.TYPE_Q4_K, synth.TYPE_Q5_K, synth.TYPE_Q6_K, synth.TYPE_Q8_0, synth.TYPE_Q4_0])
+@pytest.mark.parametrize("wtype", [synth.TYPE_Q4_K, synth.TYPE_Q5_K, synth.TYPE_Q6_K, synth.TYPE_Q8_0, synth.TYPE_Q4_0,
+                                   synth.TYPE_Q2_K, synth.TYPE_Q3_K, synth.TYPE_Q5_0])
 def test_dequantize_matches_element_formulas(wtype):
     W = synth.make_weight(wtype, 7, 512, seed=wtype)
     got = gguf.dequantize(wtype, W.blocks, 7 * 512).reshape(7, 512)
