@@ -82,8 +82,6 @@ SIGNATURES = {
     "aq_llama_silu_mul": (INT, [P, P, I64, P]),
     "aq_llama_attn_decode": (INT, [P, P, P, P, P, P, P, P, I64, I64, I64, I64, P]),
     "aq_llama_argmax": (INT, [P, P, I64, P, P, P, I64]),
-    "aq_stream_read_probe_out_words": (INT, []),
-    "aq_stream_read_probe": (INT, [P, P, ctypes.c_size_t, P]),
     "aq_qmatmul_rmsnorm_f32_device": (INT, [P, P, P, P, P, ctypes.c_float, I64, P, P]),
     "aq_qmatmul_silu_mul_f32_device": (INT, [P, P, P, I64, P]),
     "aq_qmatmul2_rmsnorm_f32_device": (INT, [P, P, P, P, P, P, ctypes.c_float, I64, P, P, P]),

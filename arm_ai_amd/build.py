@@ -2,7 +2,10 @@
 
 Run ``python -m arm_ai_amd.build`` (or ``__graft_entry__.build()``).  Every
 ``csrc/*.hip`` file is compiled with hipcc into ``_build/``, then linked into
-``arm_ai_amd/libarm_ai_amd.so`` in the source tree, next to the loader.
+``arm_ai_amd/libarm_ai_amd.so`` in the source tree, next to the loader.  The
+measurement aids in ``bench_aids/`` (read-only kernels bench.py times beside
+the matvec) go into a separate ``arm_ai_amd/libaq_bench.so``, so the product
+library exports only the ABI of include/aq.h.
 
 Flags: IEEE f32 arithmetic (no fast-math, no FMA contraction, so the
 activation quantizers divide and round exactly as the reference's Rust code
@@ -21,6 +24,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libarm_ai_amd.so")
+BENCH_AIDS = os.path.join(HERE, "bench_aids")
+BENCH_LIB = os.path.join(HERE, "libaq_bench.so")
 ARCH = os.environ.get("ARM_AI_AMD_ARCH", "gfx950")
 
 HIPCC_FLAGS = [
@@ -45,7 +50,7 @@ def hipcc() -> str:
 
 
 def _compile(src: str) -> str:
-    obj = os.path.join(BUILD, os.path.basename(src) + ".o")
+    obj = os.path.join(BUILD, os.path.relpath(src, HERE).replace(os.sep, "_") + ".o")
     cmd = [hipcc(), *HIPCC_FLAGS, "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
@@ -53,20 +58,26 @@ def _compile(src: str) -> str:
     return obj
 
 
-def build(verbose: bool = False) -> str:
-    os.makedirs(BUILD, exist_ok=True)
-    srcs = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
-    workers = min(len(srcs), max(1, (os.cpu_count() or 2) // 2), 8)
-    with cf.ThreadPoolExecutor(workers) as ex:
-        objs = list(ex.map(_compile, srcs))
-    tmp = LIB + ".tmp"
+def _link(objs: list[str], lib: str) -> None:
+    tmp = lib + ".tmp"
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
-        raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")
-    os.replace(tmp, LIB)
+        raise RuntimeError(f"link of {lib} failed:\n{r.stdout}\n{r.stderr}")
+    os.replace(tmp, lib)
+
+
+def build(verbose: bool = False) -> str:
+    os.makedirs(BUILD, exist_ok=True)
+    srcs = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
+    aids = sorted(glob.glob(os.path.join(BENCH_AIDS, "*.hip")))
+    workers = min(len(srcs) + len(aids), max(1, (os.cpu_count() or 2) // 2), 8)
+    with cf.ThreadPoolExecutor(workers) as ex:
+        objs = list(ex.map(_compile, srcs + aids))
+    _link(objs[:len(srcs)], LIB)
+    _link(objs[len(srcs):], BENCH_LIB)
     if verbose:
-        print(f"built {LIB}")
+        print(f"built {LIB} and {BENCH_LIB}")
     return LIB
 
 

@@ -906,17 +906,6 @@ int aq_llama_attn_decode(aq_ctx *ctx, const float *d_qk, const float *d_v, const
                       "attn_decode");
 }
 
-int aq_stream_read_probe_out_words(void) { return stream_read_grid(); }
-
-int aq_stream_read_probe(aq_ctx *ctx, const void *d_buf, size_t bytes, uint32_t *d_out) {
-    if (!ctx) return fail(AQ_ERR_INVALID_ARG, "null context");
-    if (!d_buf || !d_out) return fail(AQ_ERR_INVALID_ARG, "null pointer");
-    if (bytes < 16 || (bytes & 15) || ((uintptr_t)d_buf & 15))
-        return fail(AQ_ERR_INVALID_ARG, "buffer must be 16-byte aligned and a multiple of 16 bytes");
-    int rc = use_device(ctx->device);
-    if (rc) return rc;
-    return hip_status(launch_stream_read(d_buf, bytes, d_out, ctx->stream), "stream_read_probe");
-}
 
 int aq_llama_argmax(aq_ctx *ctx, const float *d_x, int64_t n, int64_t *d_tok, int64_t *d_pos, int64_t *d_hist,
                     int64_t hist_len) {

@@ -140,17 +140,18 @@ hipError_t launch_repack(int type, const uint8_t *src, int64_t n, int64_t k, uin
 // layout holding the values (q - 8, q - 16) as int8 and the same f16 d (what
 // the Q8_0 GEMM reads).  Padding is not written: zero the tiles beforehand.
 hipError_t launch_expand_q80(int type, const uint8_t *src, int64_t n, int64_t k, uint8_t *dst_slab, hipStream_t s);
-// Measurement aid (k_probe.hip): stream `bytes` of buf (16-byte aligned, a
-// multiple of 16) through a read-only kernel; out needs stream_read_grid()
-// entries.
-int stream_read_grid();
-hipError_t launch_stream_read(const void *buf, size_t bytes, uint32_t *out, hipStream_t s);
 // Decode matvec (any m; batch rows are processed up to 8 at a time).  The
 // activation is either f32 (x != nullptr: quantised inside the kernel,
 // bit-identical to the quantizer kernels) or pre-quantised planes.
 // S/Smin non-null selects the integer-dump variant ([m][n][blocks] int32).
 hipError_t launch_matvec(const WLayout &w, int64_t n, int64_t k, const float *x, const ActPlanes *act, int64_t m,
                          float *y, int32_t *S, int32_t *Smin, hipStream_t s);
+// Batch-1 Q4_K matvec with one weight row per lane (k_rowlane.hip), for
+// weights with many rows and k <= 8192; hipErrorNotSupported for other shapes.
+// x (f32, quantised in the kernel) or act (pre-quantised planes of one row).
+bool rowlane_matvec_applies(int type, int64_t n, int64_t k);
+hipError_t launch_rowlane_matvec(const WLayout &w, int64_t n, int64_t k, const float *x, const ActPlanes *act,
+                                 float *y, int32_t *S, int32_t *Smin, hipStream_t s);
 // Matvec of pre-quantised (Q8_K) rows on the int8 matrix cores, 8 rows per
 // launch, Q4_K / Q6_K weights, k <= mmv_max_k().  Returns hipErrorNotSupported
 // for other types and shapes (the caller then uses launch_matvec).

@@ -911,6 +911,10 @@ hipError_t matvec_impl(const WLayout &w, int64_t n, int64_t k, const float *x, c
     if ((S == nullptr) != (Smin == nullptr)) return hipErrorInvalidValue;
     if (m == 0) return hipSuccess;
     if (xa.xf != XF_NONE && (m != 1 || !x || S || (xa.xf == XF_NORM && !xa.norm))) return hipErrorInvalidValue;
+    if (m == 1 && xa.xf == XF_NONE && rowlane_matvec_applies(type, n, k)) {
+        const hipError_t e = launch_rowlane_matvec(w, n, k, x, act, y, S, Smin, s);
+        if (e != hipErrorNotSupported) return e;
+    }
     const int ng = w.ng;
     if ((size_t)ng * REC > LDS_CAP) return hipErrorNotSupported;  // k > 124160
     if ((int64_t)8 * n * 4 >= ((int64_t)1 << 31)) return hipErrorNotSupported;  // y of a pass: 32-bit buffer offsets

@@ -287,15 +287,6 @@ int aq_qmatmul2_rmsnorm_f32_device(aq_ctx *ctx, const aq_qweight *w1, const aq_q
 int aq_llama_argmax(aq_ctx *ctx, const float *d_x, int64_t n, int64_t *d_tok, int64_t *d_pos, int64_t *d_hist,
                     int64_t hist_len);
 
-/* ---- measurement aid (no counterpart in the reference) ----
- * Streams d_buf (16-byte aligned, bytes a multiple of 16) through a kernel
- * that only reads it, asynchronously on the context stream.  bench.py times
- * it on the headline's byte count to report the read rate a read-only kernel
- * reaches on this GPU beside the matvec's.  d_out: device memory for
- * aq_stream_read_probe_out_words() uint32 values (almost never written). */
-int aq_stream_read_probe_out_words(void);
-int aq_stream_read_probe(aq_ctx *ctx, const void *d_buf, size_t bytes, uint32_t *d_out);
-
 #ifdef __cplusplus
 }
 #endif

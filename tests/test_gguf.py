@@ -138,3 +138,92 @@ def test_loaded_model_gives_the_same_logits(tmp_path):
     a.free()
     b.free()
     ctx.close()
+
+
+# ---------------------------------------------------------------- a byte stream built from the spec
+# The file below is assembled field by field with struct.pack from the public
+# GGUF specification (ggml docs/gguf.md), without write_gguf, so a reader and
+# writer that shared a misreading (count widths, dims order, alignment padding,
+# array encoding) cannot pass together.
+def _spec_str(s: bytes) -> bytes:
+    return struct.pack("<Q", len(s)) + s
+
+
+def _spec_kv(key: bytes, vtype: int, payload: bytes) -> bytes:
+    return _spec_str(key) + struct.pack("<I", vtype) + payload
+
+
+def _spec_file(version: int, alignment: int | None, pad_byte: int = 0):
+    """A two-tensor GGUF byte string and what a correct reader must find in it."""
+    W = synth.make_weight(synth.TYPE_Q4_K, 3, 512, seed=31)  # n = 3 rows, k = 512 columns
+    norm = np.array([1.5, -2.0, 0.25, 8.0, 0.0, -0.125], "<f4")
+    kvs = [
+        _spec_kv(b"general.architecture", gguf.T_STR, _spec_str(b"llama")),
+        _spec_kv(b"t.u8", gguf.T_U8, struct.pack("<B", 200)),
+        _spec_kv(b"t.i8", gguf.T_I8, struct.pack("<b", -100)),
+        _spec_kv(b"t.u16", gguf.T_U16, struct.pack("<H", 65000)),
+        _spec_kv(b"t.i16", gguf.T_I16, struct.pack("<h", -32000)),
+        _spec_kv(b"t.i32", gguf.T_I32, struct.pack("<i", -7)),
+        _spec_kv(b"t.f64", gguf.T_F64, struct.pack("<d", 0.1)),
+        _spec_kv(b"t.u64", gguf.T_U64, struct.pack("<Q", 2 ** 40 + 3)),
+        _spec_kv(b"t.i64", gguf.T_I64, struct.pack("<q", -(2 ** 40))),
+        _spec_kv(b"t.bool", gguf.T_BOOL, struct.pack("<B", 1)),
+        # typed arrays: (element type u32, count u64, elements)
+        _spec_kv(b"t.arr_i16", gguf.T_ARR, struct.pack("<IQ", gguf.T_I16, 3) + struct.pack("<3h", -1, 2, -3)),
+        _spec_kv(b"t.arr_f32", gguf.T_ARR, struct.pack("<IQ", gguf.T_F32, 2) + struct.pack("<2f", 0.5, -4.0)),
+        _spec_kv(b"t.arr_str", gguf.T_ARR, struct.pack("<IQ", gguf.T_STR, 2) + _spec_str(b"<s>") + _spec_str(b"\xc3\xa9")),
+    ]
+    if alignment is not None:
+        kvs.append(_spec_kv(b"general.alignment", gguf.T_U32, struct.pack("<I", alignment)))
+    align = alignment or 32
+    # tensor 0: the 1-D norm at offset 0; tensor 1: the weight at the next aligned offset
+    off1 = (norm.nbytes + align - 1) // align * align
+    infos = (_spec_str(b"blk.0.attn_norm.weight") + struct.pack("<I", 1) + struct.pack("<Q", 6)
+             + struct.pack("<IQ", gguf.GGML_F32, 0)
+             + _spec_str(b"blk.0.attn_q.weight") + struct.pack("<I", 2) + struct.pack("<2Q", 512, 3)
+             + struct.pack("<IQ", synth.TYPE_Q4_K, off1))
+    head = b"GGUF" + struct.pack("<IQQ", version, 2, len(kvs)) + b"".join(kvs) + infos
+    data_start = (len(head) + align - 1) // align * align
+    body = bytearray(head + bytes([pad_byte]) * (data_start - len(head)))
+    body += norm.tobytes() + bytes([pad_byte]) * (off1 - norm.nbytes) + W.blocks.tobytes()
+    return bytes(body), data_start, off1, W, norm
+
+
+@pytest.mark.parametrize("version,alignment", [(3, 64), (2, 64), (3, None), (3, 256)])
+def test_reader_against_a_spec_built_file(tmp_path, version, alignment):
+    raw, data_start, off1, W, norm = _spec_file(version, alignment, pad_byte=0xAA)
+    p = tmp_path / "spec.gguf"
+    p.write_bytes(raw)
+    g = gguf.GGUFFile(str(p))
+    assert g.version == version
+    assert g.data_start == data_start and data_start % (alignment or 32) == 0
+    md = g.metadata
+    assert md["general.architecture"] == "llama"
+    assert (md["t.u8"], md["t.i8"], md["t.u16"], md["t.i16"], md["t.i32"]) == (200, -100, 65000, -32000, -7)
+    assert md["t.f64"] == 0.1 and md["t.u64"] == 2 ** 40 + 3 and md["t.i64"] == -(2 ** 40) and md["t.bool"] is True
+    assert md["t.arr_i16"].dtype == np.dtype("<i2") and list(md["t.arr_i16"]) == [-1, 2, -3]
+    assert md["t.arr_f32"].dtype == np.dtype("<f4") and list(md["t.arr_f32"]) == [0.5, -4.0]
+    assert md["t.arr_str"] == ["<s>", "é"]
+    if alignment is not None:
+        assert md["general.alignment"] == alignment
+    tn, tq = g.tensor("blk.0.attn_norm.weight"), g.tensor("blk.0.attn_q.weight")
+    assert (tn.dims, tn.type, tn.offset) == ((6,), gguf.GGML_F32, 0)
+    assert (tq.dims, tq.type, tq.offset) == ((512, 3), synth.TYPE_Q4_K, off1)
+    assert tq.shape == (3, 512) and tq.nbytes == 3 * 2 * 144
+    # the bytes at data_start + offset, not at the end of the infos
+    assert np.array_equal(g.f32("blk.0.attn_norm.weight"), norm)
+    q = g.qtensor("blk.0.attn_q.weight")
+    assert q.shape == (3, 512) and np.array_equal(np.asarray(q.data).reshape(-1), W.blocks.reshape(-1))
+    assert np.array_equal(np.asarray(g.raw("blk.0.attn_q.weight")), np.frombuffer(raw, np.uint8)[data_start + off1:])
+
+
+def test_spec_built_file_rejects_bad_alignment_and_short_data(tmp_path):
+    raw, data_start, off1, _, _ = _spec_file(3, 48)  # not a power of two
+    p = tmp_path / "a48.gguf"
+    p.write_bytes(raw)
+    with pytest.raises(gguf.GGUFError, match="alignment"):
+        gguf.GGUFFile(str(p))
+    raw, *_ = _spec_file(3, 64)
+    p.write_bytes(raw[:-1])  # the weight's last byte is missing
+    with pytest.raises(gguf.GGUFError, match="past the end"):
+        gguf.GGUFFile(str(p))

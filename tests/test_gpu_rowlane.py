@@ -1,0 +1,131 @@
+"""GPU parity of the batch-1 Q4_K matvec with one weight row per lane
+(csrc/k_rowlane.hip), the path a single activation row takes on a Q4_K
+weight of at least 11200 rows and k <= 8192 (Llama-3-8B ffn_up / ffn_gate).
+
+Against the oracle (candle-core 0.8.4 k_quants::matmul restated): every
+integer block sum S and Smin bit-exact, outputs within max relative error
+1e-5; the in-kernel Q8_K quantisation (16 lanes per block) must give the
+same bytes as the quantizer kernel, which the edge rows check through the
+integer sums (a quant that differs changes S or Smin).
+"""
+import numpy as np
+import pytest
+
+import arm_ai_amd as A
+import oracle as O
+from arm_ai_amd import synth as S
+from tests.test_gpu_parity import _edge_rows, _xdeq_abs, check_matmul
+
+pytestmark = pytest.mark.gpu
+
+RL_MIN_N = 11200  # rows from which a one-row Q4_K matvec takes the row-per-lane kernel
+
+
+@pytest.mark.parametrize("n,k", [
+    (14336, 4096),   # the headline shape: 256 workgroups of 56 rows, two groups per wavefront
+    (RL_MIN_N, 256),  # one group: a single quantising wavefront
+    (11203, 2048),   # ragged: the last workgroup's rows and its last row block are partial
+    (11264, 5632),   # 22 groups: three groups per wavefront, some wavefronts short
+    (12000, 8192),   # 32 groups: four per wavefront, every wavefront quantises
+])
+def test_rowlane_matches_oracle(ctx, n, k):
+    W = S.make_weight(S.TYPE_Q4_K, n, k, seed=n + k)
+    x = S.make_activation(1, k, seed=k)
+    check_matmul(ctx, W, x)
+
+
+def test_rowlane_edge_activations(ctx):
+    """Zeros, 1e-30, 1e30, equal values (first max), exact ties (rounding away
+    from zero), NaN and f32 subnormals through the in-kernel quantisation."""
+    k = 4096
+    W = S.make_weight(S.TYPE_Q4_K, RL_MIN_N, k, seed=77)
+    mm = A.QMatMul.from_qtensor(A.QTensor(W.type, (W.n, W.k), W.blocks), ctx)
+    for x in _edge_rows(k):
+        x = x[None, :]
+        xq = O.quantize(x, O.Q8_K)
+        gS, gSm = mm.block_sums(x)
+        oS, oSm = O.block_sums(W.type, k, W.blocks, xq)
+        assert np.array_equal(gS, oS) and np.array_equal(gSm, oSm)
+        y = mm.forward(x)
+        r = O.matmul_preq(W.type, xq, W.blocks, W.n, k)
+        ok = np.isfinite(r)
+        assert np.array_equal(np.isfinite(y), ok)
+        if ok.any():
+            scale = max(float(np.abs(r[ok]).max()), 1e-30)
+            assert float(np.abs(y[ok] - r[ok]).max()) / scale <= 1e-5
+    mm.free()
+
+
+def test_rowlane_extreme_values(ctx):
+    """Every quant 15, every scale and min 63: the largest integer sums the
+    kernel forms, bit-exact.  The f32 output is held to 1e-5 of the f64 value
+    of those exact sums; against the oracle it is held to the conditioning-
+    aware bar (rel_cond), because here candle's own summation order (the
+    oracle's) is 3.4e-5 away from the exact value in rel_max terms."""
+    from tests._metrics import rel_cond
+
+    n, k = RL_MIN_N, 4096
+    W = S.make_weight(S.TYPE_Q4_K, n, k, seed=5)
+    W.q[:] = 15
+    W.sc[:] = 63
+    W.mn[:] = 63
+    W.blocks = S.pack_q4k(W.d, W.dmin, W.sc, W.mn, W.q)
+    # every block's first element (-1) is its max: quants -128 and, after the
+    # clamp of +128, +127
+    x = np.full((1, k), -1.0, np.float32)
+    x[0, 1::2] = 1.0
+    mm = A.QMatMul.from_qtensor(A.QTensor(W.type, (n, k), W.blocks), ctx)
+    xq = O.quantize(x, O.Q8_K)
+    gS, gSm = mm.block_sums(x)
+    oS, oSm = O.block_sums(W.type, k, W.blocks, xq)
+    assert np.array_equal(gS, oS) and np.array_equal(gSm, oSm)
+    y = mm.forward(x)[0].astype(np.float64)
+    dx = O.q8k_fields(xq)[0].astype(np.float64)[0]
+    exact = (W.d.astype(np.float64) * dx * oS[0] - W.dmin.astype(np.float64) * dx * oSm[0]).sum(axis=1)
+    assert np.abs(y - exact).max() <= 1e-5 * np.abs(exact).max()
+    r = O.matmul_preq(W.type, xq, W.blocks, n, k)
+    _, xabs = _xdeq_abs(x, W.type)
+    assert rel_cond(y[None, :], r, W, xabs) <= 1e-5
+    mm.free()
+
+
+def test_rowlane_device_and_prequantised_entries(ctx):
+    """The f32 device entry, the pre-quantised entry and the host entry give
+    the same bits at the headline shape."""
+    from arm_ai_amd import hip
+
+    n, k = 14336, 4096
+    W = S.make_weight(S.TYPE_Q4_K, n, k, seed=21)
+    x = S.make_activation(1, k, seed=22)
+    mm = A.QMatMul.from_qtensor(A.QTensor(W.type, (n, k), W.blocks), ctx)
+    y_host = mm.forward(x)
+    dx = hip.to_device(x)
+    dy = hip.DeviceBuffer(n * 4)
+    mm.forward_device(dx.ptr, 1, dy.ptr)
+    act = hip.DeviceBuffer(A.act_bytes(mm.act_type, 1, k))
+    A.quantize_act_device(ctx, mm.act_type, dx.ptr, 1, k, act.ptr)
+    dy2 = hip.DeviceBuffer(n * 4)
+    mm.forward_preq_device(act.ptr, 1, dy2.ptr)
+    ctx.synchronize()
+    assert np.array_equal(dy.download(np.float32, (1, n)), y_host)
+    assert np.array_equal(dy2.download(np.float32, (1, n)), y_host)
+    mm.free()
+
+
+def test_rowlane_and_general_matvec_agree(ctx):
+    """The same rows through the row-per-lane kernel (n >= 11200) and through
+    the general matvec (the first 11192 rows as a weight of their own): the
+    integer sums are identical and the outputs agree to the tolerance."""
+    k = 2048
+    W = S.make_weight(S.TYPE_Q4_K, RL_MIN_N, k, seed=31)
+    x = S.make_activation(1, k, seed=32)
+    big = A.QMatMul.from_qtensor(A.QTensor(W.type, (W.n, k), W.blocks), ctx)
+    n2 = RL_MIN_N - 8
+    small = A.QMatMul.from_qtensor(A.QTensor(W.type, (n2, k), W.blocks[:n2]), ctx)
+    sb, smb = big.block_sums(x)
+    ss, sms = small.block_sums(x)
+    assert np.array_equal(sb[:, :n2], ss) and np.array_equal(smb[:, :n2], sms)
+    yb, ys = big.forward(x), small.forward(x)
+    assert float(np.abs(yb[:, :n2] - ys).max()) <= 1e-5 * float(np.abs(ys).max())
+    big.free()
+    small.free()
