@@ -50,6 +50,8 @@ SIGNATURES = {
     "aq_qweight_info": (INT, [P, ctypes.POINTER(INT), ctypes.POINTER(I64), ctypes.POINTER(I64), ctypes.POINTER(SZ)]),
     "aq_qmatmul_f32": (INT, [P, P, P, I64, I64, P]),
     "aq_qmatmul_f32_device": (INT, [P, P, P, I64, I64, P]),
+    "aq_qmatmul_f32_device_noalloc": (INT, [P, P, P, I64, I64, P]),
+    "aq_fixed_scratch_bytes": (SZ, []),
     "aq_act_bytes": (SZ, [INT, I64, I64]),
     "aq_quantize_act_device": (INT, [P, INT, P, I64, I64, P]),
     "aq_qmatmul_preq_device": (INT, [P, P, P, I64, I64, P]),

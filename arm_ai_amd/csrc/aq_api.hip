@@ -15,6 +15,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <new>
 #include <string>
 
@@ -30,7 +31,15 @@ struct aq_ctx {
     size_t scratch_bytes = 0;
     void *pinned = nullptr;  // host staging, grow-only
     size_t pinned_bytes = 0;
+    void *fixed_scratch = nullptr;  // this device's copy of g_fixed_scratch (its device address)
 };
+
+// Scratch of aq_qmatmul_f32_device_noalloc: a fixed array in the library's
+// device image, one copy per GPU (held until the process ends).  Its name is
+// only a host-side handle: device code receives the address that
+// hipGetSymbolAddress returns for the current device (fixed_scratch_of).
+constexpr size_t FIXED_SCRATCH_BYTES = (size_t)32 << 20;
+static __device__ __align__(256) uint8_t g_fixed_scratch[FIXED_SCRATCH_BYTES];
 
 struct aq_qweight {
     int type = 0;
@@ -96,6 +105,27 @@ int use_device(int device) {
     int cur = -1;
     if (hipGetDevice(&cur) == hipSuccess && cur == device) return AQ_OK;
     HIP_TRY(hipSetDevice(device));
+    return AQ_OK;
+}
+
+// The device address of g_fixed_scratch on `device`, looked up once per
+// device with that device current (aq_ctx_create makes it current).
+constexpr int MAX_DEVICES = 64;
+std::mutex g_fixed_mu;
+void *g_fixed_ptr[MAX_DEVICES] = {};
+int fixed_scratch_of(int device, void **out) {
+    if (device < 0 || device >= MAX_DEVICES) return fail(AQ_ERR_NO_DEVICE, "device %d beyond the fixed-scratch table", device);
+    std::lock_guard<std::mutex> lk(g_fixed_mu);
+    if (!g_fixed_ptr[device]) {
+        void *p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(g_fixed_scratch));
+        if (e != hipSuccess || !p) {
+            (void)hipGetLastError();
+            return fail(AQ_ERR_HIP, "hipGetSymbolAddress of the fixed scratch failed: %s", hipGetErrorString(e));
+        }
+        g_fixed_ptr[device] = p;
+    }
+    *out = g_fixed_ptr[device];
     return AQ_OK;
 }
 
@@ -247,9 +277,12 @@ int aq_ctx_create(int device, aq_ctx **out) {
     if (device < 0 || device >= n) return fail(AQ_ERR_NO_DEVICE, "device %d out of range (%d visible)", device, n);
     int rc = use_device(device);
     if (rc) return rc;
+    void *fixed = nullptr;
+    if ((rc = fixed_scratch_of(device, &fixed))) return rc;
     aq_ctx *c = new (std::nothrow) aq_ctx();
     if (!c) return fail(AQ_ERR_OOM, "out of host memory");
     c->device = device;
+    c->fixed_scratch = fixed;
     if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {
         delete c;
         return fail(AQ_ERR_HIP, "hipStreamCreateWithFlags failed");
@@ -450,6 +483,25 @@ int aq_qmatmul_f32_device(aq_ctx *ctx, const aq_qweight *w, const float *d_lhs, 
     uint8_t *S = (uint8_t *)ctx->scratch;
     return run_matmul(ctx, w, d_lhs, m, d_dst, S + L.act, nullptr, nullptr, S + L.ws, L.total - L.ws);
 }
+
+int aq_qmatmul_f32_device_noalloc(aq_ctx *ctx, const aq_qweight *w, const float *d_lhs, int64_t m, int64_t k,
+                                  float *d_dst) {
+    int rc = check_mm(ctx, w, m, k);
+    if (rc) return rc;
+    if (m == 0) return AQ_OK;
+    if (!d_lhs || !d_dst) return fail(AQ_ERR_INVALID_ARG, "null lhs or dst");
+    if (!ctx->fixed_scratch) return fail(AQ_ERR_INVALID_ARG, "context has no fixed scratch");
+    if ((rc = use_device(ctx->device))) return rc;
+    const bool gemm = use_gemm(w, m);
+    CallLayout L = call_layout(w, m, false, false, gemm);
+    if (L.total > FIXED_SCRATCH_BYTES)
+        return fail(AQ_ERR_SHAPE, "m=%lld needs %zu bytes of scratch, more than the fixed %zu; use aq_qmatmul_f32_device",
+                    (long long)m, L.total, FIXED_SCRATCH_BYTES);
+    uint8_t *S = (uint8_t *)ctx->fixed_scratch;
+    return run_matmul(ctx, w, d_lhs, m, d_dst, S + L.act, nullptr, nullptr, S + L.ws, L.total - L.ws);
+}
+
+size_t aq_fixed_scratch_bytes(void) { return FIXED_SCRATCH_BYTES; }
 
 size_t aq_act_bytes(int act_type, int64_t m, int64_t k) {
     if ((act_type != AQ_TYPE_Q8_K && act_type != AQ_TYPE_Q8_0) || m < 0 || k <= 0) return 0;

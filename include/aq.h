@@ -110,6 +110,19 @@ int aq_qmatmul_f32(aq_ctx *ctx, const aq_qweight *w, const float *lhs, int64_t m
 int aq_qmatmul_f32_device(aq_ctx *ctx, const aq_qweight *w, const float *d_lhs, int64_t m,
                           int64_t k, float *d_dst);
 
+/* aq_qmatmul_f32_device without any allocation (no counterpart in the
+ * reference): for callers that cannot allocate device memory during a call,
+ * such as code under HIP graph capture or a serving loop that forbids
+ * hipMalloc.  The quantised activation and the prefill GEMM's workspace live
+ * in a fixed array of aq_fixed_scratch_bytes() (32 MiB) per GPU, held until
+ * the process ends; a call whose m, k and n need more returns AQ_ERR_SHAPE
+ * (aq_qmatmul_f32_device has no such limit).  Every call on one GPU shares
+ * that array, so calls that overlap on one GPU (two streams, two threads)
+ * race: serialise them.  Same results as aq_qmatmul_f32_device. */
+int aq_qmatmul_f32_device_noalloc(aq_ctx *ctx, const aq_qweight *w, const float *d_lhs, int64_t m, int64_t k,
+                                  float *d_dst);
+size_t aq_fixed_scratch_bytes(void);
+
 /* Quantise-once / reuse.  candle's quantized_llama feeds the same input to
  * several QMatMuls (wq/wk/wv, w1/w3), each quantising it again inside
  * k_quants::matmul; these two calls let a caller quantise once on the device
