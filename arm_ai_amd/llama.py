@@ -45,6 +45,7 @@ trip.
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import math
 import time
@@ -126,24 +127,28 @@ class HostWeights:
 
 
 def synthetic_weights(cfg: LlamaConfig, seed: int = 0, types=tinyllama_q4km_types,
-                      output_type: int = synth.TYPE_Q6_K) -> HostWeights:
+                      output_type: int = synth.TYPE_Q6_K, unit: bool = False) -> HostWeights:
     """Random weights of the given architecture (block value distributions of
-    arm_ai_amd.synth; embedding ~ N(0, 1); norm weights ~ 1 + N(0, 0.05))."""
+    arm_ai_amd.synth.make_weight, or with unit=True synth.make_weight_unit,
+    whose values are centred and scaled by 1/sqrt(k) so activations stay of
+    order one through every layer; embedding ~ N(0, 1); norm weights ~
+    1 + N(0, 0.05))."""
     rng = np.random.default_rng(seed)
     hw = HostWeights(cfg)
     shapes = weight_shapes(cfg)
+    make = synth.make_weight_unit if unit else synth.make_weight
     for layer in range(cfg.n_layer):
         t = types(cfg, layer)
         qt = {}
         for name, (n, k) in shapes.items():
-            w = synth.make_weight(t[name], n, k, rng=rng)
+            w = make(t[name], n, k, rng=rng)
             qt[name] = QTensor(t[name], (n, k), w.blocks)
         hw.layers.append(qt)
         hw.attn_norm.append((1.0 + 0.05 * rng.standard_normal(cfg.hidden)).astype(np.float32))
         hw.ffn_norm.append((1.0 + 0.05 * rng.standard_normal(cfg.hidden)).astype(np.float32))
     hw.tok_embeddings = rng.standard_normal((cfg.vocab, cfg.hidden), dtype=np.float32)
     hw.norm = (1.0 + 0.05 * rng.standard_normal(cfg.hidden)).astype(np.float32)
-    w = synth.make_weight(output_type, cfg.vocab, cfg.hidden, rng=rng)
+    w = make(output_type, cfg.vocab, cfg.hidden, rng=rng)
     hw.output = QTensor(output_type, (cfg.vocab, cfg.hidden), w.blocks)
     return hw
 
@@ -210,6 +215,9 @@ class Llama:
         self.ctx.synchronize()
         self._n_second = {"wqk": cfg.n_kv_head * cfg.head_dim, "w13": cfg.ffn}
         self._graph = None
+        self._trace = None  # (rows, full layers, records) while trace_matmuls is active
+        self._trace_layer = -1
+        self._hidden = None  # {layer index: residual input} while capture_hidden is active
 
     def _upload_layer(self, layer: dict[str, QTensor]) -> dict[str, QMatMul]:
         """The layer's projections in HBM; wq|wk and w1|w3 become one weight each
@@ -261,7 +269,45 @@ class Llama:
         x = x.contiguous()
         y = torch.empty((x.shape[0], w.n), dtype=torch.float32, device=self.dev)
         w.forward_device(x.data_ptr(), x.shape[0], y.data_ptr())
+        if self._trace is not None:
+            rows, full, records = self._trace
+            if self._trace_layer in full:
+                sel = list(range(x.shape[0]))
+            else:
+                sel = [r for r in rows if r < x.shape[0]] or [0]
+            records.append((self._trace_layer, w, x[sel].cpu().numpy(), y[sel].cpu().numpy(), sel))
         return y
+
+    @contextlib.contextmanager
+    def capture_hidden(self, layers):
+        """Record the residual stream [L, hidden] that forward() feeds to each
+        of the given layers (index n_layer: the stream after the last layer),
+        copied to the host: a test aid."""
+        rec = {"layers": set(layers), "x": {}}
+        self._hidden = rec
+        try:
+            yield rec["x"]
+        finally:
+            self._hidden = None
+
+    def _record_hidden(self, li, x):
+        if self._hidden is not None and li in self._hidden["layers"]:
+            self._hidden["x"][li] = x.cpu().numpy()
+
+    @contextlib.contextmanager
+    def trace_matmuls(self, rows=(0,), full_layers=()):
+        """Record every QMatMul::forward made by forward() inside the block:
+        yields a list that receives (layer, QMatMul, x rows, y rows, row
+        indices) per call (layer n_layer: the output head), for the rows
+        given (those below the call's m; row 0 when none is), or every row
+        for the layers in full_layers.  A test aid: each record is copied to
+        the host as it is made, which synchronises the stream."""
+        records = []
+        self._trace = (tuple(rows), set(full_layers), records)
+        try:
+            yield records
+        finally:
+            self._trace = None
 
     def _rms_norm(self, x, w):
         torch = self.torch
@@ -321,6 +367,8 @@ class Llama:
                 mask = j > (i + index_pos)
             x = self.tok_embeddings[tokens]
             for li, lw in enumerate(self.layers):
+                self._trace_layer = li
+                self._record_hidden(li, x)
                 n = self._rms_norm(x, self.attn_norm[li])
                 q, k = self._pair(lw, "wqk", "wq", "wk", n)
                 q = self._rope(q.reshape(L, H, D), cos, sin)
@@ -330,6 +378,8 @@ class Llama:
                 self.v_cache[li, :, index_pos:end] = v.transpose(0, 1)
                 y = self._attend(q.transpose(0, 1), self.k_cache[li, :, :end], self.v_cache[li, :, :end], mask)
                 x = self._layer_tail(li, x, y.transpose(0, 1).reshape(L, H * D))
+            self._trace_layer = len(self.layers)
+            self._record_hidden(len(self.layers), x)
             last = self._rms_norm(x[L - 1:L], self.norm)
             logits = self._mm(self.output, last)[0]
         self._leave()

@@ -297,6 +297,76 @@ def make_weight(type_: int, n: int, k: int, seed: int = 0, rng: np.random.Genera
     raise ValueError(f"unsupported weight type {type_}")
 
 
+def make_weight_unit(type_: int, n: int, k: int, seed: int = 0, rng: np.random.Generator | None = None) -> QWeight:
+    """A random weight whose dequantised values have mean about 0 and standard
+    deviation about 1/sqrt(k), so a stack of layers keeps activations of order
+    one (the block distributions of make_weight give every element a mean of
+    about +3, which saturates a deep model).  Same block formats:
+
+    * Q4_K / Q5_K: sub-block scales sc ~ U[1, 8], mins m = round(sc * mid) with
+      mid the centre of the quant range (7.5 or 15.5; m <= 63 for Q4_K, Q5_K
+      uses sc ~ U[1, 4]), dmin = d, so a value d*sc*q - dmin*m is centred on
+      zero; d = f16(U[0.5, 1.5] / (sqrt(k) * rms(sc) * std(q))).
+    * Q6_K: sub-scales ~ U[-8, 8] without 0, q6 ~ U[0, 63] (value q - 32),
+      d = f16(U[0.5, 1.5] / (sqrt(k) * rms(sc) * std(q))).
+    * Q3_K: sub-scales +-U[1, 8], q3 ~ U[-4, 3]; Q2_K: sc ~ U[1, 8],
+      m = round(1.5 sc), dmin = d; Q8_0, Q4_0, Q5_0: d * (q - centre) with d
+      scaled the same way."""
+    if rng is None:
+        rng = np.random.default_rng(seed)
+    if type_ in (TYPE_Q8_0, TYPE_Q4_0, TYPE_Q5_0):  # value d * (q - centre), blocks of 32
+        if k % QK8_0:
+            raise ValueError(f"k={k} is not a multiple of {QK8_0}")
+        nb = k // QK8_0
+        spread = rng.uniform(0.5, 1.5, size=(n, nb))
+        if type_ == TYPE_Q8_0:
+            q = rng.integers(-127, 128, size=(n, nb, 32), dtype=np.int8)
+            std_q, pack = np.sqrt((255 * 255 - 1) / 12.0), pack_q8_0
+        else:
+            top = 16 if type_ == TYPE_Q4_0 else 32
+            q = rng.integers(0, top, size=(n, nb, 32), dtype=np.uint8)
+            std_q, pack = np.sqrt((top * top - 1) / 12.0), (pack_q4_0 if top == 16 else pack_q5_0)
+        d = (spread / (np.sqrt(k) * std_q)).astype(np.float32).astype(np.float16)
+        return QWeight(type_, n, k, pack(d, q), d, None, None, None, q)
+    if k % QK_K:
+        raise ValueError(f"k={k} is not a multiple of {QK_K}")
+    nb = k // QK_K
+    spread = rng.uniform(0.5, 1.5, size=(n, nb))
+    if type_ in (TYPE_Q4_K, TYPE_Q5_K):
+        five = type_ == TYPE_Q5_K
+        top = 32 if five else 16
+        smax = 4 if five else 8
+        sc = rng.integers(1, smax + 1, size=(n, nb, 8), dtype=np.uint8)
+        mn = np.minimum(np.rint(sc.astype(np.float64) * (top - 1) / 2.0), 63).astype(np.uint8)
+        q = rng.integers(0, top, size=(n, nb, 256), dtype=np.uint8)
+        rms_sc = np.sqrt(np.mean(np.arange(1, smax + 1) ** 2))
+        std_q = np.sqrt((top * top - 1) / 12.0)
+        d = (spread / (np.sqrt(k) * rms_sc * std_q)).astype(np.float32).astype(np.float16)
+        pack = pack_q5k if five else pack_q4k
+        return QWeight(type_, n, k, pack(d, d, sc, mn, q), d, d.copy(), sc, mn, q)
+    if type_ == TYPE_Q6_K:
+        mag = rng.integers(1, 9, size=(n, nb, 16))
+        sc = (mag * np.where(rng.integers(0, 2, size=mag.shape) == 1, 1, -1)).astype(np.int8)
+        q = (rng.integers(0, 64, size=(n, nb, 256), dtype=np.uint8).astype(np.int16) - 32).astype(np.int8)
+        rms_sc = np.sqrt(np.mean(np.arange(1, 9) ** 2))
+        std_q = np.sqrt((64 * 64 - 1) / 12.0)
+        d = (spread / (np.sqrt(k) * rms_sc * std_q)).astype(np.float32).astype(np.float16)
+        return QWeight(type_, n, k, pack_q6k(d, sc, q), d, None, sc, None, q)
+    if type_ == TYPE_Q3_K:  # value d * sc * q, sc = +-U[1, 8], q ~ U[-4, 3]
+        mag = rng.integers(1, 9, size=(n, nb, 16))
+        sc = (mag * np.where(rng.integers(0, 2, size=mag.shape) == 1, 1, -1)).astype(np.int8)
+        q = rng.integers(-4, 4, size=(n, nb, 256), dtype=np.int8)
+        d = (spread / (np.sqrt(k) * np.sqrt(np.mean(np.arange(1, 9) ** 2)) * np.sqrt(5.25))).astype(np.float32).astype(np.float16)
+        return QWeight(type_, n, k, pack_q3k(d, sc, q), d, None, sc, None, q)
+    if type_ == TYPE_Q2_K:  # value d * sc * q - dmin * m, sc ~ U[1, 8], m = round(1.5 sc), dmin = d
+        sc = rng.integers(1, 9, size=(n, nb, 16), dtype=np.uint8)
+        mn = np.rint(sc.astype(np.float64) * 1.5).astype(np.uint8)
+        q = rng.integers(0, 4, size=(n, nb, 256), dtype=np.uint8)
+        d = (spread / (np.sqrt(k) * np.sqrt(np.mean(np.arange(1, 9) ** 2)) * np.sqrt(1.25))).astype(np.float32).astype(np.float16)
+        return QWeight(type_, n, k, pack_q2k(d, d, sc, mn, q), d, d.copy(), sc, mn, q)
+    raise ValueError(f"make_weight_unit has no distribution for type {type_}")
+
+
 def make_activation(m: int, k: int, seed: int = 0, rng: np.random.Generator | None = None) -> np.ndarray:
     """f32 [m, k] drawn from N(0, 1)."""
     if rng is None:

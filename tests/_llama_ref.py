@@ -48,40 +48,53 @@ class RefLlama:
         out[..., 1::2] = a * s + b * c
         return out
 
-    def forward(self, tokens, index_pos):
-        cfg, hw, hd = self.cfg, self.hw, self.hd
+    def embed(self, tokens, index_pos):
         tokens = np.asarray(tokens, np.int64)
-        L = len(tokens)
-        H, Hkv = cfg.n_head, cfg.n_kv_head
-        x = hw.tok_embeddings[tokens].astype(np.float32)
         if index_pos == 0:
-            self.k = [np.zeros((Hkv, 0, hd), np.float32) for _ in range(cfg.n_layer)]
-            self.v = [np.zeros((Hkv, 0, hd), np.float32) for _ in range(cfg.n_layer)]
-        for li in range(cfg.n_layer):
-            lw = hw.layers[li]
-            n = self.rms(x, hw.attn_norm[li])
-            q = self.rope(self.mm(lw["wq"], n).reshape(L, H, hd), index_pos).transpose(1, 0, 2)
-            k = self.rope(self.mm(lw["wk"], n).reshape(L, Hkv, hd), index_pos).transpose(1, 0, 2)
-            v = self.mm(lw["wv"], n).reshape(L, Hkv, hd).transpose(1, 0, 2)
-            self.k[li] = np.concatenate([self.k[li], k], axis=1)
-            self.v[li] = np.concatenate([self.v[li], v], axis=1)
-            T = self.k[li].shape[1]
-            y = np.empty((H, L, hd), np.float32)
-            grp = H // Hkv
-            for h in range(H):
-                kk, vv = self.k[li][h // grp], self.v[li][h // grp]
-                att = (q[h] @ kk.T) / np.float32(np.sqrt(hd))
-                if L > 1:
-                    i = np.arange(L)[:, None] + index_pos
-                    j = np.arange(T)[None, :]
-                    att = np.where(j > i, -np.inf, att)
-                att = att - att.max(axis=-1, keepdims=True)
-                e = np.exp(att)
-                y[h] = (e / e.sum(axis=-1, keepdims=True)) @ vv
-            x = x + self.mm(lw["wo"], y.transpose(1, 0, 2).reshape(L, H * hd))
-            n = self.rms(x, hw.ffn_norm[li])
-            g = self.mm(lw["w1"], n)
-            u = self.mm(lw["w3"], n)
-            x = x + self.mm(lw["w2"], (g / (1.0 + np.exp(-g))) * u)
-        last = self.rms(x[L - 1:L], hw.norm)
-        return self.mm(hw.output, last)[0]
+            cfg, hd = self.cfg, self.hd
+            self.k = [np.zeros((cfg.n_kv_head, 0, hd), np.float32) for _ in range(cfg.n_layer)]
+            self.v = [np.zeros((cfg.n_kv_head, 0, hd), np.float32) for _ in range(cfg.n_layer)]
+        return self.hw.tok_embeddings[tokens].astype(np.float32)
+
+    def layer(self, li, x, index_pos):
+        """Layer li on the residual stream x [L, hidden] at positions index_pos..;
+        appends the layer's k, v to its cache and returns the new residual stream."""
+        cfg, hw, hd = self.cfg, self.hw, self.hd
+        L = x.shape[0]
+        H, Hkv = cfg.n_head, cfg.n_kv_head
+        lw = hw.layers[li]
+        n = self.rms(x, hw.attn_norm[li])
+        q = self.rope(self.mm(lw["wq"], n).reshape(L, H, hd), index_pos).transpose(1, 0, 2)
+        k = self.rope(self.mm(lw["wk"], n).reshape(L, Hkv, hd), index_pos).transpose(1, 0, 2)
+        v = self.mm(lw["wv"], n).reshape(L, Hkv, hd).transpose(1, 0, 2)
+        self.k[li] = np.concatenate([self.k[li][:, :index_pos], k], axis=1)
+        self.v[li] = np.concatenate([self.v[li][:, :index_pos], v], axis=1)
+        T = self.k[li].shape[1]
+        y = np.empty((H, L, hd), np.float32)
+        grp = H // Hkv
+        for h in range(H):
+            kk, vv = self.k[li][h // grp], self.v[li][h // grp]
+            att = (q[h] @ kk.T) / np.float32(np.sqrt(hd))
+            if L > 1:
+                i = np.arange(L)[:, None] + index_pos
+                j = np.arange(T)[None, :]
+                att = np.where(j > i, -np.inf, att)
+            att = att - att.max(axis=-1, keepdims=True)
+            e = np.exp(att)
+            y[h] = (e / e.sum(axis=-1, keepdims=True)) @ vv
+        x = x + self.mm(lw["wo"], y.transpose(1, 0, 2).reshape(L, H * hd))
+        n = self.rms(x, hw.ffn_norm[li])
+        g = self.mm(lw["w1"], n)
+        u = self.mm(lw["w3"], n)
+        return x + self.mm(lw["w2"], (g / (1.0 + np.exp(-g))) * u)
+
+    def head(self, x):
+        """Final norm and output head on the last position of x -> logits [vocab]."""
+        last = self.rms(x[-1:], self.hw.norm)
+        return self.mm(self.hw.output, last)[0]
+
+    def forward(self, tokens, index_pos):
+        x = self.embed(tokens, index_pos)
+        for li in range(self.cfg.n_layer):
+            x = self.layer(li, x, index_pos)
+        return self.head(x)
