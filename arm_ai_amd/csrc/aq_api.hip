@@ -14,6 +14,7 @@
 
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <mutex>
 #include <new>
@@ -380,9 +381,15 @@ static int upload_impl(aq_ctx *ctx, int type, const void *blocks, size_t nbytes,
         hipMemsetAsync(base, 0, total, ctx->stream) != hipSuccess)
         status = fail(AQ_ERR_HIP, "hipMemsetAsync of the weight padding failed");
 
-    // Stage whole rows through a bounded device buffer (256 MiB) unless the
-    // blocks are already on the device.
-    const size_t stage_cap = (size_t)256 << 20;
+    // Stage whole rows through a bounded device buffer (256 MiB; the
+    // environment variable ARM_AI_AMD_UPLOAD_STAGE_BYTES lowers it, which the
+    // tests use to force uploads of many chunks) unless the blocks are
+    // already on the device.
+    size_t stage_cap = (size_t)256 << 20;
+    if (const char *env = getenv("ARM_AI_AMD_UPLOAD_STAGE_BYTES")) {
+        const long long v = atoll(env);
+        if (v > 0 && (size_t)v < stage_cap) stage_cap = (size_t)v;
+    }
     int64_t rows_per = (int64_t)(stage_cap / row_bytes) / RB * RB;  // chunks start on a row block
     if (rows_per < RB) rows_per = RB;
     if (rows_per > n) rows_per = n;

@@ -331,7 +331,8 @@ __global__ __launch_bounds__(WIDE_THREADS) void attn_decode_kernel(
 // Greedy pick: the first index of the largest value (a NaN never wins; all
 // NaN gives 0).  Writes it to *d_tok (the next step's input), to
 // hist[*d_pos] when hist is given, and advances *d_pos by one.  One
-// 1024-thread workgroup, float4 loads (n % 4 == 0), several in flight.
+// 1024-thread workgroup, float4 loads (x 16-byte aligned), several in
+// flight; the last n % 4 elements are read one by one.
 __device__ __forceinline__ void better(float v, int i, float &best, int &idx) {
     if (v > best || (v == best && i < idx)) {  // NaN compares false
         best = v;
@@ -363,6 +364,7 @@ __global__ __launch_bounds__(WIDE_THREADS) void argmax_kernel(const float *__res
             better(v[u].w, i + 3, best, idx);
         }
     }
+    if ((int)threadIdx.x < (n & 3)) better(x[4 * n4 + threadIdx.x], 4 * n4 + (int)threadIdx.x, best, idx);
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) {
         const float ov = __shfl_xor(best, o);
@@ -431,7 +433,7 @@ hipError_t launch_attn_decode(const float *qk, const float *v, const float *cosb
 
 hipError_t launch_argmax(const float *x, int64_t n, int64_t *d_tok, int64_t *d_pos, int64_t *hist, int64_t hist_len,
                          hipStream_t s) {
-    if (!x || !d_tok || !d_pos || n <= 0 || n % 4 || n > 0x7fffffff) return hipErrorInvalidValue;
+    if (!x || !d_tok || !d_pos || n <= 0 || ((uintptr_t)x & 15) || n > 0x7fffffff) return hipErrorInvalidValue;
     argmax_kernel<<<1, WIDE_THREADS, 0, s>>>(x, (int)n, d_tok, d_pos, hist, hist_len);
     return hipGetLastError();
 }

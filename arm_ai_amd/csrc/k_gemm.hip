@@ -34,10 +34,10 @@
 //
 // Split-K.  When there are too few tiles to fill the 256 CUs, the K loop is
 // cut into `splits` ranges of super-blocks.  Each workgroup writes its partial
-// tile to the workspace and bumps the tile's counter; the workgroup that
-// arrives last (no one waits) sums the partials in split order -- so the
-// result does not depend on arrival order -- writes y, and resets the counter
-// to zero for the next launch.
+// tile to the workspace, and a second, small launch (gemm_splitk_reduce)
+// sums every tile's partials in split order and writes y -- so the result
+// does not depend on which workgroup finished first, and no workgroup waits
+// on another.
 #include "aq_internal.h"
 
 #include <algorithm>

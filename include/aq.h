@@ -294,9 +294,9 @@ int aq_qmatmul_silu_mul_f32_device(aq_ctx *ctx, const aq_qweight *w, const float
 int aq_qmatmul2_rmsnorm_f32_device(aq_ctx *ctx, const aq_qweight *w1, const aq_qweight *w2, const float *d_x,
                                    const float *d_delta, const float *d_norm_w, float eps, int64_t k, float *d_h_out,
                                    float *d_dst1, float *d_dst2);
-/* Greedy pick: the first index of the largest of d_x[0..n) goes to *d_tok
- * and, when d_hist is non-null and 0 <= *d_pos < hist_len, to
- * d_hist[*d_pos]; then *d_pos += 1. */
+/* Greedy pick: the first index of the largest of d_x[0..n) (d_x 16-byte
+ * aligned, any n >= 1) goes to *d_tok and, when d_hist is non-null and
+ * 0 <= *d_pos < hist_len, to d_hist[*d_pos]; then *d_pos += 1. */
 int aq_llama_argmax(aq_ctx *ctx, const float *d_x, int64_t n, int64_t *d_tok, int64_t *d_pos, int64_t *d_hist,
                     int64_t hist_len);
 

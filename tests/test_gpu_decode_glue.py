@@ -158,6 +158,31 @@ def test_argmax_first_max_history_and_position(env):
     assert h[10] == 777 and np.all(np.delete(h, 10) == -1)
 
 
+@pytest.mark.parametrize("n,where", [(32001, 32000), (32003, 32001), (32003, 5), (7, 6), (1, 0)])
+def test_argmax_vocab_not_a_multiple_of_four(env, n, where):
+    """Vocabularies such as 32001 or 32003 (some Llama-2 fine-tunes): the
+    elements past the last float4 are read one by one, and a maximum among
+    them, or tied with one before them, is picked as candle picks it."""
+    torch, lib, ctx = env
+    L = lib.load()
+    x = np.random.default_rng(n).standard_normal(n).astype(np.float32)
+    x[where] = 40.0
+    tok = torch.zeros(1, dtype=torch.int64, device="cuda:0")
+    pos = torch.zeros(1, dtype=torch.int64, device="cuda:0")
+    dx = _dev(torch, x)
+    torch.cuda.synchronize()
+    lib.check(L.aq_llama_argmax(ctx.handle, dx.data_ptr(), n, tok.data_ptr(), pos.data_ptr(), None, 0))
+    ctx.synchronize()
+    assert int(tok.item()) == where
+    if n > 4 and where >= n - (n % 4):  # a tie with an earlier element: the earlier one wins
+        x[1] = 40.0
+        dx = _dev(torch, x)
+        torch.cuda.synchronize()
+        lib.check(L.aq_llama_argmax(ctx.handle, dx.data_ptr(), n, tok.data_ptr(), pos.data_ptr(), None, 0))
+        ctx.synchronize()
+        assert int(tok.item()) == 1
+
+
 def test_embed_lookup_and_out_of_range(env):
     torch, lib, ctx = env
     L = lib.load()

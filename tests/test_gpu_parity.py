@@ -523,3 +523,31 @@ def test_device_pointer_entry_points(ctx, wtype, m):
     assert np.array_equal(mm2.forward(x), y_host)
     mm.free()
     mm2.free()
+
+
+# ------------------------------------------------------- chunked weight upload
+@pytest.mark.parametrize("wtype", [S.TYPE_Q2_K, S.TYPE_Q6_K, S.TYPE_Q5_0, S.TYPE_Q4_0, S.TYPE_Q8_0, S.TYPE_Q4_K])
+def test_upload_in_many_chunks(ctx, wtype, monkeypatch):
+    """A weight staged through the upload buffer in many chunks (8 rows each,
+    n % 8 != 0) gives the same device bytes' results as a one-chunk upload:
+    the tile rows, the Q2_K / Q6_K d planes and the Q4_0 / Q5_0 expanded GEMM
+    copies are offset per chunk.  Checked through the matvec (3 rows) and
+    the prefill GEMM (20 rows) against the oracle and the one-chunk upload."""
+    n, k = 203, 2048
+    W = S.make_weight(wtype, n, k, seed=wtype + 90)
+    one = A.QMatMul.from_qtensor(A.QTensor(wtype, (n, k), W.blocks), ctx)
+    row_bytes = W.blocks.nbytes // n
+    monkeypatch.setenv("ARM_AI_AMD_UPLOAD_STAGE_BYTES", str(8 * row_bytes))
+    many = A.QMatMul.from_qtensor(A.QTensor(wtype, (n, k), W.blocks), ctx)
+    monkeypatch.delenv("ARM_AI_AMD_UPLOAD_STAGE_BYTES")
+    for m in (3, 20):
+        x = S.make_activation(m, k, seed=m)
+        y_many, y_one = many.forward(x), one.forward(x)
+        assert np.array_equal(y_many, y_one)
+        sm, smm = many.block_sums(x)
+        so, smo = one.block_sums(x)
+        assert np.array_equal(sm, so) and np.array_equal(smm, smo)
+        r = O.matmul(wtype, x, W.blocks, n, k)
+        assert rel_max(y_many, r) <= 1e-5
+    many.free()
+    one.free()

@@ -237,3 +237,26 @@ def test_generate_stops_after_stop_token_and_edge_cases(tiny):
     assert r.tokens == first  # the stop token is emitted, then generation ends
     assert model.generate([], 5).tokens == []
     assert model.generate(prompt, 0).tokens == []
+
+
+@pytest.mark.gpu
+def test_odd_vocab_graph_generate():
+    """A vocabulary that is not a multiple of four (514): the graph-captured
+    step (device argmax) and the eager path pick the same tokens."""
+    import torch
+
+    import arm_ai_amd as A
+    from arm_ai_amd.llama import Llama, LlamaConfig, synthetic_weights
+
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    cfg = LlamaConfig(n_layer=2, hidden=256, ffn=512, n_head=4, n_kv_head=2, vocab=514, max_seq=64)
+    hw = synthetic_weights(cfg, seed=21, unit=True)
+    ctx = A.Context(0)
+    model = Llama(ctx, hw)
+    try:
+        prompt = [3, 513, 100, 7]
+        assert model.generate(prompt, 6, graph=False).tokens == model.generate(prompt, 6, graph=True).tokens
+    finally:
+        model.free()
+        ctx.close()
