@@ -132,18 +132,24 @@ def time_graph(ctx, fn, count: int, warmup: int) -> tuple[float, float]:
     return ms / count, wall / count
 
 
-def cpu_baseline(wl: Workload, runs: int = 21, budget_s: float = 20.0) -> dict:
+ISA_NOTES = {
+    "baseline": "x86-64 baseline (-O3, no FMA contraction), OpenMP dynamic chunks of 256 columns",
+    "v3": "x86-64-v3 (AVX2, FMA, BMI2; -O3, no FMA contraction, bit-identical results): the vectorised upper bound",
+}
+
+
+def cpu_baseline(wl: Workload, runs: int = 21, budget_s: float = 20.0, isa: str = "baseline") -> dict:
     import oracle as O
 
     threads = os.cpu_count() or 1
     x, W = wl.x, wl.W
     for _ in range(3):
-        O.matmul(wl.wtype, x, W.blocks, wl.n, wl.k, nthreads=threads)
+        O.matmul(wl.wtype, x, W.blocks, wl.n, wl.k, nthreads=threads, isa=isa)
     times = []
     t_start = time.perf_counter()
     while len(times) < runs and time.perf_counter() - t_start < budget_s:
         t0 = time.perf_counter()
-        O.matmul(wl.wtype, x, W.blocks, wl.n, wl.k, nthreads=threads)
+        O.matmul(wl.wtype, x, W.blocks, wl.n, wl.k, nthreads=threads, isa=isa)
         times.append(time.perf_counter() - t0)
     med = float(np.median(times))
     return {
@@ -153,8 +159,26 @@ def cpu_baseline(wl: Workload, runs: int = 21, budget_s: float = 20.0) -> dict:
         "kind": "port",
         "sample": f"full {wl.n}x{wl.k} matmul at M={wl.m} (Q8_K quantisation + vec_dot_unopt), median of {len(times)} runs, {med*1e3:.2f} ms each",
         "cpu": cpu_model(),
-        "isa": "x86-64 baseline (-O3, no FMA contraction), OpenMP dynamic chunks of 256 columns",
+        "isa": ISA_NOTES[isa],
     }
+
+
+def cpu_prefill_baseline(wl: Workload, runs: int = 3) -> dict:
+    """The oracle's k_quants::matmul at the prefill shape (every row quantised,
+    then every column's vec_dot_unopt), all host cores: median of a few runs."""
+    import oracle as O
+
+    threads = os.cpu_count() or 1
+    O.matmul(wl.wtype, wl.x, wl.W.blocks, wl.n, wl.k, nthreads=threads)
+    times = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        O.matmul(wl.wtype, wl.x, wl.W.blocks, wl.n, wl.k, nthreads=threads)
+        times.append(time.perf_counter() - t0)
+    med = float(np.median(times))
+    return {"ms": round(med * 1e3, 2), "TOPS": round(2.0 * wl.m * wl.n * wl.k / med / 1e12, 4), "cores": threads,
+            "kind": "port", "cpu": cpu_model(), "isa": ISA_NOTES["baseline"],
+            "sample": f"the full {wl.m}x{wl.n}x{wl.k} matmul, median of {runs} runs"}
 
 
 def traffic_from_profile():
@@ -183,7 +207,7 @@ def measure(ctx, wtype, n, k, m, steps, warmup, seed):
     return wl, step_ms, step_wall, kern_ms, out
 
 
-def measure_prefill(ctx, wtype, n, k, m, steps, warmup, seed):
+def measure_prefill(ctx, wtype, n, k, m, steps, warmup, seed, cpu=False):
     """Prefill GEMM at m rows: quantiser kernel + GEMM (step) and the GEMM alone
     (Q4_K, Q8_0, Q4_0: int8 MFMA; Q5_K, Q6_K: f16 MFMA after the f16 copy of
     the quants, which the GEMM time includes)."""
@@ -201,6 +225,8 @@ def measure_prefill(ctx, wtype, n, k, m, steps, warmup, seed):
     }
     if wtype in (13, 14):  # the kernel runs on the f16 matrix cores
         out["gemm_frac_f16_peak"] = round(ops / (kern_ms / 1e3) / 1e12 / F16_PEAK_TFLOPS, 4)
+    if cpu:
+        out["cpu_baseline"] = cpu_prefill_baseline(wl)
     wl.free()
     return out
 
@@ -251,7 +277,25 @@ PREFILL_CASES = {  # name: (weight type, n, k, m, seed)
 }
 
 
-def measure_decode(ctx, n_prompt, n_new, seed):
+def cpu_decode_baseline(hw, prompt, n_prompt=16, n_steps=4) -> dict:
+    """Decode on the host with the CPU restatement of candle's quantized_llama
+    (oracle/llama_ref.py: numpy f32 glue, the oracle's k_quants::matmul on all
+    host cores): a short prompt (the per-token cost of decode is the weights,
+    634 MB a token, not the context), then greedy steps, timed."""
+    from oracle.llama_ref import RefLlama
+
+    ref = RefLlama(hw)
+    logits = ref.forward(prompt[:n_prompt], 0)
+    t0 = time.perf_counter()
+    for i in range(n_steps):
+        logits = ref.forward([int(np.argmax(logits))], n_prompt + i)
+    dt = (time.perf_counter() - t0) / n_steps
+    return {"decode_tok_s": round(1.0 / dt, 3), "decode_ms_per_tok": round(dt * 1e3, 2), "cores": os.cpu_count() or 1,
+            "kind": "port", "cpu": cpu_model(), "isa": ISA_NOTES["baseline"],
+            "sample": f"{n_steps} greedy steps after a {n_prompt}-token prompt"}
+
+
+def measure_decode(ctx, n_prompt, n_new, seed, with_cpu=True):
     """Config 2: TinyLlama-1.1B-shaped Q4_K_M model with random weights, a prompt
     of uniform-random ids, greedy decode with the decode step replayed from a HIP
     graph; statistics as ArmAI.LlamaCandle.generate reports them."""
@@ -259,10 +303,9 @@ def measure_decode(ctx, n_prompt, n_new, seed):
 
     cfg = LlamaConfig(max_seq=n_prompt + n_new)
     t0 = time.perf_counter()
-    hw = synthetic_weights(cfg, seed)
+    hw = synthetic_weights(cfg, seed, unit=True)
     wbytes = sum(qt.data.size for layer in hw.layers for qt in layer.values()) + hw.output.data.size
     model = Llama(ctx, hw)
-    del hw
     log(f"c2 model ready in {time.perf_counter() - t0:.1f} s")
     rng = np.random.default_rng(seed)
     prompt = rng.integers(0, cfg.vocab, size=n_prompt).tolist()
@@ -272,8 +315,10 @@ def measure_decode(ctx, n_prompt, n_new, seed):
     eager = model.generate(prompt, 16)
     est = eager.stats(n_prompt)
     model.free()
+    cpu = cpu_decode_baseline(hw, prompt) if with_cpu else None
+    del hw
     out = {
-        "model": "TinyLlama-1.1B shape (22 layers, hidden 2048, FFN 5632, 32/4 heads, vocab 32000), Q4_K_M types, random weights",
+        "model": "TinyLlama-1.1B shape (22 layers, hidden 2048, FFN 5632, 32/4 heads, vocab 32000), Q4_K_M types, random unit-scaled weights (activations of order one through all 22 layers)",
         "n_prompt": n_prompt,
         "n_new": st["n_new"],
         "decode_tok_s": round(1e3 / st["decode_ms_per_tok"], 1),
@@ -286,6 +331,8 @@ def measure_decode(ctx, n_prompt, n_new, seed):
         "graph_and_eager_tokens_agree": res.tokens[:16] == eager.tokens,
         "timing": "wall clock around generate (llama_candle.rs:80-139 points); decode step replayed from a HIP graph",
     }
+    if cpu is not None:
+        out["cpu_baseline"] = cpu
     return out
 
 
@@ -399,13 +446,14 @@ def measure_read_family(ctx, nbytes, steps, warmup):
             "frac_hbm": best["frac_hbm"], "rotating_copies": copies, "family": members}
 
 
-def run_decode_child(name):
+def run_decode_child(name, no_cpu=False):
     """Run a decode (or vendor reference) case in a child process: the driver's
     torch glue needs torch imported before this library is loaded (one HIP
     runtime per process)."""
     import subprocess
 
-    r = subprocess.run([sys.executable, "-u", os.path.abspath(__file__), "--case", name],
+    cmd = [sys.executable, "-u", os.path.abspath(__file__), "--case", name] + (["--no-cpu"] if no_cpu else [])
+    r = subprocess.run(cmd,
                        stdout=subprocess.PIPE, text=True, cwd=ROOT)
     if r.returncode != 0:
         raise RuntimeError(f"{name} failed in its child process (exit {r.returncode})")
@@ -414,7 +462,7 @@ def run_decode_child(name):
     return out
 
 
-def run_case(ctx, name, steps, warmup):
+def run_case(ctx, name, steps, warmup, with_cpu=False):
     if name in CRATE_CASES:
         out = measure_crate(ctx, *CRATE_CASES[name], steps, warmup)
         log(f"{name}: {out['us']} us ({out.get('GBps', out.get('TOPS'))} {'GB/s' if 'GBps' in out else 'TOPS'})")
@@ -425,7 +473,7 @@ def run_case(ctx, name, steps, warmup):
         return out
     if name in DECODE_CASES:
         n_prompt, n_new, seed = DECODE_CASES[name]
-        out = measure_decode(ctx, n_prompt, n_new, seed)
+        out = measure_decode(ctx, n_prompt, n_new, seed, with_cpu=with_cpu)
         log(f"{name}: decode {out['decode_tok_s']} tok/s ({out['decode_ms_per_tok']} ms/tok; eager {out['eager_decode_tok_s']} tok/s), prefill {out['prefill_ms']} ms ({out['prefill_tok_s']} tok/s)")
         return out
     if name in MATVEC_CASES:
@@ -435,7 +483,7 @@ def run_case(ctx, name, steps, warmup):
         log(f"{name}: step {out['step_us']} us ({out['step_GBps']} GB/s), pre-quantised matvec {out['matvec_us']} us ({out['matvec_GBps']} GB/s)")
         return out
     wt, n_, k_, m_, seed = PREFILL_CASES[name]
-    out = measure_prefill(ctx, wt, n_, k_, m_, min(steps, 50), min(warmup, 5), seed)
+    out = measure_prefill(ctx, wt, n_, k_, m_, min(steps, 50), min(warmup, 5), seed, cpu=with_cpu and name.startswith("c3_"))
     log(f"{name}: step {out['step_us']} us ({out['step_TOPS']} TOPS), gemm {out['gemm_us']} us ({out['gemm_TOPS']} TOPS, {out['gemm_frac_int8_peak']} of int8 peak)")
     return out
 
@@ -483,7 +531,7 @@ def main() -> int:
     ctx = A.Context(0)
     log("context ready on device 0")
     if args.case is not None:
-        out = run_case(ctx, args.case, args.steps, args.warmup)
+        out = run_case(ctx, args.case, args.steps, args.warmup, with_cpu=not args.no_cpu)
         ctx.close()
         print(json.dumps({"case": args.case, **out}), flush=True)
         return 0
@@ -521,7 +569,7 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic_from_profile(),
-            "kernel": "rl_q4k_kernel<2, 12, true, false> (Q4_K, batch 1, one weight row per lane, Q8_K quantisation fused)",
+            "kernel": "rl_q4k_kernel<16, 1, 6, true, false> (Q4_K, batch 1, one weight row per lane, Q8_K quantisation fused)",
             "bytes_per_launch": wl.step_bytes,
             "avg_launch_us": round(step_ms * 1e3, 3),
         },
@@ -534,6 +582,13 @@ def main() -> int:
         log("cpu baseline ...")
         result["cpu_baseline"] = cpu_baseline(wl)
         log(f"cpu baseline {result['cpu_baseline']['value']} GB/s")
+        import oracle as O
+
+        if O.cpu_has_v3():
+            v3 = cpu_baseline(wl, isa="v3")
+            log(f"cpu x86-64-v3 upper bound {v3['value']} GB/s")
+        else:
+            v3 = {"skipped": "this host CPU cannot run x86-64-v3 code"}
     wl.free()
 
     if not args.no_extra:
@@ -541,17 +596,19 @@ def main() -> int:
         for name in MATVEC_CASES:
             extra[name] = run_case(ctx, name, args.steps, args.warmup)
         for name in PREFILL_CASES:
-            extra[name] = run_case(ctx, name, args.steps, args.warmup)
+            extra[name] = run_case(ctx, name, args.steps, args.warmup, with_cpu=not args.no_cpu)
         for name in CRATE_CASES:
             extra[name] = run_case(ctx, name, args.steps, args.warmup)
         for name in DECODE_CASES:
-            extra[name] = run_decode_child(name)
+            extra[name] = run_decode_child(name, no_cpu=args.no_cpu)
         for name in VENDOR_CASES:
-            extra[name] = run_decode_child(name)
+            extra[name] = run_decode_child(name, no_cpu=True)
         result["extra"] = extra
     else:
         result["extra"] = {}
     result["extra"]["c4_q4k_14336x4096_b1_prequantised"] = head_extra
+    if not args.no_cpu:
+        result["extra"]["cpu_baseline_x86_64_v3"] = v3
     ctx.close()
     print(json.dumps(result), flush=True)
     return 0

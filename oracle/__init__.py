@@ -16,26 +16,39 @@ import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "liboracle.so")
+LIB_V3_PATH = os.path.join(HERE, "liboracle_v3.so")  # same source, x86-64-v3
 
 Q2_K, Q3_K, Q4_0, Q5_0, Q4_K, Q5_K, Q6_K, Q8_0, Q8_K = 10, 11, 2, 6, 12, 13, 14, 8, 15
 BLOCK_BYTES = {Q2_K: 84, Q3_K: 110, Q4_0: 18, Q5_0: 22, Q4_K: 144, Q5_K: 176, Q6_K: 210, Q8_0: 34, Q8_K: 292}
 BLOCK_ELEMS = {Q2_K: 256, Q3_K: 256, Q4_0: 32, Q5_0: 32, Q4_K: 256, Q5_K: 256, Q6_K: 256, Q8_0: 32, Q8_K: 256}
 
-_lib = None
+_libs: dict = {}
 
 
 def build() -> str:
-    """Compile liboracle.so with its Makefile (gcc; no GPU needed)."""
+    """Compile liboracle.so (and liboracle_v3.so) with the Makefile (gcc; no GPU needed)."""
     subprocess.run(["make", "-s", "-C", HERE], check=True)
     return LIB_PATH
 
 
-def lib() -> ctypes.CDLL:
-    global _lib
-    if _lib is None:
-        if not os.path.exists(LIB_PATH):
+def cpu_has_v3() -> bool:
+    """True when this CPU runs x86-64-v3 code (AVX2, FMA, BMI2, F16C, MOVBE)."""
+    try:
+        flags = next(line for line in open("/proc/cpuinfo") if line.startswith("flags")).split()
+    except (OSError, StopIteration):
+        return False
+    return all(f in flags for f in ("avx2", "fma", "bmi2", "f16c", "movbe", "bmi1"))
+
+
+def lib(isa: str = "baseline") -> ctypes.CDLL:
+    """The oracle library: the x86-64 baseline build, or isa="v3" for the x86-64-v3 build."""
+    if isa not in _libs:
+        path = LIB_PATH if isa == "baseline" else LIB_V3_PATH
+        if isa != "baseline" and not cpu_has_v3():
+            raise RuntimeError("this CPU cannot run the x86-64-v3 build")
+        if not os.path.exists(path):
             build()
-        L = ctypes.CDLL(LIB_PATH)
+        L = ctypes.CDLL(path)
         P = ctypes.c_void_p
         i64 = ctypes.c_int64
         L.orc_f16_to_f32.argtypes = [ctypes.c_uint16]
@@ -65,8 +78,8 @@ def lib() -> ctypes.CDLL:
         L.orc_dequantize_row.restype = ctypes.c_int
         L.orc_max_threads.argtypes = []
         L.orc_max_threads.restype = ctypes.c_int
-        _lib = L
-    return _lib
+        _libs[isa] = L
+    return _libs[isa]
 
 
 def _p(a: np.ndarray) -> int:
@@ -164,7 +177,8 @@ def block_sums(wtype: int, k: int, w: np.ndarray, xq: np.ndarray, nthreads: int 
     return S, Sm
 
 
-def matmul(wtype: int, x: np.ndarray, w: np.ndarray, n: int, k: int, nthreads: int = 0) -> np.ndarray:
+def matmul(wtype: int, x: np.ndarray, w: np.ndarray, n: int, k: int, nthreads: int = 0,
+           isa: str = "baseline") -> np.ndarray:
     """k_quants::matmul: f32 [m, k] x W[n, k]^T -> f32 [m, n]."""
     x = np.ascontiguousarray(x, dtype=np.float32)
     if x.ndim == 1:
@@ -176,7 +190,7 @@ def matmul(wtype: int, x: np.ndarray, w: np.ndarray, n: int, k: int, nthreads: i
     if w.nbytes != n * _row_bytes(wtype, k):
         raise ValueError(f"weight has {w.nbytes} bytes, {n} rows of k={k} need {n * _row_bytes(wtype, k)}")
     dst = np.zeros((m, n), np.float32)
-    rc = lib().orc_matmul(wtype, m, k, n, _p(x), _p(w), _p(dst), nthreads)
+    rc = lib(isa).orc_matmul(wtype, m, k, n, _p(x), _p(w), _p(dst), nthreads)
     if rc != 0:
         raise ValueError(f"orc_matmul failed: {rc}")
     return dst

@@ -1,6 +1,7 @@
-"""CPU restatement of candle-transformers 0.8.4 quantized_llama's forward for the
-driver tests: numpy f32 for the glue, the oracle's k_quants::matmul for every
-quantized projection.  Test infrastructure only.
+"""CPU restatement of candle-transformers 0.8.4 quantized_llama's forward:
+numpy f32 for the glue, the oracle's k_quants::matmul for every quantized
+projection.  Test infrastructure only (the driver tests' reference, and the
+CPU decode baseline bench.py times beside the GPU's).
 
 Follows the call sequence the reference reaches from
 native/arm_ai_nif/src/llama_candle.rs:93 (prefill) and :119 (decode); candle's

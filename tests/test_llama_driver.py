@@ -1,7 +1,7 @@
 """The quantized matmuls' call sites (a Llama decoder driven like ArmAI.LlamaCandle).
 
 GPU tests: the driver (arm_ai_amd.llama, quantized projections on the GPU
-through the C ABI) against tests/_llama_ref.py (numpy glue + the oracle's
+through the C ABI) against oracle/llama_ref.py (numpy glue + the oracle's
 k_quants::matmul) on a small model, teacher-forced: prefill logits, decode
 logits, the graph-captured decode step against the eager one, and greedy
 generation.  Weights come from synth.make_weight_unit (values centred and
@@ -17,7 +17,7 @@ CPU test: the reference restatement's rope_i pairing against its closed form.
 import numpy as np
 import pytest
 
-from tests._llama_ref import RefLlama
+from oracle.llama_ref import RefLlama
 
 LOGIT_TOL = 1e-3
 

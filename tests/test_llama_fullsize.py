@@ -44,7 +44,7 @@ import warnings
 import numpy as np
 import pytest
 
-from tests._llama_ref import RefLlama
+from oracle.llama_ref import RefLlama
 
 pytestmark = pytest.mark.gpu
 

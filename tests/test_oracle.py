@@ -495,3 +495,20 @@ def test_q5_0_fifth_bit_and_nibble_land_on_element(e):
     want = np.zeros(32)
     want[e] = 0.5 * (7 - 16)
     assert np.array_equal(got, want)
+
+
+def test_v3_build_is_bit_identical_to_the_baseline_build():
+    """liboracle_v3.so (x86-64-v3, the upper-bound CPU line bench.py reports)
+    compiles the same source with FMA contraction off: every output equals
+    the baseline build's bit for bit."""
+    import pytest
+
+    if not O.cpu_has_v3():
+        pytest.skip("this CPU cannot run x86-64-v3 code")
+    rng = np.random.default_rng(3)
+    for wtype, n, k in ((O.Q4_K, 96, 2048), (O.Q6_K, 64, 1024), (O.Q8_0, 40, 512), (O.Q5_K, 33, 768)):
+        W = S.make_weight(wtype, n, k, seed=wtype)
+        x = rng.standard_normal((5, k)).astype(np.float32)
+        a = O.matmul(wtype, x, W.blocks, n, k, isa="baseline")
+        b = O.matmul(wtype, x, W.blocks, n, k, isa="v3")
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), wtype
