@@ -82,7 +82,10 @@ SIGNATURES = {
     "aq_llama_embed": (INT, [P, P, I64, P, I64, P]),
     "aq_llama_rmsnorm": (INT, [P, P, P, P, I64, I64, ctypes.c_float, P]),
     "aq_llama_silu_mul": (INT, [P, P, I64, P]),
+    "aq_llama_embed_rows": (INT, [P, P, I64, P, I64, I64, P]),
+    "aq_llama_silu_mul_rows": (INT, [P, P, P, I64, I64, I64, P]),
     "aq_llama_attn_decode": (INT, [P, P, P, P, P, P, P, P, I64, I64, I64, I64, P]),
+    "aq_llama_attn_prefill": (INT, [P, P, I64, P, I64, P, I64, P, P, I64, I64, P, P, I64, I64, I64, I64, P]),
     "aq_llama_argmax": (INT, [P, P, I64, P, P, P, I64]),
     "aq_qmatmul_rmsnorm_f32_device": (INT, [P, P, P, P, P, ctypes.c_float, I64, P, P]),
     "aq_qmatmul_silu_mul_f32_device": (INT, [P, P, P, I64, P]),

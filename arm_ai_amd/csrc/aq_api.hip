@@ -33,7 +33,11 @@ struct aq_ctx {
     void *pinned = nullptr;  // host staging, grow-only
     size_t pinned_bytes = 0;
     void *fixed_scratch = nullptr;  // this device's copy of g_fixed_scratch (its device address)
+    // decode attention's per-slice partial records: allocated with the
+    // context, so a captured decode step never allocates
+    float *attn_part = nullptr;
 };
+constexpr size_t ATTN_PART_BYTES = (size_t)2 << 20;
 
 // Scratch of aq_qmatmul_f32_device_noalloc: a fixed array in the library's
 // device image, one copy per GPU (held until the process ends).  Its name is
@@ -288,6 +292,11 @@ int aq_ctx_create(int device, aq_ctx **out) {
         delete c;
         return fail(AQ_ERR_HIP, "hipStreamCreateWithFlags failed");
     }
+    if (hipMalloc(&c->attn_part, ATTN_PART_BYTES) != hipSuccess) {
+        (void)hipGetLastError();
+        aq_ctx_destroy(c);
+        return fail(AQ_ERR_OOM, "allocation of the attention workspace failed");
+    }
     *out = c;
     return AQ_OK;
 }
@@ -298,6 +307,7 @@ int aq_ctx_destroy(aq_ctx *c) {
     if (c->stream) (void)hipStreamSynchronize(c->stream);
     if (c->scratch) (void)hipFree(c->scratch);
     if (c->pinned) (void)hipHostFree(c->pinned);
+    if (c->attn_part) (void)hipFree(c->attn_part);
     if (c->stream) (void)hipStreamDestroy(c->stream);
     delete c;
     return AQ_OK;
@@ -935,7 +945,16 @@ int aq_llama_embed(aq_ctx *ctx, const float *d_table, int64_t vocab, const int64
     if (!ctx) return fail(AQ_ERR_INVALID_ARG, "null context");
     int rc = use_device(ctx->device);
     if (rc) return rc;
-    return hip_status(launch_embed(d_table, vocab, d_tok, hidden, d_out, ctx->stream), "embed");
+    return hip_status(launch_embed(d_table, vocab, d_tok, 1, hidden, d_out, ctx->stream), "embed");
+}
+
+int aq_llama_embed_rows(aq_ctx *ctx, const float *d_table, int64_t vocab, const int64_t *d_tok, int64_t m,
+                        int64_t hidden, float *d_out) {
+    if (!ctx) return fail(AQ_ERR_INVALID_ARG, "null context");
+    if (m == 0) return AQ_OK;
+    int rc = use_device(ctx->device);
+    if (rc) return rc;
+    return hip_status(launch_embed(d_table, vocab, d_tok, m, hidden, d_out, ctx->stream), "embed rows");
 }
 
 int aq_llama_rmsnorm(aq_ctx *ctx, float *d_x, const float *d_delta, const float *d_w, int64_t m, int64_t n, float eps,
@@ -951,7 +970,17 @@ int aq_llama_silu_mul(aq_ctx *ctx, const float *d_gu, int64_t n, float *d_out) {
     if (!ctx) return fail(AQ_ERR_INVALID_ARG, "null context");
     int rc = use_device(ctx->device);
     if (rc) return rc;
-    return hip_status(launch_silu_mul(d_gu, n, d_out, ctx->stream), "silu_mul");
+    if (!d_gu) return fail(AQ_ERR_INVALID_ARG, "null gu");
+    return hip_status(launch_silu_mul(d_gu, d_gu + n, 2 * n, 1, n, d_out, ctx->stream), "silu_mul");
+}
+
+int aq_llama_silu_mul_rows(aq_ctx *ctx, const float *d_g, const float *d_u, int64_t ld, int64_t m, int64_t n,
+                           float *d_out) {
+    if (!ctx) return fail(AQ_ERR_INVALID_ARG, "null context");
+    if (m == 0) return AQ_OK;
+    int rc = use_device(ctx->device);
+    if (rc) return rc;
+    return hip_status(launch_silu_mul(d_g, d_u, ld, m, n, d_out, ctx->stream), "silu_mul rows");
 }
 
 int aq_llama_attn_decode(aq_ctx *ctx, const float *d_qk, const float *d_v, const float *d_cos, const float *d_sin,
@@ -960,9 +989,33 @@ int aq_llama_attn_decode(aq_ctx *ctx, const float *d_qk, const float *d_v, const
     if (!ctx) return fail(AQ_ERR_INVALID_ARG, "null context");
     int rc = use_device(ctx->device);
     if (rc) return rc;
-    return hip_status(launch_attn_decode(d_qk, d_v, d_cos, d_sin, d_pos, d_kcache, d_vcache, n_head, n_kv, head_dim,
-                                         max_seq, d_out, ctx->stream),
-                      "attn_decode");
+    if (!d_qk || !d_v || !d_cos || !d_sin || !d_pos || !d_kcache || !d_vcache || !d_out)
+        return fail(AQ_ERR_INVALID_ARG, "null pointer");
+    if (max_seq <= 0 || max_seq > 8192) return fail(AQ_ERR_INVALID_ARG, "max_seq %lld outside 1..8192", (long long)max_seq);
+    if (((uintptr_t)d_kcache | (uintptr_t)d_vcache | (uintptr_t)d_out) & 15)
+        return fail(AQ_ERR_INVALID_ARG, "caches and output must be 16-byte aligned");
+    // the query heads of a kv head together, the context split over workgroups;
+    // other head shapes: one workgroup per query head
+    hipError_t e = launch_attn_split(d_qk, d_v, d_cos, d_sin, d_pos, d_kcache, d_vcache, n_head, n_kv, head_dim,
+                                     max_seq, d_out, ctx->attn_part, ATTN_PART_BYTES, ctx->stream);
+    if (e == hipErrorNotSupported)
+        e = launch_attn_decode(d_qk, d_v, d_cos, d_sin, d_pos, d_kcache, d_vcache, n_head, n_kv, head_dim, max_seq,
+                               d_out, ctx->stream);
+    return hip_status(e, "attn_decode");
+}
+
+int aq_llama_attn_prefill(aq_ctx *ctx, const float *d_q, int64_t ldq, const float *d_k, int64_t ldk, const float *d_v,
+                          int64_t ldv, const float *d_cos, const float *d_sin, int64_t index_pos, int64_t m,
+                          float *d_kcache, float *d_vcache, int64_t n_head, int64_t n_kv, int64_t head_dim,
+                          int64_t max_seq, float *d_out) {
+    if (!ctx) return fail(AQ_ERR_INVALID_ARG, "null context");
+    if (m == 0) return AQ_OK;
+    int rc = use_device(ctx->device);
+    if (rc) return rc;
+    const hipError_t e = launch_attn_prefill(d_q, ldq, d_k, ldk, d_v, ldv, d_cos, d_sin, index_pos, m, d_kcache,
+                                             d_vcache, n_head, n_kv, head_dim, max_seq, d_out, ctx->stream);
+    if (e == hipErrorNotSupported) return fail(AQ_ERR_SHAPE, "head_dim %lld: the prompt attention takes 64 or 128", (long long)head_dim);
+    return hip_status(e, "attn_prefill");
 }
 
 

@@ -222,14 +222,28 @@ hipError_t launch_matvec2_rmsnorm(const WLayout &w1, int64_t n1, float *y1, cons
                                   float *xout, hipStream_t s);
 
 // Decode-step glue (k_decode.hip).
-hipError_t launch_embed(const float *table, int64_t vocab, const int64_t *d_tok, int64_t hidden, float *out,
+hipError_t launch_embed(const float *table, int64_t vocab, const int64_t *d_tok, int64_t m, int64_t hidden, float *out,
                         hipStream_t s);
 hipError_t launch_rmsnorm(float *x, const float *delta, const float *w, int64_t m, int64_t n, float eps, float *out,
                           hipStream_t s);
-hipError_t launch_silu_mul(const float *gu, int64_t n, float *out, hipStream_t s);
+hipError_t launch_silu_mul(const float *g, const float *u, int64_t ld, int64_t m, int64_t n, float *out, hipStream_t s);
 hipError_t launch_attn_decode(const float *qk, const float *v, const float *cosb, const float *sinb,
                               const int64_t *d_pos, float *kc, float *vc, int64_t n_head, int64_t n_kv, int64_t hd,
                               int64_t max_seq, float *out, hipStream_t s);
+// k_attn.hip: the decode attention with the context split over workgroups
+// and a second launch that combines the slices (hipErrorNotSupported for
+// shapes it does not take: head_dim other than 64 or 128, more than 8 query
+// heads per kv head, a workspace too small), its slice count and
+// partial-record bytes, and the prompt's causal attention.
+int attn_split_slices(int64_t n_kv, int64_t max_seq);
+size_t attn_split_workspace_bytes(int64_t n_head, int64_t n_kv, int64_t hd, int64_t max_seq);
+hipError_t launch_attn_split(const float *qk, const float *v, const float *cosb, const float *sinb,
+                             const int64_t *d_pos, float *kc, float *vc, int64_t n_head, int64_t n_kv, int64_t hd,
+                             int64_t max_seq, float *out, float *part, size_t part_bytes, hipStream_t s);
+hipError_t launch_attn_prefill(const float *q, int64_t ldq, const float *k, int64_t ldk, const float *v, int64_t ldv,
+                               const float *cosb, const float *sinb, int64_t index_pos, int64_t m, float *kc,
+                               float *vc, int64_t n_head, int64_t n_kv, int64_t hd, int64_t max_seq, float *out,
+                               hipStream_t s);
 hipError_t launch_argmax(const float *x, int64_t n, int64_t *d_tok, int64_t *d_pos, int64_t *hist, int64_t hist_len,
                          hipStream_t s);
 

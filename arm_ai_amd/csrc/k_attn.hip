@@ -1,0 +1,568 @@
+// k_attn.hip -- Llama attention over the KV cache on gfx950: the decode step
+// (one query position, the context split over workgroups) and the prompt
+// (prefill: every position of the prompt, causal).  Both follow
+// candle-transformers 0.8.4 quantized_llama's attention, which
+// native/arm_ai_nif/src/llama_candle.rs:93 (prompt at offset 0) and :119 (one
+// token at offset `offset`) run:
+//   q, k = rope_i(q), rope_i(k) at their positions (interleaved pairs
+//   (2i, 2i+1) rotated by pos * theta_i, from cos/sin tables [max_seq][hd/2]);
+//   k, v appended to the cache [n_kv][max_seq][hd] at their positions;
+//   each query head h attends with kv head h / (n_head / n_kv);
+//   softmax over (q . k_p) / sqrt(hd) with the causal mask p > position
+//   (candle masks whenever more than one position is fed), then . v.
+// f32 throughout (no fast-math, no FMA contraction of the rotation); sums are
+// reordered relative to candle's loops, so results agree within rounding.
+#include "aq_internal.h"
+
+namespace aq {
+
+namespace {
+
+// Sum / max over aligned groups of N = 16 or 32 lanes; every lane of a group
+// gets the result (DPP within 16-lane rows, one cross-row swap for 32).
+template <int N>
+__device__ __forceinline__ float group_sum(float v) {
+    static_assert(N == 16 || N == 32, "16- or 32-lane groups");
+    v += dpp_f<DPP_QUAD_XOR1>(v);
+    v += dpp_f<DPP_QUAD_XOR2>(v);
+    v += dpp_f<DPP_HALF_MIRROR>(v);
+    v += dpp_f<DPP_ROW_MIRROR>(v);
+    if (N == 32) v += __shfl_xor(v, 16);
+    return v;
+}
+__device__ __forceinline__ float group16_max(float v) {
+    v = fmaxf(v, dpp_f<DPP_QUAD_XOR1>(v));
+    v = fmaxf(v, dpp_f<DPP_QUAD_XOR2>(v));
+    v = fmaxf(v, dpp_f<DPP_HALF_MIRROR>(v));
+    v = fmaxf(v, dpp_f<DPP_ROW_MIRROR>(v));
+    return v;
+}
+__device__ __forceinline__ float wave_sum_f(float v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+__device__ __forceinline__ float dot4(const float4 a, const float4 b) {
+    return __builtin_fmaf(a.x, b.x, __builtin_fmaf(a.y, b.y, __builtin_fmaf(a.z, b.z, a.w * b.w)));
+}
+__device__ __forceinline__ void axpy4(float4 &acc, float w, const float4 x) {
+    acc.x = __builtin_fmaf(w, x.x, acc.x);
+    acc.y = __builtin_fmaf(w, x.y, acc.y);
+    acc.z = __builtin_fmaf(w, x.z, acc.z);
+    acc.w = __builtin_fmaf(w, x.w, acc.w);
+}
+constexpr float4 ZERO4 = {0.0f, 0.0f, 0.0f, 0.0f};
+
+// ------------------------------------------------------------------ decode
+// Two launches.  attn_split_kernel: grid (S slices, n_kv kv heads), 256
+// threads.  Workgroup (s, g) takes the positions [s*len, (s+1)*len) of
+// 0..pos (len = max(32, ceil((pos+1)/S))) for all REP = n_head / n_kv query
+// heads of kv head g, so every cached k, v row is read once per step (the
+// query heads of a group share it), and writes, per query head, the slice's
+// max score m, the sum l of e^(score - m) and the unnormalised o = sum of
+// e^(score - m) v to its partial record.  The workgroup whose slice holds pos
+// rotates k, stores k and v at pos, and uses its LDS copy for that position;
+// slices past the context exit.  attn_combine_kernel: one wavefront per query
+// head, M = max m_s, out = sum e^(m_s - M) o_s / sum e^(m_s - M) l_s.  (A
+// last-arriving-workgroup combine in the first launch measured slower here:
+// its device-scope release and the counter atomics of 256 workgroups cost
+// more than the second launch.)
+constexpr int SPL_THREADS = 256;
+constexpr int SPL_MIN_LEN = 32;     // positions per slice at least
+constexpr int SPL_MAX_LEN = 256;    // positions per slice at most (LDS scores)
+constexpr int SPL_MAX_SLICES = 256;
+constexpr int SPL_MAX_REP = 8;
+
+// the slice length and the number of slices that hold positions, for n = pos + 1
+__device__ __forceinline__ void split_shape(int n, int S, int &len, int &ns) {
+    len = (n + S - 1) / S;
+    if (len < SPL_MIN_LEN) len = SPL_MIN_LEN;
+    ns = (n + len - 1) / len;
+}
+
+template <int HD4, int REP>
+__global__ __launch_bounds__(SPL_THREADS) void attn_split_kernel(
+    const float *__restrict__ qk, const float *__restrict__ v, const float *__restrict__ cosb,
+    const float *__restrict__ sinb, const int64_t *__restrict__ d_pos, float *__restrict__ kc, float *__restrict__ vc,
+    int n_head, int max_seq, int S, float *__restrict__ part) {
+    constexpr int hd = 4 * HD4;
+    constexpr int G = SPL_THREADS / HD4;             // position groups of the value pass
+    constexpr int PSTR = REP * hd + 2 * SPL_MAX_REP; // floats per partial record: o[REP][hd], m[8], l[8]
+    constexpr int RPI = 64 / HD4;                    // key rows per wave load
+    constexpr int RPP = RPI * (SPL_THREADS / 64);    // key rows per workgroup pass
+    constexpr int KU = SPL_MIN_LEN / RPP;            // key passes loaded at the start (a whole minimum slice)
+    constexpr int VU = SPL_MIN_LEN / G;              // value rows per thread loaded at the start
+    __shared__ __align__(16) float qs[REP * hd];
+    __shared__ __align__(16) float ks[hd];
+    __shared__ __align__(16) float vs[hd];
+    __shared__ float sc[REP * SPL_MAX_LEN];
+    __shared__ float4 accs[G * REP * HD4];
+
+    const int s = blockIdx.x, kvh = blockIdx.y, tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int pos = (int)*d_pos;
+    if (pos < 0 || pos >= max_seq) return;  // the host checks; this never indexes out of the cache
+    const int n = pos + 1;
+    int len, ns;
+    split_shape(n, S, len, ns);
+    if (s >= ns) return;
+    float *kh = kc + (int64_t)kvh * max_seq * hd;
+    float *vh = vc + (int64_t)kvh * max_seq * hd;
+    float *pw = part + ((int64_t)kvh * S + s) * PSTR;
+    const int p0 = s * len, np = min(p0 + len, n) - p0;
+    const bool has_pos = p0 + np == n;
+    const int c = lane % HD4, d4 = tid % HD4, g = tid / HD4;
+
+    // the cached rows of the slice's first SPL_MIN_LEN positions: their
+    // addresses depend only on pos, so they are in flight while q and k rotate
+    float4 kv0[KU], vp[VU];
+#pragma unroll
+    for (int u = 0; u < KU; u++) {
+        const int i = u * RPP + wave * RPI + lane / HD4, p = p0 + i;
+        kv0[u] = i < np && p < pos ? ((const float4 *)(kh + (int64_t)p * hd))[c] : ZERO4;
+    }
+#pragma unroll
+    for (int u = 0; u < VU; u++) {
+        const int i = g + u * G, p = p0 + i;
+        vp[u] = i < np && p < pos ? *(const float4 *)(vh + (int64_t)p * hd + 4 * d4) : ZERO4;
+    }
+
+    const float *cr = cosb + (int64_t)pos * (hd / 2), *sr = sinb + (int64_t)pos * (hd / 2);
+    for (int i = tid; i < REP * hd / 2; i += SPL_THREADS) {
+        const int hh = i / (hd / 2), j = i % (hd / 2);
+        const float *q0 = qk + (int64_t)(kvh * REP + hh) * hd;
+        const float a = q0[2 * j], b = q0[2 * j + 1], cc = cr[j], sn = sr[j];
+        qs[hh * hd + 2 * j] = a * cc - b * sn;
+        qs[hh * hd + 2 * j + 1] = a * sn + b * cc;
+    }
+    if (has_pos) {
+        const float *k0 = qk + (int64_t)n_head * hd + (int64_t)kvh * hd;
+        if (tid < hd / 2) {
+            const float a = k0[2 * tid], b = k0[2 * tid + 1], cc = cr[tid], sn = sr[tid];
+            ks[2 * tid] = a * cc - b * sn;
+            ks[2 * tid + 1] = a * sn + b * cc;
+        } else if (tid >= 128 && tid < 128 + hd) {
+            vs[tid - 128] = v[(int64_t)kvh * hd + tid - 128];
+        }
+    }
+    __syncthreads();
+    if (has_pos) {
+        if (tid < hd) {
+            kh[(int64_t)pos * hd + tid] = ks[tid];
+            vh[(int64_t)pos * hd + tid] = vs[tid];
+        }
+#pragma unroll
+        for (int u = 0; u < KU; u++)
+            if (u * RPP + wave * RPI + lane / HD4 == np - 1) kv0[u] = ((const float4 *)ks)[c];
+#pragma unroll
+        for (int u = 0; u < VU; u++)
+            if (g + u * G == np - 1) vp[u] = ((const float4 *)vs)[d4];
+    }
+
+    // scores: HD4 lanes per key row (lane c holds float4 c of each query
+    // head), the row's REP dots summed over the lane group
+    float4 qv[REP];
+#pragma unroll
+    for (int hh = 0; hh < REP; hh++) qv[hh] = ((const float4 *)(qs + hh * hd))[c];
+    const float rs = sqrtf((float)hd);
+    auto score_rows = [&](const float4 *kv, int b0, int nu) {
+        for (int u = 0; u < nu; u++) {
+            const int i = b0 + u * RPP + wave * RPI + lane / HD4;
+#pragma unroll
+            for (int hh = 0; hh < REP; hh++) {
+                const float d = group_sum<HD4>(dot4(qv[hh], kv[u]));
+                if (i < np && c == 0) sc[hh * SPL_MAX_LEN + i] = d / rs;
+            }
+        }
+    };
+    score_rows(kv0, 0, KU);
+    for (int b0 = KU * RPP; b0 < np; b0 += KU * RPP) {  // slices longer than the minimum
+        float4 kv[KU];
+#pragma unroll
+        for (int u = 0; u < KU; u++) {
+            const int i = b0 + u * RPP + wave * RPI + lane / HD4, p = p0 + i;
+            kv[u] = ZERO4;
+            if (i < np) kv[u] = p < pos ? ((const float4 *)(kh + (int64_t)p * hd))[c] : ((const float4 *)ks)[c];
+        }
+        score_rows(kv, b0, KU);
+    }
+    __syncthreads();
+
+    // per query head: the slice's max and e_p = exp(score - max), one wave per head
+    for (int hh = wave; hh < REP; hh += SPL_THREADS / 64) {
+        float mx = -INFINITY;
+        for (int i = lane; i < np; i += 64) mx = fmaxf(mx, sc[hh * SPL_MAX_LEN + i]);
+        mx = wave_max_f(mx);
+        float sum = 0.0f;
+        for (int i = lane; i < np; i += 64) {
+            const float e = expf(sc[hh * SPL_MAX_LEN + i] - mx);
+            sc[hh * SPL_MAX_LEN + i] = e;
+            sum += e;
+        }
+        sum = wave_sum_f(sum);
+        if (lane == 0) {
+            pw[REP * hd + hh] = mx;
+            pw[REP * hd + SPL_MAX_REP + hh] = sum;
+        }
+    }
+    __syncthreads();
+
+    // o[hh][d] = sum_p e_p v_p[d]: thread (d4, g) takes positions g (mod G)
+    float4 acc[REP];
+#pragma unroll
+    for (int hh = 0; hh < REP; hh++) acc[hh] = ZERO4;
+#pragma unroll
+    for (int u = 0; u < VU; u++) {
+        const int i = g + u * G;
+        if (i < np) {
+#pragma unroll
+            for (int hh = 0; hh < REP; hh++) axpy4(acc[hh], sc[hh * SPL_MAX_LEN + i], vp[u]);
+        }
+    }
+    for (int i0 = g + VU * G; i0 < np; i0 += 2 * G) {
+        float4 v4[2];
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const int i = i0 + u * G, p = p0 + i;
+            v4[u] = ZERO4;
+            if (i < np) v4[u] = p < pos ? *(const float4 *)(vh + (int64_t)p * hd + 4 * d4) : ((const float4 *)vs)[d4];
+        }
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const int i = i0 + u * G;
+            if (i < np) {
+#pragma unroll
+                for (int hh = 0; hh < REP; hh++) axpy4(acc[hh], sc[hh * SPL_MAX_LEN + i], v4[u]);
+            }
+        }
+    }
+#pragma unroll
+    for (int hh = 0; hh < REP; hh++) accs[(g * REP + hh) * HD4 + d4] = acc[hh];
+    __syncthreads();
+    for (int f = tid; f < REP * HD4; f += SPL_THREADS) {
+        float4 t = accs[f];
+        for (int gg = 1; gg < G; gg++) {
+            const float4 u4 = accs[gg * REP * HD4 + f];
+            t.x += u4.x;
+            t.y += u4.y;
+            t.z += u4.z;
+            t.w += u4.w;
+        }
+        ((float4 *)pw)[f] = t;  // f = hh * HD4 + d4
+    }
+}
+
+// One wavefront per query head h (kv head h / REP, record slot h % REP).
+// Every lane loads the m, l of slice `lane` and its own output dims of the
+// first CS slices in one round trip; M = max m_s, weights e^(m_s - M) through
+// LDS; then each lane sums its hd / 64 dims over the slices.
+template <int HD4, int REP>
+__global__ __launch_bounds__(64) void attn_combine_kernel(const float *__restrict__ part, const int64_t *__restrict__ d_pos,
+                                                         int max_seq, int S, float *__restrict__ out) {
+    constexpr int hd = 4 * HD4;
+    constexpr int DL = hd / 64;  // output dims per lane
+    constexpr int PSTR = REP * hd + 2 * SPL_MAX_REP;
+    constexpr int CS = 64 / DL;  // slices whose outputs are loaded up front
+    __shared__ float w[SPL_MAX_SLICES];
+    const int h = blockIdx.x, kvh = h / REP, hh = h % REP, lane = threadIdx.x;
+    const int pos = (int)*d_pos;
+    if (pos < 0 || pos >= max_seq) return;
+    int len, ns;
+    split_shape(pos + 1, S, len, ns);
+    const float *pk = part + (int64_t)kvh * S * PSTR;
+    float ov[CS][DL];
+#pragma unroll
+    for (int s2 = 0; s2 < CS; s2++)
+#pragma unroll
+        for (int e = 0; e < DL; e++) ov[s2][e] = s2 < ns ? pk[(int64_t)s2 * PSTR + hh * hd + lane + 64 * e] : 0.0f;
+    float M = -INFINITY;
+    for (int s2 = lane; s2 < ns; s2 += 64) M = fmaxf(M, pk[(int64_t)s2 * PSTR + REP * hd + hh]);
+    M = wave_max_f(M);
+    float L = 0.0f;
+    for (int s2 = lane; s2 < ns; s2 += 64) {
+        const float e = expf(pk[(int64_t)s2 * PSTR + REP * hd + hh] - M);
+        w[s2] = e;
+        L = __builtin_fmaf(e, pk[(int64_t)s2 * PSTR + REP * hd + SPL_MAX_REP + hh], L);
+    }
+    L = wave_sum_f(L);
+    __syncthreads();
+    float o[DL];
+#pragma unroll
+    for (int e = 0; e < DL; e++) o[e] = 0.0f;
+#pragma unroll
+    for (int s2 = 0; s2 < CS; s2++)
+        if (s2 < ns) {
+#pragma unroll
+            for (int e = 0; e < DL; e++) o[e] = __builtin_fmaf(w[s2], ov[s2][e], o[e]);
+        }
+    for (int s2 = CS; s2 < ns; s2++) {
+#pragma unroll
+        for (int e = 0; e < DL; e++) o[e] = __builtin_fmaf(w[s2], pk[(int64_t)s2 * PSTR + hh * hd + lane + 64 * e], o[e]);
+    }
+#pragma unroll
+    for (int e = 0; e < DL; e++) out[(int64_t)h * hd + lane + 64 * e] = o[e] / L;
+}
+
+// ------------------------------------------------------------------ prefill
+// 1) rope_kv_kernel: row i of the prompt (position index_pos + i): rotate its
+//    k heads and store them, and its v heads, in the cache.  One workgroup
+//    per row.
+__global__ __launch_bounds__(256) void rope_kv_kernel(const float *__restrict__ k, int64_t ldk,
+                                                      const float *__restrict__ v, int64_t ldv,
+                                                      const float *__restrict__ cosb, const float *__restrict__ sinb,
+                                                      int index_pos, int n_kv, int hd, int max_seq,
+                                                      float *__restrict__ kc, float *__restrict__ vc) {
+    const int i = blockIdx.x, p = index_pos + i, h2 = hd / 2;
+    const float *kr = k + (int64_t)i * ldk, *vr = v + (int64_t)i * ldv;
+    const float *cr = cosb + (int64_t)p * h2, *sr = sinb + (int64_t)p * h2;
+    for (int j = threadIdx.x; j < n_kv * h2; j += 256) {
+        const int g = j / h2, jj = j % h2;
+        const float a = kr[g * hd + 2 * jj], b = kr[g * hd + 2 * jj + 1], c = cr[jj], sn = sr[jj];
+        float *dst = kc + ((int64_t)g * max_seq + p) * hd + 2 * jj;
+        dst[0] = a * c - b * sn;
+        dst[1] = a * sn + b * c;
+    }
+    for (int j = threadIdx.x; j < n_kv * hd; j += 256) {
+        const int g = j / hd, d = j % hd;
+        vc[((int64_t)g * max_seq + p) * hd + d] = vr[j];
+    }
+}
+
+// 2) attn_prefill_kernel: grid (ceil(m / 64) query tiles, n_head), 256
+//    threads.  The workgroup's 64 query rows (rotated at their positions) sit
+//    in LDS; key/value tiles of 64 cached positions stream through LDS up to
+//    the tile's last position; scores, the causal mask and an online softmax
+//    (running max and sum per row, the output rescaled when the max grows)
+//    are kept in registers.  Thread (rg = tid / 16, cg = tid % 16) owns query
+//    rows rg + 16a (a < 4), key columns cg + 16b (b < 4) of each score tile
+//    and output float4 columns cg + 16e (e < hd / 64).  LDS rows are padded
+//    by 4 floats so the 16 lanes of a row group read 16 different banks.
+constexpr int PF_QT = 64, PF_KT = 64, PF_PAD = 4;
+
+template <int HD>
+__global__ __launch_bounds__(256) void attn_prefill_kernel(const float *__restrict__ q, int64_t ldq,
+                                                           const float *__restrict__ cosb,
+                                                           const float *__restrict__ sinb,
+                                                           const float *__restrict__ kc, const float *__restrict__ vc,
+                                                           int index_pos, int m, int n_head, int n_kv, int max_seq,
+                                                           float *__restrict__ out) {
+    constexpr int HS = HD + PF_PAD;
+    constexpr int PS = PF_KT + PF_PAD;
+    constexpr int DV = HD / 64;  // output float4 columns per thread
+    __shared__ __align__(16) float qs[PF_QT * HS];
+    __shared__ __align__(16) float ks[PF_KT * HS];
+    __shared__ __align__(16) float vs[PF_KT * HS];
+    __shared__ __align__(16) float ps[PF_QT * PS];
+    const int tid = threadIdx.x, h = blockIdx.y, rg = tid / 16, cg = tid % 16;
+    const int kvh = h / (n_head / n_kv);
+    const int r0 = blockIdx.x * PF_QT;
+    const int rows = min(PF_QT, m - r0);
+    const float *kh = kc + (int64_t)kvh * max_seq * HD;
+    const float *vh = vc + (int64_t)kvh * max_seq * HD;
+
+    for (int i = tid; i < PF_QT * HD / 2; i += 256) {
+        const int r = i / (HD / 2), j = i % (HD / 2);
+        float a = 0.0f, b = 0.0f, c = 0.0f, sn = 0.0f;
+        if (r < rows) {
+            const float *qr = q + (int64_t)(r0 + r) * ldq + (int64_t)h * HD;
+            const int64_t p = index_pos + r0 + r;
+            a = qr[2 * j];
+            b = qr[2 * j + 1];
+            c = cosb[p * (HD / 2) + j];
+            sn = sinb[p * (HD / 2) + j];
+        }
+        qs[r * HS + 2 * j] = a * c - b * sn;
+        qs[r * HS + 2 * j + 1] = a * sn + b * c;
+    }
+
+    float mrun[4], lrun[4];
+    float4 o[4][DV];
+#pragma unroll
+    for (int a = 0; a < 4; a++) {
+        mrun[a] = -INFINITY;
+        lrun[a] = 0.0f;
+#pragma unroll
+        for (int e = 0; e < DV; e++) o[a][e] = ZERO4;
+    }
+    const float rs = sqrtf((float)HD);
+    const int kend = index_pos + r0 + rows;  // keys 0..kend-1 (the tile's last query position)
+    for (int k0 = 0; k0 < kend; k0 += PF_KT) {
+        __syncthreads();  // the previous tile's reads of ks, vs, ps are done (and qs is written)
+        for (int i = tid; i < PF_KT * HD / 4; i += 256) {
+            const int c = i / (HD / 4), d4 = i % (HD / 4);
+            float4 kv = ZERO4, vv = ZERO4;
+            if (k0 + c < kend) {
+                kv = *(const float4 *)(kh + (int64_t)(k0 + c) * HD + 4 * d4);
+                vv = *(const float4 *)(vh + (int64_t)(k0 + c) * HD + 4 * d4);
+            }
+            *(float4 *)&ks[c * HS + 4 * d4] = kv;
+            *(float4 *)&vs[c * HS + 4 * d4] = vv;
+        }
+        __syncthreads();
+        float sacc[4][4];
+#pragma unroll
+        for (int a = 0; a < 4; a++)
+#pragma unroll
+            for (int b = 0; b < 4; b++) sacc[a][b] = 0.0f;
+#pragma unroll 4
+        for (int d = 0; d < HD; d += 4) {
+            float4 qv[4], kv[4];
+#pragma unroll
+            for (int a = 0; a < 4; a++) qv[a] = *(const float4 *)&qs[(rg + 16 * a) * HS + d];
+#pragma unroll
+            for (int b = 0; b < 4; b++) kv[b] = *(const float4 *)&ks[(cg + 16 * b) * HS + d];
+#pragma unroll
+            for (int a = 0; a < 4; a++)
+#pragma unroll
+                for (int b = 0; b < 4; b++) {
+                    float t = sacc[a][b];
+                    t = __builtin_fmaf(qv[a].x, kv[b].x, t);
+                    t = __builtin_fmaf(qv[a].y, kv[b].y, t);
+                    t = __builtin_fmaf(qv[a].z, kv[b].z, t);
+                    t = __builtin_fmaf(qv[a].w, kv[b].w, t);
+                    sacc[a][b] = t;
+                }
+        }
+#pragma unroll
+        for (int a = 0; a < 4; a++) {
+            const int r = rg + 16 * a, qpos = index_pos + r0 + r;
+            float sv[4], tmax = -INFINITY;
+#pragma unroll
+            for (int b = 0; b < 4; b++) {
+                const int kp = k0 + cg + 16 * b;
+                sv[b] = kp > qpos ? -INFINITY : sacc[a][b] / rs;
+                tmax = fmaxf(tmax, sv[b]);
+            }
+            tmax = group16_max(tmax);
+            const float mnew = fmaxf(mrun[a], tmax);  // finite: key 0 is never masked
+            const float scale = expf(mrun[a] - mnew);
+            float psum = 0.0f;
+#pragma unroll
+            for (int b = 0; b < 4; b++) {
+                const float e = expf(sv[b] - mnew);
+                ps[r * PS + cg + 16 * b] = e;
+                psum += e;
+            }
+            psum = group_sum<16>(psum);
+            lrun[a] = __builtin_fmaf(lrun[a], scale, psum);
+            mrun[a] = mnew;
+#pragma unroll
+            for (int e = 0; e < DV; e++) {
+                o[a][e].x *= scale;
+                o[a][e].y *= scale;
+                o[a][e].z *= scale;
+                o[a][e].w *= scale;
+            }
+        }
+        __syncthreads();
+        const int kn = min(PF_KT, kend - k0);
+        for (int c = 0; c < kn; c += 4) {
+            float4 pv[4];
+#pragma unroll
+            for (int a = 0; a < 4; a++) pv[a] = *(const float4 *)&ps[(rg + 16 * a) * PS + c];
+#pragma unroll
+            for (int cc = 0; cc < 4; cc++) {
+#pragma unroll
+                for (int e = 0; e < DV; e++) {
+                    const float4 vv = *(const float4 *)&vs[(c + cc) * HS + 4 * (cg + 16 * e)];
+#pragma unroll
+                    for (int a = 0; a < 4; a++) {
+                        const float w = cc == 0 ? pv[a].x : cc == 1 ? pv[a].y : cc == 2 ? pv[a].z : pv[a].w;
+                        axpy4(o[a][e], w, vv);
+                    }
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int a = 0; a < 4; a++) {
+        const int r = rg + 16 * a;
+        if (r < rows) {
+            float *orow = out + (int64_t)(r0 + r) * n_head * HD + (int64_t)h * HD;
+            const float L = lrun[a];
+#pragma unroll
+            for (int e = 0; e < DV; e++)
+                ((float4 *)orow)[cg + 16 * e] = make_float4(o[a][e].x / L, o[a][e].y / L, o[a][e].z / L, o[a][e].w / L);
+        }
+    }
+}
+
+template <int HD4, int REP>
+void launch_split(dim3 grid, const float *qk, const float *v, const float *cosb, const float *sinb,
+                  const int64_t *d_pos, float *kc, float *vc, int n_head, int max_seq, int S, float *part, float *out,
+                  hipStream_t s) {
+    attn_split_kernel<HD4, REP><<<grid, SPL_THREADS, 0, s>>>(qk, v, cosb, sinb, d_pos, kc, vc, n_head, max_seq, S,
+                                                            part);
+    attn_combine_kernel<HD4, REP><<<(unsigned)n_head, 64, 0, s>>>(part, d_pos, max_seq, S, out);
+}
+
+}  // namespace
+
+int attn_split_slices(int64_t n_kv, int64_t max_seq) {
+    int64_t S = 256 / n_kv;
+    if (S < 32) S = 32;
+    while (S * SPL_MAX_LEN < max_seq) S *= 2;
+    return S > SPL_MAX_SLICES ? 0 : (int)S;
+}
+
+size_t attn_split_workspace_bytes(int64_t n_head, int64_t n_kv, int64_t hd, int64_t max_seq) {
+    const int S = attn_split_slices(n_kv, max_seq);
+    if (S == 0) return (size_t)-1;
+    const int64_t rep = n_head / n_kv;
+    return (size_t)(n_kv * S) * (size_t)(rep * hd + 2 * SPL_MAX_REP) * 4;
+}
+
+hipError_t launch_attn_split(const float *qk, const float *v, const float *cosb, const float *sinb,
+                             const int64_t *d_pos, float *kc, float *vc, int64_t n_head, int64_t n_kv, int64_t hd,
+                             int64_t max_seq, float *out, float *part, size_t part_bytes, hipStream_t s) {
+    if (n_head <= 0 || n_kv <= 0 || n_head % n_kv || n_kv > 65535) return hipErrorNotSupported;
+    const int64_t rep = n_head / n_kv;
+    if ((hd != 64 && hd != 128) || (rep != 1 && rep != 2 && rep != 4 && rep != 8)) return hipErrorNotSupported;
+    const int S = attn_split_slices(n_kv, max_seq);
+    if (S == 0 || attn_split_workspace_bytes(n_head, n_kv, hd, max_seq) > part_bytes) return hipErrorNotSupported;
+    const dim3 grid((unsigned)S, (unsigned)n_kv);
+    const int nh = (int)n_head, ms = (int)max_seq;
+#define AQ_SPLIT(H4, R) launch_split<H4, R>(grid, qk, v, cosb, sinb, d_pos, kc, vc, nh, ms, S, part, out, s)
+    if (hd == 64) {
+        switch (rep) {
+        case 1: AQ_SPLIT(16, 1); break;
+        case 2: AQ_SPLIT(16, 2); break;
+        case 4: AQ_SPLIT(16, 4); break;
+        default: AQ_SPLIT(16, 8); break;
+        }
+    } else {
+        switch (rep) {
+        case 1: AQ_SPLIT(32, 1); break;
+        case 2: AQ_SPLIT(32, 2); break;
+        case 4: AQ_SPLIT(32, 4); break;
+        default: AQ_SPLIT(32, 8); break;
+        }
+    }
+#undef AQ_SPLIT
+    return hipGetLastError();
+}
+
+hipError_t launch_attn_prefill(const float *q, int64_t ldq, const float *k, int64_t ldk, const float *v, int64_t ldv,
+                               const float *cosb, const float *sinb, int64_t index_pos, int64_t m, float *kc,
+                               float *vc, int64_t n_head, int64_t n_kv, int64_t hd, int64_t max_seq, float *out,
+                               hipStream_t s) {
+    if (!q || !k || !v || !cosb || !sinb || !kc || !vc || !out) return hipErrorInvalidValue;
+    if (m <= 0 || index_pos < 0 || max_seq <= 0 || index_pos + m > max_seq || max_seq > 0x7fffffff ||
+        n_head <= 0 || n_kv <= 0 || n_head % n_kv || n_head > 65535)
+        return hipErrorInvalidValue;
+    if (hd != 64 && hd != 128) return hipErrorNotSupported;
+    if (ldq < n_head * hd || ldk < n_kv * hd || ldv < n_kv * hd) return hipErrorInvalidValue;
+    if (((uintptr_t)kc | (uintptr_t)vc | (uintptr_t)out) & 15) return hipErrorInvalidValue;
+    rope_kv_kernel<<<(unsigned)m, 256, 0, s>>>(k, ldk, v, ldv, cosb, sinb, (int)index_pos, (int)n_kv, (int)hd,
+                                               (int)max_seq, kc, vc);
+    const dim3 grid((unsigned)((m + PF_QT - 1) / PF_QT), (unsigned)n_head);
+    if (hd == 64)
+        attn_prefill_kernel<64><<<grid, 256, 0, s>>>(q, ldq, cosb, sinb, kc, vc, (int)index_pos, (int)m, (int)n_head,
+                                                     (int)n_kv, (int)max_seq, out);
+    else
+        attn_prefill_kernel<128><<<grid, 256, 0, s>>>(q, ldq, cosb, sinb, kc, vc, (int)index_pos, (int)m,
+                                                      (int)n_head, (int)n_kv, (int)max_seq, out);
+    return hipGetLastError();
+}
+
+}  // namespace aq

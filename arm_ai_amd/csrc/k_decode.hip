@@ -53,16 +53,18 @@ __device__ __forceinline__ float block_max(float v, float *red) {
     return s;
 }
 
-// out = embedding row *d_tok (a token id outside [0, vocab) gives zeros).
-// hidden % 4 == 0 (checked by the launcher): float4 copies.
+// out row r = embedding row d_tok[r] (a token id outside [0, vocab) gives
+// zeros); one workgroup per row.  hidden % 4 == 0 (checked by the launcher):
+// float4 copies.
 __global__ __launch_bounds__(DEC_THREADS) void embed_kernel(const float *__restrict__ table, int64_t vocab,
                                                             const int64_t *__restrict__ d_tok, int hidden,
                                                             float *__restrict__ out) {
-    const int64_t t = *d_tok;
+    const int64_t t = d_tok[blockIdx.x];
     const bool ok = t >= 0 && t < vocab;
     const float4 *src = (const float4 *)(table + (ok ? t : 0) * hidden);
+    float4 *dst = (float4 *)(out + (int64_t)blockIdx.x * hidden);
     for (int i = threadIdx.x; i < hidden / 4; i += DEC_THREADS)
-        ((float4 *)out)[i] = ok ? src[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        dst[i] = ok ? src[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 }
 
 // One row per workgroup: x += delta (when delta is given, written back to x:
@@ -113,13 +115,15 @@ __global__ __launch_bounds__(DEC_THREADS) void rmsnorm_kernel(float *__restrict_
     }
 }
 
-// out = silu(g) * u.  gu = [g (n) | u (n)] (the merged w1|w3 output).
-__global__ __launch_bounds__(DEC_THREADS) void silu_mul_kernel(const float *__restrict__ gu, int64_t n,
-                                                               float *__restrict__ out) {
+// out[r][i] = silu(g[r][i]) * u[r][i] for rows r (grid y) of n; row r of g
+// and u starts at r * ld (the merged w1|w3 output: u = g + n, ld = 2n).
+__global__ __launch_bounds__(DEC_THREADS) void silu_mul_kernel(const float *__restrict__ g, const float *__restrict__ u,
+                                                               int64_t ld, int64_t n, float *__restrict__ out) {
     const int64_t i = (int64_t)blockIdx.x * DEC_THREADS + threadIdx.x;
     if (i >= n) return;
-    const float g = gu[i];
-    out[i] = (g / (1.0f + expf(-g))) * gu[n + i];
+    const int64_t r = blockIdx.y;
+    const float gv = g[r * ld + i];
+    out[r * n + i] = (gv / (1.0f + expf(-gv))) * u[r * ld + i];
 }
 
 // Sum over aligned groups of N lanes (N = 2, 4, 8, 16, 32 or 64), every lane
@@ -388,11 +392,12 @@ __global__ __launch_bounds__(WIDE_THREADS) void argmax_kernel(const float *__res
 
 }  // namespace
 
-hipError_t launch_embed(const float *table, int64_t vocab, const int64_t *d_tok, int64_t hidden, float *out,
+hipError_t launch_embed(const float *table, int64_t vocab, const int64_t *d_tok, int64_t m, int64_t hidden, float *out,
                         hipStream_t s) {
-    if (!table || !d_tok || !out || vocab <= 0 || hidden <= 0 || hidden % 4 || hidden > 0x7fffffff)
+    if (!table || !d_tok || !out || vocab <= 0 || hidden <= 0 || hidden % 4 || hidden > 0x7fffffff || m <= 0 ||
+        m > 0x7fffffff || (((uintptr_t)table | (uintptr_t)out) & 15))
         return hipErrorInvalidValue;
-    embed_kernel<<<1, DEC_THREADS, 0, s>>>(table, vocab, d_tok, (int)hidden, out);
+    embed_kernel<<<(unsigned)m, DEC_THREADS, 0, s>>>(table, vocab, d_tok, (int)hidden, out);
     return hipGetLastError();
 }
 
@@ -404,9 +409,10 @@ hipError_t launch_rmsnorm(float *x, const float *delta, const float *w, int64_t 
     return hipGetLastError();
 }
 
-hipError_t launch_silu_mul(const float *gu, int64_t n, float *out, hipStream_t s) {
-    if (!gu || !out || n <= 0) return hipErrorInvalidValue;
-    silu_mul_kernel<<<(unsigned)((n + DEC_THREADS - 1) / DEC_THREADS), DEC_THREADS, 0, s>>>(gu, n, out);
+hipError_t launch_silu_mul(const float *g, const float *u, int64_t ld, int64_t m, int64_t n, float *out, hipStream_t s) {
+    if (!g || !u || !out || n <= 0 || m <= 0 || m > 65535 || (m > 1 && ld < n)) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)((n + DEC_THREADS - 1) / DEC_THREADS), (unsigned)m);
+    silu_mul_kernel<<<grid, DEC_THREADS, 0, s>>>(g, u, ld, n, out);
     return hipGetLastError();
 }
 

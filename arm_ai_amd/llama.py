@@ -11,9 +11,10 @@ token, which is where the time goes.
 Here those 155 calls are this library's GPU QMatMuls (the product, through the
 C ABI, device pointers, on the context's HIP stream).  The operations between
 them (token embedding, RMSNorm, interleaved RoPE, grouped-query attention with
-a KV cache, SiLU gate, residual adds, argmax) are not part of the quantized
-matmul path; they run as PyTorch f32 operations enqueued on the same stream,
-so the whole step stays on the GPU.  They follow candle-transformers 0.8.4
+a KV cache, SiLU gate, residual adds, argmax) are the library's f32 glue
+kernels on the same stream (k_decode.hip, k_attn.hip), so the whole forward
+stays on the GPU; torch only allocates the device buffers.  They follow
+candle-transformers 0.8.4
 ``quantized_llama`` (a registry dependency of native/arm_ai_nif/Cargo.lock, not
 vendored in the reference):
 
@@ -30,9 +31,9 @@ vendored in the reference):
 
 The decode step (one token at a given position) can be captured once into a
 HIP graph and replayed per token (``Llama.generate(..., graph=True)``).  That
-step does not use torch ops: it is this library's decode-step glue kernels
-(k_decode.hip: embedding, residual add + RMSNorm, RoPE + KV-cache write +
-grouped-query attention in one launch, and a first-maximum argmax that writes
+step uses the decode forms of the glue kernels (embedding, residual add +
+RMSNorm, RoPE + KV-cache write + grouped-query attention with the context
+split over workgroups in one launch, and a first-maximum argmax that writes
 the next token and advances the device-side position) around the GPU
 QMatMuls, whose matvec forms its own input where that input is
 rms_norm(x + delta) or silu(g) * u: 5 launches per layer (wq|wk and wv share one).  Projections that share an input and a
@@ -47,7 +48,6 @@ from __future__ import annotations
 
 import contextlib
 import ctypes
-import math
 import time
 from dataclasses import dataclass, field
 
@@ -290,9 +290,9 @@ class Llama:
         finally:
             self._hidden = None
 
-    def _record_hidden(self, li, x):
+    def _record_hidden(self, li, x, delta=None):
         if self._hidden is not None and li in self._hidden["layers"]:
-            self._hidden["x"][li] = x.cpu().numpy()
+            self._hidden["x"][li] = (x + delta if delta is not None else x).cpu().numpy()
 
     @contextlib.contextmanager
     def trace_matmuls(self, rows=(0,), full_layers=()):
@@ -309,78 +309,63 @@ class Llama:
         finally:
             self._trace = None
 
-    def _rms_norm(self, x, w):
-        torch = self.torch
-        return x * torch.rsqrt(torch.mean(x * x, dim=-1, keepdim=True) + self.cfg.rms_eps) * w
-
-    def _rope(self, x, cos, sin):
-        """rope_i: rotate interleaved pairs (x[2i], x[2i+1]); x [L, H, D], cos/sin [L, D/2]."""
-        L, H, D = x.shape
-        xp = x.reshape(L, H, D // 2, 2)
-        x0, x1 = xp[..., 0], xp[..., 1]
-        c, s = cos[:, None, :], sin[:, None, :]
-        return self.torch.stack((x0 * c - x1 * s, x0 * s + x1 * c), dim=-1).reshape(L, H, D)
-
-    def _attend(self, q, k, v, mask):
-        """q [H, Lq, D], k/v [Hkv, Lk, D]; mask [Lq, Lk] bool (True = masked) or None."""
-        torch = self.torch
-        cfg = self.cfg
-        rep = cfg.n_head // cfg.n_kv_head
-        k = k.repeat_interleave(rep, dim=0)
-        v = v.repeat_interleave(rep, dim=0)
-        att = torch.matmul(q, k.transpose(1, 2).contiguous()) / math.sqrt(cfg.head_dim)
-        if mask is not None:
-            att = att.masked_fill(mask, float("-inf"))
-        att = torch.softmax(att, dim=-1)
-        return torch.matmul(att, v.contiguous())
-
-    def _layer_tail(self, i, x, y):
-        """wo, residual, FFN and its residual for layer i; y = attention output [L, H*D]."""
-        lw = self.layers[i]
-        h = x + self._mm(lw["wo"], y)
-        n = self._rms_norm(h, self.ffn_norm[i])
-        g, u = self._pair(lw, "w13", "w1", "w3", n)
-        return h + self._mm(lw["w2"], self.torch.nn.functional.silu(g) * u)
-
     # ------------------------------------------------------------ forward
     def forward(self, tokens, index_pos: int):
         """ModelWeights::forward(&x[1, L], index_pos) -> logits f32 [vocab] of the last position.
 
-        tokens: a torch int64 tensor [L] on the device, or a sequence of ints."""
+        tokens: a torch int64 tensor [L] on the device, or a sequence of ints.
+        Every step is a library kernel on the context's stream (torch only
+        allocates): the embedding rows; per layer rms_norm (with the pending
+        residual add of the previous layer's w2 output, written back to the
+        stream), wq|wk and wv, rotary embedding + KV append + causal
+        grouped-query attention (aq_llama_attn_prefill), wo, the residual add
+        and rms_norm, w1|w3, silu(g) * u, w2; the final rms_norm of the last
+        row and the output head."""
+        from . import _lib
+
         torch = self.torch
         cfg = self.cfg
+        L = _lib.load()
+        c = self.ctx.handle
+        chk = _lib.check
+        eps = ctypes.c_float(cfg.rms_eps)
+        ptr = lambda t: t.data_ptr()
         self._enter()
         with torch.cuda.stream(self.stream):
             if not torch.is_tensor(tokens):
                 tokens = torch.tensor(list(tokens), dtype=torch.int64, device=self.dev)
-            L = int(tokens.shape[0])
-            if L == 0 or index_pos + L > cfg.max_seq:
-                raise ValueError(f"positions {index_pos}..{index_pos + L} outside 0..{cfg.max_seq}")
+            tokens = tokens.contiguous()
+            n = int(tokens.shape[0])
+            if n == 0 or index_pos < 0 or index_pos + n > cfg.max_seq:
+                raise ValueError(f"positions {index_pos}..{index_pos + n} outside 0..{cfg.max_seq}")
             H, Hkv, D = cfg.n_head, cfg.n_kv_head, cfg.head_dim
-            cos = self.cos[index_pos:index_pos + L]
-            sin = self.sin[index_pos:index_pos + L]
-            end = index_pos + L
-            mask = None
-            if L > 1:  # candle builds the causal mask whenever more than one position is fed
-                i = torch.arange(L, device=self.dev)[:, None]
-                j = torch.arange(end, device=self.dev)[None, :]
-                mask = j > (i + index_pos)
-            x = self.tok_embeddings[tokens]
+            f32 = dict(dtype=torch.float32, device=self.dev)
+            x = torch.empty((n, cfg.hidden), **f32)  # the residual stream (x + delta once delta is set)
+            h = torch.empty((n, cfg.hidden), **f32)  # normed input of the next projections
+            y = torch.empty((n, H * D), **f32)       # attention output
+            a = torch.empty((n, cfg.ffn), **f32)     # silu(g) * u
+            chk(L.aq_llama_embed_rows(c, ptr(self.tok_embeddings), cfg.vocab, ptr(tokens), n, cfg.hidden, ptr(x)))
+            delta = None
             for li, lw in enumerate(self.layers):
                 self._trace_layer = li
-                self._record_hidden(li, x)
-                n = self._rms_norm(x, self.attn_norm[li])
-                q, k = self._pair(lw, "wqk", "wq", "wk", n)
-                q = self._rope(q.reshape(L, H, D), cos, sin)
-                k = self._rope(k.reshape(L, Hkv, D), cos, sin)
-                v = self._mm(lw["wv"], n).view(L, Hkv, D)
-                self.k_cache[li, :, index_pos:end] = k.transpose(0, 1)
-                self.v_cache[li, :, index_pos:end] = v.transpose(0, 1)
-                y = self._attend(q.transpose(0, 1), self.k_cache[li, :, :end], self.v_cache[li, :, :end], mask)
-                x = self._layer_tail(li, x, y.transpose(0, 1).reshape(L, H * D))
+                self._record_hidden(li, x, delta)
+                chk(L.aq_llama_rmsnorm(c, ptr(x), ptr(delta) if delta is not None else None, ptr(self.attn_norm[li]),
+                                       n, cfg.hidden, eps, ptr(h)))
+                q, k = self._pair(lw, "wqk", "wq", "wk", h)
+                v = self._mm(lw["wv"], h)
+                chk(L.aq_llama_attn_prefill(c, ptr(q), q.stride(0), ptr(k), k.stride(0), ptr(v), v.stride(0),
+                                            ptr(self.cos), ptr(self.sin), index_pos, n, ptr(self.k_cache[li]),
+                                            ptr(self.v_cache[li]), H, Hkv, D, cfg.max_seq, ptr(y)))
+                o = self._mm(lw["wo"], y)
+                chk(L.aq_llama_rmsnorm(c, ptr(x), ptr(o), ptr(self.ffn_norm[li]), n, cfg.hidden, eps, ptr(h)))
+                g, u = self._pair(lw, "w13", "w1", "w3", h)
+                chk(L.aq_llama_silu_mul_rows(c, ptr(g), ptr(u), g.stride(0), n, cfg.ffn, ptr(a)))
+                delta = self._mm(lw["w2"], a)
             self._trace_layer = len(self.layers)
-            self._record_hidden(len(self.layers), x)
-            last = self._rms_norm(x[L - 1:L], self.norm)
+            self._record_hidden(len(self.layers), x, delta)
+            last = torch.empty((1, cfg.hidden), **f32)
+            chk(L.aq_llama_rmsnorm(c, ptr(x[n - 1:]), ptr(delta[n - 1:]), ptr(self.norm), 1, cfg.hidden, eps,
+                                   ptr(last)))
             logits = self._mm(self.output, last)[0]
         self._leave()
         return logits

@@ -263,16 +263,41 @@ int aq_llama_rmsnorm(aq_ctx *ctx, float *d_x, const float *d_delta, const float 
                      float *d_out);
 /* d_out[i] = silu(g[i]) * u[i] for i < n, with d_gu = [g (n) | u (n)]. */
 int aq_llama_silu_mul(aq_ctx *ctx, const float *d_gu, int64_t n, float *d_out);
+/* The prompt's forms of embed and silu_mul (m rows, m <= 65535 for silu):
+ * d_out row r = table row d_tok[r]; d_out[r][i] = silu(d_g[r*ld + i]) *
+ * d_u[r*ld + i] for i < n (the merged w1|w3 output: d_u = d_g + n, ld = 2n). */
+int aq_llama_embed_rows(aq_ctx *ctx, const float *d_table, int64_t vocab, const int64_t *d_tok, int64_t m,
+                        int64_t hidden, float *d_out);
+int aq_llama_silu_mul_rows(aq_ctx *ctx, const float *d_g, const float *d_u, int64_t ld, int64_t m, int64_t n,
+                           float *d_out);
 /* Attention of one query position *d_pos (0 <= pos < max_seq): d_qk =
  * [q (n_head*head_dim) | k (n_kv*head_dim)], d_v (n_kv*head_dim), before
  * rotary embedding; d_cos / d_sin [max_seq][head_dim/2]; caches
  * [n_kv][max_seq][head_dim] for one layer.  Rotates q and k (interleaved
  * pairs), stores k and v at pos, and writes softmax(q.k/sqrt(head_dim)).v
  * over positions 0..pos for each query head to d_out (n_head*head_dim).
- * head_dim must divide 256 and be a multiple of 4; max_seq <= 8192. */
+ * head_dim must divide 256 and be a multiple of 4; max_seq <= 8192; caches
+ * and d_out 16-byte aligned.  For head_dim 64 or 128 with 1, 2, 4 or 8 query
+ * heads per kv head, the context is split over workgroups whose partial
+ * results go to the context's attention workspace and are combined by a
+ * second launch: calls on one context must not overlap (they are ordered
+ * on its stream). */
 int aq_llama_attn_decode(aq_ctx *ctx, const float *d_qk, const float *d_v, const float *d_cos, const float *d_sin,
                          const int64_t *d_pos, float *d_kcache, float *d_vcache, int64_t n_head, int64_t n_kv,
                          int64_t head_dim, int64_t max_seq, float *d_out);
+/* Attention of the m prompt positions index_pos .. index_pos + m - 1
+ * (index_pos + m <= max_seq; candle feeds the prompt at offset 0,
+ * llama_candle.rs:93): row r of q, k, v starts at d_q + r*ldq, d_k + r*ldk,
+ * d_v + r*ldv (n_head*head_dim, n_kv*head_dim, n_kv*head_dim values, before
+ * rotary embedding).  Rotates k and stores k and v of every row in the
+ * caches, then writes the causal softmax(q.k/sqrt(head_dim)).v over
+ * positions 0 .. its own for every row and query head to d_out
+ * [m][n_head*head_dim].  head_dim 64 or 128 (AQ_ERR_SHAPE otherwise); caches
+ * and d_out 16-byte aligned. */
+int aq_llama_attn_prefill(aq_ctx *ctx, const float *d_q, int64_t ldq, const float *d_k, int64_t ldk, const float *d_v,
+                          int64_t ldv, const float *d_cos, const float *d_sin, int64_t index_pos, int64_t m,
+                          float *d_kcache, float *d_vcache, int64_t n_head, int64_t n_kv, int64_t head_dim,
+                          int64_t max_seq, float *d_out);
 /* aq_qmatmul_f32_device for one row (m = 1) whose input is formed inside the
  * matmul kernel, so the step needs no separate launch for it:
  * rmsnorm: input = rms_norm(d_x + d_delta) * d_norm_w (eps as aq_llama_rmsnorm;
