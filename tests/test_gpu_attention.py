@@ -9,9 +9,10 @@ computes it in f32).
 Decode: the split-context kernels (head_dim 64 / 128, 1..8 query heads per kv
 head; a partial record per slice, then a combining launch) at positions on
 and around the slice boundaries, up to the longest context, called back to
-back on one context (the partial records are reused by every call).  Prefill: prompts at offset 0 and later,
-lengths that are not a multiple of the 64-row query tile, q / k / v read
-with row strides from one merged buffer."""
+back on one context (the partial records are reused by every call).
+Prefill: prompts at offset 0 and later, lengths that are not a multiple of
+the 64-row query tile, q / k / v read with row strides from one merged
+buffer."""
 import ctypes
 
 import numpy as np
@@ -89,9 +90,9 @@ def _decode_call(torch, lib, ctx, n_head, n_kv, hd, max_seq, kc, vc, qk, v, pos,
 @pytest.mark.parametrize(
     "n_head,n_kv,hd,max_seq,positions",
     [
-        # TinyLlama heads: slices of at least 16 positions, 64 slices of 4 kv heads
-        (32, 4, 64, 1024, [0, 1, 15, 16, 17, 31, 32, 600, 1023]),
-        (32, 4, 64, 8192, [8191, 1024, 1025, 4097]),  # slices longer than 16 (8192 / 64 = 128 per slice)
+        # TinyLlama heads: slices of at least 32 positions, 64 slices of 4 kv heads
+        (32, 4, 64, 1024, [0, 1, 31, 32, 33, 63, 64, 600, 1023]),
+        (32, 4, 64, 8192, [8191, 2048, 2049, 4097]),  # slices longer than 32 (8192 / 64 = 128 per slice)
         (32, 8, 128, 2048, [0, 63, 64, 511, 512, 2047]),  # Llama-3-8B heads: 4 per kv head, 32 slices
         (8, 4, 64, 512, [0, 100, 511]),  # 2 per kv head
         (8, 8, 128, 512, [0, 5, 300]),   # one query head per kv head
