@@ -9,20 +9,23 @@
 // over the 16 sub-blocks j of 16 elements, with S an exact integer (candle's
 // vec_dot keeps it exact too).
 //
-// Exactness on f16 MFMA.  The weight operand is w_e = sc_j * (q6_e - 32):
-// |w| <= 32 * 32 = 1024, an integer, so it is exact in f16; the activation
+// Exactness on f16 MFMA.  Q6_K sub-scales use the whole int8 range
+// (llama.cpp's quantizer maps the largest sub-block scale to -128), so
+// sc_j * (q6_e - 32) reaches 128 * 32 = 4096 and is not exact in f16 (odd
+// integers above 2048).  Each scale is split into two digits, sc = 16 * sh +
+// sl with sh = sc >> 4 in -8..7 and sl = sc & 15 in 0..15, and the weight
+// operand is built twice: w_h = sh * (q6 - 32) (|w_h| <= 256) and w_l = sl *
+// (q6 - 32) (|w_l| <= 480), both integers exact in f16; the activation
 // operand is the Q8_K quant qx (|qx| <= 128), exact in f16.  Each
 // v_mfma_f32_32x32x16_f16 covers one sub-block (K = 16); products are exact in
-// f32, and every partial sum of eight sub-blocks is an integer of magnitude at
-// most 8 * 16 * 1024 * 128 = 2^24, so the f32 accumulator chain over sub-blocks
-// 0..7, and the one over 8..15, hold exact integers whatever the summation
-// order.  S is their sum (converted to int32 for the integer dump; in f32 for
-// the output, where |S| <= 2^25 can round only the last bit of values the
-// BASELINE distributions never reach).
-// The weight operand is built per lane from the 6-bit quants: nibble of ql,
+// f32, and the two accumulator chains over all 16 sub-blocks of a super-block
+// hold exact integers whatever the summation order: |A_h| <= 256 * 256 * 128
+// = 2^23 and |A_l| <= 480 * 256 * 128 < 2^24.  S = 16 A_h + A_l (in int32 for
+// the integer dump; one fma in f32 for the output, exact while |S| < 2^24).
+// Each digit operand is built per lane from the 6-bit quants: nibble of ql,
 // two bits of qh, then 1024 + q as f16 bits (0x6400 | q) and one packed f16
-// fma, (1024 + q) * sc - 1056 * sc, which is exact (the result is an integer
-// of magnitude <= 1024).
+// fma, (1024 + q) * s - 1056 * s for s = sh or sl, which is exact (the result
+// is an integer of magnitude <= 480; 1056 * s has at most 9 significant bits).
 //
 // Tiling.  A workgroup (4 wavefronts, two workgroups per CU) owns a 64 (m) x
 // 128 (n) output tile; wavefront w owns columns 32w..32w+31 and both 32-row
@@ -121,9 +124,10 @@ __device__ __forceinline__ void load_w6(W6 &W, const rsrc_t &rw, const rsrc_t &r
     W.d = __builtin_amdgcn_raw_buffer_load_b16(rwd, ok ? doff + (uint32_t)(b * RB * 2) : BUF_OOB, 0, BUF_NT);
 }
 
-// The 8 f16 weight operands sc_j * (q6 - 32) of sub-block j for this lane
-// (elements 16j + 8h .. 16j + 8h + 7 of its column's super-block).
-__device__ __forceinline__ v8h w6_operand(const W6 &W, int j) {
+// The 8 f16 weight operands of sub-block j for this lane (elements 16j + 8h
+// .. 16j + 8h + 7 of its column's super-block), for the two digits of the
+// sub-scale: rh = sh * (q6 - 32), rl = sl * (q6 - 32), sc_j = 16 sh + sl.
+__device__ __forceinline__ void w6_operands(const W6 &W, int j, v8h &rh, v8h &rl) {
     const int hh = j >> 3, jj = j & 7, qq = jj >> 1, odd = jj & 1;
     const u32x2 ql = W.ql[4 * hh + 2 * (qq & 1) + odd];
     const u32x2 qh = W.qh[2 * hh + odd];
@@ -135,20 +139,22 @@ __device__ __forceinline__ v8h w6_operand(const W6 &W, int j) {
         q[i] = nib | hb;
     }
     const int sc = (int)(int8_t)((W.sc[j >> 2] >> (8 * (j & 3))) & 0xffu);
-    const _Float16 s = (_Float16)sc;
-    const _Float16 o = (_Float16)(-1056 * sc);  // exact: 33 * 32 * |sc| has at most 6 significant bits
-    const h2 s2 = {s, s}, o2 = {o, o};
-    v8h r;
+    const int sh = sc >> 4, sl = sc & 15;  // arithmetic shift: sc = 16 * sh + sl
+    const _Float16 fh = (_Float16)sh, oh = (_Float16)(-1056 * sh);  // |1056 sh| <= 2^8 * 33: exact
+    const _Float16 fl = (_Float16)sl, ol = (_Float16)(-1056 * sl);  // 1056 sl <= 2^5 * 495: exact
+    const h2 sh2 = {fh, fh}, oh2 = {oh, oh}, sl2 = {fl, fl}, ol2 = {ol, ol};
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         // bytes 2i, 2i+1 of q as 16-bit lanes, then 1024 + q as f16
         const uint32_t u = __builtin_amdgcn_perm(0u, q[i >> 1], (i & 1) ? 0x0C030C02u : 0x0C010C00u) | 0x64006400u;
         const h2 f = __builtin_bit_cast(h2, u);
-        const h2 v = __builtin_elementwise_fma(f, s2, o2);
-        r[2 * i] = v[0];
-        r[2 * i + 1] = v[1];
+        const h2 vh = __builtin_elementwise_fma(f, sh2, oh2);
+        const h2 vl = __builtin_elementwise_fma(f, sl2, ol2);
+        rh[2 * i] = vh[0];
+        rh[2 * i + 1] = vh[1];
+        rl[2 * i] = vl[0];
+        rl[2 * i + 1] = vl[1];
     }
-    return r;
 }
 
 __device__ __forceinline__ void load_w5(W5 &W, const rsrc_t &rw, uint32_t off, int b, int ng) {
@@ -258,15 +264,17 @@ __global__ __launch_bounds__(256, 2) void gemm_f16w_kernel(Gemm6Params p) {
     };
 
     auto compute6 = [&](const uint8_t *st, const W6 &W, int b) {
-        v16f acc[2][2];  // [tile][sub-blocks 0..7 / 8..15]
+        v16f acc[2][2];  // [tile][high / low digit of the sub-scales]
 #pragma unroll
         for (int j = 0; j < 16; j++) {
-            const v8h bw = w6_operand(W, j);
+            v8h bh, bl;
+            w6_operands(W, j, bh, bl);
 #pragma unroll
             for (int t = 0; t < 2; t++) {
                 const v16f z = {0};
-                const int c = j >> 3;
-                acc[t][c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(read_a(st, t, j), bw, (j & 7) == 0 ? z : acc[t][c], 0, 0, 0);
+                const v8h a = read_a(st, t, j);
+                acc[t][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, bh, j == 0 ? z : acc[t][0], 0, 0, 0);
+                acc[t][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, bl, j == 0 ? z : acc[t][1], 0, 0, 0);
             }
         }
         const float dw = f16_bits_to_f32(W.d);
@@ -278,13 +286,13 @@ __global__ __launch_bounds__(256, 2) void gemm_f16w_kernel(Gemm6Params p) {
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     const int r = 4 * g4 + i;
-                    // f32 combine: y += (d_w * d_x) * S
-                    yacc[t][r] = __builtin_fmaf(dw * dx4[i], acc[t][0][r] + acc[t][1][r], yacc[t][r]);
+                    // f32 combine: y += (d_w * d_x) * S, S = 16 A_h + A_l
+                    yacc[t][r] = __builtin_fmaf(dw * dx4[i], __builtin_fmaf(16.0f, acc[t][0][r], acc[t][1][r]), yacc[t][r]);
                     if (DUMP) {
                         const int row = m0 + 32 * t + 8 * g4 + 4 * h + i;
                         if (row < p.m && col_ok) {
                             const int64_t o = ((int64_t)row * p.n + col) * ng + b;
-                            p.S[o] = (int)acc[t][0][r] + (int)acc[t][1][r];
+                            p.S[o] = 16 * (int)acc[t][0][r] + (int)acc[t][1][r];
                             p.Smin[o] = 0;
                         }
                     }

@@ -174,15 +174,36 @@ def test_prefill_gemm_q6k_ragged_tiles(ctx, m, n, k):
     check_matmul(ctx, W, x)
 
 
-def test_prefill_gemm_q6k_extreme_values(ctx):
-    """Largest Q6_K . Q8_K sums: every weight value -32 * -32 = 1024 and
-    activation blocks of equal values (every quant -128): each half
-    super-block's f32 MFMA chain reaches exactly -2^24."""
+@pytest.mark.parametrize("m,n,k", [(1, 300, 2048), (3, 300, 2048), (8, 96, 1024), (16, 256, 2048),
+                                   (512, 256, 2048), (77, 129, 768)])
+def test_q6k_full_range_sub_scales(ctx, m, n, k):
+    """Q6_K sub-scales over the whole int8 range, as llama.cpp's quantizer
+    writes them (the largest sub-block scale of each super-block maps to
+    -128): sc * (q6 - 32) reaches 4096, beyond the integers f16 holds
+    exactly, so the prefill GEMM splits each scale into two digits.  Every
+    path -- matvec (m = 1), matrix-core matvec (m = 3, 8), GEMM (m >= 16) --
+    keeps the integer block sums bit-exact."""
+    rng = np.random.default_rng(m * 7 + n)
+    W = S.make_weight(S.TYPE_Q6_K, n, k, seed=m + n)
+    W.sc[:] = rng.integers(-128, 128, size=W.sc.shape).astype(np.int8)
+    W.sc[..., 0] = -128  # the quantizer's own extreme in every super-block
+    W.blocks = S.pack_q6k(W.d, W.sc, W.q)
+    x = S.make_activation(m, k, seed=m + k)
+    check_matmul(ctx, W, x)
+
+
+@pytest.mark.parametrize("sc", [-128, 127, -32])
+def test_prefill_gemm_q6k_extreme_values(ctx, sc):
+    """Largest Q6_K . Q8_K sums: every quant -32, every sub-scale at an end of
+    the int8 range that llama.cpp's quantizer uses (-128: S = 2^27 per
+    super-block, its high-digit chain exactly 2^23; 127: the low digit 15,
+    its chain 480 * 256 * 128 < 2^24) or -32, against activation blocks of
+    equal values (every quant +-128)."""
     n, k, m = 64, 1024, 16
     rng = np.random.default_rng(6)
     W = S.make_weight(S.TYPE_Q6_K, n, k, seed=6)
     W.q[:] = -32
-    W.sc[:] = -32
+    W.sc[:] = sc
     W.blocks = S.pack_q6k(W.d, W.sc, W.q)
     x = np.repeat(np.abs(rng.standard_normal((m, k // 256))).astype(np.float32) + 0.5, 256, axis=1)
     x[1::2] = -x[1::2]
