@@ -17,24 +17,36 @@
 // all lanes: it is read from LDS at a wave-uniform address (one 16-byte
 // broadcast read per four v_dot4), so the weights are the only per-lane data.
 //
-// Schedule.  The first ceil(groups / 4) wavefronts load the activation and
-// quantise four Q8_K blocks each (16 lanes per block, 16 elements per lane),
-// into LDS; meanwhile every wavefront has issued its first P weight pieces.
+// Schedule.  The first ceil(groups / 4) wavefronts load the activation, then
+// every wavefront issues its first P weight pieces, then those wavefronts
+// quantise four Q8_K blocks each (16 lanes per block, 16 elements per lane)
+// into LDS while the weight pieces are in flight.
 // After one barrier each wavefront walks its pieces in order, keeping P of
 // them in flight (compute piece j, issue piece j + P): a wavefront never
 // waits at the barrier behind its own blocked load issues, and the dot
 // products of the pieces that have arrived overlap the rest of the stream.
 // Partial sums of a row (one per group) are added across the wavefronts
 // through LDS, in wavefront order.
+//
+// Fewer rows (from 3200; the Llama-3-8B attention projections and ffn_down,
+// 4096 rows) with up to 64 groups: a workgroup owns 16 rows and lane l of a
+// wavefront is row l % 16 of group phase l / 16, so one load instruction
+// reads piece p of four groups for 16 rows (eight full lines) and 256
+// workgroups cover 4096 rows.  The activation operand then differs between
+// the four 16-lane sets of a wavefront (four broadcast LDS reads), and a
+// row's partials are first added across its four lanes, then across the
+// wavefronts.
 #include "aq_internal.h"
 
 namespace aq {
 
 namespace {
 
-constexpr int RL_ROWS = 56;    // weight rows per workgroup
-constexpr int RL_MAXG = 32;    // groups per row (k <= 8192)
-constexpr int RL_MIN_N = 200 * RL_ROWS;  // rows below which the general matvec is used
+constexpr int RL_ROWS = 56;    // weight rows per workgroup (one row per lane)
+constexpr int RL_MAXG = 64;    // groups per row (k <= 16384)
+constexpr int RL_MIN_N = 200 * RL_ROWS;  // rows from which 56-row workgroups are used (up to 32 groups)
+constexpr int RG_ROWS = 16;    // weight rows per workgroup of the four-group-phase form
+constexpr int RG_MIN_N = 200 * RG_ROWS;  // rows from which that form is used (up to 64 groups)
 
 struct RlParams {
     const uint8_t *w;  // row-block tiles
@@ -104,8 +116,13 @@ __device__ __forceinline__ uint4 q8k_block_row16(const float v[16], int s, int *
     return make_uint4(pack4_i8(q), pack4_i8(q + 4), pack4_i8(q + 8), pack4_i8(q + 12));
 }
 
-template <int W, int GPW, int P, bool FUSED, bool DUMP>
+// R rows per workgroup: RL_ROWS (lane = row, one group phase) or RG_ROWS
+// (lane = row + 16 * group phase, four phases).  Lane (row r, phase gp) of
+// wavefront w takes the groups w * GP + gp + W * GP * i, i < GPW.
+template <int R, int W, int GPW, int P, bool EARLY, bool FUSED, bool DUMP>
 __global__ __launch_bounds__(W * 64) void rl_q4k_kernel(RlParams p) {
+    static_assert(R == RL_ROWS || R == RG_ROWS, "56 rows, one per lane, or 16 rows in four group phases");
+    constexpr int GP = R == RL_ROWS ? 1 : 64 / R;  // group phases per wavefront
     __shared__ __align__(16) uint8_t xq[RL_MAXG][256];  // Q8_K quants of each group
     __shared__ __align__(16) int xb[RL_MAXG][8];        // bsums of the 8 sub-blocks (32 elements)
     __shared__ float xd[RL_MAXG];                       // Q8_K d
@@ -113,64 +130,87 @@ __global__ __launch_bounds__(W * 64) void rl_q4k_kernel(RlParams p) {
     constexpr int NP = 9 * GPW;  // this wavefront's pieces, in order
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-    const int row0 = (int)blockIdx.x * RL_ROWS;
-    const int row = row0 + lane;
-    const bool rok = lane < RL_ROWS && row < p.n;
+    const int rl = GP == 1 ? lane : lane % R, gp = GP == 1 ? 0 : lane / R;
+    const int row0 = (int)blockIdx.x * R;
+    const int row = row0 + rl;
+    const bool rok = rl < R && row < p.n;
     const int rb0 = row0 / RB;
     const int nrb = (p.n + RB - 1) / RB;
-    const int rbs = min(RL_ROWS / RB, nrb - rb0);
+    const int rbs = min(R / RB, nrb - rb0);
     const rsrc_t rw = buf_rsrc(p.w + (int64_t)rb0 * p.rb_stride, (uint32_t)(rbs * p.rb_stride));
-    const uint32_t lbase = rok ? (uint32_t)((lane / RB) * p.rb_stride + (lane % RB) * 16) : BUF_OOB;
+    const uint32_t lbase = rok ? (uint32_t)((rl / RB) * p.rb_stride + (rl % RB) * 16) : BUF_OOB;
+    auto group_of = [&](int j) { return wave * GP + gp + W * GP * (j / 9); };
 
     uint4 ring[P];
     auto issue = [&](int j) {
-        const int g = wave + W * (j / 9);
+        const int g = group_of(j);
         const uint32_t off = g < p.ng ? lbase + (uint32_t)((g * 9 + j % 9) * 128) : BUF_OOB;
         const u32x4 t = __builtin_amdgcn_raw_buffer_load_b128(rw, off, 0, BUF_NT);
         ring[j % P] = make_uint4(t.x, t.y, t.z, t.w);
     };
 
-    // 1. the activation: wavefront w < ceil(ng / 4) stages blocks 4w .. 4w + 3,
-    //    16 lanes (s = lane & 15) per block
+    // 1. the activation's loads: wavefront w < ceil(ng / 4) stages blocks
+    //    4w .. 4w + 3, 16 lanes (s = lane & 15) per block; then (EARLY) this
+    //    wavefront's first P weight pieces, so that they are in flight while
+    //    the activation is quantised (the loads are waited for in issue
+    //    order).  With most wavefronts quantising (the 16-wavefront form),
+    //    issuing them after the quantisation measured faster.
     const int s = lane & 15;
     const int gb = 4 * wave + (lane >> 4);
-    if (wave < (p.ng + 3) / 4) {  // uniform
+    const bool quantiser = wave < (p.ng + 3) / 4;  // uniform
+    const bool gbok = gb < p.ng;
+    u32x4 xv[4];
+    uint32_t xbs = 0, xdb = 0;
+    if (quantiser) {
+        if (FUSED) {
+            const rsrc_t rx = buf_rsrc(p.x, (uint32_t)(p.k * 4));
+            const uint32_t xo = gbok ? (uint32_t)((gb * QK_K + 16 * s) * 4) : BUF_OOB;
+#pragma unroll
+            for (int i = 0; i < 4; i++) xv[i] = __builtin_amdgcn_raw_buffer_load_b128(rx, xo + 16 * i, 0, 0);
+        } else {
+            const rsrc_t rq = buf_rsrc(p.act.qs, (uint32_t)p.k);
+            const rsrc_t rs = buf_rsrc(p.act.bsums, (uint32_t)((p.k / 16) * 2));
+            const rsrc_t rd = buf_rsrc(p.act.d, (uint32_t)((p.k / QK_K) * 4));
+            xv[0] = __builtin_amdgcn_raw_buffer_load_b128(rq, gbok ? (uint32_t)(gb * QK_K + 16 * s) : BUF_OOB, 0, 0);
+            xbs = __builtin_amdgcn_raw_buffer_load_b16(rs, gbok ? (uint32_t)((gb * 16 + s) * 2) : BUF_OOB, 0, 0);
+            xdb = __builtin_amdgcn_raw_buffer_load_b32(rd, gbok ? (uint32_t)(gb * 4) : BUF_OOB, 0, 0);
+        }
+    }
+    if (EARLY) {
+#pragma unroll
+        for (int j = 0; j < P && j < NP; j++) issue(j);
+    }
+    // 2. quantise (or unpack) into LDS, then one barrier (LDS writes only)
+    if (quantiser) {
         uint4 qv;
         int bsum;
         float d;
         if (FUSED) {
-            const rsrc_t rx = buf_rsrc(p.x, (uint32_t)(p.k * 4));
-            const uint32_t xo = gb < p.ng ? (uint32_t)((gb * QK_K + 16 * s) * 4) : BUF_OOB;
             float v[16];
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const u32x4 t = __builtin_amdgcn_raw_buffer_load_b128(rx, xo + 16 * i, 0, 0);
-                v[4 * i] = u32_as_f32(t.x);
-                v[4 * i + 1] = u32_as_f32(t.y);
-                v[4 * i + 2] = u32_as_f32(t.z);
-                v[4 * i + 3] = u32_as_f32(t.w);
+                v[4 * i] = u32_as_f32(xv[i].x);
+                v[4 * i + 1] = u32_as_f32(xv[i].y);
+                v[4 * i + 2] = u32_as_f32(xv[i].z);
+                v[4 * i + 3] = u32_as_f32(xv[i].w);
             }
             qv = q8k_block_row16(v, s, &bsum, &d);
         } else {
-            const bool ok = gb < p.ng;
-            const rsrc_t rq = buf_rsrc(p.act.qs, (uint32_t)p.k);
-            const rsrc_t rs = buf_rsrc(p.act.bsums, (uint32_t)((p.k / 16) * 2));
-            const rsrc_t rd = buf_rsrc(p.act.d, (uint32_t)((p.k / QK_K) * 4));
-            const u32x4 t = __builtin_amdgcn_raw_buffer_load_b128(rq, ok ? (uint32_t)(gb * QK_K + 16 * s) : BUF_OOB, 0, 0);
-            qv = make_uint4(t.x, t.y, t.z, t.w);
-            bsum = (int)(int16_t)__builtin_amdgcn_raw_buffer_load_b16(rs, ok ? (uint32_t)((gb * 16 + s) * 2) : BUF_OOB, 0, 0);
-            d = u32_as_f32(__builtin_amdgcn_raw_buffer_load_b32(rd, ok ? (uint32_t)(gb * 4) : BUF_OOB, 0, 0));
+            qv = make_uint4(xv[0].x, xv[0].y, xv[0].z, xv[0].w);
+            bsum = (int)(int16_t)xbs;
+            d = u32_as_f32(xdb);
         }
         const int pair = bsum + dpp_row<DPP_QUAD_XOR1>(bsum);  // sub-block s/2 (two 16-element halves)
-        if (gb < p.ng) {
+        if (gbok) {
             *(uint4 *)&xq[gb][16 * s] = qv;
             if ((s & 1) == 0) xb[gb][s >> 1] = pair;
             if (s == 0) xd[gb] = d;
         }
     }
-    // 2. the first P weight pieces, then one barrier (LDS writes only)
+    if (!EARLY) {
 #pragma unroll
-    for (int j = 0; j < P && j < NP; j++) issue(j);
+        for (int j = 0; j < P && j < NP; j++) issue(j);
+    }
     lds_barrier();
 
     // 3. walk the pieces: piece 0 of a group = d, dmin, 12 scale bytes; piece
@@ -184,13 +224,15 @@ __global__ __launch_bounds__(W * 64) void rl_q4k_kernel(RlParams p) {
 #pragma unroll
     for (int j = 0; j < NP; j++) {
         const int pc = j % 9;
-        const int g = wave + W * (j / 9);
-        if (g >= p.ng) break;  // uniform
+        const int g = group_of(j);
+        if (GP == 1 && g >= p.ng) break;  // uniform
+        const bool gok = g < p.ng;         // (lanes of several phases: per lane)
+        const int gl = gok ? g : 0;        // a group whose LDS entries are written
         const uint4 q = ring[j % P];
         if (pc == 0) {
-            *(int4 *)&bs[0] = *(const int4 *)&xb[g][0];
-            *(int4 *)&bs[4] = *(const int4 *)&xb[g][4];
-            dx = xd[g];
+            *(int4 *)&bs[0] = *(const int4 *)&xb[gl][0];
+            *(int4 *)&bs[4] = *(const int4 *)&xb[gl][4];
+            dx = xd[gl];
             // candle's utmp form of GGML get_scale_min_k4 (6-bit scales and mins)
             const uint32_t u0 = q.y, u1 = q.z, u2 = q.w;
             sc03 = u0 & 0x3F3F3F3Fu;
@@ -203,8 +245,8 @@ __global__ __launch_bounds__(W * 64) void rl_q4k_kernel(RlParams p) {
             const int c = (pc - 1) >> 1, h = (pc - 1) & 1;
             // x of the low nibbles (elements 64c + 16h ..) and of the high
             // nibbles (64c + 32 + 16h ..): the same for every lane
-            const int4 xl = *(const int4 *)&xq[g][64 * c + 16 * h];
-            const int4 xh = *(const int4 *)&xq[g][64 * c + 32 + 16 * h];
+            const int4 xl = *(const int4 *)&xq[gl][64 * c + 16 * h];
+            const int4 xh = *(const int4 *)&xq[gl][64 * c + 32 + 16 * h];
             if (h == 0) il = ih = 0;
             il = sdot4((int)(q.x & 0x0F0F0F0Fu), xl.x, il);
             ih = sdot4((int)((q.x >> 4) & 0x0F0F0F0Fu), xh.x, ih);
@@ -225,17 +267,20 @@ __global__ __launch_bounds__(W * 64) void rl_q4k_kernel(RlParams p) {
 #pragma unroll
             for (int jj = 0; jj < 8; jj++) smin += (int)(((jj < 4 ? mn03 : mn47) >> (8 * (jj & 3))) & 0xffu) * bs[jj];
             const float dw = f16_bits_to_f32(dwp), dmw = f16_bits_to_f32(dwp >> 16);
-            f += (dw * dx) * (float)S - (dmw * dx) * (float)smin;
-            if (DUMP && rok) {
+            if (gok) f += (dw * dx) * (float)S - (dmw * dx) * (float)smin;
+            if (DUMP && rok && gok) {
                 p.S[(int64_t)row * p.ng + g] = S;
                 p.Smin[(int64_t)row * p.ng + g] = smin;
             }
         }
     }
-    // 4. the row's partials of the eight wavefronts, added in wavefront order
+    // 4. the row's partials: over its group phases within the wavefront,
+    //    then over the wavefronts, in wavefront order
+    if (GP == 4) f += __shfl_xor(f, 16);
+    if (GP >= 2) f += __shfl_xor(f, 32);
     red[wave][lane] = f;
     lds_barrier();
-    if (wave == 0 && rok) {
+    if (wave == 0 && rok && gp == 0) {
         float t = 0.0f;
 #pragma unroll
         for (int w = 0; w < W; w++) t += red[w][lane];
@@ -243,22 +288,25 @@ __global__ __launch_bounds__(W * 64) void rl_q4k_kernel(RlParams p) {
     }
 }
 
-template <int W, int GPW, int P>
+template <int R, int W, int GPW, int P, bool EARLY>
 hipError_t launch_g(const RlParams &p, unsigned grid, bool fused, bool dump, hipStream_t s) {
     if (fused) {
-        if (dump) rl_q4k_kernel<W, GPW, P, true, true><<<grid, W * 64, 0, s>>>(p);
-        else rl_q4k_kernel<W, GPW, P, true, false><<<grid, W * 64, 0, s>>>(p);
+        if (dump) rl_q4k_kernel<R, W, GPW, P, EARLY, true, true><<<grid, W * 64, 0, s>>>(p);
+        else rl_q4k_kernel<R, W, GPW, P, EARLY, true, false><<<grid, W * 64, 0, s>>>(p);
     } else {
-        if (dump) rl_q4k_kernel<W, GPW, P, false, true><<<grid, W * 64, 0, s>>>(p);
-        else rl_q4k_kernel<W, GPW, P, false, false><<<grid, W * 64, 0, s>>>(p);
+        if (dump) rl_q4k_kernel<R, W, GPW, P, EARLY, false, true><<<grid, W * 64, 0, s>>>(p);
+        else rl_q4k_kernel<R, W, GPW, P, EARLY, false, false><<<grid, W * 64, 0, s>>>(p);
     }
     return hipGetLastError();
 }
 
+bool rows56(int64_t n, int ng) { return ng <= 32 && n >= RL_MIN_N; }
+
 }  // namespace
 
 bool rowlane_matvec_applies(int type, int64_t n, int64_t k) {
-    return type == TYPE_Q4_K && k % QK_K == 0 && k / QK_K <= RL_MAXG && n >= RL_MIN_N && n <= 0x7fffffff;
+    return type == TYPE_Q4_K && k % QK_K == 0 && k > 0 && k / QK_K <= RL_MAXG && n <= 0x7fffffff &&
+           (rows56(n, (int)(k / QK_K)) || n >= RG_MIN_N);
 }
 
 hipError_t launch_rowlane_matvec(const WLayout &w, int64_t n, int64_t k, const float *x, const ActPlanes *act,
@@ -268,7 +316,8 @@ hipError_t launch_rowlane_matvec(const WLayout &w, int64_t n, int64_t k, const f
     const int ng = (int)(k / QK_K);
     if (w.ng != ng || w.rb_stride != (int64_t)ng * 9 * 128) return hipErrorInvalidValue;
     if (x && ((uintptr_t)x & 15)) return hipErrorInvalidValue;
-    if ((int64_t)RL_ROWS / RB * w.rb_stride >= ((int64_t)1 << 31)) return hipErrorNotSupported;
+    const bool wide = rows56(n, ng);
+    if ((int64_t)(wide ? RL_ROWS : RG_ROWS) / RB * w.rb_stride >= ((int64_t)1 << 31)) return hipErrorNotSupported;
     RlParams p;
     p.w = w.slab;
     p.rb_stride = w.rb_stride;
@@ -280,12 +329,24 @@ hipError_t launch_rowlane_matvec(const WLayout &w, int64_t n, int64_t k, const f
     p.y = y;
     p.S = S;
     p.Smin = Smin;
-    const unsigned grid = (unsigned)((n + RL_ROWS - 1) / RL_ROWS);
     const bool fused = x != nullptr, dump = S != nullptr;
-    // 16 wavefronts with six pieces in flight each measured fastest at the
-    // headline (one group per wavefront); longer rows take two groups each
-    if (ng <= 16) return launch_g<16, 1, 6>(p, grid, fused, dump, s);
-    return launch_g<16, 2, 12>(p, grid, fused, dump, s);
+    if (wide) {
+        const unsigned grid = (unsigned)((n + RL_ROWS - 1) / RL_ROWS);
+        // 16 wavefronts with six pieces in flight each measured fastest at the
+        // headline (one group per wavefront); longer rows take two groups each
+        if (ng <= 16) return launch_g<RL_ROWS, 16, 1, 6, true>(p, grid, fused, dump, s);
+        return launch_g<RL_ROWS, 16, 2, 12, true>(p, grid, fused, dump, s);
+    }
+    // 16 rows: as many wavefronts as four groups each need (every lane one
+    // group); the quantising wavefronts (four blocks each) are then always
+    // enough.  Up to 32 groups all nine pieces of a lane's group are in
+    // flight from the start; with 16 wavefronts (ffn_down, 56 groups) five,
+    // issued after the quantisation, measured fastest (8.3 us against 8.6
+    // for nine issued late and 9.7 for nine issued early).
+    const unsigned grid = (unsigned)((n + RG_ROWS - 1) / RG_ROWS);
+    if (ng <= 16) return launch_g<RG_ROWS, 4, 1, 9, true>(p, grid, fused, dump, s);
+    if (ng <= 32) return launch_g<RG_ROWS, 8, 1, 9, true>(p, grid, fused, dump, s);
+    return launch_g<RG_ROWS, 16, 1, 5, false>(p, grid, fused, dump, s);
 }
 
 }  // namespace aq

@@ -1,6 +1,9 @@
 """GPU parity of the batch-1 Q4_K matvec with one weight row per lane
 (csrc/k_rowlane.hip), the path a single activation row takes on a Q4_K
-weight of at least 11200 rows and k <= 8192 (Llama-3-8B ffn_up / ffn_gate).
+weight of at least 11200 rows and k <= 8192 (Llama-3-8B ffn_up / ffn_gate),
+and of its 16-row form (lane = row + 16 * group phase), taken from 3200 rows
+up to k = 16384 (Llama-3-8B ffn_down 4096 x 14336, the attention
+projections 4096 x 4096).
 
 Against the oracle (candle-core 0.8.4 k_quants::matmul restated): every
 integer block sum S and Smin bit-exact, outputs within max relative error
@@ -19,6 +22,7 @@ from tests.test_gpu_parity import _edge_rows, _xdeq_abs, check_matmul
 pytestmark = pytest.mark.gpu
 
 RL_MIN_N = 11200  # rows from which a one-row Q4_K matvec takes the row-per-lane kernel
+RG_MIN_N = 3200   # rows from which it takes the 16-row form (any k <= 16384)
 
 
 @pytest.mark.parametrize("n,k", [
@@ -32,6 +36,35 @@ def test_rowlane_matches_oracle(ctx, n, k):
     W = S.make_weight(S.TYPE_Q4_K, n, k, seed=n + k)
     x = S.make_activation(1, k, seed=k)
     check_matmul(ctx, W, x)
+
+
+@pytest.mark.parametrize("n,k", [
+    (4096, 14336),   # Llama-3-8B ffn_down: 256 workgroups, 56 groups over 14 wavefronts of four phases
+    (4096, 4096),    # the attention projections: 16 groups, four wavefronts
+    (RG_MIN_N, 8192),  # 32 groups, eight wavefronts
+    (3203, 16384),   # 64 groups (the most), ragged rows: the last workgroup's second row block is partial
+    (5000, 8448),    # 33 groups: the ninth wavefront's lanes straddle the last group
+    (RL_MIN_N, 9216),  # many rows but 36 groups: the 16-row form
+])
+def test_rowlane16_matches_oracle(ctx, n, k):
+    W = S.make_weight(S.TYPE_Q4_K, n, k, seed=n + k + 1)
+    x = S.make_activation(1, k, seed=k + 1)
+    check_matmul(ctx, W, x)
+
+
+def test_rowlane16_edge_activations(ctx):
+    """The edge rows of the quantizer through the 16-row form's in-kernel
+    quantisation, integer sums bit-exact."""
+    k = 14336
+    W = S.make_weight(S.TYPE_Q4_K, 4096, k, seed=78)
+    mm = A.QMatMul.from_qtensor(A.QTensor(W.type, (W.n, W.k), W.blocks), ctx)
+    for x in _edge_rows(k):
+        x = x[None, :]
+        xq = O.quantize(x, O.Q8_K)
+        gS, gSm = mm.block_sums(x)
+        oS, oSm = O.block_sums(W.type, k, W.blocks, xq)
+        assert np.array_equal(gS, oS) and np.array_equal(gSm, oSm)
+    mm.free()
 
 
 def test_rowlane_edge_activations(ctx):
@@ -127,5 +160,24 @@ def test_rowlane_and_general_matvec_agree(ctx):
     assert np.array_equal(sb[:, :n2], ss) and np.array_equal(smb[:, :n2], sms)
     yb, ys = big.forward(x), small.forward(x)
     assert float(np.abs(yb[:, :n2] - ys).max()) <= 1e-5 * float(np.abs(ys).max())
+    big.free()
+    small.free()
+
+
+def test_rowlane16_and_general_matvec_agree(ctx):
+    """The 16-row form (n >= 3200) against the general matvec on the first
+    3192 rows of the same weight: integer sums identical, outputs within the
+    tolerance."""
+    k = 14336
+    W = S.make_weight(S.TYPE_Q4_K, RG_MIN_N, k, seed=33)
+    x = S.make_activation(1, k, seed=34)
+    big = A.QMatMul.from_qtensor(A.QTensor(W.type, (W.n, k), W.blocks), ctx)
+    n2 = RG_MIN_N - 8
+    small = A.QMatMul.from_qtensor(A.QTensor(W.type, (n2, k), W.blocks[:n2]), ctx)
+    sb, smb = big.block_sums(x)
+    ss, sms = small.block_sums(x)
+    assert np.array_equal(sb[:, :n2], ss) and np.array_equal(smb[:, :n2], sms)
+    yb, ys = big.forward(x), small.forward(x)
+    assert float(np.abs(yb[:, :n2] - ys).max()) <= 1e-4 * float(np.abs(ys).max())
     big.free()
     small.free()
