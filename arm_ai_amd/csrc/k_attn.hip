@@ -328,16 +328,20 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(const float *__restrict__ 
     }
 }
 
-// 2) attn_prefill_kernel: grid (ceil(m / 64) query tiles, n_head), 256
-//    threads.  The workgroup's 64 query rows (rotated at their positions) sit
-//    in LDS; key/value tiles of 64 cached positions stream through LDS up to
-//    the tile's last position; scores, the causal mask and an online softmax
-//    (running max and sum per row, the output rescaled when the max grows)
-//    are kept in registers.  Thread (rg = tid / 16, cg = tid % 16) owns query
-//    rows rg + 16a (a < 4), key columns cg + 16b (b < 4) of each score tile
-//    and output float4 columns cg + 16e (e < hd / 64).  LDS rows are padded
-//    by 4 floats so the 16 lanes of a row group read 16 different banks.
-constexpr int PF_QT = 64, PF_KT = 64, PF_PAD = 4;
+// 2) attn_prefill_kernel: one workgroup of 256 threads per (query tile of
+//    32 rows, query head).  The tile's query rows (rotated at their
+//    positions) sit in LDS; key/value tiles of 64 cached positions stream
+//    through LDS up to the tile's last position; scores, the causal mask and
+//    an online softmax (running max and sum per row, the output rescaled
+//    when the max grows) are kept in registers.  Thread (rg = tid / 16, cg =
+//    tid % 16) owns query rows rg + 16a (a < 2), key columns cg + 16b (b < 4)
+//    of each score tile and output float4 columns cg + 16e (e < hd / 64).
+//    LDS rows are padded by 4 floats so the 16 lanes of a row group read 16
+//    different banks.  Causal tiles differ in work (tile t reads t / 2 + 1
+//    key tiles), so workgroups are dealt light and heavy alternately: in
+//    dispatch order the tiles run 0, last, 1, last - 1, ..., each for every
+//    head, and the several workgroups a CU holds even out.
+constexpr int PF_QT = 32, PF_KT = 64, PF_PAD = 4, PF_A = PF_QT / 16;
 
 template <int HD>
 __global__ __launch_bounds__(256) void attn_prefill_kernel(const float *__restrict__ q, int64_t ldq,
@@ -353,9 +357,12 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const float *__restri
     __shared__ __align__(16) float ks[PF_KT * HS];
     __shared__ __align__(16) float vs[PF_KT * HS];
     __shared__ __align__(16) float ps[PF_QT * PS];
-    const int tid = threadIdx.x, h = blockIdx.y, rg = tid / 16, cg = tid % 16;
+    const int tid = threadIdx.x, rg = tid / 16, cg = tid % 16;
+    const int ntq = (m + PF_QT - 1) / PF_QT;
+    const int rank = blockIdx.x / n_head, h = blockIdx.x % n_head;
+    const int tq = (rank & 1) ? ntq - 1 - (rank >> 1) : (rank >> 1);  // 0, last, 1, last - 1, ...
     const int kvh = h / (n_head / n_kv);
-    const int r0 = blockIdx.x * PF_QT;
+    const int r0 = tq * PF_QT;
     const int rows = min(PF_QT, m - r0);
     const float *kh = kc + (int64_t)kvh * max_seq * HD;
     const float *vh = vc + (int64_t)kvh * max_seq * HD;
@@ -375,10 +382,10 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const float *__restri
         qs[r * HS + 2 * j + 1] = a * sn + b * c;
     }
 
-    float mrun[4], lrun[4];
-    float4 o[4][DV];
+    float mrun[PF_A], lrun[PF_A];
+    float4 o[PF_A][DV];
 #pragma unroll
-    for (int a = 0; a < 4; a++) {
+    for (int a = 0; a < PF_A; a++) {
         mrun[a] = -INFINITY;
         lrun[a] = 0.0f;
 #pragma unroll
@@ -399,20 +406,20 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const float *__restri
             *(float4 *)&vs[c * HS + 4 * d4] = vv;
         }
         __syncthreads();
-        float sacc[4][4];
+        float sacc[PF_A][4];
 #pragma unroll
-        for (int a = 0; a < 4; a++)
+        for (int a = 0; a < PF_A; a++)
 #pragma unroll
             for (int b = 0; b < 4; b++) sacc[a][b] = 0.0f;
 #pragma unroll 4
         for (int d = 0; d < HD; d += 4) {
-            float4 qv[4], kv[4];
+            float4 qv[PF_A], kv[4];
 #pragma unroll
-            for (int a = 0; a < 4; a++) qv[a] = *(const float4 *)&qs[(rg + 16 * a) * HS + d];
+            for (int a = 0; a < PF_A; a++) qv[a] = *(const float4 *)&qs[(rg + 16 * a) * HS + d];
 #pragma unroll
             for (int b = 0; b < 4; b++) kv[b] = *(const float4 *)&ks[(cg + 16 * b) * HS + d];
 #pragma unroll
-            for (int a = 0; a < 4; a++)
+            for (int a = 0; a < PF_A; a++)
 #pragma unroll
                 for (int b = 0; b < 4; b++) {
                     float t = sacc[a][b];
@@ -424,7 +431,7 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const float *__restri
                 }
         }
 #pragma unroll
-        for (int a = 0; a < 4; a++) {
+        for (int a = 0; a < PF_A; a++) {
             const int r = rg + 16 * a, qpos = index_pos + r0 + r;
             float sv[4], tmax = -INFINITY;
 #pragma unroll
@@ -457,16 +464,16 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const float *__restri
         __syncthreads();
         const int kn = min(PF_KT, kend - k0);
         for (int c = 0; c < kn; c += 4) {
-            float4 pv[4];
+            float4 pv[PF_A];
 #pragma unroll
-            for (int a = 0; a < 4; a++) pv[a] = *(const float4 *)&ps[(rg + 16 * a) * PS + c];
+            for (int a = 0; a < PF_A; a++) pv[a] = *(const float4 *)&ps[(rg + 16 * a) * PS + c];
 #pragma unroll
             for (int cc = 0; cc < 4; cc++) {
 #pragma unroll
                 for (int e = 0; e < DV; e++) {
                     const float4 vv = *(const float4 *)&vs[(c + cc) * HS + 4 * (cg + 16 * e)];
 #pragma unroll
-                    for (int a = 0; a < 4; a++) {
+                    for (int a = 0; a < PF_A; a++) {
                         const float w = cc == 0 ? pv[a].x : cc == 1 ? pv[a].y : cc == 2 ? pv[a].z : pv[a].w;
                         axpy4(o[a][e], w, vv);
                     }
@@ -475,7 +482,7 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const float *__restri
         }
     }
 #pragma unroll
-    for (int a = 0; a < 4; a++) {
+    for (int a = 0; a < PF_A; a++) {
         const int r = rg + 16 * a;
         if (r < rows) {
             float *orow = out + (int64_t)(r0 + r) * n_head * HD + (int64_t)h * HD;
@@ -555,7 +562,7 @@ hipError_t launch_attn_prefill(const float *q, int64_t ldq, const float *k, int6
     if (((uintptr_t)kc | (uintptr_t)vc | (uintptr_t)out) & 15) return hipErrorInvalidValue;
     rope_kv_kernel<<<(unsigned)m, 256, 0, s>>>(k, ldk, v, ldv, cosb, sinb, (int)index_pos, (int)n_kv, (int)hd,
                                                (int)max_seq, kc, vc);
-    const dim3 grid((unsigned)((m + PF_QT - 1) / PF_QT), (unsigned)n_head);
+    const unsigned grid = (unsigned)(((m + PF_QT - 1) / PF_QT) * n_head);
     if (hd == 64)
         attn_prefill_kernel<64><<<grid, 256, 0, s>>>(q, ldq, cosb, sinb, kc, vc, (int)index_pos, (int)m, (int)n_head,
                                                      (int)n_kv, (int)max_seq, out);
