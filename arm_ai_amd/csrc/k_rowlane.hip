@@ -47,9 +47,11 @@ constexpr int RL_MAXG = 64;    // groups per row (k <= 16384)
 constexpr int RL_MIN_N = 200 * RL_ROWS;  // rows from which 56-row workgroups are used (up to 32 groups)
 constexpr int RG_ROWS = 16;    // weight rows per workgroup of the four-group-phase form
 constexpr int RG_MIN_N = 200 * RG_ROWS;  // rows from which that form is used (up to 64 groups)
+constexpr int RL_PERSIST_CUS = 256;      // the persistent grid: one workgroup per CU
 
 struct RlParams {
     const uint8_t *w;  // row-block tiles
+    const uint16_t *wd;  // Q6_K: the d plane [n/8][ng][8] (f16)
     int64_t rb_stride;
     int n, k, ng;
     const float *x;    // fused: f32 [k]
@@ -119,35 +121,84 @@ __device__ __forceinline__ uint4 q8k_block_row16(const float v[16], int s, int *
 // R rows per workgroup: RL_ROWS (lane = row, one group phase) or RG_ROWS
 // (lane = row + 16 * group phase, four phases).  Lane (row r, phase gp) of
 // wavefront w takes the groups w * GP + gp + W * GP * i, i < GPW.
-template <int R, int W, int GPW, int P, bool EARLY, bool FUSED, bool DUMP>
-__global__ __launch_bounds__(W * 64) void rl_q4k_kernel(RlParams p) {
+//
+// Q6_K (13 pieces per group: 0-7 ql, 8-11 qh, 12 the 16 int8 sub-scales; d in
+// the d plane).  A lane takes the scales piece first and keeps it, and the
+// qh pieces before the ql pieces that need them (the order is given at
+// piece_of below); each ql piece then gives two sub-blocks' 6-bit quants
+// (its nibbles and two bits of the matching qh piece).  Sums are of the
+// stored quants q (0..63); candle's q - 32 is applied as -32 times the
+// activation's 16-element bsum, which gives the same integers.
+//
+// Persistent chunks (CH; more 56-row chunks than CUs, one group per
+// wavefront): a workgroup quantises the activation once and walks the chunks
+// blockIdx.x, blockIdx.x + gridDim.x, ...; every piece of the next chunk is
+// issued right after the same piece of the current one is consumed (P =
+// pieces per group), so the stream does not drain between chunks.
+template <int TYPE, int R, int W, int GPW, int P, bool EARLY, bool FUSED, bool DUMP, bool CH = false>
+__global__ __launch_bounds__(W * 64) void rl_kernel(RlParams p) {
     static_assert(R == RL_ROWS || R == RG_ROWS, "56 rows, one per lane, or 16 rows in four group phases");
+    static_assert(TYPE == TYPE_Q4_K || TYPE == TYPE_Q6_K, "Q4_K or Q6_K");
+    static_assert(!CH || (R == RL_ROWS && GPW == 1 && P == (TYPE == TYPE_Q6_K ? 13 : 9)),
+                  "persistent chunks: one group per wavefront, all its pieces in flight");
+    constexpr bool Q6 = TYPE == TYPE_Q6_K;
+    constexpr int NPG = Q6 ? 13 : 9;               // pieces per group
     constexpr int GP = R == RL_ROWS ? 1 : 64 / R;  // group phases per wavefront
     __shared__ __align__(16) uint8_t xq[RL_MAXG][256];  // Q8_K quants of each group
-    __shared__ __align__(16) int xb[RL_MAXG][8];        // bsums of the 8 sub-blocks (32 elements)
+    __shared__ __align__(16) int xb[RL_MAXG][Q6 ? 16 : 8];  // bsums per 16 (Q6_K) or 32 (Q4_K) elements
     __shared__ float xd[RL_MAXG];                       // Q8_K d
-    __shared__ float red[W][64];
-    constexpr int NP = 9 * GPW;  // this wavefront's pieces, in order
+    __shared__ float red[CH ? 2 : 1][W][64];
+    constexpr int NP = NPG * GPW;  // this wavefront's pieces, in order
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int rl = GP == 1 ? lane : lane % R, gp = GP == 1 ? 0 : lane / R;
-    const int row0 = (int)blockIdx.x * R;
-    const int row = row0 + rl;
-    const bool rok = rl < R && row < p.n;
-    const int rb0 = row0 / RB;
     const int nrb = (p.n + RB - 1) / RB;
-    const int rbs = min(R / RB, nrb - rb0);
-    const rsrc_t rw = buf_rsrc(p.w + (int64_t)rb0 * p.rb_stride, (uint32_t)(rbs * p.rb_stride));
-    const uint32_t lbase = rok ? (uint32_t)((rl / RB) * p.rb_stride + (rl % RB) * 16) : BUF_OOB;
-    auto group_of = [&](int j) { return wave * GP + gp + W * GP * (j / 9); };
+    // the rows of a chunk: this lane's row and the weight / d-plane descriptors
+    struct Chunk {
+        int row;
+        bool rok;
+        rsrc_t rw, rwd;
+        uint32_t lbase, dbase;
+    };
+    auto chunk_at = [&](int chunk) {
+        Chunk c;
+        const int row0 = chunk * R;
+        c.row = row0 + rl;
+        c.rok = rl < R && c.row < p.n;
+        const int rb0 = row0 / RB;
+        const int rbs = min(R / RB, nrb - rb0);
+        c.rw = buf_rsrc(p.w + (int64_t)rb0 * p.rb_stride, (uint32_t)(rbs * p.rb_stride));
+        c.lbase = c.rok ? (uint32_t)((rl / RB) * p.rb_stride + (rl % RB) * 16) : BUF_OOB;
+        c.rwd = buf_rsrc(Q6 ? p.wd + (int64_t)rb0 * p.ng * RB : nullptr, Q6 ? (uint32_t)(rbs * p.ng * RB * 2) : 0u);
+        c.dbase = c.rok ? (uint32_t)(((rl / RB) * p.ng * RB + (rl % RB)) * 2) : BUF_OOB;
+        return c;
+    };
+    Chunk cur = chunk_at((int)blockIdx.x);
+    auto group_of = [&](int j) { return wave * GP + gp + W * GP * (j / NPG); };
+    // the piece a lane reads at its j-th step within a group
+    // (Q6_K: 12, 8, 9, 0-3, 10, 11, 4-7 in the 56-row form, which holds two
+    //  qh pieces at a time; 12, 8-11, 0-7 in the 16-row form, where that
+    //  order measured fewer registers)
+    constexpr bool HALVES = R == RL_ROWS;
+    auto piece_of = [&](int pc) {
+        if (!Q6) return pc;
+        if (!HALVES) return pc == 0 ? 12 : pc < 5 ? 7 + pc : pc - 5;
+        return pc == 0 ? 12 : pc < 3 ? 7 + pc : pc < 7 ? pc - 3 : pc < 9 ? 3 + pc : pc - 5;
+    };
 
     uint4 ring[P];
-    auto issue = [&](int j) {
+    uint32_t dring[GPW];  // Q6_K: the f16 d of each of this lane's groups
+    // (on = false: an out-of-range load that returns zeros, in place of a branch)
+    auto issue_in = [&](const Chunk &c, int j, bool on) {
         const int g = group_of(j);
-        const uint32_t off = g < p.ng ? lbase + (uint32_t)((g * 9 + j % 9) * 128) : BUF_OOB;
-        const u32x4 t = __builtin_amdgcn_raw_buffer_load_b128(rw, off, 0, BUF_NT);
+        const bool ok = on && g < p.ng;
+        const uint32_t off = ok ? c.lbase + (uint32_t)((g * NPG + piece_of(j % NPG)) * 128) : BUF_OOB;
+        const u32x4 t = __builtin_amdgcn_raw_buffer_load_b128(c.rw, off, 0, BUF_NT);
         ring[j % P] = make_uint4(t.x, t.y, t.z, t.w);
+        if (Q6 && j % NPG == 0)
+            dring[j / NPG] = __builtin_amdgcn_raw_buffer_load_b16(c.rwd, ok ? c.dbase + (uint32_t)(g * RB * 2) : BUF_OOB, 0, BUF_NT);
     };
+    auto issue = [&](int j) { issue_in(cur, j, true); };
 
     // 1. the activation's loads: wavefront w < ceil(ng / 4) stages blocks
     //    4w .. 4w + 3, 16 lanes (s = lane & 15) per block; then (EARLY) this
@@ -203,7 +254,8 @@ __global__ __launch_bounds__(W * 64) void rl_q4k_kernel(RlParams p) {
         const int pair = bsum + dpp_row<DPP_QUAD_XOR1>(bsum);  // sub-block s/2 (two 16-element halves)
         if (gbok) {
             *(uint4 *)&xq[gb][16 * s] = qv;
-            if ((s & 1) == 0) xb[gb][s >> 1] = pair;
+            if (Q6) xb[gb][s] = bsum;
+            else if ((s & 1) == 0) xb[gb][s >> 1] = pair;
             if (s == 0) xd[gb] = d;
         }
     }
@@ -216,61 +268,125 @@ __global__ __launch_bounds__(W * 64) void rl_q4k_kernel(RlParams p) {
     // 3. walk the pieces: piece 0 of a group = d, dmin, 12 scale bytes; piece
     //    1 + 2c + h = qs bytes 32c + 16h .. +15 (low nibbles: elements
     //    64c + 16h + i of sub-block 2c; high: 64c + 32 + 16h + i of 2c + 1)
+    const int nch = (p.n + R - 1) / R;
+    for (int chunk = (int)blockIdx.x, it = 0;; it++) {  // one chunk unless CH
+    const int nextc = chunk + (int)gridDim.x;
+    const bool more = CH && nextc < nch;  // uniform
+    Chunk nxt = cur;
+    if (more) nxt = chunk_at(nextc);
+    const int row = cur.row;
+    const bool rok = cur.rok;
     float f = 0.0f;
+    uint32_t dwq = 0;  // Q6_K: this group's d (taken before the next chunk's load reuses the slot)
     int bs[8];
     float dx = 0.0f;
     uint32_t sc03 = 0, sc47 = 0, mn03 = 0, mn47 = 0, dwp = 0;
+    uint4 qhr[4] = {};  // Q6_K: the qh pieces held (HALVES: those of the current 128-element half)
+    uint4 sc6 = {};     // Q6_K: the group's 16 sub-scales
     int S = 0, il = 0, ih = 0;
-#pragma unroll
-    for (int j = 0; j < NP; j++) {
-        const int pc = j % 9;
-        const int g = group_of(j);
-        if (GP == 1 && g >= p.ng) break;  // uniform
-        const bool gok = g < p.ng;         // (lanes of several phases: per lane)
-        const int gl = gok ? g : 0;        // a group whose LDS entries are written
-        const uint4 q = ring[j % P];
-        if (pc == 0) {
-            *(int4 *)&bs[0] = *(const int4 *)&xb[gl][0];
-            *(int4 *)&bs[4] = *(const int4 *)&xb[gl][4];
-            dx = xd[gl];
-            // candle's utmp form of GGML get_scale_min_k4 (6-bit scales and mins)
-            const uint32_t u0 = q.y, u1 = q.z, u2 = q.w;
-            sc03 = u0 & 0x3F3F3F3Fu;
-            sc47 = (u2 & 0x0F0F0F0Fu) | (((u0 >> 6) & 0x03030303u) << 4);
-            mn03 = u1 & 0x3F3F3F3Fu;
-            mn47 = ((u2 >> 4) & 0x0F0F0F0Fu) | (((u1 >> 6) & 0x03030303u) << 4);
-            dwp = q.x;
-            S = 0;
-        } else {
-            const int c = (pc - 1) >> 1, h = (pc - 1) & 1;
-            // x of the low nibbles (elements 64c + 16h ..) and of the high
-            // nibbles (64c + 32 + 16h ..): the same for every lane
-            const int4 xl = *(const int4 *)&xq[gl][64 * c + 16 * h];
-            const int4 xh = *(const int4 *)&xq[gl][64 * c + 32 + 16 * h];
-            if (h == 0) il = ih = 0;
-            il = sdot4((int)(q.x & 0x0F0F0F0Fu), xl.x, il);
-            ih = sdot4((int)((q.x >> 4) & 0x0F0F0F0Fu), xh.x, ih);
-            il = sdot4((int)(q.y & 0x0F0F0F0Fu), xl.y, il);
-            ih = sdot4((int)((q.y >> 4) & 0x0F0F0F0Fu), xh.y, ih);
-            il = sdot4((int)(q.z & 0x0F0F0F0Fu), xl.z, il);
-            ih = sdot4((int)((q.z >> 4) & 0x0F0F0F0Fu), xh.z, ih);
-            il = sdot4((int)(q.w & 0x0F0F0F0Fu), xl.w, il);
-            ih = sdot4((int)((q.w >> 4) & 0x0F0F0F0Fu), xh.w, ih);
-            if (h == 1) {
-                const uint32_t sw = c < 2 ? sc03 : sc47;
-                S += (int)((sw >> (16 * (c & 1))) & 0xffu) * il + (int)((sw >> (16 * (c & 1) + 8)) & 0xffu) * ih;
+    // (persistent: a wavefront without a group skips the walk as a whole, so
+    //  the pieces in flight across chunks have one path through it)
+    if (!CH || group_of(0) < p.ng) {  // uniform
+    #pragma unroll
+        for (int j = 0; j < NP; j++) {
+            const int pc = j % NPG;
+            const int g = group_of(j);
+            if (GP == 1 && !CH && g >= p.ng) break;  // uniform
+            const bool gok = g < p.ng;         // (lanes of several phases: per lane)
+            const int gl = gok ? g : 0;        // a group whose LDS entries are written
+            const uint4 q = ring[j % P];
+            if (Q6) {
+                if (pc == 0) {
+                    sc6 = q;
+                    dx = xd[gl];
+                    dwq = dring[j / NPG];
+                    S = 0;
+                } else if (HALVES ? (pc == 1 || pc == 2 || pc == 7 || pc == 8) : pc < 5) {
+                    qhr[HALVES ? (pc - 1) % 2 : pc - 1] = q;
+                } else {
+                    // ql piece 4n + c: low nibbles are elements 128n + 16c + i
+                    // (sub-block 8n + c), high nibbles 128n + 64 + 16c + i
+                    // (sub-block 8n + 4 + c); their top two bits are bits
+                    // 2(c >> 1) and 2(c >> 1) + 4 of qh[32n + 16(c & 1) + i]
+                    const int ip = HALVES && pc < 7 ? pc - 3 : pc - 5, n = ip >> 2, c = ip & 3;
+                    const uint4 h = qhr[HALVES ? c & 1 : 2 * n + (c & 1)];
+                    const int sl = 2 * (c >> 1), jl = 8 * n + c, jh = jl + 4;
+                    const int4 xl = *(const int4 *)&xq[gl][16 * jl];
+                    const int4 xh = *(const int4 *)&xq[gl][16 * jh];
+                    auto lo = [&](uint32_t v, uint32_t hb) { return (int)((v & 0x0F0F0F0Fu) | (((hb >> sl) & 0x03030303u) << 4)); };
+                    auto hi = [&](uint32_t v, uint32_t hb) {
+                        return (int)(((v >> 4) & 0x0F0F0F0Fu) | (((hb >> (sl + 4)) & 0x03030303u) << 4));
+                    };
+                    int a = 0, b = 0;
+                    a = sdot4(lo(q.x, h.x), xl.x, a);
+                    b = sdot4(hi(q.x, h.x), xh.x, b);
+                    a = sdot4(lo(q.y, h.y), xl.y, a);
+                    b = sdot4(hi(q.y, h.y), xh.y, b);
+                    a = sdot4(lo(q.z, h.z), xl.z, a);
+                    b = sdot4(hi(q.z, h.z), xh.z, b);
+                    a = sdot4(lo(q.w, h.w), xl.w, a);
+                    b = sdot4(hi(q.w, h.w), xh.w, b);
+                    const uint32_t scw[4] = {sc6.x, sc6.y, sc6.z, sc6.w};
+                    const int scl = (int)(int8_t)((scw[jl >> 2] >> (8 * (jl & 3))) & 0xffu);
+                    const int sch = (int)(int8_t)((scw[jh >> 2] >> (8 * (jh & 3))) & 0xffu);
+                    S += scl * (a - 32 * xb[gl][jl]) + sch * (b - 32 * xb[gl][jh]);
+                }
+            } else if (pc == 0) {
+                *(int4 *)&bs[0] = *(const int4 *)&xb[gl][0];
+                *(int4 *)&bs[4] = *(const int4 *)&xb[gl][4];
+                dx = xd[gl];
+                // candle's utmp form of GGML get_scale_min_k4 (6-bit scales and mins)
+                const uint32_t u0 = q.y, u1 = q.z, u2 = q.w;
+                sc03 = u0 & 0x3F3F3F3Fu;
+                sc47 = (u2 & 0x0F0F0F0Fu) | (((u0 >> 6) & 0x03030303u) << 4);
+                mn03 = u1 & 0x3F3F3F3Fu;
+                mn47 = ((u2 >> 4) & 0x0F0F0F0Fu) | (((u1 >> 6) & 0x03030303u) << 4);
+                dwp = q.x;
+                S = 0;
+            } else {
+                const int c = (pc - 1) >> 1, h = (pc - 1) & 1;
+                // x of the low nibbles (elements 64c + 16h ..) and of the high
+                // nibbles (64c + 32 + 16h ..): the same for every lane
+                const int4 xl = *(const int4 *)&xq[gl][64 * c + 16 * h];
+                const int4 xh = *(const int4 *)&xq[gl][64 * c + 32 + 16 * h];
+                if (h == 0) il = ih = 0;
+                il = sdot4((int)(q.x & 0x0F0F0F0Fu), xl.x, il);
+                ih = sdot4((int)((q.x >> 4) & 0x0F0F0F0Fu), xh.x, ih);
+                il = sdot4((int)(q.y & 0x0F0F0F0Fu), xl.y, il);
+                ih = sdot4((int)((q.y >> 4) & 0x0F0F0F0Fu), xh.y, ih);
+                il = sdot4((int)(q.z & 0x0F0F0F0Fu), xl.z, il);
+                ih = sdot4((int)((q.z >> 4) & 0x0F0F0F0Fu), xh.z, ih);
+                il = sdot4((int)(q.w & 0x0F0F0F0Fu), xl.w, il);
+                ih = sdot4((int)((q.w >> 4) & 0x0F0F0F0Fu), xh.w, ih);
+                if (h == 1) {
+                    const uint32_t sw = c < 2 ? sc03 : sc47;
+                    S += (int)((sw >> (16 * (c & 1))) & 0xffu) * il + (int)((sw >> (16 * (c & 1) + 8)) & 0xffu) * ih;
+                }
             }
-        }
-        if (j + P < NP) issue(j + P);
-        if (pc == 8) {
-            int smin = 0;
-#pragma unroll
-            for (int jj = 0; jj < 8; jj++) smin += (int)(((jj < 4 ? mn03 : mn47) >> (8 * (jj & 3))) & 0xffu) * bs[jj];
-            const float dw = f16_bits_to_f32(dwp), dmw = f16_bits_to_f32(dwp >> 16);
-            if (gok) f += (dw * dx) * (float)S - (dmw * dx) * (float)smin;
-            if (DUMP && rok && gok) {
-                p.S[(int64_t)row * p.ng + g] = S;
-                p.Smin[(int64_t)row * p.ng + g] = smin;
+            if (j + P < NP) issue(j + P);
+            else if (CH) {
+                issue_in(nxt, j + P - NP, more);
+                __builtin_amdgcn_sched_barrier(0);  // keep the next chunk's load behind this piece's use
+            }
+            if (pc == NPG - 1) {
+                if (Q6) {
+                    const float dw = f16_bits_to_f32(dwq);
+                    if (gok) f += (dw * dx) * (float)S;
+                    if (DUMP && rok && gok) {
+                        p.S[(int64_t)row * p.ng + g] = S;
+                        p.Smin[(int64_t)row * p.ng + g] = 0;
+                    }
+                } else {
+                    int smin = 0;
+    #pragma unroll
+                    for (int jj = 0; jj < 8; jj++) smin += (int)(((jj < 4 ? mn03 : mn47) >> (8 * (jj & 3))) & 0xffu) * bs[jj];
+                    const float dw = f16_bits_to_f32(dwp), dmw = f16_bits_to_f32(dwp >> 16);
+                    if (gok) f += (dw * dx) * (float)S - (dmw * dx) * (float)smin;
+                    if (DUMP && rok && gok) {
+                        p.S[(int64_t)row * p.ng + g] = S;
+                        p.Smin[(int64_t)row * p.ng + g] = smin;
+                    }
+                }
             }
         }
     }
@@ -278,35 +394,69 @@ __global__ __launch_bounds__(W * 64) void rl_q4k_kernel(RlParams p) {
     //    then over the wavefronts, in wavefront order
     if (GP == 4) f += __shfl_xor(f, 16);
     if (GP >= 2) f += __shfl_xor(f, 32);
-    red[wave][lane] = f;
+    red[CH ? it & 1 : 0][wave][lane] = f;
     lds_barrier();
     if (wave == 0 && rok && gp == 0) {
         float t = 0.0f;
 #pragma unroll
-        for (int w = 0; w < W; w++) t += red[w][lane];
+        for (int w = 0; w < W; w++) t += red[CH ? it & 1 : 0][w][lane];
         p.y[row] = t;
+    }
+    if (!more) break;  // uniform
+    chunk = nextc;
+    cur = nxt;
     }
 }
 
-template <int R, int W, int GPW, int P, bool EARLY>
+template <int TYPE, int R, int W, int GPW, int P, bool EARLY, bool CH = false>
 hipError_t launch_g(const RlParams &p, unsigned grid, bool fused, bool dump, hipStream_t s) {
     if (fused) {
-        if (dump) rl_q4k_kernel<R, W, GPW, P, EARLY, true, true><<<grid, W * 64, 0, s>>>(p);
-        else rl_q4k_kernel<R, W, GPW, P, EARLY, true, false><<<grid, W * 64, 0, s>>>(p);
+        if (dump) rl_kernel<TYPE, R, W, GPW, P, EARLY, true, true, CH><<<grid, W * 64, 0, s>>>(p);
+        else rl_kernel<TYPE, R, W, GPW, P, EARLY, true, false, CH><<<grid, W * 64, 0, s>>>(p);
     } else {
-        if (dump) rl_q4k_kernel<R, W, GPW, P, EARLY, false, true><<<grid, W * 64, 0, s>>>(p);
-        else rl_q4k_kernel<R, W, GPW, P, EARLY, false, false><<<grid, W * 64, 0, s>>>(p);
+        if (dump) rl_kernel<TYPE, R, W, GPW, P, EARLY, false, true, CH><<<grid, W * 64, 0, s>>>(p);
+        else rl_kernel<TYPE, R, W, GPW, P, EARLY, false, false, CH><<<grid, W * 64, 0, s>>>(p);
     }
     return hipGetLastError();
 }
 
-bool rows56(int64_t n, int ng) { return ng <= 32 && n >= RL_MIN_N; }
+// 56-row workgroups: up to two Q4_K groups per wavefront (32 groups); one
+// Q6_K group (16; two kept 13-piece walks too many registers live)
+bool rows56(int type, int64_t n, int ng) { return ng <= (type == TYPE_Q6_K ? 16 : 32) && n >= RL_MIN_N; }
+
+// The launch shapes of one weight type (pieces in flight: P; 16 wavefronts
+// with six Q4_K pieces in flight measured fastest at the headline, one group
+// per wavefront; longer rows take two groups each)
+template <int TYPE>
+hipError_t launch_type(const RlParams &p, int64_t n, int ng, bool wide, bool fused, bool dump, hipStream_t s) {
+    constexpr bool Q6 = TYPE == TYPE_Q6_K;
+    if (wide) {
+        const int64_t nch = (n + RL_ROWS - 1) / RL_ROWS;
+        // more chunks than CUs: persistent workgroups, one per CU
+        if (ng <= 16 && nch > RL_PERSIST_CUS)
+            return launch_g<TYPE, RL_ROWS, 16, 1, Q6 ? 13 : 9, true, true>(p, RL_PERSIST_CUS, fused, dump, s);
+        const unsigned grid = (unsigned)nch;
+        if (ng <= 16) return launch_g<TYPE, RL_ROWS, 16, 1, Q6 ? 8 : 6, true>(p, grid, fused, dump, s);
+        if constexpr (!Q6) return launch_g<TYPE, RL_ROWS, 16, 2, 12, true>(p, grid, fused, dump, s);
+        return hipErrorNotSupported;
+    }
+    // 16 rows: as many wavefronts as four groups each need (every lane one
+    // group); the quantising wavefronts (four blocks each) are then always
+    // enough.  Up to 32 groups all of a lane's pieces are in flight from the
+    // start; with 16 wavefronts (Q4_K ffn_down, 56 groups) five, issued after
+    // the quantisation, measured fastest (8.3 us against 8.6 for nine issued
+    // late and 9.7 for nine issued early).
+    const unsigned grid = (unsigned)((n + RG_ROWS - 1) / RG_ROWS);
+    if (ng <= 16) return launch_g<TYPE, RG_ROWS, 4, 1, Q6 ? 13 : 9, true>(p, grid, fused, dump, s);
+    if (ng <= 32) return launch_g<TYPE, RG_ROWS, 8, 1, Q6 ? 13 : 9, true>(p, grid, fused, dump, s);
+    return launch_g<TYPE, RG_ROWS, 16, 1, Q6 ? 7 : 5, false>(p, grid, fused, dump, s);
+}
 
 }  // namespace
 
 bool rowlane_matvec_applies(int type, int64_t n, int64_t k) {
-    return type == TYPE_Q4_K && k % QK_K == 0 && k > 0 && k / QK_K <= RL_MAXG && n <= 0x7fffffff &&
-           (rows56(n, (int)(k / QK_K)) || n >= RG_MIN_N);
+    return (type == TYPE_Q4_K || type == TYPE_Q6_K) && k % QK_K == 0 && k > 0 && k / QK_K <= RL_MAXG && n <= 0x7fffffff &&
+           (rows56(type, n, (int)(k / QK_K)) || n >= RG_MIN_N);
 }
 
 hipError_t launch_rowlane_matvec(const WLayout &w, int64_t n, int64_t k, const float *x, const ActPlanes *act,
@@ -314,12 +464,15 @@ hipError_t launch_rowlane_matvec(const WLayout &w, int64_t n, int64_t k, const f
     if (!rowlane_matvec_applies(w.type, n, k)) return hipErrorNotSupported;
     if (!w.slab || !y || (!x && !act) || (S == nullptr) != (Smin == nullptr)) return hipErrorInvalidValue;
     const int ng = (int)(k / QK_K);
-    if (w.ng != ng || w.rb_stride != (int64_t)ng * 9 * 128) return hipErrorInvalidValue;
+    const int npg = w.type == TYPE_Q6_K ? 13 : 9;
+    if (w.ng != ng || w.rb_stride != (int64_t)ng * npg * 128) return hipErrorInvalidValue;
+    if (w.type == TYPE_Q6_K && !w.d) return hipErrorInvalidValue;
     if (x && ((uintptr_t)x & 15)) return hipErrorInvalidValue;
-    const bool wide = rows56(n, ng);
+    const bool wide = rows56(w.type, n, ng);
     if ((int64_t)(wide ? RL_ROWS : RG_ROWS) / RB * w.rb_stride >= ((int64_t)1 << 31)) return hipErrorNotSupported;
     RlParams p;
     p.w = w.slab;
+    p.wd = w.d;
     p.rb_stride = w.rb_stride;
     p.n = (int)n;
     p.k = (int)k;
@@ -330,23 +483,8 @@ hipError_t launch_rowlane_matvec(const WLayout &w, int64_t n, int64_t k, const f
     p.S = S;
     p.Smin = Smin;
     const bool fused = x != nullptr, dump = S != nullptr;
-    if (wide) {
-        const unsigned grid = (unsigned)((n + RL_ROWS - 1) / RL_ROWS);
-        // 16 wavefronts with six pieces in flight each measured fastest at the
-        // headline (one group per wavefront); longer rows take two groups each
-        if (ng <= 16) return launch_g<RL_ROWS, 16, 1, 6, true>(p, grid, fused, dump, s);
-        return launch_g<RL_ROWS, 16, 2, 12, true>(p, grid, fused, dump, s);
-    }
-    // 16 rows: as many wavefronts as four groups each need (every lane one
-    // group); the quantising wavefronts (four blocks each) are then always
-    // enough.  Up to 32 groups all nine pieces of a lane's group are in
-    // flight from the start; with 16 wavefronts (ffn_down, 56 groups) five,
-    // issued after the quantisation, measured fastest (8.3 us against 8.6
-    // for nine issued late and 9.7 for nine issued early).
-    const unsigned grid = (unsigned)((n + RG_ROWS - 1) / RG_ROWS);
-    if (ng <= 16) return launch_g<RG_ROWS, 4, 1, 9, true>(p, grid, fused, dump, s);
-    if (ng <= 32) return launch_g<RG_ROWS, 8, 1, 9, true>(p, grid, fused, dump, s);
-    return launch_g<RG_ROWS, 16, 1, 5, false>(p, grid, fused, dump, s);
+    if (w.type == TYPE_Q6_K) return launch_type<TYPE_Q6_K>(p, n, ng, wide, fused, dump, s);
+    return launch_type<TYPE_Q4_K>(p, n, ng, wide, fused, dump, s);
 }
 
 }  // namespace aq

@@ -238,6 +238,7 @@ MATVEC_CASES = {  # name: (weight type, n, k, m, seed)
     "c4_q4k_4096x14336_b1": (12, 4096, 14336, 1, 5),
     "c4_q4k_14336x4096_b8": (12, 14336, 4096, 8, 6),
     "c4_q4k_4096x14336_b8": (12, 4096, 14336, 8, 8),
+    "c4_q6k_4096x14336_b1": (14, 4096, 14336, 1, 20),  # ffn_down in a Q4_K_M file's Q6_K layers
     "c4_q6k_128256x4096_b1": (14, 128256, 4096, 1, 7),
     "c4_q6k_128256x4096_b8": (14, 128256, 4096, 8, 9),
     "q5k_14336x4096_b1": (13, 14336, 4096, 1, 13),  # a Q5_K_M file's ffn_up, batch 1
@@ -569,7 +570,7 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic_from_profile(),
-            "kernel": "rl_q4k_kernel<16, 1, 6, true, false> (Q4_K, batch 1, one weight row per lane, Q8_K quantisation fused)",
+            "kernel": "rl_kernel<12, 56, 16, 1, 6, true, true, false, false> (Q4_K, batch 1, one weight row per lane, Q8_K quantisation fused)",
             "bytes_per_launch": wl.step_bytes,
             "avg_launch_us": round(step_ms * 1e3, 3),
         },

@@ -26,7 +26,7 @@ RG_MIN_N = 3200   # rows from which it takes the 16-row form (any k <= 16384)
 
 
 @pytest.mark.parametrize("n,k", [
-    (14336, 4096),   # the headline shape: 256 workgroups of 56 rows, two groups per wavefront
+    (14336, 4096),   # the headline shape: 256 workgroups of 56 rows, one group per wavefront
     (RL_MIN_N, 256),  # one group: a single quantising wavefront
     (11203, 2048),   # ragged: the last workgroup's rows and its last row block are partial
     (11264, 5632),   # 22 groups: three groups per wavefront, some wavefronts short
@@ -50,6 +50,58 @@ def test_rowlane16_matches_oracle(ctx, n, k):
     W = S.make_weight(S.TYPE_Q4_K, n, k, seed=n + k + 1)
     x = S.make_activation(1, k, seed=k + 1)
     check_matmul(ctx, W, x)
+
+
+@pytest.mark.parametrize("n,k", [
+    (32000, 2048),    # config 1's lm_head: 572 workgroups of 56 rows
+    (RL_MIN_N, 256),  # one group
+    (11203, 4096),    # ragged rows, 16 groups
+    (12000, 8192),    # 32 groups: two per wavefront
+    (4096, 14336),    # Llama-3-8B ffn_down in its Q6_K layers: the 16-row form, 56 groups
+    (3203, 4096),     # 16-row form, ragged rows, four wavefronts
+    (5000, 8448),     # 33 groups, a wavefront's lanes straddling the last group
+])
+def test_rowlane_q6k_matches_oracle(ctx, n, k):
+    """Q6_K through the row-per-lane kernel (13 pieces per group, the scales
+    and qh pieces held while the ql pieces stream, the d plane read per
+    group), with llama.cpp's full int8 sub-scale range."""
+    rng = np.random.default_rng(n + k + 3)
+    W = S.make_weight(S.TYPE_Q6_K, n, k, seed=n + k + 2)
+    W.sc[:] = rng.integers(-128, 128, size=W.sc.shape).astype(np.int8)
+    W.blocks = S.pack_q6k(W.d, W.sc, W.q)
+    x = S.make_activation(1, k, seed=k + 2)
+    check_matmul(ctx, W, x)
+
+
+@pytest.mark.parametrize("typ,n,k", [
+    (S.TYPE_Q4_K, 32000, 4096),    # 572 chunks over 512 persistent workgroups: some walk two
+    (S.TYPE_Q4_K, 60001, 1024),    # 1072 chunks, ragged rows, four groups (12 idle wavefronts)
+    (S.TYPE_Q6_K, 128256, 4096),   # Llama-3-8B lm_head: 2291 chunks, about 4.5 per workgroup
+    (S.TYPE_Q6_K, 70003, 768),     # three groups, ragged rows
+])
+def test_rowlane_persistent_chunks(ctx, typ, n, k):
+    """More 56-row chunks than two per CU: workgroups quantise the activation
+    once and walk several chunks, with the next chunk's pieces in flight."""
+    rng = np.random.default_rng(n + k + 5)
+    W = S.make_weight(typ, n, k, seed=n + k + 4)
+    if typ == S.TYPE_Q6_K:
+        W.sc[:] = rng.integers(-128, 128, size=W.sc.shape).astype(np.int8)
+        W.blocks = S.pack_q6k(W.d, W.sc, W.q)
+    x = S.make_activation(1, k, seed=k + 4)
+    check_matmul(ctx, W, x)
+
+
+def test_rowlane_q6k_extreme_values(ctx):
+    """Every Q6_K quant at -32 and every sub-scale -128 against activation
+    blocks of equal values: the largest sums, bit-exact."""
+    n, k = RL_MIN_N, 4096
+    rng = np.random.default_rng(8)
+    W = S.make_weight(S.TYPE_Q6_K, n, k, seed=9)
+    W.q[:] = -32
+    W.sc[:] = -128
+    W.blocks = S.pack_q6k(W.d, W.sc, W.q)
+    x = np.repeat(np.abs(rng.standard_normal((1, k // 256))).astype(np.float32) + 0.5, 256, axis=1)
+    check_matmul(ctx, W, x, cond=False)
 
 
 def test_rowlane16_edge_activations(ctx):
