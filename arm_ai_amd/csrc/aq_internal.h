@@ -146,12 +146,20 @@ hipError_t launch_expand_q80(int type, const uint8_t *src, int64_t n, int64_t k,
 // S/Smin non-null selects the integer-dump variant ([m][n][blocks] int32).
 hipError_t launch_matvec(const WLayout &w, int64_t n, int64_t k, const float *x, const ActPlanes *act, int64_t m,
                          float *y, int32_t *S, int32_t *Smin, hipStream_t s);
-// Batch-1 Q4_K matvec with one weight row per lane (k_rowlane.hip), for
-// weights with many rows and k <= 8192; hipErrorNotSupported for other shapes.
-// x (f32, quantised in the kernel) or act (pre-quantised planes of one row).
+// Batch-1 Q4_K / Q6_K matvec with one weight row per lane (k_rowlane.hip),
+// for weights of at least 3200 rows and k <= 16384; hipErrorNotSupported for
+// other shapes.  x (f32, quantised in the kernel) or act (pre-quantised
+// planes of one row).  norm (x only, no dump, k <= 8192): quantise
+// rms_norm(x + delta) * w instead, workgroup 0 writing x + delta to xout.
+struct RlNorm {
+    const float *delta, *w;
+    float eps;
+    float *xout;
+};
 bool rowlane_matvec_applies(int type, int64_t n, int64_t k);
+bool rowlane_norm_applies(int type, int64_t n, int64_t k);
 hipError_t launch_rowlane_matvec(const WLayout &w, int64_t n, int64_t k, const float *x, const ActPlanes *act,
-                                 float *y, int32_t *S, int32_t *Smin, hipStream_t s);
+                                 float *y, int32_t *S, int32_t *Smin, hipStream_t s, const RlNorm *norm = nullptr);
 // Matvec of pre-quantised (Q8_K) rows on the int8 matrix cores, 8 rows per
 // launch, Q4_K / Q6_K weights, k <= mmv_max_k().  Returns hipErrorNotSupported
 // for other types and shapes (the caller then uses launch_matvec).
@@ -434,6 +442,55 @@ __device__ __forceinline__ uint32_t q8k_block_wave(const float v[4], int lane, i
     *bsum = quad_sum_i(q[0] + q[1] + q[2] + q[3]);
     *d = dd;
     return pack4_i8(q);
+}
+
+// One Q8_K block (candle-core 0.8.4 BlockQ8K::from_float) by the 16 lanes of a
+// DPP row: lane s holds elements 16s..16s+15 in v.  Same arithmetic as
+// q8k_block_wave: max = the first element of largest |x| (NaN
+// never wins), iscale = -128/max, q = min(round(iscale*x), 127) ties away
+// from zero, d = 1/iscale; an all-zero block gives d = 0, q = 0.  The first
+// index of the maximum is found as the smallest key (index << 1 | sign) over
+// the row, and its sign gives max = +-amax exactly.  Returns the 16 quants
+// packed; *bsum gets the sum of this lane's 16 quants, *d the block's d.
+__device__ __forceinline__ uint4 q8k_block_row16(const float v[16], int s, int *bsum, float *d) {
+    float ax[16];
+    float m = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        const float a = fabsf(v[i]);
+        ax[i] = a == a ? a : 0.0f;
+        m = fmaxf(m, ax[i]);
+    }
+    m = fmaxf(m, dpp_f<DPP_QUAD_XOR1>(m));
+    m = fmaxf(m, dpp_f<DPP_QUAD_XOR2>(m));
+    m = fmaxf(m, dpp_f<DPP_HALF_MIRROR>(m));
+    m = fmaxf(m, dpp_f<DPP_ROW_MIRROR>(m));
+    int q[16];
+    float dd = 0.0f;
+    if (m != 0.0f) {  // uniform over the row
+        int key = 1 << 30;
+#pragma unroll
+        for (int i = 15; i >= 0; i--)
+            if (ax[i] == m) key = ((16 * s + i) << 1) | (v[i] < 0.0f ? 1 : 0);
+        key = min(key, dpp_i<DPP_QUAD_XOR1>(key));
+        key = min(key, dpp_i<DPP_QUAD_XOR2>(key));
+        key = min(key, dpp_i<DPP_HALF_MIRROR>(key));
+        key = min(key, dpp_i<DPP_ROW_MIRROR>(key));
+        const float mx = (key & 1) ? -m : m;
+        const float iscale = -128.0f / mx;
+#pragma unroll
+        for (int i = 0; i < 16; i++) q[i] = sat_i8(fminf(roundf(iscale * v[i]), 127.0f));
+        dd = 1.0f / iscale;
+    } else {
+#pragma unroll
+        for (int i = 0; i < 16; i++) q[i] = 0;
+    }
+    int bs = 0;
+#pragma unroll
+    for (int i = 0; i < 16; i++) bs += q[i];
+    *bsum = bs;
+    *d = dd;
+    return make_uint4(pack4_i8(q), pack4_i8(q + 4), pack4_i8(q + 8), pack4_i8(q + 12));
 }
 
 // One Q8_0 block (BlockQ8_0::from_float) quantised by eight consecutive

@@ -915,6 +915,11 @@ hipError_t matvec_impl(const WLayout &w, int64_t n, int64_t k, const float *x, c
         const hipError_t e = launch_rowlane_matvec(w, n, k, x, act, y, S, Smin, s);
         if (e != hipErrorNotSupported) return e;
     }
+    if (xa.xf == XF_NORM && rowlane_norm_applies(type, n, k)) {
+        const RlNorm nm{xa.delta, xa.norm, xa.eps, xa.xout};
+        const hipError_t e = launch_rowlane_matvec(w, n, k, x, nullptr, y, nullptr, nullptr, s, &nm);
+        if (e != hipErrorNotSupported) return e;
+    }
     const int ng = w.ng;
     if ((size_t)ng * REC > LDS_CAP) return hipErrorNotSupported;  // k > 124160
     if ((int64_t)8 * n * 4 >= ((int64_t)1 << 31)) return hipErrorNotSupported;  // y of a pass: 32-bit buffer offsets

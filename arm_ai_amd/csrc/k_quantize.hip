@@ -10,39 +10,56 @@
 
 namespace aq {
 
-// One wavefront per 256-element block, four blocks per 256-thread workgroup.
+// Sixteen lanes (one DPP row) per 256-element block, lane s holding elements
+// 16s..16s+15: four blocks per wavefront, sixteen per 256-thread workgroup.
+// Each lane loads 64 contiguous bytes and stores its 16 quants and its own
+// 16-element bsum, so every store of the wavefront is one contiguous run.
 template <bool VEC>
 __global__ __launch_bounds__(256) void quantize_q8k_kernel(const float *__restrict__ x, int64_t nblocks,
                                                            int64_t k, ActPlanes a) {
-    const int lane = threadIdx.x & 63;
-    const int64_t bi = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (bi >= nblocks) return;  // wave-uniform
+    const int lane = threadIdx.x & 63, s = lane & 15;
+    const int64_t bi = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+    const bool ok = bi < nblocks;  // uniform over the row of 16 lanes
     const int64_t nb = k / QK_K;
-    const int64_t row = bi / nb, sb = bi - row * nb;
-    const float *xb = x + row * k + sb * QK_K + 4 * lane;
-    float v[4];
-    if (VEC) {
-        const float4 t = *(const float4 *)xb;
-        v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
+    const int64_t row = ok ? bi / nb : 0, sb = ok ? bi - row * nb : 0;
+    const int64_t e0 = row * k + sb * QK_K + 16 * s;
+    float v[16];
+    if (!ok) {
+#pragma unroll
+        for (int i = 0; i < 16; i++) v[i] = 0.0f;
+    } else if (VEC) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float4 t = *(const float4 *)(x + e0 + 4 * i);
+            v[4 * i] = t.x;
+            v[4 * i + 1] = t.y;
+            v[4 * i + 2] = t.z;
+            v[4 * i + 3] = t.w;
+        }
     } else {
-        for (int i = 0; i < 4; i++) v[i] = xb[i];
+#pragma unroll
+        for (int i = 0; i < 16; i++) v[i] = x[e0 + i];
     }
     int bsum;
     float d;
-    const uint32_t packed = q8k_block_wave(v, lane, &bsum, &d);
-    *(uint32_t *)(a.qs + row * k + sb * QK_K + 4 * lane) = packed;
+    const uint4 packed = q8k_block_row16(v, s, &bsum, &d);
+    if (!ok) return;  // after the row's DPP exchanges
+    *(uint4 *)(a.qs + e0) = packed;
     if (a.q16) {  // uniform: the f16 copy for the f16-MFMA GEMMs
-        uint32_t o[4];
+        const uint32_t w[4] = {packed.x, packed.y, packed.z, packed.w};
+        uint32_t o[8];
 #pragma unroll
-        for (int j = 0; j < 4; j++)
-            o[j] = __builtin_bit_cast(uint16_t, (_Float16)(int)(int8_t)((packed >> (8 * j)) & 0xffu));
-        *(uint2 *)(a.q16 + row * k + sb * QK_K + 4 * lane) = make_uint2(o[0] | (o[1] << 16), o[2] | (o[3] << 16));
+        for (int j = 0; j < 8; j++) {
+            const uint32_t lo = __builtin_bit_cast(uint16_t, (_Float16)(int)(int8_t)((w[j >> 1] >> (16 * (j & 1))) & 0xffu));
+            const uint32_t hi = __builtin_bit_cast(uint16_t, (_Float16)(int)(int8_t)((w[j >> 1] >> (16 * (j & 1) + 8)) & 0xffu));
+            o[j] = lo | (hi << 16);
+        }
+        *(uint4 *)(a.q16 + e0) = make_uint4(o[0], o[1], o[2], o[3]);
+        *(uint4 *)(a.q16 + e0 + 8) = make_uint4(o[4], o[5], o[6], o[7]);
     }
-    if ((lane & 3) == 0) {
-        a.bsums[row * (k / 16) + sb * 16 + (lane >> 2)] = (int16_t)bsum;
-        a.bsum16[row * (k / 16) + sb * 16 + (lane >> 2)] = __builtin_bit_cast(uint16_t, (_Float16)(float)bsum);
-    }
-    if (lane == 0) a.d[row * nb + sb] = d;
+    a.bsums[row * (k / 16) + sb * 16 + s] = (int16_t)bsum;
+    a.bsum16[row * (k / 16) + sb * 16 + s] = __builtin_bit_cast(uint16_t, (_Float16)(float)bsum);
+    if (s == 0) a.d[row * nb + sb] = d;
 }
 
 // Eight lanes per 32-element block, 32 blocks per workgroup.
@@ -78,7 +95,7 @@ hipError_t launch_quantize_q8k(const float *x, int64_t m, int64_t k, ActPlanes a
     if (!x || m < 0 || k <= 0 || k % QK_K) return hipErrorInvalidValue;
     if (m == 0) return hipSuccess;
     const int64_t nblocks = m * (k / QK_K);
-    const int64_t grid = (nblocks + 3) / 4;
+    const int64_t grid = (nblocks + 15) / 16;
     if (grid > 0x7fffffff) return hipErrorInvalidValue;
     if (((uintptr_t)x & 15) == 0)
         quantize_q8k_kernel<true><<<dim3((unsigned)grid), dim3(256), 0, s>>>(x, nblocks, k, a);

@@ -48,6 +48,7 @@ constexpr int RL_MIN_N = 200 * RL_ROWS;  // rows from which 56-row workgroups ar
 constexpr int RG_ROWS = 16;    // weight rows per workgroup of the four-group-phase form
 constexpr int RG_MIN_N = 200 * RG_ROWS;  // rows from which that form is used (up to 64 groups)
 constexpr int RL_PERSIST_CUS = 256;      // the persistent grid: one workgroup per CU
+constexpr int RL_NORM_MAXG = 32;         // the fused norm: rows of up to 8192 elements (as the general matvec)
 
 struct RlParams {
     const uint8_t *w;  // row-block tiles
@@ -55,68 +56,15 @@ struct RlParams {
     int64_t rb_stride;
     int n, k, ng;
     const float *x;    // fused: f32 [k]
+    // fused RMSNorm (NORM): quantise rms_norm(x + xdelta) * xnorm; workgroup 0
+    // writes x + xdelta to xout (xdelta, xout may be null)
+    const float *xdelta, *xnorm;
+    float *xout;
+    float eps;
     ActPlanes act;     // pre-quantised planes (x null)
     float *y;
     int32_t *S, *Smin;  // [n][ng] integer dump, or null
 };
-
-template <int CTRL>
-__device__ __forceinline__ int dpp_row(int v) {
-    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
-}
-template <int CTRL>
-__device__ __forceinline__ float dpp_rowf(float v) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
-}
-
-// One Q8_K block (candle-core 0.8.4 BlockQ8K::from_float) by the 16 lanes of a
-// DPP row: lane s holds elements 16s..16s+15 in v.  Same arithmetic as
-// q8k_block_wave (aq_internal.h): max = the first element of largest |x| (NaN
-// never wins), iscale = -128/max, q = min(round(iscale*x), 127) ties away
-// from zero, d = 1/iscale; an all-zero block gives d = 0, q = 0.  The first
-// index of the maximum is found as the smallest key (index << 1 | sign) over
-// the row, and its sign gives max = +-amax exactly.  Returns the 16 quants
-// packed; *bsum gets the sum of this lane's 16 quants, *d the block's d.
-__device__ __forceinline__ uint4 q8k_block_row16(const float v[16], int s, int *bsum, float *d) {
-    float ax[16];
-    float m = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 16; i++) {
-        const float a = fabsf(v[i]);
-        ax[i] = a == a ? a : 0.0f;
-        m = fmaxf(m, ax[i]);
-    }
-    m = fmaxf(m, dpp_rowf<DPP_QUAD_XOR1>(m));
-    m = fmaxf(m, dpp_rowf<DPP_QUAD_XOR2>(m));
-    m = fmaxf(m, dpp_rowf<DPP_HALF_MIRROR>(m));
-    m = fmaxf(m, dpp_rowf<DPP_ROW_MIRROR>(m));
-    int q[16];
-    float dd = 0.0f;
-    if (m != 0.0f) {  // uniform over the row
-        int key = 1 << 30;
-#pragma unroll
-        for (int i = 15; i >= 0; i--)
-            if (ax[i] == m) key = ((16 * s + i) << 1) | (v[i] < 0.0f ? 1 : 0);
-        key = min(key, dpp_row<DPP_QUAD_XOR1>(key));
-        key = min(key, dpp_row<DPP_QUAD_XOR2>(key));
-        key = min(key, dpp_row<DPP_HALF_MIRROR>(key));
-        key = min(key, dpp_row<DPP_ROW_MIRROR>(key));
-        const float mx = (key & 1) ? -m : m;
-        const float iscale = -128.0f / mx;
-#pragma unroll
-        for (int i = 0; i < 16; i++) q[i] = sat_i8(fminf(roundf(iscale * v[i]), 127.0f));
-        dd = 1.0f / iscale;
-    } else {
-#pragma unroll
-        for (int i = 0; i < 16; i++) q[i] = 0;
-    }
-    int bs = 0;
-#pragma unroll
-    for (int i = 0; i < 16; i++) bs += q[i];
-    *bsum = bs;
-    *d = dd;
-    return make_uint4(pack4_i8(q), pack4_i8(q + 4), pack4_i8(q + 8), pack4_i8(q + 12));
-}
 
 // R rows per workgroup: RL_ROWS (lane = row, one group phase) or RG_ROWS
 // (lane = row + 16 * group phase, four phases).  Lane (row r, phase gp) of
@@ -135,8 +83,9 @@ __device__ __forceinline__ uint4 q8k_block_row16(const float v[16], int s, int *
 // blockIdx.x, blockIdx.x + gridDim.x, ...; every piece of the next chunk is
 // issued right after the same piece of the current one is consumed (P =
 // pieces per group), so the stream does not drain between chunks.
-template <int TYPE, int R, int W, int GPW, int P, bool EARLY, bool FUSED, bool DUMP, bool CH = false>
+template <int TYPE, int R, int W, int GPW, int P, bool EARLY, bool FUSED, bool DUMP, bool CH = false, bool NORM = false>
 __global__ __launch_bounds__(W * 64) void rl_kernel(RlParams p) {
+    static_assert(!NORM || (FUSED && !DUMP), "the fused norm takes an f32 input and no integer dump");
     static_assert(R == RL_ROWS || R == RG_ROWS, "56 rows, one per lane, or 16 rows in four group phases");
     static_assert(TYPE == TYPE_Q4_K || TYPE == TYPE_Q6_K, "Q4_K or Q6_K");
     static_assert(!CH || (R == RL_ROWS && GPW == 1 && P == (TYPE == TYPE_Q6_K ? 13 : 9)),
@@ -148,6 +97,7 @@ __global__ __launch_bounds__(W * 64) void rl_kernel(RlParams p) {
     __shared__ __align__(16) int xb[RL_MAXG][Q6 ? 16 : 8];  // bsums per 16 (Q6_K) or 32 (Q4_K) elements
     __shared__ float xd[RL_MAXG];                       // Q8_K d
     __shared__ float red[CH ? 2 : 1][W][64];
+    __shared__ float nred[W];  // NORM: the quantising wavefronts' sums of squares
     constexpr int NP = NPG * GPW;  // this wavefront's pieces, in order
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
@@ -210,14 +160,23 @@ __global__ __launch_bounds__(W * 64) void rl_kernel(RlParams p) {
     const int gb = 4 * wave + (lane >> 4);
     const bool quantiser = wave < (p.ng + 3) / 4;  // uniform
     const bool gbok = gb < p.ng;
-    u32x4 xv[4];
+    u32x4 xv[4], dv[4], nv[4];
     uint32_t xbs = 0, xdb = 0;
+    const uint32_t xo = gbok ? (uint32_t)((gb * QK_K + 16 * s) * 4) : BUF_OOB;
     if (quantiser) {
         if (FUSED) {
             const rsrc_t rx = buf_rsrc(p.x, (uint32_t)(p.k * 4));
-            const uint32_t xo = gbok ? (uint32_t)((gb * QK_K + 16 * s) * 4) : BUF_OOB;
 #pragma unroll
             for (int i = 0; i < 4; i++) xv[i] = __builtin_amdgcn_raw_buffer_load_b128(rx, xo + 16 * i, 0, 0);
+            if (NORM) {  // a null delta: an empty range, zeros
+                const rsrc_t rdl = buf_rsrc(p.xdelta, p.xdelta ? (uint32_t)(p.k * 4) : 0u);
+                const rsrc_t rnw = buf_rsrc(p.xnorm, (uint32_t)(p.k * 4));
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    dv[i] = __builtin_amdgcn_raw_buffer_load_b128(rdl, xo + 16 * i, 0, 0);
+                    nv[i] = __builtin_amdgcn_raw_buffer_load_b128(rnw, xo + 16 * i, 0, 0);
+                }
+            }
         } else {
             const rsrc_t rq = buf_rsrc(p.act.qs, (uint32_t)p.k);
             const rsrc_t rs = buf_rsrc(p.act.bsums, (uint32_t)((p.k / 16) * 2));
@@ -231,27 +190,68 @@ __global__ __launch_bounds__(W * 64) void rl_kernel(RlParams p) {
 #pragma unroll
         for (int j = 0; j < P && j < NP; j++) issue(j);
     }
-    // 2. quantise (or unpack) into LDS, then one barrier (LDS writes only)
+    // 2. quantise (or unpack) into LDS, then one barrier (LDS writes only).
+    //    NORM: h = x + delta and the row's sum of squares first (every
+    //    wavefront takes the barrier; lanes past the row hold zeros), then
+    //    (h / sqrt(mean(h^2) + eps)) * w is quantised.
+    float v[16];
+    if (FUSED && quantiser) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            v[4 * i] = u32_as_f32(xv[i].x);
+            v[4 * i + 1] = u32_as_f32(xv[i].y);
+            v[4 * i + 2] = u32_as_f32(xv[i].z);
+            v[4 * i + 3] = u32_as_f32(xv[i].w);
+        }
+    }
+    if (NORM) {
+        float ss = 0.0f;
+        if (quantiser) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                v[4 * i] += u32_as_f32(dv[i].x);
+                v[4 * i + 1] += u32_as_f32(dv[i].y);
+                v[4 * i + 2] += u32_as_f32(dv[i].z);
+                v[4 * i + 3] += u32_as_f32(dv[i].w);
+            }
+#pragma unroll
+            for (int i = 0; i < 16; i++) ss = __builtin_fmaf(v[i], v[i], ss);
+#pragma unroll
+            for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
+            if (lane == 0) nred[wave] = ss;
+        }
+        lds_barrier();
+        if (quantiser) {
+            const int nq = (p.ng + 3) / 4;
+            float tot = 0.0f;
+            for (int w2 = 0; w2 < nq; w2++) tot += nred[w2];
+            const float mden = sqrtf(tot / (float)p.k + p.eps);
+            if (p.xout && blockIdx.x == 0 && gbok) {  // the residual stream x + delta
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    *(float4 *)(p.xout + gb * QK_K + 16 * s + 4 * i) = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                v[4 * i] = (v[4 * i] / mden) * u32_as_f32(nv[i].x);
+                v[4 * i + 1] = (v[4 * i + 1] / mden) * u32_as_f32(nv[i].y);
+                v[4 * i + 2] = (v[4 * i + 2] / mden) * u32_as_f32(nv[i].z);
+                v[4 * i + 3] = (v[4 * i + 3] / mden) * u32_as_f32(nv[i].w);
+            }
+        }
+    }
     if (quantiser) {
         uint4 qv;
         int bsum;
         float d;
         if (FUSED) {
-            float v[16];
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                v[4 * i] = u32_as_f32(xv[i].x);
-                v[4 * i + 1] = u32_as_f32(xv[i].y);
-                v[4 * i + 2] = u32_as_f32(xv[i].z);
-                v[4 * i + 3] = u32_as_f32(xv[i].w);
-            }
             qv = q8k_block_row16(v, s, &bsum, &d);
         } else {
             qv = make_uint4(xv[0].x, xv[0].y, xv[0].z, xv[0].w);
             bsum = (int)(int16_t)xbs;
             d = u32_as_f32(xdb);
         }
-        const int pair = bsum + dpp_row<DPP_QUAD_XOR1>(bsum);  // sub-block s/2 (two 16-element halves)
+        const int pair = bsum + dpp_i<DPP_QUAD_XOR1>(bsum);  // sub-block s/2 (two 16-element halves)
         if (gbok) {
             *(uint4 *)&xq[gb][16 * s] = qv;
             if (Q6) xb[gb][s] = bsum;
@@ -410,6 +410,10 @@ __global__ __launch_bounds__(W * 64) void rl_kernel(RlParams p) {
 
 template <int TYPE, int R, int W, int GPW, int P, bool EARLY, bool CH = false>
 hipError_t launch_g(const RlParams &p, unsigned grid, bool fused, bool dump, hipStream_t s) {
+    if (p.xnorm) {  // the fused norm (f32 input, no dump: the caller checks)
+        rl_kernel<TYPE, R, W, GPW, P, EARLY, true, false, CH, true><<<grid, W * 64, 0, s>>>(p);
+        return hipGetLastError();
+    }
     if (fused) {
         if (dump) rl_kernel<TYPE, R, W, GPW, P, EARLY, true, true, CH><<<grid, W * 64, 0, s>>>(p);
         else rl_kernel<TYPE, R, W, GPW, P, EARLY, true, false, CH><<<grid, W * 64, 0, s>>>(p);
@@ -459,10 +463,15 @@ bool rowlane_matvec_applies(int type, int64_t n, int64_t k) {
            (rows56(type, n, (int)(k / QK_K)) || n >= RG_MIN_N);
 }
 
+bool rowlane_norm_applies(int type, int64_t n, int64_t k) {
+    return rowlane_matvec_applies(type, n, k) && k / QK_K <= RL_NORM_MAXG;
+}
+
 hipError_t launch_rowlane_matvec(const WLayout &w, int64_t n, int64_t k, const float *x, const ActPlanes *act,
-                                 float *y, int32_t *S, int32_t *Smin, hipStream_t s) {
+                                 float *y, int32_t *S, int32_t *Smin, hipStream_t s, const RlNorm *norm) {
     if (!rowlane_matvec_applies(w.type, n, k)) return hipErrorNotSupported;
     if (!w.slab || !y || (!x && !act) || (S == nullptr) != (Smin == nullptr)) return hipErrorInvalidValue;
+    if (norm && (!x || S || !norm->w || k / QK_K > RL_NORM_MAXG)) return hipErrorInvalidValue;
     const int ng = (int)(k / QK_K);
     const int npg = w.type == TYPE_Q6_K ? 13 : 9;
     if (w.ng != ng || w.rb_stride != (int64_t)ng * npg * 128) return hipErrorInvalidValue;
@@ -478,6 +487,10 @@ hipError_t launch_rowlane_matvec(const WLayout &w, int64_t n, int64_t k, const f
     p.k = (int)k;
     p.ng = ng;
     p.x = x;
+    p.xdelta = norm ? norm->delta : nullptr;
+    p.xnorm = norm ? norm->w : nullptr;
+    p.xout = norm ? norm->xout : nullptr;
+    p.eps = norm ? norm->eps : 0.0f;
     p.act = act ? *act : ActPlanes{};
     p.y = y;
     p.S = S;

@@ -218,9 +218,14 @@ def _weight(A, S, wtype, n, k, ctx, seed):
     return W, A.QMatMul.from_qtensor(A.QTensor(wtype, (n, k), W.blocks), ctx)
 
 
-@pytest.mark.parametrize("wtype,n,k,with_delta", [(12, 2304, 2048, True), (14, 256, 2048, False),
-                                                  (12, 1000, 4096, True), (8, 300, 1024, True),
-                                                  (13, 2304, 2048, True)])
+@pytest.mark.parametrize("wtype,n,k,with_delta", [
+    (12, 2304, 2048, True), (14, 256, 2048, False), (12, 1000, 4096, True), (8, 300, 1024, True),
+    (13, 2304, 2048, True),
+    # the row-per-lane kernel's fused norm: 56-row workgroups, persistent
+    # chunks, the 16-row form with four and eight wavefronts, ragged rows
+    (12, 11264, 2048, True), (14, 32000, 2048, False), (12, 28672, 4096, True),
+    (12, 4096, 4096, True), (14, 5000, 8192, True), (12, 3203, 2048, False),
+])
 def test_matvec_fused_rmsnorm(env, wtype, n, k, with_delta):
     """y = W . rms_norm(x + delta) * w_norm in one launch, against the oracle's
     matmul of the same input formed in numpy; h_out = x + delta exactly."""

@@ -157,6 +157,35 @@ def test_prefill_gemm_extreme_values(ctx):
     check_matmul(ctx, W, x, cond=False)
 
 
+@pytest.mark.parametrize("m,n,k", [
+    (128, 128, 256),    # two m-tiles, one n-tile, one super-block
+    (129, 300, 1280),   # a last m-tile of one row; 5 super-blocks split 3 + 2
+    (384, 1000, 3840),  # 15 super-blocks: an odd count per split
+    (511, 64, 2048),    # one partial n-tile, many splits
+    (640, 4100, 512),   # ragged columns, two super-blocks
+])
+def test_prefill_gemm_odd_splits(ctx, m, n, k):
+    """Longer prompts with ragged rows and columns and K splits of unequal
+    super-block counts (the split-K reduction adds them in split order)."""
+    W = S.make_weight(S.TYPE_Q4_K, n, k, seed=m + n + 7)
+    x = S.make_activation(m, k, seed=m * 3 + n)
+    check_matmul(ctx, W, x)
+
+
+def test_prefill_gemm_extreme_values_long_prompt(ctx):
+    """The largest Q4_K . Q8_K sums over 256 rows (four m-tiles)."""
+    n, k, m = 256, 1024, 256
+    rng = np.random.default_rng(6)
+    W = S.make_weight(S.TYPE_Q4_K, n, k, seed=6)
+    W.q[:] = 15
+    W.sc[:] = 63
+    W.mn[:] = 63
+    W.blocks = S.pack_q4k(W.d, W.dmin, W.sc, W.mn, W.q)
+    x = np.repeat(rng.standard_normal((m, k // 256)).astype(np.float32), 256, axis=1)
+    x[1::2] = -np.abs(x[1::2])
+    check_matmul(ctx, W, x, cond=False)
+
+
 # ----------------------------------------- Q6_K prefill GEMM (f16 MFMA, m > 8)
 @pytest.mark.parametrize("n,k,m", [(256, 2048, 512), (2048, 5632, 512), (32000, 2048, 16)])
 def test_prefill_gemm_q6k(ctx, n, k, m):
