@@ -447,6 +447,37 @@ def measure_read_family(ctx, nbytes, steps, warmup):
             "frac_hbm": best["frac_hbm"], "rotating_copies": copies, "family": members}
 
 
+def measure_mfma_rates(ctx):
+    """The rate the matrix cores sustain for the GEMMs' MFMA shapes in a
+    register-only loop (libaq_bench.so, k_mfma.hip): 1024 workgroups of four
+    wavefronts, four independent accumulator chains each, one launch of a few
+    ms timed with HIP events on the context's stream."""
+    import ctypes
+
+    from arm_ai_amd import hip
+
+    lib = ctypes.CDLL(os.path.join(ROOT, "arm_ai_amd", "libaq_bench.so"))
+    lib.aq_bench_mfma.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
+    lib.aq_bench_mfma_macs.restype = ctypes.c_longlong
+    grid, iters = 1024, 20000
+    out = hip.DeviceBuffer(grid * 256 * 4)
+    rows = {}
+    for kind, name, peak in ((0, "v_mfma_i32_32x32x32_i8", INT8_PEAK_TOPS), (1, "v_mfma_i32_16x16x64_i8", INT8_PEAK_TOPS),
+                             (2, "v_mfma_f32_32x32x16_f16", F16_PEAK_TFLOPS)):
+        assert lib.aq_bench_mfma(kind, ctx.stream, grid, iters, out.ptr) == 0  # warm-up
+        e0, e1 = hip.Event(), hip.Event()
+        e0.record(ctx.stream)
+        assert lib.aq_bench_mfma(kind, ctx.stream, grid, iters, out.ptr) == 0
+        e1.record(ctx.stream)
+        e1.synchronize()
+        ms = e0.elapsed_ms(e1)
+        ops = 2.0 * lib.aq_bench_mfma_macs(kind) * 4 * iters * grid * 4  # 4 wavefronts, 4 chains
+        tops = ops / (ms / 1e3) / 1e12
+        rows[name] = {"TOPS": round(tops, 1), "frac_of_published_peak": round(tops / peak, 4), "ms": round(ms, 3)}
+    out.close()
+    return rows
+
+
 def run_decode_child(name, no_cpu=False):
     """Run a decode (or vendor reference) case in a child process: the driver's
     torch glue needs torch imported before this library is loaded (one HIP
@@ -604,6 +635,8 @@ def main() -> int:
             extra[name] = run_decode_child(name, no_cpu=args.no_cpu)
         for name in VENDOR_CASES:
             extra[name] = run_decode_child(name, no_cpu=True)
+        extra["ref_mfma_rate"] = measure_mfma_rates(ctx)
+        log(f"matrix cores, register-only loop: {extra['ref_mfma_rate']}")
         result["extra"] = extra
     else:
         result["extra"] = {}
