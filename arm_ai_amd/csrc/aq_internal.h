@@ -147,19 +147,27 @@ hipError_t launch_expand_q80(int type, const uint8_t *src, int64_t n, int64_t k,
 hipError_t launch_matvec(const WLayout &w, int64_t n, int64_t k, const float *x, const ActPlanes *act, int64_t m,
                          float *y, int32_t *S, int32_t *Smin, hipStream_t s);
 // Batch-1 Q4_K / Q6_K matvec with one weight row per lane (k_rowlane.hip),
-// for weights of at least 3200 rows and k <= 16384; hipErrorNotSupported for
+// for weights of at least 256 rows and k <= 16384; hipErrorNotSupported for
 // other shapes.  x (f32, quantised in the kernel) or act (pre-quantised
-// planes of one row).  norm (x only, no dump, k <= 8192): quantise
-// rms_norm(x + delta) * w instead, workgroup 0 writing x + delta to xout.
-struct RlNorm {
+// planes of one row).  xf (x only, no dump): kind RL_XF_NORM quantises
+// rms_norm(x + delta) * w (k <= 8192; workgroup 0 writes x + delta to
+// xout), kind RL_XF_SILU takes x = [g | u] (2k floats) and quantises
+// silu(g) * u.
+constexpr int RL_XF_NONE = 0, RL_XF_NORM = 1, RL_XF_SILU = 2;
+struct RlXf {
+    int kind;  // RL_XF_NORM or RL_XF_SILU
     const float *delta, *w;
     float eps;
     float *xout;
 };
 bool rowlane_matvec_applies(int type, int64_t n, int64_t k);
-bool rowlane_norm_applies(int type, int64_t n, int64_t k);
+bool rowlane_xf_applies(int type, int64_t n, int64_t k, int kind);
 hipError_t launch_rowlane_matvec(const WLayout &w, int64_t n, int64_t k, const float *x, const ActPlanes *act,
-                                 float *y, int32_t *S, int32_t *Smin, hipStream_t s, const RlNorm *norm = nullptr);
+                                 float *y, int32_t *S, int32_t *Smin, hipStream_t s, const RlXf *xf = nullptr);
+// Two weights of the same k on one f32 input and transform in one launch
+// (both in the 16-row form); hipErrorNotSupported when either shape is not.
+hipError_t launch_rowlane_matvec2(const WLayout &w1, int64_t n1, float *y1, const WLayout &w2, int64_t n2, float *y2,
+                                  int64_t k, const float *x, const RlXf &xf, hipStream_t s);
 // Matvec of pre-quantised (Q8_K) rows on the int8 matrix cores, 8 rows per
 // launch, Q4_K / Q6_K weights, k <= mmv_max_k().  Returns hipErrorNotSupported
 // for other types and shapes (the caller then uses launch_matvec).

@@ -915,9 +915,9 @@ hipError_t matvec_impl(const WLayout &w, int64_t n, int64_t k, const float *x, c
         const hipError_t e = launch_rowlane_matvec(w, n, k, x, act, y, S, Smin, s);
         if (e != hipErrorNotSupported) return e;
     }
-    if (xa.xf == XF_NORM && rowlane_norm_applies(type, n, k)) {
-        const RlNorm nm{xa.delta, xa.norm, xa.eps, xa.xout};
-        const hipError_t e = launch_rowlane_matvec(w, n, k, x, nullptr, y, nullptr, nullptr, s, &nm);
+    if (m == 1 && xa.xf != XF_NONE && rowlane_xf_applies(type, n, k, xa.xf == XF_NORM ? RL_XF_NORM : RL_XF_SILU)) {
+        const RlXf rx{xa.xf == XF_NORM ? RL_XF_NORM : RL_XF_SILU, xa.delta, xa.norm, xa.eps, xa.xout};
+        const hipError_t e = launch_rowlane_matvec(w, n, k, x, nullptr, y, nullptr, nullptr, s, &rx);
         if (e != hipErrorNotSupported) return e;
     }
     const int ng = w.ng;
@@ -1069,6 +1069,22 @@ hipError_t launch_matvec2_rmsnorm(const WLayout &w1, int64_t n1, float *y1, cons
                                   float *xout, hipStream_t s) {
     if ((delta && ((uintptr_t)delta & 15)) || !norm || ((uintptr_t)norm & 15) || (xout && ((uintptr_t)xout & 15)))
         return hipErrorInvalidValue;
+    // The two weights' outputs equal their single calls' bytes: both
+    // row-per-lane in one launch where the shapes allow, one launch each when
+    // only one of them takes that kernel, the general kernel for both otherwise.
+    auto kq = [](int t) { return t == TYPE_Q4_K || t == TYPE_Q6_K; };
+    if (!kq(w1.type) || !kq(w2.type) || k % QK_K || k / QK_K > PRE * NW) return hipErrorNotSupported;
+    const bool r1 = rowlane_xf_applies(w1.type, n1, k, RL_XF_NORM), r2 = rowlane_xf_applies(w2.type, n2, k, RL_XF_NORM);
+    if (r1 && r2) {
+        const RlXf rx{RL_XF_NORM, delta, norm, eps, xout};
+        const hipError_t e = launch_rowlane_matvec2(w1, n1, y1, w2, n2, y2, k, x, rx, s);
+        if (e != hipErrorNotSupported) return e;
+    }
+    if (r1 || r2) {
+        const hipError_t e = launch_matvec_rmsnorm(w1, n1, k, x, delta, norm, eps, xout, y1, s);
+        if (e != hipSuccess) return e;
+        return launch_matvec_rmsnorm(w2, n2, k, x, delta, norm, eps, nullptr, y2, s);
+    }
     XfArgs xa;
     xa.xf = XF_NORM;
     xa.delta = delta;

@@ -46,7 +46,7 @@ constexpr int RL_ROWS = 56;    // weight rows per workgroup (one row per lane)
 constexpr int RL_MAXG = 64;    // groups per row (k <= 16384)
 constexpr int RL_MIN_N = 200 * RL_ROWS;  // rows from which 56-row workgroups are used (up to 32 groups)
 constexpr int RG_ROWS = 16;    // weight rows per workgroup of the four-group-phase form
-constexpr int RG_MIN_N = 200 * RG_ROWS;  // rows from which that form is used (up to 64 groups)
+constexpr int RG_MIN_N = 16 * RG_ROWS;   // rows from which that form is used (up to 64 groups)
 constexpr int RL_PERSIST_CUS = 256;      // the persistent grid: one workgroup per CU
 constexpr int RL_NORM_MAXG = 32;         // the fused norm: rows of up to 8192 elements (as the general matvec)
 
@@ -61,6 +61,7 @@ struct RlParams {
     const float *xdelta, *xnorm;
     float *xout;
     float eps;
+    int xf;            // RL_XF_NONE / _NORM / _SILU (see rl_body)
     ActPlanes act;     // pre-quantised planes (x null)
     float *y;
     int32_t *S, *Smin;  // [n][ng] integer dump, or null
@@ -83,9 +84,18 @@ struct RlParams {
 // blockIdx.x, blockIdx.x + gridDim.x, ...; every piece of the next chunk is
 // issued right after the same piece of the current one is consumed (P =
 // pieces per group), so the stream does not drain between chunks.
-template <int TYPE, int R, int W, int GPW, int P, bool EARLY, bool FUSED, bool DUMP, bool CH = false, bool NORM = false>
-__global__ __launch_bounds__(W * 64) void rl_kernel(RlParams p) {
-    static_assert(!NORM || (FUSED && !DUMP), "the fused norm takes an f32 input and no integer dump");
+//
+// Input transforms of an f32 x (XF): RL_XF_NORM quantises
+// rms_norm(x + delta) * w (workgroup 0 writing x + delta to xout), RL_XF_SILU
+// takes x = [g (k) | u (k)] and quantises silu(g) * u, candle's
+// x / (1 + e^-x) * u.
+//
+// The body takes its workgroup index bid of nblk, so that one launch can run
+// two weights' matvecs on the same input (rl2_kernel).
+template <int TYPE, int R, int W, int GPW, int P, bool EARLY, bool FUSED, bool DUMP, bool CH, int XF>
+__device__ __forceinline__ void rl_body(const RlParams p, const int bid, const int nblk) {
+    constexpr bool NORM = XF == RL_XF_NORM, SILU = XF == RL_XF_SILU;
+    static_assert(XF == RL_XF_NONE || (FUSED && !DUMP), "input transforms take an f32 input and no integer dump");
     static_assert(R == RL_ROWS || R == RG_ROWS, "56 rows, one per lane, or 16 rows in four group phases");
     static_assert(TYPE == TYPE_Q4_K || TYPE == TYPE_Q6_K, "Q4_K or Q6_K");
     static_assert(!CH || (R == RL_ROWS && GPW == 1 && P == (TYPE == TYPE_Q6_K ? 13 : 9)),
@@ -123,7 +133,7 @@ __global__ __launch_bounds__(W * 64) void rl_kernel(RlParams p) {
         c.dbase = c.rok ? (uint32_t)(((rl / RB) * p.ng * RB + (rl % RB)) * 2) : BUF_OOB;
         return c;
     };
-    Chunk cur = chunk_at((int)blockIdx.x);
+    Chunk cur = chunk_at(bid);
     auto group_of = [&](int j) { return wave * GP + gp + W * GP * (j / NPG); };
     // the piece a lane reads at its j-th step within a group
     // (Q6_K: 12, 8, 9, 0-3, 10, 11, 4-7 in the 56-row form, which holds two
@@ -176,6 +186,10 @@ __global__ __launch_bounds__(W * 64) void rl_kernel(RlParams p) {
                     dv[i] = __builtin_amdgcn_raw_buffer_load_b128(rdl, xo + 16 * i, 0, 0);
                     nv[i] = __builtin_amdgcn_raw_buffer_load_b128(rnw, xo + 16 * i, 0, 0);
                 }
+            } else if (SILU) {  // u = the second half of x
+                const rsrc_t ru = buf_rsrc(p.x + p.k, (uint32_t)(p.k * 4));
+#pragma unroll
+                for (int i = 0; i < 4; i++) dv[i] = __builtin_amdgcn_raw_buffer_load_b128(ru, xo + 16 * i, 0, 0);
             }
         } else {
             const rsrc_t rq = buf_rsrc(p.act.qs, (uint32_t)p.k);
@@ -204,6 +218,14 @@ __global__ __launch_bounds__(W * 64) void rl_kernel(RlParams p) {
             v[4 * i + 3] = u32_as_f32(xv[i].w);
         }
     }
+    if (SILU && quantiser) {
+        const float uv[16] = {u32_as_f32(dv[0].x), u32_as_f32(dv[0].y), u32_as_f32(dv[0].z), u32_as_f32(dv[0].w),
+                              u32_as_f32(dv[1].x), u32_as_f32(dv[1].y), u32_as_f32(dv[1].z), u32_as_f32(dv[1].w),
+                              u32_as_f32(dv[2].x), u32_as_f32(dv[2].y), u32_as_f32(dv[2].z), u32_as_f32(dv[2].w),
+                              u32_as_f32(dv[3].x), u32_as_f32(dv[3].y), u32_as_f32(dv[3].z), u32_as_f32(dv[3].w)};
+#pragma unroll
+        for (int i = 0; i < 16; i++) v[i] = (v[i] / (1.0f + expf(-v[i]))) * uv[i];
+    }
     if (NORM) {
         float ss = 0.0f;
         if (quantiser) {
@@ -226,7 +248,7 @@ __global__ __launch_bounds__(W * 64) void rl_kernel(RlParams p) {
             float tot = 0.0f;
             for (int w2 = 0; w2 < nq; w2++) tot += nred[w2];
             const float mden = sqrtf(tot / (float)p.k + p.eps);
-            if (p.xout && blockIdx.x == 0 && gbok) {  // the residual stream x + delta
+            if (p.xout && bid == 0 && gbok) {  // the residual stream x + delta
 #pragma unroll
                 for (int i = 0; i < 4; i++)
                     *(float4 *)(p.xout + gb * QK_K + 16 * s + 4 * i) = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
@@ -269,8 +291,8 @@ __global__ __launch_bounds__(W * 64) void rl_kernel(RlParams p) {
     //    1 + 2c + h = qs bytes 32c + 16h .. +15 (low nibbles: elements
     //    64c + 16h + i of sub-block 2c; high: 64c + 32 + 16h + i of 2c + 1)
     const int nch = (p.n + R - 1) / R;
-    for (int chunk = (int)blockIdx.x, it = 0;; it++) {  // one chunk unless CH
-    const int nextc = chunk + (int)gridDim.x;
+    for (int chunk = bid, it = 0;; it++) {  // one chunk unless CH
+    const int nextc = chunk + nblk;
     const bool more = CH && nextc < nch;  // uniform
     Chunk nxt = cur;
     if (more) nxt = chunk_at(nextc);
@@ -408,10 +430,30 @@ __global__ __launch_bounds__(W * 64) void rl_kernel(RlParams p) {
     }
 }
 
+template <int TYPE, int R, int W, int GPW, int P, bool EARLY, bool FUSED, bool DUMP, bool CH = false, int XF = RL_XF_NONE>
+__global__ __launch_bounds__(W * 64) void rl_kernel(RlParams p) {
+    rl_body<TYPE, R, W, GPW, P, EARLY, FUSED, DUMP, CH, XF>(p, (int)blockIdx.x, (int)gridDim.x);
+}
+
+// Two weights on the same f32 input in one launch (the decode step's wq|wk
+// and wv): workgroups [0, g1) take the first, the rest the second; both in
+// the 16-row form with W wavefronts (their LDS is separate).
+template <int T1, int T2, int W, int XF>
+__global__ __launch_bounds__(W * 64) void rl2_kernel(RlParams p1, RlParams p2, int g1) {
+    constexpr int P1 = T1 == TYPE_Q6_K ? 13 : 9, P2 = T2 == TYPE_Q6_K ? 13 : 9;
+    const int bid = (int)blockIdx.x;
+    if (bid < g1) rl_body<T1, RG_ROWS, W, 1, P1, true, true, false, false, XF>(p1, bid, g1);  // uniform
+    else rl_body<T2, RG_ROWS, W, 1, P2, true, true, false, false, XF>(p2, bid - g1, (int)gridDim.x - g1);
+}
+
 template <int TYPE, int R, int W, int GPW, int P, bool EARLY, bool CH = false>
 hipError_t launch_g(const RlParams &p, unsigned grid, bool fused, bool dump, hipStream_t s) {
-    if (p.xnorm) {  // the fused norm (f32 input, no dump: the caller checks)
-        rl_kernel<TYPE, R, W, GPW, P, EARLY, true, false, CH, true><<<grid, W * 64, 0, s>>>(p);
+    if (p.xf == RL_XF_NORM) {  // input transforms: f32 input, no dump (the caller checks)
+        rl_kernel<TYPE, R, W, GPW, P, EARLY, true, false, CH, RL_XF_NORM><<<grid, W * 64, 0, s>>>(p);
+        return hipGetLastError();
+    }
+    if (p.xf == RL_XF_SILU) {
+        rl_kernel<TYPE, R, W, GPW, P, EARLY, true, false, CH, RL_XF_SILU><<<grid, W * 64, 0, s>>>(p);
         return hipGetLastError();
     }
     if (fused) {
@@ -463,15 +505,19 @@ bool rowlane_matvec_applies(int type, int64_t n, int64_t k) {
            (rows56(type, n, (int)(k / QK_K)) || n >= RG_MIN_N);
 }
 
-bool rowlane_norm_applies(int type, int64_t n, int64_t k) {
-    return rowlane_matvec_applies(type, n, k) && k / QK_K <= RL_NORM_MAXG;
+bool rowlane_xf_applies(int type, int64_t n, int64_t k, int kind) {
+    return rowlane_matvec_applies(type, n, k) && (kind != RL_XF_NORM || k / QK_K <= RL_NORM_MAXG);
 }
 
-hipError_t launch_rowlane_matvec(const WLayout &w, int64_t n, int64_t k, const float *x, const ActPlanes *act,
-                                 float *y, int32_t *S, int32_t *Smin, hipStream_t s, const RlNorm *norm) {
+namespace {
+// RlParams of one weight (checks shared by both entry points)
+hipError_t rl_params(const WLayout &w, int64_t n, int64_t k, const float *x, const ActPlanes *act, float *y,
+                     int32_t *S, int32_t *Smin, const RlXf *xf, RlParams &p) {
     if (!rowlane_matvec_applies(w.type, n, k)) return hipErrorNotSupported;
     if (!w.slab || !y || (!x && !act) || (S == nullptr) != (Smin == nullptr)) return hipErrorInvalidValue;
-    if (norm && (!x || S || !norm->w || k / QK_K > RL_NORM_MAXG)) return hipErrorInvalidValue;
+    if (xf && (!x || S || (xf->kind != RL_XF_NORM && xf->kind != RL_XF_SILU) || (xf->kind == RL_XF_NORM && !xf->w)))
+        return hipErrorInvalidValue;
+    if (xf && !rowlane_xf_applies(w.type, n, k, xf->kind)) return hipErrorNotSupported;
     const int ng = (int)(k / QK_K);
     const int npg = w.type == TYPE_Q6_K ? 13 : 9;
     if (w.ng != ng || w.rb_stride != (int64_t)ng * npg * 128) return hipErrorInvalidValue;
@@ -479,7 +525,6 @@ hipError_t launch_rowlane_matvec(const WLayout &w, int64_t n, int64_t k, const f
     if (x && ((uintptr_t)x & 15)) return hipErrorInvalidValue;
     const bool wide = rows56(w.type, n, ng);
     if ((int64_t)(wide ? RL_ROWS : RG_ROWS) / RB * w.rb_stride >= ((int64_t)1 << 31)) return hipErrorNotSupported;
-    RlParams p;
     p.w = w.slab;
     p.wd = w.d;
     p.rb_stride = w.rb_stride;
@@ -487,17 +532,59 @@ hipError_t launch_rowlane_matvec(const WLayout &w, int64_t n, int64_t k, const f
     p.k = (int)k;
     p.ng = ng;
     p.x = x;
-    p.xdelta = norm ? norm->delta : nullptr;
-    p.xnorm = norm ? norm->w : nullptr;
-    p.xout = norm ? norm->xout : nullptr;
-    p.eps = norm ? norm->eps : 0.0f;
+    p.xf = xf ? xf->kind : RL_XF_NONE;
+    p.xdelta = xf ? xf->delta : nullptr;
+    p.xnorm = xf ? xf->w : nullptr;
+    p.xout = xf ? xf->xout : nullptr;
+    p.eps = xf ? xf->eps : 0.0f;
     p.act = act ? *act : ActPlanes{};
     p.y = y;
     p.S = S;
     p.Smin = Smin;
-    const bool fused = x != nullptr, dump = S != nullptr;
-    if (w.type == TYPE_Q6_K) return launch_type<TYPE_Q6_K>(p, n, ng, wide, fused, dump, s);
-    return launch_type<TYPE_Q4_K>(p, n, ng, wide, fused, dump, s);
+    return hipSuccess;
+}
+
+template <int T1, int T2, int W>
+hipError_t launch_two_rl(const RlParams &p1, const RlParams &p2, int g1, int g2, int kind, hipStream_t s) {
+    if (kind == RL_XF_NORM) rl2_kernel<T1, T2, W, RL_XF_NORM><<<g1 + g2, W * 64, 0, s>>>(p1, p2, g1);
+    else if (kind == RL_XF_SILU) rl2_kernel<T1, T2, W, RL_XF_SILU><<<g1 + g2, W * 64, 0, s>>>(p1, p2, g1);
+    else rl2_kernel<T1, T2, W, RL_XF_NONE><<<g1 + g2, W * 64, 0, s>>>(p1, p2, g1);
+    return hipGetLastError();
+}
+
+template <int W>
+hipError_t launch_two_w(const RlParams &p1, const RlParams &p2, int t1, int t2, int g1, int g2, int kind, hipStream_t s) {
+    if (t1 == TYPE_Q4_K && t2 == TYPE_Q6_K) return launch_two_rl<TYPE_Q4_K, TYPE_Q6_K, W>(p1, p2, g1, g2, kind, s);
+    if (t1 == TYPE_Q4_K && t2 == TYPE_Q4_K) return launch_two_rl<TYPE_Q4_K, TYPE_Q4_K, W>(p1, p2, g1, g2, kind, s);
+    if (t1 == TYPE_Q6_K && t2 == TYPE_Q4_K) return launch_two_rl<TYPE_Q6_K, TYPE_Q4_K, W>(p1, p2, g1, g2, kind, s);
+    return launch_two_rl<TYPE_Q6_K, TYPE_Q6_K, W>(p1, p2, g1, g2, kind, s);
+}
+}  // namespace
+
+hipError_t launch_rowlane_matvec(const WLayout &w, int64_t n, int64_t k, const float *x, const ActPlanes *act,
+                                 float *y, int32_t *S, int32_t *Smin, hipStream_t s, const RlXf *xf) {
+    RlParams p;
+    const hipError_t e = rl_params(w, n, k, x, act, y, S, Smin, xf, p);
+    if (e != hipSuccess) return e;
+    const bool wide = rows56(w.type, n, p.ng), fused = x != nullptr, dump = S != nullptr;
+    if (w.type == TYPE_Q6_K) return launch_type<TYPE_Q6_K>(p, n, p.ng, wide, fused, dump, s);
+    return launch_type<TYPE_Q4_K>(p, n, p.ng, wide, fused, dump, s);
+}
+
+hipError_t launch_rowlane_matvec2(const WLayout &w1, int64_t n1, float *y1, const WLayout &w2, int64_t n2, float *y2,
+                                  int64_t k, const float *x, const RlXf &xf, hipStream_t s) {
+    RlParams p1, p2;
+    hipError_t e = rl_params(w1, n1, k, x, nullptr, y1, nullptr, nullptr, &xf, p1);
+    if (e != hipSuccess) return e;
+    RlXf xf2 = xf;
+    xf2.xout = nullptr;  // the residual is written once, by the first weight's workgroup 0
+    if ((e = rl_params(w2, n2, k, x, nullptr, y2, nullptr, nullptr, &xf2, p2)) != hipSuccess) return e;
+    const int ng = p1.ng;
+    if (rows56(w1.type, n1, ng) || rows56(w2.type, n2, ng)) return hipErrorNotSupported;  // 16-row forms only
+    if (ng > 32) return hipErrorNotSupported;  // four or eight wavefronts
+    const int g1 = (int)((n1 + RG_ROWS - 1) / RG_ROWS), g2 = (int)((n2 + RG_ROWS - 1) / RG_ROWS);
+    return ng <= 16 ? launch_two_w<4>(p1, p2, w1.type, w2.type, g1, g2, xf.kind, s)
+                    : launch_two_w<8>(p1, p2, w1.type, w2.type, g1, g2, xf.kind, s);
 }
 
 }  // namespace aq

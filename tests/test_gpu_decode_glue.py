@@ -260,7 +260,11 @@ def test_matvec_fused_rmsnorm(env, wtype, n, k, with_delta):
     mm.free()
 
 
-@pytest.mark.parametrize("wtype,n,k", [(12, 2048, 5632), (14, 2048, 5632), (12, 300, 256), (13, 2048, 5632)])
+@pytest.mark.parametrize("wtype,n,k", [(12, 2048, 5632), (14, 2048, 5632), (12, 300, 256), (13, 2048, 5632),
+                                        (12, 200, 1024),     # below 256 rows: the general matvec
+                                        (12, 14336, 4096),   # 56-row workgroups
+                                        (14, 4096, 14336),   # the 16-row form with 16 wavefronts
+                                        (12, 30000, 2048)])  # persistent chunks
 def test_matvec_fused_silu_mul(env, wtype, n, k):
     import oracle as O
 
@@ -305,9 +309,16 @@ def test_matvec_fused_errors(env):
     mm.free()
 
 
-@pytest.mark.parametrize("t1,n1,t2,n2,k", [(12, 2304, 14, 256, 2048), (12, 1000, 12, 300, 4096), (14, 512, 14, 96, 1024)])
+@pytest.mark.parametrize("t1,n1,t2,n2,k", [
+    (12, 2304, 14, 256, 2048),   # TinyLlama wq|wk + wv: both row-per-lane, one launch
+    (12, 1000, 12, 300, 4096),
+    (14, 5120, 14, 1024, 8192),  # eight wavefronts per workgroup
+    (14, 512, 14, 96, 1024),     # the second below 256 rows: one launch each
+    (12, 12000, 14, 256, 2048),  # the first in 56-row workgroups: one launch each
+    (12, 200, 14, 96, 1024),     # neither row-per-lane: the general two-weight kernel
+])
 def test_matvec2_fused_rmsnorm_equals_two_calls(env, t1, n1, t2, n2, k):
-    """One launch over two weights gives the bytes the two single calls give."""
+    """The two-weight call gives the bytes the two single calls give."""
     import arm_ai_amd as A
     from arm_ai_amd import synth as S
 

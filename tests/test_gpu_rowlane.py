@@ -1,9 +1,11 @@
-"""GPU parity of the batch-1 Q4_K matvec with one weight row per lane
-(csrc/k_rowlane.hip), the path a single activation row takes on a Q4_K
-weight of at least 11200 rows and k <= 8192 (Llama-3-8B ffn_up / ffn_gate),
-and of its 16-row form (lane = row + 16 * group phase), taken from 3200 rows
-up to k = 16384 (Llama-3-8B ffn_down 4096 x 14336, the attention
-projections 4096 x 4096).
+"""GPU parity of the batch-1 Q4_K / Q6_K matvec with one weight row per lane
+(csrc/k_rowlane.hip), the path a single activation row takes on a weight of
+at least 11200 rows and k <= 8192 (Llama-3-8B ffn_up / ffn_gate, the
+lm_heads, with persistent chunks beyond 256 of them), and of its 16-row
+form (lane = row + 16 * group phase), taken from 256 rows up to k = 16384
+(Llama-3-8B ffn_down 4096 x 14336, the attention projections, TinyLlama's
+wo, w2, wk, wv).  The fused transforms (RMSNorm, SiLU * up) and the
+two-weight launch are tested with the decode glue.
 
 Against the oracle (candle-core 0.8.4 k_quants::matmul restated): every
 integer block sum S and Smin bit-exact, outputs within max relative error
@@ -22,7 +24,7 @@ from tests.test_gpu_parity import _edge_rows, _xdeq_abs, check_matmul
 pytestmark = pytest.mark.gpu
 
 RL_MIN_N = 11200  # rows from which a one-row Q4_K matvec takes the row-per-lane kernel
-RG_MIN_N = 3200   # rows from which it takes the 16-row form (any k <= 16384)
+RG_MIN_N = 256    # rows from which it takes the 16-row form (any k <= 16384)
 
 
 @pytest.mark.parametrize("n,k", [
@@ -74,7 +76,7 @@ def test_rowlane_q6k_matches_oracle(ctx, n, k):
 
 
 @pytest.mark.parametrize("typ,n,k", [
-    (S.TYPE_Q4_K, 32000, 4096),    # 572 chunks over 512 persistent workgroups: some walk two
+    (S.TYPE_Q4_K, 32000, 4096),    # 572 chunks over 256 persistent workgroups: some walk three
     (S.TYPE_Q4_K, 60001, 1024),    # 1072 chunks, ragged rows, four groups (12 idle wavefronts)
     (S.TYPE_Q6_K, 128256, 4096),   # Llama-3-8B lm_head: 2291 chunks, about 4.5 per workgroup
     (S.TYPE_Q6_K, 70003, 768),     # three groups, ragged rows
@@ -217,8 +219,8 @@ def test_rowlane_and_general_matvec_agree(ctx):
 
 
 def test_rowlane16_and_general_matvec_agree(ctx):
-    """The 16-row form (n >= 3200) against the general matvec on the first
-    3192 rows of the same weight: integer sums identical, outputs within the
+    """The 16-row form (n >= 256) against the general matvec on the first
+    248 rows of the same weight: integer sums identical, outputs within the
     tolerance."""
     k = 14336
     W = S.make_weight(S.TYPE_Q4_K, RG_MIN_N, k, seed=33)
