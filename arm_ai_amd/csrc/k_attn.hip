@@ -253,9 +253,12 @@ __global__ __launch_bounds__(SPL_THREADS) void attn_split_kernel(
 }
 
 // One wavefront per query head h (kv head h / REP, record slot h % REP).
-// Every lane loads the m, l of slice `lane` and its own output dims of the
-// first CS slices in one round trip; M = max m_s, weights e^(m_s - M) through
-// LDS; then each lane sums its hd / 64 dims over the slices.
+// Every lane loads its own output dims of the first CS slices and the m, l
+// of slices lane, lane + 64, ... in one round trip, issued together with the
+// position load: records sit at fixed places, so the loads do not wait for
+// pos, and the records past the context (left by earlier calls) are masked
+// out once pos gives the slice count ns.  M = max m_s, weights e^(m_s - M)
+// through LDS; then each lane sums its hd / 64 dims over the slices.
 template <int HD4, int REP>
 __global__ __launch_bounds__(64) void attn_combine_kernel(const float *__restrict__ part, const int64_t *__restrict__ d_pos,
                                                          int max_seq, int S, float *__restrict__ out) {
@@ -263,26 +266,39 @@ __global__ __launch_bounds__(64) void attn_combine_kernel(const float *__restric
     constexpr int DL = hd / 64;  // output dims per lane
     constexpr int PSTR = REP * hd + 2 * SPL_MAX_REP;
     constexpr int CS = 64 / DL;  // slices whose outputs are loaded up front
+    constexpr int MU = SPL_MAX_SLICES / 64;  // m, l values per lane at most
     __shared__ float w[SPL_MAX_SLICES];
     const int h = blockIdx.x, kvh = h / REP, hh = h % REP, lane = threadIdx.x;
+    const float *pk = part + (int64_t)kvh * S * PSTR;
+    float ov[CS][DL], mv[MU], lv[MU];
+#pragma unroll
+    for (int s2 = 0; s2 < CS; s2++)
+#pragma unroll
+        for (int e = 0; e < DL; e++) ov[s2][e] = s2 < S ? pk[(int64_t)s2 * PSTR + hh * hd + lane + 64 * e] : 0.0f;
+#pragma unroll
+    for (int u = 0; u < MU; u++) {
+        const int s2 = lane + 64 * u;
+        mv[u] = s2 < S ? pk[(int64_t)s2 * PSTR + REP * hd + hh] : 0.0f;
+        lv[u] = s2 < S ? pk[(int64_t)s2 * PSTR + REP * hd + SPL_MAX_REP + hh] : 0.0f;
+    }
     const int pos = (int)*d_pos;
     if (pos < 0 || pos >= max_seq) return;
     int len, ns;
     split_shape(pos + 1, S, len, ns);
-    const float *pk = part + (int64_t)kvh * S * PSTR;
-    float ov[CS][DL];
-#pragma unroll
-    for (int s2 = 0; s2 < CS; s2++)
-#pragma unroll
-        for (int e = 0; e < DL; e++) ov[s2][e] = s2 < ns ? pk[(int64_t)s2 * PSTR + hh * hd + lane + 64 * e] : 0.0f;
     float M = -INFINITY;
-    for (int s2 = lane; s2 < ns; s2 += 64) M = fmaxf(M, pk[(int64_t)s2 * PSTR + REP * hd + hh]);
+#pragma unroll
+    for (int u = 0; u < MU; u++)
+        if (lane + 64 * u < ns) M = fmaxf(M, mv[u]);
     M = wave_max_f(M);
     float L = 0.0f;
-    for (int s2 = lane; s2 < ns; s2 += 64) {
-        const float e = expf(pk[(int64_t)s2 * PSTR + REP * hd + hh] - M);
-        w[s2] = e;
-        L = __builtin_fmaf(e, pk[(int64_t)s2 * PSTR + REP * hd + SPL_MAX_REP + hh], L);
+#pragma unroll
+    for (int u = 0; u < MU; u++) {
+        const int s2 = lane + 64 * u;
+        if (s2 < ns) {
+            const float e = expf(mv[u] - M);
+            w[s2] = e;
+            L = __builtin_fmaf(e, lv[u], L);
+        }
     }
     L = wave_sum_f(L);
     __syncthreads();

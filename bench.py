@@ -478,6 +478,25 @@ def measure_mfma_rates(ctx):
     return rows
 
 
+def measure_launch_floor(ctx):
+    """The cost of one dependent kernel launch: a HIP graph of 200 launches of
+    an empty kernel (libaq_bench.so, k_launch.hip) timed with HIP events, at
+    one workgroup and at 256 (one per CU)."""
+    import ctypes
+
+    from arm_ai_amd import hip
+
+    lib = ctypes.CDLL(os.path.join(ROOT, "arm_ai_amd", "libaq_bench.so"))
+    lib.aq_bench_empty.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
+    out = hip.DeviceBuffer(4)
+    rows = {}
+    for grid in (1, 256):
+        ms, _ = time_graph(ctx, lambda i: lib.aq_bench_empty(ctx.stream, grid, out.ptr), 200, 5)
+        rows[f"grid_{grid}"] = {"us_per_launch": round(ms * 1e3, 3)}
+    out.close()
+    return rows
+
+
 def run_decode_child(name, no_cpu=False):
     """Run a decode (or vendor reference) case in a child process: the driver's
     torch glue needs torch imported before this library is loaded (one HIP
@@ -637,6 +656,8 @@ def main() -> int:
             extra[name] = run_decode_child(name, no_cpu=True)
         extra["ref_mfma_rate"] = measure_mfma_rates(ctx)
         log(f"matrix cores, register-only loop: {extra['ref_mfma_rate']}")
+        extra["ref_launch_floor"] = measure_launch_floor(ctx)
+        log(f"dependent launch of an empty kernel in a graph: {extra['ref_launch_floor']}")
         result["extra"] = extra
     else:
         result["extra"] = {}
