@@ -165,7 +165,8 @@ bool rowlane_xf_applies(int type, int64_t n, int64_t k, int kind);
 hipError_t launch_rowlane_matvec(const WLayout &w, int64_t n, int64_t k, const float *x, const ActPlanes *act,
                                  float *y, int32_t *S, int32_t *Smin, hipStream_t s, const RlXf *xf = nullptr);
 // Two weights of the same k on one f32 input and transform in one launch
-// (both in the 16-row form); hipErrorNotSupported when either shape is not.
+// (both in the 16-row or both in the 8-row form, the one a launch of their
+// own takes, so the sums are the same); hipErrorNotSupported otherwise.
 hipError_t launch_rowlane_matvec2(const WLayout &w1, int64_t n1, float *y1, const WLayout &w2, int64_t n2, float *y2,
                                   int64_t k, const float *x, const RlXf &xf, hipStream_t s);
 // Matvec of pre-quantised (Q8_K) rows on the int8 matrix cores, 8 rows per

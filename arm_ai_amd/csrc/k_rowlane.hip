@@ -47,6 +47,10 @@ constexpr int RL_MAXG = 64;    // groups per row (k <= 16384)
 constexpr int RL_MIN_N = 200 * RL_ROWS;  // rows from which 56-row workgroups are used (up to 32 groups)
 constexpr int RG_ROWS = 16;    // weight rows per workgroup of the four-group-phase form
 constexpr int RG_MIN_N = 16 * RG_ROWS;   // rows from which that form is used (up to 64 groups)
+constexpr int RE_ROWS = 8;     // weight rows per workgroup of the eight-group-phase form
+// ... used from 1025 to 2048 rows (up to 32 groups): at most one 8-row
+// workgroup per CU, where 16-row workgroups would leave half the CUs idle
+constexpr int RE_MIN_N = 64 * RG_ROWS + 1, RE_MAX_N = 256 * RE_ROWS;
 constexpr int RL_PERSIST_CUS = 256;      // the persistent grid: one workgroup per CU
 constexpr int RL_NORM_MAXG = 32;         // the fused norm: rows of up to 8192 elements (as the general matvec)
 
@@ -96,7 +100,8 @@ template <int TYPE, int R, int W, int GPW, int P, bool EARLY, bool FUSED, bool D
 __device__ __forceinline__ void rl_body(const RlParams p, const int bid, const int nblk) {
     constexpr bool NORM = XF == RL_XF_NORM, SILU = XF == RL_XF_SILU;
     static_assert(XF == RL_XF_NONE || (FUSED && !DUMP), "input transforms take an f32 input and no integer dump");
-    static_assert(R == RL_ROWS || R == RG_ROWS, "56 rows, one per lane, or 16 rows in four group phases");
+    static_assert(R == RL_ROWS || R == RG_ROWS || R == RE_ROWS,
+                  "56 rows, one per lane, or 16 / 8 rows in four / eight group phases");
     static_assert(TYPE == TYPE_Q4_K || TYPE == TYPE_Q6_K, "Q4_K or Q6_K");
     static_assert(!CH || (R == RL_ROWS && GPW == 1 && P == (TYPE == TYPE_Q6_K ? 13 : 9)),
                   "persistent chunks: one group per wavefront, all its pieces in flight");
@@ -414,7 +419,8 @@ __device__ __forceinline__ void rl_body(const RlParams p, const int bid, const i
     }
     // 4. the row's partials: over its group phases within the wavefront,
     //    then over the wavefronts, in wavefront order
-    if (GP == 4) f += __shfl_xor(f, 16);
+    if (GP == 8) f += __shfl_xor(f, 8);
+    if (GP >= 4) f += __shfl_xor(f, 16);
     if (GP >= 2) f += __shfl_xor(f, 32);
     red[CH ? it & 1 : 0][wave][lane] = f;
     lds_barrier();
@@ -437,13 +443,15 @@ __global__ __launch_bounds__(W * 64) void rl_kernel(RlParams p) {
 
 // Two weights on the same f32 input in one launch (the decode step's wq|wk
 // and wv): workgroups [0, g1) take the first, the rest the second; both in
-// the 16-row form with W wavefronts (their LDS is separate).
-template <int T1, int T2, int W, int XF>
+// the form of R (16 or 8) rows with W wavefronts (their LDS is separate).
+// A wavefront past the groups adds 0 to its rows, so W wavefronts give the
+// same sums as a single weight's launch with fewer.
+template <int T1, int T2, int R, int W, int XF>
 __global__ __launch_bounds__(W * 64) void rl2_kernel(RlParams p1, RlParams p2, int g1) {
     constexpr int P1 = T1 == TYPE_Q6_K ? 13 : 9, P2 = T2 == TYPE_Q6_K ? 13 : 9;
     const int bid = (int)blockIdx.x;
-    if (bid < g1) rl_body<T1, RG_ROWS, W, 1, P1, true, true, false, false, XF>(p1, bid, g1);  // uniform
-    else rl_body<T2, RG_ROWS, W, 1, P2, true, true, false, false, XF>(p2, bid - g1, (int)gridDim.x - g1);
+    if (bid < g1) rl_body<T1, R, W, 1, P1, true, true, false, false, XF>(p1, bid, g1);  // uniform
+    else rl_body<T2, R, W, 1, P2, true, true, false, false, XF>(p2, bid - g1, (int)gridDim.x - g1);
 }
 
 template <int TYPE, int R, int W, int GPW, int P, bool EARLY, bool CH = false>
@@ -469,6 +477,8 @@ hipError_t launch_g(const RlParams &p, unsigned grid, bool fused, bool dump, hip
 // 56-row workgroups: up to two Q4_K groups per wavefront (32 groups); one
 // Q6_K group (16; two kept 13-piece walks too many registers live)
 bool rows56(int type, int64_t n, int ng) { return ng <= (type == TYPE_Q6_K ? 16 : 32) && n >= RL_MIN_N; }
+// 8-row workgroups (otherwise 16 rows), for a shape that is not rows56
+bool rows8(int64_t n, int ng) { return ng <= 32 && n >= RE_MIN_N && n <= RE_MAX_N; }
 
 // The launch shapes of one weight type (pieces in flight: P; 16 wavefronts
 // with six Q4_K pieces in flight measured fastest at the headline, one group
@@ -492,6 +502,16 @@ hipError_t launch_type(const RlParams &p, int64_t n, int ng, bool wide, bool fus
     // start; with 16 wavefronts (Q4_K ffn_down, 56 groups) five, issued after
     // the quantisation, measured fastest (8.3 us against 8.6 for nine issued
     // late and 9.7 for nine issued early).
+    constexpr int NPG = Q6 ? 13 : 9;
+    if (rows8(n, ng)) {
+        // 8 rows: a wavefront covers eight groups, and there are as many
+        // wavefronts as the quantisation needs (four blocks each)
+        const unsigned g8 = (unsigned)((n + RE_ROWS - 1) / RE_ROWS);
+        if (ng <= 8) return launch_g<TYPE, RE_ROWS, 2, 1, NPG, true>(p, g8, fused, dump, s);
+        if (ng <= 16) return launch_g<TYPE, RE_ROWS, 4, 1, NPG, true>(p, g8, fused, dump, s);
+        if (ng <= 24) return launch_g<TYPE, RE_ROWS, 6, 1, NPG, true>(p, g8, fused, dump, s);
+        return launch_g<TYPE, RE_ROWS, 8, 1, NPG, true>(p, g8, fused, dump, s);
+    }
     const unsigned grid = (unsigned)((n + RG_ROWS - 1) / RG_ROWS);
     if (ng <= 16) return launch_g<TYPE, RG_ROWS, 4, 1, Q6 ? 13 : 9, true>(p, grid, fused, dump, s);
     if (ng <= 32) return launch_g<TYPE, RG_ROWS, 8, 1, Q6 ? 13 : 9, true>(p, grid, fused, dump, s);
@@ -544,20 +564,21 @@ hipError_t rl_params(const WLayout &w, int64_t n, int64_t k, const float *x, con
     return hipSuccess;
 }
 
-template <int T1, int T2, int W>
+template <int T1, int T2, int R, int W>
 hipError_t launch_two_rl(const RlParams &p1, const RlParams &p2, int g1, int g2, int kind, hipStream_t s) {
-    if (kind == RL_XF_NORM) rl2_kernel<T1, T2, W, RL_XF_NORM><<<g1 + g2, W * 64, 0, s>>>(p1, p2, g1);
-    else if (kind == RL_XF_SILU) rl2_kernel<T1, T2, W, RL_XF_SILU><<<g1 + g2, W * 64, 0, s>>>(p1, p2, g1);
-    else rl2_kernel<T1, T2, W, RL_XF_NONE><<<g1 + g2, W * 64, 0, s>>>(p1, p2, g1);
+    if (kind == RL_XF_NORM) rl2_kernel<T1, T2, R, W, RL_XF_NORM><<<g1 + g2, W * 64, 0, s>>>(p1, p2, g1);
+    else if (kind == RL_XF_SILU) rl2_kernel<T1, T2, R, W, RL_XF_SILU><<<g1 + g2, W * 64, 0, s>>>(p1, p2, g1);
+    else rl2_kernel<T1, T2, R, W, RL_XF_NONE><<<g1 + g2, W * 64, 0, s>>>(p1, p2, g1);
     return hipGetLastError();
 }
 
-template <int W>
-hipError_t launch_two_w(const RlParams &p1, const RlParams &p2, int t1, int t2, int g1, int g2, int kind, hipStream_t s) {
-    if (t1 == TYPE_Q4_K && t2 == TYPE_Q6_K) return launch_two_rl<TYPE_Q4_K, TYPE_Q6_K, W>(p1, p2, g1, g2, kind, s);
-    if (t1 == TYPE_Q4_K && t2 == TYPE_Q4_K) return launch_two_rl<TYPE_Q4_K, TYPE_Q4_K, W>(p1, p2, g1, g2, kind, s);
-    if (t1 == TYPE_Q6_K && t2 == TYPE_Q4_K) return launch_two_rl<TYPE_Q6_K, TYPE_Q4_K, W>(p1, p2, g1, g2, kind, s);
-    return launch_two_rl<TYPE_Q6_K, TYPE_Q6_K, W>(p1, p2, g1, g2, kind, s);
+template <int R, int W>
+hipError_t launch_two_w(const RlParams &p1, const RlParams &p2, int t1, int t2, int kind, hipStream_t s) {
+    const int g1 = (p1.n + R - 1) / R, g2 = (p2.n + R - 1) / R;
+    if (t1 == TYPE_Q4_K && t2 == TYPE_Q6_K) return launch_two_rl<TYPE_Q4_K, TYPE_Q6_K, R, W>(p1, p2, g1, g2, kind, s);
+    if (t1 == TYPE_Q4_K && t2 == TYPE_Q4_K) return launch_two_rl<TYPE_Q4_K, TYPE_Q4_K, R, W>(p1, p2, g1, g2, kind, s);
+    if (t1 == TYPE_Q6_K && t2 == TYPE_Q4_K) return launch_two_rl<TYPE_Q6_K, TYPE_Q4_K, R, W>(p1, p2, g1, g2, kind, s);
+    return launch_two_rl<TYPE_Q6_K, TYPE_Q6_K, R, W>(p1, p2, g1, g2, kind, s);
 }
 }  // namespace
 
@@ -580,11 +601,16 @@ hipError_t launch_rowlane_matvec2(const WLayout &w1, int64_t n1, float *y1, cons
     xf2.xout = nullptr;  // the residual is written once, by the first weight's workgroup 0
     if ((e = rl_params(w2, n2, k, x, nullptr, y2, nullptr, nullptr, &xf2, p2)) != hipSuccess) return e;
     const int ng = p1.ng;
-    if (rows56(w1.type, n1, ng) || rows56(w2.type, n2, ng)) return hipErrorNotSupported;  // 16-row forms only
+    if (rows56(w1.type, n1, ng) || rows56(w2.type, n2, ng)) return hipErrorNotSupported;  // 16- and 8-row forms only
     if (ng > 32) return hipErrorNotSupported;  // four or eight wavefronts
-    const int g1 = (int)((n1 + RG_ROWS - 1) / RG_ROWS), g2 = (int)((n2 + RG_ROWS - 1) / RG_ROWS);
-    return ng <= 16 ? launch_two_w<4>(p1, p2, w1.type, w2.type, g1, g2, xf.kind, s)
-                    : launch_two_w<8>(p1, p2, w1.type, w2.type, g1, g2, xf.kind, s);
+    // both weights in the form a launch of their own takes, so that the sums
+    // are the same
+    const bool e1 = rows8(n1, ng), e2 = rows8(n2, ng);
+    if (e1 != e2) return hipErrorNotSupported;
+    if (e1) return ng <= 16 ? launch_two_w<RE_ROWS, 4>(p1, p2, w1.type, w2.type, xf.kind, s)
+                            : launch_two_w<RE_ROWS, 8>(p1, p2, w1.type, w2.type, xf.kind, s);
+    return ng <= 16 ? launch_two_w<RG_ROWS, 4>(p1, p2, w1.type, w2.type, xf.kind, s)
+                    : launch_two_w<RG_ROWS, 8>(p1, p2, w1.type, w2.type, xf.kind, s);
 }
 
 }  // namespace aq

@@ -315,6 +315,8 @@ def test_matvec_fused_errors(env):
     (14, 5120, 14, 1024, 8192),  # eight wavefronts per workgroup
     (14, 512, 14, 96, 1024),     # the second below 256 rows: one launch each
     (12, 12000, 14, 256, 2048),  # the first in 56-row workgroups: one launch each
+    (12, 2048, 14, 1536, 2048),  # both in 8-row workgroups: one launch
+    (12, 2048, 12, 512, 4096),   # 8-row and 16-row forms: one launch each
     (12, 200, 14, 96, 1024),     # neither row-per-lane: the general two-weight kernel
 ])
 def test_matvec2_fused_rmsnorm_equals_two_calls(env, t1, n1, t2, n2, k):

@@ -1,11 +1,13 @@
 """GPU parity of the batch-1 Q4_K / Q6_K matvec with one weight row per lane
 (csrc/k_rowlane.hip), the path a single activation row takes on a weight of
 at least 11200 rows and k <= 8192 (Llama-3-8B ffn_up / ffn_gate, the
-lm_heads, with persistent chunks beyond 256 of them), and of its 16-row
-form (lane = row + 16 * group phase), taken from 256 rows up to k = 16384
-(Llama-3-8B ffn_down 4096 x 14336, the attention projections, TinyLlama's
-wo, w2, wk, wv).  The fused transforms (RMSNorm, SiLU * up) and the
-two-weight launch are tested with the decode glue.
+lm_heads, with persistent chunks beyond 256 of them), of its 16-row form
+(lane = row + 16 * group phase), taken from 256 rows up to k = 16384
+(Llama-3-8B ffn_down 4096 x 14336, the attention projections), and of its
+8-row form (lane = row + 8 * group phase), taken from 1025 to 2048 rows up
+to k = 8192 (TinyLlama's wo and w2; its wk, wv and wq|wk take the 16-row
+form).  The fused transforms (RMSNorm,
+SiLU * up) and the two-weight launch are tested with the decode glue.
 
 Against the oracle (candle-core 0.8.4 k_quants::matmul restated): every
 integer block sum S and Smin bit-exact, outputs within max relative error
@@ -25,6 +27,7 @@ pytestmark = pytest.mark.gpu
 
 RL_MIN_N = 11200  # rows from which a one-row Q4_K matvec takes the row-per-lane kernel
 RG_MIN_N = 256    # rows from which it takes the 16-row form (any k <= 16384)
+RE_MIN_N, RE_MAX_N = 1025, 2048  # rows for which it takes the 8-row form instead (k <= 8192)
 
 
 @pytest.mark.parametrize("n,k", [
@@ -43,7 +46,8 @@ def test_rowlane_matches_oracle(ctx, n, k):
 @pytest.mark.parametrize("n,k", [
     (4096, 14336),   # Llama-3-8B ffn_down: 256 workgroups, 56 groups over 14 wavefronts of four phases
     (4096, 4096),    # the attention projections: 16 groups, four wavefronts
-    (RG_MIN_N, 8192),  # 32 groups, eight wavefronts
+    (RG_MIN_N, 8192),  # 32 groups, eight wavefronts (the fewest rows of this form)
+    (RE_MAX_N + 8, 2048),  # the first rows past the 8-row form
     (3203, 16384),   # 64 groups (the most), ragged rows: the last workgroup's second row block is partial
     (5000, 8448),    # 33 groups: the ninth wavefront's lanes straddle the last group
     (RL_MIN_N, 9216),  # many rows but 36 groups: the 16-row form
@@ -55,12 +59,30 @@ def test_rowlane16_matches_oracle(ctx, n, k):
 
 
 @pytest.mark.parametrize("n,k", [
+    (RE_MAX_N, 2048),  # TinyLlama wo: 256 workgroups of 8 rows, 8 groups over two wavefronts
+    (2048, 5632),      # TinyLlama w2: 22 groups over six wavefronts (three walk, all quantise)
+    (RE_MIN_N, 256),   # one group, ragged rows: the last workgroup has one
+    (2043, 2304),      # ragged rows (the last workgroup has three), 9 groups: four wavefronts
+    (1500, 4352),      # 17 groups: six wavefronts, ragged rows
+    (1999, 6400),      # 25 groups: eight wavefronts, ragged rows
+    (RE_MAX_N, 8192),  # 32 groups (the most for this form)
+])
+def test_rowlane8_matches_oracle(ctx, n, k):
+    W = S.make_weight(S.TYPE_Q4_K, n, k, seed=n + k + 5)
+    x = S.make_activation(1, k, seed=k + 5)
+    check_matmul(ctx, W, x)
+
+
+@pytest.mark.parametrize("n,k", [
     (32000, 2048),    # config 1's lm_head: 572 workgroups of 56 rows
     (RL_MIN_N, 256),  # one group
     (11203, 4096),    # ragged rows, 16 groups
     (12000, 8192),    # 32 groups: two per wavefront
     (4096, 14336),    # Llama-3-8B ffn_down in its Q6_K layers: the 16-row form, 56 groups
     (3203, 4096),     # 16-row form, ragged rows, four wavefronts
+    (2048, 5632),     # TinyLlama w2 in its Q6_K layers: 8-row form, 22 groups over six wavefronts
+    (1027, 4096),     # 8-row form, ragged rows (the last workgroup has three), 16 groups
+    (256, 2048),      # TinyLlama wv: 16 workgroups of 16 rows, 8 groups
     (5000, 8448),     # 33 groups, a wavefront's lanes straddling the last group
 ])
 def test_rowlane_q6k_matches_oracle(ctx, n, k):
