@@ -170,7 +170,8 @@ __device__ __forceinline__ void rl_body(const RlParams p, const int bid, const i
     //    wavefront's first P weight pieces, so that they are in flight while
     //    the activation is quantised (the loads are waited for in issue
     //    order).  With most wavefronts quantising (the 16-wavefront form),
-    //    issuing them after the quantisation measured faster.
+    //    issuing only the first piece before the quantisation and the rest
+    //    after it measured faster than either all before or all after.
     const int s = lane & 15;
     const int gb = 4 * wave + (lane >> 4);
     const bool quantiser = wave < (p.ng + 3) / 4;  // uniform
@@ -205,9 +206,9 @@ __device__ __forceinline__ void rl_body(const RlParams p, const int bid, const i
             xdb = __builtin_amdgcn_raw_buffer_load_b32(rd, gbok ? (uint32_t)(gb * 4) : BUF_OOB, 0, 0);
         }
     }
-    if (EARLY) {
+    {
 #pragma unroll
-        for (int j = 0; j < P && j < NP; j++) issue(j);
+        for (int j = 0; j < (EARLY ? P : 1) && j < NP; j++) issue(j);
     }
     // 2. quantise (or unpack) into LDS, then one barrier (LDS writes only).
     //    NORM: h = x + delta and the row's sum of squares first (every
@@ -288,7 +289,7 @@ __device__ __forceinline__ void rl_body(const RlParams p, const int bid, const i
     }
     if (!EARLY) {
 #pragma unroll
-        for (int j = 0; j < P && j < NP; j++) issue(j);
+        for (int j = 1; j < P && j < NP; j++) issue(j);
     }
     lds_barrier();
 
@@ -499,9 +500,9 @@ hipError_t launch_type(const RlParams &p, int64_t n, int ng, bool wide, bool fus
     // 16 rows: as many wavefronts as four groups each need (every lane one
     // group); the quantising wavefronts (four blocks each) are then always
     // enough.  Up to 32 groups all of a lane's pieces are in flight from the
-    // start; with 16 wavefronts (Q4_K ffn_down, 56 groups) five, issued after
-    // the quantisation, measured fastest (8.3 us against 8.6 for nine issued
-    // late and 9.7 for nine issued early).
+    // start; with 16 wavefronts (ffn_down, 56 groups) five (Q4_K) or seven
+    // (Q6_K), the first issued before the quantisation and the rest after
+    // it, measured fastest.
     constexpr int NPG = Q6 ? 13 : 9;
     if (rows8(n, ng)) {
         // 8 rows: a wavefront covers eight groups, and there are as many
