@@ -259,6 +259,19 @@ def test_k_coverage(ctx, wtype, k, m):
     check_matmul(ctx, W, x)
 
 
+@pytest.mark.parametrize("wtype,n,k", [
+    (S.TYPE_Q4_K, 4096, 14336),   # Llama-3-8B ffn_down at batch 8: four chunk wavefronts per tile
+    (S.TYPE_Q4_K, 32768, 8192),   # one chunk per tile, eight steps per wavefront (more than stay in flight)
+    (S.TYPE_Q6_K, 4096, 14336),
+])
+def test_batch8_long_rows(ctx, wtype, n, k):
+    """The matrix-core matvec at batch 8 on long rows: every step of a
+    wavefront's chunk, with later steps' weights in flight."""
+    W = S.make_weight(wtype, n, k, seed=n + k + 8)
+    x = S.make_activation(8, k, seed=k + 8)
+    check_matmul(ctx, W, x, cond=False)
+
+
 @pytest.mark.parametrize("k", [55296, 65536])
 @pytest.mark.parametrize("wtype", [S.TYPE_Q4_K, S.TYPE_Q8_0])
 @pytest.mark.parametrize("m", [1, 3])
