@@ -523,5 +523,23 @@ __device__ __forceinline__ uint32_t q8_0_block_8lanes(const float v[4], uint16_t
     return pack4_i8(q);
 }
 
+// The same block quantised by two adjacent lanes (2j, 2j + 1 of a 16-lane
+// set, 16 consecutive elements each; the row-per-lane matvec's prologue).
+// Returns the 16 packed quants; *d16 gets the f16 bits (the same on both
+// lanes).  All 64 lanes of the wave must be active.
+__device__ __forceinline__ uint4 q8_0_block_2lanes(const float v[16], uint16_t *d16) {
+    float am = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; i++) am = fmaxf(am, fabsf(v[i]));
+    am = fmaxf(am, dpp_f<DPP_QUAD_XOR1>(am));
+    const float d = am / 127.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    int q[16];
+#pragma unroll
+    for (int i = 0; i < 16; i++) q[i] = sat_i8(roundf(v[i] * id));
+    *d16 = f32_to_f16_rne(d);
+    return make_uint4(pack4_i8(q), pack4_i8(q + 4), pack4_i8(q + 8), pack4_i8(q + 12));
+}
+
 }  // namespace aq
 #endif

@@ -102,15 +102,17 @@ __device__ __forceinline__ void rl_body(const RlParams p, const int bid, const i
     static_assert(XF == RL_XF_NONE || (FUSED && !DUMP), "input transforms take an f32 input and no integer dump");
     static_assert(R == RL_ROWS || R == RG_ROWS || R == RE_ROWS,
                   "56 rows, one per lane, or 16 / 8 rows in four / eight group phases");
-    static_assert(TYPE == TYPE_Q4_K || TYPE == TYPE_Q6_K, "Q4_K or Q6_K");
+    static_assert(TYPE == TYPE_Q4_K || TYPE == TYPE_Q6_K || TYPE == TYPE_Q8_0, "Q4_K, Q6_K or Q8_0");
     static_assert(!CH || (R == RL_ROWS && GPW == 1 && P == (TYPE == TYPE_Q6_K ? 13 : 9)),
                   "persistent chunks: one group per wavefront, all its pieces in flight");
-    constexpr bool Q6 = TYPE == TYPE_Q6_K;
-    constexpr int NPG = Q6 ? 13 : 9;               // pieces per group
+    static_assert(TYPE != TYPE_Q8_0 || (R != RL_ROWS && GPW == 1), "Q8_0: the 16- and 8-row forms");
+    constexpr bool Q6 = TYPE == TYPE_Q6_K, Q80 = TYPE == TYPE_Q8_0;
+    constexpr int NPG = Q6 ? 13 : Q80 ? 17 : 9;    // pieces per group
     constexpr int GP = R == RL_ROWS ? 1 : 64 / R;  // group phases per wavefront
     __shared__ __align__(16) uint8_t xq[RL_MAXG][256];  // Q8_K quants of each group
     __shared__ __align__(16) int xb[RL_MAXG][Q6 ? 16 : 8];  // bsums per 16 (Q6_K) or 32 (Q4_K) elements
     __shared__ float xd[RL_MAXG];                       // Q8_K d
+    __shared__ float xd8[Q80 ? RL_MAXG : 1][8];         // Q8_0: the f16 d of each block, as f32
     __shared__ float red[CH ? 2 : 1][W][64];
     __shared__ float nred[W];  // NORM: the quantising wavefronts' sums of squares
     constexpr int NP = NPG * GPW;  // this wavefront's pieces, in order
@@ -146,6 +148,7 @@ __device__ __forceinline__ void rl_body(const RlParams p, const int bid, const i
     //  order measured fewer registers)
     constexpr bool HALVES = R == RL_ROWS;
     auto piece_of = [&](int pc) {
+        if (Q80) return pc == 0 ? 16 : pc - 1;  // the eight d first, then the quants in order
         if (!Q6) return pc;
         if (!HALVES) return pc == 0 ? 12 : pc < 5 ? 7 + pc : pc - 5;
         return pc == 0 ? 12 : pc < 3 ? 7 + pc : pc < 7 ? pc - 3 : pc < 9 ? 3 + pc : pc - 5;
@@ -200,10 +203,13 @@ __device__ __forceinline__ void rl_body(const RlParams p, const int bid, const i
         } else {
             const rsrc_t rq = buf_rsrc(p.act.qs, (uint32_t)p.k);
             const rsrc_t rs = buf_rsrc(p.act.bsums, (uint32_t)((p.k / 16) * 2));
-            const rsrc_t rd = buf_rsrc(p.act.d, (uint32_t)((p.k / QK_K) * 4));
+            const rsrc_t rd = buf_rsrc(p.act.d, (uint32_t)((p.k / (Q80 ? QK8_0 : QK_K)) * 4));
             xv[0] = __builtin_amdgcn_raw_buffer_load_b128(rq, gbok ? (uint32_t)(gb * QK_K + 16 * s) : BUF_OOB, 0, 0);
-            xbs = __builtin_amdgcn_raw_buffer_load_b16(rs, gbok ? (uint32_t)((gb * 16 + s) * 2) : BUF_OOB, 0, 0);
-            xdb = __builtin_amdgcn_raw_buffer_load_b32(rd, gbok ? (uint32_t)(gb * 4) : BUF_OOB, 0, 0);
+            if (!Q80)
+                xbs = __builtin_amdgcn_raw_buffer_load_b16(rs, gbok ? (uint32_t)((gb * 16 + s) * 2) : BUF_OOB, 0, 0);
+            // Q8_0: d of block 8 gb + s / 2 (the two lanes of a block read the same)
+            const uint32_t dof = Q80 ? (uint32_t)((gb * 8 + (s >> 1)) * 4) : (uint32_t)(gb * 4);
+            xdb = __builtin_amdgcn_raw_buffer_load_b32(rd, gbok ? dof : BUF_OOB, 0, 0);
         }
     }
     {
@@ -272,7 +278,12 @@ __device__ __forceinline__ void rl_body(const RlParams p, const int bid, const i
         uint4 qv;
         int bsum;
         float d;
-        if (FUSED) {
+        if (FUSED && Q80) {
+            uint16_t d16;
+            qv = q8_0_block_2lanes(v, &d16);
+            d = f16_bits_to_f32(d16);
+            bsum = 0;
+        } else if (FUSED) {
             qv = q8k_block_row16(v, s, &bsum, &d);
         } else {
             qv = make_uint4(xv[0].x, xv[0].y, xv[0].z, xv[0].w);
@@ -282,9 +293,13 @@ __device__ __forceinline__ void rl_body(const RlParams p, const int bid, const i
         const int pair = bsum + dpp_i<DPP_QUAD_XOR1>(bsum);  // sub-block s/2 (two 16-element halves)
         if (gbok) {
             *(uint4 *)&xq[gb][16 * s] = qv;
-            if (Q6) xb[gb][s] = bsum;
-            else if ((s & 1) == 0) xb[gb][s >> 1] = pair;
-            if (s == 0) xd[gb] = d;
+            if (Q80) {
+                if ((s & 1) == 0) xd8[gb][s >> 1] = d;
+            } else {
+                if (Q6) xb[gb][s] = bsum;
+                else if ((s & 1) == 0) xb[gb][s >> 1] = pair;
+                if (s == 0) xd[gb] = d;
+            }
         }
     }
     if (!EARLY) {
@@ -323,7 +338,31 @@ __device__ __forceinline__ void rl_body(const RlParams p, const int bid, const i
             const bool gok = g < p.ng;         // (lanes of several phases: per lane)
             const int gl = gok ? g : 0;        // a group whose LDS entries are written
             const uint4 q = ring[j % P];
-            if (Q6) {
+            if (Q80) {
+                // piece 0: the eight blocks' f16 d (kept in sc6); piece 1 + i:
+                // quants 16i .. 16i + 15, the half i & 1 of block i / 2, whose
+                // dot closes as candle's ((isum * d_w) * d_x)
+                if (pc == 0) {
+                    sc6 = q;
+                } else {
+                    const int i = pc - 1, jb = i >> 1;
+                    const int4 xv4 = *(const int4 *)&xq[gl][16 * i];
+                    if ((i & 1) == 0) il = 0;
+                    il = sdot4((int)q.x, xv4.x, il);
+                    il = sdot4((int)q.y, xv4.y, il);
+                    il = sdot4((int)q.z, xv4.z, il);
+                    il = sdot4((int)q.w, xv4.w, il);
+                    if (i & 1) {
+                        const uint32_t dws[4] = {sc6.x, sc6.y, sc6.z, sc6.w};
+                        const float dw = f16_bits_to_f32(dws[jb >> 1] >> (16 * (jb & 1)));
+                        if (gok) f += ((float)il * dw) * xd8[gl][jb];
+                        if (DUMP && rok && gok) {  // per 32-element block (k is a multiple of 256)
+                            p.S[(int64_t)row * (8 * p.ng) + 8 * g + jb] = il;
+                            p.Smin[(int64_t)row * (8 * p.ng) + 8 * g + jb] = 0;
+                        }
+                    }
+                }
+            } else if (Q6) {
                 if (pc == 0) {
                     sc6 = q;
                     dx = xd[gl];
@@ -396,7 +435,7 @@ __device__ __forceinline__ void rl_body(const RlParams p, const int bid, const i
                 issue_in(nxt, j + P - NP, more);
                 __builtin_amdgcn_sched_barrier(0);  // keep the next chunk's load behind this piece's use
             }
-            if (pc == NPG - 1) {
+            if (!Q80 && pc == NPG - 1) {
                 if (Q6) {
                     const float dw = f16_bits_to_f32(dwq);
                     if (gok) f += (dw * dx) * (float)S;
@@ -477,7 +516,9 @@ hipError_t launch_g(const RlParams &p, unsigned grid, bool fused, bool dump, hip
 
 // 56-row workgroups: up to two Q4_K groups per wavefront (32 groups); one
 // Q6_K group (16; two kept 13-piece walks too many registers live)
-bool rows56(int type, int64_t n, int ng) { return ng <= (type == TYPE_Q6_K ? 16 : 32) && n >= RL_MIN_N; }
+bool rows56(int type, int64_t n, int ng) {
+    return type != TYPE_Q8_0 && ng <= (type == TYPE_Q6_K ? 16 : 32) && n >= RL_MIN_N;
+}
 // 8-row workgroups (otherwise 16 rows), for a shape that is not rows56
 bool rows8(int64_t n, int ng) { return ng <= 32 && n >= RE_MIN_N && n <= RE_MAX_N; }
 
@@ -486,8 +527,8 @@ bool rows8(int64_t n, int ng) { return ng <= 32 && n >= RE_MIN_N && n <= RE_MAX_
 // per wavefront; longer rows take two groups each)
 template <int TYPE>
 hipError_t launch_type(const RlParams &p, int64_t n, int ng, bool wide, bool fused, bool dump, hipStream_t s) {
-    constexpr bool Q6 = TYPE == TYPE_Q6_K;
-    if (wide) {
+    constexpr bool Q6 = TYPE == TYPE_Q6_K, Q80 = TYPE == TYPE_Q8_0;
+    if constexpr (!Q80) if (wide) {
         const int64_t nch = (n + RL_ROWS - 1) / RL_ROWS;
         // more chunks than CUs: persistent workgroups, one per CU
         if (ng <= 16 && nch > RL_PERSIST_CUS)
@@ -503,7 +544,7 @@ hipError_t launch_type(const RlParams &p, int64_t n, int ng, bool wide, bool fus
     // start; with 16 wavefronts (ffn_down, 56 groups) five (Q4_K) or seven
     // (Q6_K), the first issued before the quantisation and the rest after
     // it, measured fastest.
-    constexpr int NPG = Q6 ? 13 : 9;
+    constexpr int NPG = Q6 ? 13 : Q80 ? 17 : 9;
     if (rows8(n, ng)) {
         // 8 rows: a wavefront covers eight groups, and there are as many
         // wavefronts as the quantisation needs (four blocks each)
@@ -514,16 +555,19 @@ hipError_t launch_type(const RlParams &p, int64_t n, int ng, bool wide, bool fus
         return launch_g<TYPE, RE_ROWS, 8, 1, NPG, true>(p, g8, fused, dump, s);
     }
     const unsigned grid = (unsigned)((n + RG_ROWS - 1) / RG_ROWS);
-    if (ng <= 16) return launch_g<TYPE, RG_ROWS, 4, 1, Q6 ? 13 : 9, true>(p, grid, fused, dump, s);
-    if (ng <= 32) return launch_g<TYPE, RG_ROWS, 8, 1, Q6 ? 13 : 9, true>(p, grid, fused, dump, s);
-    return launch_g<TYPE, RG_ROWS, 16, 1, Q6 ? 7 : 5, false>(p, grid, fused, dump, s);
+    if (ng <= 16) return launch_g<TYPE, RG_ROWS, 4, 1, NPG, true>(p, grid, fused, dump, s);
+    if (ng <= 32) return launch_g<TYPE, RG_ROWS, 8, 1, NPG, true>(p, grid, fused, dump, s);
+    if constexpr (Q80) return hipErrorNotSupported;  // Q8_0: up to 32 groups
+    else return launch_g<TYPE, RG_ROWS, 16, 1, Q6 ? 7 : 5, false>(p, grid, fused, dump, s);
 }
 
 }  // namespace
 
 bool rowlane_matvec_applies(int type, int64_t n, int64_t k) {
-    return (type == TYPE_Q4_K || type == TYPE_Q6_K) && k % QK_K == 0 && k > 0 && k / QK_K <= RL_MAXG && n <= 0x7fffffff &&
-           (rows56(type, n, (int)(k / QK_K)) || n >= RG_MIN_N);
+    // Q8_0: rows of whole 256-element groups, up to 32 of them
+    const int64_t maxg = type == TYPE_Q8_0 ? 32 : RL_MAXG;
+    return (type == TYPE_Q4_K || type == TYPE_Q6_K || type == TYPE_Q8_0) && k % QK_K == 0 && k > 0 &&
+           k / QK_K <= maxg && n <= 0x7fffffff && (rows56(type, n, (int)(k / QK_K)) || n >= RG_MIN_N);
 }
 
 bool rowlane_xf_applies(int type, int64_t n, int64_t k, int kind) {
@@ -540,7 +584,7 @@ hipError_t rl_params(const WLayout &w, int64_t n, int64_t k, const float *x, con
         return hipErrorInvalidValue;
     if (xf && !rowlane_xf_applies(w.type, n, k, xf->kind)) return hipErrorNotSupported;
     const int ng = (int)(k / QK_K);
-    const int npg = w.type == TYPE_Q6_K ? 13 : 9;
+    const int npg = slabs_of(w.type);
     if (w.ng != ng || w.rb_stride != (int64_t)ng * npg * 128) return hipErrorInvalidValue;
     if (w.type == TYPE_Q6_K && !w.d) return hipErrorInvalidValue;
     if (x && ((uintptr_t)x & 15)) return hipErrorInvalidValue;
@@ -590,6 +634,7 @@ hipError_t launch_rowlane_matvec(const WLayout &w, int64_t n, int64_t k, const f
     if (e != hipSuccess) return e;
     const bool wide = rows56(w.type, n, p.ng), fused = x != nullptr, dump = S != nullptr;
     if (w.type == TYPE_Q6_K) return launch_type<TYPE_Q6_K>(p, n, p.ng, wide, fused, dump, s);
+    if (w.type == TYPE_Q8_0) return launch_type<TYPE_Q8_0>(p, n, p.ng, wide, fused, dump, s);
     return launch_type<TYPE_Q4_K>(p, n, p.ng, wide, fused, dump, s);
 }
 
@@ -602,6 +647,8 @@ hipError_t launch_rowlane_matvec2(const WLayout &w1, int64_t n1, float *y1, cons
     xf2.xout = nullptr;  // the residual is written once, by the first weight's workgroup 0
     if ((e = rl_params(w2, n2, k, x, nullptr, y2, nullptr, nullptr, &xf2, p2)) != hipSuccess) return e;
     const int ng = p1.ng;
+    auto kq = [](int t) { return t == TYPE_Q4_K || t == TYPE_Q6_K; };
+    if (!kq(w1.type) || !kq(w2.type)) return hipErrorNotSupported;
     if (rows56(w1.type, n1, ng) || rows56(w2.type, n2, ng)) return hipErrorNotSupported;  // 16- and 8-row forms only
     if (ng > 32) return hipErrorNotSupported;  // four or eight wavefronts
     // both weights in the form a launch of their own takes, so that the sums

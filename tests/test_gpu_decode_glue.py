@@ -264,7 +264,8 @@ def test_matvec_fused_rmsnorm(env, wtype, n, k, with_delta):
                                         (12, 200, 1024),     # below 256 rows: the general matvec
                                         (12, 14336, 4096),   # 56-row workgroups
                                         (14, 4096, 14336),   # the 16-row form with 16 wavefronts
-                                        (12, 30000, 2048)])  # persistent chunks
+                                        (12, 30000, 2048),   # persistent chunks
+                                        (8, 2048, 2048)])    # Q8_0: the activation quantised to Q8_0 blocks
 def test_matvec_fused_silu_mul(env, wtype, n, k):
     import oracle as O
 

@@ -6,7 +6,8 @@ lm_heads, with persistent chunks beyond 256 of them), of its 16-row form
 (Llama-3-8B ffn_down 4096 x 14336, the attention projections), and of its
 8-row form (lane = row + 8 * group phase), taken from 1025 to 2048 rows up
 to k = 8192 (TinyLlama's wo and w2; its wk, wv and wq|wk take the 16-row
-form).  The fused transforms (RMSNorm,
+form).  Q8_0 weights (up to k = 8192, k a multiple of 256) take the 16- and
+8-row forms with the activation quantised to Q8_0 in the prologue.  The fused transforms (RMSNorm,
 SiLU * up) and the two-weight launch are tested with the decode glue.
 
 Against the oracle (candle-core 0.8.4 k_quants::matmul restated): every
@@ -126,6 +127,55 @@ def test_rowlane_q6k_extreme_values(ctx):
     W.blocks = S.pack_q6k(W.d, W.sc, W.q)
     x = np.repeat(np.abs(rng.standard_normal((1, k // 256))).astype(np.float32) + 0.5, 256, axis=1)
     check_matmul(ctx, W, x, cond=False)
+
+
+@pytest.mark.parametrize("n,k", [
+    (2048, 2048),     # config 1's Q8_0 matvec: 256 workgroups of 8 rows, 8 groups of eight blocks
+    (256, 2048),      # 16 workgroups of 16 rows
+    (1025, 256),      # one group, ragged rows: the last 8-row workgroup has one
+    (2043, 2304),     # 9 groups over four wavefronts, ragged rows
+    (3203, 4096),     # 16-row form, ragged rows: the last workgroup's second row block is partial
+    (4096, 8192),     # 32 groups (the most for Q8_0), eight wavefronts
+    (20000, 2048),    # many rows: Q8_0 keeps the 16-row form
+])
+def test_rowlane_q80_matches_oracle(ctx, n, k):
+    """Q8_0 through the row-per-lane kernel: the activation quantised to Q8_0
+    blocks in the prologue (two lanes per 32-element block), 17 pieces per
+    group (the eight d first), every block's integer dot bit-exact."""
+    W = S.make_weight(S.TYPE_Q8_0, n, k, seed=n + k + 9)
+    x = S.make_activation(1, k, seed=k + 9)
+    check_matmul(ctx, W, x)
+
+
+def test_rowlane_q80_edge_activations_and_entries(ctx):
+    """The edge rows of the Q8_0 quantizer (zeros, 1e-30, 1e30, equal values,
+    ties) through the row-per-lane prologue, block sums bit-exact; and the f32
+    device entry, the pre-quantised entry and the host entry giving the same
+    bits."""
+    from arm_ai_amd import hip
+
+    n, k = 2048, 2048
+    W = S.make_weight(S.TYPE_Q8_0, n, k, seed=91)
+    mm = A.QMatMul.from_qtensor(A.QTensor(W.type, (n, k), W.blocks), ctx)
+    for x in _edge_rows(k):
+        x = x[None, :]
+        xq = O.quantize(x, O.Q8_0)
+        gS, gSm = mm.block_sums(x)
+        oS, oSm = O.block_sums(W.type, k, W.blocks, xq)
+        assert np.array_equal(gS, oS) and np.array_equal(gSm, oSm)
+    x = S.make_activation(1, k, seed=92)
+    y_host = mm.forward(x)
+    dx = hip.to_device(x)
+    dy = hip.DeviceBuffer(n * 4)
+    mm.forward_device(dx.ptr, 1, dy.ptr)
+    act = hip.DeviceBuffer(A.act_bytes(mm.act_type, 1, k))
+    A.quantize_act_device(ctx, mm.act_type, dx.ptr, 1, k, act.ptr)
+    dy2 = hip.DeviceBuffer(n * 4)
+    mm.forward_preq_device(act.ptr, 1, dy2.ptr)
+    ctx.synchronize()
+    assert np.array_equal(dy.download(np.float32, (1, n)), y_host)
+    assert np.array_equal(dy2.download(np.float32, (1, n)), y_host)
+    mm.free()
 
 
 def test_rowlane16_edge_activations(ctx):
