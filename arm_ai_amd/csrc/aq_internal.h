@@ -273,6 +273,9 @@ hipError_t launch_argmax(const float *x, int64_t n, int64_t *d_tok, int64_t *d_p
 namespace aq {
 
 __device__ __forceinline__ int sdot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
+// Bits 0..3 of n (n < 16) to bit 4 of bytes 0..3: n * 0x204081 places bit i
+// of n at bit 9i (no overlap; a 24-bit multiply).
+__device__ __forceinline__ uint32_t spread4(uint32_t n) { return ((n * 0x204081u) & 0x01010101u) << 4; }
 
 // Raw buffer accesses through a descriptor over [base, base + bytes): a lane
 // whose offset lies past the range reads zeros / drops its store without a

@@ -436,10 +436,7 @@ __device__ __forceinline__ void dot_q40(const Wt<TYPE_Q4_0> &W, const uint8_t *l
 // bit 16 + e of qh << 4; value - 16 (GGML dequantize_row_q5_0).  candle:
 // sum_i (x * qx) as f32 * f16(d_w) * f16(d_x), the integer sum formed as
 // sum q*qx - 16 * sum qx.  Four qh bits go to bit 4 of four bytes with one
-// 24-bit multiply: n * 0x204081 places bit i of n at bit 9i (no overlap).
-__device__ __forceinline__ uint32_t spread4(uint32_t n) {
-    return ((n * 0x204081u) & 0x01010101u) << 4;  // n < 16: a 24-bit multiply
-}
+// 24-bit multiply (spread4).
 
 template <int B, bool DUMP>
 __device__ __forceinline__ void dot_q50(const Wt<TYPE_Q5_0> &W, const uint8_t *lds, int ng, int g, int m,

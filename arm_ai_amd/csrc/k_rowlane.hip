@@ -102,17 +102,21 @@ __device__ __forceinline__ void rl_body(const RlParams p, const int bid, const i
     static_assert(XF == RL_XF_NONE || (FUSED && !DUMP), "input transforms take an f32 input and no integer dump");
     static_assert(R == RL_ROWS || R == RG_ROWS || R == RE_ROWS,
                   "56 rows, one per lane, or 16 / 8 rows in four / eight group phases");
-    static_assert(TYPE == TYPE_Q4_K || TYPE == TYPE_Q6_K || TYPE == TYPE_Q8_0, "Q4_K, Q6_K or Q8_0");
-    static_assert(!CH || (R == RL_ROWS && GPW == 1 && P == (TYPE == TYPE_Q6_K ? 13 : 9)),
+    static_assert(TYPE == TYPE_Q4_K || TYPE == TYPE_Q5_K || TYPE == TYPE_Q6_K || TYPE == TYPE_Q8_0 ||
+                  TYPE == TYPE_Q4_0 || TYPE == TYPE_Q5_0, "Q4_K, Q5_K, Q6_K, Q8_0, Q4_0 or Q5_0");
+    constexpr bool Q6 = TYPE == TYPE_Q6_K, Q80 = TYPE == TYPE_Q8_0, Q5K = TYPE == TYPE_Q5_K;
+    constexpr bool Q40 = TYPE == TYPE_Q4_0, Q50 = TYPE == TYPE_Q5_0;
+    constexpr bool A80 = Q80 || Q40 || Q50;  // the activation in Q8_0 blocks of 32
+    constexpr int NPG = slabs_of(TYPE);      // pieces per group
+    static_assert(!CH || (R == RL_ROWS && GPW == 1 && P == NPG),
                   "persistent chunks: one group per wavefront, all its pieces in flight");
     static_assert(TYPE != TYPE_Q8_0 || (R != RL_ROWS && GPW == 1), "Q8_0: the 16- and 8-row forms");
-    constexpr bool Q6 = TYPE == TYPE_Q6_K, Q80 = TYPE == TYPE_Q8_0;
-    constexpr int NPG = Q6 ? 13 : Q80 ? 17 : 9;    // pieces per group
     constexpr int GP = R == RL_ROWS ? 1 : 64 / R;  // group phases per wavefront
     __shared__ __align__(16) uint8_t xq[RL_MAXG][256];  // Q8_K quants of each group
     __shared__ __align__(16) int xb[RL_MAXG][Q6 ? 16 : 8];  // bsums per 16 (Q6_K) or 32 (Q4_K) elements
     __shared__ float xd[RL_MAXG];                       // Q8_K d
-    __shared__ float xd8[Q80 ? RL_MAXG : 1][8];         // Q8_0: the f16 d of each block, as f32
+    __shared__ float xd8[A80 ? RL_MAXG : 1][8];         // Q8_0 blocks: the f16 d of each, as f32
+    __shared__ int xb8[Q40 || Q50 ? RL_MAXG : 1][8];    // ... and the sum of its 32 quants
     __shared__ float red[CH ? 2 : 1][W][64];
     __shared__ float nred[W];  // NORM: the quantising wavefronts' sums of squares
     constexpr int NP = NPG * GPW;  // this wavefront's pieces, in order
@@ -148,7 +152,11 @@ __device__ __forceinline__ void rl_body(const RlParams p, const int bid, const i
     //  order measured fewer registers)
     constexpr bool HALVES = R == RL_ROWS;
     auto piece_of = [&](int pc) {
-        if (Q80) return pc == 0 ? 16 : pc - 1;  // the eight d first, then the quants in order
+        // the eight d of a Q8_0 / Q4_0 / Q5_0 group first (Q5_0: then its two
+        // qh pieces), then the quants in order
+        if (Q80) return pc == 0 ? 16 : pc - 1;
+        if (Q40) return pc == 0 ? 8 : pc - 1;
+        if (Q50) return pc == 0 ? 10 : pc < 3 ? 7 + pc : pc - 3;
         if (!Q6) return pc;
         if (!HALVES) return pc == 0 ? 12 : pc < 5 ? 7 + pc : pc - 5;
         return pc == 0 ? 12 : pc < 3 ? 7 + pc : pc < 7 ? pc - 3 : pc < 9 ? 3 + pc : pc - 5;
@@ -203,12 +211,12 @@ __device__ __forceinline__ void rl_body(const RlParams p, const int bid, const i
         } else {
             const rsrc_t rq = buf_rsrc(p.act.qs, (uint32_t)p.k);
             const rsrc_t rs = buf_rsrc(p.act.bsums, (uint32_t)((p.k / 16) * 2));
-            const rsrc_t rd = buf_rsrc(p.act.d, (uint32_t)((p.k / (Q80 ? QK8_0 : QK_K)) * 4));
+            const rsrc_t rd = buf_rsrc(p.act.d, (uint32_t)((p.k / (A80 ? QK8_0 : QK_K)) * 4));
             xv[0] = __builtin_amdgcn_raw_buffer_load_b128(rq, gbok ? (uint32_t)(gb * QK_K + 16 * s) : BUF_OOB, 0, 0);
-            if (!Q80)
+            if (!A80)
                 xbs = __builtin_amdgcn_raw_buffer_load_b16(rs, gbok ? (uint32_t)((gb * 16 + s) * 2) : BUF_OOB, 0, 0);
-            // Q8_0: d of block 8 gb + s / 2 (the two lanes of a block read the same)
-            const uint32_t dof = Q80 ? (uint32_t)((gb * 8 + (s >> 1)) * 4) : (uint32_t)(gb * 4);
+            // Q8_0 blocks: d of block 8 gb + s / 2 (the two lanes of a block read the same)
+            const uint32_t dof = A80 ? (uint32_t)((gb * 8 + (s >> 1)) * 4) : (uint32_t)(gb * 4);
             xdb = __builtin_amdgcn_raw_buffer_load_b32(rd, gbok ? dof : BUF_OOB, 0, 0);
         }
     }
@@ -278,7 +286,7 @@ __device__ __forceinline__ void rl_body(const RlParams p, const int bid, const i
         uint4 qv;
         int bsum;
         float d;
-        if (FUSED && Q80) {
+        if (FUSED && A80) {
             uint16_t d16;
             qv = q8_0_block_2lanes(v, &d16);
             d = f16_bits_to_f32(d16);
@@ -290,11 +298,20 @@ __device__ __forceinline__ void rl_body(const RlParams p, const int bid, const i
             bsum = (int)(int16_t)xbs;
             d = u32_as_f32(xdb);
         }
+        if (Q40 || Q50) {  // a Q8_0 block's quant sum: this lane's 16, then the pair's
+            bsum = sdot4((int)qv.x, 0x01010101, 0);
+            bsum = sdot4((int)qv.y, 0x01010101, bsum);
+            bsum = sdot4((int)qv.z, 0x01010101, bsum);
+            bsum = sdot4((int)qv.w, 0x01010101, bsum);
+        }
         const int pair = bsum + dpp_i<DPP_QUAD_XOR1>(bsum);  // sub-block s/2 (two 16-element halves)
         if (gbok) {
             *(uint4 *)&xq[gb][16 * s] = qv;
-            if (Q80) {
-                if ((s & 1) == 0) xd8[gb][s >> 1] = d;
+            if (A80) {
+                if ((s & 1) == 0) {
+                    xd8[gb][s >> 1] = d;
+                    if (Q40 || Q50) xb8[gb][s >> 1] = pair;
+                }
             } else {
                 if (Q6) xb[gb][s] = bsum;
                 else if ((s & 1) == 0) xb[gb][s >> 1] = pair;
@@ -362,6 +379,48 @@ __device__ __forceinline__ void rl_body(const RlParams p, const int bid, const i
                         }
                     }
                 }
+            } else if (Q40 || Q50) {
+                // piece 0: the eight f16 d (kept in sc6); Q5_0: pieces 1, 2: the
+                // 32-bit qh of blocks 0-3, 4-7; then block jb per piece: low
+                // nibbles elements 0..15, high nibbles 16..31, value q - 8
+                // (Q5_0: bit e of qh at bit 4, value q - 16).  candle's
+                // ((isum * d_w) * d_x), isum = sum q*qx - 8 (16) * sum qx
+                constexpr int QB = Q50 ? 3 : 1;  // the first quant piece
+                if (pc == 0) {
+                    sc6 = q;
+                } else if (Q50 && pc < QB) {
+                    qhr[pc - 1] = q;
+                } else {
+                    const int jb = pc - QB;
+                    const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
+                    uint32_t hq = 0;
+                    if (Q50) {
+                        const uint4 hh = qhr[jb >> 2];
+                        const uint32_t hw[4] = {hh.x, hh.y, hh.z, hh.w};
+                        hq = hw[jb & 3];
+                    }
+                    const int4 x0 = *(const int4 *)&xq[gl][32 * jb], x1 = *(const int4 *)&xq[gl][32 * jb + 16];
+                    const int x0v[4] = {x0.x, x0.y, x0.z, x0.w}, x1v[4] = {x1.x, x1.y, x1.z, x1.w};
+                    int isum = 0;
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        uint32_t lo = qw[i] & 0x0F0F0F0Fu, hi = (qw[i] >> 4) & 0x0F0F0F0Fu;
+                        if (Q50) {
+                            lo |= spread4((hq >> (4 * i)) & 0xFu);
+                            hi |= spread4((hq >> (16 + 4 * i)) & 0xFu);
+                        }
+                        isum = sdot4((int)lo, x0v[i], isum);
+                        isum = sdot4((int)hi, x1v[i], isum);
+                    }
+                    isum -= (Q50 ? 16 : 8) * xb8[gl][jb];
+                    const uint32_t dws[4] = {sc6.x, sc6.y, sc6.z, sc6.w};
+                    const float dw = f16_bits_to_f32(dws[jb >> 1] >> (16 * (jb & 1)));
+                    if (gok) f += ((float)isum * dw) * xd8[gl][jb];
+                    if (DUMP && rok && gok) {  // per 32-element block (k is a multiple of 256)
+                        p.S[(int64_t)row * (8 * p.ng) + 8 * g + jb] = isum;
+                        p.Smin[(int64_t)row * (8 * p.ng) + 8 * g + jb] = 0;
+                    }
+                }
             } else if (Q6) {
                 if (pc == 0) {
                     sc6 = q;
@@ -410,21 +469,36 @@ __device__ __forceinline__ void rl_body(const RlParams p, const int bid, const i
                 mn47 = ((u2 >> 4) & 0x0F0F0F0Fu) | (((u1 >> 6) & 0x03030303u) << 4);
                 dwp = q.x;
                 S = 0;
+            } else if (Q5K && pc < 3) {
+                qhr[pc - 1] = q;  // qh bytes 0..15, 16..31
             } else {
-                const int c = (pc - 1) >> 1, h = (pc - 1) & 1;
+                // qs piece 1 + 2c + h (Q5_K: 3 + 2c + h)
+                const int c = (pc - (Q5K ? 3 : 1)) >> 1, h = (pc - (Q5K ? 3 : 1)) & 1;
                 // x of the low nibbles (elements 64c + 16h ..) and of the high
                 // nibbles (64c + 32 + 16h ..): the same for every lane
                 const int4 xl = *(const int4 *)&xq[gl][64 * c + 16 * h];
                 const int4 xh = *(const int4 *)&xq[gl][64 * c + 32 + 16 * h];
                 if (h == 0) il = ih = 0;
-                il = sdot4((int)(q.x & 0x0F0F0F0Fu), xl.x, il);
-                ih = sdot4((int)((q.x >> 4) & 0x0F0F0F0Fu), xh.x, ih);
-                il = sdot4((int)(q.y & 0x0F0F0F0Fu), xl.y, il);
-                ih = sdot4((int)((q.y >> 4) & 0x0F0F0F0Fu), xh.y, ih);
-                il = sdot4((int)(q.z & 0x0F0F0F0Fu), xl.z, il);
-                ih = sdot4((int)((q.z >> 4) & 0x0F0F0F0Fu), xh.z, ih);
-                il = sdot4((int)(q.w & 0x0F0F0F0Fu), xl.w, il);
-                ih = sdot4((int)((q.w >> 4) & 0x0F0F0F0Fu), xh.w, ih);
+                const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
+                uint32_t hw[4] = {0u, 0u, 0u, 0u};
+                if (Q5K) {  // qh bytes 16h + i: bit 2c for the low nibble's element, 2c + 1 for the high
+                    const uint4 hb = qhr[h];
+                    hw[0] = hb.x;
+                    hw[1] = hb.y;
+                    hw[2] = hb.z;
+                    hw[3] = hb.w;
+                }
+                const int xlv[4] = {xl.x, xl.y, xl.z, xl.w}, xhv[4] = {xh.x, xh.y, xh.z, xh.w};
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    uint32_t lo = qw[i] & 0x0F0F0F0Fu, hi = (qw[i] >> 4) & 0x0F0F0F0Fu;
+                    if (Q5K) {
+                        lo |= ((hw[i] >> (2 * c)) & 0x01010101u) << 4;
+                        hi |= ((hw[i] >> (2 * c + 1)) & 0x01010101u) << 4;
+                    }
+                    il = sdot4((int)lo, xlv[i], il);
+                    ih = sdot4((int)hi, xhv[i], ih);
+                }
                 if (h == 1) {
                     const uint32_t sw = c < 2 ? sc03 : sc47;
                     S += (int)((sw >> (16 * (c & 1))) & 0xffu) * il + (int)((sw >> (16 * (c & 1) + 8)) & 0xffu) * ih;
@@ -435,7 +509,7 @@ __device__ __forceinline__ void rl_body(const RlParams p, const int bid, const i
                 issue_in(nxt, j + P - NP, more);
                 __builtin_amdgcn_sched_barrier(0);  // keep the next chunk's load behind this piece's use
             }
-            if (!Q80 && pc == NPG - 1) {
+            if (!A80 && pc == NPG - 1) {
                 if (Q6) {
                     const float dw = f16_bits_to_f32(dwq);
                     if (gok) f += (dw * dx) * (float)S;
@@ -528,13 +602,14 @@ bool rows8(int64_t n, int ng) { return ng <= 32 && n >= RE_MIN_N && n <= RE_MAX_
 template <int TYPE>
 hipError_t launch_type(const RlParams &p, int64_t n, int ng, bool wide, bool fused, bool dump, hipStream_t s) {
     constexpr bool Q6 = TYPE == TYPE_Q6_K, Q80 = TYPE == TYPE_Q8_0;
+    constexpr int NPG = slabs_of(TYPE);  // 9 (Q4_K, Q4_0), 11 (Q5_K, Q5_0), 13 (Q6_K), 17 (Q8_0)
     if constexpr (!Q80) if (wide) {
         const int64_t nch = (n + RL_ROWS - 1) / RL_ROWS;
         // more chunks than CUs: persistent workgroups, one per CU
         if (ng <= 16 && nch > RL_PERSIST_CUS)
-            return launch_g<TYPE, RL_ROWS, 16, 1, Q6 ? 13 : 9, true, true>(p, RL_PERSIST_CUS, fused, dump, s);
+            return launch_g<TYPE, RL_ROWS, 16, 1, NPG, true, true>(p, RL_PERSIST_CUS, fused, dump, s);
         const unsigned grid = (unsigned)nch;
-        if (ng <= 16) return launch_g<TYPE, RL_ROWS, 16, 1, Q6 ? 8 : 6, true>(p, grid, fused, dump, s);
+        if (ng <= 16) return launch_g<TYPE, RL_ROWS, 16, 1, Q6 ? 8 : NPG == 11 ? 7 : 6, true>(p, grid, fused, dump, s);
         if constexpr (!Q6) return launch_g<TYPE, RL_ROWS, 16, 2, 12, true>(p, grid, fused, dump, s);
         return hipErrorNotSupported;
     }
@@ -544,7 +619,6 @@ hipError_t launch_type(const RlParams &p, int64_t n, int ng, bool wide, bool fus
     // start; with 16 wavefronts (ffn_down, 56 groups) five (Q4_K) or seven
     // (Q6_K), the first issued before the quantisation and the rest after
     // it, measured fastest.
-    constexpr int NPG = Q6 ? 13 : Q80 ? 17 : 9;
     if (rows8(n, ng)) {
         // 8 rows: a wavefront covers eight groups, and there are as many
         // wavefronts as the quantisation needs (four blocks each)
@@ -558,7 +632,7 @@ hipError_t launch_type(const RlParams &p, int64_t n, int ng, bool wide, bool fus
     if (ng <= 16) return launch_g<TYPE, RG_ROWS, 4, 1, NPG, true>(p, grid, fused, dump, s);
     if (ng <= 32) return launch_g<TYPE, RG_ROWS, 8, 1, NPG, true>(p, grid, fused, dump, s);
     if constexpr (Q80) return hipErrorNotSupported;  // Q8_0: up to 32 groups
-    else return launch_g<TYPE, RG_ROWS, 16, 1, Q6 ? 7 : 5, false>(p, grid, fused, dump, s);
+    else return launch_g<TYPE, RG_ROWS, 16, 1, Q6 ? 7 : NPG == 11 ? 6 : 5, false>(p, grid, fused, dump, s);
 }
 
 }  // namespace
@@ -566,7 +640,8 @@ hipError_t launch_type(const RlParams &p, int64_t n, int ng, bool wide, bool fus
 bool rowlane_matvec_applies(int type, int64_t n, int64_t k) {
     // Q8_0: rows of whole 256-element groups, up to 32 of them
     const int64_t maxg = type == TYPE_Q8_0 ? 32 : RL_MAXG;
-    return (type == TYPE_Q4_K || type == TYPE_Q6_K || type == TYPE_Q8_0) && k % QK_K == 0 && k > 0 &&
+    return (type == TYPE_Q4_K || type == TYPE_Q5_K || type == TYPE_Q6_K || type == TYPE_Q8_0 || type == TYPE_Q4_0 ||
+            type == TYPE_Q5_0) && k % QK_K == 0 && k > 0 &&
            k / QK_K <= maxg && n <= 0x7fffffff && (rows56(type, n, (int)(k / QK_K)) || n >= RG_MIN_N);
 }
 
@@ -635,6 +710,9 @@ hipError_t launch_rowlane_matvec(const WLayout &w, int64_t n, int64_t k, const f
     const bool wide = rows56(w.type, n, p.ng), fused = x != nullptr, dump = S != nullptr;
     if (w.type == TYPE_Q6_K) return launch_type<TYPE_Q6_K>(p, n, p.ng, wide, fused, dump, s);
     if (w.type == TYPE_Q8_0) return launch_type<TYPE_Q8_0>(p, n, p.ng, wide, fused, dump, s);
+    if (w.type == TYPE_Q5_K) return launch_type<TYPE_Q5_K>(p, n, p.ng, wide, fused, dump, s);
+    if (w.type == TYPE_Q4_0) return launch_type<TYPE_Q4_0>(p, n, p.ng, wide, fused, dump, s);
+    if (w.type == TYPE_Q5_0) return launch_type<TYPE_Q5_0>(p, n, p.ng, wide, fused, dump, s);
     return launch_type<TYPE_Q4_K>(p, n, p.ng, wide, fused, dump, s);
 }
 

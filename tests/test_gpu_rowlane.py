@@ -6,8 +6,10 @@ lm_heads, with persistent chunks beyond 256 of them), of its 16-row form
 (Llama-3-8B ffn_down 4096 x 14336, the attention projections), and of its
 8-row form (lane = row + 8 * group phase), taken from 1025 to 2048 rows up
 to k = 8192 (TinyLlama's wo and w2; its wk, wv and wq|wk take the 16-row
-form).  Q8_0 weights (up to k = 8192, k a multiple of 256) take the 16- and
-8-row forms with the activation quantised to Q8_0 in the prologue.  The fused transforms (RMSNorm,
+form).  Q5_K, Q4_0 and Q5_0 weights take the same forms as Q4_K; Q8_0
+weights (up to k = 8192) the 16- and 8-row forms; for Q8_0, Q4_0 and Q5_0
+the activation is quantised to Q8_0 blocks in the prologue (k a multiple of
+256 for all).  The fused transforms (RMSNorm,
 SiLU * up) and the two-weight launch are tested with the decode glue.
 
 Against the oracle (candle-core 0.8.4 k_quants::matmul restated): every
@@ -147,15 +149,60 @@ def test_rowlane_q80_matches_oracle(ctx, n, k):
     check_matmul(ctx, W, x)
 
 
-def test_rowlane_q80_edge_activations_and_entries(ctx):
+@pytest.mark.parametrize("typ", [S.TYPE_Q4_0, S.TYPE_Q5_0, S.TYPE_Q5_K])
+@pytest.mark.parametrize("n,k", [
+    (14336, 4096),    # 56-row workgroups, one group per wavefront
+    (11264, 5632),    # 56-row workgroups, two groups per wavefront (22 groups)
+    (16001, 2048),    # more 56-row chunks than CUs: persistent workgroups, ragged rows
+    (4096, 14336),    # the 16-row form with 16 wavefronts (56 groups)
+    (3203, 4096),     # 16-row form, ragged rows
+    (2043, 2304),     # 8-row form, ragged rows, 9 groups
+])
+def test_rowlane_legacy_and_q5k_match_oracle(ctx, typ, n, k):
+    """Q4_0, Q5_0 (the activation in Q8_0 blocks; q - 8 and q - 16 taken as
+    the block's quant sum times 8 or 16) and Q5_K (the fifth bit from the qh
+    pieces held in registers) through every row-per-lane form, integer sums
+    bit-exact."""
+    W = S.make_weight(typ, n, k, seed=n + k + typ)
+    x = S.make_activation(1, k, seed=k + typ)
+    check_matmul(ctx, W, x)
+
+
+@pytest.mark.parametrize("typ", [S.TYPE_Q4_0, S.TYPE_Q5_0, S.TYPE_Q5_K])
+def test_rowlane_legacy_and_q5k_extreme_values(ctx, typ):
+    """Every quant at its top value (Q4_0 15, Q5_0 31 with every qh bit set,
+    Q5_K 31 with scales and mins 63) against activation blocks of equal
+    values (every quant +-127 or -128), in the 56-row, 16-row and 8-row
+    forms: the largest sums, bit-exact."""
+    rng = np.random.default_rng(typ)
+    for n, k in ((11200, 2048), (4096, 4096), (2048, 2048)):
+        W = S.make_weight(typ, n, k, seed=typ + n)
+        if typ == S.TYPE_Q4_0:
+            W.q[:] = 15
+            W.blocks = S.pack_q4_0(W.d, W.q)
+        elif typ == S.TYPE_Q5_0:
+            W.q[:] = 31
+            W.blocks = S.pack_q5_0(W.d, W.q)
+        else:
+            W.q[:] = 31
+            W.sc[:] = 63
+            W.mn[:] = 63
+            W.blocks = S.pack_q5k(W.d, W.dmin, W.sc, W.mn, W.q)
+        blk = 256 if typ == S.TYPE_Q5_K else 32
+        x = np.repeat(rng.standard_normal((1, k // blk)).astype(np.float32), blk, axis=1)
+        check_matmul(ctx, W, x, cond=False)
+
+
+@pytest.mark.parametrize("typ", [S.TYPE_Q8_0, S.TYPE_Q4_0, S.TYPE_Q5_0])
+def test_rowlane_q80_edge_activations_and_entries(ctx, typ):
     """The edge rows of the Q8_0 quantizer (zeros, 1e-30, 1e30, equal values,
-    ties) through the row-per-lane prologue, block sums bit-exact; and the f32
-    device entry, the pre-quantised entry and the host entry giving the same
-    bits."""
+    ties) through the row-per-lane prologue (with the block quant sums Q4_0
+    and Q5_0 take), block sums bit-exact; and the f32 device entry, the
+    pre-quantised entry and the host entry giving the same bits."""
     from arm_ai_amd import hip
 
     n, k = 2048, 2048
-    W = S.make_weight(S.TYPE_Q8_0, n, k, seed=91)
+    W = S.make_weight(typ, n, k, seed=91 + typ)
     mm = A.QMatMul.from_qtensor(A.QTensor(W.type, (n, k), W.blocks), ctx)
     for x in _edge_rows(k):
         x = x[None, :]
