@@ -103,9 +103,13 @@ __device__ __forceinline__ void rl_body(const RlParams p, const int bid, const i
     static_assert(R == RL_ROWS || R == RG_ROWS || R == RE_ROWS,
                   "56 rows, one per lane, or 16 / 8 rows in four / eight group phases");
     static_assert(TYPE == TYPE_Q4_K || TYPE == TYPE_Q5_K || TYPE == TYPE_Q6_K || TYPE == TYPE_Q8_0 ||
-                  TYPE == TYPE_Q4_0 || TYPE == TYPE_Q5_0, "Q4_K, Q5_K, Q6_K, Q8_0, Q4_0 or Q5_0");
+                  TYPE == TYPE_Q4_0 || TYPE == TYPE_Q5_0 || TYPE == TYPE_Q2_K || TYPE == TYPE_Q3_K,
+                  "a type with a row-per-lane walk");
     constexpr bool Q6 = TYPE == TYPE_Q6_K, Q80 = TYPE == TYPE_Q8_0, Q5K = TYPE == TYPE_Q5_K;
-    constexpr bool Q40 = TYPE == TYPE_Q4_0, Q50 = TYPE == TYPE_Q5_0;
+    constexpr bool Q40 = TYPE == TYPE_Q4_0, Q50 = TYPE == TYPE_Q5_0, Q2K = TYPE == TYPE_Q2_K, Q3K = TYPE == TYPE_Q3_K;
+    constexpr bool B16 = Q6 || Q2K || Q3K;  // bsums per 16 elements (else per 32)
+    constexpr bool DP = Q6 || Q2K;          // a d plane: f16 d (Q6_K), f16 d | f16 dmin << 16 (Q2_K)
+    constexpr int DB = Q2K ? 4 : 2;         // bytes per d-plane entry
     constexpr bool A80 = Q80 || Q40 || Q50;  // the activation in Q8_0 blocks of 32
     constexpr int NPG = slabs_of(TYPE);      // pieces per group
     static_assert(!CH || (R == RL_ROWS && GPW == 1 && P == NPG),
@@ -113,7 +117,7 @@ __device__ __forceinline__ void rl_body(const RlParams p, const int bid, const i
     static_assert(TYPE != TYPE_Q8_0 || (R != RL_ROWS && GPW == 1), "Q8_0: the 16- and 8-row forms");
     constexpr int GP = R == RL_ROWS ? 1 : 64 / R;  // group phases per wavefront
     __shared__ __align__(16) uint8_t xq[RL_MAXG][256];  // Q8_K quants of each group
-    __shared__ __align__(16) int xb[RL_MAXG][Q6 ? 16 : 8];  // bsums per 16 (Q6_K) or 32 (Q4_K) elements
+    __shared__ __align__(16) int xb[RL_MAXG][B16 ? 16 : 8];  // bsums per 16 (Q6_K, Q2_K, Q3_K) or 32 elements
     __shared__ float xd[RL_MAXG];                       // Q8_K d
     __shared__ float xd8[A80 ? RL_MAXG : 1][8];         // Q8_0 blocks: the f16 d of each, as f32
     __shared__ int xb8[Q40 || Q50 ? RL_MAXG : 1][8];    // ... and the sum of its 32 quants
@@ -140,8 +144,9 @@ __device__ __forceinline__ void rl_body(const RlParams p, const int bid, const i
         const int rbs = min(R / RB, nrb - rb0);
         c.rw = buf_rsrc(p.w + (int64_t)rb0 * p.rb_stride, (uint32_t)(rbs * p.rb_stride));
         c.lbase = c.rok ? (uint32_t)((rl / RB) * p.rb_stride + (rl % RB) * 16) : BUF_OOB;
-        c.rwd = buf_rsrc(Q6 ? p.wd + (int64_t)rb0 * p.ng * RB : nullptr, Q6 ? (uint32_t)(rbs * p.ng * RB * 2) : 0u);
-        c.dbase = c.rok ? (uint32_t)(((rl / RB) * p.ng * RB + (rl % RB)) * 2) : BUF_OOB;
+        c.rwd = buf_rsrc(DP ? (const uint8_t *)p.wd + (int64_t)rb0 * p.ng * RB * DB : nullptr,
+                         DP ? (uint32_t)(rbs * p.ng * RB * DB) : 0u);
+        c.dbase = c.rok ? (uint32_t)(((rl / RB) * p.ng * RB + (rl % RB)) * DB) : BUF_OOB;
         return c;
     };
     Chunk cur = chunk_at(bid);
@@ -157,6 +162,7 @@ __device__ __forceinline__ void rl_body(const RlParams p, const int bid, const i
         if (Q80) return pc == 0 ? 16 : pc - 1;
         if (Q40) return pc == 0 ? 8 : pc - 1;
         if (Q50) return pc == 0 ? 10 : pc < 3 ? 7 + pc : pc - 3;
+        if (Q3K) return pc == 0 ? 6 : pc - 1;  // scales and d, hmask, then qs
         if (!Q6) return pc;
         if (!HALVES) return pc == 0 ? 12 : pc < 5 ? 7 + pc : pc - 5;
         return pc == 0 ? 12 : pc < 3 ? 7 + pc : pc < 7 ? pc - 3 : pc < 9 ? 3 + pc : pc - 5;
@@ -171,8 +177,11 @@ __device__ __forceinline__ void rl_body(const RlParams p, const int bid, const i
         const uint32_t off = ok ? c.lbase + (uint32_t)((g * NPG + piece_of(j % NPG)) * 128) : BUF_OOB;
         const u32x4 t = __builtin_amdgcn_raw_buffer_load_b128(c.rw, off, 0, BUF_NT);
         ring[j % P] = make_uint4(t.x, t.y, t.z, t.w);
-        if (Q6 && j % NPG == 0)
-            dring[j / NPG] = __builtin_amdgcn_raw_buffer_load_b16(c.rwd, ok ? c.dbase + (uint32_t)(g * RB * 2) : BUF_OOB, 0, BUF_NT);
+        if (DP && j % NPG == 0) {
+            const uint32_t doff = ok ? c.dbase + (uint32_t)(g * RB * DB) : BUF_OOB;
+            dring[j / NPG] = Q2K ? __builtin_amdgcn_raw_buffer_load_b32(c.rwd, doff, 0, BUF_NT)
+                                 : __builtin_amdgcn_raw_buffer_load_b16(c.rwd, doff, 0, BUF_NT);
+        }
     };
     auto issue = [&](int j) { issue_in(cur, j, true); };
 
@@ -313,7 +322,7 @@ __device__ __forceinline__ void rl_body(const RlParams p, const int bid, const i
                     if (Q40 || Q50) xb8[gb][s >> 1] = pair;
                 }
             } else {
-                if (Q6) xb[gb][s] = bsum;
+                if (B16) xb[gb][s] = bsum;
                 else if ((s & 1) == 0) xb[gb][s >> 1] = pair;
                 if (s == 0) xd[gb] = d;
             }
@@ -421,6 +430,69 @@ __device__ __forceinline__ void rl_body(const RlParams p, const int bid, const i
                         p.Smin[(int64_t)row * (8 * p.ng) + 8 * g + jb] = 0;
                     }
                 }
+            } else if (Q2K) {
+                // piece 0: scale | min << 4 of the 16 16-element groups (kept in
+                // sc6); piece 1 + 2hf + t: qs bytes 32hf + 16t .., whose bits
+                // 2jj, 2jj + 1 are elements 128hf + 32jj + 16t + i (group
+                // 8hf + 2jj + t)
+                if (pc == 0) {
+                    sc6 = q;
+                    dx = xd[gl];
+                    dwq = dring[j / NPG];
+                    S = 0;
+                } else {
+                    const int hf = (pc - 1) >> 1, t = (pc - 1) & 1;
+                    const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
+                    const uint32_t scw[4] = {sc6.x, sc6.y, sc6.z, sc6.w};
+#pragma unroll
+                    for (int jj = 0; jj < 4; jj++) {
+                        const int grp = 8 * hf + 2 * jj + t;
+                        const int4 xv4 = *(const int4 *)&xq[gl][128 * hf + 32 * jj + 16 * t];
+                        const int xa[4] = {xv4.x, xv4.y, xv4.z, xv4.w};
+                        int is = 0;
+#pragma unroll
+                        for (int i = 0; i < 4; i++) is = sdot4((int)((qw[i] >> (2 * jj)) & 0x03030303u), xa[i], is);
+                        S += (int)((scw[grp >> 2] >> (8 * (grp & 3))) & 15u) * is;
+                    }
+                }
+            } else if (Q3K) {
+                // piece 0: scales[12] then the f16 d; pieces 1, 2: hmask bytes
+                // 0..15, 16..31 (kept); piece 3 + 2hf + t: qs bytes 32hf + 16t ..
+                // with the elements as Q2_K's, value (the two bits | hmask bit
+                // 4hf + jj << 2) - 4, taken as the group's bsum times 4; the
+                // 6-bit group scale (candle's auxs form) - 32
+                if (pc == 0) {
+                    const uint32_t a0 = q.x, a1 = q.y, tmp = q.z;
+                    sc6 = make_uint4((a0 & 0x0F0F0F0Fu) | ((tmp & 0x03030303u) << 4),
+                                     (a1 & 0x0F0F0F0Fu) | (((tmp >> 2) & 0x03030303u) << 4),
+                                     ((a0 >> 4) & 0x0F0F0F0Fu) | (((tmp >> 4) & 0x03030303u) << 4),
+                                     ((a1 >> 4) & 0x0F0F0F0Fu) | (((tmp >> 6) & 0x03030303u) << 4));
+                    dwq = q.w;
+                    dx = xd[gl];
+                    S = 0;
+                } else if (pc < 3) {
+                    qhr[pc - 1] = q;
+                } else {
+                    const int hf = (pc - 3) >> 1, t = (pc - 3) & 1;
+                    const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
+                    const uint4 hb = qhr[t];
+                    const uint32_t hv[4] = {hb.x, hb.y, hb.z, hb.w};
+                    const uint32_t scw[4] = {sc6.x, sc6.y, sc6.z, sc6.w};
+#pragma unroll
+                    for (int jj = 0; jj < 4; jj++) {
+                        const int grp = 8 * hf + 2 * jj + t;
+                        const int4 xv4 = *(const int4 *)&xq[gl][128 * hf + 32 * jj + 16 * t];
+                        const int xa[4] = {xv4.x, xv4.y, xv4.z, xv4.w};
+                        int is = 0;
+#pragma unroll
+                        for (int i = 0; i < 4; i++) {
+                            const uint32_t u = ((qw[i] >> (2 * jj)) & 0x03030303u) |
+                                               (((hv[i] >> (4 * hf + jj)) & 0x01010101u) << 2);
+                            is = sdot4((int)u, xa[i], is);
+                        }
+                        S += ((int)((scw[grp >> 2] >> (8 * (grp & 3))) & 0xffu) - 32) * (is - 4 * xb[gl][grp]);
+                    }
+                }
             } else if (Q6) {
                 if (pc == 0) {
                     sc6 = q;
@@ -510,7 +582,25 @@ __device__ __forceinline__ void rl_body(const RlParams p, const int bid, const i
                 __builtin_amdgcn_sched_barrier(0);  // keep the next chunk's load behind this piece's use
             }
             if (!A80 && pc == NPG - 1) {
-                if (Q6) {
+                if (Q2K) {
+                    int smin = 0;
+                    const uint32_t scw[4] = {sc6.x, sc6.y, sc6.z, sc6.w};
+#pragma unroll
+                    for (int gq = 0; gq < 16; gq++) smin += (int)((scw[gq >> 2] >> (8 * (gq & 3) + 4)) & 15u) * xb[gl][gq];
+                    const float dw = f16_bits_to_f32(dwq), dmw = f16_bits_to_f32(dwq >> 16);
+                    if (gok) f += (dw * dx) * (float)S - (dmw * dx) * (float)smin;
+                    if (DUMP && rok && gok) {
+                        p.S[(int64_t)row * p.ng + g] = S;
+                        p.Smin[(int64_t)row * p.ng + g] = smin;
+                    }
+                } else if (Q3K) {
+                    const float dw = f16_bits_to_f32(dwq);
+                    if (gok) f += (dw * dx) * (float)S;
+                    if (DUMP && rok && gok) {
+                        p.S[(int64_t)row * p.ng + g] = S;
+                        p.Smin[(int64_t)row * p.ng + g] = 0;
+                    }
+                } else if (Q6) {
                     const float dw = f16_bits_to_f32(dwq);
                     if (gok) f += (dw * dx) * (float)S;
                     if (DUMP && rok && gok) {
@@ -641,7 +731,7 @@ bool rowlane_matvec_applies(int type, int64_t n, int64_t k) {
     // Q8_0: rows of whole 256-element groups, up to 32 of them
     const int64_t maxg = type == TYPE_Q8_0 ? 32 : RL_MAXG;
     return (type == TYPE_Q4_K || type == TYPE_Q5_K || type == TYPE_Q6_K || type == TYPE_Q8_0 || type == TYPE_Q4_0 ||
-            type == TYPE_Q5_0) && k % QK_K == 0 && k > 0 &&
+            type == TYPE_Q5_0 || type == TYPE_Q2_K || type == TYPE_Q3_K) && k % QK_K == 0 && k > 0 &&
            k / QK_K <= maxg && n <= 0x7fffffff && (rows56(type, n, (int)(k / QK_K)) || n >= RG_MIN_N);
 }
 
@@ -661,7 +751,7 @@ hipError_t rl_params(const WLayout &w, int64_t n, int64_t k, const float *x, con
     const int ng = (int)(k / QK_K);
     const int npg = slabs_of(w.type);
     if (w.ng != ng || w.rb_stride != (int64_t)ng * npg * 128) return hipErrorInvalidValue;
-    if (w.type == TYPE_Q6_K && !w.d) return hipErrorInvalidValue;
+    if ((w.type == TYPE_Q6_K || w.type == TYPE_Q2_K) && !w.d) return hipErrorInvalidValue;
     if (x && ((uintptr_t)x & 15)) return hipErrorInvalidValue;
     const bool wide = rows56(w.type, n, ng);
     if ((int64_t)(wide ? RL_ROWS : RG_ROWS) / RB * w.rb_stride >= ((int64_t)1 << 31)) return hipErrorNotSupported;
@@ -713,6 +803,8 @@ hipError_t launch_rowlane_matvec(const WLayout &w, int64_t n, int64_t k, const f
     if (w.type == TYPE_Q5_K) return launch_type<TYPE_Q5_K>(p, n, p.ng, wide, fused, dump, s);
     if (w.type == TYPE_Q4_0) return launch_type<TYPE_Q4_0>(p, n, p.ng, wide, fused, dump, s);
     if (w.type == TYPE_Q5_0) return launch_type<TYPE_Q5_0>(p, n, p.ng, wide, fused, dump, s);
+    if (w.type == TYPE_Q2_K) return launch_type<TYPE_Q2_K>(p, n, p.ng, wide, fused, dump, s);
+    if (w.type == TYPE_Q3_K) return launch_type<TYPE_Q3_K>(p, n, p.ng, wide, fused, dump, s);
     return launch_type<TYPE_Q4_K>(p, n, p.ng, wide, fused, dump, s);
 }
 

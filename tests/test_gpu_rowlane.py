@@ -6,7 +6,8 @@ lm_heads, with persistent chunks beyond 256 of them), of its 16-row form
 (Llama-3-8B ffn_down 4096 x 14336, the attention projections), and of its
 8-row form (lane = row + 8 * group phase), taken from 1025 to 2048 rows up
 to k = 8192 (TinyLlama's wo and w2; its wk, wv and wq|wk take the 16-row
-form).  Q5_K, Q4_0 and Q5_0 weights take the same forms as Q4_K; Q8_0
+form).  Q5_K, Q4_0, Q5_0, Q2_K and Q3_K weights take the same forms as
+Q4_K; Q8_0
 weights (up to k = 8192) the 16- and 8-row forms; for Q8_0, Q4_0 and Q5_0
 the activation is quantised to Q8_0 blocks in the prologue (k a multiple of
 256 for all).  The fused transforms (RMSNorm,
@@ -149,7 +150,7 @@ def test_rowlane_q80_matches_oracle(ctx, n, k):
     check_matmul(ctx, W, x)
 
 
-@pytest.mark.parametrize("typ", [S.TYPE_Q4_0, S.TYPE_Q5_0, S.TYPE_Q5_K])
+@pytest.mark.parametrize("typ", [S.TYPE_Q4_0, S.TYPE_Q5_0, S.TYPE_Q5_K, S.TYPE_Q2_K, S.TYPE_Q3_K])
 @pytest.mark.parametrize("n,k", [
     (14336, 4096),    # 56-row workgroups, one group per wavefront
     (11264, 5632),    # 56-row workgroups, two groups per wavefront (22 groups)
@@ -160,19 +161,22 @@ def test_rowlane_q80_matches_oracle(ctx, n, k):
 ])
 def test_rowlane_legacy_and_q5k_match_oracle(ctx, typ, n, k):
     """Q4_0, Q5_0 (the activation in Q8_0 blocks; q - 8 and q - 16 taken as
-    the block's quant sum times 8 or 16) and Q5_K (the fifth bit from the qh
-    pieces held in registers) through every row-per-lane form, integer sums
-    bit-exact."""
+    the block's quant sum times 8 or 16), Q5_K (the fifth bit from the qh
+    pieces held in registers), Q2_K (d and dmin from the d plane) and Q3_K
+    (the hmask pieces held; q - 4 and the scale - 32) through every
+    row-per-lane form, integer sums bit-exact."""
     W = S.make_weight(typ, n, k, seed=n + k + typ)
     x = S.make_activation(1, k, seed=k + typ)
     check_matmul(ctx, W, x)
 
 
-@pytest.mark.parametrize("typ", [S.TYPE_Q4_0, S.TYPE_Q5_0, S.TYPE_Q5_K])
-def test_rowlane_legacy_and_q5k_extreme_values(ctx, typ):
-    """Every quant at its top value (Q4_0 15, Q5_0 31 with every qh bit set,
-    Q5_K 31 with scales and mins 63) against activation blocks of equal
-    values (every quant +-127 or -128), in the 56-row, 16-row and 8-row
+@pytest.mark.parametrize("typ,low", [(S.TYPE_Q4_0, False), (S.TYPE_Q5_0, False), (S.TYPE_Q5_K, False),
+                                     (S.TYPE_Q2_K, False), (S.TYPE_Q3_K, False), (S.TYPE_Q3_K, True)])
+def test_rowlane_legacy_and_q5k_extreme_values(ctx, typ, low):
+    """Every quant at an end of its range (Q4_0 15, Q5_0 31 with every qh bit
+    set, Q5_K 31 with scales and mins 63, Q2_K 3 with scales and mins 15,
+    Q3_K 3 with scale 31 or -4 with scale -32) against activation blocks of
+    equal values (every quant +-127 or -128), in the 56-row, 16-row and 8-row
     forms: the largest sums, bit-exact."""
     rng = np.random.default_rng(typ)
     for n, k in ((11200, 2048), (4096, 4096), (2048, 2048)):
@@ -183,12 +187,21 @@ def test_rowlane_legacy_and_q5k_extreme_values(ctx, typ):
         elif typ == S.TYPE_Q5_0:
             W.q[:] = 31
             W.blocks = S.pack_q5_0(W.d, W.q)
-        else:
+        elif typ == S.TYPE_Q5_K:
             W.q[:] = 31
             W.sc[:] = 63
             W.mn[:] = 63
             W.blocks = S.pack_q5k(W.d, W.dmin, W.sc, W.mn, W.q)
-        blk = 256 if typ == S.TYPE_Q5_K else 32
+        elif typ == S.TYPE_Q2_K:
+            W.q[:] = 3
+            W.sc[:] = 15
+            W.mn[:] = 15
+            W.blocks = S.pack_q2k(W.d, W.dmin, W.sc, W.mn, W.q)
+        else:
+            W.q[:] = -4 if low else 3
+            W.sc[:] = -32 if low else 31
+            W.blocks = S.pack_q3k(W.d, W.sc, W.q)
+        blk = 32 if typ in (S.TYPE_Q4_0, S.TYPE_Q5_0) else 256
         x = np.repeat(rng.standard_normal((1, k // blk)).astype(np.float32), blk, axis=1)
         check_matmul(ctx, W, x, cond=False)
 
