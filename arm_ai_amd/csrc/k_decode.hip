@@ -335,8 +335,9 @@ __global__ __launch_bounds__(WIDE_THREADS) void attn_decode_kernel(
 // Greedy pick: the first index of the largest value (a NaN never wins; all
 // NaN gives 0).  Writes it to *d_tok (the next step's input), to
 // hist[*d_pos] when hist is given, and advances *d_pos by one.  One
-// 1024-thread workgroup, float4 loads (x 16-byte aligned), several in
-// flight; the last n % 4 elements are read one by one.
+// 1024-thread workgroup, float4 loads (x 16-byte aligned), eight per thread
+// in flight (one round trip up to 32768 values); the last n % 4 elements are
+// read one by one, and the position is loaded with the first round.
 __device__ __forceinline__ void better(float v, int i, float &best, int &idx) {
     if (v > best || (v == best && i < idx)) {  // NaN compares false
         best = v;
@@ -352,15 +353,16 @@ __global__ __launch_bounds__(WIDE_THREADS) void argmax_kernel(const float *__res
     int idx = 0x7fffffff;
     const float4 *x4 = (const float4 *)x;
     const int n4 = n / 4;
-    for (int i0 = threadIdx.x; i0 < n4; i0 += 4 * WIDE_THREADS) {
-        float4 v[4];
+    const int64_t pos = threadIdx.x == 0 ? *d_pos : 0;  // only thread 0 uses it
+    for (int i0 = threadIdx.x; i0 < n4; i0 += 8 * WIDE_THREADS) {
+        float4 v[8];
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
+        for (int u = 0; u < 8; u++) {
             const int i = i0 + u * WIDE_THREADS;
             v[u] = i < n4 ? x4[i] : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
         }
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
+        for (int u = 0; u < 8; u++) {
             const int i = 4 * (i0 + u * WIDE_THREADS);
             better(v[u].x, i, best, idx);
             better(v[u].y, i + 1, best, idx);
@@ -383,7 +385,6 @@ __global__ __launch_bounds__(WIDE_THREADS) void argmax_kernel(const float *__res
     if (threadIdx.x == 0) {
         for (int w = 1; w < WIDE_THREADS / 64; w++) better(bv[w], bi[w], best, idx);
         if (idx == 0x7fffffff) idx = 0;
-        const int64_t pos = *d_pos;
         *d_tok = idx;
         if (hist && pos >= 0 && pos < hist_len) hist[pos] = idx;
         *d_pos = pos + 1;

@@ -158,6 +158,30 @@ def test_argmax_first_max_history_and_position(env):
     assert h[10] == 777 and np.all(np.delete(h, 10) == -1)
 
 
+@pytest.mark.parametrize("n,where", [(128256, 120001), (128256, 3)])
+def test_argmax_llama3_vocab_tie_across_rounds(env, n, where):
+    """A Llama-3 vocabulary (several rounds of eight float4 per thread): the
+    maximum in a later round, then tied with one in the first round (the
+    earlier index wins)."""
+    torch, lib, ctx = env
+    L = lib.load()
+    x = np.random.default_rng(n + where).standard_normal(n).astype(np.float32)
+    x[where] = 30.0
+    tok = torch.zeros(1, dtype=torch.int64, device="cuda:0")
+    pos = torch.tensor([3], dtype=torch.int64, device="cuda:0")
+    dx = _dev(torch, x)
+    torch.cuda.synchronize()
+    lib.check(L.aq_llama_argmax(ctx.handle, dx.data_ptr(), n, tok.data_ptr(), pos.data_ptr(), None, 0))
+    ctx.synchronize()
+    assert int(tok.item()) == where and int(pos.item()) == 4
+    x[n - 1 - where] = 30.0
+    dx = _dev(torch, x)
+    torch.cuda.synchronize()
+    lib.check(L.aq_llama_argmax(ctx.handle, dx.data_ptr(), n, tok.data_ptr(), pos.data_ptr(), None, 0))
+    ctx.synchronize()
+    assert int(tok.item()) == min(where, n - 1 - where) and int(pos.item()) == 5
+
+
 @pytest.mark.parametrize("n,where", [(32001, 32000), (32003, 32001), (32003, 5), (7, 6), (1, 0)])
 def test_argmax_vocab_not_a_multiple_of_four(env, n, where):
     """Vocabularies such as 32001 or 32003 (some Llama-2 fine-tunes): the
