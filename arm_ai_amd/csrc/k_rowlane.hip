@@ -1,26 +1,28 @@
-// k_rowlane.hip -- batch-1 Q4_K matvec with one weight row per lane, gfx950.
+// k_rowlane.hip -- batch-1 matvec with one weight row per lane, gfx950, for
+// Q4_K, Q5_K, Q6_K, Q8_0, Q4_0, Q5_0, Q2_K and Q3_K weights.
 //
-// Replaces the column loop of candle-core 0.8.4 k_quants::matmul<BlockQ4K>
-// (each output column = BlockQ4K::vec_dot(k, W[col], xq)) for one activation
-// row, the decode call at native/arm_ai_nif/src/llama_candle.rs:119, on
-// weights with many rows (Llama-3-8B ffn_up / ffn_gate: 14336 x 4096).  The
-// integer sums S and Smin of every super-block are exact; only the f32
-// combination order differs from candle's vec_dot_unopt.
+// Replaces the column loop of candle-core 0.8.4 k_quants::matmul<T> (each
+// output column = T::vec_dot(k, W[col], xq)) for one activation row, the
+// decode call at native/arm_ai_nif/src/llama_candle.rs:119.  The integer sums
+// of every block are exact; only the f32 combination order differs from
+// candle's vec_dot_unopt.
 //
 // Mapping.  A workgroup (W = 16 wavefronts) owns 56 consecutive weight rows (seven
 // 8-row blocks of the row-block tile layout, so every CU of a 256-CU GPU gets
-// the same bytes at the headline shape).  Lane l of every wavefront is row
-// row0 + l (lanes 56..63 are idle); wavefront w takes the 256-element groups
-// w, w + W, ...  A load instruction therefore reads piece p of one group for
-// 56 rows: seven full 128-byte lines.  Because all lanes of a wavefront work
-// on the same group, the activation operand of every v_dot4 is the same for
-// all lanes: it is read from LDS at a wave-uniform address (one 16-byte
-// broadcast read per four v_dot4), so the weights are the only per-lane data.
+// the same bytes at the headline shape, Q4_K 14336 x 4096).  Lane l of every
+// wavefront is row row0 + l (lanes 56..63 are idle); wavefront w takes the
+// 256-element groups w, w + W, ...  A load instruction therefore reads piece
+// p of one group for 56 rows: seven full 128-byte lines.  Because all lanes of
+// a wavefront work on the same group, the activation operand of every v_dot4
+// is the same for all lanes: it is read from LDS at a wave-uniform address
+// (one 16-byte broadcast read per four v_dot4), so the weights are the only
+// per-lane data.
 //
 // Schedule.  The first ceil(groups / 4) wavefronts load the activation, then
 // every wavefront issues its first P weight pieces, then those wavefronts
-// quantise four Q8_K blocks each (16 lanes per block, 16 elements per lane)
-// into LDS while the weight pieces are in flight.
+// quantise four blocks of 256 each (Q8_K, or eight Q8_0 blocks of 32 for the
+// Q8_0 / Q4_0 / Q5_0 weights; 16 lanes per 256, 16 elements per lane) into
+// LDS while the weight pieces are in flight.
 // After one barrier each wavefront walks its pieces in order, keeping P of
 // them in flight (compute piece j, issue piece j + P): a wavefront never
 // waits at the barrier behind its own blocked load issues, and the dot
@@ -28,14 +30,15 @@
 // Partial sums of a row (one per group) are added across the wavefronts
 // through LDS, in wavefront order.
 //
-// Fewer rows (from 3200; the Llama-3-8B attention projections and ffn_down,
+// Fewer rows (from 256; the Llama-3-8B attention projections and ffn_down,
 // 4096 rows) with up to 64 groups: a workgroup owns 16 rows and lane l of a
 // wavefront is row l % 16 of group phase l / 16, so one load instruction
 // reads piece p of four groups for 16 rows (eight full lines) and 256
 // workgroups cover 4096 rows.  The activation operand then differs between
 // the four 16-lane sets of a wavefront (four broadcast LDS reads), and a
 // row's partials are first added across its four lanes, then across the
-// wavefronts.
+// wavefronts.  From 1025 to 2048 rows, 8-row workgroups (eight group phases)
+// fill the CUs instead.
 #include "aq_internal.h"
 
 namespace aq {
