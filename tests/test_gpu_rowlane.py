@@ -350,6 +350,28 @@ def test_rowlane_and_general_matvec_agree(ctx):
     small.free()
 
 
+@pytest.mark.parametrize("typ", [S.TYPE_Q5_K, S.TYPE_Q6_K, S.TYPE_Q8_0, S.TYPE_Q4_0, S.TYPE_Q5_0, S.TYPE_Q2_K,
+                                 S.TYPE_Q3_K])
+def test_rowlane_and_general_matvec_agree_every_type(ctx, typ):
+    """At the row count where the row-per-lane kernel takes over (256 rows,
+    16-row form) against the general matvec on the first 248 rows as a
+    weight of their own: the integer sums are identical and the outputs agree
+    to the tolerance, for every type the kernel takes."""
+    k = 4096
+    W = S.make_weight(typ, RG_MIN_N, k, seed=40 + typ)
+    x = S.make_activation(1, k, seed=41 + typ)
+    big = A.QMatMul.from_qtensor(A.QTensor(W.type, (W.n, k), W.blocks), ctx)
+    n2 = RG_MIN_N - 8
+    small = A.QMatMul.from_qtensor(A.QTensor(W.type, (n2, k), W.blocks[:n2]), ctx)
+    sb, smb = big.block_sums(x)
+    ss, sms = small.block_sums(x)
+    assert np.array_equal(sb[:, :n2], ss) and np.array_equal(smb[:, :n2], sms)
+    yb, ys = big.forward(x), small.forward(x)
+    assert float(np.abs(yb[:, :n2] - ys).max()) <= 1e-5 * float(np.abs(ys).max())
+    big.free()
+    small.free()
+
+
 def test_rowlane16_and_general_matvec_agree(ctx):
     """The 16-row form (n >= 256) against the general matvec on the first
     248 rows of the same weight: integer sums identical, outputs within the
