@@ -566,7 +566,10 @@ __device__ __forceinline__ void rl_body(const RlParams p, const int bid, const i
                 const int xlv[4] = {xl.x, xl.y, xl.z, xl.w}, xhv[4] = {xh.x, xh.y, xh.z, xh.w};
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
-                    uint32_t lo = qw[i] & 0x0F0F0F0Fu, hi = (qw[i] >> 4) & 0x0F0F0F0Fu;
+                    // Q4_K: the high nibbles in place, (q & 0xF0) ^ 0x80 = 16 q - 128 as
+                    // a signed byte (one three-input bit operation)
+                    uint32_t lo = qw[i] & 0x0F0F0F0Fu;
+                    uint32_t hi = Q5K ? (qw[i] >> 4) & 0x0F0F0F0Fu : (qw[i] & 0xF0F0F0F0u) ^ 0x80808080u;
                     if (Q5K) {
                         lo |= ((hw[i] >> (2 * c)) & 0x01010101u) << 4;
                         hi |= ((hw[i] >> (2 * c + 1)) & 0x01010101u) << 4;
@@ -575,6 +578,8 @@ __device__ __forceinline__ void rl_body(const RlParams p, const int bid, const i
                     ih = sdot4((int)hi, xhv[i], ih);
                 }
                 if (h == 1) {
+                    // Q4_K: sum q x = (sum (16 q - 128) x + 128 sum x) / 16, exactly
+                    if (!Q5K) ih = (ih + 128 * bs[2 * c + 1]) >> 4;
                     const uint32_t sw = c < 2 ? sc03 : sc47;
                     S += (int)((sw >> (16 * (c & 1))) & 0xffu) * il + (int)((sw >> (16 * (c & 1) + 8)) & 0xffu) * ih;
                 }
