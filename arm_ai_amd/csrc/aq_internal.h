@@ -146,8 +146,9 @@ hipError_t launch_expand_q80(int type, const uint8_t *src, int64_t n, int64_t k,
 // S/Smin non-null selects the integer-dump variant ([m][n][blocks] int32).
 hipError_t launch_matvec(const WLayout &w, int64_t n, int64_t k, const float *x, const ActPlanes *act, int64_t m,
                          float *y, int32_t *S, int32_t *Smin, hipStream_t s);
-// Batch-1 Q4_K / Q6_K matvec with one weight row per lane (k_rowlane.hip),
-// for weights of at least 256 rows and k <= 16384; hipErrorNotSupported for
+// Batch-1 matvec with one weight row per lane (k_rowlane.hip) for Q4_K,
+// Q5_K, Q6_K, Q8_0, Q4_0, Q5_0, Q2_K and Q3_K weights of at least 256 rows, k
+// a multiple of 256 and <= 16384 (8192 for Q8_0); hipErrorNotSupported for
 // other shapes.  x (f32, quantised in the kernel) or act (pre-quantised
 // planes of one row).  xf (x only, no dump): kind RL_XF_NORM quantises
 // rms_norm(x + delta) * w (k <= 8192; workgroup 0 writes x + delta to
