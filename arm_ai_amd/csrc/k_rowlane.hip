@@ -356,6 +356,11 @@ __device__ __forceinline__ void rl_body(const RlParams p, const int bid, const i
     uint4 qhr[4] = {};  // Q6_K: the qh pieces held (HALVES: those of the current 128-element half)
     uint4 sc6 = {};     // Q6_K: the group's 16 sub-scales
     int S = 0, il = 0, ih = 0;
+    // a group's terms that need only its piece 0 and the activation, taken
+    // when piece 0 arrives rather than after its last piece: d_w * d_x, and
+    // (Q4_K, Q5_K, Q2_K) the min sum and (dmin_w * d_x) * smin
+    int smin = 0;
+    float dwdx = 0.0f, fmin = 0.0f;
     // (persistent: a wavefront without a group skips the walk as a whole, so
     //  the pieces in flight across chunks have one path through it)
     if (!CH || group_of(0) < p.ng) {  // uniform
@@ -443,6 +448,13 @@ __device__ __forceinline__ void rl_body(const RlParams p, const int bid, const i
                     dx = xd[gl];
                     dwq = dring[j / NPG];
                     S = 0;
+                    smin = 0;
+                    const uint32_t scw[4] = {sc6.x, sc6.y, sc6.z, sc6.w};
+#pragma unroll
+                    for (int gq = 0; gq < 16; gq++) smin += (int)((scw[gq >> 2] >> (8 * (gq & 3) + 4)) & 15u) * xb[gl][gq];
+                    const float dw = f16_bits_to_f32(dwq), dmw = f16_bits_to_f32(dwq >> 16);
+                    dwdx = dw * dx;
+                    fmin = (dmw * dx) * (float)smin;
                 } else {
                     const int hf = (pc - 1) >> 1, t = (pc - 1) & 1;
                     const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
@@ -472,6 +484,7 @@ __device__ __forceinline__ void rl_body(const RlParams p, const int bid, const i
                                      ((a1 >> 4) & 0x0F0F0F0Fu) | (((tmp >> 6) & 0x03030303u) << 4));
                     dwq = q.w;
                     dx = xd[gl];
+                    dwdx = f16_bits_to_f32(dwq) * dx;
                     S = 0;
                 } else if (pc < 3) {
                     qhr[pc - 1] = q;
@@ -501,6 +514,7 @@ __device__ __forceinline__ void rl_body(const RlParams p, const int bid, const i
                     sc6 = q;
                     dx = xd[gl];
                     dwq = dring[j / NPG];
+                    dwdx = f16_bits_to_f32(dwq) * dx;
                     S = 0;
                 } else if (HALVES ? (pc == 1 || pc == 2 || pc == 7 || pc == 8) : pc < 5) {
                     qhr[HALVES ? (pc - 1) % 2 : pc - 1] = q;
@@ -544,6 +558,12 @@ __device__ __forceinline__ void rl_body(const RlParams p, const int bid, const i
                 mn47 = ((u2 >> 4) & 0x0F0F0F0Fu) | (((u1 >> 6) & 0x03030303u) << 4);
                 dwp = q.x;
                 S = 0;
+                smin = 0;
+#pragma unroll
+                for (int jj = 0; jj < 8; jj++) smin += (int)(((jj < 4 ? mn03 : mn47) >> (8 * (jj & 3))) & 0xffu) * bs[jj];
+                const float dw = f16_bits_to_f32(dwp), dmw = f16_bits_to_f32(dwp >> 16);
+                dwdx = dw * dx;
+                fmin = (dmw * dx) * (float)smin;
             } else if (Q5K && pc < 3) {
                 qhr[pc - 1] = q;  // qh bytes 0..15, 16..31
             } else {
@@ -590,41 +610,16 @@ __device__ __forceinline__ void rl_body(const RlParams p, const int bid, const i
                 __builtin_amdgcn_sched_barrier(0);  // keep the next chunk's load behind this piece's use
             }
             if (!A80 && pc == NPG - 1) {
-                if (Q2K) {
-                    int smin = 0;
-                    const uint32_t scw[4] = {sc6.x, sc6.y, sc6.z, sc6.w};
-#pragma unroll
-                    for (int gq = 0; gq < 16; gq++) smin += (int)((scw[gq >> 2] >> (8 * (gq & 3) + 4)) & 15u) * xb[gl][gq];
-                    const float dw = f16_bits_to_f32(dwq), dmw = f16_bits_to_f32(dwq >> 16);
-                    if (gok) f += (dw * dx) * (float)S - (dmw * dx) * (float)smin;
-                    if (DUMP && rok && gok) {
-                        p.S[(int64_t)row * p.ng + g] = S;
-                        p.Smin[(int64_t)row * p.ng + g] = smin;
-                    }
-                } else if (Q3K) {
-                    const float dw = f16_bits_to_f32(dwq);
-                    if (gok) f += (dw * dx) * (float)S;
-                    if (DUMP && rok && gok) {
-                        p.S[(int64_t)row * p.ng + g] = S;
-                        p.Smin[(int64_t)row * p.ng + g] = 0;
-                    }
-                } else if (Q6) {
-                    const float dw = f16_bits_to_f32(dwq);
-                    if (gok) f += (dw * dx) * (float)S;
-                    if (DUMP && rok && gok) {
-                        p.S[(int64_t)row * p.ng + g] = S;
-                        p.Smin[(int64_t)row * p.ng + g] = 0;
-                    }
-                } else {
-                    int smin = 0;
-    #pragma unroll
-                    for (int jj = 0; jj < 8; jj++) smin += (int)(((jj < 4 ? mn03 : mn47) >> (8 * (jj & 3))) & 0xffu) * bs[jj];
-                    const float dw = f16_bits_to_f32(dwp), dmw = f16_bits_to_f32(dwp >> 16);
-                    if (gok) f += (dw * dx) * (float)S - (dmw * dx) * (float)smin;
-                    if (DUMP && rok && gok) {
-                        p.S[(int64_t)row * p.ng + g] = S;
-                        p.Smin[(int64_t)row * p.ng + g] = smin;
-                    }
+                // (d_w * d_x) * S - (dmin_w * d_x) * smin (Q4_K, Q5_K, Q2_K),
+                // (d_w * d_x) * S (Q6_K, Q3_K)
+                constexpr bool MIN = !(Q6 || Q3K);
+                if (gok) {
+                    if (MIN) f += dwdx * (float)S - fmin;
+                    else f += dwdx * (float)S;
+                }
+                if (DUMP && rok && gok) {
+                    p.S[(int64_t)row * p.ng + g] = S;
+                    p.Smin[(int64_t)row * p.ng + g] = MIN ? smin : 0;
                 }
             }
         }
