@@ -208,10 +208,12 @@ __device__ __forceinline__ v4f superblock(const WStage<TYPE> &W, const uint8_t *
                 const v4i acc = __builtin_amdgcn_mfma_i32_16x16x32_i8(as_long(u32x2{x.x & keep, x.y & keep}),
                                                                       as_long(u32x2{qv[0], qv[1]}), z, 0, 0, 0);
                 const int sc = sbyte(scw[pi >> 1], 8 * (2 * (pi & 1) + L.h));
-                S[0] += sc * acc.x;
-                S[1] += sc * acc.y;
-                S[2] += sc * acc.z;
-                S[3] += sc * acc.w;
+                // |acc| <= 16 * 63 * 128 and |sc| <= 128 fit 24 bits: the
+                // full-rate 24-bit multiply gives the same integers
+                S[0] += __mul24(sc, acc.x);
+                S[1] += __mul24(sc, acc.y);
+                S[2] += __mul24(sc, acc.z);
+                S[3] += __mul24(sc, acc.w);
             }
         }
         // offset term: K slot 4j + t is bsums[4j + t] against scale 4j + t
@@ -447,10 +449,12 @@ __global__ __launch_bounds__(512) void mmv_q4k_kernel(MmvParams p) {
                 }
 #pragma unroll
                 for (int h = 0; h < 2; h++) {
-                    S[h][0] += sc * acc[h].x;
-                    S[h][1] += sc * acc[h].y;
-                    S[h][2] += sc * acc[h].z;
-                    S[h][3] += sc * acc[h].w;
+                    // |acc| <= 32 * 15 * 128 and sc <= 63 fit 24 bits: the
+                    // full-rate 24-bit multiply gives the same integers
+                    S[h][0] += __mul24(sc, acc[h].x);
+                    S[h][1] += __mul24(sc, acc[h].y);
+                    S[h][2] += __mul24(sc, acc[h].z);
+                    S[h][3] += __mul24(sc, acc[h].w);
                 }
             }
             // min term: K slot 8u + t is bsums[8u + t] of sub-block 4u + t/2
