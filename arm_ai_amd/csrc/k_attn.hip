@@ -54,8 +54,9 @@ __device__ __forceinline__ void axpy4(float4 &acc, float w, const float4 x) {
 constexpr float4 ZERO4 = {0.0f, 0.0f, 0.0f, 0.0f};
 
 // ------------------------------------------------------------------ decode
-// Two launches.  attn_split_kernel: grid (S slices, n_kv kv heads), 256
-// threads.  Workgroup (s, g) takes the positions [s*len, (s+1)*len) of
+// Two launches.  attn_split_kernel: grid (slices, n_kv kv heads), 256
+// threads, for the S slices of the workspace or, when max_seq is shorter,
+// the ceil(max_seq / 32) that can ever hold positions.  Workgroup (s, g) takes the positions [s*len, (s+1)*len) of
 // 0..pos (len = max(32, ceil((pos+1)/S))) for all REP = n_head / n_kv query
 // heads of kv head g, so every cached k, v row is read once per step (the
 // query heads of a group share it), and writes, per query head, the slice's
@@ -72,6 +73,13 @@ constexpr int SPL_MIN_LEN = 32;     // positions per slice at least
 constexpr int SPL_MAX_LEN = 256;    // positions per slice at most (LDS scores)
 constexpr int SPL_MAX_SLICES = 256;
 constexpr int SPL_MAX_REP = 8;
+
+// The slices that can ever hold positions: len >= SPL_MIN_LEN, so ns <=
+// ceil(max_seq / SPL_MIN_LEN) (and ns <= S) at every position.
+__host__ __device__ __forceinline__ int split_max_slices(int S, int max_seq) {
+    const int c = (max_seq + SPL_MIN_LEN - 1) / SPL_MIN_LEN;
+    return c < S ? c : S;
+}
 
 // the slice length and the number of slices that hold positions, for n = pos + 1
 __device__ __forceinline__ void split_shape(int n, int S, int &len, int &ns) {
@@ -270,16 +278,17 @@ __global__ __launch_bounds__(64) void attn_combine_kernel(const float *__restric
     __shared__ float w[SPL_MAX_SLICES];
     const int h = blockIdx.x, kvh = h / REP, hh = h % REP, lane = threadIdx.x;
     const float *pk = part + (int64_t)kvh * S * PSTR;
+    const int smax = split_max_slices(S, max_seq);  // no record past it is ever used
     float ov[CS][DL], mv[MU], lv[MU];
 #pragma unroll
     for (int s2 = 0; s2 < CS; s2++)
 #pragma unroll
-        for (int e = 0; e < DL; e++) ov[s2][e] = s2 < S ? pk[(int64_t)s2 * PSTR + hh * hd + lane + 64 * e] : 0.0f;
+        for (int e = 0; e < DL; e++) ov[s2][e] = s2 < smax ? pk[(int64_t)s2 * PSTR + hh * hd + lane + 64 * e] : 0.0f;
 #pragma unroll
     for (int u = 0; u < MU; u++) {
         const int s2 = lane + 64 * u;
-        mv[u] = s2 < S ? pk[(int64_t)s2 * PSTR + REP * hd + hh] : 0.0f;
-        lv[u] = s2 < S ? pk[(int64_t)s2 * PSTR + REP * hd + SPL_MAX_REP + hh] : 0.0f;
+        mv[u] = s2 < smax ? pk[(int64_t)s2 * PSTR + REP * hd + hh] : 0.0f;
+        lv[u] = s2 < smax ? pk[(int64_t)s2 * PSTR + REP * hd + SPL_MAX_REP + hh] : 0.0f;
     }
     const int pos = (int)*d_pos;
     if (pos < 0 || pos >= max_seq) return;
@@ -543,7 +552,8 @@ hipError_t launch_attn_split(const float *qk, const float *v, const float *cosb,
     if ((hd != 64 && hd != 128) || (rep != 1 && rep != 2 && rep != 4 && rep != 8)) return hipErrorNotSupported;
     const int S = attn_split_slices(n_kv, max_seq);
     if (S == 0 || attn_split_workspace_bytes(n_head, n_kv, hd, max_seq) > part_bytes) return hipErrorNotSupported;
-    const dim3 grid((unsigned)S, (unsigned)n_kv);
+    // slices past split_max_slices never hold a position: no workgroup for them
+    const dim3 grid((unsigned)split_max_slices(S, (int)max_seq), (unsigned)n_kv);
     const int nh = (int)n_head, ms = (int)max_seq;
 #define AQ_SPLIT(H4, R) launch_split<H4, R>(grid, qk, v, cosb, sinb, d_pos, kc, vc, nh, ms, S, part, out, s)
     if (hd == 64) {
