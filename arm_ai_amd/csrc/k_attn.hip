@@ -56,8 +56,8 @@ constexpr float4 ZERO4 = {0.0f, 0.0f, 0.0f, 0.0f};
 // ------------------------------------------------------------------ decode
 // Two launches.  attn_split_kernel: grid (slices, n_kv kv heads), 256
 // threads, for the S slices of the workspace or, when max_seq is shorter,
-// the ceil(max_seq / 32) that can ever hold positions.  Workgroup (s, g) takes the positions [s*len, (s+1)*len) of
-// 0..pos (len = max(32, ceil((pos+1)/S))) for all REP = n_head / n_kv query
+// the ceil(max_seq / 16) that can ever hold positions.  Workgroup (s, g) takes the positions [s*len, (s+1)*len) of
+// 0..pos (len = max(16, ceil((pos+1)/S))) for all REP = n_head / n_kv query
 // heads of kv head g, so every cached k, v row is read once per step (the
 // query heads of a group share it), and writes, per query head, the slice's
 // max score m, the sum l of e^(score - m) and the unnormalised o = sum of
@@ -69,7 +69,8 @@ constexpr float4 ZERO4 = {0.0f, 0.0f, 0.0f, 0.0f};
 // its device-scope release and the counter atomics of 256 workgroups cost
 // more than the second launch.)
 constexpr int SPL_THREADS = 256;
-constexpr int SPL_MIN_LEN = 32;     // positions per slice at least
+constexpr int SPL_MIN_LEN = 16;     // positions per slice at least (slices of 16 measured faster than 32:
+                                    // more, shorter workgroups on the latency-bound step)
 constexpr int SPL_MAX_LEN = 256;    // positions per slice at most (LDS scores)
 constexpr int SPL_MAX_SLICES = 256;
 constexpr int SPL_MAX_REP = 8;
@@ -100,6 +101,8 @@ __global__ __launch_bounds__(SPL_THREADS) void attn_split_kernel(
     constexpr int RPP = RPI * (SPL_THREADS / 64);    // key rows per workgroup pass
     constexpr int KU = SPL_MIN_LEN / RPP;            // key passes loaded at the start (a whole minimum slice)
     constexpr int VU = SPL_MIN_LEN / G;              // value rows per thread loaded at the start
+    static_assert(KU >= 1 && KU * RPP == SPL_MIN_LEN && VU >= 1 && VU * G == SPL_MIN_LEN,
+                  "a minimum slice is whole key passes and whole value rounds");
     __shared__ __align__(16) float qs[REP * hd];
     __shared__ __align__(16) float ks[hd];
     __shared__ __align__(16) float vs[hd];

@@ -90,11 +90,11 @@ def _decode_call(torch, lib, ctx, n_head, n_kv, hd, max_seq, kc, vc, qk, v, pos,
 @pytest.mark.parametrize(
     "n_head,n_kv,hd,max_seq,positions",
     [
-        # TinyLlama heads: slices of at least 32 positions, 64 slices of 4 kv heads
+        # TinyLlama heads: slices of at least 16 positions, 64 slices of 4 kv heads
         (32, 4, 64, 1024, [0, 1, 31, 32, 33, 63, 64, 600, 1023]),
-        # max_seq not a multiple of 32: 19 slices can hold positions, the last from 576
-        (32, 4, 64, 600, [0, 31, 32, 575, 576, 599]),
-        (32, 4, 64, 8192, [8191, 2048, 2049, 4097]),  # slices longer than 32 (8192 / 64 = 128 per slice)
+        # max_seq not a multiple of 16: 38 slices can hold positions, the last from 592
+        (32, 4, 64, 600, [0, 15, 16, 591, 592, 599]),
+        (32, 4, 64, 8192, [8191, 2048, 2049, 4097]),  # slices longer than 16 (8192 / 64 = 128 per slice)
         (32, 8, 128, 2048, [0, 63, 64, 511, 512, 2047]),  # Llama-3-8B heads: 4 per kv head, 32 slices
         (8, 4, 64, 512, [0, 100, 511]),  # 2 per kv head
         (8, 8, 128, 512, [0, 5, 300]),   # one query head per kv head
