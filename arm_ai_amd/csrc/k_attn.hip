@@ -146,21 +146,23 @@ __global__ __launch_bounds__(SPL_THREADS) void attn_split_kernel(
         qs[hh * hd + 2 * j] = a * cc - b * sn;
         qs[hh * hd + 2 * j + 1] = a * sn + b * cc;
     }
-    if (has_pos) {
+    if (has_pos) {  // k's hd / 2 rotated pairs, then v's hd values
         const float *k0 = qk + (int64_t)n_head * hd + (int64_t)kvh * hd;
-        if (tid < hd / 2) {
-            const float a = k0[2 * tid], b = k0[2 * tid + 1], cc = cr[tid], sn = sr[tid];
-            ks[2 * tid] = a * cc - b * sn;
-            ks[2 * tid + 1] = a * sn + b * cc;
-        } else if (tid >= 128 && tid < 128 + hd) {
-            vs[tid - 128] = v[(int64_t)kvh * hd + tid - 128];
+        for (int t = tid; t < hd / 2 + hd; t += SPL_THREADS) {
+            if (t < hd / 2) {
+                const float a = k0[2 * t], b = k0[2 * t + 1], cc = cr[t], sn = sr[t];
+                ks[2 * t] = a * cc - b * sn;
+                ks[2 * t + 1] = a * sn + b * cc;
+            } else {
+                vs[t - hd / 2] = v[(int64_t)kvh * hd + t - hd / 2];
+            }
         }
     }
     __syncthreads();
     if (has_pos) {
-        if (tid < hd) {
-            kh[(int64_t)pos * hd + tid] = ks[tid];
-            vh[(int64_t)pos * hd + tid] = vs[tid];
+        for (int t = tid; t < hd; t += SPL_THREADS) {
+            kh[(int64_t)pos * hd + t] = ks[t];
+            vh[(int64_t)pos * hd + t] = vs[t];
         }
 #pragma unroll
         for (int u = 0; u < KU; u++)
