@@ -709,9 +709,9 @@ hipError_t launch_type(const RlParams &p, int64_t n, int ng, bool wide, bool fus
     // 16 rows: as many wavefronts as four groups each need (every lane one
     // group); the quantising wavefronts (four blocks each) are then always
     // enough.  Up to 32 groups all of a lane's pieces are in flight from the
-    // start; with 16 wavefronts (ffn_down, 56 groups) six (seven for Q6_K),
-    // the first issued before the quantisation and the rest after it,
-    // measured fastest.
+    // start; with 16 wavefronts (ffn_down, 56 groups) six (seven for the
+    // 11- and 13-piece types), the first issued before the quantisation and
+    // the rest after it, measured fastest.
     if (rows8(n, ng)) {
         // 8 rows: a wavefront covers eight groups, and there are as many
         // wavefronts as the quantisation needs (four blocks each)
@@ -725,7 +725,7 @@ hipError_t launch_type(const RlParams &p, int64_t n, int ng, bool wide, bool fus
     if (ng <= 16) return launch_g<TYPE, RG_ROWS, 4, 1, NPG, true>(p, grid, fused, dump, s);
     if (ng <= 32) return launch_g<TYPE, RG_ROWS, 8, 1, NPG, true>(p, grid, fused, dump, s);
     if constexpr (Q80) return hipErrorNotSupported;  // Q8_0: up to 32 groups
-    else return launch_g<TYPE, RG_ROWS, 16, 1, Q6 ? 7 : 6, false>(p, grid, fused, dump, s);
+    else return launch_g<TYPE, RG_ROWS, 16, 1, Q6 || NPG == 11 ? 7 : 6, false>(p, grid, fused, dump, s);
 }
 
 }  // namespace
