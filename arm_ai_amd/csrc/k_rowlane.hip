@@ -7,7 +7,7 @@
 // of every block are exact; only the f32 combination order differs from
 // candle's vec_dot_unopt.
 //
-// Mapping.  A workgroup (W = 16 wavefronts) owns 56 consecutive weight rows (seven
+// Mapping.  A workgroup (W = 16 wavefronts; 8 for rows of up to 8 groups) owns 56 consecutive weight rows (seven
 // 8-row blocks of the row-block tile layout, so every CU of a 256-CU GPU gets
 // the same bytes at the headline shape, Q4_K 14336 x 4096).  Lane l of every
 // wavefront is row row0 + l (lanes 56..63 are idle); wavefront w takes the
@@ -699,9 +699,14 @@ hipError_t launch_type(const RlParams &p, int64_t n, int ng, bool wide, bool fus
     if constexpr (!Q80) if (wide) {
         const int64_t nch = (n + RL_ROWS - 1) / RL_ROWS;
         // more chunks than CUs: persistent workgroups, one per CU
+        // (one wavefront per group: 8 wavefronts for up to 8 groups, where
+        //  the other 8 of 16 would only wait)
+        if (ng <= 8 && nch > RL_PERSIST_CUS)
+            return launch_g<TYPE, RL_ROWS, 8, 1, NPG, true, true>(p, RL_PERSIST_CUS, fused, dump, s);
         if (ng <= 16 && nch > RL_PERSIST_CUS)
             return launch_g<TYPE, RL_ROWS, 16, 1, NPG, true, true>(p, RL_PERSIST_CUS, fused, dump, s);
         const unsigned grid = (unsigned)nch;
+        if (ng <= 8) return launch_g<TYPE, RL_ROWS, 8, 1, Q6 ? 8 : NPG == 11 ? 7 : 6, true>(p, grid, fused, dump, s);
         if (ng <= 16) return launch_g<TYPE, RL_ROWS, 16, 1, Q6 ? 8 : NPG == 11 ? 7 : 6, true>(p, grid, fused, dump, s);
         if constexpr (!Q6) return launch_g<TYPE, RL_ROWS, 16, 2, 12, true>(p, grid, fused, dump, s);
         return hipErrorNotSupported;
