@@ -144,7 +144,9 @@ __device__ __forceinline__ void rl_body(const RlParams p, const int bid, const i
         c.row = row0 + rl;
         c.rok = rl < R && c.row < p.n;
         const int rb0 = row0 / RB;
-        const int rbs = min(R / RB, nrb - rb0);
+        // (a chunk past the rows, which no launch here makes: an empty
+        //  range, so that every load of it reads zeros)
+        const int rbs = max(0, min(R / RB, nrb - rb0));
         c.rw = buf_rsrc(p.w + (int64_t)rb0 * p.rb_stride, (uint32_t)(rbs * p.rb_stride));
         c.lbase = c.rok ? (uint32_t)((rl / RB) * p.rb_stride + (rl % RB) * 16) : BUF_OOB;
         c.rwd = buf_rsrc(DP ? (const uint8_t *)p.wd + (int64_t)rb0 * p.ng * RB * DB : nullptr,
