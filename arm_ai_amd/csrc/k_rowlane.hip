@@ -717,9 +717,9 @@ hipError_t launch_type(const RlParams &p, int64_t n, int ng, bool wide, bool fus
     // group; two for up to 8 groups, where a third and fourth wavefront
     // would only quantise and wait: 7 % faster at 5632 x 2048); the
     // quantising wavefronts (four blocks each) are then always enough.  Up to 32 groups all of a lane's pieces are in flight from the
-    // start; with 16 wavefronts (ffn_down, 56 groups) six (seven for the
-    // 11- and 13-piece types), the first issued before the quantisation and
-    // the rest after it, measured fastest.
+    // start; with 12-16 wavefronts (ffn_down, 56 groups: 14) six (seven for
+    // the 11- and 13-piece types), the first issued before the quantisation
+    // and the rest after it, measured fastest.
     if (rows8(n, ng)) {
         // 8 rows: a wavefront covers eight groups, and there are as many
         // wavefronts as the quantisation needs (four blocks each)
@@ -734,7 +734,12 @@ hipError_t launch_type(const RlParams &p, int64_t n, int ng, bool wide, bool fus
     if (ng <= 16) return launch_g<TYPE, RG_ROWS, 4, 1, NPG, true>(p, grid, fused, dump, s);
     if (ng <= 32) return launch_g<TYPE, RG_ROWS, 8, 1, NPG, true>(p, grid, fused, dump, s);
     if constexpr (Q80) return hipErrorNotSupported;  // Q8_0: up to 32 groups
-    else return launch_g<TYPE, RG_ROWS, 16, 1, Q6 || NPG == 11 ? 7 : 6, false>(p, grid, fused, dump, s);
+    else {  // as many wavefronts as the groups need (four each): none only waits
+        constexpr int PW = Q6 || NPG == 11 ? 7 : 6;
+        if (ng <= 48) return launch_g<TYPE, RG_ROWS, 12, 1, PW, false>(p, grid, fused, dump, s);
+        if (ng <= 56) return launch_g<TYPE, RG_ROWS, 14, 1, PW, false>(p, grid, fused, dump, s);
+        return launch_g<TYPE, RG_ROWS, 16, 1, PW, false>(p, grid, fused, dump, s);
+    }
 }
 
 }  // namespace
