@@ -552,7 +552,7 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: the quantized-matmul path runs on a single MI355X "
-              "(multi-GPU sharding is described in DESIGN.md, not run). Use --gpus 1.", file=sys.stderr)
+              "(it would shard by weight rows, one slice per GPU; not run here). Use --gpus 1.", file=sys.stderr)
         return 2
     if args.steps < 1:
         print("--steps must be >= 1", file=sys.stderr)

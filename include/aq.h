@@ -12,7 +12,8 @@
  *   candle-core 0.8.4 QuantizedType::matmul_t((m,k,n), lhs, dst) -> k_quants::matmul<T>
  * (candle-core is pinned by native/arm_ai_nif/Cargo.lock; it is a registry
  * crate and not vendored).  A Rust caller binds these functions with
- * `extern "C"` declarations; the binding is spelled out in INTEGRATION.md.
+ * `extern "C"` declarations of the same names and argument types
+ * (native/arm_ai_nif/src/aq_sys.rs holds them).
  *
  * Conventions
  *  - Every function returns an aq_status (0 = AQ_OK, negative = error) and
