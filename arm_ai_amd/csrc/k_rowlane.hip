@@ -40,22 +40,18 @@
 // wavefronts.  From 1025 to 2048 rows, 8-row workgroups (eight group phases)
 // fill the CUs instead.
 #include "aq_internal.h"
+#include "rl_plan.h"
 
 namespace aq {
 
 namespace {
 
-constexpr int RL_ROWS = 56;    // weight rows per workgroup (one row per lane)
-constexpr int RL_MAXG = 64;    // groups per row (k <= 16384)
-constexpr int RL_MIN_N = 200 * RL_ROWS;  // rows from which 56-row workgroups are used (up to 32 groups)
-constexpr int RG_ROWS = 16;    // weight rows per workgroup of the four-group-phase form
-constexpr int RG_MIN_N = 16 * RG_ROWS;   // rows from which that form is used (up to 64 groups)
-constexpr int RE_ROWS = 8;     // weight rows per workgroup of the eight-group-phase form
-// ... used from 1025 to 2048 rows (up to 32 groups): at most one 8-row
-// workgroup per CU, where 16-row workgroups would leave half the CUs idle
-constexpr int RE_MIN_N = 64 * RG_ROWS + 1, RE_MAX_N = 256 * RE_ROWS;
-constexpr int RL_PERSIST_CUS = 256;      // the persistent grid: one workgroup per CU
-constexpr int RL_NORM_MAXG = 32;         // the fused norm: rows of up to 8192 elements (as the general matvec)
+constexpr int RL_ROWS = rl::ROWS56;    // weight rows per workgroup (one row per lane)
+constexpr int RL_MAXG = rl::MAXG;      // groups per row (k <= 16384)
+constexpr int RG_ROWS = rl::ROWS16;    // weight rows per workgroup of the four-group-phase form
+constexpr int RG_MIN_N = rl::MIN_N16;  // rows from which that form is used (up to 64 groups)
+constexpr int RE_ROWS = rl::ROWS8;     // weight rows per workgroup of the eight-group-phase form
+constexpr int RL_NORM_MAXG = rl::NORM_MAXG;  // the fused norm: rows of up to 8192 elements (as the general matvec)
 
 struct RlParams {
     const uint8_t *w;  // row-block tiles
@@ -144,8 +140,10 @@ __device__ __forceinline__ void rl_body(const RlParams p, const int bid, const i
         c.row = row0 + rl;
         c.rok = rl < R && c.row < p.n;
         const int rb0 = row0 / RB;
-        // (a chunk past the rows, which no launch here makes: an empty
-        //  range, so that every load of it reads zeros)
+        // (a chunk past the rows -- which the host check rl::grid_ok
+        //  keeps any launch from making -- gets an empty range, so that
+        //  every load of it reads zeros: a grid larger than the chunk count
+        //  would otherwise wrap rbs * rb_stride to a 4 GB range)
         const int rbs = max(0, min(R / RB, nrb - rb0));
         c.rw = buf_rsrc(p.w + (int64_t)rb0 * p.rb_stride, (uint32_t)(rbs * p.rb_stride));
         c.lbase = c.rok ? (uint32_t)((rl / RB) * p.rb_stride + (rl % RB) * 16) : BUF_OOB;
@@ -665,6 +663,9 @@ __global__ __launch_bounds__(W * 64) void rl2_kernel(RlParams p1, RlParams p2, i
 
 template <int TYPE, int R, int W, int GPW, int P, bool EARLY, bool CH = false>
 hipError_t launch_g(const RlParams &p, unsigned grid, bool fused, bool dump, hipStream_t s) {
+    // one workgroup per chunk (persistent: at most one per chunk), never a
+    // workgroup past the weight's rows
+    if (!rl::grid_ok(R, p.n, grid, CH)) return hipErrorInvalidValue;
     if (p.xf == RL_XF_NORM) {  // input transforms: f32 input, no dump (the caller checks)
         rl_kernel<TYPE, R, W, GPW, P, EARLY, true, false, CH, RL_XF_NORM><<<grid, W * 64, 0, s>>>(p);
         return hipGetLastError();
@@ -683,13 +684,8 @@ hipError_t launch_g(const RlParams &p, unsigned grid, bool fused, bool dump, hip
     return hipGetLastError();
 }
 
-// 56-row workgroups: up to two Q4_K groups per wavefront (32 groups); one
-// Q6_K group (16; two kept 13-piece walks too many registers live)
-bool rows56(int type, int64_t n, int ng) {
-    return type != TYPE_Q8_0 && ng <= (type == TYPE_Q6_K ? 16 : 32) && n >= RL_MIN_N;
-}
-// 8-row workgroups (otherwise 16 rows), for a shape that is not rows56
-bool rows8(int64_t n, int ng) { return ng <= 32 && n >= RE_MIN_N && n <= RE_MAX_N; }
+bool rows56(int type, int64_t n, int ng) { return rl::wide(type == TYPE_Q6_K, type == TYPE_Q8_0, n, ng); }
+bool rows8(int64_t n, int ng) { return rl::narrow8(n, ng); }
 
 // The launch shapes of one weight type (pieces in flight: P; 16 wavefronts
 // with six Q4_K pieces in flight measured fastest at the headline, one group
@@ -698,16 +694,14 @@ template <int TYPE>
 hipError_t launch_type(const RlParams &p, int64_t n, int ng, bool wide, bool fused, bool dump, hipStream_t s) {
     constexpr bool Q6 = TYPE == TYPE_Q6_K, Q80 = TYPE == TYPE_Q8_0;
     constexpr int NPG = slabs_of(TYPE);  // 9 (Q4_K, Q4_0), 11 (Q5_K, Q5_0), 13 (Q6_K), 17 (Q8_0)
+    const rl::Plan pl = rl::plan(Q6, Q80, n, ng);
+    const unsigned grid = pl.grid;
     if constexpr (!Q80) if (wide) {
-        const int64_t nch = (n + RL_ROWS - 1) / RL_ROWS;
         // more chunks than CUs: persistent workgroups, one per CU
         // (one wavefront per group: 8 wavefronts for up to 8 groups, where
         //  the other 8 of 16 would only wait)
-        if (ng <= 8 && nch > RL_PERSIST_CUS)
-            return launch_g<TYPE, RL_ROWS, 8, 1, NPG, true, true>(p, RL_PERSIST_CUS, fused, dump, s);
-        if (ng <= 16 && nch > RL_PERSIST_CUS)
-            return launch_g<TYPE, RL_ROWS, 16, 1, NPG, true, true>(p, RL_PERSIST_CUS, fused, dump, s);
-        const unsigned grid = (unsigned)nch;
+        if (ng <= 8 && pl.persistent) return launch_g<TYPE, RL_ROWS, 8, 1, NPG, true, true>(p, grid, fused, dump, s);
+        if (ng <= 16 && pl.persistent) return launch_g<TYPE, RL_ROWS, 16, 1, NPG, true, true>(p, grid, fused, dump, s);
         if (ng <= 8) return launch_g<TYPE, RL_ROWS, 8, 1, Q6 ? 8 : NPG == 11 ? 7 : 6, true>(p, grid, fused, dump, s);
         if (ng <= 16) return launch_g<TYPE, RL_ROWS, 16, 1, Q6 ? 8 : NPG == 11 ? 7 : 6, true>(p, grid, fused, dump, s);
         if constexpr (!Q6) return launch_g<TYPE, RL_ROWS, 16, 2, 12, true>(p, grid, fused, dump, s);
@@ -720,16 +714,14 @@ hipError_t launch_type(const RlParams &p, int64_t n, int ng, bool wide, bool fus
     // start; with 12-16 wavefronts (ffn_down, 56 groups: 14) six (seven for
     // the 11- and 13-piece types), the first issued before the quantisation
     // and the rest after it, measured fastest.
-    if (rows8(n, ng)) {
+    if (pl.rows == RE_ROWS) {
         // 8 rows: a wavefront covers eight groups, and there are as many
         // wavefronts as the quantisation needs (four blocks each)
-        const unsigned g8 = (unsigned)((n + RE_ROWS - 1) / RE_ROWS);
-        if (ng <= 8) return launch_g<TYPE, RE_ROWS, 2, 1, NPG, true>(p, g8, fused, dump, s);
-        if (ng <= 16) return launch_g<TYPE, RE_ROWS, 4, 1, NPG, true>(p, g8, fused, dump, s);
-        if (ng <= 24) return launch_g<TYPE, RE_ROWS, 6, 1, NPG, true>(p, g8, fused, dump, s);
-        return launch_g<TYPE, RE_ROWS, 8, 1, NPG, true>(p, g8, fused, dump, s);
+        if (ng <= 8) return launch_g<TYPE, RE_ROWS, 2, 1, NPG, true>(p, grid, fused, dump, s);
+        if (ng <= 16) return launch_g<TYPE, RE_ROWS, 4, 1, NPG, true>(p, grid, fused, dump, s);
+        if (ng <= 24) return launch_g<TYPE, RE_ROWS, 6, 1, NPG, true>(p, grid, fused, dump, s);
+        return launch_g<TYPE, RE_ROWS, 8, 1, NPG, true>(p, grid, fused, dump, s);
     }
-    const unsigned grid = (unsigned)((n + RG_ROWS - 1) / RG_ROWS);
     if (ng <= 8) return launch_g<TYPE, RG_ROWS, 2, 1, NPG, true>(p, grid, fused, dump, s);
     if (ng <= 16) return launch_g<TYPE, RG_ROWS, 4, 1, NPG, true>(p, grid, fused, dump, s);
     if (ng <= 32) return launch_g<TYPE, RG_ROWS, 8, 1, NPG, true>(p, grid, fused, dump, s);
@@ -793,6 +785,7 @@ hipError_t rl_params(const WLayout &w, int64_t n, int64_t k, const float *x, con
 
 template <int T1, int T2, int R, int W>
 hipError_t launch_two_rl(const RlParams &p1, const RlParams &p2, int g1, int g2, int kind, hipStream_t s) {
+    if (!rl::grid_ok(R, p1.n, g1, false) || !rl::grid_ok(R, p2.n, g2, false)) return hipErrorInvalidValue;
     if (kind == RL_XF_NORM) rl2_kernel<T1, T2, R, W, RL_XF_NORM><<<g1 + g2, W * 64, 0, s>>>(p1, p2, g1);
     else if (kind == RL_XF_SILU) rl2_kernel<T1, T2, R, W, RL_XF_SILU><<<g1 + g2, W * 64, 0, s>>>(p1, p2, g1);
     else rl2_kernel<T1, T2, R, W, RL_XF_NONE><<<g1 + g2, W * 64, 0, s>>>(p1, p2, g1);
