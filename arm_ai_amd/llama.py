@@ -485,18 +485,27 @@ class Llama:
         return int(logits.argmax().item())
 
     def generate(self, prompt: list[int], max_new: int, stop_tokens=(), graph: bool = False,
-                 chunk: int = 16) -> GenerateResult:
+                 chunk: int = 16, on_token=None) -> GenerateResult:
         """generate_greedy (llama_candle.rs:58-139): prefill at offset 0, then one
         forward per new token; stops after emitting a stop token (kept in the output).
 
         With graph=True the captured step is replayed `chunk` times back to back
         (each replay feeds the next from device memory), then the chunk's tokens
         are read and checked for a stop token; tokens after the first stop token
-        are dropped, so the output is the same as stepping one token at a time."""
+        are dropped, so the output is the same as stepping one token at a time.
+
+        on_token: called with each token as soon as it is chosen, in order --
+        the streaming form (llama_candle_stream_op's {:llama_token, id},
+        native/arm_ai_nif/src/lib.rs:1682-1699).  With graph=True it sets the
+        chunk to one: one replay, one token read back, the callback, then the
+        next replay (native/arm_ai_nif/src/gpu_llama.rs generate_greedy_with)."""
         if max_new == 0 or len(prompt) == 0:
             return GenerateResult([], 0, 0)
         if len(prompt) + max_new - 1 > self.cfg.max_seq:
             raise ValueError("prompt + max_new exceeds max_seq")
+        if on_token is not None:
+            chunk = 1
+        emit = on_token if on_token is not None else (lambda _t: None)
         if graph and self._graph is None:
             self._capture()
         self.ctx.synchronize()
@@ -505,6 +514,7 @@ class Llama:
         nxt = self.argmax_first(logits)  # .item() synchronises
         prefill_us = int((time.perf_counter() - t0) * 1e6)
         generated = [nxt]
+        emit(nxt)
         t1 = time.perf_counter()
         offset = len(prompt)
         if graph and max_new > 1 and nxt not in stop_tokens:
@@ -521,6 +531,7 @@ class Llama:
                     toks = self._hist[offset:offset + n].tolist()  # copies on the stream, then synchronises
                 for t in toks:
                     generated.append(int(t))
+                    emit(int(t))
                     if t in stop_tokens:
                         done = True
                         break
@@ -532,6 +543,7 @@ class Llama:
                     break
                 nxt = self.argmax_first(self.forward([nxt], offset))
                 generated.append(nxt)
+                emit(nxt)
                 offset += 1
         decode_us = int((time.perf_counter() - t1) * 1e6)
         return GenerateResult(generated, prefill_us, decode_us)

@@ -260,3 +260,38 @@ def test_odd_vocab_graph_generate():
     finally:
         model.free()
         ctx.close()
+
+
+@pytest.mark.gpu
+def test_generate_streams_each_token_before_the_next_step(tiny):
+    """generate(..., on_token=cb), the streaming form of llama_candle_stream_op
+    (native/arm_ai_nif/src/lib.rs:1682-1699, gpu_llama.rs generate_greedy_with):
+    the callback fires once per token, in order, with the tokens of the eager
+    generate; with the graph, token j (j >= 1) is delivered after exactly j
+    replays (the device position reads prompt + j when the callback runs), so
+    no step runs ahead of the delivery; a stop token is delivered and ends the
+    stream."""
+    hw, model = tiny
+    prompt = [7, 100, 33, 250, 3, 9]
+    eager = model.generate(prompt, 8).tokens
+    assert len(eager) == 8
+    for graph in (False, True):
+        seen, pos_at = [], []
+
+        def cb(t, graph=graph):
+            seen.append(t)
+            if graph and len(seen) > 1:
+                pos_at.append(int(model._pos.item()))
+
+        res = model.generate(prompt, 8, graph=graph, on_token=cb)
+        assert seen == res.tokens == eager, f"graph={graph}"
+        if graph:
+            assert pos_at == [len(prompt) + j for j in range(1, 8)]
+    stop = eager[3]
+    first = eager.index(stop)
+    seen = []
+    res = model.generate(prompt, 8, stop_tokens=(stop,), graph=True, on_token=seen.append)
+    assert res.tokens == eager[:first + 1] == seen
+    seen = []
+    assert model.generate(prompt, 8, stop_tokens=(eager[0],), graph=True, on_token=seen.append).tokens == eager[:1]
+    assert seen == eager[:1]
