@@ -18,22 +18,32 @@
 // v_mfma_f32_32x32x16_f16: every operand is exact in f16 and every partial
 // sum (<= 16 * 2048 * 63 < 2^24) exact in f32, so Smin is exact too.
 //
-// Tiling.  A workgroup (4 wavefronts) owns a 32*MT (m) x 128 (n) output
-// tile; wavefront w owns columns 32w..32w+31 and all rows (MT 32x32 MFMA
-// tiles), so each weight digit operand it builds is used MT times.  The
-// activation rows of two super-blocks at a time (quants, bsums, d) are copied
-// global -> LDS directly (global_load_lds, no registers), double-buffered, the
-// 16-byte quant chunks of each row XOR-swizzled so that 16 consecutive rows
-// read distinct banks.  Each lane loads its own weight column's pieces (the
-// meta piece and the four quant pieces of its half of the super-block) into
-// registers one stage ahead; in the row-block tile layout the 32 columns of a
-// wavefront's half read 4 full 128-byte lines per instruction.
+// Tiling.  A workgroup (4 wavefronts) owns a 64 (m) x 128 (n) output tile;
+// wavefront w owns columns 32w..32w+31 and both 32-row MFMA tiles, so each
+// weight digit operand it builds feeds two MFMAs.  Two workgroups share a CU
+// (launch bounds 256, 2), so one's VALU work overlaps the other's MFMAs.
+//
+// Data movement, per super-block:
+//   * the activation rows (Q8_K quants, bsums as f16, d) go global -> LDS by
+//     buffer-to-LDS copies (no registers), into a ring of NS stages issued
+//     NS - 1 super-blocks ahead; each row's 16-byte quant chunks are
+//     XOR-swizzled by the row index, so the fragment reads of 16 consecutive
+//     rows hit distinct banks;
+//   * each lane loads its own weight column's pieces (the meta piece and the
+//     four quant pieces of its half of the super-block) straight into
+//     registers, one super-block ahead (two register sets, the loop unrolled
+//     by two); in the row-block tile layout the 32 columns of a half-wavefront
+//     read four full 128-byte lines per load instruction.
+// One explicit wait (this wavefront's copies of the stage and its weight
+// registers) and one barrier start each super-block; the copies in flight
+// for later stages stay outstanding.
+//
 // Work items (tile, k-split) are numbered so that all m-tiles and k-splits of
 // one n-tile run on the same XCD (workgroups are dealt to the 8 XCDs
 // round-robin), where they share that XCD's L2 copy of the weight tile.
 //
-// Split-K.  When there are too few tiles to fill the 256 CUs, the K loop is
-// cut into `splits` ranges of super-blocks.  Each workgroup writes its partial
+// Split-K.  When there are too few tiles to fill the CUs, the K loop is cut
+// into `splits` ranges of super-blocks.  Each workgroup writes its partial
 // tile to the workspace, and a second, small launch (gemm_splitk_reduce)
 // sums every tile's partials in split order and writes y -- so the result
 // does not depend on which workgroup finished first, and no workgroup waits
@@ -52,11 +62,12 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef unsigned short us2 __attribute__((ext_vector_type(2)));
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int GBN = 128;   // columns (n) per workgroup
+constexpr int GBM = 64;    // rows (m) per workgroup: two 32-row MFMA tiles
 constexpr int NXCD = 8;
 constexpr int TARGET_WG = 256;  // split K until there is a work item per CU
+constexpr int NS = 4;           // activation stages in LDS
 
 struct GemmParams {
     const uint8_t *w;  // row-block tiles
@@ -68,49 +79,46 @@ struct GemmParams {
     float *y;
     int m, n, k;
     int ntm, tiles, splits, kbs, items, per_xcd;
-    float *part;   // [tiles][splits][32*MT][GBN] partial sums (splits > 1)
+    float *part;   // [tiles][splits][GBM][GBN] partial sums (splits > 1)
     int32_t *S, *Smin;  // integer dump [m][n][ng] or null
 };
 
+// LDS of one workgroup: NS stages of quants [64 rows][256] (chunk c of row r
+// at chunk c ^ (r & 15)) and bsums [64 rows][16] f16, and NS + 1 slots of d
+// [64 rows] (one more than the stages: the epilogue of super-block i, spread
+// over step i + 1, reads its d after the copies of stage i + NS started).
+struct Lds {
+    static constexpr int QS = GBM * 256;
+    static constexpr int BS = GBM * 32;
+    static constexpr int DS = GBM * 4;
+    static constexpr int ND = NS + 1;
+    static constexpr int Q0 = 0, B0 = NS * QS, D0 = B0 + NS * BS;
+    static constexpr int BYTES = D0 + ND * DS;
+};
+static_assert(2 * Lds::BYTES <= 160 * 1024, "two workgroups per CU");
+
 // bytes b (each <= 15) times s (<= 7), bytewise without carries: two 16-bit
-// lanes per dword (v_pk_mul_lo_u16).
-__device__ __forceinline__ int pkmul(uint32_t x, uint32_t s) {
-    const us2 a = __builtin_bit_cast(us2, x);
-    const us2 r = a * (us2){(unsigned short)s, (unsigned short)s};
+// lanes per dword (v_pk_mul_lo_u16); m holds s in both 16-bit halves.
+__device__ __forceinline__ int pkmul(uint32_t x, uint32_t m) {
+    const us2 r = __builtin_bit_cast(us2, x) * __builtin_bit_cast(us2, m);
     return (int)__builtin_bit_cast(uint32_t, r);
 }
+// byte b of w in both 16-bit halves (v_perm_b32; selector 0x0c gives 0)
+__device__ __forceinline__ uint32_t bcast_byte16(uint32_t w, int b) {
+    return __builtin_amdgcn_perm(w, w, 0x0c000c00u | (uint32_t)b | ((uint32_t)b << 16));
+}
+// f16 pair (v, v) for byte b (<= 63) of w: bytes (v, 0x64) are 1024 + v as
+// f16, exact, and the packed add of -1024 leaves v exactly.
+__device__ __forceinline__ uint32_t f16pair_of_byte(uint32_t w, int b) {
+    const uint32_t t = __builtin_amdgcn_perm(0x64646464u, w, 0x04000400u | (uint32_t)b | ((uint32_t)b << 16));
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    const h2 r = __builtin_bit_cast(h2, t) + (h2){(_Float16)-1024.0f, (_Float16)-1024.0f};
+    return __builtin_bit_cast(uint32_t, r);
+}
 
-// LDS of one workgroup (a tile of 32*MT rows x GBN columns):
-//   two main stages, one super-block each:
-//     quants [rows][256] i8, 16-byte chunk c of row r at chunk c ^ (r & 15), so
-//       the 16-byte reads of 16 consecutive rows hit distinct banks;
-//     weight pieces [9][GBN columns][16 B] (piece 0: d, dmin, scales; 1..8:
-//       qs), each piece padded by 64 B so the half-wavefronts' reads of pieces
-//       1 + 2c and 2 + 2c start on different banks;
-//   three small stages (a ring), one super-block each:
-//     bsums [rows][16] as f16;
-//     d: one 256-byte slot per 32 rows, row 32s + i at slot s entry i (entries
-//       32..63 receive duplicates).
-// The ring is one stage deeper than the main stages because the f32 epilogue
-// of super-block b runs during step b + 1, after the copies for b + 2 started.
-template <int MT>
-struct TileLds {
-    static constexpr int ROWS = 32 * MT;
-    static constexpr int QS = ROWS * 256;
-    static constexpr int BP = GBN * 16 + 64;
-    static constexpr int MAIN = QS + 9 * BP;  // one main stage; weights at QS
-    static constexpr int BS = ROWS * 32, DS = MT * 256;
-    static constexpr int SMALL = BS + DS;     // one ring stage; d at BS
-    static constexpr int RING0 = 2 * MAIN;
-    static constexpr int BYTES = RING0 + 3 * SMALL;
-};
-
-template <int MT, bool DUMP>
-__global__ __launch_bounds__(256, 2) void gemm_q4k_kernel(GemmParams p) {
-    static_assert(MT == 2, "the epilogue is spread as one (tile, 4-row group) part per sub-block");
-    constexpr int GBM = 32 * MT;
-    using TL = TileLds<MT>;
-    __shared__ __align__(16) uint8_t lds[TL::BYTES];
+template <bool DUMP>
+__global__ __launch_bounds__(256, DUMP ? 1 : 2) void gemm_q4k_kernel(GemmParams p) {
+    __shared__ __align__(16) uint8_t lds[Lds::BYTES];
 
     // workgroup -> (tile, split): contiguous ranges per XCD, m-tiles then splits fastest
     const int xcd = blockIdx.x % NXCD, local = blockIdx.x / NXCD;
@@ -120,7 +128,7 @@ __global__ __launch_bounds__(256, 2) void gemm_q4k_kernel(GemmParams p) {
     const int tn = tile / p.ntm, tm = tile - tn * p.ntm;
     const int m0 = tm * GBM;
     const int kb0 = split * p.kbs;
-    const int kb1 = min(p.ng, kb0 + p.kbs);
+    const int nit = min(p.ng, kb0 + p.kbs) - kb0;
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -130,7 +138,7 @@ __global__ __launch_bounds__(256, 2) void gemm_q4k_kernel(GemmParams p) {
     const bool col_ok = col < p.n;
     const int ng = p.ng, k = p.k;
 
-    // ---- the copies: raw buffer loads into LDS through wave-uniform
+    // ---- copies and weight loads: raw buffer accesses through wave-uniform
     // descriptors; per-lane offsets are fixed for the whole K loop and the
     // super-block advances the scalar offset only.  Activation rows past m and
     // weight columns past n fall outside the descriptors' ranges and read
@@ -141,122 +149,113 @@ __global__ __launch_bounds__(256, 2) void gemm_q4k_kernel(GemmParams p) {
     const int nrb = (p.n + RB - 1) / RB;
     const int rb_here = min(16, nrb - 16 * tn);  // row blocks (8 columns each) of this n-tile
     const rsrc_t rw = buf_rsrc(p.w + (int64_t)16 * tn * p.rb_stride, (uint32_t)(rb_here * p.rb_stride));
-    uint32_t qoff[2 * MT];
+    uint32_t qoff[4];  // wave w copies rows 16w..16w+15, four rows per instruction
 #pragma unroll
-    for (int i = 0; i < 2 * MT; i++) {
-        const int r = 4 * (2 * MT * wave + i) + (lane >> 4), cp = lane & 15;
+    for (int i = 0; i < 4; i++) {
+        const int r = 4 * (4 * wave + i) + (lane >> 4), cp = lane & 15;
         qoff[i] = (uint32_t)((m0 + r) * k + 16 * (cp ^ (r & 15)));
     }
-    const int s32 = wave % MT;  // 32-row slice this wave copies bsums and d for (waves < MT)
-    const uint32_t bsoff = (uint32_t)(((m0 + 32 * s32 + (lane >> 1)) * (k / 16) + 8 * (lane & 1)) * 2);
-    const uint32_t dxoff = (uint32_t)((m0 + 32 * s32 + (lane & 31)) * ng * 4);
-    // weight copy (piece, half): lane L loads the 16 bytes of column 64*half + L,
-    // i.e. row (L % 8) of this n-tile's row block 8*half + L/8
-    const uint32_t woff0 = (uint32_t)((lane >> 3) * p.rb_stride + (lane & 7) * 16);
-    const uint32_t woff1 = woff0 + (uint32_t)(8 * p.rb_stride);
+    // waves 0, 1: bsums of rows 32w..32w+31 (32 B a row, two lanes each); waves 2 and 3 both
+    // copy the d of the 64 rows (the same bytes to the same place), so every
+    // wavefront issues the same number of loads per step
+    const uint32_t bsoff = (uint32_t)(((m0 + 32 * (wave & 1) + (lane >> 1)) * (k / 16) + 8 * (lane & 1)) * 2);
+    const uint32_t dxoff = (uint32_t)((m0 + lane) * ng * 4);
+    // weights: this lane's column is row l32 % 8 of row block 4w + l32 / 8;
+    // piece 0 (d, dmin, scales) and quant pieces 1 + 2c + h, c = 0..3
+    const uint32_t woff = (uint32_t)((4 * wave + (l32 >> 3)) * p.rb_stride + (l32 & 7) * 16);
+    const uint32_t wqoff = woff + 128u * (1 + h);
 
-    auto issue = [&](uint8_t *main, uint8_t *ring, int b) {
+    // A step issues its loads whether or not super-block kb0 + i exists, so
+    // every step waits on the same counts; past the last one every lane's
+    // offset is BUF_OOB (the range check covers the per-lane offset, not the
+    // scalar one), so those loads read zeros without touching memory.
+    auto issue_act = [&](int i) {  // super-block kb0 + i into stage i % NS, its d into slot i % ND
+        const int b = kb0 + i;
+        const bool live = i < nit;
+        uint8_t *q = lds + Lds::Q0 + (i % NS) * Lds::QS;
 #pragma unroll
-        for (int i = 0; i < 2 * MT; i++) buf_to_lds16(rq, main + 1024 * (2 * MT * wave + i), qoff[i], b * QK_K);
-        if (wave < MT) {  // wave-uniform
-            buf_to_lds16(rbs, ring + 1024 * s32, bsoff, b * 32);
-            buf_to_lds4(rdx, ring + TL::BS + 256 * s32, dxoff, b * 4);
-        }
-        for (int c = wave; c < 18; c += 4) {  // wave-uniform
-            const int piece = c >> 1, half = c & 1;
-            buf_to_lds16(rw, main + TL::QS + piece * TL::BP + 1024 * half, half ? woff1 : woff0, (b * 9 + piece) * 128);
-        }
+        for (int c = 0; c < 4; c++) buf_to_lds16(rq, q + 1024 * (4 * wave + c), live ? qoff[c] : BUF_OOB, b * QK_K);
+        if (wave < 2)
+            buf_to_lds16(rbs, lds + Lds::B0 + (i % NS) * Lds::BS + 1024 * wave, live ? bsoff : BUF_OOB, b * 32);
+        else
+            buf_to_lds4(rdx, lds + Lds::D0 + (i % Lds::ND) * Lds::DS, live ? dxoff : BUF_OOB, b * 4);
+    };
+    auto issue_w = [&](u32x4 &meta, u32x4 (&q)[4], int i) {
+        const int soff = (kb0 + i) * 9 * 128;
+        const bool live = i < nit;
+        meta = __builtin_amdgcn_raw_buffer_load_b128(rw, live ? woff : BUF_OOB, soff, 0);
+#pragma unroll
+        for (int c = 0; c < 4; c++)
+            q[c] = __builtin_amdgcn_raw_buffer_load_b128(rw, live ? wqoff + 256u * c : BUF_OOB, soff, 0);
     };
 
-    v16f yacc[MT];
+    v16f yacc[2];
 #pragma unroll
-    for (int t = 0; t < MT; t++)
+    for (int t = 0; t < 2; t++)
 #pragma unroll
         for (int r = 0; r < 16; r++) yacc[t][r] = 0.0f;
 
-    // Carried from super-block b - 1 into step b: its exact integer sums and
-    // scales; its f32 epilogue  y += d_x * (d_w * S - dmin_w * Smin)  is spread
-    // over the sub-blocks of b, one (tile, 4-row group) part after each
-    // sub-block's MFMAs, so the VALU work overlaps the matrix cores.  Before
-    // the first super-block the carried sums and scales are zero (the parts
-    // then add d_x * 0, with d_x read from a stage that holds real data).
-    v16i pS[MT];
-    v16f pSm[MT];
+    // Carried from super-block i - 1 into step i: T = d_w * S - dmin_w * Smin
+    // per output, formed as soon as the super-block's sums are complete; the
+    // remaining  y += d_x * T  is spread over the sub-blocks of step i, one
+    // (tile, 4-row group) part after each sub-block's MFMAs.  Before the
+    // first super-block T is zero (the parts then add d_x * 0, with d_x read
+    // from a filled slot).
+    v16f pT[2];
 #pragma unroll
-    for (int t = 0; t < MT; t++)
+    for (int t = 0; t < 2; t++)
 #pragma unroll
-        for (int r = 0; r < 16; r++) {
-            pS[t][r] = 0;
-            pSm[t][r] = 0.0f;
-        }
-    float pdw = 0.0f, pdmw = 0.0f;
-    const uint8_t *pring = lds + TL::RING0;
-    int pb = -1;
+        for (int r = 0; r < 16; r++) pT[t][r] = 0.0f;
+    const uint8_t *pd = lds + Lds::D0;  // d slot of the carried super-block
 
     auto epi_part = [&](int q) {  // q = 4 * t + r4: rows 8 * r4 + 4 * h + i of tile t
         const int t = q >> 2, r4 = q & 3;
-        const v4f dx4 = *(const v4f *)(pring + TL::BS + 256 * t + 4 * (8 * r4 + 4 * h));
+        const v4f dx4 = *(const v4f *)(pd + 4 * (32 * t + 8 * r4 + 4 * h));
         const float dx[4] = {dx4[0], dx4[1], dx4[2], dx4[3]};
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int r = 4 * r4 + i;
-            // f32 combine (the tolerance-bound part of the result): fused multiply-adds
-            yacc[t][r] = __builtin_fmaf(dx[i], __builtin_fmaf(-pdmw, pSm[t][r], pdw * (float)pS[t][r]), yacc[t][r]);
-            if (DUMP) {
-                const int row = m0 + 32 * t + 8 * r4 + 4 * h + i;
-                if (pb >= 0 && row < p.m && col_ok) {
-                    const int64_t o = ((int64_t)row * p.n + col) * ng + pb;
-                    p.S[o] = pS[t][r];
-                    p.Smin[o] = (int)pSm[t][r];
-                }
-            }
-        }
+        for (int i = 0; i < 4; i++) yacc[t][4 * r4 + i] = __builtin_fmaf(dx[i], pT[t][4 * r4 + i], yacc[t][4 * r4 + i]);
     };
 
-    auto compute = [&](const uint8_t *main, const uint8_t *ring, int b) {
-        // this lane's column: piece 0 and the four quant pieces of its half
-        const uint8_t *wp = main + TL::QS + ccol * 16;
-        const u32x4 meta = *(const u32x4 *)wp;
-        u32x4 bq[4];
-#pragma unroll
-        for (int c = 0; c < 4; c++) bq[c] = *(const u32x4 *)(wp + (1 + 2 * c + h) * TL::BP);
+    auto compute = [&](int i, const u32x4 &meta, const u32x4 (&wq)[4]) {
+        const uint8_t *qs = lds + Lds::Q0 + (i % NS) * Lds::QS;
+        const uint8_t *bsl = lds + Lds::B0 + (i % NS) * Lds::BS;
         // scales / mins of this lane's column (candle's utmp form of get_scale_min_k4)
         const uint32_t u0 = meta.y, u1 = meta.z, u2 = meta.w;
         const uint32_t sc03 = u0 & 0x3F3F3F3Fu;
-        const uint32_t sc47 = (u2 & 0x0F0F0F0Fu) | (((u0 >> 6) & 0x03030303u) << 4);
+        const uint32_t sc47 = (u2 & 0x0F0F0F0Fu) | ((u0 >> 2) & 0x30303030u);
         const uint32_t mn03 = u1 & 0x3F3F3F3Fu;
-        const uint32_t mn47 = ((u2 >> 4) & 0x0F0F0F0Fu) | (((u1 >> 6) & 0x03030303u) << 4);
+        const uint32_t mn47 = ((u2 >> 4) & 0x0F0F0F0Fu) | ((u1 >> 2) & 0x30303030u);
+        const uint32_t dg1[2] = {(sc03 >> 3) & 0x07070707u, (sc47 >> 3) & 0x07070707u};  // s1 per sub-block
+        const uint32_t dg0[2] = {sc03 & 0x07070707u, sc47 & 0x07070707u};                // s0 per sub-block
         const float dw = f16_bits_to_f32(meta.x), dmw = f16_bits_to_f32(meta.x >> 16);
 
         // S = 8 * acc1 + acc0 over the 8 sub-blocks; the A fragments of
         // sub-block j + 1 are read from LDS while the MFMAs of j run.
-        auto read_a = [&](v4i (&a)[MT], int j) {
+        auto read_a = [&](v4i (&a)[2], int j) {
 #pragma unroll
-            for (int t = 0; t < MT; t++) {
+            for (int t = 0; t < 2; t++) {
                 const int R = 32 * t + l32, C = 2 * j + h;
-                a[t] = *(const v4i *)(main + R * 256 + 16 * (C ^ (R & 15)));
+                a[t] = *(const v4i *)(qs + R * 256 + 16 * (C ^ (R & 15)));
             }
         };
-        v16i acc1[MT], acc0[MT];
-        v4i abuf[2][MT];
+        v16i acc1[2], acc0[2];
+        v4i abuf[2][2];
         read_a(abuf[0], 0);
 #pragma unroll
         for (int j = 0; j < 8; j++) {
-            const u32x4 pq = bq[j >> 1];
+            const u32x4 pq = wq[j >> 1];
             const uint32_t qv[4] = {pq.x, pq.y, pq.z, pq.w};
-            const uint32_t sw = j < 4 ? sc03 : sc47;
-            const uint32_t sc = (sw >> (8 * (j & 3))) & 0xffu;
-            const uint32_t s1 = sc >> 3, s0 = sc & 7u;
+            const uint32_t m1 = bcast_byte16(dg1[j >> 2], j & 3), m0s = bcast_byte16(dg0[j >> 2], j & 3);
             v4i d1, d0;
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const uint32_t nib = (j & 1) ? (qv[i] >> 4) & 0x0F0F0F0Fu : qv[i] & 0x0F0F0F0Fu;
-                d1[i] = pkmul(nib, s1);
-                d0[i] = pkmul(nib, s0);
+            for (int e = 0; e < 4; e++) {
+                const uint32_t nib = (j & 1) ? (qv[e] >> 4) & 0x0F0F0F0Fu : qv[e] & 0x0F0F0F0Fu;
+                d1[e] = pkmul(nib, m1);
+                d0[e] = pkmul(nib, m0s);
             }
             if (j < 7) read_a(abuf[(j + 1) & 1], j + 1);
 #pragma unroll
-            for (int t = 0; t < MT; t++) {
+            for (int t = 0; t < 2; t++) {
                 const v16i z = {0};
                 acc1[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(abuf[j & 1][t], d1, j == 0 ? z : acc1[t], 0, 0, 0);
                 acc0[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(abuf[j & 1][t], d0, j == 0 ? z : acc0[t], 0, 0, 0);
@@ -264,51 +263,66 @@ __global__ __launch_bounds__(256, 2) void gemm_q4k_kernel(GemmParams p) {
             epi_part(j);  // the previous super-block's part j
         }
 
-        // Smin of b on f16 MFMA: A[m][g] = bsums (g = 8h + i), B[g][n] = mn[g/2]
+        // Smin on f16 MFMA: A[m][g] = bsums (g = 8h + i), B[g][n] = mn[g/2]
         const uint32_t mw = h ? mn47 : mn03;
-        v8h bmn;
+        const uint32_t bp[4] = {f16pair_of_byte(mw, 0), f16pair_of_byte(mw, 1), f16pair_of_byte(mw, 2),
+                                f16pair_of_byte(mw, 3)};
+        const v8h bmn = __builtin_bit_cast(v8h, (u32x4){bp[0], bp[1], bp[2], bp[3]});
 #pragma unroll
-        for (int i = 0; i < 8; i++) bmn[i] = (_Float16)(int)((mw >> (8 * (i >> 1))) & 0xffu);
-#pragma unroll
-        for (int t = 0; t < MT; t++) {
-            const v8h abs = *(const v8h *)(ring + (32 * t + l32) * 32 + 16 * h);
+        for (int t = 0; t < 2; t++) {
+            const v8h abs = *(const v8h *)(bsl + (32 * t + l32) * 32 + 16 * h);
             const v16f z = {0};
-            pSm[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(abs, bmn, z, 0, 0, 0);
-            pS[t] = (acc1[t] << 3) + acc0[t];
+            const v16f sm = __builtin_amdgcn_mfma_f32_32x32x16_f16(abs, bmn, z, 0, 0, 0);
+            const v16i S = (acc1[t] << 3) + acc0[t];
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                // f32 combine (the tolerance-bound part of the result): fused multiply-add
+                pT[t][r] = __builtin_fmaf(-dmw, sm[r], dw * (float)S[r]);
+                if (DUMP) {
+                    const int row = m0 + 32 * t + 8 * (r >> 2) + 4 * h + (r & 3);
+                    if (row < p.m && col_ok) {
+                        const int64_t o = ((int64_t)row * p.n + col) * ng + kb0 + i;
+                        p.S[o] = S[r];
+                        p.Smin[o] = (int)sm[r];
+                    }
+                }
+            }
         }
-        pdw = dw;
-        pdmw = dmw;
-        pring = ring;
-        pb = b;
+        pd = lds + Lds::D0 + (i % Lds::ND) * Lds::DS;
     };
 
-    // Main stages alternate, ring stages rotate over three.  The copies for
-    // super-block b + 1 are issued right after the barrier and have the
-    // compute of b to land; each step begins by waiting for this wave's
-    // outstanding copies (only those of the stage about to be read are
-    // outstanding by then).  At step b the copies overwrite the main stage
-    // of b - 1 (read during step b - 1) and the ring stage of b - 2 (whose
-    // epilogue ran during step b - 1).
-    issue(lds, lds + TL::RING0, kb0);
-    for (int b = kb0; b < kb1; b++) {
-        const int i = b - kb0;
-        uint8_t *main = lds + (i & 1) * TL::MAIN;
-        uint8_t *ring = lds + TL::RING0 + (i % 3) * TL::SMALL;
-        if (i == 0) pring = ring;  // the first parts read real d_x and add d_x * 0
-        wait_vmcnt<0>();
+    // The steps.  Before step i: wait for this wavefront's copies of stage i
+    // and its weight registers of super-block i (issued before the copies of
+    // step i - 1, which may stay in flight), then a barrier, so every
+    // wavefront's copies have landed and every wavefront has finished step
+    // i - 1, whose stage the copies issued in step i overwrite.
+    constexpr int CA = 5;  // loads per copy issue
+    auto step = [&](int i, const u32x4 &meta, const u32x4 (&wq)[4], u32x4 &nmeta, u32x4 (&nwq)[4]) {
+        issue_w(nmeta, nwq, i + 1);
+        issue_act(i + NS - 1);
+        compute(i, meta, wq);
+        wait_vmcnt<CA>();
         stage_barrier();
-        if (b + 1 < kb1)
-            issue(lds + ((i + 1) & 1) * TL::MAIN, lds + TL::RING0 + ((i + 1) % 3) * TL::SMALL, b + 1);
-        compute(main, ring, b);
+    };
+
+    u32x4 meta0, meta1, wq0[4], wq1[4];
+    issue_w(meta0, wq0, 0);
+#pragma unroll
+    for (int i = 0; i < NS - 1; i++) issue_act(i);
+    wait_vmcnt<(NS - 2) * CA>();
+    stage_barrier();
+    for (int i = 0; i < nit; i += 2) {
+        step(i, meta0, wq0, meta1, wq1);
+        if (i + 1 < nit) step(i + 1, meta1, wq1, meta0, wq0);
     }
 #pragma unroll
-    for (int q = 0; q < 4 * MT; q++) epi_part(q);  // the last super-block's epilogue
-    stage_barrier();  // the split-K tail below reuses no stage, but keeps waves together
+    for (int q = 0; q < 8; q++) epi_part(q);  // the last super-block's epilogue
+    wait_vmcnt<0>();  // the copies issued past the last super-block still write LDS
 
     if (p.splits == 1) {
         if (col_ok) {
 #pragma unroll
-            for (int t = 0; t < MT; t++)
+            for (int t = 0; t < 2; t++)
 #pragma unroll
                 for (int r = 0; r < 16; r++) {
                     const int row = m0 + 32 * t + 8 * (r >> 2) + 4 * h + (r & 3);
@@ -322,7 +336,7 @@ __global__ __launch_bounds__(256, 2) void gemm_q4k_kernel(GemmParams p) {
     // on the stream) sums the partials in split order
     float *mine = p.part + ((int64_t)tile * p.splits + split) * (GBM * GBN);
 #pragma unroll
-    for (int t = 0; t < MT; t++)
+    for (int t = 0; t < 2; t++)
 #pragma unroll
         for (int r = 0; r < 16; r++) mine[(32 * t + 8 * (r >> 2) + 4 * h + (r & 3)) * GBN + ccol] = yacc[t][r];
 }
@@ -352,22 +366,20 @@ struct GemmPlan {
     size_t ws;
 };
 
-// 64 x 128 tiles, two workgroups per CU (their wavefronts share the SIMDs but
-// not their barriers, so one's VALU epilogue overlaps the other's MFMAs);
-// the K loop is split (halves, quarters, ...) while there are fewer items than
-// CUs, each split keeping at least two super-blocks.
+// 64 x 128 tiles, two workgroups per CU; the K loop is split (halves,
+// quarters, ...) while there are fewer items than CUs, each split keeping at
+// least two super-blocks.
 GemmPlan gemm_plan(int64_t m, int64_t n, int64_t k) {
     GemmPlan g;
     const int ng = (int)(k / QK_K);
-    const int gbm = 32 * 2;
     g.ntn = (int)((n + GBN - 1) / GBN);
-    g.ntm = (int)((m + gbm - 1) / gbm);
+    g.ntm = (int)((m + GBM - 1) / GBM);
     g.tiles = g.ntm * g.ntn;
     g.splits = 1;
     while ((int64_t)g.tiles * g.splits < TARGET_WG && ng / (2 * g.splits) >= 2) g.splits *= 2;
     g.kbs = (ng + g.splits - 1) / g.splits;
     g.splits = (ng + g.kbs - 1) / g.kbs;
-    g.ws = g.splits > 1 ? (size_t)g.tiles * g.splits * gbm * GBN * 4 : 0;
+    g.ws = g.splits > 1 ? (size_t)g.tiles * g.splits * GBM * GBN * 4 : 0;
     return g;
 }
 
@@ -440,14 +452,14 @@ hipError_t launch_gemm(const WLayout &w, int64_t n, int64_t k, const ActPlanes &
         p.S = S ? S + r0 * n * ng : nullptr;
         p.Smin = Smin ? Smin + r0 * n * ng : nullptr;
         const unsigned grid = (unsigned)(p.per_xcd * NXCD);
-        if (S) gemm_q4k_kernel<2, true><<<grid, 256, 0, s>>>(p);
-        else gemm_q4k_kernel<2, false><<<grid, 256, 0, s>>>(p);
+        if (S) gemm_q4k_kernel<true><<<grid, 256, 0, s>>>(p);
+        else gemm_q4k_kernel<false><<<grid, 256, 0, s>>>(p);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
         if (g.splits > 1) {
-            const int64_t elems = (int64_t)g.tiles * 64 * GBN;
-            gemm_splitk_reduce<<<(unsigned)((elems + 255) / 256), 256, 0, s>>>(p.part, p.y, p.m, p.n, g.ntm, 64, g.splits,
-                                                                             g.tiles);
+            const int64_t elems = (int64_t)g.tiles * GBM * GBN;
+            gemm_splitk_reduce<<<(unsigned)((elems + 255) / 256), 256, 0, s>>>(p.part, p.y, p.m, p.n, g.ntm, GBM,
+                                                                             g.splits, g.tiles);
             if ((e = hipGetLastError()) != hipSuccess) return e;
         }
     }
