@@ -43,6 +43,43 @@ __global__ __launch_bounds__(256) void mfma_loop(int iters, int *out) {
     out[blockIdx.x * 256 + t] = s;
 }
 
+// The issue cost of v_mfma_i32_32x32x32_i8 next to VALU work: four
+// independent accumulator chains per wavefront on operands loaded from
+// memory (random bytes, as a GEMM's), each MFMA followed by NV independent
+// f32 fmas, the two kinds interleaved by sched_group_barrier; launch bounds
+// (256, 2) and 512 workgroups give two wavefronts per SIMD.  Time per MFMA
+// per SIMD against NV shows how much of the VALU work the matrix core hides.
+template <int NV>
+__global__ __launch_bounds__(256, 2) void coexec_loop(const int *src, int iters, int *out) {
+    const int t = (int)threadIdx.x;
+    v4i a[2], b[2];
+    for (int i = 0; i < 2; i++) {
+        a[i] = *(const v4i *)(src + 8 * t + 4 * i);
+        b[i] = *(const v4i *)(src + 2048 + 8 * t + 4 * i);
+    }
+    float f[8];
+    for (int i = 0; i < 8; i++) f[i] = (float)(src[4096 + t + i] & 255);
+    const float g = 0.5f + (float)(src[5000 + t] & 1), hh = (float)(src[5100 + t] & 7);
+    v16i c[4] = {};
+    for (int i = 0; i < iters; i++) {
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            c[u] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[(u >> 1) & 1], b[u & 1], c[u], 0, 0, 0);
+#pragma unroll
+            for (int v = 0; v < NV; v++) f[v & 7] = __builtin_fmaf(f[v & 7], g, hh);
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA, then the NV fmas
+            if (NV) __builtin_amdgcn_sched_group_barrier(0x002, NV, 0);
+        }
+    }
+    int s = 0;
+#pragma unroll
+    for (int u = 0; u < 4; u++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) s += c[u][r];
+    for (int i = 0; i < 8; i++) s += (int)f[i];
+    out[blockIdx.x * 256 + t] = s;
+}
+
 }  // namespace
 
 extern "C" {
@@ -61,6 +98,21 @@ int aq_bench_mfma(int kind, void *stream, int grid, int iters, int *d_out) {
     if (kind == 0) mfma_loop<0><<<grid, 256, 0, s>>>(iters, d_out);
     else if (kind == 1) mfma_loop<1><<<grid, 256, 0, s>>>(iters, d_out);
     else mfma_loop<2><<<grid, 256, 0, s>>>(iters, d_out);
+    return hipGetLastError() == hipSuccess ? 0 : -5;
+}
+
+// coexec_loop<nv> for nv in {0, 4, 8, 16}: 512 workgroups (two wavefronts
+// per SIMD), each wavefront issuing 4 * iters MFMAs; d_src holds 8192 ints
+// (the operands), d_out 512 * 256 ints.  Returns 0, -1 for bad arguments, -5
+// for a launch error.
+int aq_bench_coexec(int nv, void *stream, int iters, const int *d_src, int *d_out) {
+    if (iters <= 0 || !d_src || !d_out) return -1;
+    hipStream_t s = (hipStream_t)stream;
+    if (nv == 0) coexec_loop<0><<<512, 256, 0, s>>>(d_src, iters, d_out);
+    else if (nv == 4) coexec_loop<4><<<512, 256, 0, s>>>(d_src, iters, d_out);
+    else if (nv == 8) coexec_loop<8><<<512, 256, 0, s>>>(d_src, iters, d_out);
+    else if (nv == 16) coexec_loop<16><<<512, 256, 0, s>>>(d_src, iters, d_out);
+    else return -1;
     return hipGetLastError() == hipSuccess ? 0 : -5;
 }
 

@@ -166,27 +166,27 @@ __global__ __launch_bounds__(256, DUMP ? 1 : 2) void gemm_q4k_kernel(GemmParams 
     const uint32_t wqoff = woff + 128u * (1 + h);
 
     // A step issues its loads whether or not super-block kb0 + i exists, so
-    // every step waits on the same counts; past the last one every lane's
-    // offset is BUF_OOB (the range check covers the per-lane offset, not the
-    // scalar one), so those loads read zeros without touching memory.
+    // every step waits on the same counts; past the last one the loads go
+    // through descriptors of zero bytes (the range check covers the per-lane
+    // offset, not the scalar one), so they read zeros without touching
+    // memory.  The choice of descriptor is scalar: no per-lane selects.
+    const rsrc_t rnone = buf_rsrc(p.xq, 0u);
     auto issue_act = [&](int i) {  // super-block kb0 + i into stage i % NS, its d into slot i % ND
         const int b = kb0 + i;
         const bool live = i < nit;
         uint8_t *q = lds + Lds::Q0 + (i % NS) * Lds::QS;
+        const rsrc_t r1 = live ? rq : rnone;
 #pragma unroll
-        for (int c = 0; c < 4; c++) buf_to_lds16(rq, q + 1024 * (4 * wave + c), live ? qoff[c] : BUF_OOB, b * QK_K);
-        if (wave < 2)
-            buf_to_lds16(rbs, lds + Lds::B0 + (i % NS) * Lds::BS + 1024 * wave, live ? bsoff : BUF_OOB, b * 32);
-        else
-            buf_to_lds4(rdx, lds + Lds::D0 + (i % Lds::ND) * Lds::DS, live ? dxoff : BUF_OOB, b * 4);
+        for (int c = 0; c < 4; c++) buf_to_lds16(r1, q + 1024 * (4 * wave + c), qoff[c], b * QK_K);
+        if (wave < 2) buf_to_lds16(live ? rbs : rnone, lds + Lds::B0 + (i % NS) * Lds::BS + 1024 * wave, bsoff, b * 32);
+        else buf_to_lds4(live ? rdx : rnone, lds + Lds::D0 + (i % Lds::ND) * Lds::DS, dxoff, b * 4);
     };
     auto issue_w = [&](u32x4 &meta, u32x4 (&q)[4], int i) {
         const int soff = (kb0 + i) * 9 * 128;
-        const bool live = i < nit;
-        meta = __builtin_amdgcn_raw_buffer_load_b128(rw, live ? woff : BUF_OOB, soff, 0);
+        const rsrc_t r = i < nit ? rw : rnone;
+        meta = __builtin_amdgcn_raw_buffer_load_b128(r, woff, soff, 0);
 #pragma unroll
-        for (int c = 0; c < 4; c++)
-            q[c] = __builtin_amdgcn_raw_buffer_load_b128(rw, live ? wqoff + 256u * c : BUF_OOB, soff, 0);
+        for (int c = 0; c < 4; c++) q[c] = __builtin_amdgcn_raw_buffer_load_b128(r, wqoff + 256u * c, soff, 0);
     };
 
     v16f yacc[2];
