@@ -554,7 +554,7 @@ hipError_t launch_attn_split(const float *qk, const float *v, const float *cosb,
                              int64_t max_seq, float *out, float *part, size_t part_bytes, hipStream_t s) {
     if (n_head <= 0 || n_kv <= 0 || n_head % n_kv || n_kv > 65535) return hipErrorNotSupported;
     const int64_t rep = n_head / n_kv;
-    if ((hd != 64 && hd != 128) || (rep != 1 && rep != 2 && rep != 4 && rep != 8)) return hipErrorNotSupported;
+    if ((hd != 64 && hd != 128) || (rep != 1 && rep != 2 && rep != 3 && rep != 4 && rep != 8)) return hipErrorNotSupported;
     const int S = attn_split_slices(n_kv, max_seq);
     if (S == 0 || attn_split_workspace_bytes(n_head, n_kv, hd, max_seq) > part_bytes) return hipErrorNotSupported;
     // slices past split_max_slices never hold a position: no workgroup for them
@@ -565,6 +565,7 @@ hipError_t launch_attn_split(const float *qk, const float *v, const float *cosb,
         switch (rep) {
         case 1: AQ_SPLIT(16, 1); break;
         case 2: AQ_SPLIT(16, 2); break;
+        case 3: AQ_SPLIT(16, 3); break;
         case 4: AQ_SPLIT(16, 4); break;
         default: AQ_SPLIT(16, 8); break;
         }
@@ -572,6 +573,7 @@ hipError_t launch_attn_split(const float *qk, const float *v, const float *cosb,
         switch (rep) {
         case 1: AQ_SPLIT(32, 1); break;
         case 2: AQ_SPLIT(32, 2); break;
+        case 3: AQ_SPLIT(32, 3); break;
         case 4: AQ_SPLIT(32, 4); break;
         default: AQ_SPLIT(32, 8); break;
         }

@@ -278,7 +278,7 @@ int aq_llama_silu_mul_rows(aq_ctx *ctx, const float *d_g, const float *d_u, int6
  * pairs), stores k and v at pos, and writes softmax(q.k/sqrt(head_dim)).v
  * over positions 0..pos for each query head to d_out (n_head*head_dim).
  * head_dim must divide 256 and be a multiple of 4; max_seq <= 8192; caches
- * and d_out 16-byte aligned.  For head_dim 64 or 128 with 1, 2, 4 or 8 query
+ * and d_out 16-byte aligned.  For head_dim 64 or 128 with 1, 2, 3, 4 or 8 query
  * heads per kv head, the context is split over workgroups whose partial
  * results go to the context's attention workspace and are combined by a
  * second launch: calls on one context must not overlap (they are ordered

@@ -99,6 +99,8 @@ def _decode_call(torch, lib, ctx, n_head, n_kv, hd, max_seq, kc, vc, qk, v, pos,
         (8, 4, 64, 512, [0, 100, 511]),  # 2 per kv head
         (8, 8, 128, 512, [0, 5, 300]),   # one query head per kv head
         (64, 8, 128, 256, [0, 255]),     # 8 per kv head at head_dim 128
+        (9, 3, 64, 640, [0, 15, 16, 511, 512, 639]),  # SmolLM-135M heads: 3 per kv head, 85 slices
+        (15, 5, 64, 300, [0, 17, 299]),  # 3 per kv head, five kv heads
     ],
 )
 def test_split_decode_against_numpy_back_to_back(env, n_head, n_kv, hd, max_seq, positions):
@@ -164,7 +166,8 @@ def _prefill_ref(q, k, v, kc, vc, cos, sin, index_pos, n_head, n_kv, hd):
 @pytest.mark.parametrize(
     "n_head,n_kv,hd,index_pos,m,max_seq",
     [(4, 2, 64, 0, 7, 64), (32, 4, 64, 0, 512, 640), (32, 4, 64, 0, 100, 128), (8, 8, 128, 5, 70, 128),
-     (32, 8, 128, 0, 65, 128), (32, 4, 64, 200, 1, 256), (16, 2, 64, 37, 130, 256)],
+     (32, 8, 128, 0, 65, 128), (32, 4, 64, 200, 1, 256), (16, 2, 64, 37, 130, 256),
+     (9, 3, 64, 0, 512, 640), (9, 3, 64, 512, 3, 640)],  # SmolLM-135M heads: 3 per kv head
 )
 def test_prefill_against_numpy(env, n_head, n_kv, hd, index_pos, m, max_seq):
     torch, lib, ctx = env

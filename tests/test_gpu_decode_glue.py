@@ -95,7 +95,9 @@ def _rope(x, c, s):
     [(32, 4, 64, 0, 1024), (32, 4, 64, 517, 1024), (8, 8, 128, 300, 1024), (4, 2, 32, 1023, 1024),
      # contexts past the rows each thread loads ahead (one key row, up to
      # eight value rows per thread), the narrowest and widest heads
-     (32, 4, 64, 4095, 4096), (8, 2, 256, 2500, 4096), (16, 4, 8, 3000, 4096), (8, 1, 128, 1800, 2048)],
+     (32, 4, 64, 4095, 4096), (8, 2, 256, 2500, 4096), (16, 4, 8, 3000, 4096), (8, 1, 128, 1800, 2048),
+     # three query heads per kv head (SmolLM-135M: 9 / 3)
+     (9, 3, 64, 0, 640), (9, 3, 64, 600, 640), (6, 2, 128, 2047, 2048)],
 )
 def test_attn_decode_against_numpy(env, n_head, n_kv, hd, pos, max_seq):
     torch, lib, ctx = env
