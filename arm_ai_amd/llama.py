@@ -98,6 +98,36 @@ def tinyllama_q5km_types(cfg: LlamaConfig, layer: int) -> dict[str, int]:
             for name, t in tinyllama_q4km_types(cfg, layer).items()}
 
 
+def smollm_135m_config(max_seq: int = 1024) -> LlamaConfig:
+    """SmolLM-135M's shape (one of the models the reference's chatbot loads,
+    examples/chatbot/README.md:36-37): 30 layers, hidden 576, FFN 1536, 9
+    query heads over 3 kv heads (head_dim 64), vocabulary 49152, output head
+    tied to the token embedding."""
+    return LlamaConfig(n_layer=30, hidden=576, ffn=1536, n_head=9, n_kv_head=3, vocab=49152, max_seq=max_seq)
+
+
+def gguf_fallback_type(t: int, k: int) -> int:
+    """The type llama.cpp's quantizer writes for a tensor whose rows (k) are
+    not a multiple of 256, which no K-quant block can hold: Q4_K -> Q5_0,
+    Q6_K -> Q8_0 (Q2_K / Q3_K -> IQ4_NL and Q5_K -> Q5_1 have no kernels
+    here and are not produced by the mixes below)."""
+    if k % 256 == 0:
+        return t
+    fb = {synth.TYPE_Q4_K: synth.TYPE_Q5_0, synth.TYPE_Q6_K: synth.TYPE_Q8_0}
+    if t not in fb:
+        raise ValueError(f"no fallback type for GGML type {t} at k={k}")
+    return fb[t]
+
+
+# The Q4_K_M mix of a model whose hidden width is not a multiple of 256
+# (SmolLM-135M: 576): every projection that reads the hidden state (wq, wk,
+# wv, wo, w1, w3) takes its fallback type, w2 (k = ffn = 1536) keeps its
+# K-quant.
+def fallback_q4km_types(cfg: LlamaConfig, layer: int) -> dict[str, int]:
+    shapes = weight_shapes(cfg)
+    return {name: gguf_fallback_type(t, shapes[name][1]) for name, t in tinyllama_q4km_types(cfg, layer).items()}
+
+
 def weight_shapes(cfg: LlamaConfig) -> dict[str, tuple[int, int]]:
     """(n, k) of each per-layer projection (candle's (out, in))."""
     hd = cfg.head_dim

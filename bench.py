@@ -256,8 +256,11 @@ VENDOR_CASES = {  # name: (m, n, k)
     "ref_vendor_int8_gemm_512x5632x2048": (512, 5632, 2048),
     "ref_vendor_int8_gemm_512x2048x5632": (512, 2048, 5632),
 }
-DECODE_CASES = {  # name: (prompt tokens, new tokens, seed)
-    "c2_tinyllama_decode": (512, 128, 2),
+DECODE_CASES = {  # name: (model, prompt tokens, new tokens, seed)
+    "c2_tinyllama_decode": ("tinyllama", 512, 128, 2),
+    # SmolLM-135M's shape (docs/perf_llm.md:98-99 quotes its Q4_K_M decode on
+    # a phone): hidden 576, so its Q4_K_M file holds the fallback types
+    "smollm135m_decode": ("smollm135m", 512, 128, 3),
 }
 CRATE_CASES = {  # the NIF crate's own kernels: name: (kind, m, n, k)
     "crate_q4_x_q8_gemv_4096x4096": ("q4_x_q8", 1, 4096, 4096),
@@ -296,18 +299,35 @@ def cpu_decode_baseline(hw, prompt, n_prompt=16, n_steps=4) -> dict:
             "sample": f"{n_steps} greedy steps after a {n_prompt}-token prompt"}
 
 
-def measure_decode(ctx, n_prompt, n_new, seed, with_cpu=True):
-    """Config 2: TinyLlama-1.1B-shaped Q4_K_M model with random weights, a prompt
-    of uniform-random ids, greedy decode with the decode step replayed from a HIP
-    graph; statistics as ArmAI.LlamaCandle.generate reports them."""
-    from arm_ai_amd.llama import Llama, LlamaConfig, synthetic_weights
+def decode_model(name, max_seq, seed):
+    """The host weights of a decode case: TinyLlama-1.1B's shape with its
+    Q4_K_M mix (config 2), or SmolLM-135M's with the Q4_K_M fallback types."""
+    from arm_ai_amd import synth
+    from arm_ai_amd.llama import LlamaConfig, fallback_q4km_types, smollm_135m_config, synthetic_weights
 
-    cfg = LlamaConfig(max_seq=n_prompt + n_new)
+    if name == "tinyllama":
+        cfg = LlamaConfig(max_seq=max_seq)
+        desc = "TinyLlama-1.1B shape (22 layers, hidden 2048, FFN 5632, 32/4 heads, vocab 32000), Q4_K_M types"
+        return desc, synthetic_weights(cfg, seed, unit=True)
+    cfg = smollm_135m_config(max_seq=max_seq)
+    desc = ("SmolLM-135M shape (30 layers, hidden 576, FFN 1536, 9/3 heads, vocab 49152, tied output), Q4_K_M "
+            "types with the fallbacks of rows of 576 (Q5_0, Q8_0)")
+    return desc, synthetic_weights(cfg, seed, types=fallback_q4km_types, output_type=synth.TYPE_Q8_0, unit=True)
+
+
+def measure_decode(ctx, model_name, n_prompt, n_new, seed, with_cpu=True):
+    """A Llama-shaped model with random weights (config 2: TinyLlama-1.1B's
+    Q4_K_M shape), a prompt of uniform-random ids, greedy decode with the
+    decode step replayed from a HIP graph; statistics as
+    ArmAI.LlamaCandle.generate reports them."""
+    from arm_ai_amd.llama import Llama
+
     t0 = time.perf_counter()
-    hw = synthetic_weights(cfg, seed, unit=True)
+    desc, hw = decode_model(model_name, n_prompt + n_new, seed)
+    cfg = hw.cfg
     wbytes = sum(qt.data.size for layer in hw.layers for qt in layer.values()) + hw.output.data.size
     model = Llama(ctx, hw)
-    log(f"c2 model ready in {time.perf_counter() - t0:.1f} s")
+    log(f"{model_name} model ready in {time.perf_counter() - t0:.1f} s")
     rng = np.random.default_rng(seed)
     prompt = rng.integers(0, cfg.vocab, size=n_prompt).tolist()
     model.generate(prompt[:16], 4, graph=True)  # capture the step, first-call set-up
@@ -319,7 +339,7 @@ def measure_decode(ctx, n_prompt, n_new, seed, with_cpu=True):
     cpu = cpu_decode_baseline(hw, prompt) if with_cpu else None
     del hw
     out = {
-        "model": "TinyLlama-1.1B shape (22 layers, hidden 2048, FFN 5632, 32/4 heads, vocab 32000), Q4_K_M types, random unit-scaled weights (activations of order one through all 22 layers)",
+        "model": desc + ", random unit-scaled weights (activations of order one through every layer)",
         "n_prompt": n_prompt,
         "n_new": st["n_new"],
         "decode_tok_s": round(1e3 / st["decode_ms_per_tok"], 1),
@@ -557,8 +577,8 @@ def run_case(ctx, name, steps, warmup, with_cpu=False):
         log(f"{name}: {out['us']} us ({out['TOPS']} TOPS, {out['frac_int8_peak']} of int8 peak)")
         return out
     if name in DECODE_CASES:
-        n_prompt, n_new, seed = DECODE_CASES[name]
-        out = measure_decode(ctx, n_prompt, n_new, seed, with_cpu=with_cpu)
+        model_name, n_prompt, n_new, seed = DECODE_CASES[name]
+        out = measure_decode(ctx, model_name, n_prompt, n_new, seed, with_cpu=with_cpu)
         log(f"{name}: decode {out['decode_tok_s']} tok/s ({out['decode_ms_per_tok']} ms/tok; eager {out['eager_decode_tok_s']} tok/s), prefill {out['prefill_ms']} ms ({out['prefill_tok_s']} tok/s)")
         return out
     if name in MATVEC_CASES:

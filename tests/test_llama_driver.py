@@ -295,3 +295,94 @@ def test_generate_streams_each_token_before_the_next_step(tiny):
     seen = []
     assert model.generate(prompt, 8, stop_tokens=(eager[0],), graph=True, on_token=seen.append).tokens == eager[:1]
     assert seen == eager[:1]
+
+
+# ------------------------------------------------------------ SmolLM-135M shape
+def test_gguf_fallback_types_for_rows_not_a_multiple_of_256():
+    """llama.cpp's Q4_K_M writes the fallback type where a row (k) is not a
+    multiple of 256: SmolLM-135M's hidden 576 turns Q4_K into Q5_0 and Q6_K
+    into Q8_0; w2 (k = 1536) keeps its K-quant."""
+    from arm_ai_amd import synth
+    from arm_ai_amd.llama import fallback_q4km_types, gguf_fallback_type, smollm_135m_config
+
+    cfg = smollm_135m_config()
+    assert cfg.head_dim == 64 and cfg.n_head // cfg.n_kv_head == 3
+    t0, t1 = fallback_q4km_types(cfg, 0), fallback_q4km_types(cfg, 1)
+    assert t0 == {"wq": synth.TYPE_Q5_0, "wk": synth.TYPE_Q5_0, "wv": synth.TYPE_Q8_0, "wo": synth.TYPE_Q5_0,
+                  "w1": synth.TYPE_Q5_0, "w3": synth.TYPE_Q5_0, "w2": synth.TYPE_Q4_K}
+    assert t1["w2"] == synth.TYPE_Q6_K
+    assert gguf_fallback_type(synth.TYPE_Q6_K, 576) == synth.TYPE_Q8_0
+    assert gguf_fallback_type(synth.TYPE_Q4_K, 512) == synth.TYPE_Q4_K
+
+
+@pytest.fixture(scope="module")
+def smollm():
+    """SmolLM-135M's widths and heads (hidden 576, FFN 1536, 9 query / 3 kv
+    heads, vocabulary 49152) with three of its 30 layers, the Q4_K_M mix with
+    the fallback types (Q5_0, Q8_0) of rows that are not a multiple of 256,
+    and the Q8_0 output head of the tied embedding."""
+    import torch
+
+    import arm_ai_amd as A
+    from arm_ai_amd import synth
+    from arm_ai_amd.llama import Llama, fallback_q4km_types, smollm_135m_config, synthetic_weights
+
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    cfg = smollm_135m_config(max_seq=96)
+    cfg.n_layer = 3
+    hw = synthetic_weights(cfg, seed=31, types=fallback_q4km_types, output_type=synth.TYPE_Q8_0, unit=True)
+    ctx = A.Context(0)
+    model = Llama(ctx, hw)
+    yield hw, model
+    model.free()
+    ctx.close()
+
+
+@pytest.mark.gpu
+def test_smollm_shape_matmuls_glue_graph_step_and_generate(smollm):
+    """Prefill (Q5_0 / Q8_0 GEMMs on k = 576, the Q4_K / Q6_K ones on k =
+    1536, prompt attention at three query heads per kv head) and two decode
+    steps, checked as the full-size test checks config 2: every projection
+    on the GPU's own input against the oracle (block sums bit-exact on one
+    row), layer 0's glue step by step, the logits against an independent CPU
+    run at the bar the Q8 rounding-boundary compounding allows (a norm output
+    one ulp apart moves quants of 32-element Q8_0 blocks across a boundary:
+    measured 3e-3 on the hidden state after one layer, 1.3e-2 on the logits
+    after three); then the graph-captured step against the eager one and
+    greedy generation, graph against eager teacher-forced."""
+    from tests.test_llama_fullsize import _check_records, _Glue, _graph_vs_eager, _host_blocks, _layer_records
+
+    hw, model = smollm
+    cfg = hw.cfg
+    ref = RefLlama(hw)
+    host_of = _host_blocks(model, hw)
+    glue = _Glue(ref, 0)
+    rng = np.random.default_rng(33)
+    prompt = rng.integers(0, cfg.vocab, size=40).tolist()
+    pos = 0
+    for i, toks in enumerate([prompt, [int(rng.integers(0, cfg.vocab))], [int(rng.integers(0, cfg.vocab))]]):
+        what = "prefill" if i == 0 else f"decode step {i - 1}"
+        with model.capture_hidden({0, 1}) as hx, model.trace_matmuls((0, 1, len(toks) - 1), full_layers=(0,)) as recs:
+            g = model.forward(toks, pos).cpu().numpy()
+        assert np.all(np.isfinite(g))
+        assert len(recs) == 5 * cfg.n_layer + 1
+        _check_records(recs, host_of, what)
+        for name, e in glue.check(hx[0], _layer_records(recs, 0), hx[1], pos).items():
+            assert e <= 1e-5, f"{what}, layer 0: {name} rel {e:.3e}"
+        r = ref.forward(toks, pos)
+        assert _rel(g, r) <= 5e-2, f"{what}: logits against the independent CPU run rel {_rel(g, r):.3e}"
+        pos += len(toks)
+    gerr = _graph_vs_eager(model, rng.integers(0, cfg.vocab, size=4).tolist(), pos)
+    assert max(gerr) <= 5e-2, f"graph step vs eager rel {max(gerr):.3e}"
+    # greedy generation: the graph's tokens against the eager argmax fed the
+    # same tokens, wherever the eager margin is clear of the step difference
+    toks = model.generate(prompt, 8, graph=True).tokens
+    lg = model.forward(prompt, 0).cpu().numpy()
+    margin = 2.0 * max(max(gerr), 1e-3)
+    for i, t in enumerate(toks):
+        top2 = np.sort(lg)[-2:]
+        if top2[1] - top2[0] > margin * np.max(np.abs(lg)):
+            assert t == int(np.argmax(lg)), f"token {i}"
+        if i + 1 < len(toks):
+            lg = model.forward([t], len(prompt) + i).cpu().numpy()
