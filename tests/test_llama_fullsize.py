@@ -27,7 +27,12 @@ Checks (GPU):
    positions' outputs by up to 4e-3 while the rest agree to 1e-7.
 3. The final norm and output head on the GPU's last hidden state (HEAD_TOL).
 4. The graph-captured decode step (device-resident glue kernels) against
-   the eager step, one step at a time from the same cache, for 16 tokens.
+   the eager step, one step at a time from the same cache, for 16 tokens;
+   and config 2's whole run, generate(graph=True) over 128 greedy steps
+   (each replay feeding the next from device memory), against the eager
+   path teacher-forced with the graph's tokens: the logits of the last
+   replay at positions 560 and 638, and every token whose eager top-2 margin
+   is wider than twice the measured graph-vs-eager difference.
    Its glue rounds differently from the eager step's torch ops, so the
    boundary effect above applies: a step either agrees to f32 rounding or
    some quant crossed a boundary somewhere in the stack (measured at two
@@ -60,6 +65,7 @@ GRAPH_TOL_22 = 8e-2
 FREE_TOL = 1e-1
 FREE_TOL_2 = 5e-2
 N_GRAPH = 16
+N_GEN = 128  # greedy steps of the graph-replayed generate (config 2's decode length)
 
 
 def _rel(a, b):
@@ -117,7 +123,7 @@ def full():
 
     if not torch.cuda.is_available():
         pytest.fail("GPU tests need torch to see the GPU")
-    cfg = LlamaConfig(max_seq=N_PROMPT + N_STEPS + 4)
+    cfg = LlamaConfig(max_seq=N_PROMPT + N_GEN)
     hw = synthetic_weights(cfg, seed=2, unit=True)
     ctx = A.Context(0)
     model = Llama(ctx, hw)
@@ -269,3 +275,45 @@ def test_config2_widths_two_layers_graph_step_and_free_run():
     finally:
         model.free()
         ctx.close()
+
+
+def test_config2_graph_generate_128_steps_against_teacher_forced_eager(full):
+    """generate(graph=True) for config 2's 128 greedy steps after the
+    512-token prompt: positions 512..638 run as chained replays of the
+    captured step (token and position advanced on the device).  The eager
+    forward, fed the graph's tokens, gives the logits of every position: the
+    graph's last replay must match them at positions 560 (a 50-token run) and
+    638 (the 128-token run) within GRAPH_TOL_22, and wherever the eager top-2
+    margin exceeds twice the larger of those two differences, the graph must
+    have picked the eager argmax."""
+    hw, model = full
+    cfg = hw.cfg
+    rng = np.random.default_rng(43)
+    prompt = rng.integers(0, cfg.vocab, size=N_PROMPT).tolist()
+    res = model.generate(prompt, N_GEN, graph=True)
+    toks = res.tokens
+    assert len(toks) == N_GEN
+    g_last = model._logits.cpu().numpy().copy()  # the replay at position N_PROMPT + N_GEN - 2
+    short = model.generate(prompt, 50, graph=True)
+    assert short.tokens == toks[:50], "replays of the same prompt diverged"
+    g_mid = model._logits.cpu().numpy().copy()  # position N_PROMPT + 48 = 560
+    eager = {}
+    logits = model.forward(prompt, 0).cpu().numpy()
+    choices = [logits]
+    for i in range(N_GEN - 1):
+        logits = model.forward([toks[i]], N_PROMPT + i).cpu().numpy()
+        eager[N_PROMPT + i] = logits
+        choices.append(logits)
+    assert np.all(np.isfinite(np.stack(choices)))
+    e_mid, e_last = _rel(g_mid, eager[N_PROMPT + 48]), _rel(g_last, eager[N_PROMPT + N_GEN - 2])
+    assert e_mid <= GRAPH_TOL_22, f"position {N_PROMPT + 48}: graph vs teacher-forced eager rel {e_mid:.3e}"
+    assert e_last <= GRAPH_TOL_22, f"position {N_PROMPT + N_GEN - 2}: graph vs eager rel {e_last:.3e}"
+    margin = 2.0 * max(e_mid, e_last)
+    clear = 0
+    for i, lg in enumerate(choices):
+        top2 = np.sort(lg)[-2:]
+        if top2[1] - top2[0] > margin * np.max(np.abs(lg)):
+            assert toks[i] == int(np.argmax(lg)), f"token {i}: graph chose {toks[i]}, eager argmax {int(np.argmax(lg))}"
+            clear += 1
+    print(f"\n128 graph steps: rel at 560 {e_mid:.2e}, at 638 {e_last:.2e}; {clear} of {N_GEN} tokens with a clear margin")
+    assert clear >= N_GEN // 16, f"only {clear} of {N_GEN} steps had a clear top-2 margin"
