@@ -50,6 +50,56 @@ __global__ void read_strided(const uint8_t *buf, uint32_t bytes, uint32_t *out) 
     if (acc == 0x9E3779B9u) out[blockIdx.x % 1024] = acc;
 }
 
+// The headline matvec's own access pattern, loads only: Q4_K weights of
+// rows of ng groups in the row-block tile layout (8-row blocks of ng * 9
+// pieces of 128 bytes, one 16-byte piece per row), taken in 56-row chunks;
+// lane l of a wavefront is row l of its chunk (lanes 56-63 idle) and
+// wavefront w of the chunk group w, P pieces in flight, as the row-per-lane
+// kernel walks them.  CM = false: the layout the library stores, so one load
+// instruction reads seven 128-byte lines one block (ng * 1152 bytes) apart;
+// CM = true: the same pieces stored chunk-major (the chunk's seven lines of a
+// piece next to each other), so it reads 896 contiguous bytes.  WAVES
+// wavefronts per workgroup, ng / WAVES workgroups per chunk.
+template <bool CM, int WAVES, int P>
+__global__ void read_pattern(const uint8_t *buf, int ng, uint32_t *out) {
+    constexpr int NPG = 9, ROWS = 56;
+    const uint32_t rbs = (uint32_t)ng * NPG * 128;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int per_chunk = ng / WAVES;
+    const int chunk = blockIdx.x / per_chunk;
+    const int g = (blockIdx.x % per_chunk) * WAVES + wave;
+    const rsrc_t r = buf_rsrc(buf + (size_t)chunk * (ROWS / 8) * rbs, (ROWS / 8) * rbs);
+    auto off = [&](int pc) -> uint32_t {
+        if (lane >= ROWS) return BUF_OOB;
+        return CM ? (uint32_t)((g * NPG + pc) * ROWS * 16 + lane * 16)
+                  : (uint32_t)((lane / 8) * rbs + (g * NPG + pc) * 128 + (lane % 8) * 16);
+    };
+    u32x4 ring[P];
+#pragma unroll
+    for (int j = 0; j < P; j++) ring[j] = __builtin_amdgcn_raw_buffer_load_b128(r, off(j), 0, BUF_NT);
+    uint32_t acc = 0;
+#pragma unroll
+    for (int j = 0; j < NPG; j++) {
+        acc ^= ring[j % P].x ^ ring[j % P].y ^ ring[j % P].z ^ ring[j % P].w;
+        if (j + P < NPG) ring[j % P] = __builtin_amdgcn_raw_buffer_load_b128(r, off(j + P), 0, BUF_NT);
+    }
+    if (acc == 0x9E3779B9u) out[blockIdx.x % 1024] = acc;
+}
+
+struct Pattern {
+    const char *name;
+    bool cm;
+    int waves, p;
+};
+const Pattern PATTERNS[] = {
+    {"matvec pattern: row-block layout, 1024-thread workgroups, 6 pieces in flight", false, 16, 6},
+    {"matvec pattern: row-block layout, 1024-thread workgroups, 9 pieces in flight", false, 16, 9},
+    {"matvec pattern: row-block layout, 256-thread workgroups, 6 pieces in flight", false, 4, 6},
+    {"matvec pattern: chunk-major layout, 1024-thread workgroups, 6 pieces in flight", true, 16, 6},
+    {"matvec pattern: chunk-major layout, 256-thread workgroups, 6 pieces in flight", true, 4, 6},
+};
+constexpr int N_PATTERNS = sizeof(PATTERNS) / sizeof(PATTERNS[0]);
+
 struct Member {
     const char *name;
     int oneshot, loads, threads, grid;  // grid 0: one-shot (from the byte count)
@@ -101,6 +151,33 @@ int aq_bench_read(int member, void *stream, const void *d_buf, size_t bytes, uin
     } else {
         if (m.loads == 4) read_strided<4><<<grid, m.threads, 0, s>>>(b, n, d_out);
         else read_strided<2><<<grid, m.threads, 0, s>>>(b, n, d_out);
+    }
+    return hipGetLastError() == hipSuccess ? 0 : -5;
+}
+
+int aq_bench_read_patterns(void) { return N_PATTERNS; }
+
+const char *aq_bench_read_pattern_name(int v) { return v >= 0 && v < N_PATTERNS ? PATTERNS[v].name : ""; }
+
+// Read the Q4_K weight of n rows x ng groups (n a multiple of 56, ng a
+// multiple of 16, at most 64; n * ng * 144 bytes of d_buf, 16-byte aligned)
+// in access pattern v.  Returns 0, -1 for bad arguments, -5 for a launch
+// error.
+int aq_bench_read_pattern(int v, void *stream, const void *d_buf, int n, int ng, uint32_t *d_out) {
+    if (v < 0 || v >= N_PATTERNS || !d_buf || !d_out || n <= 0 || n % 56 || ng <= 0 || ng % 16 || ng > 64 ||
+        (int64_t)n * ng * 144 >= ((int64_t)1 << 31) || ((uintptr_t)d_buf & 15))
+        return -1;
+    const Pattern &pt = PATTERNS[v];
+    const hipStream_t s = (hipStream_t)stream;
+    const uint8_t *b = (const uint8_t *)d_buf;
+    const unsigned grid = (unsigned)(n / 56) * (unsigned)(ng / pt.waves);
+    const unsigned thr = 64u * pt.waves;
+    switch (v) {
+    case 0: read_pattern<false, 16, 6><<<grid, thr, 0, s>>>(b, ng, d_out); break;
+    case 1: read_pattern<false, 16, 9><<<grid, thr, 0, s>>>(b, ng, d_out); break;
+    case 2: read_pattern<false, 4, 6><<<grid, thr, 0, s>>>(b, ng, d_out); break;
+    case 3: read_pattern<true, 16, 6><<<grid, thr, 0, s>>>(b, ng, d_out); break;
+    default: read_pattern<true, 4, 6><<<grid, thr, 0, s>>>(b, ng, d_out); break;
     }
     return hipGetLastError() == hipSuccess ? 0 : -5;
 }

@@ -436,12 +436,16 @@ def measure_vendor_int8(m, n, k, steps, warmup):
             "rotating_weight_copies": copies}
 
 
-def measure_read_family(ctx, nbytes, steps, warmup):
+def measure_read_family(ctx, nbytes, steps, warmup, pattern=None):
     """The read rate of kernels that only stream nbytes (the read-only family of
     libaq_bench.so, a measurement aid outside the product library), each over
     enough rotating buffers to exceed the Infinity Cache and timed like the
     matvec.  The fastest member is the practical ceiling for a single launch
-    of that many bytes on this GPU."""
+    of that many bytes on this GPU.  pattern = (rows, groups): also time
+    loads-only kernels in the Q4_K row-per-lane matvec's own access pattern
+    (56-row chunks, a wavefront per group) over that weight's bytes, and
+    variants of it (workgroup size, pieces in flight, chunk-major storage),
+    reported under "matvec_pattern"."""
     import ctypes
 
     from arm_ai_amd import hip
@@ -463,8 +467,26 @@ def measure_read_family(ctx, nbytes, steps, warmup):
         members.append({"kernel": lib.aq_bench_read_name(mb).decode(), "us": round(ms * 1e3, 3),
                         "GBps": round(gbps, 1), "frac_hbm": round(gbps / HBM_PEAK_GBS, 4)})
     best = min(members, key=lambda r: r["us"])
-    return {"kernel": best["kernel"], "bytes": nbytes, "us": best["us"], "GBps": best["GBps"],
-            "frac_hbm": best["frac_hbm"], "rotating_copies": copies, "family": members}
+    res = {"kernel": best["kernel"], "bytes": nbytes, "us": best["us"], "GBps": best["GBps"],
+           "frac_hbm": best["frac_hbm"], "rotating_copies": copies, "family": members}
+    if pattern is not None:
+        rows, ng = pattern
+        wbytes = rows * ng * 144
+        assert wbytes <= nbytes
+        lib.aq_bench_read_pattern_name.restype = ctypes.c_char_p
+        lib.aq_bench_read_pattern_name.argtypes = [ctypes.c_int]
+        lib.aq_bench_read_pattern.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int,
+                                              ctypes.c_int, ctypes.c_void_p]
+        pats = []
+        for v in range(lib.aq_bench_read_patterns()):
+            fn = lambda i, v=v: lib.aq_bench_read_pattern(v, ctx.stream, bufs[i % copies].ptr, rows, ng, out.ptr)
+            assert fn(0) == 0
+            ms, _ = time_graph(ctx, fn, steps, warmup)
+            gbps = wbytes / (ms / 1e3) / 1e9
+            pats.append({"kernel": lib.aq_bench_read_pattern_name(v).decode(), "bytes": wbytes,
+                         "us": round(ms * 1e3, 3), "GBps": round(gbps, 1), "frac_hbm": round(gbps / HBM_PEAK_GBS, 4)})
+        res["matvec_pattern"] = pats
+    return res
 
 
 def measure_mfma_rates(ctx):
@@ -679,7 +701,7 @@ def main() -> int:
             "avg_launch_us": round(step_ms * 1e3, 3),
         },
     }
-    ref = measure_read_family(ctx, wl.step_bytes, args.steps, args.warmup)
+    ref = measure_read_family(ctx, wl.step_bytes, args.steps, args.warmup, pattern=(wl.n, wl.k // 256))
     log(f"fastest of {len(ref['family'])} read-only kernels on the same {ref['bytes']} bytes: {ref['kernel']}, {ref['us']} us ({ref['GBps']} GB/s, {ref['frac_hbm']} of peak)")
     result["roofline"]["read_only_reference"] = ref
     result["roofline"]["frac_of_read_only_reference"] = round(achieved / ref["GBps"], 4)
