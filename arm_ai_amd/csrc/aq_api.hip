@@ -1040,6 +1040,39 @@ int aq_qmatmul_rmsnorm_f32_device(aq_ctx *ctx, const aq_qweight *w, const float 
     return hip_status(e, "matvec rmsnorm");
 }
 
+int aq_llama_swiglu_pairs(aq_ctx *ctx, const float *d_y, int64_t ld, int64_t m, int64_t ffn, float *d_out) {
+    if (!ctx) return fail(AQ_ERR_INVALID_ARG, "null context");
+    if (m == 0) return AQ_OK;
+    if (ffn <= 0 || ffn % 4) return fail(AQ_ERR_SHAPE, "ffn=%lld is not a positive multiple of 4", (long long)ffn);
+    int rc = use_device(ctx->device);
+    if (rc) return rc;
+    return hip_status(launch_swiglu_pairs(d_y, ld, m, ffn, d_out, ctx->stream), "swiglu pairs");
+}
+
+int aq_swiglu_fused(int type, int64_t n, int64_t k) {
+    return n > 0 && k > 0 && n % 8 == 0 && rowlane_xf_applies(type, n, k, RL_XF_NORM) ? 1 : 0;
+}
+
+int aq_qmatmul_rmsnorm_swiglu_f32_device(aq_ctx *ctx, const aq_qweight *w, const float *d_x, const float *d_delta,
+                                         const float *d_norm_w, float eps, int64_t k, float *d_h_out, float *d_dst) {
+    int rc = check_mm(ctx, w, 1, k);
+    if (rc) return rc;
+    if (!d_x || !d_norm_w || !d_dst) return fail(AQ_ERR_INVALID_ARG, "null pointer");
+    if (d_h_out && (d_h_out == d_x || d_h_out == d_delta)) return fail(AQ_ERR_INVALID_ARG, "d_h_out aliases an input");
+    if (w->n % 8) return fail(AQ_ERR_SHAPE, "n=%lld: a paired gate|up weight has whole 8-row blocks", (long long)w->n);
+    if ((rc = use_device(ctx->device))) return rc;
+    hipError_t e = launch_matvec_rmsnorm_swiglu(w->layout, w->n, w->k, d_x, d_delta, d_norm_w, eps, d_h_out, d_dst,
+                                                ctx->stream);
+    if (e != hipErrorNotSupported) return hip_status(e, "matvec rmsnorm swiglu");
+    // the fused-norm matmul into scratch, then the pairs
+    if ((rc = ensure_scratch(ctx, (size_t)w->n * sizeof(float)))) return rc;
+    float *y = (float *)ctx->scratch;
+    e = launch_matvec_rmsnorm(w->layout, w->n, w->k, d_x, d_delta, d_norm_w, eps, d_h_out, y, ctx->stream);
+    if (e == hipErrorNotSupported) return fail(AQ_ERR_SHAPE, "k=%lld is too long for the fused norm", (long long)k);
+    if (e != hipSuccess) return hip_status(e, "matvec rmsnorm");
+    return hip_status(launch_swiglu_pairs(y, w->n, 1, w->n / 2, d_dst, ctx->stream), "swiglu pairs");
+}
+
 int aq_qmatmul_silu_mul_f32_device(aq_ctx *ctx, const aq_qweight *w, const float *d_gu, int64_t k, float *d_dst) {
     int rc = check_mm(ctx, w, 1, k);
     if (rc) return rc;

@@ -153,13 +153,17 @@ hipError_t launch_matvec(const WLayout &w, int64_t n, int64_t k, const float *x,
 // planes of one row).  xf (x only, no dump): kind RL_XF_NORM quantises
 // rms_norm(x + delta) * w (k <= 8192; workgroup 0 writes x + delta to
 // xout), kind RL_XF_SILU takes x = [g | u] (2k floats) and quantises
-// silu(g) * u.
+// silu(g) * u.  swiglu (an output transform): the weight's rows are gate and
+// up rows in pairs of four (swiglu_pair_rows: rows 8b..8b+3 gate rows
+// 4b..4b+3, rows 8b+4..8b+7 the up rows of the same indices; n a multiple of
+// 8), and y receives the n / 2 values silu(g) * u in place of the n sums.
 constexpr int RL_XF_NONE = 0, RL_XF_NORM = 1, RL_XF_SILU = 2;
 struct RlXf {
     int kind;  // RL_XF_NORM or RL_XF_SILU
     const float *delta, *w;
     float eps;
     float *xout;
+    bool swiglu = false;
 };
 bool rowlane_matvec_applies(int type, int64_t n, int64_t k);
 bool rowlane_xf_applies(int type, int64_t n, int64_t k, int kind);
@@ -232,6 +236,11 @@ hipError_t launch_dequant_rows(int wt, const void *table, const float *scales, i
 hipError_t launch_matvec_rmsnorm(const WLayout &w, int64_t n, int64_t k, const float *x, const float *delta,
                                  const float *norm, float eps, float *xout, float *y, hipStream_t s);
 hipError_t launch_matvec_silu(const WLayout &w, int64_t n, int64_t k, const float *gu, float *y, hipStream_t s);
+// The fused-norm matvec of a weight of gate and up rows in pairs of four
+// (n a multiple of 8), writing the n / 2 values silu(g) * u to h; the
+// row-per-lane forms only (hipErrorNotSupported otherwise).
+hipError_t launch_matvec_rmsnorm_swiglu(const WLayout &w, int64_t n, int64_t k, const float *x, const float *delta,
+                                        const float *norm, float eps, float *xout, float *h, hipStream_t s);
 // Two fused-norm matvecs of the same row in one launch (Q4_K / Q6_K weights
 // w1 and w2, outputs y1 and y2); xout is written once.  hipErrorNotSupported
 // for other types or rows too long to fuse.
@@ -245,6 +254,9 @@ hipError_t launch_embed(const float *table, int64_t vocab, const int64_t *d_tok,
 hipError_t launch_rmsnorm(float *x, const float *delta, const float *w, int64_t m, int64_t n, float eps, float *out,
                           hipStream_t s);
 hipError_t launch_silu_mul(const float *g, const float *u, int64_t ld, int64_t m, int64_t n, float *out, hipStream_t s);
+// silu(g) * u of m rows of a paired gate|up weight's output (row stride ld,
+// n = the number of pairs, a multiple of 4)
+hipError_t launch_swiglu_pairs(const float *y, int64_t ld, int64_t m, int64_t n, float *out, hipStream_t s);
 hipError_t launch_attn_decode(const float *qk, const float *v, const float *cosb, const float *sinb,
                               const int64_t *d_pos, float *kc, float *vc, int64_t n_head, int64_t n_kv, int64_t hd,
                               int64_t max_seq, float *out, hipStream_t s);

@@ -126,6 +126,20 @@ __global__ __launch_bounds__(DEC_THREADS) void silu_mul_kernel(const float *__re
     out[r * n + i] = (gv / (1.0f + expf(-gv))) * u[r * ld + i];
 }
 
+// out[r][i] = silu(g) * u for the output row r (grid y) of a weight whose
+// rows are gate and up rows in pairs of four (row 8b + j: gate row 4b + j
+// for j < 4, up row 4b + j - 4 after): g = y[r][8(i/4) + i%4], u four places
+// on.  n (a multiple of 4) outputs per row; row r of y starts at r * ld.
+__global__ __launch_bounds__(DEC_THREADS) void swiglu_pairs_kernel(const float *__restrict__ y, int64_t ld, int64_t n,
+                                                                   float *__restrict__ out) {
+    const int64_t i = (int64_t)blockIdx.x * DEC_THREADS + threadIdx.x;
+    if (i >= n) return;
+    const int64_t r = blockIdx.y;
+    const int64_t j = r * ld + 8 * (i >> 2) + (i & 3);
+    const float gv = y[j];
+    out[r * n + i] = (gv / (1.0f + expf(-gv))) * y[j + 4];
+}
+
 // Sum over aligned groups of N lanes (N = 2, 4, 8, 16, 32 or 64), every lane
 // of a group getting the same value: DPP moves within 16-lane rows (quad
 // swaps, half-row mirror, row rotations), cross-lane permutes only between
@@ -414,6 +428,13 @@ hipError_t launch_silu_mul(const float *g, const float *u, int64_t ld, int64_t m
     if (!g || !u || !out || n <= 0 || m <= 0 || m > 65535 || (m > 1 && ld < n)) return hipErrorInvalidValue;
     const dim3 grid((unsigned)((n + DEC_THREADS - 1) / DEC_THREADS), (unsigned)m);
     silu_mul_kernel<<<grid, DEC_THREADS, 0, s>>>(g, u, ld, n, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_swiglu_pairs(const float *y, int64_t ld, int64_t m, int64_t n, float *out, hipStream_t s) {
+    if (!y || !out || n <= 0 || n % 4 || m <= 0 || m > 65535 || (m > 1 && ld < 2 * n)) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)((n + DEC_THREADS - 1) / DEC_THREADS), (unsigned)m);
+    swiglu_pairs_kernel<<<grid, DEC_THREADS, 0, s>>>(y, ld, n, out);
     return hipGetLastError();
 }
 

@@ -1001,6 +1001,17 @@ hipError_t launch_matvec_rmsnorm(const WLayout &w, int64_t n, int64_t k, const f
     return matvec_impl(w, n, k, x, nullptr, 1, y, nullptr, nullptr, xa, s);
 }
 
+hipError_t launch_matvec_rmsnorm_swiglu(const WLayout &w, int64_t n, int64_t k, const float *x, const float *delta,
+                                        const float *norm, float eps, float *xout, float *h, hipStream_t s) {
+    if ((delta && ((uintptr_t)delta & 15)) || !norm || ((uintptr_t)norm & 15) || (xout && ((uintptr_t)xout & 15)) ||
+        n % 8)
+        return hipErrorInvalidValue;
+    if (!rowlane_xf_applies(w.type, n, k, RL_XF_NORM)) return hipErrorNotSupported;
+    RlXf rx{RL_XF_NORM, delta, norm, eps, xout};
+    rx.swiglu = true;
+    return launch_rowlane_matvec(w, n, k, x, nullptr, h, nullptr, nullptr, s, &rx);
+}
+
 hipError_t launch_matvec_silu(const WLayout &w, int64_t n, int64_t k, const float *gu, float *y, hipStream_t s) {
     XfArgs xa;
     xa.xf = XF_SILU;

@@ -67,6 +67,7 @@ struct RlParams {
     int xf;            // RL_XF_NONE / _NORM / _SILU (see rl_body)
     ActPlanes act;     // pre-quantised planes (x null)
     float *y;
+    int swiglu;        // y[4b + j] = silu(row 8b + j) * row (8b + 4 + j), j < 4
     int32_t *S, *Smin;  // [n][ng] integer dump, or null
 };
 
@@ -631,7 +632,18 @@ __device__ __forceinline__ void rl_body(const RlParams p, const int bid, const i
     if (GP >= 2) f += __shfl_xor(f, 32);
     red[CH ? it & 1 : 0][wave][lane] = f;
     lds_barrier();
-    if (wave == 0 && rok && gp == 0) {
+    if (p.swiglu) {  // uniform
+        // every lane of wavefront 0 holds the sum of row (its lane mod R);
+        // an 8-row block's gate rows 0-3 take their up rows 4-7 four lanes
+        // on, and write candle's silu(g) * u = (g / (1 + e^-g)) * u
+        if (wave == 0) {
+            float t = 0.0f;
+#pragma unroll
+            for (int w = 0; w < W; w++) t += red[CH ? it & 1 : 0][w][lane];
+            const float u = __shfl_down(t, 4);
+            if (rok && gp == 0 && (row & 4) == 0) p.y[(row >> 3) * 4 + (row & 3)] = (t / (1.0f + expf(-t))) * u;
+        }
+    } else if (wave == 0 && rok && gp == 0) {
         float t = 0.0f;
 #pragma unroll
         for (int w = 0; w < W; w++) t += red[CH ? it & 1 : 0][w][lane];
@@ -757,6 +769,7 @@ hipError_t rl_params(const WLayout &w, int64_t n, int64_t k, const float *x, con
     if (xf && (!x || S || (xf->kind != RL_XF_NORM && xf->kind != RL_XF_SILU) || (xf->kind == RL_XF_NORM && !xf->w)))
         return hipErrorInvalidValue;
     if (xf && !rowlane_xf_applies(w.type, n, k, xf->kind)) return hipErrorNotSupported;
+    if (xf && xf->swiglu && n % RB) return hipErrorInvalidValue;  // whole 8-row blocks of four gate, four up rows
     const int ng = (int)(k / QK_K);
     const int npg = slabs_of(w.type);
     if (w.ng != ng || w.rb_stride != (int64_t)ng * npg * 128) return hipErrorInvalidValue;
@@ -778,6 +791,7 @@ hipError_t rl_params(const WLayout &w, int64_t n, int64_t k, const float *x, con
     p.eps = xf ? xf->eps : 0.0f;
     p.act = act ? *act : ActPlanes{};
     p.y = y;
+    p.swiglu = xf && xf->swiglu ? 1 : 0;
     p.S = S;
     p.Smin = Smin;
     return hipSuccess;
@@ -820,6 +834,7 @@ hipError_t launch_rowlane_matvec(const WLayout &w, int64_t n, int64_t k, const f
 
 hipError_t launch_rowlane_matvec2(const WLayout &w1, int64_t n1, float *y1, const WLayout &w2, int64_t n2, float *y2,
                                   int64_t k, const float *x, const RlXf &xf, hipStream_t s) {
+    if (xf.swiglu) return hipErrorNotSupported;
     RlParams p1, p2;
     hipError_t e = rl_params(w1, n1, k, x, nullptr, y1, nullptr, nullptr, &xf, p1);
     if (e != hipSuccess) return e;

@@ -183,6 +183,23 @@ def synthetic_weights(cfg: LlamaConfig, seed: int = 0, types=tinyllama_q4km_type
     return hw
 
 
+def swiglu_pair_rows(w1: QTensor, w3: QTensor) -> QTensor:
+    """The gate (w1) and up (w3) projections as one weight of gate and up rows
+    in pairs of four: row 8b + j is w1 row 4b + j for j < 4, w3 row 4b + j - 4
+    for j >= 4.  One matmul then gives both, and silu(g) * u of index i sits
+    in output columns 8(i / 4) + i % 4 and four on (aq_llama_swiglu_pairs), so
+    a matvec kernel can close each 8-row block with its four SwiGLU values
+    (aq_qmatmul_rmsnorm_swiglu_f32_device).  The rows are the quantized
+    blocks of the two tensors, unchanged."""
+    if w1.dtype != w3.dtype or w1.shape != w3.shape or w1.shape[0] % 4:
+        raise ValueError("w1 and w3 need one type, one shape and rows in whole fours")
+    ffn = w1.shape[0]
+    rb = w1.data.size // ffn  # bytes per row
+    a = np.asarray(w1.data).reshape(ffn // 4, 1, 4 * rb)
+    b = np.asarray(w3.data).reshape(ffn // 4, 1, 4 * rb)
+    return QTensor(w1.dtype, (2 * ffn, w1.shape[1]), np.concatenate([a, b], axis=1).reshape(-1))
+
+
 def rope_tables(cfg: LlamaConfig, n_pos: int) -> tuple[np.ndarray, np.ndarray]:
     """cos, sin [n_pos][head_dim/2] as candle's precompute_freqs_cis (f32)."""
     hd = cfg.head_dim
@@ -250,18 +267,33 @@ class Llama:
         self._hidden = None  # {layer index: residual input} while capture_hidden is active
 
     def _upload_layer(self, layer: dict[str, QTensor]) -> dict[str, QMatMul]:
-        """The layer's projections in HBM; wq|wk and w1|w3 become one weight each
-        (rows concatenated) when the pair has one type, so one launch serves both."""
+        """The layer's projections in HBM; when a pair has one type, one weight
+        serves both: wq|wk with its rows concatenated ("wqk"), w1|w3 as gate
+        and up rows in pairs of four ("w13p", swiglu_pair_rows) where the
+        decode matvec then forms silu(g) * u in the same launch
+        (aq_swiglu_fused), else concatenated ("w13")."""
+        from . import _lib
+
         out = {}
-        for a, b, name in (("wq", "wk", "wqk"), ("w1", "w3", "w13")):
-            qa, qb = layer[a], layer[b]
-            if qa.dtype == qb.dtype and qa.shape[1] == qb.shape[1]:
-                cat = QTensor(qa.dtype, (qa.shape[0] + qb.shape[0], qa.shape[1]),
-                              np.concatenate([qa.data.reshape(-1), qb.data.reshape(-1)]))
-                out[name] = QMatMul.from_qtensor(cat, self.ctx)
-            else:
-                out[a] = QMatMul.from_qtensor(qa, self.ctx)
-                out[b] = QMatMul.from_qtensor(qb, self.ctx)
+        qa, qb = layer["wq"], layer["wk"]
+        if qa.dtype == qb.dtype and qa.shape[1] == qb.shape[1]:
+            cat = QTensor(qa.dtype, (qa.shape[0] + qb.shape[0], qa.shape[1]),
+                          np.concatenate([qa.data.reshape(-1), qb.data.reshape(-1)]))
+            out["wqk"] = QMatMul.from_qtensor(cat, self.ctx)
+        else:
+            out["wq"] = QMatMul.from_qtensor(qa, self.ctx)
+            out["wk"] = QMatMul.from_qtensor(qb, self.ctx)
+        qa, qb = layer["w1"], layer["w3"]
+        if qa.dtype == qb.dtype and qa.shape == qb.shape and qa.shape[0] % 4 == 0 and \
+                _lib.load().aq_swiglu_fused(int(qa.dtype), 2 * qa.shape[0], qa.shape[1]):
+            out["w13p"] = QMatMul.from_qtensor(swiglu_pair_rows(qa, qb), self.ctx)
+        elif qa.dtype == qb.dtype and qa.shape[1] == qb.shape[1]:
+            cat = QTensor(qa.dtype, (qa.shape[0] + qb.shape[0], qa.shape[1]),
+                          np.concatenate([qa.data.reshape(-1), qb.data.reshape(-1)]))
+            out["w13"] = QMatMul.from_qtensor(cat, self.ctx)
+        else:
+            out["w1"] = QMatMul.from_qtensor(qa, self.ctx)
+            out["w3"] = QMatMul.from_qtensor(qb, self.ctx)
         for name in ("wv", "wo", "w2"):
             out[name] = QMatMul.from_qtensor(layer[name], self.ctx)
         return out
@@ -388,8 +420,12 @@ class Llama:
                                             ptr(self.v_cache[li]), H, Hkv, D, cfg.max_seq, ptr(y)))
                 o = self._mm(lw["wo"], y)
                 chk(L.aq_llama_rmsnorm(c, ptr(x), ptr(o), ptr(self.ffn_norm[li]), n, cfg.hidden, eps, ptr(h)))
-                g, u = self._pair(lw, "w13", "w1", "w3", h)
-                chk(L.aq_llama_silu_mul_rows(c, ptr(g), ptr(u), g.stride(0), n, cfg.ffn, ptr(a)))
+                if "w13p" in lw:  # gate and up rows in pairs of four
+                    gu = self._mm(lw["w13p"], h)
+                    chk(L.aq_llama_swiglu_pairs(c, ptr(gu), gu.stride(0), n, cfg.ffn, ptr(a)))
+                else:
+                    g, u = self._pair(lw, "w13", "w1", "w3", h)
+                    chk(L.aq_llama_silu_mul_rows(c, ptr(g), ptr(u), g.stride(0), n, cfg.ffn, ptr(a)))
                 delta = self._mm(lw["w2"], a)
             self._trace_layer = len(self.layers)
             self._record_hidden(len(self.layers), x, delta)
@@ -417,6 +453,7 @@ class Llama:
         self._att = torch.zeros(cfg.n_head * hd, **f32)
         self._o = torch.zeros(cfg.hidden, **f32)       # wo output
         self._gu = torch.zeros(2 * cfg.ffn, **f32)
+        self._a = torch.zeros(cfg.ffn, **f32)         # silu(g) * u
         self._d = torch.zeros(cfg.hidden, **f32)       # w2 output (the pending residual delta)
         self._logits = torch.zeros(cfg.vocab, **f32)
 
@@ -425,11 +462,14 @@ class Llama:
         (both device memory); leaves the logits in self._logits, the next token
         in self._tok and in self._hist[pos], and pos + 1 in self._pos.
 
-        Per layer five launches: the QMatMuls of wq|wk and wv, one launch for
+        Per layer six launches: the QMatMuls of wq|wk and wv, one launch for
         both, take rms_norm(x + delta) as their input (formed inside the
         matvec, which also writes the residual x + delta once), attention
-        (RoPE, KV write, GQA), wo, w1|w3 on rms_norm(h + wo), w2 on
-        silu(g) * u."""
+        (RoPE, KV write, GQA: a split launch and a combining launch), wo,
+        w1|w3 on rms_norm(h + wo), w2.  silu(g) * u is formed by the w1|w3
+        launch where its gate and up rows are paired ("w13p": each 8-row
+        block closes with four SwiGLU values), else by the w2 launch's
+        prologue from [g | u]."""
         from . import _lib
 
         L = _lib.load()
@@ -465,12 +505,17 @@ class Llama:
                                        cfg.max_seq, ptr(self._att)))
             lw["wo"].forward_device(ptr(self._att), 1, ptr(self._o))
             fn = self.ffn_norm[li]
-            if "w13" in lw:
-                mm_norm(lw["w13"], other, ptr(self._o), fn, ptr(self._gu), h_out=cur)
-            else:
-                mm_norm(lw["w1"], other, ptr(self._o), fn, ptr(self._gu), h_out=cur)
-                mm_norm(lw["w3"], other, ptr(self._o), fn, ptr(self._gu) + 4 * cfg.ffn)
-            chk(L.aq_qmatmul_silu_mul_f32_device(c, lw["w2"].handle, ptr(self._gu), cfg.ffn, ptr(self._d)))
+            if "w13p" in lw:  # silu(g) * u formed by the w1|w3 launch, w2 on it
+                chk(L.aq_qmatmul_rmsnorm_swiglu_f32_device(c, lw["w13p"].handle, ptr(other), ptr(self._o), ptr(fn),
+                                                           eps, cfg.hidden, ptr(cur), ptr(self._a)))
+                lw["w2"].forward_device(ptr(self._a), 1, ptr(self._d))
+            else:  # [g | u], silu(g) * u formed by the w2 launch
+                if "w13" in lw:
+                    mm_norm(lw["w13"], other, ptr(self._o), fn, ptr(self._gu), h_out=cur)
+                else:
+                    mm_norm(lw["w1"], other, ptr(self._o), fn, ptr(self._gu), h_out=cur)
+                    mm_norm(lw["w3"], other, ptr(self._o), fn, ptr(self._gu) + 4 * cfg.ffn)
+                chk(L.aq_qmatmul_silu_mul_f32_device(c, lw["w2"].handle, ptr(self._gu), cfg.ffn, ptr(self._d)))
             delta = ptr(self._d)  # the residual is now x + wo + w2 = cur + d
         mm_norm(self.output, cur, delta, self.norm, ptr(self._logits))
         chk(L.aq_llama_argmax(c, ptr(self._logits), cfg.vocab, ptr(self._tok), ptr(self._pos), ptr(self._hist),

@@ -320,6 +320,29 @@ int aq_qmatmul_silu_mul_f32_device(aq_ctx *ctx, const aq_qweight *w, const float
 int aq_qmatmul2_rmsnorm_f32_device(aq_ctx *ctx, const aq_qweight *w1, const aq_qweight *w2, const float *d_x,
                                    const float *d_delta, const float *d_norm_w, float eps, int64_t k, float *d_h_out,
                                    float *d_dst1, float *d_dst2);
+/* Paired gate|up weights (the SwiGLU MLP, silu(w1 x) * (w3 x)).  A weight
+ * holding the gate (w1) and up (w3) rows in pairs of four -- row 8b + j is
+ * gate row 4b + j for j < 4 and up row 4b + j - 4 for j >= 4; n = 2 * ffn,
+ * ffn a multiple of 4 (arm_ai_amd.llama.swiglu_pair_rows builds it) --
+ * yields silu(g) * u without splitting its output:
+ * aq_llama_swiglu_pairs: d_out[r][i] = silu(g) * u, i < ffn, of row r of
+ *   such a weight's output d_y (row stride ld >= 2 * ffn; m <= 65535).
+ * aq_qmatmul_rmsnorm_swiglu_f32_device: aq_qmatmul_rmsnorm_f32_device on such
+ *   a weight, writing the ffn values silu(g) * u to d_dst in place of the n
+ *   sums; the same values as the fused-norm matmul followed by
+ *   aq_llama_swiglu_pairs (the row-per-lane forms apply silu in the matmul
+ *   kernel; other shapes run those two steps, the matmul output in the
+ *   context's scratch). */
+int aq_llama_swiglu_pairs(aq_ctx *ctx, const float *d_y, int64_t ld, int64_t m, int64_t ffn, float *d_out);
+/* 1 when aq_qmatmul_rmsnorm_swiglu_f32_device forms silu(g) * u inside the
+ * matmul launch for a paired weight of this type (AQ_TYPE_*) and shape (n
+ * rows, k columns), else 0 (it would run the matmul and the pairs as two
+ * launches, and a caller keeping the two halves apart -- rows concatenated,
+ * aq_qmatmul_silu_mul_f32_device on [g | u] -- launches fewer kernels).  No
+ * GPU call. */
+int aq_swiglu_fused(int type, int64_t n, int64_t k);
+int aq_qmatmul_rmsnorm_swiglu_f32_device(aq_ctx *ctx, const aq_qweight *w, const float *d_x, const float *d_delta,
+                                         const float *d_norm_w, float eps, int64_t k, float *d_h_out, float *d_dst);
 /* Greedy pick: the first index of the largest of d_x[0..n) (d_x 16-byte
  * aligned, any n >= 1) goes to *d_tok and, when d_hist is non-null and
  * 0 <= *d_pos < hist_len, to d_hist[*d_pos]; then *d_pos += 1. */

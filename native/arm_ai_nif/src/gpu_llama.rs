@@ -60,6 +60,8 @@ impl Config {
 /// (same GGUF type), or two.
 enum Pair {
     Merged(GpuQMatMul),
+    /// w1|w3 as gate and up rows in pairs of four (see upload_pair)
+    Paired(GpuQMatMul),
     Split(GpuQMatMul, GpuQMatMul),
 }
 
@@ -187,18 +189,32 @@ fn upload(ctx: &GpuCtx, g: &mut Gguf, name: &str) -> Result<GpuQMatMul, String> 
     GpuQMatMul::from_blocks(ctx, ty, &bytes, n, k)
 }
 
-/// wq|wk, w1|w3: one weight of both tensors' rows when they share a type.
-fn upload_pair(ctx: &GpuCtx, g: &mut Gguf, a: &str, b: &str) -> Result<Pair, String> {
+/// wq|wk, w1|w3: one weight of both tensors' rows when they share a type,
+/// concatenated -- except w1|w3 (`swiglu`) where the decode matvec forms
+/// silu(g) * u in its own launch (aq_swiglu_fused): there one weight of gate
+/// and up rows in pairs of four (row 8b + j is gate row 4b + j for j < 4, up
+/// row 4b + j - 4 after; aq_qmatmul_rmsnorm_swiglu_f32_device,
+/// aq_llama_swiglu_pairs), as arm_ai_amd.llama.swiglu_pair_rows builds it.
+fn upload_pair(ctx: &GpuCtx, g: &mut Gguf, a: &str, b: &str, swiglu: bool) -> Result<Pair, String> {
     let (da, (na, ka), mut ba) = g.raw(a)?;
     let (db, (nb, kb), bb) = g.raw(b)?;
     let ta = aq_type(da).ok_or_else(|| format!("{a}: unsupported dtype {da:?}"))?;
     let tb = aq_type(db).ok_or_else(|| format!("{b}: unsupported dtype {db:?}"))?;
-    if ta == tb && ka == kb {
-        ba.extend_from_slice(&bb);
-        Ok(Pair::Merged(GpuQMatMul::from_blocks(ctx, ta, &ba, na + nb, ka)?))
-    } else {
-        Ok(Pair::Split(GpuQMatMul::from_blocks(ctx, ta, &ba, na, ka)?, GpuQMatMul::from_blocks(ctx, tb, &bb, nb, kb)?))
+    if ta != tb || ka != kb {
+        return Ok(Pair::Split(GpuQMatMul::from_blocks(ctx, ta, &ba, na, ka)?,
+                              GpuQMatMul::from_blocks(ctx, tb, &bb, nb, kb)?));
     }
+    if swiglu && na == nb && na % 4 == 0 && unsafe { aq_swiglu_fused(ta, (na + nb) as i64, ka as i64) } == 1 {
+        let four = ba.len() / na * 4;  // the bytes of four rows
+        let mut out = Vec::with_capacity(ba.len() + bb.len());
+        for (x, y) in ba.chunks(four).zip(bb.chunks(four)) {
+            out.extend_from_slice(x);
+            out.extend_from_slice(y);
+        }
+        return Ok(Pair::Paired(GpuQMatMul::from_blocks(ctx, ta, &out, na + nb, ka)?));
+    }
+    ba.extend_from_slice(&bb);
+    Ok(Pair::Merged(GpuQMatMul::from_blocks(ctx, ta, &ba, na + nb, ka)?))
 }
 
 /// Load a GGUF Llama-family model (llama_candle.rs:35-48) onto GPU 0.
@@ -240,10 +256,10 @@ pub fn load_model_on(path: &str, device: i32, max_seq: usize) -> Result<LlamaRes
     for i in 0..cfg.n_layer {
         let p = |s: &str| format!("blk.{i}.{s}.weight");
         layers.push(Layer {
-            wqk: upload_pair(&ctx, &mut g, &p("attn_q"), &p("attn_k"))?,
+            wqk: upload_pair(&ctx, &mut g, &p("attn_q"), &p("attn_k"), false)?,
             wv: upload(&ctx, &mut g, &p("attn_v"))?,
             wo: upload(&ctx, &mut g, &p("attn_output"))?,
-            w13: upload_pair(&ctx, &mut g, &p("ffn_gate"), &p("ffn_up"))?,
+            w13: upload_pair(&ctx, &mut g, &p("ffn_gate"), &p("ffn_up"), true)?,
             w2: upload(&ctx, &mut g, &p("ffn_down"))?,
             attn_norm: DeviceBuf::from_slice(&g.f32(&p("attn_norm"))?, stream)?,
             ffn_norm: DeviceBuf::from_slice(&g.f32(&p("ffn_norm"))?, stream)?,
@@ -360,7 +376,7 @@ impl GpuLlama {
             check(unsafe { aq_llama_rmsnorm(c, p.x.f32(), delta, l.attn_norm.f32(), n64, hid, cfg.eps, p.h.f32()) },
                   "rmsnorm")?;
             let (q, ldq, k, ldk) = match &l.wqk {
-                Pair::Merged(w) => {
+                Pair::Merged(w) | Pair::Paired(w) => {  // (wq|wk is never paired)
                     w.forward_device(p.h.f32(), n, p.qk.f32())?;
                     (p.qk.f32(), (h_ + kv) * hd, p.qk.f32_at(h_ * hd), (h_ + kv) * hd)
                 }
@@ -380,18 +396,24 @@ impl GpuLlama {
             l.wo.forward_device(p.y.f32(), n, p.o.f32())?;
             check(unsafe { aq_llama_rmsnorm(c, p.x.f32(), p.o.f32(), l.ffn_norm.f32(), n64, hid, cfg.eps, p.h.f32()) },
                   "rmsnorm")?;
-            let (g, u, ld) = match &l.w13 {
+            match &l.w13 {
+                Pair::Paired(w) => {  // gate and up rows in pairs of four
+                    w.forward_device(p.h.f32(), n, p.gu.f32())?;
+                    check(unsafe { aq_llama_swiglu_pairs(c, p.gu.f32(), (2 * cfg.ffn) as i64, n64, cfg.ffn as i64,
+                                                         p.a.f32()) }, "swiglu_pairs")?;
+                }
                 Pair::Merged(w) => {
                     w.forward_device(p.h.f32(), n, p.gu.f32())?;
-                    (p.gu.f32(), p.gu.f32_at(cfg.ffn), 2 * cfg.ffn)
+                    check(unsafe { aq_llama_silu_mul_rows(c, p.gu.f32(), p.gu.f32_at(cfg.ffn), (2 * cfg.ffn) as i64,
+                                                          n64, cfg.ffn as i64, p.a.f32()) }, "silu_mul")?;
                 }
                 Pair::Split(w1, w3) => {
                     w1.forward_device(p.h.f32(), n, p.gu.f32())?;
                     w3.forward_device(p.h.f32(), n, p.gu.f32_at(n * cfg.ffn))?;
-                    (p.gu.f32(), p.gu.f32_at(n * cfg.ffn), cfg.ffn)
+                    check(unsafe { aq_llama_silu_mul_rows(c, p.gu.f32(), p.gu.f32_at(n * cfg.ffn), cfg.ffn as i64,
+                                                          n64, cfg.ffn as i64, p.a.f32()) }, "silu_mul")?;
                 }
-            };
-            check(unsafe { aq_llama_silu_mul_rows(c, g, u, ld as i64, n64, cfg.ffn as i64, p.a.f32()) }, "silu_mul")?;
+            }
             l.w2.forward_device(p.a.f32(), n, p.d.f32())?;
             delta = p.d.f32();
         }
@@ -450,7 +472,7 @@ impl GpuLlama {
                     aq_qmatmul2_rmsnorm_f32_device(c, w.w, l.wv.w, cur, delta, an, cfg.eps, hid, other, s.qk.f32(),
                                                    s.v.f32())
                 }, "qmatmul2 rmsnorm")?,
-                Pair::Merged(w) => {
+                Pair::Merged(w) | Pair::Paired(w) => {  // (wq|wk is never paired)
                     mm_norm(w, cur, delta, an, s.qk.f32(), other)?;
                     mm_norm(&l.wv, cur, delta, an, s.v.f32(), std::ptr::null_mut())?;
                 }
@@ -468,14 +490,24 @@ impl GpuLlama {
             l.wo.forward_device(s.att.f32(), 1, s.o.f32())?;
             let fnm = l.ffn_norm.f32();
             match &l.w13 {
-                Pair::Merged(w) => mm_norm(w, other, s.o.f32(), fnm, s.gu.f32(), cur)?,
-                Pair::Split(w1, w3) => {
-                    mm_norm(w1, other, s.o.f32(), fnm, s.gu.f32(), cur)?;
-                    mm_norm(w3, other, s.o.f32(), fnm, s.gu.f32_at(cfg.ffn), std::ptr::null_mut())?;
+                Pair::Paired(w) => {  // silu(g) * u formed by the w1|w3 launch, w2 on it
+                    check(unsafe { aq_qmatmul_rmsnorm_swiglu_f32_device(c, w.w, other, s.o.f32(), fnm, cfg.eps,
+                                                                        cfg.hidden as i64, cur, s.gu.f32()) },
+                          "qmatmul rmsnorm swiglu")?;
+                    l.w2.forward_device(s.gu.f32(), 1, s.d.f32())?;
+                }
+                _ => {  // [g | u], silu(g) * u formed by the w2 launch
+                    match &l.w13 {
+                        Pair::Split(w1, w3) => {
+                            mm_norm(w1, other, s.o.f32(), fnm, s.gu.f32(), cur)?;
+                            mm_norm(w3, other, s.o.f32(), fnm, s.gu.f32_at(cfg.ffn), std::ptr::null_mut())?;
+                        }
+                        Pair::Merged(w) | Pair::Paired(w) => mm_norm(w, other, s.o.f32(), fnm, s.gu.f32(), cur)?,
+                    }
+                    check(unsafe { aq_qmatmul_silu_mul_f32_device(c, l.w2.w, s.gu.f32(), cfg.ffn as i64, s.d.f32()) },
+                          "qmatmul silu")?;
                 }
             }
-            check(unsafe { aq_qmatmul_silu_mul_f32_device(c, l.w2.w, s.gu.f32(), cfg.ffn as i64, s.d.f32()) },
-                  "qmatmul silu")?;
             // the residual x + wo + w2 is now cur + d: the next layer's norm
             // input, with `other` again receiving the sum
             delta = s.d.f32();

@@ -82,3 +82,20 @@ def test_header_types_match_gguf_ids():
     for name, val in (("Q8_0", 8), ("Q4_K", 12), ("Q6_K", 14), ("Q8_K", 15)):
         assert re.search(rf"AQ_TYPE_{name}\s*=\s*{val}\b", src)
         assert int(getattr(A.GgmlDType, name.replace("_K", "K") if name != "Q8_0" else name)) == val
+
+
+def test_swiglu_fused_query():
+    """aq_swiglu_fused: which paired gate|up weights get silu(g) * u inside the
+    matvec launch (the row-per-lane forms with the fused norm, whole 8-row
+    blocks); a pure host query."""
+    L = _lib.load()
+    Q4K, Q6K, Q8_0, Q5_0 = 12, 14, 8, 6
+    assert L.aq_swiglu_fused(Q4K, 11264, 2048) == 1   # TinyLlama w1|w3
+    assert L.aq_swiglu_fused(Q4K, 28672, 4096) == 1   # Llama-3-8B w1|w3
+    assert L.aq_swiglu_fused(Q6K, 1024, 4096) == 1
+    assert L.aq_swiglu_fused(Q8_0, 2048, 2048) == 1
+    assert L.aq_swiglu_fused(Q5_0, 3072, 576) == 0    # SmolLM-135M: rows of 576
+    assert L.aq_swiglu_fused(Q4K, 200, 1024) == 0     # below 256 rows
+    assert L.aq_swiglu_fused(Q4K, 11260, 2048) == 0   # not whole 8-row blocks
+    assert L.aq_swiglu_fused(Q4K, 11264, 16384) == 0  # too long a row for the fused norm
+    assert L.aq_swiglu_fused(Q4K, 0, 2048) == 0 and L.aq_swiglu_fused(99, 11264, 2048) == 0

@@ -315,6 +315,95 @@ def test_matvec_fused_silu_mul(env, wtype, n, k):
     mm.free()
 
 
+def _unpair(y, ffn):
+    p = np.asarray(y).reshape(-1, ffn // 4, 2, 4)
+    return p[:, :, 0, :].reshape(-1, ffn), p[:, :, 1, :].reshape(-1, ffn)
+
+
+def test_swiglu_pairs(env):
+    """silu(g) * u of rows of a paired gate|up output (column 8b + j: gate 4b + j
+    for j < 4, up four on), rows at a stride wider than the row: the same
+    values as aq_llama_silu_mul_rows on the split halves, bit for bit, and
+    candle's formula within f32 rounding."""
+    torch, lib, ctx = env
+    L = lib.load()
+    rng = np.random.default_rng(3)
+    m, ffn, ld = 3, 5632, 2 * 5632 + 8
+    y = (4 * rng.standard_normal((m, ld))).astype(np.float32)
+    y[0, 0], y[1, 9] = -100.0, 100.0  # exp overflow / underflow ends (gate entries)
+    dy = _dev(torch, y)
+    out = torch.empty((m, ffn), dtype=torch.float32, device="cuda:0")
+    lib.check(L.aq_llama_swiglu_pairs(ctx.handle, dy.data_ptr(), ld, m, ffn, out.data_ptr()))
+    g, u = _unpair(y[:, :2 * ffn], ffn)
+    dg, du = _dev(torch, g), _dev(torch, u)
+    o2 = torch.empty((m, ffn), dtype=torch.float32, device="cuda:0")
+    lib.check(L.aq_llama_silu_mul_rows(ctx.handle, dg.data_ptr(), du.data_ptr(), ffn, m, ffn, o2.data_ptr()))
+    ctx.synchronize()
+    got = out.cpu().numpy()
+    assert np.array_equal(got, o2.cpu().numpy())
+    g64, u64 = g.astype(np.float64), u.astype(np.float64)
+    assert np.all(np.isfinite(got))
+    assert _rel(got, g64 / (1 + np.exp(-g64)) * u64) <= 1e-5
+    assert L.aq_llama_swiglu_pairs(ctx.handle, dy.data_ptr(), ld, m, 5630, out.data_ptr()) == lib.AQ_ERR_SHAPE
+
+
+@pytest.mark.parametrize("wtype,n,k", [
+    (12, 11264, 2048),   # TinyLlama w1|w3: 56-row workgroups
+    (12, 28672, 4096),   # Llama-3-8B w1|w3: 56-row workgroups, 16 wavefronts
+    (14, 11264, 2048),   # Q6_K, 56 rows
+    (12, 1024, 4096),    # the 16-row form
+    (14, 1600, 2048),    # the 8-row form
+    (8, 2048, 2048),     # Q8_0 (8-row form, Q8_0-block activation)
+    (12, 200, 1024),     # below 256 rows: the general fused-norm matmul, then the pairs
+])
+def test_matvec_fused_rmsnorm_swiglu(env, wtype, n, k):
+    """The fused-norm matvec of a paired gate|up weight writing silu(g) * u:
+    bit for bit the fused-norm matvec of the same weight followed by
+    aq_llama_swiglu_pairs, the residual written as there, and within the
+    oracle's tolerance of silu(g) * u of the oracle's matmul."""
+    import oracle as O
+
+    import arm_ai_amd as A
+    from arm_ai_amd import synth as S
+
+    torch, lib, ctx = env
+    L = lib.load()
+    rng = np.random.default_rng(n + k)
+    W, mm = _weight(A, S, wtype, n, k, ctx, seed=n)
+    x = rng.standard_normal(k).astype(np.float32)
+    d = rng.standard_normal(k).astype(np.float32)
+    wn = (1 + 0.1 * rng.standard_normal(k)).astype(np.float32)
+    dx, dd, dw = _dev(torch, x), _dev(torch, d), _dev(torch, wn)
+    eps = ctypes.c_float(1e-5)
+    ffn = n // 2
+    h1 = torch.empty(ffn, dtype=torch.float32, device="cuda:0")
+    xo1 = torch.empty(k, dtype=torch.float32, device="cuda:0")
+    y = torch.empty(n, dtype=torch.float32, device="cuda:0")
+    h2 = torch.empty(ffn, dtype=torch.float32, device="cuda:0")
+    xo2 = torch.empty(k, dtype=torch.float32, device="cuda:0")
+    torch.cuda.synchronize()
+    for _ in range(2):  # twice: the second call finds its scratch grown
+        lib.check(L.aq_qmatmul_rmsnorm_swiglu_f32_device(ctx.handle, mm.handle, dx.data_ptr(), dd.data_ptr(),
+                                                         dw.data_ptr(), eps, k, xo1.data_ptr(), h1.data_ptr()))
+    lib.check(L.aq_qmatmul_rmsnorm_f32_device(ctx.handle, mm.handle, dx.data_ptr(), dd.data_ptr(), dw.data_ptr(), eps,
+                                              k, xo2.data_ptr(), y.data_ptr()))
+    lib.check(L.aq_llama_swiglu_pairs(ctx.handle, y.data_ptr(), n, 1, ffn, h2.data_ptr()))
+    ctx.synchronize()
+    got = h1.cpu().numpy()
+    assert np.array_equal(got, h2.cpu().numpy())
+    assert np.array_equal(xo1.cpu().numpy(), xo2.cpu().numpy())
+    assert np.array_equal(xo1.cpu().numpy(), x + d)
+    h = x + d
+    ms = np.float32(np.mean(h.astype(np.float64) ** 2))
+    xin = ((h / np.sqrt(ms + np.float32(1e-5))) * wn).astype(np.float32)[None, :]
+    g, u = _unpair(O.matmul(wtype, xin, W.blocks, n, k), ffn)
+    want = (g / (np.float32(1) + np.exp(-g))) * u
+    # the norm's sum of squares is reduced in another order, which can move a
+    # Q8_K quant by one step: compare at 1e-3 of the output's scale
+    assert _rel(got, want[0]) <= 1e-3
+    mm.free()
+
+
 def test_matvec_fused_errors(env):
     import arm_ai_amd as A
     from arm_ai_amd import synth as S

@@ -298,6 +298,31 @@ def test_generate_streams_each_token_before_the_next_step(tiny):
 
 
 # ------------------------------------------------------------ SmolLM-135M shape
+def test_swiglu_pair_rows_interleaves_gate_and_up_rows_in_fours():
+    """Row 8b + j of the paired weight is gate row 4b + j (j < 4) or up row
+    4b + j - 4, every row's quantized blocks unchanged; mismatched pairs are
+    refused."""
+    from arm_ai_amd import synth
+    from arm_ai_amd.llama import swiglu_pair_rows
+    from arm_ai_amd.qmatmul import QTensor
+
+    ffn, k = 24, 256
+    rb = 144  # one Q4_K block per row
+    w1 = QTensor(synth.TYPE_Q4_K, (ffn, k), np.repeat(np.arange(ffn, dtype=np.uint8), rb))
+    w3 = QTensor(synth.TYPE_Q4_K, (ffn, k), np.repeat(np.arange(100, 100 + ffn, dtype=np.uint8), rb))
+    p = swiglu_pair_rows(w1, w3)
+    assert p.dtype == synth.TYPE_Q4_K and tuple(p.shape) == (2 * ffn, k)
+    rows = np.asarray(p.data).reshape(2 * ffn, rb)
+    assert np.all(rows == rows[:, :1])
+    want = [4 * (r // 8) + r % 4 + (0 if r % 8 < 4 else 100) for r in range(2 * ffn)]
+    assert rows[:, 0].tolist() == want
+    with pytest.raises(ValueError):
+        swiglu_pair_rows(w1, QTensor(synth.TYPE_Q6_K, (ffn, k), np.zeros(ffn * 210, np.uint8)))
+    with pytest.raises(ValueError):
+        swiglu_pair_rows(QTensor(synth.TYPE_Q4_K, (6, k), np.zeros(6 * rb, np.uint8)),
+                         QTensor(synth.TYPE_Q4_K, (6, k), np.zeros(6 * rb, np.uint8)))
+
+
 def test_gguf_fallback_types_for_rows_not_a_multiple_of_256():
     """llama.cpp's Q4_K_M writes the fallback type where a row (k) is not a
     multiple of 256: SmolLM-135M's hidden 576 turns Q4_K into Q5_0 and Q6_K
@@ -357,7 +382,8 @@ def test_smollm_shape_matmuls_glue_graph_step_and_generate(smollm):
     cfg = hw.cfg
     ref = RefLlama(hw)
     host_of = _host_blocks(model, hw)
-    glue = _Glue(ref, 0)
+    assert "w13" in model.layers[0]  # rows of 576: [g | u], silu(g) * u in the w2 launch
+    glue = _Glue(ref, 0, "w13p" in model.layers[0])
     rng = np.random.default_rng(33)
     prompt = rng.integers(0, cfg.vocab, size=40).tolist()
     pos = 0

@@ -75,7 +75,9 @@ def _rel(a, b):
 
 
 def _host_blocks(model, hw):
-    """QMatMul handle -> host QTensor (the concatenated pair where the driver merged one)."""
+    """QMatMul handle -> host QTensor (where the driver merged a pair: wq|wk
+    and w13 rows concatenated, w13p gate and up rows in pairs of four)."""
+    from arm_ai_amd.llama import swiglu_pair_rows
     from arm_ai_amd.qmatmul import QTensor
 
     out = {id(model.output): hw.output}
@@ -83,12 +85,20 @@ def _host_blocks(model, hw):
         for name, qm in dev.items():
             if name in host:
                 out[id(qm)] = host[name]
-            else:  # wqk / w13: rows of the pair, concatenated
-                a, b = {"wqk": ("wq", "wk"), "w13": ("w1", "w3")}[name]
-                qa, qb = host[a], host[b]
+            elif name == "w13p":
+                out[id(qm)] = swiglu_pair_rows(host["w1"], host["w3"])
+            else:
+                qa, qb = (host["wq"], host["wk"]) if name == "wqk" else (host["w1"], host["w3"])
                 out[id(qm)] = QTensor(qa.dtype, (qa.shape[0] + qb.shape[0], qa.shape[1]),
                                       np.concatenate([qa.data.reshape(-1), qb.data.reshape(-1)]))
     return out
+
+
+def _unpair(gu, ffn):
+    """g, u of rows of a paired w1|w3 output (column 8b + j: gate 4b + j for
+    j < 4, up 4b + j - 4 after)."""
+    p = gu.reshape(gu.shape[0], ffn // 4, 2, 4)
+    return p[:, :, 0, :].reshape(-1, ffn), p[:, :, 1, :].reshape(-1, ffn)
 
 
 def _check_records(records, host_of, what):
@@ -136,9 +146,10 @@ class _Glue:
     """The reference's glue for one layer, run on the GPU's matmul inputs and
     outputs; keeps the layer's rotated k and v of every position seen."""
 
-    def __init__(self, ref, li):
+    def __init__(self, ref, li, paired):
         cfg = ref.cfg
         self.ref, self.li, self.cfg = ref, li, cfg
+        self.paired = paired  # w1|w3 rows in pairs of four (the driver's "w13p")
         hd = cfg.hidden // cfg.n_head
         self.k = np.zeros((cfg.n_kv_head, 0, hd), np.float32)
         self.v = np.zeros((cfg.n_kv_head, 0, hd), np.float32)
@@ -168,7 +179,10 @@ class _Glue:
         err["attention"] = _rel(att_in, y.transpose(1, 0, 2).reshape(L, H * hd))
         h_res = x + o_out
         err["ffn_norm"] = _rel(f_in, ref.rms(h_res, hw.ffn_norm[li]))
-        g, u = gu[:, :cfg.ffn], gu[:, cfg.ffn:]
+        if self.paired:
+            g, u = _unpair(gu, cfg.ffn)
+        else:
+            g, u = gu[:, :cfg.ffn], gu[:, cfg.ffn:]
         err["silu_mul"] = _rel(s_in, (g / (1.0 + np.exp(-g))) * u)
         assert np.array_equal(x_next, h_res + d_out), f"layer {li}: the residual adds are not exact"
         return err
@@ -194,6 +208,7 @@ def test_config2_full_size_prefill_decode_and_graph_step(full):
     cfg = hw.cfg
     assert (cfg.n_layer, cfg.hidden, cfg.ffn, cfg.n_head, cfg.n_kv_head, cfg.vocab) == (22, 2048, 5632, 32, 4, 32000)
     host_of = _host_blocks(model, hw)
+    assert all("w13p" in lw for lw in model.layers)  # silu(g) * u in the w1|w3 launch
     rng = np.random.default_rng(42)
     prompt = rng.integers(0, cfg.vocab, size=N_PROMPT).tolist()
     steps = rng.integers(0, cfg.vocab, size=N_STEPS).tolist()
@@ -202,7 +217,7 @@ def test_config2_full_size_prefill_decode_and_graph_step(full):
     with warnings.catch_warnings():
         warnings.simplefilter("error", RuntimeWarning)
         ref = RefLlama(hw)
-        glue = {li: _Glue(ref, li) for li in GLUE_LAYERS}
+        glue = {li: _Glue(ref, li, "w13p" in model.layers[li]) for li in GLUE_LAYERS}
         pos = 0
         for i, toks in enumerate([prompt] + [[t] for t in steps]):
             what = "prefill" if i == 0 else f"decode step {i - 1}"
