@@ -36,8 +36,11 @@ struct aq_ctx {
     // decode attention's per-slice partial records: allocated with the
     // context, so a captured decode step never allocates
     float *attn_part = nullptr;
+    // the output head's per-workgroup (largest logit, row) pairs
+    int2 *head_part = nullptr;
 };
 constexpr size_t ATTN_PART_BYTES = (size_t)2 << 20;
+constexpr int HEAD_PARTS = 4096;
 
 // Scratch of aq_qmatmul_f32_device_noalloc: a fixed array in the library's
 // device image, one copy per GPU (held until the process ends).  Its name is
@@ -292,10 +295,11 @@ int aq_ctx_create(int device, aq_ctx **out) {
         delete c;
         return fail(AQ_ERR_HIP, "hipStreamCreateWithFlags failed");
     }
-    if (hipMalloc(&c->attn_part, ATTN_PART_BYTES) != hipSuccess) {
+    if (hipMalloc(&c->attn_part, ATTN_PART_BYTES) != hipSuccess ||
+        hipMalloc(&c->head_part, HEAD_PARTS * sizeof(int2)) != hipSuccess) {
         (void)hipGetLastError();
         aq_ctx_destroy(c);
-        return fail(AQ_ERR_OOM, "allocation of the attention workspace failed");
+        return fail(AQ_ERR_OOM, "allocation of the decode workspaces failed");
     }
     *out = c;
     return AQ_OK;
@@ -308,6 +312,7 @@ int aq_ctx_destroy(aq_ctx *c) {
     if (c->scratch) (void)hipFree(c->scratch);
     if (c->pinned) (void)hipHostFree(c->pinned);
     if (c->attn_part) (void)hipFree(c->attn_part);
+    if (c->head_part) (void)hipFree(c->head_part);
     if (c->stream) (void)hipStreamDestroy(c->stream);
     delete c;
     return AQ_OK;
@@ -1047,6 +1052,34 @@ int aq_llama_swiglu_pairs(aq_ctx *ctx, const float *d_y, int64_t ld, int64_t m, 
     int rc = use_device(ctx->device);
     if (rc) return rc;
     return hip_status(launch_swiglu_pairs(d_y, ld, m, ffn, d_out, ctx->stream), "swiglu pairs");
+}
+
+int aq_llama_head_argmax_embed(aq_ctx *ctx, const aq_qweight *w, const float *d_x, const float *d_delta,
+                               const float *d_norm_w, float eps, int64_t k, float *d_logits, int64_t *d_tok,
+                               int64_t *d_pos, int64_t *d_hist, int64_t hist_len, const float *d_table,
+                               int64_t hidden, float *d_x_next) {
+    int rc = check_mm(ctx, w, 1, k);
+    if (rc) return rc;
+    if (!d_x || !d_norm_w || !d_logits || !d_tok || !d_pos || !d_table || !d_x_next)
+        return fail(AQ_ERR_INVALID_ARG, "null pointer");
+    if (hidden <= 0 || hidden % 4 || (((uintptr_t)d_table | (uintptr_t)d_x_next | (uintptr_t)d_logits) & 15))
+        return fail(AQ_ERR_INVALID_ARG, "hidden must be a positive multiple of 4, table / output / logits 16-byte aligned");
+    if ((rc = use_device(ctx->device))) return rc;
+    int nparts = 0;
+    hipError_t e = launch_matvec_rmsnorm_argmax(w->layout, w->n, w->k, d_x, d_delta, d_norm_w, eps, d_logits,
+                                                ctx->head_part, HEAD_PARTS, &nparts, ctx->stream);
+    if (e == hipSuccess)
+        return hip_status(launch_argmax_parts_embed(ctx->head_part, nparts, d_tok, d_pos, d_hist, hist_len, d_table,
+                                                    w->n, hidden, d_x_next, ctx->stream),
+                          "argmax parts embed");
+    if (e != hipErrorNotSupported) return hip_status(e, "matvec rmsnorm argmax");
+    // other heads: the fused-norm matvec, the argmax over the logits, the embedding
+    e = launch_matvec_rmsnorm(w->layout, w->n, w->k, d_x, d_delta, d_norm_w, eps, nullptr, d_logits, ctx->stream);
+    if (e == hipErrorNotSupported) return fail(AQ_ERR_SHAPE, "k=%lld is too long for the fused norm", (long long)k);
+    if (e != hipSuccess) return hip_status(e, "matvec rmsnorm");
+    if ((e = launch_argmax(d_logits, w->n, d_tok, d_pos, d_hist, hist_len, ctx->stream)) != hipSuccess)
+        return hip_status(e, "argmax");
+    return hip_status(launch_embed(d_table, w->n, d_tok, 1, hidden, d_x_next, ctx->stream), "embed");
 }
 
 int aq_swiglu_fused(int type, int64_t n, int64_t k) {

@@ -164,7 +164,11 @@ struct RlXf {
     float eps;
     float *xout;
     bool swiglu = false;
+    // or null: per workgroup (grid: rowlane_grid), the bits of the largest
+    // output and its row, the first of equal values (a NaN never wins)
+    int2 *amax = nullptr;
 };
+int rowlane_grid(int type, int64_t n, int64_t k);
 bool rowlane_matvec_applies(int type, int64_t n, int64_t k);
 bool rowlane_xf_applies(int type, int64_t n, int64_t k, int kind);
 hipError_t launch_rowlane_matvec(const WLayout &w, int64_t n, int64_t k, const float *x, const ActPlanes *act,
@@ -241,6 +245,12 @@ hipError_t launch_matvec_silu(const WLayout &w, int64_t n, int64_t k, const floa
 // row-per-lane forms only (hipErrorNotSupported otherwise).
 hipError_t launch_matvec_rmsnorm_swiglu(const WLayout &w, int64_t n, int64_t k, const float *x, const float *delta,
                                         const float *norm, float eps, float *xout, float *h, hipStream_t s);
+// The fused-norm matvec also leaving, per workgroup, its largest output and
+// that row in amax (*nparts entries, at most max_parts); the row-per-lane
+// forms only (hipErrorNotSupported otherwise).
+hipError_t launch_matvec_rmsnorm_argmax(const WLayout &w, int64_t n, int64_t k, const float *x, const float *delta,
+                                        const float *norm, float eps, float *y, int2 *amax, int max_parts,
+                                        int *nparts, hipStream_t s);
 // Two fused-norm matvecs of the same row in one launch (Q4_K / Q6_K weights
 // w1 and w2, outputs y1 and y2); xout is written once.  hipErrorNotSupported
 // for other types or rows too long to fuse.
@@ -276,6 +286,11 @@ hipError_t launch_attn_prefill(const float *q, int64_t ldq, const float *k, int6
                                hipStream_t s);
 hipError_t launch_argmax(const float *x, int64_t n, int64_t *d_tok, int64_t *d_pos, int64_t *hist, int64_t hist_len,
                          hipStream_t s);
+// The greedy pick from per-workgroup (value bits, row) pairs (the first row
+// of the largest value), then that token's embedding row into xout.
+hipError_t launch_argmax_parts_embed(const int2 *parts, int nparts, int64_t *d_tok, int64_t *d_pos, int64_t *hist,
+                                     int64_t hist_len, const float *table, int64_t vocab, int64_t hidden, float *xout,
+                                     hipStream_t s);
 
 }  // namespace aq
 

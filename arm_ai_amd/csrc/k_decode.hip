@@ -405,7 +405,65 @@ __global__ __launch_bounds__(WIDE_THREADS) void argmax_kernel(const float *__res
     }
 }
 
+// The greedy pick from per-workgroup (value bits, row) pairs that a
+// matvec's workgroups left (each the first row of its largest value), with
+// argmax_kernel's rule: the first row of the largest value, a NaN never
+// wins, none at all gives 0; then token, history and position as there, and
+// the token's embedding row (table [vocab][hidden], hidden % 4 == 0) to xout
+// -- the next step's input.  One 256-thread workgroup.
+__global__ __launch_bounds__(DEC_THREADS) void argmax_parts_embed_kernel(
+    const int2 *__restrict__ parts, int nparts, int64_t *__restrict__ d_tok, int64_t *__restrict__ d_pos,
+    int64_t *__restrict__ hist, int64_t hist_len, const float *__restrict__ table, int64_t vocab, int hidden,
+    float *__restrict__ xout) {
+    __shared__ float bv[DEC_THREADS / 64];
+    __shared__ int bi[DEC_THREADS / 64];
+    __shared__ int tok;
+    float best = -INFINITY;
+    int idx = 0x7fffffff;
+    const int64_t pos = threadIdx.x == 0 ? *d_pos : 0;  // only thread 0 uses it
+    for (int i = threadIdx.x; i < nparts; i += DEC_THREADS) {
+        const int2 q = parts[i];
+        better(u32_as_f32((uint32_t)q.x), q.y, best, idx);
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        const float ov = __shfl_xor(best, o);
+        const int oi = __shfl_xor(idx, o);
+        better(ov, oi, best, idx);
+    }
+    if ((threadIdx.x & 63) == 0) {
+        bv[threadIdx.x >> 6] = best;
+        bi[threadIdx.x >> 6] = idx;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < DEC_THREADS / 64; w++) better(bv[w], bi[w], best, idx);
+        if (idx == 0x7fffffff) idx = 0;
+        *d_tok = idx;
+        if (hist && pos >= 0 && pos < hist_len) hist[pos] = idx;
+        *d_pos = pos + 1;
+        tok = idx;
+    }
+    __syncthreads();
+    const int64_t t = tok;
+    const bool ok = t >= 0 && t < vocab;
+    const float4 *src = (const float4 *)(table + (ok ? t : 0) * (int64_t)hidden);
+    for (int i = threadIdx.x; i < hidden / 4; i += DEC_THREADS)
+        ((float4 *)xout)[i] = ok ? src[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+}
+
 }  // namespace
+
+hipError_t launch_argmax_parts_embed(const int2 *parts, int nparts, int64_t *d_tok, int64_t *d_pos, int64_t *hist,
+                                     int64_t hist_len, const float *table, int64_t vocab, int64_t hidden, float *xout,
+                                     hipStream_t s) {
+    if (!parts || nparts <= 0 || !d_tok || !d_pos || !table || !xout || vocab <= 0 || hidden <= 0 || hidden % 4 ||
+        hidden > 0x7fffffff || (((uintptr_t)table | (uintptr_t)xout) & 15))
+        return hipErrorInvalidValue;
+    argmax_parts_embed_kernel<<<1, DEC_THREADS, 0, s>>>(parts, nparts, d_tok, d_pos, hist, hist_len, table, vocab,
+                                                        (int)hidden, xout);
+    return hipGetLastError();
+}
 
 hipError_t launch_embed(const float *table, int64_t vocab, const int64_t *d_tok, int64_t m, int64_t hidden, float *out,
                         hipStream_t s) {

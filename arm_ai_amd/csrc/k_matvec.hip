@@ -1012,6 +1012,20 @@ hipError_t launch_matvec_rmsnorm_swiglu(const WLayout &w, int64_t n, int64_t k, 
     return launch_rowlane_matvec(w, n, k, x, nullptr, h, nullptr, nullptr, s, &rx);
 }
 
+hipError_t launch_matvec_rmsnorm_argmax(const WLayout &w, int64_t n, int64_t k, const float *x, const float *delta,
+                                        const float *norm, float eps, float *y, int2 *amax, int max_parts,
+                                        int *nparts, hipStream_t s) {
+    if ((delta && ((uintptr_t)delta & 15)) || !norm || ((uintptr_t)norm & 15) || !amax || !nparts)
+        return hipErrorInvalidValue;
+    if (!rowlane_xf_applies(w.type, n, k, RL_XF_NORM)) return hipErrorNotSupported;
+    const int g = rowlane_grid(w.type, n, k);
+    if (g <= 0 || g > max_parts) return hipErrorNotSupported;
+    RlXf rx{RL_XF_NORM, delta, norm, eps, nullptr};
+    rx.amax = amax;
+    *nparts = g;
+    return launch_rowlane_matvec(w, n, k, x, nullptr, y, nullptr, nullptr, s, &rx);
+}
+
 hipError_t launch_matvec_silu(const WLayout &w, int64_t n, int64_t k, const float *gu, float *y, hipStream_t s) {
     XfArgs xa;
     xa.xf = XF_SILU;

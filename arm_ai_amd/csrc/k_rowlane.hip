@@ -68,6 +68,7 @@ struct RlParams {
     ActPlanes act;     // pre-quantised planes (x null)
     float *y;
     int swiglu;        // y[4b + j] = silu(row 8b + j) * row (8b + 4 + j), j < 4
+    int2 *amax;        // or null: per workgroup, (bits of the largest y, its row) over the rows it wrote
     int32_t *S, *Smin;  // [n][ng] integer dump, or null
 };
 
@@ -342,6 +343,10 @@ __device__ __forceinline__ void rl_body(const RlParams p, const int bid, const i
     //    1 + 2c + h = qs bytes 32c + 16h .. +15 (low nibbles: elements
     //    64c + 16h + i of sub-block 2c; high: 64c + 32 + 16h + i of 2c + 1)
     const int nch = (p.n + R - 1) / R;
+    // (amax: this lane's largest value so far and its row -- the first of
+    //  equal values; a NaN never wins)
+    float abv = -INFINITY;
+    int abi = 0x7fffffff;
     for (int chunk = bid, it = 0;; it++) {  // one chunk unless CH
     const int nextc = chunk + nblk;
     const bool more = CH && nextc < nch;  // uniform
@@ -643,15 +648,33 @@ __device__ __forceinline__ void rl_body(const RlParams p, const int bid, const i
             const float u = __shfl_down(t, 4);
             if (rok && gp == 0 && (row & 4) == 0) p.y[(row >> 3) * 4 + (row & 3)] = (t / (1.0f + expf(-t))) * u;
         }
-    } else if (wave == 0 && rok && gp == 0) {
+    } else if (wave == 0) {
         float t = 0.0f;
 #pragma unroll
         for (int w = 0; w < W; w++) t += red[CH ? it & 1 : 0][w][lane];
-        p.y[row] = t;
+        if (rok && gp == 0) {
+            p.y[row] = t;
+            if (t > abv || (t == abv && row < abi)) {
+                abv = t;
+                abi = row;
+            }
+        }
     }
     if (!more) break;  // uniform
     chunk = nextc;
     cur = nxt;
+    }
+    if (p.amax && wave == 0) {  // uniform: the workgroup's largest value and its row
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) {
+            const float ov = __shfl_xor(abv, o);
+            const int oi = __shfl_xor(abi, o);
+            if (ov > abv || (ov == abv && oi < abi)) {
+                abv = ov;
+                abi = oi;
+            }
+        }
+        if (lane == 0) p.amax[bid] = make_int2((int)f32_as_u32(abv), abi);
     }
 }
 
@@ -697,6 +720,13 @@ hipError_t launch_g(const RlParams &p, unsigned grid, bool fused, bool dump, hip
 }
 
 bool rows56(int type, int64_t n, int ng) { return rl::wide(type == TYPE_Q6_K, type == TYPE_Q8_0, n, ng); }
+}  // namespace
+
+int rowlane_grid(int type, int64_t n, int64_t k) {
+    return (int)rl::plan(type == TYPE_Q6_K, type == TYPE_Q8_0, n, (int)(k / QK_K)).grid;
+}
+
+namespace {
 bool rows8(int64_t n, int ng) { return rl::narrow8(n, ng); }
 
 // The launch shapes of one weight type (pieces in flight: P; 16 wavefronts
@@ -770,6 +800,7 @@ hipError_t rl_params(const WLayout &w, int64_t n, int64_t k, const float *x, con
         return hipErrorInvalidValue;
     if (xf && !rowlane_xf_applies(w.type, n, k, xf->kind)) return hipErrorNotSupported;
     if (xf && xf->swiglu && n % RB) return hipErrorInvalidValue;  // whole 8-row blocks of four gate, four up rows
+    if (xf && xf->swiglu && xf->amax) return hipErrorInvalidValue;
     const int ng = (int)(k / QK_K);
     const int npg = slabs_of(w.type);
     if (w.ng != ng || w.rb_stride != (int64_t)ng * npg * 128) return hipErrorInvalidValue;
@@ -792,6 +823,7 @@ hipError_t rl_params(const WLayout &w, int64_t n, int64_t k, const float *x, con
     p.act = act ? *act : ActPlanes{};
     p.y = y;
     p.swiglu = xf && xf->swiglu ? 1 : 0;
+    p.amax = xf ? xf->amax : nullptr;
     p.S = S;
     p.Smin = Smin;
     return hipSuccess;
@@ -834,7 +866,7 @@ hipError_t launch_rowlane_matvec(const WLayout &w, int64_t n, int64_t k, const f
 
 hipError_t launch_rowlane_matvec2(const WLayout &w1, int64_t n1, float *y1, const WLayout &w2, int64_t n2, float *y2,
                                   int64_t k, const float *x, const RlXf &xf, hipStream_t s) {
-    if (xf.swiglu) return hipErrorNotSupported;
+    if (xf.swiglu || xf.amax) return hipErrorNotSupported;
     RlParams p1, p2;
     hipError_t e = rl_params(w1, n1, k, x, nullptr, y1, nullptr, nullptr, &xf, p1);
     if (e != hipSuccess) return e;

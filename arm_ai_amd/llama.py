@@ -459,8 +459,10 @@ class Llama:
 
     def _decode_step_static(self):
         """One decode step for the token in self._tok at the position in self._pos
-        (both device memory); leaves the logits in self._logits, the next token
-        in self._tok and in self._hist[pos], and pos + 1 in self._pos.
+        (both device memory), whose embedding row is in self._ra; leaves the
+        logits in self._logits, the next token in self._tok and in
+        self._hist[pos], its embedding row in self._ra, and pos + 1 in
+        self._pos.
 
         Per layer six launches: the QMatMuls of wq|wk and wv, one launch for
         both, take rms_norm(x + delta) as their input (formed inside the
@@ -484,8 +486,7 @@ class Llama:
             chk(L.aq_qmatmul_rmsnorm_f32_device(c, w.handle, ptr(x), delta, ptr(norm), eps, w.k,
                                                 ptr(h_out) if h_out is not None else None, out))
 
-        chk(L.aq_llama_embed(c, ptr(self.tok_embeddings), cfg.vocab, ptr(self._tok), cfg.hidden, ptr(self._ra)))
-        cur, other = self._ra, self._rb
+        cur, other = self._ra, self._rb  # cur: the token's embedding row, left by the step before (or _set_token)
         delta = None
         for li, lw in enumerate(self.layers):
             an = self.attn_norm[li]
@@ -517,9 +518,11 @@ class Llama:
                     mm_norm(lw["w3"], other, ptr(self._o), fn, ptr(self._gu) + 4 * cfg.ffn)
                 chk(L.aq_qmatmul_silu_mul_f32_device(c, lw["w2"].handle, ptr(self._gu), cfg.ffn, ptr(self._d)))
             delta = ptr(self._d)  # the residual is now x + wo + w2 = cur + d
-        mm_norm(self.output, cur, delta, self.norm, ptr(self._logits))
-        chk(L.aq_llama_argmax(c, ptr(self._logits), cfg.vocab, ptr(self._tok), ptr(self._pos), ptr(self._hist),
-                              cfg.max_seq))
+        # the head, the greedy pick (token, history, position) and the picked
+        # token's embedding row into _ra, the next step's input
+        chk(L.aq_llama_head_argmax_embed(c, self.output.handle, ptr(cur), delta, ptr(self.norm), eps, cfg.hidden,
+                                         ptr(self._logits), ptr(self._tok), ptr(self._pos), ptr(self._hist),
+                                         cfg.max_seq, ptr(self.tok_embeddings), cfg.hidden, ptr(self._ra)))
 
     def _capture(self):
         torch = self.torch
@@ -530,7 +533,7 @@ class Llama:
         # cache slot: a step writes only its own position's k, v, so the cache
         # entries of a sequence in progress stay intact.
         with torch.cuda.stream(self.stream):
-            self._pos.fill_(self.cfg.max_seq - 1)
+            self._set_token(0, self.cfg.max_seq - 1)
             self._decode_step_static()
         self.ctx.synchronize()
         g = torch.cuda.CUDAGraph()
@@ -538,6 +541,16 @@ class Llama:
             self._decode_step_static()
         self._graph = g
         self._leave()
+
+    def _set_token(self, token: int, pos: int):
+        """The decode step's input on the library stream: the token, its position
+        and its embedding row (a replay then feeds the next one itself)."""
+        from . import _lib
+
+        self._pos.fill_(pos)
+        self._tok.fill_(token)
+        _lib.check(_lib.load().aq_llama_embed(self.ctx.handle, self.tok_embeddings.data_ptr(), self.cfg.vocab,
+                                              self._tok.data_ptr(), self.cfg.hidden, self._ra.data_ptr()))
 
     def decode_step_graph(self, token: int, pos: int):
         """Replay the captured decode step for `token` at position `pos`; returns the device logits."""
@@ -547,8 +560,7 @@ class Llama:
             raise ValueError(f"position {pos} outside 0..{self.cfg.max_seq}")
         self._enter()
         with self.torch.cuda.stream(self.stream):
-            self._pos.fill_(pos)
-            self._tok.fill_(token)
+            self._set_token(token, pos)
             self._graph.replay()
         self._leave()
         return self._logits
@@ -595,8 +607,7 @@ class Llama:
         if graph and max_new > 1 and nxt not in stop_tokens:
             self._enter()
             with self.torch.cuda.stream(self.stream):
-                self._pos.fill_(offset)
-                self._tok.fill_(nxt)
+                self._set_token(nxt, offset)
             done = False
             while not done and len(generated) < max_new:
                 n = min(chunk, max_new - len(generated))

@@ -343,6 +343,21 @@ int aq_llama_swiglu_pairs(aq_ctx *ctx, const float *d_y, int64_t ld, int64_t m, 
 int aq_swiglu_fused(int type, int64_t n, int64_t k);
 int aq_qmatmul_rmsnorm_swiglu_f32_device(aq_ctx *ctx, const aq_qweight *w, const float *d_x, const float *d_delta,
                                          const float *d_norm_w, float eps, int64_t k, float *d_h_out, float *d_dst);
+/* The end of a decode step and the start of the next, as
+ * aq_qmatmul_rmsnorm_f32_device on the output head w (d_logits, w->n =
+ * vocab values, no residual written), aq_llama_argmax over the logits
+ * (d_tok, d_hist[*d_pos], *d_pos += 1) and aq_llama_embed of that token from
+ * the f32 table d_table [vocab][hidden] into d_x_next (written after the
+ * head has read d_x and d_delta, so it may be either): the same values.  Where the head takes the row-per-lane
+ * matvec with the fused norm, each of its workgroups also keeps its largest
+ * logit and row, and one more launch picks the token from those and writes
+ * its embedding row (two launches in place of three, the argmax reading a
+ * few KB in place of the logits).  Uses the context's head workspace: calls
+ * on one context must not overlap. */
+int aq_llama_head_argmax_embed(aq_ctx *ctx, const aq_qweight *w, const float *d_x, const float *d_delta,
+                               const float *d_norm_w, float eps, int64_t k, float *d_logits, int64_t *d_tok,
+                               int64_t *d_pos, int64_t *d_hist, int64_t hist_len, const float *d_table,
+                               int64_t hidden, float *d_x_next);
 /* Greedy pick: the first index of the largest of d_x[0..n) (d_x 16-byte
  * aligned, any n >= 1) goes to *d_tok and, when d_hist is non-null and
  * 0 <= *d_pos < hist_len, to d_hist[*d_pos]; then *d_pos += 1. */

@@ -130,6 +130,9 @@ pub fn aq_abi_version() -> c_int;
     pub fn aq_llama_swiglu_pairs(ctx: *mut AqCtx, d_y: *const f32, ld: i64, m: i64, ffn: i64, d_out: *mut f32)
         -> c_int;
     pub fn aq_swiglu_fused(wtype: c_int, n: i64, k: i64) -> c_int;
+    pub fn aq_llama_head_argmax_embed(ctx: *mut AqCtx, w: *const AqQWeight, d_x: *const f32, d_delta: *const f32,
+        d_norm_w: *const f32, eps: f32, k: i64, d_logits: *mut f32, d_tok: *mut i64, d_pos: *mut i64,
+        d_hist: *mut i64, hist_len: i64, d_table: *const f32, hidden: i64, d_x_next: *mut f32) -> c_int;
     pub fn aq_qmatmul_rmsnorm_swiglu_f32_device(ctx: *mut AqCtx, w: *const AqQWeight, d_x: *const f32,
         d_delta: *const f32, d_norm_w: *const f32, eps: f32, k: i64, d_h_out: *mut f32, d_dst: *mut f32) -> c_int;
     pub fn aq_llama_argmax(ctx: *mut AqCtx, d_x: *const f32, n: i64, d_tok: *mut i64, d_pos: *mut i64,

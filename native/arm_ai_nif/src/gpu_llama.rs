@@ -462,7 +462,6 @@ impl GpuLlama {
             check(unsafe { aq_qmatmul_rmsnorm_f32_device(c, w.w, x, delta, norm, cfg.eps, w.k as i64, h_out, out) },
                   "qmatmul rmsnorm")
         };
-        check(unsafe { aq_llama_embed(c, self.tok_emb.f32(), cfg.vocab as i64, s.tok.i64(), hid, s.ra.f32()) }, "embed")?;
         let (cur, other) = (s.ra.f32(), s.rb.f32());
         let mut delta: *const f32 = std::ptr::null();
         for (li, l) in self.layers.iter().enumerate() {
@@ -512,9 +511,13 @@ impl GpuLlama {
             // input, with `other` again receiving the sum
             delta = s.d.f32();
         }
-        mm_norm(&self.output, cur, delta, self.norm.f32(), s.logits.f32(), std::ptr::null_mut())?;
-        check(unsafe { aq_llama_argmax(c, s.logits.f32(), cfg.vocab as i64, s.tok.i64(), s.pos.i64(), s.hist.i64(),
-                                       cfg.max_seq as i64) }, "argmax")
+        // the head, the greedy pick (token, history, position) and the picked
+        // token's embedding row into `ra`, the next step's input
+        check(unsafe {
+            aq_llama_head_argmax_embed(c, self.output.w, cur, delta, self.norm.f32(), cfg.eps, hid, s.logits.f32(),
+                                       s.tok.i64(), s.pos.i64(), s.hist.i64(), cfg.max_seq as i64,
+                                       self.tok_emb.f32(), hid, s.ra.f32())
+        }, "head argmax embed")
     }
 
     /// Capture the decode step once (after one eager run at the last cache
@@ -580,9 +583,9 @@ fn generate_chunked(res: &LlamaResource, prompt: &[u32], max_new: usize, stop_to
         return Err(format!("prompt ({}) + max_new ({}) exceeds the {} cached positions", prompt.len(), max_new, max_seq));
     }
     let graph = model.ensure_graph()?;
-    let (tok, pos, hist, logits) = {
+    let (tok, pos, hist, logits, ra) = {
         let s = model.step.as_ref().unwrap();
-        (s.tok.i64(), s.pos.i64(), s.hist.i64(), s.logits.f32())
+        (s.tok.i64(), s.pos.i64(), s.hist.i64(), s.logits.f32(), s.ra.f32())
     };
 
     let prefill_start = std::time::Instant::now();
@@ -591,6 +594,9 @@ fn generate_chunked(res: &LlamaResource, prompt: &[u32], max_new: usize, stop_to
     model.h2d_i64(pos, prompt.len() as i64 - 1)?;
     check(unsafe { aq_llama_argmax(model.c(), logits, model.cfg.vocab as i64, tok, pos, hist, max_seq as i64) },
           "argmax")?;
+    // the step's input: the token's embedding row (each replay then leaves the next one's)
+    check(unsafe { aq_llama_embed(model.c(), model.tok_emb.f32(), model.cfg.vocab as i64, tok,
+                                  model.cfg.hidden as i64, ra) }, "embed")?;
     let mut next = model.d2h_i64(tok, 1)?[0] as u32;
     let prefill_us = prefill_start.elapsed().as_micros() as u64;
     let mut generated = vec![next];

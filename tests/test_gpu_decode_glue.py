@@ -404,6 +404,82 @@ def test_matvec_fused_rmsnorm_swiglu(env, wtype, n, k):
     mm.free()
 
 
+@pytest.mark.parametrize("wtype,vocab,k,tie,alias", [
+    (14, 32000, 2048, False, True),   # TinyLlama's head: persistent 56-row chunks; the next x over the input
+    (14, 32000, 2048, True, False),   # the largest logit in two rows of different workgroups
+    (12, 4000, 2048, True, False),    # the 16-row form
+    (8, 2048, 2048, False, False),    # Q8_0, the 8-row form
+    (12, 200, 1024, False, True),     # below 256 rows: the general matvec, then argmax and embedding launches
+])
+def test_head_argmax_embed(env, wtype, vocab, k, tie, alias):
+    """aq_llama_head_argmax_embed against its three steps run apart (the
+    fused-norm head, aq_llama_argmax over the logits, aq_llama_embed of the
+    token): the same logits bit for bit, the same token (the first row of the
+    largest logit, also when two workgroups hold it), history, position and
+    embedding row."""
+    import arm_ai_amd as A
+    from arm_ai_amd import synth as S
+
+    torch, lib, ctx = env
+    L = lib.load()
+    rng = np.random.default_rng(vocab + k)
+    W = S.make_weight(wtype, vocab, k, seed=vocab)
+    x = rng.standard_normal(k).astype(np.float32)
+    d = rng.standard_normal(k).astype(np.float32)
+    wn = (1 + 0.1 * rng.standard_normal(k)).astype(np.float32)
+    table = rng.standard_normal((vocab, k)).astype(np.float32)
+    dx, dd, dw, dt = _dev(torch, x), _dev(torch, d), _dev(torch, wn), _dev(torch, table)
+    eps = ctypes.c_float(1e-5)
+    pos0, hist_len = 37, 64
+
+    def separate(mm):
+        logits = torch.empty(vocab, dtype=torch.float32, device="cuda:0")
+        tok = torch.zeros(1, dtype=torch.int64, device="cuda:0")
+        pos = torch.full((1,), pos0, dtype=torch.int64, device="cuda:0")
+        hist = torch.zeros(hist_len, dtype=torch.int64, device="cuda:0")
+        xn = torch.empty(k, dtype=torch.float32, device="cuda:0")
+        torch.cuda.synchronize()
+        lib.check(L.aq_qmatmul_rmsnorm_f32_device(ctx.handle, mm.handle, dx.data_ptr(), dd.data_ptr(), dw.data_ptr(),
+                                                  eps, k, None, logits.data_ptr()))
+        lib.check(L.aq_llama_argmax(ctx.handle, logits.data_ptr(), vocab, tok.data_ptr(), pos.data_ptr(),
+                                    hist.data_ptr(), hist_len))
+        lib.check(L.aq_llama_embed(ctx.handle, dt.data_ptr(), vocab, tok.data_ptr(), k, xn.data_ptr()))
+        ctx.synchronize()
+        return [t.cpu().numpy() for t in (logits, tok, pos, hist, xn)]
+
+    mm = A.QMatMul.from_qtensor(A.QTensor(wtype, (vocab, k), W.blocks), ctx)
+    want = separate(mm)
+    expect = int(np.argmax(want[0]))
+    if tie:  # copy the winning row to an earlier row of another workgroup: it must win
+        m = expect
+        r2 = m - 150 if m >= 150 else m + 150
+        rows = np.asarray(W.blocks).reshape(vocab, -1).copy()
+        rows[r2] = rows[m]
+        mm.free()
+        mm = A.QMatMul.from_qtensor(A.QTensor(wtype, (vocab, k), rows.reshape(-1)), ctx)
+        want = separate(mm)
+        expect = min(m, r2)
+        assert want[0][r2] == want[0][m]
+    assert int(want[1][0]) == expect
+    logits = torch.empty(vocab, dtype=torch.float32, device="cuda:0")
+    tok = torch.zeros(1, dtype=torch.int64, device="cuda:0")
+    pos = torch.full((1,), pos0, dtype=torch.int64, device="cuda:0")
+    hist = torch.zeros(hist_len, dtype=torch.int64, device="cuda:0")
+    dx2 = _dev(torch, x)
+    xn = dx2 if alias else torch.empty(k, dtype=torch.float32, device="cuda:0")
+    torch.cuda.synchronize()
+    lib.check(L.aq_llama_head_argmax_embed(ctx.handle, mm.handle, dx2.data_ptr(), dd.data_ptr(), dw.data_ptr(), eps, k,
+                                           logits.data_ptr(), tok.data_ptr(), pos.data_ptr(), hist.data_ptr(),
+                                           hist_len, dt.data_ptr(), k, xn.data_ptr()))
+    ctx.synchronize()
+    got = [t.cpu().numpy() for t in (logits, tok, pos, hist, xn)]
+    assert np.array_equal(got[0], want[0])
+    assert int(got[1][0]) == expect and int(got[2][0]) == pos0 + 1 and int(got[3][pos0]) == expect
+    assert np.array_equal(got[3], want[3])
+    assert np.array_equal(got[4], table[expect])
+    mm.free()
+
+
 def test_matvec_fused_errors(env):
     import arm_ai_amd as A
     from arm_ai_amd import synth as S
