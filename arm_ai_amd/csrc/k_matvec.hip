@@ -668,6 +668,7 @@ __device__ __forceinline__ void matvec_body(const MvParams &p, const int bid, co
         float tot = 0.0f;
         for (int w = 0; w < nw; w++) tot += nred[w];
         const float mden = sqrtf(tot / (float)p.k + p.eps);
+        const float rm = 1.0f / mden;  // candle's h / m as h * (1 / m), as the row-per-lane kernel forms it
         const rsrc_t rxo = buf_rsrc(p.xout, p.xout && bid == 0 ? (uint32_t)(p.k * 4) : 0u);
 #pragma unroll
         for (int r = 0; r < PRE; r++) {
@@ -681,10 +682,10 @@ __device__ __forceinline__ void matvec_body(const MvParams &p, const int bid, co
             }
             __builtin_amdgcn_raw_buffer_store_b128(as.q[r], rxo, off, 0, 0);  // the residual stream x + delta
             const u32x4 h4 = as.q[r], w4 = as.q3[r];
-            as.q[r] = (u32x4){f32_as_u32((u32_as_f32(h4.x) / mden) * u32_as_f32(w4.x)),
-                              f32_as_u32((u32_as_f32(h4.y) / mden) * u32_as_f32(w4.y)),
-                              f32_as_u32((u32_as_f32(h4.z) / mden) * u32_as_f32(w4.z)),
-                              f32_as_u32((u32_as_f32(h4.w) / mden) * u32_as_f32(w4.w))};
+            as.q[r] = (u32x4){f32_as_u32((u32_as_f32(h4.x) * rm) * u32_as_f32(w4.x)),
+                              f32_as_u32((u32_as_f32(h4.y) * rm) * u32_as_f32(w4.y)),
+                              f32_as_u32((u32_as_f32(h4.z) * rm) * u32_as_f32(w4.z)),
+                              f32_as_u32((u32_as_f32(h4.w) * rm) * u32_as_f32(w4.w))};
         }
     } else if (XF == XF_SILU) {
 #pragma unroll

@@ -241,7 +241,7 @@ __device__ __forceinline__ void rl_body(const RlParams p, const int bid, const i
     // 2. quantise (or unpack) into LDS, then one barrier (LDS writes only).
     //    NORM: h = x + delta and the row's sum of squares first (every
     //    wavefront takes the barrier; lanes past the row hold zeros), then
-    //    (h / sqrt(mean(h^2) + eps)) * w is quantised.
+    //    (h * (1 / sqrt(mean(h^2) + eps))) * w is quantised.
     float v[16];
     if (FUSED && quantiser) {
 #pragma unroll
@@ -287,12 +287,16 @@ __device__ __forceinline__ void rl_body(const RlParams p, const int bid, const i
                 for (int i = 0; i < 4; i++)
                     *(float4 *)(p.xout + gb * QK_K + 16 * s + 4 * i) = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
             }
+            // candle's h / m as h * (1 / m): one division per lane, not 16
+            // (within one rounding of the quotient; the reordered sum of
+            // squares already moves m by as much)
+            const float rm = 1.0f / mden;
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                v[4 * i] = (v[4 * i] / mden) * u32_as_f32(nv[i].x);
-                v[4 * i + 1] = (v[4 * i + 1] / mden) * u32_as_f32(nv[i].y);
-                v[4 * i + 2] = (v[4 * i + 2] / mden) * u32_as_f32(nv[i].z);
-                v[4 * i + 3] = (v[4 * i + 3] / mden) * u32_as_f32(nv[i].w);
+                v[4 * i] = (v[4 * i] * rm) * u32_as_f32(nv[i].x);
+                v[4 * i + 1] = (v[4 * i + 1] * rm) * u32_as_f32(nv[i].y);
+                v[4 * i + 2] = (v[4 * i + 2] * rm) * u32_as_f32(nv[i].z);
+                v[4 * i + 3] = (v[4 * i + 3] * rm) * u32_as_f32(nv[i].w);
             }
         }
     }
