@@ -49,22 +49,33 @@ __global__ __launch_bounds__(256) void mfma_loop(int iters, int *out) {
 // f32 fmas, the two kinds interleaved by sched_group_barrier; launch bounds
 // (256, 2) and 512 workgroups give two wavefronts per SIMD.  Time per MFMA
 // per SIMD against NV shows how much of the VALU work the matrix core hides.
-template <int NV>
+// F16: v_mfma_f32_32x32x16_f16 instead, on random integers as a Q4_K GEMM
+// without the scale split would feed it (weights sc*q in 0..945, activations
+// -128..127, both exact in f16).
+template <int NV, bool F16>
 __global__ __launch_bounds__(256, 2) void coexec_loop(const int *src, int iters, int *out) {
     const int t = (int)threadIdx.x;
     v4i a[2], b[2];
+    v8h ha[2], hb[2];
     for (int i = 0; i < 2; i++) {
         a[i] = *(const v4i *)(src + 8 * t + 4 * i);
         b[i] = *(const v4i *)(src + 2048 + 8 * t + 4 * i);
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            ha[i][j] = (_Float16)(float)((uint32_t)src[8 * t + j + 4 * i] % 946u);
+            hb[i][j] = (_Float16)(float)((int)((uint32_t)src[2048 + 8 * t + j + 4 * i] % 256u) - 128);
+        }
     }
     float f[8];
     for (int i = 0; i < 8; i++) f[i] = (float)(src[4096 + t + i] & 255);
     const float g = 0.5f + (float)(src[5000 + t] & 1), hh = (float)(src[5100 + t] & 7);
     v16i c[4] = {};
+    v16f cf[4] = {};
     for (int i = 0; i < iters; i++) {
 #pragma unroll
         for (int u = 0; u < 4; u++) {
-            c[u] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[(u >> 1) & 1], b[u & 1], c[u], 0, 0, 0);
+            if (F16) cf[u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ha[(u >> 1) & 1], hb[u & 1], cf[u], 0, 0, 0);
+            else c[u] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[(u >> 1) & 1], b[u & 1], c[u], 0, 0, 0);
 #pragma unroll
             for (int v = 0; v < NV; v++) f[v & 7] = __builtin_fmaf(f[v & 7], g, hh);
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA, then the NV fmas
@@ -75,7 +86,7 @@ __global__ __launch_bounds__(256, 2) void coexec_loop(const int *src, int iters,
 #pragma unroll
     for (int u = 0; u < 4; u++)
 #pragma unroll
-        for (int r = 0; r < 16; r++) s += c[u][r];
+        for (int r = 0; r < 16; r++) s += c[u][r] + (int)cf[u][r];
     for (int i = 0; i < 8; i++) s += (int)f[i];
     out[blockIdx.x * 256 + t] = s;
 }
@@ -108,10 +119,22 @@ int aq_bench_mfma(int kind, void *stream, int grid, int iters, int *d_out) {
 int aq_bench_coexec(int nv, void *stream, int iters, const int *d_src, int *d_out) {
     if (iters <= 0 || !d_src || !d_out) return -1;
     hipStream_t s = (hipStream_t)stream;
-    if (nv == 0) coexec_loop<0><<<512, 256, 0, s>>>(d_src, iters, d_out);
-    else if (nv == 4) coexec_loop<4><<<512, 256, 0, s>>>(d_src, iters, d_out);
-    else if (nv == 8) coexec_loop<8><<<512, 256, 0, s>>>(d_src, iters, d_out);
-    else if (nv == 16) coexec_loop<16><<<512, 256, 0, s>>>(d_src, iters, d_out);
+    if (nv == 0) coexec_loop<0, false><<<512, 256, 0, s>>>(d_src, iters, d_out);
+    else if (nv == 4) coexec_loop<4, false><<<512, 256, 0, s>>>(d_src, iters, d_out);
+    else if (nv == 8) coexec_loop<8, false><<<512, 256, 0, s>>>(d_src, iters, d_out);
+    else if (nv == 16) coexec_loop<16, false><<<512, 256, 0, s>>>(d_src, iters, d_out);
+    else return -1;
+    return hipGetLastError() == hipSuccess ? 0 : -5;
+}
+
+// The same with v_mfma_f32_32x32x16_f16 (coexec_loop<nv, true>).
+int aq_bench_coexec_f16(int nv, void *stream, int iters, const int *d_src, int *d_out) {
+    if (iters <= 0 || !d_src || !d_out) return -1;
+    hipStream_t s = (hipStream_t)stream;
+    if (nv == 0) coexec_loop<0, true><<<512, 256, 0, s>>>(d_src, iters, d_out);
+    else if (nv == 4) coexec_loop<4, true><<<512, 256, 0, s>>>(d_src, iters, d_out);
+    else if (nv == 8) coexec_loop<8, true><<<512, 256, 0, s>>>(d_src, iters, d_out);
+    else if (nv == 16) coexec_loop<16, true><<<512, 256, 0, s>>>(d_src, iters, d_out);
     else return -1;
     return hipGetLastError() == hipSuccess ? 0 : -5;
 }

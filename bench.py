@@ -518,40 +518,45 @@ def measure_mfma_rates(ctx):
         rows[name] = {"TOPS": round(tops, 1), "frac_of_published_peak": round(tops / peak, 4), "ms": round(ms, 3)}
     out.close()
     rows["coexec_i8_random_operands"] = measure_coexec(ctx)
+    rows["coexec_f16_random_operands"] = measure_coexec(ctx, f16=True)
     return rows
 
 
-def measure_coexec(ctx):
-    """What VALU work costs next to v_mfma_i32_32x32x32_i8 (libaq_bench.so,
-    k_mfma.hip coexec_loop): two wavefronts per SIMD, four accumulator chains
-    each on random operands, each MFMA followed by nv independent f32 fmas;
-    time per MFMA per SIMD for nv = 0, 4, 8, 16.  The slope is the time each
-    VALU instruction adds, i.e. how much of it the matrix core does not hide."""
+def measure_coexec(ctx, f16=False):
+    """What VALU work costs next to v_mfma_i32_32x32x32_i8 (f16: next to
+    v_mfma_f32_32x32x16_f16 on integer values as a Q4_K GEMM without the
+    scale split would feed it) (libaq_bench.so, k_mfma.hip coexec_loop): two
+    wavefronts per SIMD, four accumulator chains each on random operands,
+    each MFMA followed by nv independent f32 fmas; time per MFMA per SIMD for
+    nv = 0, 4, 8, 16.  The slope is the time each VALU instruction adds, i.e.
+    how much of it the matrix core does not hide."""
     import ctypes
 
     from arm_ai_amd import hip
 
     lib = ctypes.CDLL(os.path.join(ROOT, "arm_ai_amd", "libaq_bench.so"))
-    lib.aq_bench_coexec.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    fn = lib.aq_bench_coexec_f16 if f16 else lib.aq_bench_coexec
+    fn.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
     rng = np.random.default_rng(1)
     src = hip.to_device(rng.integers(-2**31, 2**31 - 1, size=8192, dtype=np.int64).astype(np.int32))
     out = hip.DeviceBuffer(512 * 256 * 4)
     iters = 2000
     ns = {}
     for nv in (0, 4, 8, 16):
-        assert lib.aq_bench_coexec(nv, ctx.stream, 50, src.ptr, out.ptr) == 0  # warm-up
+        assert fn(nv, ctx.stream, 50, src.ptr, out.ptr) == 0  # warm-up
         e0, e1 = hip.Event(), hip.Event()
         e0.record(ctx.stream)
-        assert lib.aq_bench_coexec(nv, ctx.stream, iters, src.ptr, out.ptr) == 0
+        assert fn(nv, ctx.stream, iters, src.ptr, out.ptr) == 0
         e1.record(ctx.stream)
         e1.synchronize()
         ns[nv] = e0.elapsed_ms(e1) * 1e6 / (4 * iters * 2)  # 4 MFMAs per iteration, 2 wavefronts per SIMD
     out.close()
     src.close()
     slope = (ns[16] - ns[4]) / 12.0
+    kk = 16 if f16 else 32  # the MFMA's k
     return {"ns_per_mfma_per_simd": {f"valu_per_mfma_{nv}": round(v, 3) for nv, v in ns.items()},
             "ns_per_valu_beyond_4": round(slope, 3),
-            "mfma_TOPS_random_operands": round(2.0 * 32 * 32 * 32 / (ns[0] * 1e-9) * 1024 / 1e12, 1)}
+            "mfma_TOPS_random_operands": round(2.0 * 32 * 32 * kk / (ns[0] * 1e-9) * 1024 / 1e12, 1)}
 
 
 def measure_launch_floor(ctx):
