@@ -60,17 +60,21 @@ __global__ void read_strided(const uint8_t *buf, uint32_t bytes, uint32_t *out) 
 // CM = true: the same pieces stored chunk-major (the chunk's seven lines of a
 // piece next to each other), so it reads 896 contiguous bytes.  WAVES
 // wavefronts per workgroup, ng / WAVES workgroups per chunk.
-template <bool CM, int WAVES, int P>
+// GPW > 1: a wavefront takes GPW consecutive groups of its chunk (NPG * GPW
+// pieces, P of them in flight), one workgroup of ng / GPW wavefronts per
+// chunk.
+template <bool CM, int WAVES, int P, int GPW = 1>
 __global__ void read_pattern(const uint8_t *buf, int ng, uint32_t *out) {
-    constexpr int NPG = 9, ROWS = 56;
+    constexpr int NPG = 9, ROWS = 56, NP = NPG * GPW;
     const uint32_t rbs = (uint32_t)ng * NPG * 128;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int per_chunk = ng / WAVES;
+    const int per_chunk = ng / (WAVES * GPW);
     const int chunk = blockIdx.x / per_chunk;
-    const int g = (blockIdx.x % per_chunk) * WAVES + wave;
+    const int g0 = ((blockIdx.x % per_chunk) * WAVES + wave) * GPW;
     const rsrc_t r = buf_rsrc(buf + (size_t)chunk * (ROWS / 8) * rbs, (ROWS / 8) * rbs);
-    auto off = [&](int pc) -> uint32_t {
+    auto off = [&](int j) -> uint32_t {
         if (lane >= ROWS) return BUF_OOB;
+        const int g = g0 + j / NPG, pc = j % NPG;
         return CM ? (uint32_t)((g * NPG + pc) * ROWS * 16 + lane * 16)
                   : (uint32_t)((lane / 8) * rbs + (g * NPG + pc) * 128 + (lane % 8) * 16);
     };
@@ -79,9 +83,9 @@ __global__ void read_pattern(const uint8_t *buf, int ng, uint32_t *out) {
     for (int j = 0; j < P; j++) ring[j] = __builtin_amdgcn_raw_buffer_load_b128(r, off(j), 0, BUF_NT);
     uint32_t acc = 0;
 #pragma unroll
-    for (int j = 0; j < NPG; j++) {
+    for (int j = 0; j < NP; j++) {
         acc ^= ring[j % P].x ^ ring[j % P].y ^ ring[j % P].z ^ ring[j % P].w;
-        if (j + P < NPG) ring[j % P] = __builtin_amdgcn_raw_buffer_load_b128(r, off(j + P), 0, BUF_NT);
+        if (j + P < NP) ring[j % P] = __builtin_amdgcn_raw_buffer_load_b128(r, off(j + P), 0, BUF_NT);
     }
     if (acc == 0x9E3779B9u) out[blockIdx.x % 1024] = acc;
 }
@@ -97,6 +101,9 @@ const Pattern PATTERNS[] = {
     {"matvec pattern: row-block layout, 256-thread workgroups, 6 pieces in flight", false, 4, 6},
     {"matvec pattern: chunk-major layout, 1024-thread workgroups, 6 pieces in flight", true, 16, 6},
     {"matvec pattern: chunk-major layout, 256-thread workgroups, 6 pieces in flight", true, 4, 6},
+    {"matvec pattern: row-block layout, one 256-thread workgroup per chunk, 4 groups per wavefront, all 36 pieces in flight", false, 4, 36},
+    {"matvec pattern: row-block layout, one 256-thread workgroup per chunk, 4 groups per wavefront, 18 pieces in flight", false, 4, 18},
+    {"matvec pattern: row-block layout, one 512-thread workgroup per chunk, 2 groups per wavefront, all 18 pieces in flight", false, 8, 18},
 };
 constexpr int N_PATTERNS = sizeof(PATTERNS) / sizeof(PATTERNS[0]);
 
@@ -161,8 +168,8 @@ const char *aq_bench_read_pattern_name(int v) { return v >= 0 && v < N_PATTERNS 
 
 // Read the Q4_K weight of n rows x ng groups (n a multiple of 56, ng a
 // multiple of 16, at most 64; n * ng * 144 bytes of d_buf, 16-byte aligned)
-// in access pattern v.  Returns 0, -1 for bad arguments, -5 for a launch
-// error.
+// in access pattern v.  Returns 0, -1 for bad arguments (or an ng the
+// pattern's wavefronts x groups do not divide), -5 for a launch error.
 int aq_bench_read_pattern(int v, void *stream, const void *d_buf, int n, int ng, uint32_t *d_out) {
     if (v < 0 || v >= N_PATTERNS || !d_buf || !d_out || n <= 0 || n % 56 || ng <= 0 || ng % 16 || ng > 64 ||
         (int64_t)n * ng * 144 >= ((int64_t)1 << 31) || ((uintptr_t)d_buf & 15))
@@ -170,14 +177,19 @@ int aq_bench_read_pattern(int v, void *stream, const void *d_buf, int n, int ng,
     const Pattern &pt = PATTERNS[v];
     const hipStream_t s = (hipStream_t)stream;
     const uint8_t *b = (const uint8_t *)d_buf;
-    const unsigned grid = (unsigned)(n / 56) * (unsigned)(ng / pt.waves);
+    const int gpw = v >= 5 ? (pt.waves == 4 ? 4 : 2) : 1;  // groups per wavefront
+    if (ng % (pt.waves * gpw)) return -1;
+    const unsigned grid = (unsigned)(n / 56) * (unsigned)(ng / (pt.waves * gpw));
     const unsigned thr = 64u * pt.waves;
     switch (v) {
     case 0: read_pattern<false, 16, 6><<<grid, thr, 0, s>>>(b, ng, d_out); break;
     case 1: read_pattern<false, 16, 9><<<grid, thr, 0, s>>>(b, ng, d_out); break;
     case 2: read_pattern<false, 4, 6><<<grid, thr, 0, s>>>(b, ng, d_out); break;
     case 3: read_pattern<true, 16, 6><<<grid, thr, 0, s>>>(b, ng, d_out); break;
-    default: read_pattern<true, 4, 6><<<grid, thr, 0, s>>>(b, ng, d_out); break;
+    case 4: read_pattern<true, 4, 6><<<grid, thr, 0, s>>>(b, ng, d_out); break;
+    case 5: read_pattern<false, 4, 36, 4><<<grid, thr, 0, s>>>(b, ng, d_out); break;
+    case 6: read_pattern<false, 4, 18, 4><<<grid, thr, 0, s>>>(b, ng, d_out); break;
+    default: read_pattern<false, 8, 18, 2><<<grid, thr, 0, s>>>(b, ng, d_out); break;
     }
     return hipGetLastError() == hipSuccess ? 0 : -5;
 }
