@@ -281,22 +281,31 @@ PREFILL_CASES = {  # name: (weight type, n, k, m, seed)
 }
 
 
-def cpu_decode_baseline(hw, prompt, n_prompt=16, n_steps=4) -> dict:
+def cpu_decode_baseline(hw, prompt, n_steps=4, seed=0) -> dict:
     """Decode on the host with the CPU restatement of candle's quantized_llama
     (oracle/llama_ref.py: numpy f32 glue, the oracle's k_quants::matmul on all
-    host cores): a short prompt (the per-token cost of decode is the weights,
-    634 MB a token, not the context), then greedy steps, timed."""
+    host cores) at the GPU run's context: the KV cache of every layer filled
+    to the prompt's length (random values: a step's cost does not depend on
+    them, and a CPU prefill of 512 rows would take tens of seconds), then
+    n_steps greedy steps from there, timed -- positions len(prompt) ..
+    len(prompt) + n_steps - 1, the GPU run's first n_steps."""
     from oracle.llama_ref import RefLlama
 
+    cfg = hw.cfg
     ref = RefLlama(hw)
-    logits = ref.forward(prompt[:n_prompt], 0)
+    rng = np.random.default_rng(seed)
+    n = len(prompt)
+    ref.k = [rng.standard_normal((cfg.n_kv_head, n, cfg.head_dim)).astype(np.float32) for _ in range(cfg.n_layer)]
+    ref.v = [rng.standard_normal((cfg.n_kv_head, n, cfg.head_dim)).astype(np.float32) for _ in range(cfg.n_layer)]
+    tok = int(prompt[-1])
     t0 = time.perf_counter()
     for i in range(n_steps):
-        logits = ref.forward([int(np.argmax(logits))], n_prompt + i)
+        tok = int(np.argmax(ref.forward([tok], n + i)))
     dt = (time.perf_counter() - t0) / n_steps
     return {"decode_tok_s": round(1.0 / dt, 3), "decode_ms_per_tok": round(dt * 1e3, 2), "cores": os.cpu_count() or 1,
             "kind": "port", "cpu": cpu_model(), "isa": ISA_NOTES["baseline"],
-            "sample": f"{n_steps} greedy steps after a {n_prompt}-token prompt"}
+            "sample": f"{n_steps} greedy steps at positions {n}..{n + n_steps - 1} (the GPU run's context; KV cache "
+                      f"filled to {n} positions)"}
 
 
 def decode_model(name, max_seq, seed):
