@@ -18,6 +18,8 @@ namespace aq {
 
 namespace {
 
+typedef float v16f __attribute__((ext_vector_type(16)));
+
 // Sum / max over aligned groups of N = 16 or 32 lanes; every lane of a group
 // gets the result (DPP within 16-lane rows, one cross-row swap for 32).
 template <int N>
@@ -358,168 +360,191 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(const float *__restrict__ 
     }
 }
 
-// 2) attn_prefill_kernel: one workgroup of 256 threads per (query tile of
-//    32 rows, query head).  The tile's query rows (rotated at their
-//    positions) sit in LDS; key/value tiles of 64 cached positions stream
-//    through LDS up to the tile's last position; scores, the causal mask and
-//    an online softmax (running max and sum per row, the output rescaled
-//    when the max grows) are kept in registers.  Thread (rg = tid / 16, cg =
-//    tid % 16) owns query rows rg + 16a (a < 2), key columns cg + 16b (b < 4)
-//    of each score tile and output float4 columns cg + 16e (e < hd / 64).
-//    LDS rows are padded by 4 floats so the 16 lanes of a row group read 16
-//    different banks.  Causal tiles differ in work (tile t reads t / 2 + 1
-//    key tiles), so workgroups are dealt light and heavy alternately: in
-//    dispatch order the tiles run 0, last, 1, last - 1, ..., each for every
-//    head, and the several workgroups a CU holds even out.
-constexpr int PF_QT = 32, PF_KT = 64, PF_PAD = 4, PF_A = PF_QT / 16;
+// 2) attn_prefill_kernel: one workgroup of four wavefronts per (query tile
+//    of 32 rows, query head), on the f32 matrix cores
+//    (v_mfma_f32_32x32x2f32: f32 products, f32 sums).  Wavefront w takes the
+//    key blocks w, w + 4, ... (32 cached positions each) up to the tile's
+//    last position, and keeps a running max, sum and output per query row;
+//    the four are combined through LDS at the end (M = max m_w, out = sum
+//    e^(m_w - M) o_w / sum e^(m_w - M) l_w).
+//    Scores are formed transposed, S^T[key][query] = K . Q^T: lane (j, hh)
+//    holds query j against 16 keys, so the softmax of a query row needs only
+//    its own registers and the other lane half (lane ^ 32).  Those registers
+//    are also the B operand of the P . V product, taken as
+//    O^T[dim][query] += V^T[dim][key] . P^T[key][query], so the output rows
+//    stay with their lanes and no probability moves between lanes.  The head
+//    dims of the score product are split between the lane halves (hh * hd/2
+//    ..), so each lane reads its q and k rows as contiguous halves.
+//    A block's V values are loaded before its score MFMAs and the next
+//    block's K half-rows before its P . V MFMAs, so each load waits under the
+//    other half's matrix work.  Workgroups are dispatched with the tiles that
+//    have the most keys first.
+constexpr int PM_QT = 32, PM_KB = 32, PM_W = 4;
 
 template <int HD>
-__global__ __launch_bounds__(256) void attn_prefill_kernel(const float *__restrict__ q, int64_t ldq,
-                                                           const float *__restrict__ cosb,
-                                                           const float *__restrict__ sinb,
-                                                           const float *__restrict__ kc, const float *__restrict__ vc,
-                                                           int index_pos, int m, int n_head, int n_kv, int max_seq,
-                                                           float *__restrict__ out) {
-    constexpr int HS = HD + PF_PAD;
-    constexpr int PS = PF_KT + PF_PAD;
-    constexpr int DV = HD / 64;  // output float4 columns per thread
-    __shared__ __align__(16) float qs[PF_QT * HS];
-    __shared__ __align__(16) float ks[PF_KT * HS];
-    __shared__ __align__(16) float vs[PF_KT * HS];
-    __shared__ __align__(16) float ps[PF_QT * PS];
-    const int tid = threadIdx.x, rg = tid / 16, cg = tid % 16;
-    const int ntq = (m + PF_QT - 1) / PF_QT;
+__global__ __launch_bounds__(64 * PM_W) void attn_prefill_kernel(const float *__restrict__ q, int64_t ldq,
+                                                                 const float *__restrict__ cosb,
+                                                                 const float *__restrict__ sinb,
+                                                                 const float *__restrict__ kc,
+                                                                 const float *__restrict__ vc, int index_pos, int m,
+                                                                 int n_head, int n_kv, int max_seq,
+                                                                 float *__restrict__ out) {
+    constexpr int H2 = HD / 2;   // head dims per lane half: the score MFMAs' K steps
+    constexpr int NB = HD / 32;  // 32-row blocks of the output's head dims
+    __shared__ float sm_m[PM_W][PM_QT], sm_l[PM_W][PM_QT];
+    __shared__ float sm_o[PM_W][PM_QT][32 + 1];
+
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int j = lane & 31, hh = lane >> 5;
+    const int ntq = (m + PM_QT - 1) / PM_QT;
     const int rank = blockIdx.x / n_head, h = blockIdx.x % n_head;
-    const int tq = (rank & 1) ? ntq - 1 - (rank >> 1) : (rank >> 1);  // 0, last, 1, last - 1, ...
+    const int tq = ntq - 1 - rank;  // the tiles with the most keys first
+    const int qb = tq * PM_QT, rows = min(PM_QT, m - qb);
     const int kvh = h / (n_head / n_kv);
-    const int r0 = tq * PF_QT;
-    const int rows = min(PF_QT, m - r0);
     const float *kh = kc + (int64_t)kvh * max_seq * HD;
     const float *vh = vc + (int64_t)kvh * max_seq * HD;
+    const int kend = index_pos + qb + rows;  // keys 0 .. kend - 1
+    const int nkb = (kend + PM_KB - 1) / PM_KB;
+    const int qpos = index_pos + qb + j;
 
-    for (int i = tid; i < PF_QT * HD / 2; i += 256) {
-        const int r = i / (HD / 2), j = i % (HD / 2);
-        float a = 0.0f, b = 0.0f, c = 0.0f, sn = 0.0f;
-        if (r < rows) {
-            const float *qr = q + (int64_t)(r0 + r) * ldq + (int64_t)h * HD;
-            const int64_t p = index_pos + r0 + r;
-            a = qr[2 * j];
-            b = qr[2 * j + 1];
-            c = cosb[p * (HD / 2) + j];
-            sn = sinb[p * (HD / 2) + j];
+    // this lane's query fragment: dims hh * H2 .. of row qb + j, rotated at qpos
+    float qv[H2];
+#pragma unroll
+    for (int i = 0; i < H2; i++) qv[i] = 0.0f;
+    if (j < rows) {
+        const float *qr = q + (int64_t)(qb + j) * ldq + (int64_t)h * HD + hh * H2;
+        const float *cr = cosb + (int64_t)qpos * (HD / 2) + hh * (H2 / 2);
+        const float *sr = sinb + (int64_t)qpos * (HD / 2) + hh * (H2 / 2);
+#pragma unroll
+        for (int i = 0; i < H2 / 2; i++) {
+            const float a = qr[2 * i], b = qr[2 * i + 1], c = cr[i], sn = sr[i];
+            qv[2 * i] = a * c - b * sn;
+            qv[2 * i + 1] = a * sn + b * c;
         }
-        qs[r * HS + 2 * j] = a * c - b * sn;
-        qs[r * HS + 2 * j + 1] = a * sn + b * c;
     }
 
-    float mrun[PF_A], lrun[PF_A];
-    float4 o[PF_A][DV];
-#pragma unroll
-    for (int a = 0; a < PF_A; a++) {
-        mrun[a] = -INFINITY;
-        lrun[a] = 0.0f;
-#pragma unroll
-        for (int e = 0; e < DV; e++) o[a][e] = ZERO4;
-    }
     const float rs = sqrtf((float)HD);
-    const int kend = index_pos + r0 + rows;  // keys 0..kend-1 (the tile's last query position)
-    for (int k0 = 0; k0 < kend; k0 += PF_KT) {
-        __syncthreads();  // the previous tile's reads of ks, vs, ps are done (and qs is written)
-        for (int i = tid; i < PF_KT * HD / 4; i += 256) {
-            const int c = i / (HD / 4), d4 = i % (HD / 4);
-            float4 kv = ZERO4, vv = ZERO4;
-            if (k0 + c < kend) {
-                kv = *(const float4 *)(kh + (int64_t)(k0 + c) * HD + 4 * d4);
-                vv = *(const float4 *)(vh + (int64_t)(k0 + c) * HD + 4 * d4);
-            }
-            *(float4 *)&ks[c * HS + 4 * d4] = kv;
-            *(float4 *)&vs[c * HS + 4 * d4] = vv;
+    float mrun = -INFINITY, lrun = 0.0f;
+    v16f o[NB];
+#pragma unroll
+    for (int b = 0; b < NB; b++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) o[b][r] = 0.0f;
+
+    // loads: a key block's V rows are issued before its score MFMAs and the
+    // next block's K rows before its PV MFMAs, so each load's latency passes
+    // under the other half's matrix work.  Rows past kend are clamped to the
+    // last valid row (their probabilities are zero; the values stay finite).
+    float kv[H2], vv[NB][16];
+    auto load_k = [&](int kb) {
+        const int krow = min(kb * PM_KB + j, kend - 1);
+        const float4 *kr4 = (const float4 *)(kh + (int64_t)krow * HD + hh * H2);
+#pragma unroll
+        for (int i = 0; i < H2 / 4; i++) {
+            const float4 t = kr4[i];
+            kv[4 * i] = t.x;
+            kv[4 * i + 1] = t.y;
+            kv[4 * i + 2] = t.z;
+            kv[4 * i + 3] = t.w;
         }
-        __syncthreads();
-        float sacc[PF_A][4];
+    };
+    if (w < nkb) load_k(w);
+    for (int kb = w; kb < nkb; kb += PM_W) {
+        const int k0 = kb * PM_KB;
 #pragma unroll
-        for (int a = 0; a < PF_A; a++)
+        for (int b = 0; b < NB; b++)
 #pragma unroll
-            for (int b = 0; b < 4; b++) sacc[a][b] = 0.0f;
-#pragma unroll 4
-        for (int d = 0; d < HD; d += 4) {
-            float4 qv[PF_A], kv[4];
+            for (int st = 0; st < 16; st++) {
+                const int key = min(k0 + 8 * (st >> 2) + 4 * hh + (st & 3), kend - 1);
+                vv[b][st] = vh[(int64_t)key * HD + 32 * b + j];
+            }
+        // S^T[key][query] = sum over the head dims of K[key] * Q[query]
+        v16f s, s1;  // two independent chains (even and odd steps), added at the end
 #pragma unroll
-            for (int a = 0; a < PF_A; a++) qv[a] = *(const float4 *)&qs[(rg + 16 * a) * HS + d];
+        for (int r = 0; r < 16; r++) s[r] = s1[r] = 0.0f;
 #pragma unroll
-            for (int b = 0; b < 4; b++) kv[b] = *(const float4 *)&ks[(cg + 16 * b) * HS + d];
-#pragma unroll
-            for (int a = 0; a < PF_A; a++)
-#pragma unroll
-                for (int b = 0; b < 4; b++) {
-                    float t = sacc[a][b];
-                    t = __builtin_fmaf(qv[a].x, kv[b].x, t);
-                    t = __builtin_fmaf(qv[a].y, kv[b].y, t);
-                    t = __builtin_fmaf(qv[a].z, kv[b].z, t);
-                    t = __builtin_fmaf(qv[a].w, kv[b].w, t);
-                    sacc[a][b] = t;
-                }
+        for (int d = 0; d < H2; d += 2) {
+            s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv[d], qv[d], s, 0, 0, 0);
+            s1 = __builtin_amdgcn_mfma_f32_32x32x2f32(kv[d + 1], qv[d + 1], s1, 0, 0, 0);
         }
+        s += s1;
+        if (kb + PM_W < nkb) load_k(kb + PM_W);
+        // lane (j, hh) register r: query j, key k0 + 8 (r / 4) + 4 hh + r % 4
+        float pv[16];
+        float bm = -INFINITY;
 #pragma unroll
-        for (int a = 0; a < PF_A; a++) {
-            const int r = rg + 16 * a, qpos = index_pos + r0 + r;
-            float sv[4], tmax = -INFINITY;
-#pragma unroll
-            for (int b = 0; b < 4; b++) {
-                const int kp = k0 + cg + 16 * b;
-                sv[b] = kp > qpos ? -INFINITY : sacc[a][b] / rs;
-                tmax = fmaxf(tmax, sv[b]);
-            }
-            tmax = group16_max(tmax);
-            const float mnew = fmaxf(mrun[a], tmax);  // finite: key 0 is never masked
-            const float scale = expf(mrun[a] - mnew);
-            float psum = 0.0f;
-#pragma unroll
-            for (int b = 0; b < 4; b++) {
-                const float e = expf(sv[b] - mnew);
-                ps[r * PS + cg + 16 * b] = e;
-                psum += e;
-            }
-            psum = group_sum<16>(psum);
-            lrun[a] = __builtin_fmaf(lrun[a], scale, psum);
-            mrun[a] = mnew;
-#pragma unroll
-            for (int e = 0; e < DV; e++) {
-                o[a][e].x *= scale;
-                o[a][e].y *= scale;
-                o[a][e].z *= scale;
-                o[a][e].w *= scale;
-            }
+        for (int r = 0; r < 16; r++) {
+            const int key = k0 + 8 * (r >> 2) + 4 * hh + (r & 3);
+            pv[r] = key > qpos ? -INFINITY : s[r] / rs;
+            bm = fmaxf(bm, pv[r]);
         }
-        __syncthreads();
-        const int kn = min(PF_KT, kend - k0);
-        for (int c = 0; c < kn; c += 4) {
-            float4 pv[PF_A];
+        bm = fmaxf(bm, __shfl_xor(bm, 32));
+        const float mnew = fmaxf(mrun, bm);
+        const float msafe = mnew == -INFINITY ? 0.0f : mnew;  // a block wholly past this query
+        const float scale = expf(mrun - msafe);
+        float ps = 0.0f;
 #pragma unroll
-            for (int a = 0; a < PF_A; a++) pv[a] = *(const float4 *)&ps[(rg + 16 * a) * PS + c];
-#pragma unroll
-            for (int cc = 0; cc < 4; cc++) {
-#pragma unroll
-                for (int e = 0; e < DV; e++) {
-                    const float4 vv = *(const float4 *)&vs[(c + cc) * HS + 4 * (cg + 16 * e)];
-#pragma unroll
-                    for (int a = 0; a < PF_A; a++) {
-                        const float w = cc == 0 ? pv[a].x : cc == 1 ? pv[a].y : cc == 2 ? pv[a].z : pv[a].w;
-                        axpy4(o[a][e], w, vv);
-                    }
-                }
-            }
+        for (int r = 0; r < 16; r++) {
+            pv[r] = expf(pv[r] - msafe);
+            ps += pv[r];
         }
+        ps += __shfl_xor(ps, 32);
+        lrun = __builtin_fmaf(lrun, scale, ps);
+        mrun = mnew;
+#pragma unroll
+        for (int b = 0; b < NB; b++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) o[b][r] *= scale;
+        // O^T[head dim][query] += V^T[head dim][key] . P^T[key][query]
+#pragma unroll
+        for (int st = 0; st < 16; st++)
+#pragma unroll
+            for (int b = 0; b < NB; b++) o[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv[b][st], pv[st], o[b], 0, 0, 0);
     }
+
+    // combine the four wavefronts' key ranges: M = max m_w, out = sum e^(m_w - M) o_w / sum e^(m_w - M) l_w
+    if (hh == 0) {
+        sm_m[w][j] = mrun;
+        sm_l[w][j] = lrun;
+    }
+    // 32-dim rounds: the threads split the tile's 32 rows x 32 dims
+    constexpr int TPR = 2 * PM_W;       // threads per query row
+    constexpr int DPT = 32 / TPR;       // dims per thread per round (8 or 4)
+    const int qq = tid / TPR, part = tid % TPR;
 #pragma unroll
-    for (int a = 0; a < PF_A; a++) {
-        const int r = rg + 16 * a;
-        if (r < rows) {
-            float *orow = out + (int64_t)(r0 + r) * n_head * HD + (int64_t)h * HD;
-            const float L = lrun[a];
+    for (int b = 0; b < NB; b++) {
+        __syncthreads();  // the previous round's reads are done (and m, l written)
 #pragma unroll
-            for (int e = 0; e < DV; e++)
-                ((float4 *)orow)[cg + 16 * e] = make_float4(o[a][e].x / L, o[a][e].y / L, o[a][e].z / L, o[a][e].w / L);
+        for (int r = 0; r < 16; r++) sm_o[w][j][8 * (r >> 2) + 4 * hh + (r & 3)] = o[b][r];
+        __syncthreads();
+        float ew[PM_W], M = -INFINITY;
+#pragma unroll
+        for (int ww = 0; ww < PM_W; ww++) M = fmaxf(M, sm_m[ww][qq]);
+        const float Ms = M == -INFINITY ? 0.0f : M;
+        float L = 0.0f;
+#pragma unroll
+        for (int ww = 0; ww < PM_W; ww++) {
+            ew[ww] = expf(sm_m[ww][qq] - Ms);
+            L = __builtin_fmaf(ew[ww], sm_l[ww][qq], L);
+        }
+        if (qq < rows) {
+            float res[DPT];
+#pragma unroll
+            for (int dd = 0; dd < DPT; dd++) {
+                float acc = 0.0f;
+#pragma unroll
+                for (int ww = 0; ww < PM_W; ww++) acc = __builtin_fmaf(ew[ww], sm_o[ww][qq][part * DPT + dd], acc);
+                res[dd] = acc / L;
+            }
+            float *orow = out + (int64_t)(qb + qq) * n_head * HD + (int64_t)h * HD + 32 * b + part * DPT;
+            if constexpr (DPT % 4 == 0) {
+#pragma unroll
+                for (int u = 0; u < DPT / 4; u++)
+                    ((float4 *)orow)[u] = make_float4(res[4 * u], res[4 * u + 1], res[4 * u + 2], res[4 * u + 3]);
+            } else {
+#pragma unroll
+                for (int u = 0; u < DPT / 2; u++) ((float2 *)orow)[u] = make_float2(res[2 * u], res[2 * u + 1]);
+            }
         }
     }
 }
@@ -595,12 +620,12 @@ hipError_t launch_attn_prefill(const float *q, int64_t ldq, const float *k, int6
     if (((uintptr_t)kc | (uintptr_t)vc | (uintptr_t)out) & 15) return hipErrorInvalidValue;
     rope_kv_kernel<<<(unsigned)m, 256, 0, s>>>(k, ldk, v, ldv, cosb, sinb, (int)index_pos, (int)n_kv, (int)hd,
                                                (int)max_seq, kc, vc);
-    const unsigned grid = (unsigned)(((m + PF_QT - 1) / PF_QT) * n_head);
+    const unsigned grid = (unsigned)(((m + PM_QT - 1) / PM_QT) * n_head);
     if (hd == 64)
-        attn_prefill_kernel<64><<<grid, 256, 0, s>>>(q, ldq, cosb, sinb, kc, vc, (int)index_pos, (int)m, (int)n_head,
+        attn_prefill_kernel<64><<<grid, 64 * PM_W, 0, s>>>(q, ldq, cosb, sinb, kc, vc, (int)index_pos, (int)m, (int)n_head,
                                                      (int)n_kv, (int)max_seq, out);
     else
-        attn_prefill_kernel<128><<<grid, 256, 0, s>>>(q, ldq, cosb, sinb, kc, vc, (int)index_pos, (int)m,
+        attn_prefill_kernel<128><<<grid, 64 * PM_W, 0, s>>>(q, ldq, cosb, sinb, kc, vc, (int)index_pos, (int)m,
                                                       (int)n_head, (int)n_kv, (int)max_seq, out);
     return hipGetLastError();
 }

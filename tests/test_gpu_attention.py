@@ -11,7 +11,7 @@ head; a partial record per slice, then a combining launch) at positions on
 and around the slice boundaries, up to the longest context, called back to
 back on one context (the partial records are reused by every call).
 Prefill: prompts at offset 0 and later, lengths that are not a multiple of
-the 64-row query tile, q / k / v read with row strides from one merged
+the 32-row query tile, q / k / v read with row strides from one merged
 buffer."""
 import ctypes
 
