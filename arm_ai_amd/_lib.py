@@ -91,6 +91,8 @@ SIGNATURES = {
     "aq_qmatmul_silu_mul_f32_device": (INT, [P, P, P, I64, P]),
     "aq_qmatmul2_rmsnorm_f32_device": (INT, [P, P, P, P, P, P, ctypes.c_float, I64, P, P, P]),
     "aq_llama_swiglu_pairs": (INT, [P, P, I64, I64, I64, P]),
+    "aq_llama_rmsnorm_act": (INT, [P, P, P, P, I64, I64, ctypes.c_float, P, P]),
+    "aq_llama_swiglu_pairs_act": (INT, [P, P, I64, I64, I64, P, P]),
     "aq_swiglu_fused": (INT, [INT, I64, I64]),
     "aq_llama_head_argmax_embed": (INT, [P, P, P, P, P, ctypes.c_float, I64, P, P, P, P, I64, P, I64, P]),
     "aq_qmatmul_rmsnorm_swiglu_f32_device": (INT, [P, P, P, P, P, ctypes.c_float, I64, P, P]),

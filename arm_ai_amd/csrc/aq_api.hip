@@ -227,7 +227,7 @@ int run_matmul(aq_ctx *ctx, const aq_qweight *w, const float *d_x, int64_t m, fl
     hipError_t e;
     if (use_gemm(w, m)) {
         ActPlanes a = act_planes(act, m, w->k);
-        a.q16 = gemm_q16_plane(w->glayout.type, m, w->n, w->k, ws);  // f16-MFMA GEMMs: quants as f16 too
+        if (w->glayout.type != TYPE_Q6_K && w->glayout.type != TYPE_Q5_K) a.q16 = nullptr;  // f16-MFMA GEMMs only
         e = act_q80(w->type) ? launch_quantize_q8_0(d_x, m, w->k, a, ctx->stream)
                                     : launch_quantize_q8k(d_x, m, w->k, a, ctx->stream);
         if (e != hipSuccess) return fail(AQ_ERR_HIP, "activation quantizer: %s", hipGetErrorString(e));
@@ -237,6 +237,7 @@ int run_matmul(aq_ctx *ctx, const aq_qweight *w, const float *d_x, int64_t m, fl
         e = launch_matvec(w->layout, w->n, w->k, nullptr, &a, m, d_y, dS, dSmin, ctx->stream);
     } else if (use_mmv(w, m)) {
         ActPlanes a = act_planes(act, m, w->k);
+        a.q16 = nullptr;
         e = launch_quantize_q8k(d_x, m, w->k, a, ctx->stream);
         if (e != hipSuccess) return fail(AQ_ERR_HIP, "activation quantizer: %s", hipGetErrorString(e));
         e = launch_mmv(w->layout, w->n, w->k, a, m, d_y, dS, dSmin, ctx->stream);
@@ -246,6 +247,7 @@ int run_matmul(aq_ctx *ctx, const aq_qweight *w, const float *d_x, int64_t m, fl
     } else {
         // the fused prologue reads float4; quantise separately instead
         ActPlanes a = act_planes(act, m, w->k);
+        a.q16 = nullptr;
         e = act_q80(w->type) ? launch_quantize_q8_0(d_x, m, w->k, a, ctx->stream)
                                     : launch_quantize_q8k(d_x, m, w->k, a, ctx->stream);
         if (e != hipSuccess) return fail(AQ_ERR_HIP, "activation quantizer: %s", hipGetErrorString(e));
@@ -589,6 +591,7 @@ static int quantize_host(aq_ctx *ctx, int atype, const float *x, int64_t m, int6
     memcpy(ctx->pinned, x, xin);
     HIP_TRY(hipMemcpyAsync(d_x, ctx->pinned, xin, hipMemcpyHostToDevice, ctx->stream));
     ActPlanes a = act_planes(S, m, k);
+    a.q16 = nullptr;
     hipError_t e = atype == AQ_TYPE_Q8_K ? launch_quantize_q8k(d_x, m, k, a, ctx->stream)
                                          : launch_quantize_q8_0(d_x, m, k, a, ctx->stream);
     if (e != hipSuccess) return fail(AQ_ERR_HIP, "quantizer: %s", hipGetErrorString(e));
@@ -1052,6 +1055,37 @@ int aq_llama_swiglu_pairs(aq_ctx *ctx, const float *d_y, int64_t ld, int64_t m, 
     int rc = use_device(ctx->device);
     if (rc) return rc;
     return hip_status(launch_swiglu_pairs(d_y, ld, m, ffn, d_out, ctx->stream), "swiglu pairs");
+}
+
+int aq_llama_rmsnorm_act(aq_ctx *ctx, float *d_x, const float *d_delta, const float *d_w, int64_t m, int64_t n,
+                         float eps, float *d_out, void *d_act) {
+    if (!ctx) return fail(AQ_ERR_INVALID_ARG, "null context");
+    if (m < 0 || n <= 0 || n % QK_K) return fail(AQ_ERR_SHAPE, "n=%lld is not a positive multiple of 256", (long long)n);
+    if (m == 0) return AQ_OK;
+    if (!d_x || !d_w || !d_act) return fail(AQ_ERR_INVALID_ARG, "null argument");
+    if ((uintptr_t)d_act & 255) return fail(AQ_ERR_INVALID_ARG, "activation buffer must be 256-byte aligned");
+    if (((uintptr_t)d_x | (uintptr_t)d_delta | (uintptr_t)d_w | (uintptr_t)d_out) & 15)
+        return fail(AQ_ERR_INVALID_ARG, "x, delta, w and out must be 16-byte aligned");
+    int rc = use_device(ctx->device);
+    if (rc) return rc;
+    return hip_status(launch_rmsnorm_act(d_x, d_delta, d_w, m, n, eps, d_out, act_planes(d_act, m, n), ctx->stream),
+                      "rmsnorm + quantize");
+}
+
+int aq_llama_swiglu_pairs_act(aq_ctx *ctx, const float *d_y, int64_t ld, int64_t m, int64_t ffn, float *d_out,
+                              void *d_act) {
+    if (!ctx) return fail(AQ_ERR_INVALID_ARG, "null context");
+    if (m < 0 || ffn <= 0 || ffn % QK_K)
+        return fail(AQ_ERR_SHAPE, "ffn=%lld is not a positive multiple of 256", (long long)ffn);
+    if (m == 0) return AQ_OK;
+    if (!d_y || !d_act) return fail(AQ_ERR_INVALID_ARG, "null argument");
+    if ((uintptr_t)d_act & 255) return fail(AQ_ERR_INVALID_ARG, "activation buffer must be 256-byte aligned");
+    if ((((uintptr_t)d_y | (uintptr_t)d_out) & 15) || ld % 4)
+        return fail(AQ_ERR_INVALID_ARG, "y and out must be 16-byte aligned, ld a multiple of 4");
+    int rc = use_device(ctx->device);
+    if (rc) return rc;
+    return hip_status(launch_swiglu_pairs_act(d_y, ld, m, ffn, d_out, act_planes(d_act, m, ffn), ctx->stream),
+                      "swiglu pairs + quantize");
 }
 
 int aq_llama_head_argmax_embed(aq_ctx *ctx, const aq_qweight *w, const float *d_x, const float *d_delta,

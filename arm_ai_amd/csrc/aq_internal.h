@@ -86,20 +86,24 @@ inline int groups_of(int type, int64_t k) {
 //   bsums [m][k/16]   i16 (Q8_K)
 //   bsum16 [m][k/16]  the same bsums as f16 bits (exact: |bsum| <= 2048), the
 //                     A operand of the GEMM's f16 MFMA for the min term
+//   q16   [m][k]      the qs as f16 bits, the activation operand of the
+//                     f16-MFMA GEMMs (Q6_K, Q5_K); written by the Q8_K
+//                     quantizers when the pointer is set (paths that feed no
+//                     such GEMM clear it)
 struct ActPlanes {
     int8_t *qs;
     float *d;
     uint16_t *d16;
     int16_t *bsums;
     uint16_t *bsum16;
-    uint16_t *q16 = nullptr;  // optional: the qs as f16 [m][k], written by the Q8_K quantizer when set
+    uint16_t *q16 = nullptr;
 };
 
 inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
 // Sizes of the activation planes for m rows of k (bytes, each plane 256-B aligned).
 struct ActSizes {
-    size_t qs, d, d16, bsums, bsum16, total;
+    size_t qs, d, d16, bsums, bsum16, q16, total;
 };
 inline ActSizes act_sizes(int64_t m, int64_t k) {
     ActSizes s;
@@ -108,7 +112,8 @@ inline ActSizes act_sizes(int64_t m, int64_t k) {
     s.d16 = align_up((size_t)m * (k / 32) * 2, 256);
     s.bsums = align_up((size_t)m * (k / 16) * 2, 256);
     s.bsum16 = s.bsums;
-    s.total = s.qs + s.d + s.d16 + s.bsums + s.bsum16;
+    s.q16 = align_up((size_t)m * k * 2, 256);
+    s.total = s.qs + s.d + s.d16 + s.bsums + s.bsum16 + s.q16;
     return s;
 }
 inline ActPlanes act_planes(void *base, int64_t m, int64_t k) {
@@ -120,6 +125,7 @@ inline ActPlanes act_planes(void *base, int64_t m, int64_t k) {
     a.d16 = (uint16_t *)(p + s.qs + s.d);
     a.bsums = (int16_t *)(p + s.qs + s.d + s.d16);
     a.bsum16 = (uint16_t *)(p + s.qs + s.d + s.d16 + s.bsums);
+    a.q16 = (uint16_t *)(p + s.qs + s.d + s.d16 + s.bsums + s.bsum16);
     return a;
 }
 
@@ -194,15 +200,10 @@ hipError_t launch_gemm(const WLayout &w, int64_t n, int64_t k, const ActPlanes &
 // weight type / shape has no GEMM (the matvec then serves m > 8 too).
 size_t gemm_workspace_bytes(int type, int64_t m, int64_t n, int64_t k);
 // The Q6_K and Q5_K GEMM on f16 MFMA (k_gemm6.hip), reached through launch_gemm /
-// gemm_workspace_bytes; its workspace holds the f16 copy of the activation
-// quants and the split-K partials.
+// gemm_workspace_bytes.  It reads the activation quants as f16 from
+// ActPlanes::q16 when that is set (the quantizer wrote them), else converts
+// them into its workspace first; the workspace also holds the split-K partials.
 size_t gemm6_workspace_bytes(int64_t m, int64_t n, int64_t k);
-// Where in ws the GEMM for this weight type reads f16 activation quants, or
-// null if it reads none (or converts them per launch chunk).  A Q8_K
-// quantizer given this plane as ActPlanes::q16 writes them there, and the
-// GEMM then skips its own conversion launch.
-uint16_t *gemm_q16_plane(int type, int64_t m, int64_t n, int64_t k, void *ws);
-uint16_t *gemm6_q16_plane(int64_t m, int64_t n, int64_t k, void *ws);
 hipError_t launch_gemm6(const WLayout &w, int64_t n, int64_t k, const ActPlanes &x, int64_t m, float *y, int32_t *S,
                         int32_t *Smin, void *ws, size_t ws_bytes, hipStream_t s);
 // The Q8_0 GEMM on int8 MFMA (k_gemm8.hip), reached through launch_gemm /
@@ -264,6 +265,14 @@ hipError_t launch_embed(const float *table, int64_t vocab, const int64_t *d_tok,
 hipError_t launch_rmsnorm(float *x, const float *delta, const float *w, int64_t m, int64_t n, float eps, float *out,
                           hipStream_t s);
 hipError_t launch_silu_mul(const float *g, const float *u, int64_t ld, int64_t m, int64_t n, float *out, hipStream_t s);
+// The prompt's norm and SwiGLU quantised to Q8_K in the same launch (the
+// planes of a, q16 written when set): the values of launch_rmsnorm and
+// launch_swiglu_pairs bit for bit (also written to out when it is non-null);
+// n a multiple of 256.
+hipError_t launch_rmsnorm_act(float *x, const float *delta, const float *w, int64_t m, int64_t n, float eps,
+                              float *out, const ActPlanes &a, hipStream_t s);
+hipError_t launch_swiglu_pairs_act(const float *y, int64_t ld, int64_t m, int64_t n, float *out, const ActPlanes &a,
+                                   hipStream_t s);
 // silu(g) * u of m rows of a paired gate|up weight's output (row stride ld,
 // n = the number of pairs, a multiple of 4)
 hipError_t launch_swiglu_pairs(const float *y, int64_t ld, int64_t m, int64_t n, float *out, hipStream_t s);
@@ -531,6 +540,30 @@ __device__ __forceinline__ uint4 q8k_block_row16(const float v[16], int s, int *
     *bsum = bs;
     *d = dd;
     return make_uint4(pack4_i8(q), pack4_i8(q + 4), pack4_i8(q + 8), pack4_i8(q + 12));
+}
+
+// The stores of one Q8_K block by its 16 lanes (q8k_block_row16's layout):
+// lane s writes quants 16s..16s+15 (and their f16 copy when a.q16 is set)
+// and bsum s; lane 0 writes d.  Block sb of row `row`, rows of k elements.
+__device__ __forceinline__ void store_q8k_block16(const ActPlanes &a, int64_t row, int64_t k, int64_t sb, int s,
+                                                  uint4 packed, int bsum, float d) {
+    const int64_t e0 = row * k + sb * QK_K + 16 * s;
+    *(uint4 *)(a.qs + e0) = packed;
+    if (a.q16) {
+        const uint32_t w[4] = {packed.x, packed.y, packed.z, packed.w};
+        uint32_t o[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const uint32_t lo = __builtin_bit_cast(uint16_t, (_Float16)(int)(int8_t)((w[j >> 1] >> (16 * (j & 1))) & 0xffu));
+            const uint32_t hi = __builtin_bit_cast(uint16_t, (_Float16)(int)(int8_t)((w[j >> 1] >> (16 * (j & 1) + 8)) & 0xffu));
+            o[j] = lo | (hi << 16);
+        }
+        *(uint4 *)(a.q16 + e0) = make_uint4(o[0], o[1], o[2], o[3]);
+        *(uint4 *)(a.q16 + e0 + 8) = make_uint4(o[4], o[5], o[6], o[7]);
+    }
+    a.bsums[row * (k / 16) + sb * 16 + s] = (int16_t)bsum;
+    a.bsum16[row * (k / 16) + sb * 16 + s] = __builtin_bit_cast(uint16_t, (_Float16)(float)bsum);
+    if (s == 0) a.d[row * (k / QK_K) + sb] = d;
 }
 
 // One Q8_0 block (BlockQ8_0::from_float) quantised by eight consecutive

@@ -70,15 +70,16 @@ __global__ __launch_bounds__(DEC_THREADS) void embed_kernel(const float *__restr
 // One row per workgroup: x += delta (when delta is given, written back to x:
 // the residual stream), then out = x / sqrt(sum(x^2)/n + eps) * w.  The row
 // (n % 4 == 0, n <= 4 * RMS_V * DEC_THREADS) is held in registers, so x is
-// read once and every load is issued before the first use.
+// read once and every load is issued before the first use.  The body is
+// shared by the kernel that quantises the result in the same launch
+// (rmsnorm_act_kernel), so both produce the same values bit for bit: `put`
+// receives float4 i of the output row.
 constexpr int RMS_V = 8;
-__global__ __launch_bounds__(DEC_THREADS) void rmsnorm_kernel(float *__restrict__ x, const float *__restrict__ delta,
-                                                              const float *__restrict__ w, int n, float eps,
-                                                              float *__restrict__ out) {
-    __shared__ float red[DEC_THREADS / 64];
+template <typename Put>
+__device__ __forceinline__ void rmsnorm_row(float *__restrict__ x, const float *__restrict__ delta,
+                                            const float *__restrict__ w, int n, float eps, float *red, Put put) {
     float4 *xr = (float4 *)(x + (int64_t)blockIdx.x * n);
     const float4 *dr = delta ? (const float4 *)(delta + (int64_t)blockIdx.x * n) : nullptr;
-    float4 *orow = (float4 *)(out + (int64_t)blockIdx.x * n);
     const float4 *w4 = (const float4 *)w;
     const int n4 = n / 4;
     float4 v[RMS_V], d[RMS_V];
@@ -110,9 +111,61 @@ __global__ __launch_bounds__(DEC_THREADS) void rmsnorm_kernel(float *__restrict_
         const int i = threadIdx.x + j * DEC_THREADS;
         if (i < n4) {
             const float4 ww = w4[i];
-            orow[i] = make_float4((v[j].x / m) * ww.x, (v[j].y / m) * ww.y, (v[j].z / m) * ww.z, (v[j].w / m) * ww.w);
+            put(i, make_float4((v[j].x / m) * ww.x, (v[j].y / m) * ww.y, (v[j].z / m) * ww.z, (v[j].w / m) * ww.w));
         }
     }
+}
+
+__global__ __launch_bounds__(DEC_THREADS) void rmsnorm_kernel(float *__restrict__ x, const float *__restrict__ delta,
+                                                              const float *__restrict__ w, int n, float eps,
+                                                              float *__restrict__ out) {
+    __shared__ float red[DEC_THREADS / 64];
+    float4 *orow = (float4 *)(out + (int64_t)blockIdx.x * n);
+    rmsnorm_row(x, delta, w, n, eps, red, [&](int i, float4 h) { orow[i] = h; });
+}
+
+// Q8_K quantisation of the row of n (a multiple of 256) values in LDS into
+// row `row` of the planes a: the quantizer kernel's per-block code and stores
+// (16 lanes per block, q8k_block_row16), the workgroup's 16 lane rows taking
+// blocks b, b + 16, ...
+__device__ __forceinline__ void quantize_row_from_lds(const float *hs, int n, int64_t row, const ActPlanes &a) {
+    const int s = threadIdx.x & 15, grp = threadIdx.x >> 4;
+    const int nb = n / QK_K;
+    for (int b0 = 0; b0 < nb; b0 += DEC_THREADS / 16) {  // uniform trip count
+        const int b = b0 + grp;
+        const bool ok = b < nb;  // uniform over the 16-lane row
+        float v[16];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float4 t = ok ? *(const float4 *)(hs + b * QK_K + 16 * s + 4 * i) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            v[4 * i] = t.x;
+            v[4 * i + 1] = t.y;
+            v[4 * i + 2] = t.z;
+            v[4 * i + 3] = t.w;
+        }
+        int bsum;
+        float d;
+        const uint4 packed = q8k_block_row16(v, s, &bsum, &d);
+        if (ok) store_q8k_block16(a, row, n, b, s, packed, bsum, d);
+    }
+}
+
+// rmsnorm_kernel's output quantised to Q8_K in the same launch (the prompt's
+// norm before a prefill GEMM): the normed row goes to LDS (and to out when it
+// is given), then the quantizer's per-block code writes the planes.
+__global__ __launch_bounds__(DEC_THREADS) void rmsnorm_act_kernel(float *__restrict__ x,
+                                                                  const float *__restrict__ delta,
+                                                                  const float *__restrict__ w, int n, float eps,
+                                                                  float *__restrict__ out, ActPlanes a) {
+    __shared__ float red[DEC_THREADS / 64];
+    __shared__ __align__(16) float hs[4 * RMS_V * DEC_THREADS];
+    float4 *orow = out ? (float4 *)(out + (int64_t)blockIdx.x * n) : nullptr;
+    rmsnorm_row(x, delta, w, n, eps, red, [&](int i, float4 h) {
+        ((float4 *)hs)[i] = h;
+        if (orow) orow[i] = h;
+    });
+    __syncthreads();
+    quantize_row_from_lds(hs, n, blockIdx.x, a);
 }
 
 // out[r][i] = silu(g[r][i]) * u[r][i] for rows r (grid y) of n; row r of g
@@ -138,6 +191,45 @@ __global__ __launch_bounds__(DEC_THREADS) void swiglu_pairs_kernel(const float *
     const int64_t j = r * ld + 8 * (i >> 2) + (i & 3);
     const float gv = y[j];
     out[r * n + i] = (gv / (1.0f + expf(-gv))) * y[j + 4];
+}
+
+// swiglu_pairs_kernel's values quantised to Q8_K in the same launch: grid
+// (ceil(n / 4096), m) workgroups; each 16-lane row of a workgroup forms the
+// 256 values of one block (lane s: values 16s..16s+15, by the same
+// expression as swiglu_pairs_kernel, from two float4 loads per four values:
+// gate and up sit four apart) and quantises them with the quantizer's
+// per-block code.  y 16-byte aligned, ld a multiple of 4 (checked by the
+// launcher).
+__global__ __launch_bounds__(DEC_THREADS) void swiglu_pairs_act_kernel(const float *__restrict__ y, int64_t ld, int n,
+                                                                       float *__restrict__ out, ActPlanes a) {
+    const int s = threadIdx.x & 15;
+    const int b = blockIdx.x * (DEC_THREADS / 16) + (threadIdx.x >> 4);
+    const int64_t r = blockIdx.y;
+    const bool ok = b < n / QK_K;  // uniform over the 16-lane row
+    float v[16];
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const int e0 = b * QK_K + 16 * s + 4 * q;  // values e0..e0+3: gate at y[8 (e0/4) + 0..3], up four on
+        float4 g = make_float4(0.0f, 0.0f, 0.0f, 0.0f), u = g;
+        if (ok) {
+            const float4 *src = (const float4 *)(y + r * ld + 2 * (int64_t)e0);
+            g = src[0];
+            u = src[1];
+        }
+        v[4 * q] = (g.x / (1.0f + expf(-g.x))) * u.x;
+        v[4 * q + 1] = (g.y / (1.0f + expf(-g.y))) * u.y;
+        v[4 * q + 2] = (g.z / (1.0f + expf(-g.z))) * u.z;
+        v[4 * q + 3] = (g.w / (1.0f + expf(-g.w))) * u.w;
+    }
+    if (ok && out) {
+        float4 *dst = (float4 *)(out + r * n + b * QK_K + 16 * s);
+#pragma unroll
+        for (int q = 0; q < 4; q++) dst[q] = make_float4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
+    }
+    int bsum;
+    float d;
+    const uint4 packed = q8k_block_row16(v, s, &bsum, &d);
+    if (ok) store_q8k_block16(a, r, n, b, s, packed, bsum, d);
 }
 
 // Sum over aligned groups of N lanes (N = 2, 4, 8, 16, 32 or 64), every lane
@@ -479,6 +571,25 @@ hipError_t launch_rmsnorm(float *x, const float *delta, const float *w, int64_t 
     if (!x || !w || !out || m <= 0 || n <= 0 || n % 4 || n > 4 * RMS_V * DEC_THREADS || m > 0x7fffffff)
         return hipErrorInvalidValue;
     rmsnorm_kernel<<<(unsigned)m, DEC_THREADS, 0, s>>>(x, delta, w, (int)n, eps, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_rmsnorm_act(float *x, const float *delta, const float *w, int64_t m, int64_t n, float eps,
+                              float *out, const ActPlanes &a, hipStream_t s) {
+    if (!x || !w || !a.qs || !a.d || !a.bsums || !a.bsum16 || m <= 0 || n <= 0 || n % QK_K ||
+        n > 4 * RMS_V * DEC_THREADS || m > 0x7fffffff)
+        return hipErrorInvalidValue;
+    rmsnorm_act_kernel<<<(unsigned)m, DEC_THREADS, 0, s>>>(x, delta, w, (int)n, eps, out, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_swiglu_pairs_act(const float *y, int64_t ld, int64_t m, int64_t n, float *out, const ActPlanes &a,
+                                   hipStream_t s) {
+    if (!y || !a.qs || !a.d || !a.bsums || !a.bsum16 || n <= 0 || n % QK_K || n > 0x7fffffff / 2 || m <= 0 ||
+        m > 65535 || ld % 4 || (m > 1 && ld < 2 * n) || (((uintptr_t)y | (uintptr_t)out) & 15))
+        return hipErrorInvalidValue;
+    const dim3 grid((unsigned)((n / QK_K + DEC_THREADS / 16 - 1) / (DEC_THREADS / 16)), (unsigned)m);
+    swiglu_pairs_act_kernel<<<grid, DEC_THREADS, 0, s>>>(y, ld, (int)n, out, a);
     return hipGetLastError();
 }
 

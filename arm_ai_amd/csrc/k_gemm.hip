@@ -368,7 +368,11 @@ struct GemmPlan {
 
 // 64 x 128 tiles, two workgroups per CU; the K loop is split (halves,
 // quarters, ...) while there are fewer items than CUs, each split keeping at
-// least two super-blocks.
+// least two super-blocks -- and, from half a CU's worth of items up, at least
+// eight: a split of fewer costs more in its reduce launch than the idle CUs
+// it fills (512 x 2304 x 2048: 23.4 us in two splits of four super-blocks
+// with the reduce, 15.8 us unsplit; 512 x 2048 x 5632: 28.4 us in two
+// splits of eleven, 34.9 us unsplit).
 GemmPlan gemm_plan(int64_t m, int64_t n, int64_t k) {
     GemmPlan g;
     const int ng = (int)(k / QK_K);
@@ -376,7 +380,9 @@ GemmPlan gemm_plan(int64_t m, int64_t n, int64_t k) {
     g.ntm = (int)((m + GBM - 1) / GBM);
     g.tiles = g.ntm * g.ntn;
     g.splits = 1;
-    while ((int64_t)g.tiles * g.splits < TARGET_WG && ng / (2 * g.splits) >= 2) g.splits *= 2;
+    while ((int64_t)g.tiles * g.splits < TARGET_WG && ng / (2 * g.splits) >= 2 &&
+           ((int64_t)g.tiles * g.splits < TARGET_WG / 2 || ng / (2 * g.splits) >= 8))
+        g.splits *= 2;
     g.kbs = (ng + g.splits - 1) / g.splits;
     g.splits = (ng + g.kbs - 1) / g.kbs;
     g.ws = g.splits > 1 ? (size_t)g.tiles * g.splits * GBM * GBN * 4 : 0;
@@ -409,10 +415,6 @@ size_t gemm_workspace_bytes(int type, int64_t m, int64_t n, int64_t k) {
     size_t ws = g.ws;
     if (m % mc) ws = std::max(ws, gemm_plan(m % mc, n, k).ws);  // the last, shorter launch
     return ws;
-}
-
-uint16_t *gemm_q16_plane(int type, int64_t m, int64_t n, int64_t k, void *ws) {
-    return type == TYPE_Q6_K || type == TYPE_Q5_K ? gemm6_q16_plane(m, n, k, ws) : nullptr;
 }
 
 hipError_t launch_gemm(const WLayout &w, int64_t n, int64_t k, const ActPlanes &x, int64_t m, float *y, int32_t *S,

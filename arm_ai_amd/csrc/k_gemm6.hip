@@ -470,11 +470,6 @@ size_t gemm6_workspace_bytes(int64_t m, int64_t n, int64_t k) {
     return ws;
 }
 
-uint16_t *gemm6_q16_plane(int64_t m, int64_t n, int64_t k, void *ws) {
-    if (!ws || m <= 0 || n <= 0 || k <= 0 || k % QK_K || m > gemm6_chunk_rows(k)) return nullptr;  // one launch only
-    return (uint16_t *)((uint8_t *)ws + align_up(gemm6_plan(m, n, k).part, 256));
-}
-
 hipError_t launch_gemm6(const WLayout &w, int64_t n, int64_t k, const ActPlanes &x, int64_t m, float *y, int32_t *S,
                         int32_t *Smin, void *ws, size_t ws_bytes, hipStream_t s) {
     if (w.type != TYPE_Q6_K && w.type != TYPE_Q5_K) return hipErrorNotSupported;
@@ -492,9 +487,11 @@ hipError_t launch_gemm6(const WLayout &w, int64_t n, int64_t k, const ActPlanes 
         const Gemm6Plan g = gemm6_plan(mm, n, k);
         if (g.tiles > GEMM_MAX_TILES) return hipErrorNotSupported;
         if (!ws || ws_bytes < g.ws) return hipErrorInvalidValue;
-        uint16_t *x16 = (uint16_t *)((uint8_t *)ws + align_up(g.part, 256));
+        // the quants as f16: the activation's own plane when its quantizer
+        // wrote one, else converted into the workspace here
+        uint16_t *x16 = x.q16 ? x.q16 + r0 * k : (uint16_t *)((uint8_t *)ws + align_up(g.part, 256));
         hipError_t e;
-        if (!(r0 == 0 && mm == m && x.q16 == x16)) {  // not already written there by the quantizer
+        if (!x.q16) {
             const int64_t n4 = mm * k / 4;
             qs_to_f16_kernel<<<(unsigned)((n4 + 255) / 256), 256, 0, s>>>(x.qs + r0 * k, n4, x16);
             if ((e = hipGetLastError()) != hipSuccess) return e;

@@ -44,22 +44,7 @@ __global__ __launch_bounds__(256) void quantize_q8k_kernel(const float *__restri
     float d;
     const uint4 packed = q8k_block_row16(v, s, &bsum, &d);
     if (!ok) return;  // after the row's DPP exchanges
-    *(uint4 *)(a.qs + e0) = packed;
-    if (a.q16) {  // uniform: the f16 copy for the f16-MFMA GEMMs
-        const uint32_t w[4] = {packed.x, packed.y, packed.z, packed.w};
-        uint32_t o[8];
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const uint32_t lo = __builtin_bit_cast(uint16_t, (_Float16)(int)(int8_t)((w[j >> 1] >> (16 * (j & 1))) & 0xffu));
-            const uint32_t hi = __builtin_bit_cast(uint16_t, (_Float16)(int)(int8_t)((w[j >> 1] >> (16 * (j & 1) + 8)) & 0xffu));
-            o[j] = lo | (hi << 16);
-        }
-        *(uint4 *)(a.q16 + e0) = make_uint4(o[0], o[1], o[2], o[3]);
-        *(uint4 *)(a.q16 + e0 + 8) = make_uint4(o[4], o[5], o[6], o[7]);
-    }
-    a.bsums[row * (k / 16) + sb * 16 + s] = (int16_t)bsum;
-    a.bsum16[row * (k / 16) + sb * 16 + s] = __builtin_bit_cast(uint16_t, (_Float16)(float)bsum);
-    if (s == 0) a.d[row * nb + sb] = d;
+    store_q8k_block16(a, row, k, sb, s, packed, bsum, d);
 }
 
 // Eight lanes per 32-element block, 32 blocks per workgroup.

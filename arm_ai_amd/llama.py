@@ -261,6 +261,15 @@ class Llama:
             self.v_cache = torch.zeros((cfg.n_layer, cfg.n_kv_head, cfg.max_seq, hd), **f32)
         self.ctx.synchronize()
         self._n_second = {"wqk": cfg.n_kv_head * cfg.head_dim, "w13": cfg.ffn}
+        # The prompt quantises each norm / SwiGLU output once, in the launch
+        # that forms it (aq_llama_rmsnorm_act, aq_llama_swiglu_pairs_act), and
+        # feeds the planes to every GEMM that reads it: when every layer's
+        # projections after the norms take Q8_K activations, w1|w3 is paired
+        # and the widths are whole Q8_K blocks.
+        q8k = lambda w: w.act_type == GgmlDType.Q8K
+        self._prompt_act = cfg.hidden % 256 == 0 and cfg.ffn % 256 == 0 and cfg.hidden <= 8192 and \
+            cfg.ffn <= 16384 and all(
+                "w13p" in lw and all(q8k(w) for name, w in lw.items() if name != "wo") for lw in self.layers)
         self._graph = None
         self._trace = None  # (rows, full layers, records) while trace_matmuls is active
         self._trace_layer = -1
@@ -298,6 +307,14 @@ class Llama:
             out[name] = QMatMul.from_qtensor(layer[name], self.ctx)
         return out
 
+    def _pair_act(self, lw, act, m, x):
+        """q and k from the quantised norm output: one GEMM on wq|wk, or two."""
+        if "wqk" in lw:
+            y = self._mm_act(lw["wqk"], act, m, x)
+            na = y.shape[1] - self._n_second["wqk"]
+            return y[:, :na], y[:, na:]
+        return self._mm_act(lw["wq"], act, m, x), self._mm_act(lw["wk"], act, m, x)
+
     def _pair(self, lw, merged, a, b, x):
         """Outputs of projections a and b of x: one launch on the merged weight, or two."""
         if merged in lw:
@@ -331,6 +348,22 @@ class Llama:
         x = x.contiguous()
         y = torch.empty((x.shape[0], w.n), dtype=torch.float32, device=self.dev)
         w.forward_device(x.data_ptr(), x.shape[0], y.data_ptr())
+        self._record_mm(w, x, y)
+        return y
+
+    def _mm_act(self, w: QMatMul, act, m: int, x=None):
+        """QMatMul::forward on activation planes already quantised (act, from
+        aq_llama_rmsnorm_act / aq_llama_swiglu_pairs_act); x, the f32 values
+        they were quantised from, only for trace_matmuls."""
+        from . import _lib
+
+        y = self.torch.empty((m, w.n), dtype=self.torch.float32, device=self.dev)
+        _lib.check(_lib.load().aq_qmatmul_preq_device(self.ctx.handle, w.handle, act.data_ptr(), m, w.k,
+                                                      y.data_ptr()))
+        self._record_mm(w, x, y)
+        return y
+
+    def _record_mm(self, w, x, y):
         if self._trace is not None:
             rows, full, records = self._trace
             if self._trace_layer in full:
@@ -338,7 +371,6 @@ class Llama:
             else:
                 sel = [r for r in rows if r < x.shape[0]] or [0]
             records.append((self._trace_layer, w, x[sel].cpu().numpy(), y[sel].cpu().numpy(), sel))
-        return y
 
     @contextlib.contextmanager
     def capture_hidden(self, layers):
@@ -408,9 +440,32 @@ class Llama:
             a = torch.empty((n, cfg.ffn), **f32)     # silu(g) * u
             chk(L.aq_llama_embed_rows(c, ptr(self.tok_embeddings), cfg.vocab, ptr(tokens), n, cfg.hidden, ptr(x)))
             delta = None
+            fused = self._prompt_act and n > 8  # GEMM-sized prompts (fewer rows: fused-quantisation matvecs)
+            if fused:  # the quantised norm / SwiGLU outputs (their f32 values only while tracing)
+                u8 = dict(dtype=torch.uint8, device=self.dev)
+                act_h = torch.empty(int(L.aq_act_bytes(int(GgmlDType.Q8K), n, cfg.hidden)), **u8)
+                act_a = torch.empty(int(L.aq_act_bytes(int(GgmlDType.Q8K), n, cfg.ffn)), **u8)
+                keep = self._trace is not None
             for li, lw in enumerate(self.layers):
                 self._trace_layer = li
                 self._record_hidden(li, x, delta)
+                if fused:
+                    chk(L.aq_llama_rmsnorm_act(c, ptr(x), ptr(delta) if delta is not None else None,
+                                               ptr(self.attn_norm[li]), n, cfg.hidden, eps, ptr(h) if keep else None,
+                                               ptr(act_h)))
+                    q, k = self._pair_act(lw, act_h, n, h)
+                    v = self._mm_act(lw["wv"], act_h, n, h)
+                    chk(L.aq_llama_attn_prefill(c, ptr(q), q.stride(0), ptr(k), k.stride(0), ptr(v), v.stride(0),
+                                                ptr(self.cos), ptr(self.sin), index_pos, n, ptr(self.k_cache[li]),
+                                                ptr(self.v_cache[li]), H, Hkv, D, cfg.max_seq, ptr(y)))
+                    o = self._mm(lw["wo"], y)
+                    chk(L.aq_llama_rmsnorm_act(c, ptr(x), ptr(o), ptr(self.ffn_norm[li]), n, cfg.hidden, eps,
+                                               ptr(h) if keep else None, ptr(act_h)))
+                    gu = self._mm_act(lw["w13p"], act_h, n, h)
+                    chk(L.aq_llama_swiglu_pairs_act(c, ptr(gu), gu.stride(0), n, cfg.ffn, ptr(a) if keep else None,
+                                                    ptr(act_a)))
+                    delta = self._mm_act(lw["w2"], act_a, n, a)
+                    continue
                 chk(L.aq_llama_rmsnorm(c, ptr(x), ptr(delta) if delta is not None else None, ptr(self.attn_norm[li]),
                                        n, cfg.hidden, eps, ptr(h)))
                 q, k = self._pair(lw, "wqk", "wq", "wk", h)

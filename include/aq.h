@@ -334,6 +334,23 @@ int aq_qmatmul2_rmsnorm_f32_device(aq_ctx *ctx, const aq_qweight *w1, const aq_q
  *   kernel; other shapes run those two steps, the matmul output in the
  *   context's scratch). */
 int aq_llama_swiglu_pairs(aq_ctx *ctx, const float *d_y, int64_t ld, int64_t m, int64_t ffn, float *d_out);
+/* The prompt's norm (aq_llama_rmsnorm) and SwiGLU pairs
+ * (aq_llama_swiglu_pairs) with the result quantised to Q8_K in the same
+ * launch, into the activation planes at d_act (aq_act_bytes(AQ_TYPE_Q8_K, m,
+ * n or ffn) bytes, 256-byte aligned; the planes include the f16 copy of the
+ * quants that the Q6_K / Q5_K GEMMs read) for aq_qmatmul_preq_device.  The
+ * values are those of the unfused call followed by aq_quantize_act_device,
+ * bit for bit; d_out, when non-null, receives the f32 values as well.  n is
+ * a multiple of 256 up to 8192, ffn a multiple of 256 with m <= 65535 and ld
+ * a multiple of 4; x, delta, w, y and out 16-byte aligned.  No counterpart
+ * in the reference, whose prompt runs candle's rms_norm and silu ops and
+ * then QMatMul::forward (which quantises its input again,
+ * llama_candle.rs:93); these fold the quantisation into the op before the
+ * GEMM. */
+int aq_llama_rmsnorm_act(aq_ctx *ctx, float *d_x, const float *d_delta, const float *d_w, int64_t m, int64_t n,
+                         float eps, float *d_out, void *d_act);
+int aq_llama_swiglu_pairs_act(aq_ctx *ctx, const float *d_y, int64_t ld, int64_t m, int64_t ffn, float *d_out,
+                              void *d_act);
 /* 1 when aq_qmatmul_rmsnorm_swiglu_f32_device forms silu(g) * u inside the
  * matmul launch for a paired weight of this type (AQ_TYPE_*) and shape (n
  * rows, k columns), else 0 (it would run the matmul and the pairs as two

@@ -129,6 +129,10 @@ pub fn aq_abi_version() -> c_int;
         d_dst1: *mut f32, d_dst2: *mut f32) -> c_int;
     pub fn aq_llama_swiglu_pairs(ctx: *mut AqCtx, d_y: *const f32, ld: i64, m: i64, ffn: i64, d_out: *mut f32)
         -> c_int;
+    pub fn aq_llama_rmsnorm_act(ctx: *mut AqCtx, d_x: *mut f32, d_delta: *const f32, d_w: *const f32, m: i64,
+        n: i64, eps: f32, d_out: *mut f32, d_act: *mut c_void) -> c_int;
+    pub fn aq_llama_swiglu_pairs_act(ctx: *mut AqCtx, d_y: *const f32, ld: i64, m: i64, ffn: i64, d_out: *mut f32,
+        d_act: *mut c_void) -> c_int;
     pub fn aq_swiglu_fused(wtype: c_int, n: i64, k: i64) -> c_int;
     pub fn aq_llama_head_argmax_embed(ctx: *mut AqCtx, w: *const AqQWeight, d_x: *const f32, d_delta: *const f32,
         d_norm_w: *const f32, eps: f32, k: i64, d_logits: *mut f32, d_tok: *mut i64, d_pos: *mut i64,

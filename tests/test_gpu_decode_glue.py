@@ -545,3 +545,123 @@ def test_matvec2_fused_rmsnorm_equals_two_calls(env, t1, n1, t2, n2, k):
                                             k, None, outs[0].data_ptr(), outs[1].data_ptr()) == lib.AQ_ERR_SHAPE
     for mm in (m1, m2, m3):
         mm.free()
+
+
+# ---------------------------------------------------------------- prompt glue quantised in the same launch
+def _act(torch, lib, m, k):
+    L = lib.load()
+    return torch.zeros(int(L.aq_act_bytes(15, m, k)), dtype=torch.uint8, device="cuda:0")  # AQ_TYPE_Q8_K
+
+
+def _planes(buf):
+    """The activation buffer's bytes (all of its planes)."""
+    return buf.cpu().numpy()
+
+
+@pytest.mark.parametrize("m,n,with_delta", [(1, 256, False), (3, 2048, True), (512, 2048, True), (5, 4096, False),
+                                            (2, 8192, True)])
+def test_rmsnorm_act_equals_rmsnorm_then_quantize(env, m, n, with_delta):
+    """aq_llama_rmsnorm_act: the residual add, the normed values and every
+    quantised plane (qs, d, bsums, their f16 forms, the f16 quants) bit for bit
+    as aq_llama_rmsnorm followed by aq_quantize_act_device."""
+    torch, lib, ctx = env
+    L = lib.load()
+    rng = np.random.default_rng(m + n)
+    x = (2 * rng.standard_normal((m, n))).astype(np.float32)
+    d = rng.standard_normal((m, n)).astype(np.float32)
+    w = (1 + 0.1 * rng.standard_normal(n)).astype(np.float32)
+    x[0, 5] = 0.0
+    dx1, dx2, dd, dw = _dev(torch, x), _dev(torch, x), _dev(torch, d), _dev(torch, w)
+    h1 = torch.empty((m, n), dtype=torch.float32, device="cuda:0")
+    h2 = torch.empty((m, n), dtype=torch.float32, device="cuda:0")
+    a1, a2 = _act(torch, lib, m, n), _act(torch, lib, m, n)
+    torch.cuda.synchronize()
+    delta = dd.data_ptr() if with_delta else None
+    eps = ctypes.c_float(1e-5)
+    lib.check(L.aq_llama_rmsnorm(ctx.handle, dx1.data_ptr(), delta, dw.data_ptr(), m, n, eps, h1.data_ptr()))
+    lib.check(L.aq_quantize_act_device(ctx.handle, 15, h1.data_ptr(), m, n, a1.data_ptr()))
+    lib.check(L.aq_llama_rmsnorm_act(ctx.handle, dx2.data_ptr(), delta, dw.data_ptr(), m, n, eps, h2.data_ptr(),
+                                     a2.data_ptr()))
+    ctx.synchronize()
+    assert np.array_equal(dx1.cpu().numpy(), dx2.cpu().numpy())
+    assert np.array_equal(h1.cpu().numpy(), h2.cpu().numpy())
+    assert np.array_equal(_planes(a1), _planes(a2))
+    # without the f32 copy: the same planes
+    a3 = _act(torch, lib, m, n)
+    dx3 = _dev(torch, x)
+    torch.cuda.synchronize()
+    lib.check(L.aq_llama_rmsnorm_act(ctx.handle, dx3.data_ptr(), delta, dw.data_ptr(), m, n, eps, None,
+                                     a3.data_ptr()))
+    ctx.synchronize()
+    assert np.array_equal(_planes(a1), _planes(a3))
+
+
+@pytest.mark.parametrize("m,ffn,pad", [(1, 256, 0), (7, 5632, 0), (64, 5632, 8), (3, 14336, 0)])
+def test_swiglu_pairs_act_equals_swiglu_pairs_then_quantize(env, m, ffn, pad):
+    torch, lib, ctx = env
+    L = lib.load()
+    rng = np.random.default_rng(ffn + m)
+    ld = 2 * ffn + pad
+    y = (3 * rng.standard_normal((m, ld))).astype(np.float32)
+    y[0, 0], y[0, 1] = -100.0, 100.0  # exp overflow / underflow ends of silu
+    dy = _dev(torch, y)
+    o1 = torch.empty((m, ffn), dtype=torch.float32, device="cuda:0")
+    o2 = torch.empty((m, ffn), dtype=torch.float32, device="cuda:0")
+    a1, a2 = _act(torch, lib, m, ffn), _act(torch, lib, m, ffn)
+    torch.cuda.synchronize()
+    lib.check(L.aq_llama_swiglu_pairs(ctx.handle, dy.data_ptr(), ld, m, ffn, o1.data_ptr()))
+    lib.check(L.aq_quantize_act_device(ctx.handle, 15, o1.data_ptr(), m, ffn, a1.data_ptr()))
+    lib.check(L.aq_llama_swiglu_pairs_act(ctx.handle, dy.data_ptr(), ld, m, ffn, o2.data_ptr(), a2.data_ptr()))
+    ctx.synchronize()
+    assert np.array_equal(o1.cpu().numpy(), o2.cpu().numpy())
+    assert np.array_equal(_planes(a1), _planes(a2))
+
+
+@pytest.mark.parametrize("wtype,n,k,m", [(14, 256, 2048, 512), (14, 2048, 5632, 64), (13, 512, 2048, 33),
+                                         (12, 2304, 2048, 96)])
+def test_prequantised_gemm_reads_the_planes_f16_quants(env, wtype, n, k, m):
+    """aq_qmatmul_preq_device on planes from the fused prompt glue: the f16
+    MFMA GEMMs (Q6_K, Q5_K) read the activation's own f16 quants; the result
+    equals the f32-input call, which quantises first."""
+    import arm_ai_amd as A
+    from arm_ai_amd import synth as S
+
+    torch, lib, ctx = env
+    L = lib.load()
+    W = S.make_weight(wtype, n, k, seed=n + k)
+    mm = A.QMatMul.from_qtensor(A.QTensor(wtype, (n, k), W.blocks), ctx)
+    rng = np.random.default_rng(m)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    wn = np.ones(k, np.float32)
+    dx, dwn = _dev(torch, x), _dev(torch, wn)
+    h = torch.empty((m, k), dtype=torch.float32, device="cuda:0")
+    act = _act(torch, lib, m, k)
+    y1 = torch.empty((m, n), dtype=torch.float32, device="cuda:0")
+    y2 = torch.empty((m, n), dtype=torch.float32, device="cuda:0")
+    torch.cuda.synchronize()
+    lib.check(L.aq_llama_rmsnorm_act(ctx.handle, dx.data_ptr(), None, dwn.data_ptr(), m, k, ctypes.c_float(1e-5),
+                                     h.data_ptr(), act.data_ptr()))
+    lib.check(L.aq_qmatmul_preq_device(ctx.handle, mm.handle, act.data_ptr(), m, k, y1.data_ptr()))
+    lib.check(L.aq_qmatmul_f32_device(ctx.handle, mm.handle, h.data_ptr(), m, k, y2.data_ptr()))
+    ctx.synchronize()
+    assert np.array_equal(y1.cpu().numpy(), y2.cpu().numpy())
+    mm.free()
+
+
+def test_prompt_glue_act_errors(env):
+    torch, lib, ctx = env
+    L = lib.load()
+    buf = torch.zeros(1 << 20, dtype=torch.uint8, device="cuda:0")
+    f = torch.zeros(4096, dtype=torch.float32, device="cuda:0")
+    p, a = f.data_ptr(), buf.data_ptr()
+    eps = ctypes.c_float(1e-5)
+    assert L.aq_llama_rmsnorm_act(ctx.handle, p, None, p, 2, 576, eps, None, a) == lib.AQ_ERR_SHAPE  # not whole blocks
+    assert L.aq_llama_rmsnorm_act(ctx.handle, p, None, p, 2, 256, eps, None, a + 16) == lib.AQ_ERR_INVALID_ARG
+    assert L.aq_llama_rmsnorm_act(ctx.handle, p, None, p, 2, 256, eps, None, None) == lib.AQ_ERR_INVALID_ARG
+    assert L.aq_llama_rmsnorm_act(ctx.handle, p, None, p, 1, 16384, eps, None, a) == lib.AQ_ERR_SHAPE  # over 8192
+    assert L.aq_llama_swiglu_pairs_act(ctx.handle, p, 1280, 2, 640, None, a) == lib.AQ_ERR_SHAPE  # not whole blocks
+    assert L.aq_llama_swiglu_pairs_act(ctx.handle, p, 256, 2, 256, None, a) == lib.AQ_ERR_SHAPE  # ld < 2 * ffn
+    assert L.aq_llama_swiglu_pairs_act(ctx.handle, p, 514, 2, 256, None, a) == lib.AQ_ERR_INVALID_ARG  # ld % 4
+    assert L.aq_llama_swiglu_pairs_act(ctx.handle, p + 4, 512, 2, 256, None, a) == lib.AQ_ERR_INVALID_ARG  # y align
+    assert L.aq_llama_rmsnorm_act(ctx.handle, p, None, p, 0, 256, eps, None, a) == lib.AQ_OK
+    ctx.synchronize()
