@@ -12,6 +12,7 @@
 // Cargo.toml:33, which this library must not inherit).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
@@ -175,7 +176,10 @@ int ensure_pinned(aq_ctx *c, size_t bytes) {
     return AQ_OK;
 }
 
-// Scratch layout for one matmul call: [activation planes | x f32 | y f32 | S | Smin | gemm workspace]
+bool use_mmv(const aq_qweight *w, int64_t m);
+
+// Scratch layout for one matmul call: [activation planes | x f32 | y f32 | S | Smin | gemm or
+// batched-matvec workspace]
 struct CallLayout {
     size_t act, x, y, s, smin, ws, total;
 };
@@ -194,7 +198,10 @@ CallLayout call_layout(const aq_qweight *w, int64_t m, bool host_io, bool dump, 
     L.smin = off;
     if (dump) off += align_up((size_t)m * w->n * nblk * 4, 256);
     L.ws = off;
-    if (gemm) off += align_up(gemm_workspace_bytes(w->glayout.type, m, w->n, w->k), 256);
+    // (a GEMM that declines the shape falls back to the batched matvec: room for either)
+    size_t ws = gemm ? gemm_workspace_bytes(w->glayout.type, m, w->n, w->k) : 0;
+    if (use_mmv(w, m)) ws = std::max(ws, mmv_workspace_bytes(w->layout.type, w->n, w->k));
+    off += align_up(ws, 256);
     L.total = off;
     return L;
 }
@@ -240,7 +247,7 @@ int run_matmul(aq_ctx *ctx, const aq_qweight *w, const float *d_x, int64_t m, fl
         a.q16 = nullptr;
         e = launch_quantize_q8k(d_x, m, w->k, a, ctx->stream);
         if (e != hipSuccess) return fail(AQ_ERR_HIP, "activation quantizer: %s", hipGetErrorString(e));
-        e = launch_mmv(w->layout, w->n, w->k, a, m, d_y, dS, dSmin, ctx->stream);
+        e = launch_mmv(w->layout, w->n, w->k, a, m, d_y, dS, dSmin, ws, ws_bytes, ctx->stream);
         if (e == hipErrorNotSupported) e = launch_matvec(w->layout, w->n, w->k, nullptr, &a, m, d_y, dS, dSmin, ctx->stream);
     } else if (((uintptr_t)d_x & 15) == 0) {
         e = launch_matvec(w->layout, w->n, w->k, d_x, nullptr, m, d_y, dS, dSmin, ctx->stream);
@@ -559,15 +566,17 @@ int aq_qmatmul_preq_device(aq_ctx *ctx, const aq_qweight *w, const void *d_act, 
     if ((rc = use_device(ctx->device))) return rc;
     ActPlanes a = act_planes((void *)d_act, m, k);
     hipError_t e = hipErrorNotSupported;
-    if (use_gemm(w, m)) {
-        CallLayout L = call_layout(w, m, false, false, true);
-        if ((rc = ensure_scratch(ctx, L.total))) return rc;
+    const bool gemm = use_gemm(w, m);
+    CallLayout L = call_layout(w, m, false, false, gemm);
+    if ((gemm || use_mmv(w, m)) && (rc = ensure_scratch(ctx, L.total))) return rc;
+    if (gemm) {
         e = launch_gemm(w->glayout, w->n, w->k, a, m, d_dst, nullptr, nullptr, (uint8_t *)ctx->scratch + L.ws,
                         L.total - L.ws, ctx->stream);
         if (e != hipSuccess && e != hipErrorNotSupported) return fail(AQ_ERR_HIP, "gemm: %s", hipGetErrorString(e));
     }
     if (e == hipErrorNotSupported && use_mmv(w, m))
-        e = launch_mmv(w->layout, w->n, w->k, a, m, d_dst, nullptr, nullptr, ctx->stream);
+        e = launch_mmv(w->layout, w->n, w->k, a, m, d_dst, nullptr, nullptr, (uint8_t *)ctx->scratch + L.ws,
+                       L.total - L.ws, ctx->stream);
     if (e == hipErrorNotSupported) e = launch_matvec(w->layout, w->n, w->k, nullptr, &a, m, d_dst, nullptr, nullptr, ctx->stream);
     if (e == hipErrorNotSupported) return fail(AQ_ERR_SHAPE, "k=%lld is larger than the matvec supports", (long long)w->k);
     if (e != hipSuccess) return fail(AQ_ERR_HIP, "matvec: %s", hipGetErrorString(e));

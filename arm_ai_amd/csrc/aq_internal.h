@@ -186,10 +186,13 @@ hipError_t launch_rowlane_matvec2(const WLayout &w1, int64_t n1, float *y1, cons
                                   int64_t k, const float *x, const RlXf &xf, hipStream_t s);
 // Matvec of pre-quantised (Q8_K) rows on the int8 matrix cores, 8 rows per
 // launch, Q4_K / Q6_K weights, k <= mmv_max_k().  Returns hipErrorNotSupported
-// for other types and shapes (the caller then uses launch_matvec).
+// for other types and shapes (the caller then uses launch_matvec).  Shapes
+// whose K is split over workgroups sum the parts in ws
+// (mmv_workspace_bytes(type, n, k) bytes, 0 when there is no split).
 int mmv_max_k();
+size_t mmv_workspace_bytes(int type, int64_t n, int64_t k);
 hipError_t launch_mmv(const WLayout &w, int64_t n, int64_t k, const ActPlanes &act, int64_t m, float *y, int32_t *S,
-                      int32_t *Smin, hipStream_t s);
+                      int32_t *Smin, void *ws, size_t ws_bytes, hipStream_t s);
 // Prefill GEMM on MFMA (m > 8).  Returns hipErrorNotSupported for shapes it
 // does not take; the caller then uses launch_matvec.  ws: gemm_workspace_bytes
 // of scratch (split-K partials, summed by a second launch on the stream).

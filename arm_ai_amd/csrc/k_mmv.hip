@@ -45,6 +45,10 @@
 // kch-th one); the wavefronts of a tile's chunks are in one workgroup and add
 // their partials in chunk order through LDS (deterministic).  Workgroups stay resident and
 // loop over the (tiles x chunks) iterations, so each fills its LDS once.
+// Q4_K rows of more than 8 quads (4 super-blocks each) are split into K
+// parts: a workgroup holds one part's activation and takes tiles of that
+// part only (the grid is a multiple of the part count), writes the part's
+// sums to a workspace, and mmv_reduce_kernel adds the parts in order.
 #include "aq_internal.h"
 
 #include <algorithm>
@@ -100,6 +104,8 @@ struct MmvParams {
     int64_t rb_stride;
     int n, k, ng, nrb, m;
     int tiles, kch, gpc, tpw, iters;  // an iteration: tpw tiles x kch chunks, one wavefront each
+    int ks, qpp;                      // Q4_K: K parts of qpp quads (iterations: tile groups x parts)
+    float *part;                      // ks > 1: the parts' sums [ks][m][n], added by mmv_reduce_kernel
     const int8_t *qs;                 // [m][k]
     const float *d;                   // [m][k/256]
     const uint16_t *bs16;             // [m][k/16] f16 bsums
@@ -142,25 +148,25 @@ __device__ __forceinline__ void load_w(WStage<TYPE> &W, const MmvParams &p, cons
     }
 }
 
-// The pass's activation into LDS, issued by every wavefront (copy q of a
-// region goes to LDS q * 1024 (256 for d); lane l takes row l%8 and piece
-// l/8 of the copy).  Rows past m read zeros; the copies past the last
-// super-block land in the regions' padding.  ZERO: also clear the zero
-// block.  Waited for by the caller (vmcnt for the copies, lgkmcnt for the
-// clearing).
+// The pass's activation into LDS, super-blocks g0 .. g0 + ngk - 1, issued
+// by every wavefront (copy q of a region goes to LDS q * 1024 (256 for d);
+// lane l takes row l%8 and piece l/8 of the copy; super-block g0 + i lands
+// at entry i).  Rows past m read zeros; the copies past the last super-block
+// land in the regions' padding.  ZERO: also clear the zero block.  Waited
+// for by the caller (vmcnt for the copies, lgkmcnt for the clearing).
 template <bool ZERO>
-__device__ __forceinline__ void fill_act(uint8_t *lds, const MmvParams &p, const ActLds &a, int wave, int nw,
-                                         int lane) {
+__device__ __forceinline__ void fill_act(uint8_t *lds, const MmvParams &p, const ActLds &a, int g0, int ngk, int wave,
+                                         int nw, int lane) {
     const int b = lane & 7, pc = lane >> 3;
     const rsrc_t rq = buf_rsrc(p.qs, (uint32_t)(p.m * p.k));
-    const uint32_t vq = (uint32_t)(b * p.k + 16 * pc);
-    for (int q = wave; q < 2 * p.ng; q += nw) buf_to_lds16(rq, lds + q * 1024, vq + 128 * q, 0);
+    const uint32_t vq = (uint32_t)(b * p.k + g0 * QK_K + 16 * pc);
+    for (int q = wave; q < 2 * ngk; q += nw) buf_to_lds16(rq, lds + q * 1024, vq + 128 * q, 0);
     const rsrc_t rbs = buf_rsrc(p.bs16, (uint32_t)(p.m * (p.k / 16) * 2));
-    const uint32_t vb = (uint32_t)(b * (p.k / 8) + 16 * pc);
-    for (int q = wave; q < (p.ng + 3) / 4; q += nw) buf_to_lds16(rbs, lds + a.bs + q * 1024, vb + 128 * q, 0);
+    const uint32_t vb = (uint32_t)(b * (p.k / 8) + g0 * 32 + 16 * pc);
+    for (int q = wave; q < (ngk + 3) / 4; q += nw) buf_to_lds16(rbs, lds + a.bs + q * 1024, vb + 128 * q, 0);
     const rsrc_t rd = buf_rsrc(p.d, (uint32_t)(p.m * p.ng * 4));
-    const uint32_t vd = (uint32_t)((b * p.ng + pc) * 4);
-    for (int q = wave; q < (p.ng + 7) / 8; q += nw) buf_to_lds4(rd, lds + a.d + q * 256, vd + 32 * q, 0);
+    const uint32_t vd = (uint32_t)((b * p.ng + g0 + pc) * 4);
+    for (int q = wave; q < (ngk + 7) / 8; q += nw) buf_to_lds4(rd, lds + a.d + q * 256, vd + 32 * q, 0);
     if (ZERO)
         for (int t = 64 * wave + lane; t < LZ / 16; t += 64 * nw) *(u32x4 *)(lds + a.zero + 16 * t) = u32x4{0u, 0u, 0u, 0u};
 }
@@ -264,7 +270,7 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void mmv_kernel(MmvParams p) {
 
     // the activation copies first, then the first weight stages: waiting for
     // the copies (vmcnt down to the weight loads) leaves the weights in flight
-    fill_act<false>(lds, p, al, wave, nw, L.lane);
+    fill_act<false>(lds, p, al, 0, p.ng, wave, nw, L.lane);
     __builtin_amdgcn_sched_barrier(0);
     begin(blockIdx.x);
     __builtin_amdgcn_sched_barrier(0);
@@ -368,23 +374,27 @@ __global__ __launch_bounds__(512) void mmv_q4k_kernel(MmvParams p) {
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int nw = p.tpw * p.kch;
     const int tw = wave / p.kch, chunk = wave - tw * p.kch;
-    const ActLds al = act_lds(p.ng, nw);
+    // K part kp of this workgroup (the grid is a multiple of ks, so every
+    // iteration of the workgroup is in the same part): quads q0 .. q0 + nqk - 1
+    const int kp = (int)blockIdx.x % p.ks;
+    const int q0 = kp * p.qpp, nq = (p.ng + 3) / 4;
+    const int nqk = min(p.qpp, nq - q0), g0 = 4 * q0;
+    const ActLds al = act_lds(4 * p.qpp, nw);
     float *red = (float *)(lds + al.red);  // [wave][b][tile row]
-    // chunk c takes quads (4 super-blocks) c, c + kch, ...
-    const int nq = (p.ng + 3) / 4;
-    const int nmine = chunk < nq ? (nq - chunk + p.kch - 1) / p.kch : 0;
+    // chunk c takes quads (4 super-blocks) q0 + c, q0 + c + kch, ...
+    const int nmine = chunk < nqk ? (nqk - chunk + p.kch - 1) / p.kch : 0;
 
     int tile = 0, cnt = 0;
     rsrc_t rw;
     u32x4 wa[9], wb[9];
     auto load = [&](u32x4 (&W)[9], int s) {
-        const int g = 4 * (chunk + s * p.kch) + j;
+        const int g = 4 * (q0 + chunk + s * p.kch) + j;
         const uint32_t off = g < p.ng ? (uint32_t)((n >> 3) * p.rb_stride + g * 9 * 128 + (n & 7) * 16) : BUF_OOB;
 #pragma unroll
         for (int i = 0; i < 9; i++) W[i] = __builtin_amdgcn_raw_buffer_load_b128(rw, off + i * 128, 0, BUF_NT);
     };
     auto begin = [&](int it) {  // set up iteration it and issue its first step's loads
-        tile = it * p.tpw + tw;
+        tile = it / p.ks * p.tpw + tw;
         cnt = it < p.iters && tile < p.tiles ? nmine : 0;  // wave-uniform
         const int rb0 = 2 * tile;
         const int nrb_t = cnt > 0 ? min(2, p.nrb - rb0) : 0;
@@ -394,27 +404,27 @@ __global__ __launch_bounds__(512) void mmv_q4k_kernel(MmvParams p) {
 
     // the activation copies first, then the first weight loads: waiting for
     // the copies (vmcnt down to the 9 weight loads) leaves the weights in flight
-    fill_act<true>(lds, p, al, wave, nw, lane);
+    fill_act<true>(lds, p, al, g0, 4 * nqk, wave, nw, lane);
     __builtin_amdgcn_sched_barrier(0);
     begin(blockIdx.x);
     __builtin_amdgcn_sched_barrier(0);
     wait_vmcnt<9>();
     lds_barrier();
 
-    const rsrc_t ry = buf_rsrc(p.y, (uint32_t)(p.m * p.n * 4));
+    const rsrc_t ry = buf_rsrc(p.ks > 1 ? p.part + (int64_t)kp * p.m * p.n : p.y, (uint32_t)(p.m * p.n * 4));
     const v4i z = {0, 0, 0, 0};
     const v4f zf = {0.0f, 0.0f, 0.0f, 0.0f};
     for (int it = blockIdx.x; it < p.iters; it += gridDim.x) {  // workgroup-uniform
         const int row = tile * TILE + n;
         float f[2][4] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};  // [batch half][r]: batch row 4h + r
         auto step = [&](const u32x4 (&W)[9], int s) {
-            const int g = 4 * (chunk + s * p.kch) + j;  // this lane group's super-block
+            const int g = 4 * (q0 + chunk + s * p.kch) + j;  // this lane group's super-block
             const bool g_ok = g < p.ng;
-            const int gg = g_ok ? g : 0;
+            const int gl = g_ok ? g - g0 : 0;  // its LDS entry
             // activation operand of lane (i = n, j): row 4h + n%4 of super-block g when j = n/4
             const bool act = g_ok && j == (n >> 2);
-            const int ab = act ? gg * LQ + (n & 3) * 16 : al.zero;  // + 64 for batch half 1 (zero block: stays zero)
-            const int bb = act ? al.bs + gg * LB + (n & 3) * 16 : al.zero;
+            const int ab = act ? gl * LQ + (n & 3) * 16 : al.zero;  // + 64 for batch half 1 (zero block: stays zero)
+            const int bb = act ? al.bs + gl * LB + (n & 3) * 16 : al.zero;
             const uint32_t u0 = W[0].y, u1 = W[0].z, u2 = W[0].w;
             // candle's utmp form of GGML get_scale_min_k4 (6-bit scales and mins)
             const uint32_t sc03 = u0 & 0x3F3F3F3Fu;
@@ -478,7 +488,7 @@ __global__ __launch_bounds__(512) void mmv_q4k_kernel(MmvParams p) {
                     const v8h bm = __builtin_shufflevector(bmh[u][0], bmh[u][1], 0, 1, 2, 3, 4, 5, 6, 7);
                     sm = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bm, sm, 0, 0, 0);
                 }
-                const v4f dx = *(const v4f *)(lds + al.d + gg * LD + 16 * h);
+                const v4f dx = *(const v4f *)(lds + al.d + gl * LD + 16 * h);
                 const float dxv[4] = {dx.x, dx.y, dx.z, dx.w}, smv[4] = {sm.x, sm.y, sm.z, sm.w};
 #pragma unroll
                 for (int r = 0; r < 4; r++) f[h][r] += (dw * dxv[r]) * (float)S[h][r] - (dmw * dxv[r]) * smv[r];
@@ -555,6 +565,16 @@ __global__ __launch_bounds__(512) void mmv_q4k_kernel(MmvParams p) {
     }
 }
 
+// y[i] = sum over the K parts of part[kp][i], in part order (one output per thread)
+__global__ __launch_bounds__(256) void mmv_reduce_kernel(const float *__restrict__ part, int ks, int mn,
+                                                         float *__restrict__ y) {
+    const int i = (int)blockIdx.x * 256 + (int)threadIdx.x;
+    if (i >= mn) return;
+    float t = part[i];
+    for (int kp = 1; kp < ks; kp++) t += part[(int64_t)kp * mn + i];
+    y[i] = t;
+}
+
 int cu_count() {
     static int cached[64];
     int dev = 0;
@@ -578,11 +598,17 @@ hipError_t allow_lds() {
     return err;
 }
 
+// ng_lds: the super-blocks of activation a workgroup holds in LDS (the
+// whole row, or a Q4_K K part)
 template <void (*F)(MmvParams)>
-hipError_t launch_f(MmvParams p, int64_t m, const ActPlanes &act, float *y, int32_t *S, int32_t *Smin, hipStream_t s) {
+hipError_t launch_f(MmvParams p, int ng_lds, int64_t m, const ActPlanes &act, float *y, int32_t *S, int32_t *Smin,
+                    void *ws, size_t ws_bytes, hipStream_t s) {
     const int nw = p.tpw * p.kch;
-    const size_t lds = (size_t)act_lds(p.ng, nw).bytes;
+    const size_t lds = (size_t)act_lds(ng_lds, nw).bytes;
     if (lds > LDS_CAP) return hipErrorNotSupported;
+    if (p.ks < 1 || p.iters % p.ks) return hipErrorInvalidValue;
+    if (p.ks > 1 && (!ws || ws_bytes < (size_t)p.ks * MAXB * p.n * 4)) return hipErrorInvalidValue;
+    p.part = p.ks > 1 ? (float *)ws : nullptr;
     hipError_t e = allow_lds<F>();
     if (e != hipSuccess) return e;
     int per_cu = 0;
@@ -590,7 +616,10 @@ hipError_t launch_f(MmvParams p, int64_t m, const ActPlanes &act, float *y, int3
     if (e != hipSuccess) return e;
     const int cus = cu_count();
     if (per_cu <= 0 || cus <= 0) return hipErrorNotSupported;
-    const unsigned grid = (unsigned)std::min((int64_t)p.iters, (int64_t)per_cu * cus);
+    // a multiple of ks workgroups, so that each stays in one K part
+    int64_t g = std::min((int64_t)p.iters, (int64_t)per_cu * cus);
+    g = std::max<int64_t>(p.ks, g / p.ks * p.ks);
+    const unsigned grid = (unsigned)g;
     // passes of up to MAXB rows; every plane is row-major, so a pass is an offset
     for (int64_t r0 = 0; r0 < m; r0 += MAXB) {
         p.m = (int)(m - r0 < MAXB ? m - r0 : MAXB);
@@ -603,27 +632,66 @@ hipError_t launch_f(MmvParams p, int64_t m, const ActPlanes &act, float *y, int3
         F<<<grid, dim3(nw * 64), lds, s>>>(p);
         e = hipGetLastError();
         if (e != hipSuccess) return e;
+        if (p.ks > 1) {
+            const int mn = p.m * p.n;
+            mmv_reduce_kernel<<<(unsigned)((mn + 255) / 256), 256, 0, s>>>(p.part, p.ks, mn, p.y);
+            if ((e = hipGetLastError()) != hipSuccess) return e;
+        }
     }
     return hipSuccess;
 }
 
-}  // namespace
+// The Q4_K launch shape: kch chunks per tile, tpw tiles per workgroup, ks K
+// parts (quads split as evenly as whole quads allow)
+struct Q4kShape {
+    int kch, tpw, ks;
+};
+Q4kShape q4k_shape(int tiles, int ng) {
+    // quads of 4 super-blocks per step; chunks of at least 3 quads when
+    // there are that many, about 2048 wavefronts in all, up to 8 per
+    // workgroup (a wavefront streams a few steps of 9.2 KB with two in
+    // flight, which keeps HBM busy at a few wavefronts per CU)
+    const int nq = (ng + 3) / 4;
+    const int64_t want = (2048 + tiles - 1) / tiles;
+    Q4kShape q;
+    q.kch = (int)std::min<int64_t>(want, std::min(8, std::max(1, nq / 3)));
+    q.tpw = std::max(1, 4 / q.kch);
+    q.ks = 1;
+    if (nq > 8) {
+        // long rows: every workgroup copies the activation of its K range
+        // into LDS, which for a whole row (8 rows x k bytes of quants) is as
+        // many bytes as a tile's weights.  K parts of 4 quads, one wavefront
+        // per tile and 4 tiles per workgroup: 4096 x 14336 at batch 8 took
+        // 11.8-12.0 us with the parts' reduce launch against 13.0 us whole
+        // (3 and 7 parts, 2-8 tiles and 2 chunks per tile measured slower)
+        q.ks = (nq + 3) / 4;
+        q.kch = 1;
+        q.tpw = 4;
+    }
+    return q;
+}
 
-int mmv_max_k() { return 16384; }
+hipError_t launch_q4k(MmvParams p, Q4kShape q, int64_t m, const ActPlanes &act, float *y, int32_t *S, int32_t *Smin,
+                      void *ws, size_t ws_bytes, hipStream_t s) {
+    const int nq = (p.ng + 3) / 4;
+    if (q.kch < 1 || q.tpw < 1 || q.kch * q.tpw > MAX_WAVES || q.ks < 1 || q.ks > nq) return hipErrorInvalidValue;
+    p.qpp = (nq + q.ks - 1) / q.ks;
+    p.ks = (nq + p.qpp - 1) / p.qpp;  // every part holds a quad
+    p.kch = std::min(q.kch, p.qpp);
+    p.tpw = q.tpw;
+    p.gpc = 0;
+    p.iters = (p.tiles + p.tpw - 1) / p.tpw * p.ks;
+    return S ? launch_f<mmv_q4k_kernel<true>>(p, 4 * p.qpp, m, act, y, S, Smin, ws, ws_bytes, s)
+             : launch_f<mmv_q4k_kernel<false>>(p, 4 * p.qpp, m, act, y, S, Smin, ws, ws_bytes, s);
+}
 
-hipError_t launch_mmv(const WLayout &w, int64_t n, int64_t k, const ActPlanes &act, int64_t m, float *y, int32_t *S,
-                      int32_t *Smin, hipStream_t s) {
-    const int type = w.type;
-    if (type != TYPE_Q4_K && type != TYPE_Q6_K) return hipErrorNotSupported;
-    if (m < 1 || n <= 0 || k <= 0 || k % QK_K || k > mmv_max_k() || n > 0x7fffffff) return hipErrorNotSupported;
-    if (!w.slab || !y || !act.qs || !act.d || !act.bsum16) return hipErrorInvalidValue;
-    if (type == TYPE_Q6_K && !w.d) return hipErrorInvalidValue;
-    if (w.ng != groups_of(type, k)) return hipErrorInvalidValue;
-    if ((S == nullptr) != (Smin == nullptr)) return hipErrorInvalidValue;
-    // 32-bit buffer offsets: activation and y of a pass, the tile's two row blocks
-    if ((int64_t)MAXB * k >= ((int64_t)1 << 31) || (int64_t)MAXB * n * 4 >= ((int64_t)1 << 31)) return hipErrorNotSupported;
-    if (2 * w.rb_stride >= ((int64_t)1 << 31)) return hipErrorNotSupported;
-    MmvParams p;
+bool mmv_args_ok(const WLayout &w, int64_t n, int64_t k) {
+    return (int64_t)MAXB * k < ((int64_t)1 << 31) && (int64_t)MAXB * n * 4 < ((int64_t)1 << 31) &&
+           2 * w.rb_stride < ((int64_t)1 << 31);
+}
+
+MmvParams mmv_params(const WLayout &w, int64_t n, int64_t k) {
+    MmvParams p{};
     p.w = w.slab;
     p.wd = w.d;
     p.rb_stride = w.rb_stride;
@@ -632,21 +700,34 @@ hipError_t launch_mmv(const WLayout &w, int64_t n, int64_t k, const ActPlanes &a
     p.ng = w.ng;
     p.nrb = (int)((n + RB - 1) / RB);
     p.tiles = (int)((n + TILE - 1) / TILE);
+    p.ks = 1;
+    return p;
+}
+
+}  // namespace
+
+int mmv_max_k() { return 16384; }
+
+size_t mmv_workspace_bytes(int type, int64_t n, int64_t k) {
+    if (type != TYPE_Q4_K || k % QK_K || n <= 0) return 0;
+    const Q4kShape q = q4k_shape((int)((n + TILE - 1) / TILE), (int)(k / QK_K));
+    return q.ks > 1 ? (size_t)q.ks * MAXB * (size_t)n * 4 : 0;
+}
+
+hipError_t launch_mmv(const WLayout &w, int64_t n, int64_t k, const ActPlanes &act, int64_t m, float *y, int32_t *S,
+                      int32_t *Smin, void *ws, size_t ws_bytes, hipStream_t s) {
+    const int type = w.type;
+    if (type != TYPE_Q4_K && type != TYPE_Q6_K) return hipErrorNotSupported;
+    if (m < 1 || n <= 0 || k <= 0 || k % QK_K || k > mmv_max_k() || n > 0x7fffffff) return hipErrorNotSupported;
+    if (!w.slab || !y || !act.qs || !act.d || !act.bsum16) return hipErrorInvalidValue;
+    if (type == TYPE_Q6_K && !w.d) return hipErrorInvalidValue;
+    if (w.ng != groups_of(type, k)) return hipErrorInvalidValue;
+    if ((S == nullptr) != (Smin == nullptr)) return hipErrorInvalidValue;
+    // 32-bit buffer offsets: activation and y of a pass, the tile's two row blocks
+    if (!mmv_args_ok(w, n, k)) return hipErrorNotSupported;
+    MmvParams p = mmv_params(w, n, k);
     const bool dump = S != nullptr;
-    if (type == TYPE_Q4_K) {
-        // quads of 4 super-blocks per step; chunks of at least 3 quads when
-        // there are that many, about 2048 wavefronts in all, up to 8 per
-        // workgroup (a wavefront streams a few steps of 9.2 KB with two in
-        // flight, which keeps HBM busy at a few wavefronts per CU)
-        const int nq = (p.ng + 3) / 4;
-        const int64_t want = (2048 + p.tiles - 1) / p.tiles;
-        p.kch = (int)std::min<int64_t>(want, std::min(8, std::max(1, nq / 3)));
-        p.gpc = 0;
-        p.tpw = std::max(1, 4 / p.kch);
-        p.iters = (p.tiles + p.tpw - 1) / p.tpw;
-        return dump ? launch_f<mmv_q4k_kernel<true>>(p, m, act, y, S, Smin, s)
-                    : launch_f<mmv_q4k_kernel<false>>(p, m, act, y, S, Smin, s);
-    }
+    if (type == TYPE_Q4_K) return launch_q4k(p, q4k_shape(p.tiles, p.ng), m, act, y, S, Smin, ws, ws_bytes, s);
     // Q6_K: chunks per tile: about TARGET_WAVES wavefronts in all, chunks of
     // at least MIN_GPC super-blocks, as even as the super-block count allows
     int64_t want = (TARGET_WAVES + p.tiles - 1) / p.tiles;
@@ -655,8 +736,8 @@ hipError_t launch_mmv(const WLayout &w, int64_t n, int64_t k, const ActPlanes &a
     p.kch = (p.ng + p.gpc - 1) / p.gpc;
     p.tpw = std::max(1, MAX_WAVES / p.kch);  // tiles per workgroup: up to MAX_WAVES wavefronts
     p.iters = (p.tiles + p.tpw - 1) / p.tpw;
-    return dump ? launch_f<mmv_kernel<TYPE_Q6_K, true>>(p, m, act, y, S, Smin, s)
-                : launch_f<mmv_kernel<TYPE_Q6_K, false>>(p, m, act, y, S, Smin, s);
+    return dump ? launch_f<mmv_kernel<TYPE_Q6_K, true>>(p, p.ng, m, act, y, S, Smin, ws, ws_bytes, s)
+                : launch_f<mmv_kernel<TYPE_Q6_K, false>>(p, p.ng, m, act, y, S, Smin, ws, ws_bytes, s);
 }
 
 }  // namespace aq

@@ -272,6 +272,20 @@ def test_batch8_long_rows(ctx, wtype, n, k):
     check_matmul(ctx, W, x, cond=False)
 
 
+@pytest.mark.parametrize("n,k,m", [
+    (200, 8960, 5),    # 35 super-blocks: 9 quads, the last one of three, parts of 3 quads
+    (64, 9216, 8),     # 9 quads in 3 parts
+    (4096, 16384, 2),  # 16 quads in 4 parts, many tile groups per workgroup
+    (24, 14336, 8),    # fewer tiles than a workgroup takes
+])
+def test_batch_q4k_k_parts(ctx, n, k, m):
+    """Q4_K rows of more than 8 quads at batch 2-8: K split over
+    workgroups, the parts added by a second launch; block sums bit-exact."""
+    W = S.make_weight(S.TYPE_Q4_K, n, k, seed=n + k + m)
+    x = S.make_activation(m, k, seed=k + m + 1)
+    check_matmul(ctx, W, x, cond=(k < 14336))
+
+
 @pytest.mark.parametrize("k", [55296, 65536])
 @pytest.mark.parametrize("wtype", [S.TYPE_Q4_K, S.TYPE_Q8_0])
 @pytest.mark.parametrize("m", [1, 3])
