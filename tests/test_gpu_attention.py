@@ -194,6 +194,35 @@ def test_prefill_against_numpy(env, n_head, n_kv, hd, index_pos, m, max_seq):
     assert np.array_equal(dvc.cpu().numpy(), vc2)
 
 
+def test_prefill_sharp_softmax(env):
+    """One key row twenty times the others and queries three times larger:
+    scores far apart across the key blocks of the four wavefronts, so the
+    running maxima (base-2 units) and the combine's rescaling decide the
+    result."""
+    torch, lib, ctx = env
+    L = lib.load()
+    n_head, n_kv, hd, m, max_seq = 32, 4, 64, 300, 320
+    rng = np.random.default_rng(21)
+    width = (n_head + n_kv) * hd
+    qk = rng.standard_normal((m, width)).astype(np.float32)
+    qk[:, :n_head * hd] *= 3.0
+    qk[57, n_head * hd:] *= 20.0  # key 57 far above the others for every later query
+    v = rng.standard_normal((m, n_kv * hd)).astype(np.float32)
+    kc = np.zeros((n_kv, max_seq, hd), np.float32)
+    vc = np.zeros((n_kv, max_seq, hd), np.float32)
+    cos, sin = _tables(hd, max_seq)
+    dqk, dv, dkc, dvc = _dev(torch, qk), _dev(torch, v), _dev(torch, kc), _dev(torch, vc)
+    dcos, dsin = _dev(torch, cos), _dev(torch, sin)
+    out = torch.empty((m, n_head * hd), dtype=torch.float32, device="cuda:0")
+    torch.cuda.synchronize()
+    lib.check(L.aq_llama_attn_prefill(ctx.handle, dqk.data_ptr(), width, dqk.data_ptr() + 4 * n_head * hd, width,
+                                      dv.data_ptr(), n_kv * hd, dcos.data_ptr(), dsin.data_ptr(), 0, m,
+                                      dkc.data_ptr(), dvc.data_ptr(), n_head, n_kv, hd, max_seq, out.data_ptr()))
+    ctx.synchronize()
+    want, _, _ = _prefill_ref(qk[:, :n_head * hd], qk[:, n_head * hd:], v, kc, vc, cos, sin, 0, n_head, n_kv, hd)
+    assert _rel(out.cpu().numpy(), want) <= 1e-5
+
+
 def test_prefill_then_decode_continue_the_same_cache(env):
     """A prompt through the prefill kernel, then decode steps at the next
     positions read the cache it wrote (the layout both kernels share)."""
