@@ -55,6 +55,7 @@ SIGNATURES = {
     "aq_act_bytes": (SZ, [INT, I64, I64]),
     "aq_quantize_act_device": (INT, [P, INT, P, I64, I64, P]),
     "aq_qmatmul_preq_device": (INT, [P, P, P, I64, I64, P]),
+    "aq_qmatmul2_preq_device": (INT, [P, P, P, P, I64, I64, P, P]),
     "aq_quantize_q8k": (INT, [P, P, I64, I64, P]),
     "aq_quantize_q8_0": (INT, [P, P, I64, I64, P]),
     "aq_qmatmul_block_sums": (INT, [P, P, P, I64, I64, P, P]),

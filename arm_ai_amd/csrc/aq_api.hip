@@ -583,6 +583,28 @@ int aq_qmatmul_preq_device(aq_ctx *ctx, const aq_qweight *w, const void *d_act, 
     return AQ_OK;
 }
 
+int aq_qmatmul2_preq_device(aq_ctx *ctx, const aq_qweight *w1, const aq_qweight *w2, const void *d_act, int64_t m,
+                            int64_t k, float *d_y1, float *d_y2) {
+    int rc = check_mm(ctx, w1, m, k);
+    if (rc) return rc;
+    if ((rc = check_mm(ctx, w2, m, k))) return rc;
+    if (m == 0) return AQ_OK;
+    if (!d_act || !d_y1 || !d_y2) return fail(AQ_ERR_INVALID_ARG, "null activation or output");
+    if ((uintptr_t)d_act & 255) return fail(AQ_ERR_INVALID_ARG, "activation buffer must be 256-byte aligned");
+    if ((rc = use_device(ctx->device))) return rc;
+    hipError_t e = hipErrorNotSupported;
+    if (use_gemm(w1, m) && use_gemm(w2, m)) {
+        CallLayout L = call_layout(w2, m, false, false, true);  // the second GEMM's split-K partials
+        if ((rc = ensure_scratch(ctx, L.total))) return rc;
+        e = launch_gemm_pair(w1->glayout, w1->n, d_y1, w2->glayout, w2->n, d_y2, k, act_planes((void *)d_act, m, k), m,
+                             (uint8_t *)ctx->scratch + L.ws, L.total - L.ws, ctx->stream);
+    }
+    if (e == hipSuccess) return AQ_OK;
+    if (e != hipErrorNotSupported) return fail(AQ_ERR_HIP, "paired gemm: %s", hipGetErrorString(e));
+    if ((rc = aq_qmatmul_preq_device(ctx, w1, d_act, m, k, d_y1))) return rc;
+    return aq_qmatmul_preq_device(ctx, w2, d_act, m, k, d_y2);
+}
+
 static int quantize_host(aq_ctx *ctx, int atype, const float *x, int64_t m, int64_t k, void *out_blocks) {
     if (!ctx) return fail(AQ_ERR_INVALID_ARG, "null context");
     const int blk = atype == AQ_TYPE_Q8_K ? QK_K : QK8_0;

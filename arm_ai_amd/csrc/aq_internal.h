@@ -199,6 +199,15 @@ hipError_t launch_mmv(const WLayout &w, int64_t n, int64_t k, const ActPlanes &a
 constexpr int GEMM_MAX_TILES = 1 << 20;
 hipError_t launch_gemm(const WLayout &w, int64_t n, int64_t k, const ActPlanes &x, int64_t m, float *y, int32_t *S,
                        int32_t *Smin, void *ws, size_t ws_bytes, hipStream_t s);
+// A Q4_K weight and a Q6_K / Q5_K weight of the same k on one activation
+// (with its f16 quants plane) in one launch, the first unsplit, the second
+// split over k as launch_gemm would (its partials in ws, gemm_workspace_bytes
+// of the second weight's shape, and its reduce launch after).
+// hipErrorNotSupported when the types differ from that, the rows need more
+// than one launch, or the two together have more work items than the CUs
+// hold at once (the caller then runs launch_gemm twice).
+hipError_t launch_gemm_pair(const WLayout &w1, int64_t n1, float *y1, const WLayout &w2, int64_t n2, float *y2,
+                            int64_t k, const ActPlanes &x, int64_t m, void *ws, size_t ws_bytes, hipStream_t s);
 // Workspace bytes launch_gemm needs for this shape, or (size_t)-1 if the
 // weight type / shape has no GEMM (the matvec then serves m > 8 too).
 size_t gemm_workspace_bytes(int type, int64_t m, int64_t n, int64_t k);

@@ -49,6 +49,7 @@
 // does not depend on which workgroup finished first, and no workgroup waits
 // on another.
 #include "aq_internal.h"
+#include "gemm6_impl.h"
 
 #include <algorithm>
 
@@ -116,12 +117,12 @@ __device__ __forceinline__ uint32_t f16pair_of_byte(uint32_t w, int b) {
     return __builtin_bit_cast(uint32_t, r);
 }
 
+// The kernel's body for workgroup bid of the launch, on LDS of Lds::BYTES
+// (so that another launch can run it beside other work).
 template <bool DUMP>
-__global__ __launch_bounds__(256, DUMP ? 1 : 2) void gemm_q4k_kernel(GemmParams p) {
-    __shared__ __align__(16) uint8_t lds[Lds::BYTES];
-
+__device__ __forceinline__ void gemm_q4k_body(GemmParams p, uint8_t *lds, int bid) {
     // workgroup -> (tile, split): contiguous ranges per XCD, m-tiles then splits fastest
-    const int xcd = blockIdx.x % NXCD, local = blockIdx.x / NXCD;
+    const int xcd = bid % NXCD, local = bid / NXCD;
     const int item = xcd * p.per_xcd + local;
     if (local >= p.per_xcd || item >= p.items) return;  // uniform over the workgroup
     const int tile = item / p.splits, split = item - tile * p.splits;
@@ -341,6 +342,24 @@ __global__ __launch_bounds__(256, DUMP ? 1 : 2) void gemm_q4k_kernel(GemmParams 
         for (int r = 0; r < 16; r++) mine[(32 * t + 8 * (r >> 2) + 4 * h + (r & 3)) * GBN + ccol] = yacc[t][r];
 }
 
+template <bool DUMP>
+__global__ __launch_bounds__(256, DUMP ? 1 : 2) void gemm_q4k_kernel(GemmParams p) {
+    __shared__ __align__(16) uint8_t lds[Lds::BYTES];
+    gemm_q4k_body<DUMP>(p, lds, (int)blockIdx.x);
+}
+
+// A Q4_K GEMM and a Q6_K / Q5_K one (T2) on the same activation in one
+// launch: workgroups [0, g1) run the first (g1 a multiple of the XCD count,
+// so its XCD mapping is kept), the rest the second, on one LDS buffer that
+// either body fits.  The first is not split over K; the second may be (its
+// partials then go to the workspace and the reduce launch follows).
+template <int T2>
+__global__ __launch_bounds__(256, 2) void gemm_pair_kernel(GemmParams p1, Gemm6Params p2, int g1) {
+    __shared__ __align__(16) uint8_t lds[Lds::BYTES > Lds6::BYTES ? Lds::BYTES : Lds6::BYTES];
+    if ((int)blockIdx.x < g1) gemm_q4k_body<false>(p1, lds, (int)blockIdx.x);  // uniform
+    else gemm_f16w_body<T2, false>(p2, lds, (int)blockIdx.x - g1);
+}
+
 // y = sum over splits (in split order) of the partial tiles; one thread per
 // output element of a tile row.  A kernel boundary, not a fence, makes the
 // partials visible: a device-scope fence per workgroup costs an L2
@@ -466,6 +485,75 @@ hipError_t launch_gemm(const WLayout &w, int64_t n, int64_t k, const ActPlanes &
         }
     }
     return hipSuccess;
+}
+
+hipError_t launch_gemm_pair(const WLayout &w1, int64_t n1, float *y1, const WLayout &w2, int64_t n2, float *y2,
+                            int64_t k, const ActPlanes &x, int64_t m, void *ws, size_t ws_bytes, hipStream_t s) {
+    if (w1.type != TYPE_Q4_K || (w2.type != TYPE_Q6_K && w2.type != TYPE_Q5_K)) return hipErrorNotSupported;
+    const bool q5 = w2.type == TYPE_Q5_K;
+    if (!w1.slab || !w2.slab || (!q5 && !w2.d) || !y1 || !y2 || !x.qs || !x.d || !x.bsum16) return hipErrorInvalidValue;
+    if (!x.q16) return hipErrorNotSupported;  // the second GEMM reads the f16 quants the quantizer wrote
+    if (m <= 0 || n1 <= 0 || n2 <= 0 || k <= 0 || k % QK_K || m > 0x7fffffff || n1 > 0x7fffffff ||
+        n2 > 0x7fffffff || k > (1 << 24) || w1.ng != k / QK_K || w2.ng != k / QK_K)
+        return hipErrorInvalidValue;
+    if ((int64_t)16 * w1.rb_stride >= ((int64_t)1 << 31) || (int64_t)16 * w2.rb_stride >= ((int64_t)1 << 31))
+        return hipErrorNotSupported;
+    // one launch of each (no row chunks), the first unsplit, the second split
+    // as its own launch would be, and together no more workgroups than the
+    // CUs hold at once
+    if (gemm_chunk_rows(m, k) < m || gemm6_chunk_rows(k) < m) return hipErrorNotSupported;
+    GemmPlan g1 = gemm_plan(m, n1, k);
+    Gemm6Plan g2 = gemm6_plan(m, n2, k);
+    if ((int64_t)g1.tiles + (int64_t)g2.tiles * g2.splits > TARGET_WG6 || g1.tiles > GEMM_MAX_TILES ||
+        g2.tiles > GEMM_MAX_TILES)
+        return hipErrorNotSupported;
+    if (g2.splits > 1 && (!ws || ws_bytes < g2.part)) return hipErrorInvalidValue;
+    const int ng = w1.ng;
+    GemmParams p;
+    p.w = w1.slab;
+    p.rb_stride = w1.rb_stride;
+    p.ng = ng;
+    p.xq = x.qs;
+    p.xd = x.d;
+    p.xbs = x.bsum16;
+    p.y = y1;
+    p.m = (int)m;
+    p.n = (int)n1;
+    p.k = (int)k;
+    p.ntm = g1.ntm;
+    p.tiles = g1.tiles;
+    p.splits = 1;
+    p.kbs = ng;
+    p.items = g1.tiles;
+    p.per_xcd = (p.items + NXCD - 1) / NXCD;
+    p.part = nullptr;
+    p.S = p.Smin = nullptr;
+    Gemm6Params q;
+    q.w = w2.slab;
+    q.wd = w2.d;
+    q.rb_stride = w2.rb_stride;
+    q.ng = ng;
+    q.x16 = x.q16;
+    q.xd = x.d;
+    q.xbs = q5 ? x.bsum16 : nullptr;
+    q.y = y2;
+    q.m = (int)m;
+    q.n = (int)n2;
+    q.k = (int)k;
+    q.ntm = g2.ntm;
+    q.tiles = g2.tiles;
+    q.splits = g2.splits;
+    q.kbs = g2.kbs;
+    q.items = g2.tiles * g2.splits;
+    q.per_xcd = (q.items + NXCD6 - 1) / NXCD6;
+    q.part = (float *)ws;
+    q.S = q.Smin = nullptr;
+    const int b1 = p.per_xcd * NXCD, b2 = q.per_xcd * NXCD6;
+    if (q5) gemm_pair_kernel<TYPE_Q5_K><<<(unsigned)(b1 + b2), 256, 0, s>>>(p, q, b1);
+    else gemm_pair_kernel<TYPE_Q6_K><<<(unsigned)(b1 + b2), 256, 0, s>>>(p, q, b1);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || g2.splits == 1) return e;
+    return launch_splitk_reduce(q.part, y2, q.m, q.n, g2.ntm, G6M, g2.splits, g2.tiles, s);
 }
 
 }  // namespace aq

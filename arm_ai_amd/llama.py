@@ -315,6 +315,24 @@ class Llama:
             return y[:, :na], y[:, na:]
         return self._mm_act(lw["wq"], act, m, x), self._mm_act(lw["wk"], act, m, x)
 
+    def _qkv_act(self, lw, act, m, x):
+        """q, k and v from the quantised norm output: wq|wk and wv in one
+        call (aq_qmatmul2_preq_device: one launch where their types allow)."""
+        from . import _lib
+
+        if "wqk" not in lw:
+            q, k = self._pair_act(lw, act, m, x)
+            return q, k, self._mm_act(lw["wv"], act, m, x)
+        w1, w2 = lw["wqk"], lw["wv"]
+        f32 = dict(dtype=self.torch.float32, device=self.dev)
+        y1, y2 = self.torch.empty((m, w1.n), **f32), self.torch.empty((m, w2.n), **f32)
+        _lib.check(_lib.load().aq_qmatmul2_preq_device(self.ctx.handle, w1.handle, w2.handle, act.data_ptr(), m, w1.k,
+                                                       y1.data_ptr(), y2.data_ptr()))
+        self._record_mm(w1, x, y1)
+        self._record_mm(w2, x, y2)
+        na = w1.n - self._n_second["wqk"]
+        return y1[:, :na], y1[:, na:], y2
+
     def _pair(self, lw, merged, a, b, x):
         """Outputs of projections a and b of x: one launch on the merged weight, or two."""
         if merged in lw:
@@ -453,8 +471,7 @@ class Llama:
                     chk(L.aq_llama_rmsnorm_act(c, ptr(x), ptr(delta) if delta is not None else None,
                                                ptr(self.attn_norm[li]), n, cfg.hidden, eps, ptr(h) if keep else None,
                                                ptr(act_h)))
-                    q, k = self._pair_act(lw, act_h, n, h)
-                    v = self._mm_act(lw["wv"], act_h, n, h)
+                    q, k, v = self._qkv_act(lw, act_h, n, h)
                     chk(L.aq_llama_attn_prefill(c, ptr(q), q.stride(0), ptr(k), k.stride(0), ptr(v), v.stride(0),
                                                 ptr(self.cos), ptr(self.sin), index_pos, n, ptr(self.k_cache[li]),
                                                 ptr(self.v_cache[li]), H, Hkv, D, cfg.max_seq, ptr(y)))

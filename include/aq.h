@@ -134,6 +134,16 @@ size_t aq_act_bytes(int act_type, int64_t m, int64_t k);
 int aq_quantize_act_device(aq_ctx *ctx, int act_type, const float *d_x, int64_t m, int64_t k, void *d_act);
 int aq_qmatmul_preq_device(aq_ctx *ctx, const aq_qweight *w, const void *d_act, int64_t m, int64_t k,
                            float *d_dst);
+/* Two QMatMul::forward calls on the same pre-quantised activation, w1's
+ * result in d_y1 [m][w1 n] and w2's in d_y2 [m][w2 n] (llama's wq|wk and wv
+ * on the attention norm's output, candle quantized_llama's attention block,
+ * reached from llama_candle.rs:93).  A Q4_K w1 with a Q6_K or Q5_K w2 at a
+ * GEMM-sized m runs as one launch (the two GEMMs in separate workgroups, w1
+ * not split over k; w2's split partials then summed by a small second
+ * launch); other cases make the two aq_qmatmul_preq_device calls.  Same
+ * results as those calls up to the f32 summation order of w1's partials. */
+int aq_qmatmul2_preq_device(aq_ctx *ctx, const aq_qweight *w1, const aq_qweight *w2, const void *d_act, int64_t m,
+                            int64_t k, float *d_y1, float *d_y2);
 
 /* BlockQ8K::from_float on the GPU: host f32 [m][k] -> host Q8_K blocks
  * (m * k/256 blocks of 292 bytes: f32 d, i8 qs[256], i16 bsums[16]). */

@@ -68,6 +68,8 @@ pub fn aq_abi_version() -> c_int;
         d_act: *mut c_void) -> c_int;
     pub fn aq_qmatmul_preq_device(ctx: *mut AqCtx, w: *const AqQWeight, d_act: *const c_void, m: i64, k: i64,
         d_dst: *mut f32) -> c_int;
+    pub fn aq_qmatmul2_preq_device(ctx: *mut AqCtx, w1: *const AqQWeight, w2: *const AqQWeight, d_act: *const c_void,
+        m: i64, k: i64, d_y1: *mut f32, d_y2: *mut f32) -> c_int;
     pub fn aq_quantize_q8k(ctx: *mut AqCtx, x: *const f32, m: i64, k: i64, out_blocks: *mut c_void) -> c_int;
     pub fn aq_quantize_q8_0(ctx: *mut AqCtx, x: *const f32, m: i64, k: i64, out_blocks: *mut c_void) -> c_int;
     pub fn aq_qmatmul_block_sums(ctx: *mut AqCtx, w: *const AqQWeight, lhs: *const f32, m: i64, k: i64, S: *mut i32,

@@ -648,6 +648,56 @@ def test_prequantised_gemm_reads_the_planes_f16_quants(env, wtype, n, k, m):
     mm.free()
 
 
+@pytest.mark.parametrize("t1,t2,n1,n2,k,m", [
+    (12, 14, 2304, 256, 2048, 512),   # TinyLlama wq|wk and wv, a 512-token prompt: one launch
+    (12, 14, 2304, 256, 2048, 100),   # ragged m-tiles
+    (12, 13, 2304, 256, 2048, 33),    # a Q5_K wv
+    (12, 14, 5120, 1024, 4096, 64),   # Llama-3-8B heads
+    (12, 14, 2304, 256, 2048, 5),     # batch rows: two matrix-core matvec calls
+    (12, 12, 2304, 256, 2048, 40),    # two Q4_K weights: two GEMM calls
+])
+def test_qmatmul2_preq_equals_two_calls(env, t1, t2, n1, n2, k, m):
+    """aq_qmatmul2_preq_device against two aq_qmatmul_preq_device calls on
+    the same planes: the paired launch runs the Q4_K GEMM unsplit, so only the
+    f32 order of its split-K partials may differ (within 1e-6 of the largest
+    output); the cases that make the two calls are bit-identical."""
+    import arm_ai_amd as A
+    from arm_ai_amd import synth as S
+
+    torch, lib, ctx = env
+    L = lib.load()
+    W1 = S.make_weight(t1, n1, k, seed=n1 + k)
+    W2 = S.make_weight(t2, n2, k, seed=n2 + k + 1)
+    mm1 = A.QMatMul.from_qtensor(A.QTensor(t1, (n1, k), W1.blocks), ctx)
+    mm2 = A.QMatMul.from_qtensor(A.QTensor(t2, (n2, k), W2.blocks), ctx)
+    x = np.random.default_rng(m + k).standard_normal((m, k)).astype(np.float32)
+    dx, dwn = _dev(torch, x), _dev(torch, np.ones(k, np.float32))
+    act = _act(torch, lib, m, k)
+    f32 = dict(dtype=torch.float32, device="cuda:0")
+    y1, y2 = torch.empty((m, n1), **f32), torch.empty((m, n2), **f32)
+    r1, r2 = torch.empty((m, n1), **f32), torch.empty((m, n2), **f32)
+    torch.cuda.synchronize()
+    lib.check(L.aq_llama_rmsnorm_act(ctx.handle, dx.data_ptr(), None, dwn.data_ptr(), m, k, ctypes.c_float(1e-5),
+                                     None, act.data_ptr()))
+    lib.check(L.aq_qmatmul2_preq_device(ctx.handle, mm1.handle, mm2.handle, act.data_ptr(), m, k, y1.data_ptr(),
+                                        y2.data_ptr()))
+    lib.check(L.aq_qmatmul_preq_device(ctx.handle, mm1.handle, act.data_ptr(), m, k, r1.data_ptr()))
+    lib.check(L.aq_qmatmul_preq_device(ctx.handle, mm2.handle, act.data_ptr(), m, k, r2.data_ptr()))
+    ctx.synchronize()
+    paired = m > 8 and t1 == 12 and t2 in (13, 14)
+    for got, want in ((y1, r1), (y2, r2)):
+        got, want = got.cpu().numpy(), want.cpu().numpy()
+        assert np.all(np.isfinite(got))
+        if paired:
+            assert np.max(np.abs(got - want)) <= 1e-6 * np.max(np.abs(want))
+        else:
+            assert np.array_equal(got, want)
+    assert L.aq_qmatmul2_preq_device(ctx.handle, mm1.handle, mm2.handle, act.data_ptr(), m, k + 256, y1.data_ptr(),
+                                     y2.data_ptr()) == lib.AQ_ERR_SHAPE
+    mm1.free()
+    mm2.free()
+
+
 def test_prompt_glue_act_errors(env):
     torch, lib, ctx = env
     L = lib.load()
