@@ -578,6 +578,31 @@ __device__ __forceinline__ void store_q8k_block16(const ActPlanes &a, int64_t ro
     if (s == 0) a.d[row * (k / QK_K) + sb] = d;
 }
 
+// The stores of one Q8_K block by a wavefront (q8k_block_wave's layout):
+// lane l writes quants 4l..4l+3 (and their f16 copy when a.q16 is set), the
+// first lane of each quad its bsum, lane 0 d.  Block sb of row `row`, rows of
+// k elements.
+__device__ __forceinline__ void store_q8k_block64(const ActPlanes &a, int64_t row, int64_t k, int64_t sb, int lane,
+                                                  uint32_t packed, int bsum, float d) {
+    const int64_t e0 = row * k + sb * QK_K + 4 * lane;
+    *(uint32_t *)(a.qs + e0) = packed;
+    if (a.q16) {
+        uint32_t o[2];
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const uint32_t lo = __builtin_bit_cast(uint16_t, (_Float16)(int)(int8_t)((packed >> (16 * j)) & 0xffu));
+            const uint32_t hi = __builtin_bit_cast(uint16_t, (_Float16)(int)(int8_t)((packed >> (16 * j + 8)) & 0xffu));
+            o[j] = lo | (hi << 16);
+        }
+        *(uint2 *)(a.q16 + e0) = make_uint2(o[0], o[1]);
+    }
+    if ((lane & 3) == 0) {
+        a.bsums[row * (k / 16) + sb * 16 + (lane >> 2)] = (int16_t)bsum;
+        a.bsum16[row * (k / 16) + sb * 16 + (lane >> 2)] = __builtin_bit_cast(uint16_t, (_Float16)(float)bsum);
+    }
+    if (lane == 0) a.d[row * (k / QK_K) + sb] = d;
+}
+
 // One Q8_0 block (BlockQ8_0::from_float) quantised by eight consecutive
 // lanes (lane sub = l%8 holds elements 4sub..4sub+3): d = amax/127, id = 1/d
 // (0 if d == 0), q = round(x*id) as i8, stored d = f16(d) (RNE).  Returns the

@@ -73,7 +73,7 @@ __global__ __launch_bounds__(DEC_THREADS) void embed_kernel(const float *__restr
 // read once and every load is issued before the first use.  The body is
 // shared by the kernel that quantises the result in the same launch
 // (rmsnorm_act_kernel), so both produce the same values bit for bit: `put`
-// receives float4 i of the output row.
+// receives float4 i = threadIdx.x + j * DEC_THREADS of the output row.
 constexpr int RMS_V = 8;
 template <typename Put>
 __device__ __forceinline__ void rmsnorm_row(float *__restrict__ x, const float *__restrict__ delta,
@@ -111,7 +111,7 @@ __device__ __forceinline__ void rmsnorm_row(float *__restrict__ x, const float *
         const int i = threadIdx.x + j * DEC_THREADS;
         if (i < n4) {
             const float4 ww = w4[i];
-            put(i, make_float4((v[j].x / m) * ww.x, (v[j].y / m) * ww.y, (v[j].z / m) * ww.z, (v[j].w / m) * ww.w));
+            put(j, i, make_float4((v[j].x / m) * ww.x, (v[j].y / m) * ww.y, (v[j].z / m) * ww.z, (v[j].w / m) * ww.w));
         }
     }
 }
@@ -121,51 +121,40 @@ __global__ __launch_bounds__(DEC_THREADS) void rmsnorm_kernel(float *__restrict_
                                                               float *__restrict__ out) {
     __shared__ float red[DEC_THREADS / 64];
     float4 *orow = (float4 *)(out + (int64_t)blockIdx.x * n);
-    rmsnorm_row(x, delta, w, n, eps, red, [&](int i, float4 h) { orow[i] = h; });
-}
-
-// Q8_K quantisation of the row of n (a multiple of 256) values in LDS into
-// row `row` of the planes a: the quantizer kernel's per-block code and stores
-// (16 lanes per block, q8k_block_row16), the workgroup's 16 lane rows taking
-// blocks b, b + 16, ...
-__device__ __forceinline__ void quantize_row_from_lds(const float *hs, int n, int64_t row, const ActPlanes &a) {
-    const int s = threadIdx.x & 15, grp = threadIdx.x >> 4;
-    const int nb = n / QK_K;
-    for (int b0 = 0; b0 < nb; b0 += DEC_THREADS / 16) {  // uniform trip count
-        const int b = b0 + grp;
-        const bool ok = b < nb;  // uniform over the 16-lane row
-        float v[16];
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const float4 t = ok ? *(const float4 *)(hs + b * QK_K + 16 * s + 4 * i) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            v[4 * i] = t.x;
-            v[4 * i + 1] = t.y;
-            v[4 * i + 2] = t.z;
-            v[4 * i + 3] = t.w;
-        }
-        int bsum;
-        float d;
-        const uint4 packed = q8k_block_row16(v, s, &bsum, &d);
-        if (ok) store_q8k_block16(a, row, n, b, s, packed, bsum, d);
-    }
+    rmsnorm_row(x, delta, w, n, eps, red, [&](int, int i, float4 h) { orow[i] = h; });
 }
 
 // rmsnorm_kernel's output quantised to Q8_K in the same launch (the prompt's
-// norm before a prefill GEMM): the normed row goes to LDS (and to out when it
-// is given), then the quantizer's per-block code writes the planes.
+// norm before a prefill GEMM).  Float4 i = threadIdx.x + j * DEC_THREADS of
+// the row is held by lane l of wavefront w (threadIdx.x = 64 w + l), so
+// wavefront w holds Q8_K block w + 4j whole, four values a lane: each
+// wavefront quantises its blocks from registers with the quantizer's
+// one-wavefront code (q8k_block_wave, the arithmetic of the quantizer
+// kernel's), with no LDS and no barrier after the norm.  out, when given,
+// gets the normed row.
 __global__ __launch_bounds__(DEC_THREADS) void rmsnorm_act_kernel(float *__restrict__ x,
                                                                   const float *__restrict__ delta,
                                                                   const float *__restrict__ w, int n, float eps,
                                                                   float *__restrict__ out, ActPlanes a) {
+    static_assert(DEC_THREADS == 256, "wavefront w holds blocks w + 4j");
     __shared__ float red[DEC_THREADS / 64];
-    __shared__ __align__(16) float hs[4 * RMS_V * DEC_THREADS];
     float4 *orow = out ? (float4 *)(out + (int64_t)blockIdx.x * n) : nullptr;
-    rmsnorm_row(x, delta, w, n, eps, red, [&](int i, float4 h) {
-        ((float4 *)hs)[i] = h;
+    float4 hv[RMS_V];
+    rmsnorm_row(x, delta, w, n, eps, red, [&](int j, int i, float4 h) {
+        hv[j] = h;
         if (orow) orow[i] = h;
     });
-    __syncthreads();
-    quantize_row_from_lds(hs, n, blockIdx.x, a);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nb = n / QK_K;
+#pragma unroll
+    for (int j = 0; j < RMS_V; j++) {
+        const int b = wave + 4 * j;
+        if (b >= nb) break;  // uniform over the wavefront
+        const float v[4] = {hv[j].x, hv[j].y, hv[j].z, hv[j].w};
+        int bsum;
+        float d;
+        const uint32_t packed = q8k_block_wave(v, lane, &bsum, &d);
+        store_q8k_block64(a, blockIdx.x, n, b, lane, packed, bsum, d);
+    }
 }
 
 // out[r][i] = silu(g[r][i]) * u[r][i] for rows r (grid y) of n; row r of g
