@@ -36,6 +36,7 @@ def _both(ctx, mm, x):
     (S.TYPE_Q4_K, 2048, 5632, (64, 20, 1)),   # int8 GEMM, then a smaller GEMM, then the matvec
     (S.TYPE_Q6_K, 2048, 2048, (96, 33)),      # f16 GEMM (quants copied to f16 in the scratch)
     (S.TYPE_Q8_0, 1024, 4096, (48, 9)),       # Q8_0 GEMM (Q8_0 activation planes)
+    (S.TYPE_Q4_K, 512, 14336, (8, 3)),        # batched matvec in K parts (the parts' sums in the scratch)
 ])
 def test_noalloc_matches_the_allocating_entry(ctx, wtype, n, k, ms):
     W = S.make_weight(wtype, n, k, seed=n + k + wtype)
@@ -45,7 +46,8 @@ def test_noalloc_matches_the_allocating_entry(ctx, wtype, n, k, ms):
         ya, yb = _both(ctx, mm, x)
         assert np.array_equal(ya, yb), f"m={m}: the fixed-scratch call differs from the allocating one"
         r = O.matmul(wtype, x, W.blocks, n, k)
-        assert float(np.abs(yb - r).max()) <= 1e-5 * float(np.abs(r).max())
+        tol = 1e-4 if k >= 14336 else 1e-5  # the parity bar for rows of 14336 and more
+        assert float(np.abs(yb - r).max()) <= tol * float(np.abs(r).max())
     mm.free()
 
 
