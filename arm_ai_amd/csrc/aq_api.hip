@@ -1138,10 +1138,17 @@ int aq_llama_head_argmax_embed(aq_ctx *ctx, const aq_qweight *w, const float *d_
                                                     w->n, hidden, d_x_next, ctx->stream),
                           "argmax parts embed");
     if (e != hipErrorNotSupported) return hip_status(e, "matvec rmsnorm argmax");
-    // other heads: the fused-norm matvec, the argmax over the logits, the embedding
+    // other heads: the fused-norm matvec, first maxima of the logits per
+    // workgroup, then the pick and the embedding as above
     e = launch_matvec_rmsnorm(w->layout, w->n, w->k, d_x, d_delta, d_norm_w, eps, nullptr, d_logits, ctx->stream);
     if (e == hipErrorNotSupported) return fail(AQ_ERR_SHAPE, "k=%lld is too long for the fused norm", (long long)k);
     if (e != hipSuccess) return hip_status(e, "matvec rmsnorm");
+    e = launch_argmax_parts(d_logits, w->n, ctx->head_part, HEAD_PARTS, &nparts, ctx->stream);
+    if (e == hipSuccess)
+        return hip_status(launch_argmax_parts_embed(ctx->head_part, nparts, d_tok, d_pos, d_hist, hist_len, d_table,
+                                                    w->n, hidden, d_x_next, ctx->stream),
+                          "argmax parts embed");
+    if (e != hipErrorNotSupported) return hip_status(e, "argmax parts");
     if ((e = launch_argmax(d_logits, w->n, d_tok, d_pos, d_hist, hist_len, ctx->stream)) != hipSuccess)
         return hip_status(e, "argmax");
     return hip_status(launch_embed(d_table, w->n, d_tok, 1, hidden, d_x_next, ctx->stream), "embed");
@@ -1193,6 +1200,6 @@ int aq_qmatmul2_rmsnorm_f32_device(aq_ctx *ctx, const aq_qweight *w1, const aq_q
     const hipError_t e = launch_matvec2_rmsnorm(w1->layout, w1->n, d_dst1, w2->layout, w2->n, d_dst2, k, d_x, d_delta,
                                                 d_norm_w, eps, d_h_out, ctx->stream);
     if (e == hipErrorNotSupported)
-        return fail(AQ_ERR_SHAPE, "the two-weight fused norm takes Q4_K / Q6_K weights with k <= 8192");
+        return fail(AQ_ERR_SHAPE, "k=%lld is too long for the fused norm", (long long)k);
     return hip_status(e, "matvec2 rmsnorm");
 }

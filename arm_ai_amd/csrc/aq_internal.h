@@ -309,6 +309,9 @@ hipError_t launch_argmax(const float *x, int64_t n, int64_t *d_tok, int64_t *d_p
                          hipStream_t s);
 // The greedy pick from per-workgroup (value bits, row) pairs (the first row
 // of the largest value), then that token's embedding row into xout.
+// Per-workgroup first maxima of x (one (value bits, index) pair per 512
+// values, at most max_parts) for launch_argmax_parts_embed.
+hipError_t launch_argmax_parts(const float *x, int64_t n, int2 *parts, int max_parts, int *nparts, hipStream_t s);
 hipError_t launch_argmax_parts_embed(const int2 *parts, int nparts, int64_t *d_tok, int64_t *d_pos, int64_t *hist,
                                      int64_t hist_len, const float *table, int64_t vocab, int64_t hidden, float *xout,
                                      hipStream_t s);

@@ -549,7 +549,46 @@ __global__ __launch_bounds__(DEC_THREADS) void argmax_parts_embed_kernel(
         ((float4 *)xout)[i] = ok ? src[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 }
 
+// The first maximum of each range of len values of x (a NaN never wins):
+// workgroup b takes [b len, min(n, (b + 1) len)) and writes (bits of the
+// value, index) to parts[b], the pairs argmax_parts_embed_kernel reduces.  For
+// heads whose matvec does not keep the pairs itself.
+__global__ __launch_bounds__(DEC_THREADS) void argmax_parts_kernel(const float *__restrict__ x, int n, int len,
+                                                                   int2 *__restrict__ parts) {
+    __shared__ float bv[DEC_THREADS / 64];
+    __shared__ int bi[DEC_THREADS / 64];
+    const int b0 = (int)blockIdx.x * len, b1 = min(n, b0 + len);
+    float best = -INFINITY;
+    int idx = 0x7fffffff;
+    for (int i = b0 + (int)threadIdx.x; i < b1; i += DEC_THREADS) better(x[i], i, best, idx);
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        const float ov = __shfl_xor(best, o);
+        const int oi = __shfl_xor(idx, o);
+        better(ov, oi, best, idx);
+    }
+    if ((threadIdx.x & 63) == 0) {
+        bv[threadIdx.x >> 6] = best;
+        bi[threadIdx.x >> 6] = idx;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < DEC_THREADS / 64; w++) better(bv[w], bi[w], best, idx);
+        parts[blockIdx.x] = make_int2((int)f32_as_u32(best), idx);
+    }
+}
+
 }  // namespace
+
+hipError_t launch_argmax_parts(const float *x, int64_t n, int2 *parts, int max_parts, int *nparts, hipStream_t s) {
+    constexpr int LEN = 2 * DEC_THREADS;  // values per workgroup
+    if (!x || !parts || !nparts || n <= 0 || n > 0x7fffffff) return hipErrorInvalidValue;
+    const int64_t g = (n + LEN - 1) / LEN;
+    if (g > max_parts) return hipErrorNotSupported;
+    argmax_parts_kernel<<<(unsigned)g, DEC_THREADS, 0, s>>>(x, (int)n, LEN, parts);
+    *nparts = (int)g;
+    return hipGetLastError();
+}
 
 hipError_t launch_argmax_parts_embed(const int2 *parts, int nparts, int64_t *d_tok, int64_t *d_pos, int64_t *hist,
                                      int64_t hist_len, const float *table, int64_t vocab, int64_t hidden, float *xout,

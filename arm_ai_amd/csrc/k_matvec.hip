@@ -1038,8 +1038,9 @@ namespace {
 hipError_t norm_params(const WLayout &w, int64_t n, int64_t k, const float *x, const XfArgs &xa, float *y,
                        MvParams &p, int64_t &grid, size_t &lds) {
     const int type = w.type;
-    if (type != TYPE_Q4_K && type != TYPE_Q6_K) return hipErrorNotSupported;
-    if (!w.slab || n <= 0 || k <= 0 || k % QK_K || n > 0x7fffffff || k > 0x7fffffff || !y || !x) return hipErrorInvalidValue;
+    if (type != TYPE_Q4_K && type != TYPE_Q6_K && type != TYPE_Q5_0 && type != TYPE_Q8_0) return hipErrorNotSupported;
+    const int blk = act_q80(type) ? QK8_0 : QK_K;
+    if (!w.slab || n <= 0 || k <= 0 || k % blk || n > 0x7fffffff || k > 0x7fffffff || !y || !x) return hipErrorInvalidValue;
     if ((type == TYPE_Q6_K || type == TYPE_Q2_K) && !w.d) return hipErrorInvalidValue;
     if (w.ng != groups_of(type, k) || ((uintptr_t)x & 15) || !xa.norm) return hipErrorInvalidValue;
     const int ng = w.ng;
@@ -1093,21 +1094,26 @@ hipError_t launch_matvec2_rmsnorm(const WLayout &w1, int64_t n1, float *y1, cons
     if ((delta && ((uintptr_t)delta & 15)) || !norm || ((uintptr_t)norm & 15) || (xout && ((uintptr_t)xout & 15)))
         return hipErrorInvalidValue;
     // The two weights' outputs equal their single calls' bytes: both
-    // row-per-lane in one launch where the shapes allow, one launch each when
-    // only one of them takes that kernel, the general kernel for both otherwise.
+    // row-per-lane in one launch where the shapes allow, the general kernel
+    // for both in one launch for the type pairs instantiated below (Q4_K /
+    // Q6_K, and the Q5_0 / Q8_0 a Q4_K_M file holds for rows that are not
+    // whole 256-element groups), one launch each otherwise.
     auto kq = [](int t) { return t == TYPE_Q4_K || t == TYPE_Q6_K; };
-    if (!kq(w1.type) || !kq(w2.type) || k % QK_K || k / QK_K > PRE * NW) return hipErrorNotSupported;
+    auto q0 = [](int t) { return t == TYPE_Q5_0 || t == TYPE_Q8_0; };
+    const bool pair_k = kq(w1.type) && kq(w2.type), pair_0 = q0(w1.type) && q0(w2.type);
+    if (pair_k && (k % QK_K || k / QK_K > PRE * NW)) return hipErrorNotSupported;
     const bool r1 = rowlane_xf_applies(w1.type, n1, k, RL_XF_NORM), r2 = rowlane_xf_applies(w2.type, n2, k, RL_XF_NORM);
-    if (r1 && r2) {
+    if (r1 && r2 && pair_k) {
         const RlXf rx{RL_XF_NORM, delta, norm, eps, xout};
         const hipError_t e = launch_rowlane_matvec2(w1, n1, y1, w2, n2, y2, k, x, rx, s);
         if (e != hipErrorNotSupported) return e;
     }
-    if (r1 || r2) {
+    auto singles = [&]() {
         const hipError_t e = launch_matvec_rmsnorm(w1, n1, k, x, delta, norm, eps, xout, y1, s);
         if (e != hipSuccess) return e;
         return launch_matvec_rmsnorm(w2, n2, k, x, delta, norm, eps, nullptr, y2, s);
-    }
+    };
+    if (r1 || r2 || !(pair_k || pair_0)) return singles();
     XfArgs xa;
     xa.xf = XF_NORM;
     xa.delta = delta;
@@ -1118,12 +1124,20 @@ hipError_t launch_matvec2_rmsnorm(const WLayout &w1, int64_t n1, float *y1, cons
     int64_t g1, g2;
     size_t l1, l2;
     hipError_t e = norm_params(w1, n1, k, x, xa, y1, p1, g1, l1);
+    if (e == hipErrorNotSupported) return singles();
     if (e != hipSuccess) return e;
     xa.xout = nullptr;  // the residual is written once, by weight 1's workgroup 0
-    if ((e = norm_params(w2, n2, k, x, xa, y2, p2, g2, l2)) != hipSuccess) return e;
-    if (g1 + g2 > 0x7fffffff) return hipErrorNotSupported;
+    if ((e = norm_params(w2, n2, k, x, xa, y2, p2, g2, l2)) == hipErrorNotSupported) return singles();
+    if (e != hipSuccess) return e;
+    if (g1 + g2 > 0x7fffffff) return singles();
     const size_t lds = l1 > l2 ? l1 : l2;
     const int t1 = w1.type, t2 = w2.type;
+    if (pair_0) {
+        if (t1 == TYPE_Q5_0 && t2 == TYPE_Q8_0) return launch_two<TYPE_Q5_0, TYPE_Q8_0>(p1, p2, g1, g2, lds, s);
+        if (t1 == TYPE_Q5_0 && t2 == TYPE_Q5_0) return launch_two<TYPE_Q5_0, TYPE_Q5_0>(p1, p2, g1, g2, lds, s);
+        if (t1 == TYPE_Q8_0 && t2 == TYPE_Q8_0) return launch_two<TYPE_Q8_0, TYPE_Q8_0>(p1, p2, g1, g2, lds, s);
+        return launch_two<TYPE_Q8_0, TYPE_Q5_0>(p1, p2, g1, g2, lds, s);
+    }
     if (t1 == TYPE_Q4_K && t2 == TYPE_Q6_K) return launch_two<TYPE_Q4_K, TYPE_Q6_K>(p1, p2, g1, g2, lds, s);
     if (t1 == TYPE_Q4_K && t2 == TYPE_Q4_K) return launch_two<TYPE_Q4_K, TYPE_Q4_K>(p1, p2, g1, g2, lds, s);
     if (t1 == TYPE_Q6_K && t2 == TYPE_Q4_K) return launch_two<TYPE_Q6_K, TYPE_Q4_K>(p1, p2, g1, g2, lds, s);

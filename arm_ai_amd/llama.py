@@ -56,7 +56,6 @@ import numpy as np
 from . import synth
 from .qmatmul import Context, GgmlDType, QMatMul, QTensor
 
-_NORM2 = (GgmlDType.Q4K, GgmlDType.Q6K)  # types the two-weight fused-norm launch takes
 
 
 @dataclass
@@ -562,16 +561,13 @@ class Llama:
         delta = None
         for li, lw in enumerate(self.layers):
             an = self.attn_norm[li]
-            if "wqk" in lw and lw["wqk"].dtype in _NORM2 and lw["wv"].dtype in _NORM2:
-                # wq|wk and wv in one launch
+            if "wqk" in lw:
+                # wq|wk and wv: one launch for Q4_K / Q6_K and for Q5_0 / Q8_0 pairs
                 chk(L.aq_qmatmul2_rmsnorm_f32_device(c, lw["wqk"].handle, lw["wv"].handle, ptr(cur), delta, ptr(an),
                                                      eps, cfg.hidden, ptr(other), ptr(self._qk), ptr(self._v)))
             else:
-                if "wqk" in lw:
-                    mm_norm(lw["wqk"], cur, delta, an, ptr(self._qk), h_out=other)
-                else:
-                    mm_norm(lw["wq"], cur, delta, an, ptr(self._qk), h_out=other)
-                    mm_norm(lw["wk"], cur, delta, an, ptr(self._qk) + 4 * cfg.n_head * hd)
+                mm_norm(lw["wq"], cur, delta, an, ptr(self._qk), h_out=other)
+                mm_norm(lw["wk"], cur, delta, an, ptr(self._qk) + 4 * cfg.n_head * hd)
                 mm_norm(lw["wv"], cur, delta, an, ptr(self._v))
             chk(L.aq_llama_attn_decode(c, ptr(self._qk), ptr(self._v), ptr(self.cos), ptr(self.sin), ptr(self._pos),
                                        ptr(self.k_cache[li]), ptr(self.v_cache[li]), cfg.n_head, cfg.n_kv_head, hd,

@@ -323,10 +323,12 @@ int aq_qmatmul_rmsnorm_f32_device(aq_ctx *ctx, const aq_qweight *w, const float 
                                   const float *d_norm_w, float eps, int64_t k, float *d_h_out, float *d_dst);
 int aq_qmatmul_silu_mul_f32_device(aq_ctx *ctx, const aq_qweight *w, const float *d_gu, int64_t k, float *d_dst);
 /* Two aq_qmatmul_rmsnorm_f32_device calls on the same input (w1 -> d_dst1,
- * w2 -> d_dst2, both k columns, Q4_K or Q6_K) in one kernel launch, with the
- * same results as the two calls; d_h_out is written once.  For the
- * projections that share an input but not a type (TinyLlama Q4_K_M: wq|wk
- * and wv). */
+ * w2 -> d_dst2, both k columns) with the same results as the two calls;
+ * d_h_out is written once.  For the projections that share an input but not
+ * a type (TinyLlama Q4_K_M: wq|wk and wv).  One kernel launch for two Q4_K /
+ * Q6_K weights, and for two Q5_0 / Q8_0 weights (a Q4_K_M file's types for
+ * rows that are not whole 256-element groups, SmolLM-135M's 576); the two
+ * calls for other pairs. */
 int aq_qmatmul2_rmsnorm_f32_device(aq_ctx *ctx, const aq_qweight *w1, const aq_qweight *w2, const float *d_x,
                                    const float *d_delta, const float *d_norm_w, float eps, int64_t k, float *d_h_out,
                                    float *d_dst1, float *d_dst2);

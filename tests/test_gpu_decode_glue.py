@@ -410,6 +410,8 @@ def test_matvec_fused_rmsnorm_swiglu(env, wtype, n, k):
     (12, 4000, 2048, True, False),    # the 16-row form
     (8, 2048, 2048, False, False),    # Q8_0, the 8-row form
     (12, 200, 1024, False, True),     # below 256 rows: the general matvec, then argmax and embedding launches
+    (8, 49152, 576, True, False),     # SmolLM-135M's tied head (Q8_0, rows of 576): first maxima of 96 ranges
+    (6, 3000, 576, False, True),      # a Q5_0 head on the general matvec
 ])
 def test_head_argmax_embed(env, wtype, vocab, k, tie, alias):
     """aq_llama_head_argmax_embed against its three steps run apart (the
@@ -510,6 +512,10 @@ def test_matvec_fused_errors(env):
     (12, 2048, 14, 1536, 2048),  # both in 8-row workgroups: one launch
     (12, 2048, 12, 512, 4096),   # 8-row and 16-row forms: one launch each
     (12, 200, 14, 96, 1024),     # neither row-per-lane: the general two-weight kernel
+    (6, 768, 8, 192, 576),       # SmolLM-135M wq|wk (Q5_0) + wv (Q8_0), rows of 576: the general kernel, one launch
+    (6, 300, 6, 100, 576),       # two Q5_0 weights
+    (8, 200, 8, 64, 1024),       # two Q8_0 weights below 256 rows
+    (12, 2048, 8, 256, 2048),    # Q4_K with Q8_0: one launch each
 ])
 def test_matvec2_fused_rmsnorm_equals_two_calls(env, t1, n1, t2, n2, k):
     """The two-weight call gives the bytes the two single calls give."""
@@ -539,11 +545,10 @@ def test_matvec2_fused_rmsnorm_equals_two_calls(env, t1, n1, t2, n2, k):
     o = [t.cpu().numpy() for t in outs]
     assert np.array_equal(o[0], o[2]) and np.array_equal(o[1], o[3])
     assert np.array_equal(h1.cpu().numpy(), h2.cpu().numpy())
-    # a Q8_0 weight is not taken by the two-weight launch
-    _, m3 = _weight(A, S, 8, 64, k, ctx, seed=3)
-    assert L.aq_qmatmul2_rmsnorm_f32_device(ctx.handle, m1.handle, m3.handle, x.data_ptr(), None, wn.data_ptr(), eps,
-                                            k, None, outs[0].data_ptr(), outs[1].data_ptr()) == lib.AQ_ERR_SHAPE
-    for mm in (m1, m2, m3):
+    # a k the weights do not have
+    assert L.aq_qmatmul2_rmsnorm_f32_device(ctx.handle, m1.handle, m2.handle, x.data_ptr(), None, wn.data_ptr(), eps,
+                                            k + 32, None, outs[0].data_ptr(), outs[1].data_ptr()) == lib.AQ_ERR_SHAPE
+    for mm in (m1, m2):
         mm.free()
 
 
