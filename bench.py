@@ -360,7 +360,12 @@ def measure_decode(ctx, model_name, n_prompt, n_new, seed, with_cpu=True):
         "eager_decode_tok_s": round(1e3 / est["decode_ms_per_tok"], 1),
         "matmul_weight_bytes_per_token": int(wbytes),
         "weight_GBps_at_decode": round(wbytes / (st["decode_ms_per_tok"] / 1e3) / 1e9, 1),
-        "graph_and_eager_tokens_agree": res.tokens[:16] == eager.tokens,
+        # greedy paths on random weights part where a top-2 logit margin is
+        # below the graph step's rounding difference from the eager step
+        # (tests/test_llama_fullsize.py holds them teacher-forced to the margin)
+        "graph_eager_tokens_equal_before": next(
+            (i for i, (a, b) in enumerate(zip(res.tokens, eager.tokens)) if a != b), len(eager.tokens)),
+        "graph_eager_tokens_compared": len(eager.tokens),
         "timing": "wall clock around generate (llama_candle.rs:80-139 points); decode step replayed from a HIP graph",
     }
     if cpu is not None:
