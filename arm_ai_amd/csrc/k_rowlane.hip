@@ -22,7 +22,9 @@
 // every wavefront issues its first P weight pieces, then those wavefronts
 // quantise four blocks of 256 each (Q8_K, or eight Q8_0 blocks of 32 for the
 // Q8_0 / Q4_0 / Q5_0 weights; 16 lanes per 256, 16 elements per lane) into
-// LDS while the weight pieces are in flight.
+// LDS while the weight pieces are in flight.  The 8-wavefront form with an
+// f32 input instead quantises one block per wavefront (4 elements per lane),
+// so that all four SIMDs take part.
 // After one barrier each wavefront walks its pieces in order, keeping P of
 // them in flight (compute piece j, issue piece j + P): a wavefront never
 // waits at the barrier behind its own blocked load issues, and the dot
@@ -191,36 +193,44 @@ __device__ __forceinline__ void rl_body(const RlParams p, const int bid, const i
     auto issue = [&](int j) { issue_in(cur, j, true); };
 
     // 1. the activation's loads: wavefront w < ceil(ng / 4) stages blocks
-    //    4w .. 4w + 3, 16 lanes (s = lane & 15) per block; then (EARLY) this
+    //    4w .. 4w + 3, 16 lanes (s = lane & 15) per block, or (WIDE: an f32
+    //    input in a form with a wavefront for every block) wavefront w < ng
+    //    block w, lane l its elements 4l .. 4l + 3; then (EARLY) this
     //    wavefront's first P weight pieces, so that they are in flight while
     //    the activation is quantised (the loads are waited for in issue
     //    order).  With most wavefronts quantising (the 16-wavefront form),
     //    issuing only the first piece before the quantisation and the rest
     //    after it measured faster than either all before or all after.
+    //    WIDE is the 8-wavefront form only, where the 16-lane quantisers would
+    //    leave two of the four SIMDs idle; in the 16-wavefront form the four
+    //    16-lane quantisers already take one SIMD each, and 64-lane blocks
+    //    measured slower there (the headline 7.5 against 6.7 us).
+    constexpr bool WIDE = FUSED && R == RL_ROWS && GPW == 1 && W == 8;  // the host picks W >= ng for these
+    constexpr int NV = WIDE ? 4 : 16;  // activation values per lane
     const int s = lane & 15;
-    const int gb = 4 * wave + (lane >> 4);
-    const bool quantiser = wave < (p.ng + 3) / 4;  // uniform
+    const int gb = WIDE ? wave : 4 * wave + (lane >> 4);
+    const bool quantiser = WIDE ? wave < p.ng : wave < (p.ng + 3) / 4;  // uniform
     const bool gbok = gb < p.ng;
     u32x4 xv[4], dv[4], nv[4];
     uint32_t xbs = 0, xdb = 0;
-    const uint32_t xo = gbok ? (uint32_t)((gb * QK_K + 16 * s) * 4) : BUF_OOB;
+    const uint32_t xo = gbok ? (uint32_t)((gb * QK_K + (WIDE ? 4 * lane : 16 * s)) * 4) : BUF_OOB;
     if (quantiser) {
         if (FUSED) {
             const rsrc_t rx = buf_rsrc(p.x, (uint32_t)(p.k * 4));
 #pragma unroll
-            for (int i = 0; i < 4; i++) xv[i] = __builtin_amdgcn_raw_buffer_load_b128(rx, xo + 16 * i, 0, 0);
+            for (int i = 0; i < NV / 4; i++) xv[i] = __builtin_amdgcn_raw_buffer_load_b128(rx, xo + 16 * i, 0, 0);
             if (NORM) {  // a null delta: an empty range, zeros
                 const rsrc_t rdl = buf_rsrc(p.xdelta, p.xdelta ? (uint32_t)(p.k * 4) : 0u);
                 const rsrc_t rnw = buf_rsrc(p.xnorm, (uint32_t)(p.k * 4));
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
+                for (int i = 0; i < NV / 4; i++) {
                     dv[i] = __builtin_amdgcn_raw_buffer_load_b128(rdl, xo + 16 * i, 0, 0);
                     nv[i] = __builtin_amdgcn_raw_buffer_load_b128(rnw, xo + 16 * i, 0, 0);
                 }
             } else if (SILU) {  // u = the second half of x
                 const rsrc_t ru = buf_rsrc(p.x + p.k, (uint32_t)(p.k * 4));
 #pragma unroll
-                for (int i = 0; i < 4; i++) dv[i] = __builtin_amdgcn_raw_buffer_load_b128(ru, xo + 16 * i, 0, 0);
+                for (int i = 0; i < NV / 4; i++) dv[i] = __builtin_amdgcn_raw_buffer_load_b128(ru, xo + 16 * i, 0, 0);
             }
         } else {
             const rsrc_t rq = buf_rsrc(p.act.qs, (uint32_t)p.k);
@@ -242,10 +252,10 @@ __device__ __forceinline__ void rl_body(const RlParams p, const int bid, const i
     //    NORM: h = x + delta and the row's sum of squares first (every
     //    wavefront takes the barrier; lanes past the row hold zeros), then
     //    (h * (1 / sqrt(mean(h^2) + eps))) * w is quantised.
-    float v[16];
+    float v[NV];
     if (FUSED && quantiser) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
+        for (int i = 0; i < NV / 4; i++) {
             v[4 * i] = u32_as_f32(xv[i].x);
             v[4 * i + 1] = u32_as_f32(xv[i].y);
             v[4 * i + 2] = u32_as_f32(xv[i].z);
@@ -253,46 +263,51 @@ __device__ __forceinline__ void rl_body(const RlParams p, const int bid, const i
         }
     }
     if (SILU && quantiser) {
-        const float uv[16] = {u32_as_f32(dv[0].x), u32_as_f32(dv[0].y), u32_as_f32(dv[0].z), u32_as_f32(dv[0].w),
-                              u32_as_f32(dv[1].x), u32_as_f32(dv[1].y), u32_as_f32(dv[1].z), u32_as_f32(dv[1].w),
-                              u32_as_f32(dv[2].x), u32_as_f32(dv[2].y), u32_as_f32(dv[2].z), u32_as_f32(dv[2].w),
-                              u32_as_f32(dv[3].x), u32_as_f32(dv[3].y), u32_as_f32(dv[3].z), u32_as_f32(dv[3].w)};
+        float uv[NV];
 #pragma unroll
-        for (int i = 0; i < 16; i++) v[i] = (v[i] / (1.0f + expf(-v[i]))) * uv[i];
+        for (int i = 0; i < NV / 4; i++) {
+            uv[4 * i] = u32_as_f32(dv[i].x);
+            uv[4 * i + 1] = u32_as_f32(dv[i].y);
+            uv[4 * i + 2] = u32_as_f32(dv[i].z);
+            uv[4 * i + 3] = u32_as_f32(dv[i].w);
+        }
+#pragma unroll
+        for (int i = 0; i < NV; i++) v[i] = (v[i] / (1.0f + expf(-v[i]))) * uv[i];
     }
     if (NORM) {
         float ss = 0.0f;
         if (quantiser) {
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
+            for (int i = 0; i < NV / 4; i++) {
                 v[4 * i] += u32_as_f32(dv[i].x);
                 v[4 * i + 1] += u32_as_f32(dv[i].y);
                 v[4 * i + 2] += u32_as_f32(dv[i].z);
                 v[4 * i + 3] += u32_as_f32(dv[i].w);
             }
 #pragma unroll
-            for (int i = 0; i < 16; i++) ss = __builtin_fmaf(v[i], v[i], ss);
+            for (int i = 0; i < NV; i++) ss = __builtin_fmaf(v[i], v[i], ss);
 #pragma unroll
             for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
             if (lane == 0) nred[wave] = ss;
         }
         lds_barrier();
         if (quantiser) {
-            const int nq = (p.ng + 3) / 4;
+            const int nq = WIDE ? p.ng : (p.ng + 3) / 4;
             float tot = 0.0f;
             for (int w2 = 0; w2 < nq; w2++) tot += nred[w2];
             const float mden = sqrtf(tot / (float)p.k + p.eps);
             if (p.xout && bid == 0 && gbok) {  // the residual stream x + delta
 #pragma unroll
-                for (int i = 0; i < 4; i++)
-                    *(float4 *)(p.xout + gb * QK_K + 16 * s + 4 * i) = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
+                for (int i = 0; i < NV / 4; i++)
+                    *(float4 *)(p.xout + gb * QK_K + (WIDE ? 4 * lane : 16 * s) + 4 * i) =
+                        make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
             }
             // candle's h / m as h * (1 / m): one division per lane, not 16
             // (within one rounding of the quotient; the reordered sum of
             // squares already moves m by as much)
             const float rm = 1.0f / mden;
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
+            for (int i = 0; i < NV / 4; i++) {
                 v[4 * i] = (v[4 * i] * rm) * u32_as_f32(nv[i].x);
                 v[4 * i + 1] = (v[4 * i + 1] * rm) * u32_as_f32(nv[i].y);
                 v[4 * i + 2] = (v[4 * i + 2] * rm) * u32_as_f32(nv[i].z);
@@ -300,7 +315,37 @@ __device__ __forceinline__ void rl_body(const RlParams p, const int bid, const i
             }
         }
     }
-    if (quantiser) {
+    if constexpr (WIDE) {
+        if (quantiser) {
+            // lane l: quants 4l .. 4l + 3 of block gb; the 8 lanes of a 32-element
+            // sub-block (a Q8_0 block) are one half-row, the 4 of a 16-element one a quad
+            if (A80) {
+                uint16_t d16;
+                const uint32_t qv = q8_0_block_8lanes(v, &d16);
+                int bsum = sdot4((int)qv, 0x01010101, 0);
+                bsum += dpp_i<DPP_QUAD_XOR1>(bsum);
+                bsum += dpp_i<DPP_QUAD_XOR2>(bsum);
+                bsum += dpp_i<DPP_HALF_MIRROR>(bsum);
+                *(uint32_t *)&xq[gb][4 * lane] = qv;
+                if ((lane & 7) == 0) {
+                    xd8[gb][lane >> 3] = f16_bits_to_f32(d16);
+                    if (Q40 || Q50) xb8[gb][lane >> 3] = bsum;
+                }
+            } else {
+                int bsum;  // this quad's 16 quants
+                float d;
+                const uint32_t qv = q8k_block_wave(v, lane, &bsum, &d);
+                const int pair = bsum + dpp_i<DPP_HALF_MIRROR>(bsum);  // and the other quad of the half-row
+                *(uint32_t *)&xq[gb][4 * lane] = qv;
+                if (B16) {
+                    if ((lane & 3) == 0) xb[gb][lane >> 2] = bsum;
+                } else if ((lane & 7) == 0) {
+                    xb[gb][lane >> 3] = pair;
+                }
+                if (lane == 0) xd[gb] = d;
+            }
+        }
+    } else if (quantiser) {
         uint4 qv;
         int bsum;
         float d;
@@ -705,6 +750,9 @@ hipError_t launch_g(const RlParams &p, unsigned grid, bool fused, bool dump, hip
     // one workgroup per chunk (persistent: at most one per chunk), never a
     // workgroup past the weight's rows
     if (!rl::grid_ok(R, p.n, grid, CH)) return hipErrorInvalidValue;
+    // one group per wavefront: a wavefront for every group (the f32-input
+    // forms quantise block w in wavefront w)
+    if (R == RL_ROWS && GPW == 1 && p.ng > W) return hipErrorInvalidValue;
     if (p.xf == RL_XF_NORM) {  // input transforms: f32 input, no dump (the caller checks)
         rl_kernel<TYPE, R, W, GPW, P, EARLY, true, false, CH, RL_XF_NORM><<<grid, W * 64, 0, s>>>(p);
         return hipGetLastError();

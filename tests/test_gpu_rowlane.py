@@ -389,3 +389,33 @@ def test_rowlane16_and_general_matvec_agree(ctx):
     assert float(np.abs(yb[:, :n2] - ys).max()) <= 1e-4 * float(np.abs(ys).max())
     big.free()
     small.free()
+
+
+@pytest.mark.parametrize("typ", [S.TYPE_Q4_K, S.TYPE_Q6_K, S.TYPE_Q4_0, S.TYPE_Q5_0])
+def test_rowlane8w_edge_activations(ctx, typ):
+    """The edge rows of the quantizer, plus ties of |x| across lanes (the
+    first index wins) and within a Q8_0 block, through the 8-wavefront
+    56-row form, whose prologue quantises one block per wavefront with four
+    elements per lane (Q8_K: 64 lanes per block; Q8_0: eight per block):
+    integer sums bit-exact, outputs within 1e-5."""
+    n, k = RL_MIN_N, 2048  # 200 workgroups of 56 rows, 8 groups: one per wavefront
+    W = S.make_weight(typ, n, k, seed=80 + typ)
+    mm = A.QMatMul.from_qtensor(A.QTensor(W.type, (W.n, W.k), W.blocks), ctx)
+    extra = np.zeros((2, k), np.float32)
+    extra[0, 256 + 7], extra[0, 256 + 8], extra[0, 256 + 200] = -3.0, 3.0, 3.0  # lanes 1, 2, 50 of block 1
+    extra[1, 512 + 33], extra[1, 512 + 62] = 2.0, -2.0                        # one Q8_0 block, two lanes
+    qtype = O.Q8_0 if typ in (S.TYPE_Q4_0, S.TYPE_Q5_0) else O.Q8_K
+    for x in np.concatenate([_edge_rows(k), extra]):
+        x = x[None, :]
+        xq = O.quantize(x, qtype)
+        gS, gSm = mm.block_sums(x)
+        oS, oSm = O.block_sums(W.type, k, W.blocks, xq)
+        assert np.array_equal(gS, oS) and np.array_equal(gSm, oSm)
+        y = mm.forward(x)
+        r = O.matmul_preq(W.type, xq, W.blocks, W.n, k)
+        ok = np.isfinite(r)
+        assert np.array_equal(np.isfinite(y), ok)
+        if ok.any():
+            scale = max(float(np.abs(r[ok]).max()), 1e-30)
+            assert float(np.abs(y[ok] - r[ok]).max()) / scale <= 1e-5
+    mm.free()
