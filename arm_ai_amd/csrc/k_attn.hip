@@ -113,51 +113,94 @@ __global__ __launch_bounds__(SPL_THREADS) void attn_split_kernel(
 
     const int s = blockIdx.x, kvh = blockIdx.y, tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
+    const int c = lane % HD4, d4 = tid % HD4, g = tid / HD4;
+    float *kh = kc + (int64_t)kvh * max_seq * hd;
+    float *vh = vc + (int64_t)kvh * max_seq * hd;
+
+    // Loads whose addresses do not depend on pos go out together with the
+    // position load: q's values, the new k's and v's, and -- when the S
+    // slices of SPL_MIN_LEN cover max_seq, so that slice s is positions
+    // [SPL_MIN_LEN s, SPL_MIN_LEN (s + 1)) at every pos -- the cached rows of
+    // the slice's first SPL_MIN_LEN positions (those at or past pos are
+    // zeroed once pos is known).  Otherwise those rows are loaded after it.
+    constexpr int QN = (REP * hd / 2 + SPL_THREADS - 1) / SPL_THREADS;  // q pairs per thread
+    static_assert(hd / 2 + hd <= SPL_THREADS, "one of the new k's pairs or v's values per thread");
+    float qa[QN], qb[QN];
+#pragma unroll
+    for (int u = 0; u < QN; u++) {
+        const int i = tid + u * SPL_THREADS, hh = i / (hd / 2), j = i % (hd / 2);
+        const float *q0 = qk + (int64_t)(kvh * REP + hh) * hd;
+        qa[u] = i < REP * hd / 2 ? q0[2 * j] : 0.0f;
+        qb[u] = i < REP * hd / 2 ? q0[2 * j + 1] : 0.0f;
+    }
+    float na = 0.0f, nb = 0.0f;  // thread t < hd / 2: the new k's pair t; t < hd / 2 + hd: v's value t - hd / 2
+    {
+        const float *k0 = qk + (int64_t)n_head * hd + (int64_t)kvh * hd;
+        if (tid < hd / 2) {
+            na = k0[2 * tid];
+            nb = k0[2 * tid + 1];
+        } else if (tid < hd / 2 + hd) {
+            na = v[(int64_t)kvh * hd + tid - hd / 2];
+        }
+    }
+    const bool fixed = (int64_t)SPL_MIN_LEN * S >= max_seq;  // uniform
+    float4 kv0[KU], vp[VU];
+    if (fixed) {
+        const int pf = s * SPL_MIN_LEN;
+#pragma unroll
+        for (int u = 0; u < KU; u++) {
+            const int p = pf + u * RPP + wave * RPI + lane / HD4;
+            kv0[u] = p < max_seq ? ((const float4 *)(kh + (int64_t)p * hd))[c] : ZERO4;
+        }
+#pragma unroll
+        for (int u = 0; u < VU; u++) {
+            const int p = pf + g + u * G;
+            vp[u] = p < max_seq ? *(const float4 *)(vh + (int64_t)p * hd + 4 * d4) : ZERO4;
+        }
+    }
+
     const int pos = (int)*d_pos;
     if (pos < 0 || pos >= max_seq) return;  // the host checks; this never indexes out of the cache
     const int n = pos + 1;
     int len, ns;
     split_shape(n, S, len, ns);
     if (s >= ns) return;
-    float *kh = kc + (int64_t)kvh * max_seq * hd;
-    float *vh = vc + (int64_t)kvh * max_seq * hd;
     float *pw = part + ((int64_t)kvh * S + s) * PSTR;
-    const int p0 = s * len, np = min(p0 + len, n) - p0;
+    const int p0 = s * len, np = min(p0 + len, n) - p0;  // (fixed: len = SPL_MIN_LEN, p0 = pf)
     const bool has_pos = p0 + np == n;
-    const int c = lane % HD4, d4 = tid % HD4, g = tid / HD4;
 
-    // the cached rows of the slice's first SPL_MIN_LEN positions: their
-    // addresses depend only on pos, so they are in flight while q and k rotate
-    float4 kv0[KU], vp[VU];
+    // the cached rows of the slice's first SPL_MIN_LEN positions (before pos
+    // only): in flight while q and k rotate
 #pragma unroll
     for (int u = 0; u < KU; u++) {
         const int i = u * RPP + wave * RPI + lane / HD4, p = p0 + i;
-        kv0[u] = i < np && p < pos ? ((const float4 *)(kh + (int64_t)p * hd))[c] : ZERO4;
+        if (!fixed) kv0[u] = i < np && p < pos ? ((const float4 *)(kh + (int64_t)p * hd))[c] : ZERO4;
+        else if (!(i < np && p < pos)) kv0[u] = ZERO4;
     }
 #pragma unroll
     for (int u = 0; u < VU; u++) {
         const int i = g + u * G, p = p0 + i;
-        vp[u] = i < np && p < pos ? *(const float4 *)(vh + (int64_t)p * hd + 4 * d4) : ZERO4;
+        if (!fixed) vp[u] = i < np && p < pos ? *(const float4 *)(vh + (int64_t)p * hd + 4 * d4) : ZERO4;
+        else if (!(i < np && p < pos)) vp[u] = ZERO4;
     }
 
     const float *cr = cosb + (int64_t)pos * (hd / 2), *sr = sinb + (int64_t)pos * (hd / 2);
-    for (int i = tid; i < REP * hd / 2; i += SPL_THREADS) {
-        const int hh = i / (hd / 2), j = i % (hd / 2);
-        const float *q0 = qk + (int64_t)(kvh * REP + hh) * hd;
-        const float a = q0[2 * j], b = q0[2 * j + 1], cc = cr[j], sn = sr[j];
-        qs[hh * hd + 2 * j] = a * cc - b * sn;
-        qs[hh * hd + 2 * j + 1] = a * sn + b * cc;
+#pragma unroll
+    for (int u = 0; u < QN; u++) {
+        const int i = tid + u * SPL_THREADS, hh = i / (hd / 2), j = i % (hd / 2);
+        if (i < REP * hd / 2) {
+            const float a = qa[u], b = qb[u], cc = cr[j], sn = sr[j];
+            qs[hh * hd + 2 * j] = a * cc - b * sn;
+            qs[hh * hd + 2 * j + 1] = a * sn + b * cc;
+        }
     }
     if (has_pos) {  // k's hd / 2 rotated pairs, then v's hd values
-        const float *k0 = qk + (int64_t)n_head * hd + (int64_t)kvh * hd;
-        for (int t = tid; t < hd / 2 + hd; t += SPL_THREADS) {
-            if (t < hd / 2) {
-                const float a = k0[2 * t], b = k0[2 * t + 1], cc = cr[t], sn = sr[t];
-                ks[2 * t] = a * cc - b * sn;
-                ks[2 * t + 1] = a * sn + b * cc;
-            } else {
-                vs[t - hd / 2] = v[(int64_t)kvh * hd + t - hd / 2];
-            }
+        if (tid < hd / 2) {
+            const float a = na, b = nb, cc = cr[tid], sn = sr[tid];
+            ks[2 * tid] = a * cc - b * sn;
+            ks[2 * tid + 1] = a * sn + b * cc;
+        } else if (tid < hd / 2 + hd) {
+            vs[tid - hd / 2] = na;
         }
     }
     __syncthreads();
