@@ -230,7 +230,11 @@ class Llama:
     """ModelWeights on one MI355X: quantized projections in HBM (this library),
     f32 embedding / norms / KV cache as torch tensors on the same device."""
 
-    def __init__(self, ctx: Context, hw: HostWeights):
+    RESERVE_TOKENS = 512  # the prompt length whose buffers a new model reserves (llama.cpp's default micro-batch)
+
+    def __init__(self, ctx: Context, hw: HostWeights, reserve: int | None = None):
+        """reserve: prompt length whose buffers are reserved here (see
+        reserve()); None takes min(max_seq, RESERVE_TOKENS), 0 none."""
         import torch
 
         self.torch = torch
@@ -273,6 +277,24 @@ class Llama:
         self._trace = None  # (rows, full layers, records) while trace_matmuls is active
         self._trace_layer = -1
         self._hidden = None  # {layer index: residual input} while capture_hidden is active
+        self.reserve(min(cfg.max_seq, self.RESERVE_TOKENS) if reserve is None else reserve)
+
+    def reserve(self, n: int) -> None:
+        """Make the buffers of a prompt of up to n tokens exist before the
+        first real one, as llama.cpp reserves its compute buffers when a
+        context is created: one forward of n tokens at offset 0 (torch keeps
+        the blocks it allocates on this stream, the context keeps its grown
+        scratch), then the KV cache is cleared.  Without it the first prompt
+        of a new length pays for those allocations (torch's new segments,
+        and the scratch's synchronise, free and larger allocation)."""
+        n = min(int(n), self.cfg.max_seq)
+        if n <= 0:
+            return
+        self.forward([0] * n, 0)
+        with self.torch.cuda.stream(self.stream):
+            self.k_cache.zero_()
+            self.v_cache.zero_()
+        self.ctx.synchronize()
 
     def _upload_layer(self, layer: dict[str, QTensor]) -> dict[str, QMatMul]:
         """The layer's projections in HBM; when a pair has one type, one weight
@@ -604,9 +626,16 @@ class Llama:
             self._set_token(0, self.cfg.max_seq - 1)
             self._decode_step_static()
         self.ctx.synchronize()
+        # (capture_begin / capture_end rather than the torch.cuda.graph
+        #  context, which empties torch's block cache on entry and so would
+        #  release the prompt buffers reserve() set aside)
         g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g, stream=self.stream):
-            self._decode_step_static()
+        with torch.cuda.stream(self.stream):
+            g.capture_begin()
+            try:
+                self._decode_step_static()
+            finally:
+                g.capture_end()
         self._graph = g
         self._leave()
 

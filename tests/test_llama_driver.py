@@ -297,6 +297,34 @@ def test_generate_streams_each_token_before_the_next_step(tiny):
     assert seen == eager[:1]
 
 
+def test_reserve_leaves_no_trace(tiny):
+    """Llama reserves a prompt's buffers at construction (one forward of
+    min(max_seq, 512) tokens at offset 0, then the KV cache cleared): a model
+    built without it gives the same logits and tokens, bit for bit, and the
+    reserving model's cache starts at zero."""
+    import arm_ai_amd as A
+    from arm_ai_amd.llama import Llama
+
+    hw, model = tiny
+    rng = np.random.default_rng(41)
+    prompt = rng.integers(0, hw.cfg.vocab, size=20).tolist()
+    ctx = A.Context(0)
+    fresh = Llama(ctx, hw, reserve=0)
+    try:
+        reserved = Llama(ctx, hw)
+        try:
+            assert float(reserved.k_cache.abs().sum()) == 0.0 and float(reserved.v_cache.abs().sum()) == 0.0
+            a = reserved.forward(prompt, 0).cpu().numpy()
+            b = fresh.forward(prompt, 0).cpu().numpy()
+            assert np.array_equal(a, b)
+            assert reserved.generate(prompt, 5).tokens == fresh.generate(prompt, 5).tokens
+        finally:
+            reserved.free()
+    finally:
+        fresh.free()
+        ctx.close()
+
+
 # ------------------------------------------------------------ SmolLM-135M shape
 def test_swiglu_pair_rows_interleaves_gate_and_up_rows_in_fours():
     """Row 8b + j of the paired weight is gate row 4b + j (j < 4) or up row
