@@ -283,7 +283,7 @@ pub fn load_model_on(path: &str, device: i32, max_seq: usize) -> Result<LlamaRes
         }
     }
     let cache_bytes = cfg.n_layer * cfg.n_kv * max_seq * hd * 4;
-    let model = GpuLlama {
+    let mut model = GpuLlama {
         layers,
         output,
         tok_emb,
@@ -299,6 +299,11 @@ pub fn load_model_on(path: &str, device: i32, max_seq: usize) -> Result<LlamaRes
         cfg,
         ctx,
     };
+    // a prompt's buffers up front (llama.cpp reserves its compute buffers at
+    // context creation), so that the first prompt of up to 512 tokens does
+    // not allocate
+    let reserve = model.cfg.max_seq.min(512);
+    model.prompt_bufs(reserve)?;
     Ok(LlamaResource { model: Mutex::new(model) })
 }
 
