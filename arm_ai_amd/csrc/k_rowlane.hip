@@ -99,7 +99,7 @@ struct RlParams {
 //
 // The body takes its workgroup index bid of nblk, so that one launch can run
 // two weights' matvecs on the same input (rl2_kernel).
-template <int TYPE, int R, int W, int GPW, int P, bool EARLY, bool FUSED, bool DUMP, bool CH, int XF>
+template <int TYPE, int R, int W, int GPW, int P, bool EARLY, bool FUSED, bool DUMP, bool CH, int XF, bool WQ>
 __device__ __forceinline__ void rl_body(const RlParams p, const int bid, const int nblk) {
     constexpr bool NORM = XF == RL_XF_NORM, SILU = XF == RL_XF_SILU;
     static_assert(XF == RL_XF_NONE || (FUSED && !DUMP), "input transforms take an f32 input and no integer dump");
@@ -194,18 +194,21 @@ __device__ __forceinline__ void rl_body(const RlParams p, const int bid, const i
 
     // 1. the activation's loads: wavefront w < ceil(ng / 4) stages blocks
     //    4w .. 4w + 3, 16 lanes (s = lane & 15) per block, or (WIDE: an f32
-    //    input in a form with a wavefront for every block) wavefront w < ng
-    //    block w, lane l its elements 4l .. 4l + 3; then (EARLY) this
+    //    input in a form launched with a wavefront for every block, WQ)
+    //    wavefront w < ng block w, lane l its elements 4l .. 4l + 3; then (EARLY) this
     //    wavefront's first P weight pieces, so that they are in flight while
     //    the activation is quantised (the loads are waited for in issue
     //    order).  With most wavefronts quantising (the 16-wavefront form),
     //    issuing only the first piece before the quantisation and the rest
     //    after it measured faster than either all before or all after.
-    //    WIDE is the 8-wavefront form only, where the 16-lane quantisers would
-    //    leave two of the four SIMDs idle; in the 16-wavefront form the four
-    //    16-lane quantisers already take one SIMD each, and 64-lane blocks
-    //    measured slower there (the headline 7.5 against 6.7 us).
-    constexpr bool WIDE = FUSED && R == RL_ROWS && GPW == 1 && W == 8;  // the host picks W >= ng for these
+    //    WQ is taken by the 8-wavefront 56-row form (rows of up to 8
+    //    groups), where 16-lane quantisers would leave two of the four SIMDs
+    //    idle; in the 16-wavefront form the four 16-lane quantisers already
+    //    take one SIMD each, and 64-lane blocks measured slower there (the
+    //    headline 7.5 against 6.7 us), as did eight such wavefronts in place
+    //    of two in the 16- and 8-row forms.
+    static_assert(!WQ || GPW == 1, "one block per wavefront: one group per wavefront");
+    constexpr bool WIDE = FUSED && WQ;  // the host checks ng <= W
     constexpr int NV = WIDE ? 4 : 16;  // activation values per lane
     const int s = lane & 15;
     const int gb = WIDE ? wave : 4 * wave + (lane >> 4);
@@ -416,9 +419,12 @@ __device__ __forceinline__ void rl_body(const RlParams p, const int bid, const i
     // (Q4_K, Q5_K, Q2_K) the min sum and (dmin_w * d_x) * smin
     int smin = 0;
     float dwdx = 0.0f, fmin = 0.0f;
-    // (persistent: a wavefront without a group skips the walk as a whole, so
-    //  the pieces in flight across chunks have one path through it)
-    if (!CH || group_of(0) < p.ng) {  // uniform
+    // (a wavefront without a group -- those that only quantise, e.g. three of
+    //  the six at 22 groups in the 8-row form -- skips the walk as a whole:
+    //  its out-of-range loads and zero sums cost w2 of the decode step about
+    //  0.4-1.0 us; persistent, the pieces in flight across chunks then have
+    //  one path through it)
+    if (wave * GP < p.ng) {  // uniform: the wavefront's first group (its phase 0)
     #pragma unroll
         for (int j = 0; j < NP; j++) {
             const int pc = j % NPG;
@@ -727,9 +733,10 @@ __device__ __forceinline__ void rl_body(const RlParams p, const int bid, const i
     }
 }
 
-template <int TYPE, int R, int W, int GPW, int P, bool EARLY, bool FUSED, bool DUMP, bool CH = false, int XF = RL_XF_NONE>
+template <int TYPE, int R, int W, int GPW, int P, bool EARLY, bool FUSED, bool DUMP, bool CH = false, int XF = RL_XF_NONE,
+          bool WQ = false>
 __global__ __launch_bounds__(W * 64) void rl_kernel(RlParams p) {
-    rl_body<TYPE, R, W, GPW, P, EARLY, FUSED, DUMP, CH, XF>(p, (int)blockIdx.x, (int)gridDim.x);
+    rl_body<TYPE, R, W, GPW, P, EARLY, FUSED, DUMP, CH, XF, WQ>(p, (int)blockIdx.x, (int)gridDim.x);
 }
 
 // Two weights on the same f32 input in one launch (the decode step's wq|wk
@@ -737,33 +744,33 @@ __global__ __launch_bounds__(W * 64) void rl_kernel(RlParams p) {
 // the form of R (16 or 8) rows with W wavefronts (their LDS is separate).
 // A wavefront past the groups adds 0 to its rows, so W wavefronts give the
 // same sums as a single weight's launch with fewer.
-template <int T1, int T2, int R, int W, int XF>
+template <int T1, int T2, int R, int W, int XF, bool WQ>
 __global__ __launch_bounds__(W * 64) void rl2_kernel(RlParams p1, RlParams p2, int g1) {
     constexpr int P1 = T1 == TYPE_Q6_K ? 13 : 9, P2 = T2 == TYPE_Q6_K ? 13 : 9;
     const int bid = (int)blockIdx.x;
-    if (bid < g1) rl_body<T1, R, W, 1, P1, true, true, false, false, XF>(p1, bid, g1);  // uniform
-    else rl_body<T2, R, W, 1, P2, true, true, false, false, XF>(p2, bid - g1, (int)gridDim.x - g1);
+    if (bid < g1) rl_body<T1, R, W, 1, P1, true, true, false, false, XF, WQ>(p1, bid, g1);  // uniform
+    else rl_body<T2, R, W, 1, P2, true, true, false, false, XF, WQ>(p2, bid - g1, (int)gridDim.x - g1);
 }
 
-template <int TYPE, int R, int W, int GPW, int P, bool EARLY, bool CH = false>
+template <int TYPE, int R, int W, int GPW, int P, bool EARLY, bool CH = false, bool WQ = false>
 hipError_t launch_g(const RlParams &p, unsigned grid, bool fused, bool dump, hipStream_t s) {
     // one workgroup per chunk (persistent: at most one per chunk), never a
     // workgroup past the weight's rows
     if (!rl::grid_ok(R, p.n, grid, CH)) return hipErrorInvalidValue;
-    // one group per wavefront: a wavefront for every group (the f32-input
-    // forms quantise block w in wavefront w)
-    if (R == RL_ROWS && GPW == 1 && p.ng > W) return hipErrorInvalidValue;
+    // one group per wavefront: a wavefront for every group; WQ: a wavefront
+    // for every block (an f32 input is quantised block w in wavefront w)
+    if (((R == RL_ROWS && GPW == 1) || WQ) && p.ng > W) return hipErrorInvalidValue;
     if (p.xf == RL_XF_NORM) {  // input transforms: f32 input, no dump (the caller checks)
-        rl_kernel<TYPE, R, W, GPW, P, EARLY, true, false, CH, RL_XF_NORM><<<grid, W * 64, 0, s>>>(p);
+        rl_kernel<TYPE, R, W, GPW, P, EARLY, true, false, CH, RL_XF_NORM, WQ><<<grid, W * 64, 0, s>>>(p);
         return hipGetLastError();
     }
     if (p.xf == RL_XF_SILU) {
-        rl_kernel<TYPE, R, W, GPW, P, EARLY, true, false, CH, RL_XF_SILU><<<grid, W * 64, 0, s>>>(p);
+        rl_kernel<TYPE, R, W, GPW, P, EARLY, true, false, CH, RL_XF_SILU, WQ><<<grid, W * 64, 0, s>>>(p);
         return hipGetLastError();
     }
     if (fused) {
-        if (dump) rl_kernel<TYPE, R, W, GPW, P, EARLY, true, true, CH><<<grid, W * 64, 0, s>>>(p);
-        else rl_kernel<TYPE, R, W, GPW, P, EARLY, true, false, CH><<<grid, W * 64, 0, s>>>(p);
+        if (dump) rl_kernel<TYPE, R, W, GPW, P, EARLY, true, true, CH, RL_XF_NONE, WQ><<<grid, W * 64, 0, s>>>(p);
+        else rl_kernel<TYPE, R, W, GPW, P, EARLY, true, false, CH, RL_XF_NONE, WQ><<<grid, W * 64, 0, s>>>(p);
     } else {
         if (dump) rl_kernel<TYPE, R, W, GPW, P, EARLY, false, true, CH><<<grid, W * 64, 0, s>>>(p);
         else rl_kernel<TYPE, R, W, GPW, P, EARLY, false, false, CH><<<grid, W * 64, 0, s>>>(p);
@@ -794,28 +801,38 @@ hipError_t launch_type(const RlParams &p, int64_t n, int ng, bool wide, bool fus
         // more chunks than CUs: persistent workgroups, one per CU
         // (one wavefront per group: 8 wavefronts for up to 8 groups, where
         //  the other 8 of 16 would only wait)
-        if (ng <= 8 && pl.persistent) return launch_g<TYPE, RL_ROWS, 8, 1, NPG, true, true>(p, grid, fused, dump, s);
+        if (ng <= 8 && pl.persistent) return launch_g<TYPE, RL_ROWS, 8, 1, NPG, true, true, true>(p, grid, fused, dump, s);
         if (ng <= 16 && pl.persistent) return launch_g<TYPE, RL_ROWS, 16, 1, NPG, true, true>(p, grid, fused, dump, s);
-        if (ng <= 8) return launch_g<TYPE, RL_ROWS, 8, 1, Q6 ? 8 : NPG == 11 ? 7 : 6, true>(p, grid, fused, dump, s);
+        if (ng <= 8) return launch_g<TYPE, RL_ROWS, 8, 1, Q6 ? 8 : NPG == 11 ? 7 : 6, true, false, true>(p, grid, fused, dump, s);
         if (ng <= 16) return launch_g<TYPE, RL_ROWS, 16, 1, Q6 ? 8 : NPG == 11 ? 7 : 6, true>(p, grid, fused, dump, s);
         if constexpr (!Q6) return launch_g<TYPE, RL_ROWS, 16, 2, 12, true>(p, grid, fused, dump, s);
         return hipErrorNotSupported;
     }
     // 16 rows: as many wavefronts as four groups each need (every lane one
     // group; two for up to 8 groups, where a third and fourth wavefront
-    // would only quantise and wait: 7 % faster at 5632 x 2048); the
-    // quantising wavefronts (four blocks each) are then always enough.  Up to 32 groups all of a lane's pieces are in flight from the
+    // would only quantise and wait: 7 % faster at 5632 x 2048, and eight
+    // quantising one block each measured slower still); the quantising
+    // wavefronts (four blocks each) are then always enough.  Up to 32 groups all of a lane's pieces are in flight from the
     // start; with 12-16 wavefronts (ffn_down, 56 groups: 14) six (seven for
     // the 11- and 13-piece types), the first issued before the quantisation
     // and the rest after it, measured fastest.
     if (pl.rows == RE_ROWS) {
         // 8 rows: a wavefront covers eight groups, and there are as many
-        // wavefronts as the quantisation needs (four blocks each)
+        // wavefronts as the quantisation needs (four blocks each); those past
+        // the groups skip the walk
         if (ng <= 8) return launch_g<TYPE, RE_ROWS, 2, 1, NPG, true>(p, grid, fused, dump, s);
         if (ng <= 16) return launch_g<TYPE, RE_ROWS, 4, 1, NPG, true>(p, grid, fused, dump, s);
         if (ng <= 24) return launch_g<TYPE, RE_ROWS, 6, 1, NPG, true>(p, grid, fused, dump, s);
         return launch_g<TYPE, RE_ROWS, 8, 1, NPG, true>(p, grid, fused, dump, s);
     }
+    // (a grid of at most 128 workgroups with an f32 input, RMSNorm aside:
+    //  eight wavefronts quantising one block each, the six past the groups
+    //  skipping the walk -- with SmolLM-135M's w2, 36 workgroups, its decode
+    //  measured 1.4 % more tokens/s; at 352 and 256 workgroups (5632 x 2048,
+    //  2048 x 2048) the eight were 0.5-1 us slower.  RMSNorm keeps two, as the
+    //  two-weight launch does, so that the two give the same sums)
+    if (ng <= 8 && fused && p.xf != RL_XF_NORM && grid <= 128)
+        return launch_g<TYPE, RG_ROWS, 8, 1, NPG, true, false, true>(p, grid, fused, dump, s);
     if (ng <= 8) return launch_g<TYPE, RG_ROWS, 2, 1, NPG, true>(p, grid, fused, dump, s);
     if (ng <= 16) return launch_g<TYPE, RG_ROWS, 4, 1, NPG, true>(p, grid, fused, dump, s);
     if (ng <= 32) return launch_g<TYPE, RG_ROWS, 8, 1, NPG, true>(p, grid, fused, dump, s);
@@ -881,22 +898,23 @@ hipError_t rl_params(const WLayout &w, int64_t n, int64_t k, const float *x, con
     return hipSuccess;
 }
 
-template <int T1, int T2, int R, int W>
+template <int T1, int T2, int R, int W, bool WQ>
 hipError_t launch_two_rl(const RlParams &p1, const RlParams &p2, int g1, int g2, int kind, hipStream_t s) {
     if (!rl::grid_ok(R, p1.n, g1, false) || !rl::grid_ok(R, p2.n, g2, false)) return hipErrorInvalidValue;
-    if (kind == RL_XF_NORM) rl2_kernel<T1, T2, R, W, RL_XF_NORM><<<g1 + g2, W * 64, 0, s>>>(p1, p2, g1);
-    else if (kind == RL_XF_SILU) rl2_kernel<T1, T2, R, W, RL_XF_SILU><<<g1 + g2, W * 64, 0, s>>>(p1, p2, g1);
-    else rl2_kernel<T1, T2, R, W, RL_XF_NONE><<<g1 + g2, W * 64, 0, s>>>(p1, p2, g1);
+    if (WQ && p1.ng > W) return hipErrorInvalidValue;  // a wavefront for every block
+    if (kind == RL_XF_NORM) rl2_kernel<T1, T2, R, W, RL_XF_NORM, WQ><<<g1 + g2, W * 64, 0, s>>>(p1, p2, g1);
+    else if (kind == RL_XF_SILU) rl2_kernel<T1, T2, R, W, RL_XF_SILU, WQ><<<g1 + g2, W * 64, 0, s>>>(p1, p2, g1);
+    else rl2_kernel<T1, T2, R, W, RL_XF_NONE, WQ><<<g1 + g2, W * 64, 0, s>>>(p1, p2, g1);
     return hipGetLastError();
 }
 
-template <int R, int W>
+template <int R, int W, bool WQ = false>
 hipError_t launch_two_w(const RlParams &p1, const RlParams &p2, int t1, int t2, int kind, hipStream_t s) {
     const int g1 = (p1.n + R - 1) / R, g2 = (p2.n + R - 1) / R;
-    if (t1 == TYPE_Q4_K && t2 == TYPE_Q6_K) return launch_two_rl<TYPE_Q4_K, TYPE_Q6_K, R, W>(p1, p2, g1, g2, kind, s);
-    if (t1 == TYPE_Q4_K && t2 == TYPE_Q4_K) return launch_two_rl<TYPE_Q4_K, TYPE_Q4_K, R, W>(p1, p2, g1, g2, kind, s);
-    if (t1 == TYPE_Q6_K && t2 == TYPE_Q4_K) return launch_two_rl<TYPE_Q6_K, TYPE_Q4_K, R, W>(p1, p2, g1, g2, kind, s);
-    return launch_two_rl<TYPE_Q6_K, TYPE_Q6_K, R, W>(p1, p2, g1, g2, kind, s);
+    if (t1 == TYPE_Q4_K && t2 == TYPE_Q6_K) return launch_two_rl<TYPE_Q4_K, TYPE_Q6_K, R, W, WQ>(p1, p2, g1, g2, kind, s);
+    if (t1 == TYPE_Q4_K && t2 == TYPE_Q4_K) return launch_two_rl<TYPE_Q4_K, TYPE_Q4_K, R, W, WQ>(p1, p2, g1, g2, kind, s);
+    if (t1 == TYPE_Q6_K && t2 == TYPE_Q4_K) return launch_two_rl<TYPE_Q6_K, TYPE_Q4_K, R, W, WQ>(p1, p2, g1, g2, kind, s);
+    return launch_two_rl<TYPE_Q6_K, TYPE_Q6_K, R, W, WQ>(p1, p2, g1, g2, kind, s);
 }
 }  // namespace
 

@@ -392,13 +392,16 @@ def test_rowlane16_and_general_matvec_agree(ctx):
 
 
 @pytest.mark.parametrize("typ", [S.TYPE_Q4_K, S.TYPE_Q6_K, S.TYPE_Q4_0, S.TYPE_Q5_0])
-def test_rowlane8w_edge_activations(ctx, typ):
+@pytest.mark.parametrize("n", [RL_MIN_N, 512])
+def test_rowlane8w_edge_activations(ctx, typ, n):
     """The edge rows of the quantizer, plus ties of |x| across lanes (the
-    first index wins) and within a Q8_0 block, through the 8-wavefront
-    56-row form, whose prologue quantises one block per wavefront with four
-    elements per lane (Q8_K: 64 lanes per block; Q8_0: eight per block):
-    integer sums bit-exact, outputs within 1e-5."""
-    n, k = RL_MIN_N, 2048  # 200 workgroups of 56 rows, 8 groups: one per wavefront
+    first index wins) and within a Q8_0 block, through the forms whose
+    prologue quantises one block per wavefront with four elements per lane
+    (Q8_K: 64 lanes per block; Q8_0: eight per block) -- the 8-wavefront
+    56-row form (RL_MIN_N rows: 200 workgroups) and the 16-row form with a
+    grid of at most 128 workgroups (512 rows: 32) -- integer sums bit-exact,
+    outputs within 1e-5."""
+    k = 2048  # 8 groups: one per wavefront
     W = S.make_weight(typ, n, k, seed=80 + typ)
     mm = A.QMatMul.from_qtensor(A.QTensor(W.type, (W.n, W.k), W.blocks), ctx)
     extra = np.zeros((2, k), np.float32)
