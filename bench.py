@@ -717,7 +717,7 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic_from_profile(),
-            "kernel": "rl_kernel<12, 56, 16, 1, 6, true, true, false, false, 0> (Q4_K, batch 1, one weight row per lane, Q8_K quantisation fused)",
+            "kernel": "rl_kernel<12, 56, 16, 1, 6, true, true, false, false, 0, false> (Q4_K, batch 1, one weight row per lane, Q8_K quantisation fused)",
             "bytes_per_launch": wl.step_bytes,
             "avg_launch_us": round(step_ms * 1e3, 3),
         },
