@@ -183,58 +183,32 @@ __global__ __launch_bounds__(DEC_THREADS) void swiglu_pairs_kernel(const float *
 }
 
 // swiglu_pairs_kernel's values quantised to Q8_K in the same launch: grid
-// (ceil(n / 4096), m) workgroups, a wavefront per four blocks of 256 values.
-// The wavefront reads the 2048 paired columns of its blocks in whole 1 KB
-// runs (lane l of step c: float4 64c + l, the gate half of a pair of four
-// values when l is even, the up half when odd), swaps halves with its
-// neighbour lane, forms two of the four values by swiglu_pairs_kernel's
-// expression and puts them in LDS in value order; then each 16-lane row
-// quantises one block with the quantizer's per-block code (lane s: values
-// 16s..16s+15).  y 16-byte aligned, ld a multiple of 4 (checked by the
-// launcher).
+// (ceil(n / 1024), m) workgroups, a wavefront per block of 256 values (no
+// workgroup takes more blocks than another, no LDS, no barrier).  Lane l
+// forms values 4l .. 4l + 3 of its block by swiglu_pairs_kernel's
+// expression from the 32 bytes 8l .. 8l + 7 of the block's 512 paired
+// columns (the gate four, then the up four), and the wavefront quantises
+// the block with the quantizer's 64-lane code (q8k_block_wave, the same
+// bytes as the per-block kernel).  y 16-byte aligned, ld a multiple of 4
+// (checked by the launcher).
 __global__ __launch_bounds__(DEC_THREADS) void swiglu_pairs_act_kernel(const float *__restrict__ y, int64_t ld, int n,
                                                                        float *__restrict__ out, ActPlanes a) {
-    __shared__ __align__(16) float vs[DEC_THREADS / 64][4 * QK_K];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int nb = n / QK_K;
-    const int bw = blockIdx.x * (DEC_THREADS / 16) + 4 * wave;  // the wavefront's first block
+    const int b = blockIdx.x * (DEC_THREADS / 64) + wave;  // this wavefront's block
     const int64_t r = blockIdx.y;
-    const int nv = min(4, nb - bw) * QK_K;  // values the wavefront forms (none past the row)
-    const float4 *src = (const float4 *)(y + r * ld + 2 * (int64_t)bw * QK_K);
-    const bool odd = lane & 1;
-    float *vw = vs[wave];
-#pragma unroll
-    for (int c = 0; c < 8; c++) {
-        const int f = 64 * c + lane, e = 2 * (f & ~1);  // the pair's values e .. e + 3
-        float4 t = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        if (e < nv) t = src[f];
-        const float4 o = make_float4(__shfl_xor(t.x, 1), __shfl_xor(t.y, 1), __shfl_xor(t.z, 1), __shfl_xor(t.w, 1));
-        const float4 g = odd ? o : t, u = odd ? t : o;
-        // even lane: values e, e + 1; odd lane: e + 2, e + 3
-        const float g0 = odd ? g.z : g.x, g1 = odd ? g.w : g.y, u0 = odd ? u.z : u.x, u1 = odd ? u.w : u.y;
-        if (e < nv) *(float2 *)(vw + e + 2 * odd) = make_float2((g0 / (1.0f + expf(-g0))) * u0, (g1 / (1.0f + expf(-g1))) * u1);
-    }
-    __syncthreads();
-    const int s = lane & 15, bq = lane >> 4, b = bw + bq;
-    const bool ok = b < nb;  // uniform over the 16-lane row
-    float v[16];
-#pragma unroll
-    for (int q = 0; q < 4; q++) {
-        const float4 t = ok ? *(const float4 *)(vw + bq * QK_K + 16 * s + 4 * q) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        v[4 * q] = t.x;
-        v[4 * q + 1] = t.y;
-        v[4 * q + 2] = t.z;
-        v[4 * q + 3] = t.w;
-    }
-    if (ok && out) {
-        float4 *dst = (float4 *)(out + r * n + b * QK_K + 16 * s);
-#pragma unroll
-        for (int q = 0; q < 4; q++) dst[q] = make_float4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
-    }
+    if (b >= n / QK_K) return;  // uniform over the wavefront
+    const float4 *src = (const float4 *)(y + r * ld + 2 * (int64_t)b * QK_K + 8 * lane);
+    const float4 g = src[0], u = src[1];
+    float v[4];
+    v[0] = (g.x / (1.0f + expf(-g.x))) * u.x;
+    v[1] = (g.y / (1.0f + expf(-g.y))) * u.y;
+    v[2] = (g.z / (1.0f + expf(-g.z))) * u.z;
+    v[3] = (g.w / (1.0f + expf(-g.w))) * u.w;
+    if (out) *(float4 *)(out + r * n + (int64_t)b * QK_K + 4 * lane) = make_float4(v[0], v[1], v[2], v[3]);
     int bsum;
     float d;
-    const uint4 packed = q8k_block_row16(v, s, &bsum, &d);
-    if (ok) store_q8k_block16(a, r, n, b, s, packed, bsum, d);
+    const uint32_t packed = q8k_block_wave(v, lane, &bsum, &d);
+    store_q8k_block64(a, r, n, b, lane, packed, bsum, d);
 }
 
 // Sum over aligned groups of N lanes (N = 2, 4, 8, 16, 32 or 64), every lane
@@ -632,7 +606,7 @@ hipError_t launch_swiglu_pairs_act(const float *y, int64_t ld, int64_t m, int64_
     if (!y || !a.qs || !a.d || !a.bsums || !a.bsum16 || n <= 0 || n % QK_K || n > 0x7fffffff / 2 || m <= 0 ||
         m > 65535 || ld % 4 || (m > 1 && ld < 2 * n) || (((uintptr_t)y | (uintptr_t)out) & 15))
         return hipErrorInvalidValue;
-    const dim3 grid((unsigned)((n / QK_K + DEC_THREADS / 16 - 1) / (DEC_THREADS / 16)), (unsigned)m);
+    const dim3 grid((unsigned)((n / QK_K + DEC_THREADS / 64 - 1) / (DEC_THREADS / 64)), (unsigned)m);
     swiglu_pairs_act_kernel<<<grid, DEC_THREADS, 0, s>>>(y, ld, (int)n, out, a);
     return hipGetLastError();
 }
