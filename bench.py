@@ -1,15 +1,15 @@
 """Benchmark of the quantized-matmul hot path on one MI355X.
 
-Metric: "Q4_K matvec HBM GB/s (% of peak) + prefill int8 TOPS;
-decode tok/s".  The headline workload is the Llama-3-8B FFN up/gate
+Metric: "Q4_K matvec HBM GB/s (% of peak) + prefill int8 TOPS; decode
+tok/s" (the reference's headline).  The headline workload is the Llama-3-8B FFN up/gate
 projection (config 4): Q4_K weight 14336 x 4096, batch 1.  A step is one pass
 of the hot path over one activation row: Q8_K quantisation of x (f32 [1, 4096])
 and the Q4_K matvec, i.e. candle's QMatMul::forward for that call.  At batch
 <= 8 both run in one kernel (the matvec quantises x into LDS itself).
 
-* Inputs are resident in HBM before timing.  Ten copies of the weight
-  (330 MB > the 256 MB Infinity Cache) are used round-robin, so every step
-  streams its weight from HBM.
+* Inputs are resident in HBM before timing.  Enough copies of the weight
+  to hold 1.25 times the 256 MB Infinity Cache (11 of the headline's 33 MB)
+  are used round-robin, so every step streams its weight from HBM.
 * The K timed steps are captured once into a HIP graph and replayed, so the
   number is the GPU's, not the Python launch loop's.
 * value = algorithmic bytes per step / time per step, bytes =
