@@ -364,20 +364,41 @@ __global__ __launch_bounds__(256, 2) void gemm_pair_kernel(GemmParams p1, Gemm6P
 // output element of a tile row.  A kernel boundary, not a fence, makes the
 // partials visible: a device-scope fence per workgroup costs an L2
 // write-back on this GPU.
+// V consecutive columns of one tile row per thread (V = 4: 16-byte loads and
+// stores, where n % 4 == 0 and y is 16-byte aligned, so that the four stay in
+// one output row; the partial tiles are 128 columns wide).  Indices in 32
+// bits: the launcher checks that the tiles' elements fit.  The sum starts
+// from 0 and adds the parts in order, whatever V.
+template <int V>
 __global__ __launch_bounds__(256) void gemm_splitk_reduce(const float *__restrict__ part, float *__restrict__ y, int m,
                                                           int n, int ntm, int gbm, int splits, int tiles) {
-    const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    const int64_t per_tile = (int64_t)gbm * GBN;
-    if (e >= (int64_t)tiles * per_tile) return;
-    const int tile = (int)(e / per_tile);
-    const int w = (int)(e - (int64_t)tile * per_tile);
+    const int per_tile = gbm * GBN;
+    const int e = ((int)blockIdx.x * 256 + (int)threadIdx.x) * V;
+    if (e >= tiles * per_tile) return;
+    const int tile = e / per_tile;
+    const int w = e - tile * per_tile;
     const int tn = tile / ntm, tm = tile - tn * ntm;
     const int row = tm * gbm + w / GBN, c = tn * GBN + w % GBN;
     if (row >= m || c >= n) return;
     const float *src = part + (int64_t)tile * splits * per_tile + w;
-    float acc = 0.0f;
-    for (int s2 = 0; s2 < splits; s2++) acc += src[(int64_t)s2 * per_tile];
-    y[(int64_t)row * n + c] = acc;
+    float *dst = y + (int64_t)row * n + c;
+    if (V == 4 && c + 4 <= n) {
+        float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        for (int s2 = 0; s2 < splits; s2++) {
+            const float4 t = *(const float4 *)(src + (int64_t)s2 * per_tile);
+            acc.x += t.x;
+            acc.y += t.y;
+            acc.z += t.z;
+            acc.w += t.w;
+        }
+        *(float4 *)dst = acc;
+    } else {
+        for (int j = 0; j < V && c + j < n; j++) {
+            float acc = 0.0f;
+            for (int s2 = 0; s2 < splits; s2++) acc += src[(int64_t)s2 * per_tile + j];
+            dst[j] = acc;
+        }
+    }
 }
 
 struct GemmPlan {
@@ -420,7 +441,11 @@ static int64_t gemm_chunk_rows(int64_t m, int64_t k) {
 hipError_t launch_splitk_reduce(const float *part, float *y, int m, int n, int ntm, int gbm, int splits, int tiles,
                                 hipStream_t s) {
     const int64_t elems = (int64_t)tiles * gbm * GBN;
-    gemm_splitk_reduce<<<(unsigned)((elems + 255) / 256), 256, 0, s>>>(part, y, m, n, ntm, gbm, splits, tiles);
+    if (elems + 4 * 256 > 0x7fffffff) return hipErrorInvalidValue;
+    if (n % 4 == 0 && (((uintptr_t)y | (uintptr_t)part) & 15) == 0)
+        gemm_splitk_reduce<4><<<(unsigned)((elems / 4 + 255) / 256), 256, 0, s>>>(part, y, m, n, ntm, gbm, splits, tiles);
+    else
+        gemm_splitk_reduce<1><<<(unsigned)((elems + 255) / 256), 256, 0, s>>>(part, y, m, n, ntm, gbm, splits, tiles);
     return hipGetLastError();
 }
 
@@ -477,12 +502,8 @@ hipError_t launch_gemm(const WLayout &w, int64_t n, int64_t k, const ActPlanes &
         else gemm_q4k_kernel<false><<<grid, 256, 0, s>>>(p);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
-        if (g.splits > 1) {
-            const int64_t elems = (int64_t)g.tiles * GBM * GBN;
-            gemm_splitk_reduce<<<(unsigned)((elems + 255) / 256), 256, 0, s>>>(p.part, p.y, p.m, p.n, g.ntm, GBM,
-                                                                             g.splits, g.tiles);
-            if ((e = hipGetLastError()) != hipSuccess) return e;
-        }
+        if (g.splits > 1 && (e = launch_splitk_reduce(p.part, p.y, p.m, p.n, g.ntm, GBM, g.splits, g.tiles, s)) != hipSuccess)
+            return e;
     }
     return hipSuccess;
 }

@@ -163,10 +163,12 @@ def test_prefill_gemm_extreme_values(ctx):
     (384, 1000, 3840),  # 15 super-blocks: an odd count per split
     (511, 64, 2048),    # one partial n-tile, many splits
     (640, 4100, 512),   # ragged columns, two super-blocks
+    (200, 301, 2304),   # n % 4 != 0: the reduction one column per thread (else four)
 ])
 def test_prefill_gemm_odd_splits(ctx, m, n, k):
     """Longer prompts with ragged rows and columns and K splits of unequal
-    super-block counts (the split-K reduction adds them in split order)."""
+    super-block counts (the split-K reduction adds them in split order, four
+    columns per thread where n % 4 == 0, else one)."""
     W = S.make_weight(S.TYPE_Q4_K, n, k, seed=m + n + 7)
     x = S.make_activation(m, k, seed=m * 3 + n)
     check_matmul(ctx, W, x)
