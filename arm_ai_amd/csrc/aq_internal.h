@@ -557,30 +557,6 @@ __device__ __forceinline__ uint4 q8k_block_row16(const float v[16], int s, int *
     return make_uint4(pack4_i8(q), pack4_i8(q + 4), pack4_i8(q + 8), pack4_i8(q + 12));
 }
 
-// The stores of one Q8_K block by its 16 lanes (q8k_block_row16's layout):
-// lane s writes quants 16s..16s+15 (and their f16 copy when a.q16 is set)
-// and bsum s; lane 0 writes d.  Block sb of row `row`, rows of k elements.
-__device__ __forceinline__ void store_q8k_block16(const ActPlanes &a, int64_t row, int64_t k, int64_t sb, int s,
-                                                  uint4 packed, int bsum, float d) {
-    const int64_t e0 = row * k + sb * QK_K + 16 * s;
-    *(uint4 *)(a.qs + e0) = packed;
-    if (a.q16) {
-        const uint32_t w[4] = {packed.x, packed.y, packed.z, packed.w};
-        uint32_t o[8];
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const uint32_t lo = __builtin_bit_cast(uint16_t, (_Float16)(int)(int8_t)((w[j >> 1] >> (16 * (j & 1))) & 0xffu));
-            const uint32_t hi = __builtin_bit_cast(uint16_t, (_Float16)(int)(int8_t)((w[j >> 1] >> (16 * (j & 1) + 8)) & 0xffu));
-            o[j] = lo | (hi << 16);
-        }
-        *(uint4 *)(a.q16 + e0) = make_uint4(o[0], o[1], o[2], o[3]);
-        *(uint4 *)(a.q16 + e0 + 8) = make_uint4(o[4], o[5], o[6], o[7]);
-    }
-    a.bsums[row * (k / 16) + sb * 16 + s] = (int16_t)bsum;
-    a.bsum16[row * (k / 16) + sb * 16 + s] = __builtin_bit_cast(uint16_t, (_Float16)(float)bsum);
-    if (s == 0) a.d[row * (k / QK_K) + sb] = d;
-}
-
 // The stores of one Q8_K block by a wavefront (q8k_block_wave's layout):
 // lane l writes quants 4l..4l+3 (and their f16 copy when a.q16 is set), the
 // first lane of each quad its bsum, lane 0 d.  Block sb of row `row`, rows of

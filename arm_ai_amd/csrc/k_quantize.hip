@@ -10,41 +10,35 @@
 
 namespace aq {
 
-// Sixteen lanes (one DPP row) per 256-element block, lane s holding elements
-// 16s..16s+15: four blocks per wavefront, sixteen per 256-thread workgroup.
-// Each lane loads 64 contiguous bytes and stores its 16 quants and its own
-// 16-element bsum, so every store of the wavefront is one contiguous run.
+// One wavefront per 256-element block, lane l holding elements 4l..4l+3
+// (q8k_block_wave, the fused prologues' code): four blocks per 256-thread
+// workgroup.  The block's row and index within the row are wave-uniform
+// (scalar arithmetic).
 template <bool VEC>
 __global__ __launch_bounds__(256) void quantize_q8k_kernel(const float *__restrict__ x, int64_t nblocks,
                                                            int64_t k, ActPlanes a) {
-    const int lane = threadIdx.x & 63, s = lane & 15;
-    const int64_t bi = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
-    const bool ok = bi < nblocks;  // uniform over the row of 16 lanes
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int64_t bi = (int64_t)blockIdx.x * 4 + wave;
+    if (bi >= nblocks) return;  // uniform over the wavefront
     const int64_t nb = k / QK_K;
-    const int64_t row = ok ? bi / nb : 0, sb = ok ? bi - row * nb : 0;
-    const int64_t e0 = row * k + sb * QK_K + 16 * s;
-    float v[16];
-    if (!ok) {
-#pragma unroll
-        for (int i = 0; i < 16; i++) v[i] = 0.0f;
-    } else if (VEC) {
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const float4 t = *(const float4 *)(x + e0 + 4 * i);
-            v[4 * i] = t.x;
-            v[4 * i + 1] = t.y;
-            v[4 * i + 2] = t.z;
-            v[4 * i + 3] = t.w;
-        }
+    const int64_t row = bi / nb, sb = bi - row * nb;
+    const int64_t e0 = row * k + sb * QK_K + 4 * lane;
+    float v[4];
+    if (VEC) {
+        const float4 t = *(const float4 *)(x + e0);
+        v[0] = t.x;
+        v[1] = t.y;
+        v[2] = t.z;
+        v[3] = t.w;
     } else {
 #pragma unroll
-        for (int i = 0; i < 16; i++) v[i] = x[e0 + i];
+        for (int i = 0; i < 4; i++) v[i] = x[e0 + i];
     }
     int bsum;
     float d;
-    const uint4 packed = q8k_block_row16(v, s, &bsum, &d);
-    if (!ok) return;  // after the row's DPP exchanges
-    store_q8k_block16(a, row, k, sb, s, packed, bsum, d);
+    const uint32_t packed = q8k_block_wave(v, lane, &bsum, &d);
+    store_q8k_block64(a, row, k, sb, lane, packed, bsum, d);
 }
 
 // Eight lanes per 32-element block, 32 blocks per workgroup.
@@ -80,7 +74,7 @@ hipError_t launch_quantize_q8k(const float *x, int64_t m, int64_t k, ActPlanes a
     if (!x || m < 0 || k <= 0 || k % QK_K) return hipErrorInvalidValue;
     if (m == 0) return hipSuccess;
     const int64_t nblocks = m * (k / QK_K);
-    const int64_t grid = (nblocks + 15) / 16;
+    const int64_t grid = (nblocks + 3) / 4;
     if (grid > 0x7fffffff) return hipErrorInvalidValue;
     if (((uintptr_t)x & 15) == 0)
         quantize_q8k_kernel<true><<<dim3((unsigned)grid), dim3(256), 0, s>>>(x, nblocks, k, a);
