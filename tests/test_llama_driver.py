@@ -297,6 +297,7 @@ def test_generate_streams_each_token_before_the_next_step(tiny):
     assert seen == eager[:1]
 
 
+@pytest.mark.gpu
 def test_reserve_leaves_no_trace(tiny):
     """Llama reserves a prompt's buffers at construction (one forward of
     min(max_seq, 512) tokens at offset 0, then the KV cache cleared): a model
